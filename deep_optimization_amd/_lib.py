@@ -1,0 +1,75 @@
+"""ctypes binding of libdopt.so (the C ABI declared in include/dopt.h).
+
+There is no fallback: if the library is missing, or a call fails, an exception is raised.
+Bad ``bits`` raise ``ValueError`` (as act_triton_kernel.py:329-330 does); every other failure
+raises ``RuntimeError`` carrying the library's dopt_last_error() message.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+_PKG = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_PKG, "libdopt.so")
+
+F32, F16, BF16 = 0, 1, 2
+ROUND_NEAREST, ROUND_STOCH_NOISE, ROUND_STOCH_PHILOX = 0, 1, 2
+FLAG_CLAMP, FLAG_SQUASH = 1, 2
+
+OK, EBITS, EINVAL, EUNSUPPORTED, EHIP = 0, -1, -2, -3, -4
+
+EXPORTS = (
+    "dopt_abi_version",
+    "dopt_last_error",
+    "dopt_quant_pack",
+    "dopt_dequant_unpack",
+    "dopt_pack_codes",
+    "dopt_unpack_codes",
+    "dopt_fp8_gemm_nt",
+)
+
+_lib = None
+
+
+class DoptError(RuntimeError):
+    def __init__(self, code: int, msg: str):
+        super().__init__(msg)
+        self.code = code
+
+
+def lib() -> ctypes.CDLL:
+    """Load libdopt.so once; raise if it has not been built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(
+                f"{LIB_PATH} is missing: the HIP kernels are not built. "
+                "Run `python -m deep_optimization_amd.build` (or __graft_entry__.build())."
+            )
+        L = ctypes.CDLL(LIB_PATH)
+        vp, i64, i32, u64, f32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_uint64, ctypes.c_float
+        L.dopt_abi_version.argtypes = []
+        L.dopt_abi_version.restype = i32
+        L.dopt_last_error.argtypes = []
+        L.dopt_last_error.restype = ctypes.c_char_p
+        L.dopt_quant_pack.argtypes = [vp, i32, i64, i32, i32, vp, i32, vp, u64, u64, i32, f32, vp, vp, vp, i32, vp]
+        L.dopt_quant_pack.restype = i32
+        L.dopt_dequant_unpack.argtypes = [vp, vp, vp, i32, i64, i32, i32, vp, vp, i32, vp]
+        L.dopt_dequant_unpack.restype = i32
+        L.dopt_pack_codes.argtypes = [vp, i64, i32, i32, vp, vp]
+        L.dopt_pack_codes.restype = i32
+        L.dopt_unpack_codes.argtypes = [vp, i64, i32, i32, vp, vp]
+        L.dopt_unpack_codes.restype = i32
+        L.dopt_fp8_gemm_nt.argtypes = [vp, vp, i64, i64, i64, i64, i64, f32, vp, i64, vp]
+        L.dopt_fp8_gemm_nt.restype = i32
+        _lib = L
+    return _lib
+
+
+def check(rc: int, what: str) -> None:
+    if rc == OK:
+        return
+    msg = lib().dopt_last_error().decode(errors="replace")
+    if rc == EBITS:
+        raise ValueError(msg)
+    raise DoptError(rc, f"{what} failed ({rc}): {msg}")

@@ -1,0 +1,338 @@
+"""``torch.ops.act_lib`` operators backed by the gfx950 HIP kernels of libdopt.so.
+
+Drop-in for Activation_Compression/act_triton_kernel.py:336-473: the four reference operators
+keep their names and schemas,
+
+    act_lib::quant_pack_triton(x, bits, group_size, avg_alam, alam_bits, clamp, clamp_alpha)
+        -> (packed int32 [N*G, W], scale [N, G], min [N, G])          (reference :336-368)
+    act_lib::dequant_unpack_triton(packed, scale, xmin, bits, group_size, avg_alam, alam_bits)
+        -> bf16 [N, G, g]                                              (reference :372-395)
+    act_lib::pack_triton(x, bits, group_size) -> int32 [N*G, W]        (reference :398-417)
+    act_lib::unpack_triton(packed, bits, N, G, group_size) -> int8 [N, G, g]   (reference :419-433)
+
+with the reference's semantics (tanh squash always on, nearest rounding, bf16 scale/min).
+The general operators below expose what the reference leaves fixed: rounding mode (nearest,
+stochastic from a noise tensor, stochastic from Philox(seed, offset)), the squash pre-transform,
+the scale/min dtype (fp32 or bf16), the output dtype, and the fused s x s spatial-tile layout
+(act_lib::quant_pack_tiles / act_lib::dequant_unpack_tiles), which removes the permute copy of
+tensor_act_reshape_utils.py:128 and :152.
+
+Every operator is registered for CUDA (HIP) tensors only and has a fake (meta) implementation
+with the correct output shapes; there is no CPU implementation.
+"""
+from __future__ import annotations
+
+from typing import Optional, Tuple
+
+import torch
+from torch import Tensor
+
+from . import _lib
+
+_DTYPE_CODE = {torch.float32: _lib.F32, torch.float16: _lib.F16, torch.bfloat16: _lib.BF16}
+_META_CODE = {torch.float32: _lib.F32, torch.bfloat16: _lib.BF16}
+_OUT_CODE = {torch.float32: _lib.F32, torch.bfloat16: _lib.BF16}
+
+ROUND_NEAREST = _lib.ROUND_NEAREST
+ROUND_STOCH_NOISE = _lib.ROUND_STOCH_NOISE
+ROUND_STOCH_PHILOX = _lib.ROUND_STOCH_PHILOX
+_ROUNDING_NAMES = {"nearest": ROUND_NEAREST, "stochastic": ROUND_STOCH_PHILOX,
+                   "stochastic_philox": ROUND_STOCH_PHILOX, "stochastic_noise": ROUND_STOCH_NOISE}
+
+_U64 = (1 << 64) - 1
+
+
+def _bits_consts(bits: int, group_size: int):
+    """(values per int32 word, words per group, max code); same contract as
+    act_triton_kernel.py:328-334 (ValueError for bits outside {1, 2, 4, 8})."""
+    if bits not in (1, 2, 4, 8):
+        raise ValueError(f"bits must be one of (1,2,4,8). got {bits}")
+    vpw = 32 // bits
+    nwords = group_size // vpw
+    qmax = (1 << bits) - 1
+    return vpw, nwords, qmax
+
+
+def rounding_code(rounding) -> int:
+    if isinstance(rounding, int):
+        return rounding
+    try:
+        return _ROUNDING_NAMES[rounding]
+    except KeyError:
+        raise ValueError(f"unknown rounding mode {rounding!r}") from None
+
+
+def _stream(t: Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _require_cuda(*ts: Tensor) -> None:
+    for t in ts:
+        if t is not None and t.device.type != "cuda":
+            raise RuntimeError("act_lib operators run on HIP (cuda) tensors only")
+
+
+def _aligned(t: Tensor) -> Tensor:
+    """Contiguous view with a 16-byte aligned base (the kernels use 128-bit accesses)."""
+    t = t.contiguous()
+    if t.data_ptr() % 16:
+        t = t.clone()
+    return t
+
+
+def _flags(clamp: bool, squash: bool) -> int:
+    return (_lib.FLAG_CLAMP if clamp else 0) | (_lib.FLAG_SQUASH if squash else 0)
+
+
+def _quant_pack_launch(x: Tensor, n_groups: int, bits: int, group_size: int, tile, clamp: bool,
+                       clamp_alpha: float, squash: bool, rounding: int, noise: Optional[Tensor],
+                       seed: int, offset: int, scale_dtype: torch.dtype):
+    _, nwords, _ = _bits_consts(bits, group_size)
+    if x.dtype not in _DTYPE_CODE:
+        raise RuntimeError(f"quant_pack: unsupported input dtype {x.dtype}")
+    if scale_dtype not in _META_CODE:
+        raise RuntimeError(f"quant_pack: scale dtype must be float32 or bfloat16, got {scale_dtype}")
+    _require_cuda(x, noise)
+    x = _aligned(x)
+    packed = torch.empty((n_groups, nwords), dtype=torch.int32, device=x.device)
+    scale = torch.empty((n_groups,), dtype=scale_dtype, device=x.device)
+    xmin = torch.empty((n_groups,), dtype=scale_dtype, device=x.device)
+    nz_ptr = None
+    if rounding == ROUND_STOCH_NOISE:
+        if noise is None:
+            raise RuntimeError("quant_pack: rounding=stochastic_noise needs a noise tensor")
+        if noise.numel() != n_groups * group_size:
+            raise RuntimeError(f"quant_pack: noise has {noise.numel()} values, expected {n_groups * group_size}")
+        noise = _aligned(noise.to(torch.float32))
+        nz_ptr = noise.data_ptr()
+    tile_arr = None
+    if tile is not None:
+        import ctypes
+        tile_arr = (ctypes.c_int64 * 4)(*tile)
+    rc = _lib.lib().dopt_quant_pack(
+        x.data_ptr(), _DTYPE_CODE[x.dtype], n_groups, group_size, bits, tile_arr, rounding, nz_ptr,
+        seed & _U64, offset & _U64, _flags(clamp, squash), float(clamp_alpha), packed.data_ptr(),
+        scale.data_ptr(), xmin.data_ptr(), _META_CODE[scale_dtype], _stream(x))
+    _lib.check(rc, "quant_pack")
+    return packed, scale, xmin
+
+
+def _dequant_launch(packed: Tensor, scale: Tensor, xmin: Tensor, n_groups: int, bits: int,
+                    group_size: int, tile, out: Tensor):
+    _bits_consts(bits, group_size)
+    if scale.dtype not in _META_CODE or xmin.dtype != scale.dtype:
+        raise RuntimeError("dequant_unpack: scale and min must both be float32 or both bfloat16")
+    _require_cuda(packed, scale, xmin)
+    packed = _aligned(packed)
+    scale = scale.contiguous()
+    xmin = xmin.contiguous()
+    tile_arr = None
+    if tile is not None:
+        import ctypes
+        tile_arr = (ctypes.c_int64 * 4)(*tile)
+    rc = _lib.lib().dopt_dequant_unpack(
+        packed.data_ptr(), scale.data_ptr(), xmin.data_ptr(), _META_CODE[scale.dtype], n_groups,
+        group_size, bits, tile_arr, out.data_ptr(), _OUT_CODE[out.dtype], _stream(packed))
+    _lib.check(rc, "dequant_unpack")
+    return out
+
+
+# --------------------------------------------------------------------------- general operators
+@torch.library.custom_op("act_lib::quant_pack", mutates_args=(), device_types="cuda")
+def quant_pack(x: Tensor, bits: int, group_size: int, clamp: bool, clamp_alpha: float, squash: bool,
+               rounding: int, noise: Optional[Tensor], seed: int, offset: int,
+               scale_dtype: torch.dtype) -> Tuple[Tensor, Tensor, Tensor]:
+    """x [N, G, group_size] -> (packed int32 [N*G, W], scale [N, G], min [N, G])."""
+    if x.dim() != 3 or x.shape[-1] != group_size:
+        raise RuntimeError(f"quant_pack expects x of shape [N, G, {group_size}], got {tuple(x.shape)}")
+    N, G, _ = x.shape
+    packed, scale, xmin = _quant_pack_launch(x, N * G, bits, group_size, None, clamp, clamp_alpha,
+                                             squash, rounding, noise, seed, offset, scale_dtype)
+    return packed, scale.view(N, G), xmin.view(N, G)
+
+
+@quant_pack.register_fake
+def _(x, bits, group_size, clamp, clamp_alpha, squash, rounding, noise, seed, offset, scale_dtype):
+    N, G = x.shape[0], x.shape[1]
+    _, nwords, _ = _bits_consts(bits, group_size)
+    return (x.new_empty((N * G, nwords), dtype=torch.int32), x.new_empty((N, G), dtype=scale_dtype),
+            x.new_empty((N, G), dtype=scale_dtype))
+
+
+def _tile_groups(shape, group_size: int):
+    if len(shape) != 4:
+        raise RuntimeError(f"tile layout expects a 4-D [N, C, H, W] tensor, got {tuple(shape)}")
+    s = int(round(group_size ** 0.5))
+    N, C, H, W = (int(v) for v in shape)
+    if s * s != group_size or H % s or W % s:
+        raise RuntimeError(f"tile layout needs s*s == group_size and H, W divisible by s "
+                           f"(group_size={group_size}, H={H}, W={W})")
+    return N, C * (H // s) * (W // s)
+
+
+@torch.library.custom_op("act_lib::quant_pack_tiles", mutates_args=(), device_types="cuda")
+def quant_pack_tiles(x: Tensor, bits: int, group_size: int, clamp: bool, clamp_alpha: float,
+                     squash: bool, rounding: int, noise: Optional[Tensor], seed: int, offset: int,
+                     scale_dtype: torch.dtype) -> Tuple[Tensor, Tensor, Tensor]:
+    """x [N, C, H, W] grouped into s x s spatial tiles (s*s = group_size), read in place."""
+    N, G = _tile_groups(x.shape, group_size)
+    packed, scale, xmin = _quant_pack_launch(x, N * G, bits, group_size, tuple(x.shape), clamp,
+                                             clamp_alpha, squash, rounding, noise, seed, offset,
+                                             scale_dtype)
+    return packed, scale.view(N, G), xmin.view(N, G)
+
+
+@quant_pack_tiles.register_fake
+def _(x, bits, group_size, clamp, clamp_alpha, squash, rounding, noise, seed, offset, scale_dtype):
+    N, G = _tile_groups(x.shape, group_size)
+    _, nwords, _ = _bits_consts(bits, group_size)
+    return (x.new_empty((N * G, nwords), dtype=torch.int32), x.new_empty((N, G), dtype=scale_dtype),
+            x.new_empty((N, G), dtype=scale_dtype))
+
+
+@torch.library.custom_op("act_lib::dequant_unpack", mutates_args=(), device_types="cuda")
+def dequant_unpack(packed: Tensor, scale: Tensor, xmin: Tensor, bits: int, group_size: int,
+                   out_dtype: torch.dtype) -> Tensor:
+    """-> [N, G, group_size] of out_dtype (float32 or bfloat16)."""
+    N, G = scale.shape
+    if out_dtype not in _OUT_CODE:
+        raise RuntimeError(f"dequant_unpack: output dtype must be float32 or bfloat16, got {out_dtype}")
+    y = torch.empty((N, G, group_size), dtype=out_dtype, device=packed.device)
+    return _dequant_launch(packed, scale, xmin, N * G, bits, group_size, None, y)
+
+
+@dequant_unpack.register_fake
+def _(packed, scale, xmin, bits, group_size, out_dtype):
+    N, G = scale.shape
+    return packed.new_empty((N, G, group_size), dtype=out_dtype)
+
+
+@torch.library.custom_op("act_lib::dequant_unpack_tiles", mutates_args=(), device_types="cuda")
+def dequant_unpack_tiles(packed: Tensor, scale: Tensor, xmin: Tensor, bits: int, group_size: int,
+                         N: int, C: int, H: int, W: int, out_dtype: torch.dtype) -> Tensor:
+    """-> [N, C, H, W] of out_dtype: the inverse tile scatter is fused into the stores."""
+    n, G = _tile_groups((N, C, H, W), group_size)
+    if tuple(scale.shape) != (n, G):
+        raise RuntimeError(f"dequant_unpack_tiles: scale shape {tuple(scale.shape)} != {(n, G)}")
+    if out_dtype not in _OUT_CODE:
+        raise RuntimeError(f"dequant_unpack_tiles: output dtype must be float32 or bfloat16, got {out_dtype}")
+    y = torch.empty((N, C, H, W), dtype=out_dtype, device=packed.device)
+    return _dequant_launch(packed, scale, xmin, n * G, bits, group_size, (N, C, H, W), y)
+
+
+@dequant_unpack_tiles.register_fake
+def _(packed, scale, xmin, bits, group_size, N, C, H, W, out_dtype):
+    return packed.new_empty((N, C, H, W), dtype=out_dtype)
+
+
+# --------------------------------------------------------------------------- reference schemas
+def _no_alam(avg_alam: bool, where: str) -> None:
+    if avg_alam:
+        raise NotImplementedError(
+            f"{where}: avg_alam=True is not implemented (the reference disables it for every "
+            "Linear/Conv layer, controller.py:186-187, and its dequant noise uses Triton's tl.randn)")
+
+
+@torch.library.custom_op("act_lib::quant_pack_triton", mutates_args=(), device_types="cuda")
+def quant_pack_triton(x: Tensor, bits: int, group_size: int, avg_alam: bool, alam_bits: int,
+                      clamp: bool, clamp_alpha: float) -> Tuple[Tensor, Tensor, Tensor]:
+    """Reference semantics (act_triton_kernel.py:336-368): [clamp], tanh squash, nearest
+    rounding, bf16 scale and min."""
+    _no_alam(avg_alam, "quant_pack_triton")
+    if x.dim() != 3:
+        raise RuntimeError(f"quant_pack_triton expects x of shape [N, G, g], got {tuple(x.shape)}")
+    N, G, _ = x.shape
+    packed, scale, xmin = _quant_pack_launch(x, N * G, bits, group_size, None, clamp, clamp_alpha,
+                                             True, ROUND_NEAREST, None, 0, 0, torch.bfloat16)
+    return packed, scale.view(N, G), xmin.view(N, G)
+
+
+@quant_pack_triton.register_fake
+def _(x, bits, group_size, avg_alam, alam_bits, clamp, clamp_alpha):
+    N, G = x.shape[0], x.shape[1]
+    _, nwords, _ = _bits_consts(bits, group_size)
+    return (x.new_empty((N * G, nwords), dtype=torch.int32), x.new_empty((N, G), dtype=torch.bfloat16),
+            x.new_empty((N, G), dtype=torch.bfloat16))
+
+
+@torch.library.custom_op("act_lib::dequant_unpack_triton", mutates_args=(), device_types="cuda")
+def dequant_unpack_triton(packed: Tensor, scale: Tensor, xmin: Tensor, bits: int, group_size: int,
+                          avg_alam: bool, alam_bits: int) -> Tensor:
+    """Reference semantics (act_triton_kernel.py:372-395): bf16 output [N, G, g]."""
+    _no_alam(avg_alam, "dequant_unpack_triton")
+    N, G = scale.shape
+    y = torch.empty((N, G, group_size), dtype=torch.bfloat16, device=packed.device)
+    return _dequant_launch(packed, scale, xmin, N * G, bits, group_size, None, y)
+
+
+@dequant_unpack_triton.register_fake
+def _(packed, scale, xmin, bits, group_size, avg_alam, alam_bits):
+    N, G = scale.shape
+    return packed.new_empty((N, G, group_size), dtype=torch.bfloat16)
+
+
+@torch.library.custom_op("act_lib::pack_triton", mutates_args=(), device_types="cuda")
+def pack_triton(x: Tensor, bits: int, group_size: int) -> Tensor:
+    """int8 codes [N, G, g] -> int32 words [N*G, W] (act_triton_kernel.py:398-417)."""
+    if x.dim() != 3 or x.shape[-1] != group_size:
+        raise RuntimeError(f"pack_triton expects x of shape [N, G, {group_size}], got {tuple(x.shape)}")
+    _, nwords, _ = _bits_consts(bits, group_size)
+    _require_cuda(x)
+    N, G, _ = x.shape
+    codes = _aligned(x.to(torch.int8) if x.dtype != torch.int8 else x)
+    packed = torch.empty((N * G, nwords), dtype=torch.int32, device=x.device)
+    rc = _lib.lib().dopt_pack_codes(codes.data_ptr(), N * G, group_size, bits, packed.data_ptr(), _stream(x))
+    _lib.check(rc, "pack_codes")
+    return packed
+
+
+@pack_triton.register_fake
+def _(x, bits, group_size):
+    N, G, _ = x.shape
+    _, nwords, _ = _bits_consts(bits, group_size)
+    return x.new_empty((N * G, nwords), dtype=torch.int32)
+
+
+@torch.library.custom_op("act_lib::unpack_triton", mutates_args=(), device_types="cuda")
+def unpack_triton(packed: Tensor, bits: int, N: int, G: int, group_size: int) -> Tensor:
+    """int32 words [N*G, W] -> int8 codes [N, G, g] (act_triton_kernel.py:419-433)."""
+    _bits_consts(bits, group_size)
+    _require_cuda(packed)
+    NG = packed.shape[0]
+    if NG != N * G:
+        raise RuntimeError(f"unpack_triton: packed has {NG} groups, expected N*G = {N * G}")
+    packed = _aligned(packed)
+    out = torch.empty((NG, group_size), dtype=torch.int8, device=packed.device)
+    rc = _lib.lib().dopt_unpack_codes(packed.data_ptr(), NG, group_size, bits, out.data_ptr(), _stream(packed))
+    _lib.check(rc, "unpack_codes")
+    return out.view(N, G, group_size)
+
+
+@unpack_triton.register_fake
+def _(packed, bits, N, G, group_size):
+    return packed.new_empty((N, G, group_size), dtype=torch.int8)
+
+
+# --------------------------------------------------------------------------- FP8 GEMM
+@torch.library.custom_op("act_lib::fp8_gemm_nt", mutates_args=(), device_types="cuda")
+def fp8_gemm_nt(a: Tensor, b: Tensor, out_scale: float) -> Tensor:
+    """a [M, K] e4m3, b [N, K] e4m3 -> bf16 [M, N] = out_scale * a @ b.T (fp32 accumulate)."""
+    if a.dtype != torch.float8_e4m3fn or b.dtype != torch.float8_e4m3fn:
+        raise RuntimeError("fp8_gemm_nt expects torch.float8_e4m3fn operands")
+    if a.dim() != 2 or b.dim() != 2 or a.shape[1] != b.shape[1]:
+        raise RuntimeError(f"fp8_gemm_nt: shapes {tuple(a.shape)} x {tuple(b.shape)}^T do not contract")
+    _require_cuda(a, b)
+    a = _aligned(a)
+    b = _aligned(b)
+    M, K = a.shape
+    N = b.shape[0]
+    c = torch.empty((M, N), dtype=torch.bfloat16, device=a.device)
+    rc = _lib.lib().dopt_fp8_gemm_nt(a.data_ptr(), b.data_ptr(), M, N, K, K, K, float(out_scale),
+                                     c.data_ptr(), N, _stream(a))
+    _lib.check(rc, "fp8_gemm_nt")
+    return c
+
+
+@fp8_gemm_nt.register_fake
+def _(a, b, out_scale):
+    return a.new_empty((a.shape[0], b.shape[0]), dtype=torch.bfloat16)

@@ -1,0 +1,220 @@
+// extern "C" entry points of libdopt.so (declared in include/dopt.h): argument validation,
+// layout set-up and dispatch to the templated gfx950 kernels. No entry point allocates,
+// frees or synchronises; all work is enqueued on the caller's stream.
+#include <stdarg.h>
+#include <stdio.h>
+
+#include "../../include/dopt.h"
+#include "dequant_unpack.h"
+#include "quant_pack.h"
+
+namespace dopt {
+int launch_pack_codes(const int8_t* codes, uint32_t* out, uint64_t n_words, int bits, hipStream_t s);
+int launch_unpack_codes(const uint32_t* packed, int8_t* codes, uint64_t n_words, int bits, hipStream_t s);
+int launch_fp8_gemm_nt(const uint8_t* A, const uint8_t* B, int64_t M, int64_t N, int64_t K, int64_t lda,
+                       int64_t ldb, float out_scale, uint16_t* C, int64_t ldc, hipStream_t s);
+}  // namespace dopt
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof(g_err), fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+int ok() {
+    g_err[0] = '\0';
+    return DOPT_OK;
+}
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+int check_bits(int bits) {
+    if (bits != 1 && bits != 2 && bits != 4 && bits != 8)
+        return fail(DOPT_EBITS, "bits must be one of (1,2,4,8). got %d", bits);
+    return DOPT_OK;
+}
+
+int check_group(int g) {
+    if (g < 64 || g > 1024 || (g & (g - 1)))
+        return fail(DOPT_EINVAL, "group_size must be a power of two in [64, 1024], got %d", g);
+    return DOPT_OK;
+}
+
+int ilog2(int v) {
+    int l = 0;
+    while ((1 << l) < v) ++l;
+    return l;
+}
+
+// Validates an optional [N, C, H, W] tile descriptor and returns (tiles_w, log2 s, row).
+int setup_tiles(const int64_t* t, int64_t n_groups, int g, uint32_t* tiled, uint32_t* tiles_w, uint32_t* log2s,
+                uint64_t* row) {
+    *tiled = 0;
+    *tiles_w = 1;
+    *log2s = 0;
+    *row = 0;
+    if (!t) return DOPT_OK;
+    int s = 1;
+    while (s * s < g) ++s;
+    if (s * s != g)
+        return fail(DOPT_EINVAL, "tile layout needs a square group size (s*s == g), got g=%d", g);
+    const int64_t N = t[0], C = t[1], H = t[2], W = t[3];
+    if (N < 0 || C < 0 || H <= 0 || W <= 0 || H % s || W % s)
+        return fail(DOPT_EINVAL, "tile layout needs H %% %d == 0 and W %% %d == 0 (got N=%lld C=%lld H=%lld W=%lld)", s,
+                    s, (long long)N, (long long)C, (long long)H, (long long)W);
+    if (N * C * (H / s) * (W / s) != n_groups)
+        return fail(DOPT_EINVAL, "n_groups=%lld does not match the tile layout (%lld)", (long long)n_groups,
+                    (long long)(N * C * (H / s) * (W / s)));
+    *tiled = 1;
+    *tiles_w = (uint32_t)(W / s);
+    *log2s = (uint32_t)ilog2(s);
+    *row = (uint64_t)W;
+    return DOPT_OK;
+}
+
+int hip_status(const char* what) {
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail(DOPT_EHIP, "%s: %s", what, hipGetErrorString(e));
+    return ok();
+}
+
+}  // namespace
+
+extern "C" {
+
+int dopt_abi_version(void) { return DOPT_ABI_VERSION; }
+
+const char* dopt_last_error(void) { return g_err; }
+
+int dopt_quant_pack(const void* x, int x_dtype, int64_t n_groups, int group_size, int bits, const int64_t* tile_nchw,
+                    int rounding, const float* noise, uint64_t seed, uint64_t offset, int flags, float clamp_alpha,
+                    uint32_t* packed, void* scale, void* minv, int meta_dtype, void* stream) {
+    int rc;
+    if ((rc = check_bits(bits))) return rc;
+    if ((rc = check_group(group_size))) return rc;
+    if (n_groups < 0 || n_groups >= (int64_t)1 << 31)
+        return fail(DOPT_EINVAL, "n_groups must be in [0, 2^31), got %lld", (long long)n_groups);
+    if (x_dtype != DOPT_F32 && x_dtype != DOPT_F16 && x_dtype != DOPT_BF16)
+        return fail(DOPT_EINVAL, "unsupported input dtype code %d", x_dtype);
+    if (meta_dtype != DOPT_F32 && meta_dtype != DOPT_BF16)
+        return fail(DOPT_EINVAL, "scale/min dtype must be F32 or BF16, got code %d", meta_dtype);
+    if (rounding < DOPT_ROUND_NEAREST || rounding > DOPT_ROUND_STOCH_PHILOX)
+        return fail(DOPT_EINVAL, "unknown rounding mode %d", rounding);
+    if (flags & ~(DOPT_FLAG_CLAMP | DOPT_FLAG_SQUASH)) return fail(DOPT_EINVAL, "unknown flags 0x%x", flags);
+    dopt::QuantPackArgs a{};
+    if ((rc = setup_tiles(tile_nchw, n_groups, group_size, &a.tiled, &a.tiles_w, &a.log2s, &a.row))) return rc;
+    if (n_groups == 0) return ok();
+    if (!x || !packed || !scale || !minv) return fail(DOPT_EINVAL, "null pointer argument");
+    if (!aligned16(x) || !aligned16(packed))
+        return fail(DOPT_EINVAL, "x and packed must be 16-byte aligned");
+    if (rounding == DOPT_ROUND_STOCH_NOISE && (!noise || !aligned16(noise)))
+        return fail(DOPT_EINVAL, "stochastic rounding with a noise tensor needs a 16-byte aligned fp32 noise pointer");
+    a.x = x;
+    a.noise = noise;
+    a.packed = packed;
+    a.scale = scale;
+    a.minv = minv;
+    a.n_groups = (uint32_t)n_groups;
+    a.seed_lo = (uint32_t)seed;
+    a.seed_hi = (uint32_t)(seed >> 32);
+    a.off_lo = (uint32_t)offset;
+    a.off_hi = (uint32_t)(offset >> 32);
+    a.clamp_alpha = clamp_alpha;
+    a.flags = (uint32_t)flags;
+    a.meta_bf16 = meta_dtype == DOPT_BF16;
+    hipStream_t s = (hipStream_t)stream;
+    (void)hipGetLastError();
+    switch (x_dtype) {
+        case DOPT_F32: rc = dopt::launch_quant_pack_dt<dopt::DT_F32>(a, bits, group_size, rounding, s); break;
+        case DOPT_F16: rc = dopt::launch_quant_pack_dt<dopt::DT_F16>(a, bits, group_size, rounding, s); break;
+        default: rc = dopt::launch_quant_pack_dt<dopt::DT_BF16>(a, bits, group_size, rounding, s); break;
+    }
+    if (rc) return fail(DOPT_EUNSUPPORTED, "no quant-pack kernel for bits=%d g=%d rounding=%d", bits, group_size, rounding);
+    return hip_status("quant_pack launch");
+}
+
+int dopt_dequant_unpack(const uint32_t* packed, const void* scale, const void* minv, int meta_dtype, int64_t n_groups,
+                        int group_size, int bits, const int64_t* tile_nchw, void* y, int y_dtype, void* stream) {
+    int rc;
+    if ((rc = check_bits(bits))) return rc;
+    if ((rc = check_group(group_size))) return rc;
+    if (n_groups < 0 || n_groups >= (int64_t)1 << 31)
+        return fail(DOPT_EINVAL, "n_groups must be in [0, 2^31), got %lld", (long long)n_groups);
+    if (meta_dtype != DOPT_F32 && meta_dtype != DOPT_BF16)
+        return fail(DOPT_EINVAL, "scale/min dtype must be F32 or BF16, got code %d", meta_dtype);
+    if (y_dtype != DOPT_F32 && y_dtype != DOPT_BF16)
+        return fail(DOPT_EINVAL, "output dtype must be F32 or BF16, got code %d", y_dtype);
+    dopt::DequantArgs a{};
+    if ((rc = setup_tiles(tile_nchw, n_groups, group_size, &a.tiled, &a.tiles_w, &a.log2s, &a.row))) return rc;
+    if (n_groups == 0) return ok();
+    if (!packed || !scale || !minv || !y) return fail(DOPT_EINVAL, "null pointer argument");
+    if (!aligned16(y) || ((uintptr_t)packed & 7u))
+        return fail(DOPT_EINVAL, "y must be 16-byte and packed 8-byte aligned");
+    a.packed = packed;
+    a.scale = scale;
+    a.minv = minv;
+    a.y = y;
+    a.n_groups = (uint32_t)n_groups;
+    a.meta_bf16 = meta_dtype == DOPT_BF16;
+    hipStream_t s = (hipStream_t)stream;
+    (void)hipGetLastError();
+    if (y_dtype == DOPT_F32)
+        rc = dopt::launch_dequant_unpack_dt<dopt::DT_F32>(a, bits, group_size, s);
+    else
+        rc = dopt::launch_dequant_unpack_dt<dopt::DT_BF16>(a, bits, group_size, s);
+    if (rc) return fail(DOPT_EUNSUPPORTED, "no dequant kernel for bits=%d g=%d", bits, group_size);
+    return hip_status("dequant_unpack launch");
+}
+
+int dopt_pack_codes(const int8_t* codes, int64_t n_groups, int group_size, int bits, uint32_t* packed, void* stream) {
+    int rc;
+    if ((rc = check_bits(bits))) return rc;
+    if ((rc = check_group(group_size))) return rc;
+    if (n_groups < 0) return fail(DOPT_EINVAL, "n_groups must be >= 0");
+    if (n_groups == 0) return ok();
+    if (!codes || !packed) return fail(DOPT_EINVAL, "null pointer argument");
+    if (!aligned16(codes) || ((uintptr_t)packed & 3u)) return fail(DOPT_EINVAL, "codes must be 16-byte aligned");
+    const uint64_t n_words = (uint64_t)n_groups * (uint64_t)(group_size * bits / 32);
+    (void)hipGetLastError();
+    dopt::launch_pack_codes(codes, packed, n_words, bits, (hipStream_t)stream);
+    return hip_status("pack_codes launch");
+}
+
+int dopt_unpack_codes(const uint32_t* packed, int64_t n_groups, int group_size, int bits, int8_t* codes, void* stream) {
+    int rc;
+    if ((rc = check_bits(bits))) return rc;
+    if ((rc = check_group(group_size))) return rc;
+    if (n_groups < 0) return fail(DOPT_EINVAL, "n_groups must be >= 0");
+    if (n_groups == 0) return ok();
+    if (!codes || !packed) return fail(DOPT_EINVAL, "null pointer argument");
+    if (!aligned16(codes) || ((uintptr_t)packed & 3u)) return fail(DOPT_EINVAL, "codes must be 16-byte aligned");
+    const uint64_t n_words = (uint64_t)n_groups * (uint64_t)(group_size * bits / 32);
+    (void)hipGetLastError();
+    dopt::launch_unpack_codes(packed, codes, n_words, bits, (hipStream_t)stream);
+    return hip_status("unpack_codes launch");
+}
+
+int dopt_fp8_gemm_nt(const uint8_t* A, const uint8_t* B, int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb,
+                     float out_scale, void* C, int64_t ldc, void* stream) {
+    if (M < 0 || N < 0 || K < 0) return fail(DOPT_EINVAL, "negative GEMM extent");
+    if (M == 0 || N == 0) return ok();
+    if (!A || !B || !C) return fail(DOPT_EINVAL, "null pointer argument");
+    if (M % 256 || N % 256 || K % 128)
+        return fail(DOPT_EUNSUPPORTED, "fp8 GEMM needs M %% 256 == 0, N %% 256 == 0, K %% 128 == 0 (got %lld, %lld, %lld)",
+                    (long long)M, (long long)N, (long long)K);
+    if (lda < K || ldb < K || ldc < N || lda % 16 || ldb % 16 || ldc % 8 || !aligned16(A) || !aligned16(B) ||
+        !aligned16(C))
+        return fail(DOPT_EINVAL, "fp8 GEMM needs 16-byte aligned rows with lda, ldb >= K and ldc >= N");
+    (void)hipGetLastError();
+    const int rc = dopt::launch_fp8_gemm_nt(A, B, M, N, K, lda, ldb, out_scale, (uint16_t*)C, ldc, (hipStream_t)stream);
+    if (rc) return fail(DOPT_EUNSUPPORTED, "fp8 GEMM launch configuration unsupported");
+    return hip_status("fp8_gemm launch");
+}
+
+}  // extern "C"

@@ -1,0 +1,131 @@
+// Device-side helpers shared by the gfx950 activation-compression kernels.
+//
+// Wave model: CDNA4 wavefronts are 64 lanes. A group of `group_size` values is spread over LPG
+// consecutive lanes (LPG a power of two, aligned), so every cross-lane reduction stays inside an
+// aligned LPG-lane block and is done with DPP lane permutes (no LDS round trip) up to 16 lanes,
+// and with ds_bpermute-based shuffles beyond that.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace dopt {
+
+enum { DT_F32 = 0, DT_F16 = 1, DT_BF16 = 2 };
+enum { RN_NEAREST = 0, RN_NOISE = 1, RN_PHILOX = 2 };
+enum { FL_CLAMP = 1, FL_SQUASH = 2 };
+
+template <int DT>
+struct DType {
+    static constexpr int bytes = DT == DT_F32 ? 4 : 2;
+    static constexpr int per16 = 16 / bytes;  // elements in one 16-byte chunk
+};
+
+// ------------------------------------------------------------------ lane permutes (DPP)
+// DPP controls: quad_perm [1,0,3,2] = 0xB1 (lane ^ 1), quad_perm [2,3,0,1] = 0x4E (lane ^ 2),
+// row_half_mirror = 0x141 (lane i <-> 7-i within 8), row_mirror = 0x140 (i <-> 15-i within 16),
+// row_shl:4 = 0x104 (lane i reads lane i+4 within its row of 16).
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, CTRL, 0xF, 0xF, true);
+}
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+    return __uint_as_float(dpp_u32<CTRL>(__float_as_uint(v)));
+}
+
+// All-reduce min and max over aligned blocks of LPG lanes. After the first two steps every lane
+// of a quad holds the quad's result, so the mirror permutes (which pair lane i with 7-i / 15-i)
+// combine exactly the two halves of the 8- and 16-lane blocks.
+template <int LPG>
+__device__ __forceinline__ void block_minmax(float& mn, float& mx) {
+    if constexpr (LPG >= 2) {
+        mn = fminf(mn, dpp_f32<0xB1>(mn));
+        mx = fmaxf(mx, dpp_f32<0xB1>(mx));
+    }
+    if constexpr (LPG >= 4) {
+        mn = fminf(mn, dpp_f32<0x4E>(mn));
+        mx = fmaxf(mx, dpp_f32<0x4E>(mx));
+    }
+    if constexpr (LPG >= 8) {
+        mn = fminf(mn, dpp_f32<0x141>(mn));
+        mx = fmaxf(mx, dpp_f32<0x141>(mx));
+    }
+    if constexpr (LPG >= 16) {
+        mn = fminf(mn, dpp_f32<0x140>(mn));
+        mx = fmaxf(mx, dpp_f32<0x140>(mx));
+    }
+    if constexpr (LPG >= 32) {
+        mn = fminf(mn, __shfl_xor(mn, 16, 64));
+        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    }
+    if constexpr (LPG >= 64) {
+        mn = fminf(mn, __shfl_xor(mn, 32, 64));
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    }
+}
+
+// ------------------------------------------------------------------ element conversions
+template <int DT>
+__device__ __forceinline__ void widen16(const uint4& r, float* f) {
+    const uint32_t w[4] = {r.x, r.y, r.z, r.w};
+    if constexpr (DT == DT_F32) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) f[k] = __uint_as_float(w[k]);
+    } else if constexpr (DT == DT_BF16) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            f[2 * k] = __uint_as_float(w[k] << 16);
+            f[2 * k + 1] = __uint_as_float(w[k] & 0xffff0000u);
+        }
+    } else {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            f[2 * k] = (float)__builtin_bit_cast(_Float16, (uint16_t)(w[k] & 0xffffu));
+            f[2 * k + 1] = (float)__builtin_bit_cast(_Float16, (uint16_t)(w[k] >> 16));
+        }
+    }
+}
+
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
+// Round-to-nearest-even fp32 pair -> packed bf16 pair (v_cvt_pk_bf16_f32 on gfx950).
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+    f32x2_t v = {lo, hi};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
+}
+
+__device__ __forceinline__ uint16_t to_bf16(float v) { return (uint16_t)(pack_bf16x2(v, 0.0f) & 0xffffu); }
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
+
+// ------------------------------------------------------------------ Philox4x32-10
+// Salmon et al., SC'11: multipliers 0xD2511F53 / 0xCD9E8D57, Weyl key increments
+// 0x9E3779B9 / 0xBB67AE85, key bumped between rounds.
+__device__ __forceinline__ uint4 philox4x32_10(uint32_t c0, uint32_t c1, uint32_t c2, uint32_t c3,
+                                               uint32_t k0, uint32_t k1) {
+#pragma unroll
+    for (int r = 0; r < 10; ++r) {
+        if (r) {
+            k0 += 0x9E3779B9u;
+            k1 += 0xBB67AE85u;
+        }
+        const uint64_t p0 = (uint64_t)0xD2511F53u * c0;
+        const uint64_t p1 = (uint64_t)0xCD9E8D57u * c2;
+        const uint32_t n0 = (uint32_t)(p1 >> 32) ^ c1 ^ k0;
+        const uint32_t n2 = (uint32_t)(p0 >> 32) ^ c3 ^ k1;
+        c1 = (uint32_t)p1;
+        c3 = (uint32_t)p0;
+        c0 = n0;
+        c2 = n2;
+    }
+    return make_uint4(c0, c1, c2, c3);
+}
+
+// 16-bit half h of a Philox word -> u = (h + 0.5) * 2^-16, exact in fp32.
+__device__ __forceinline__ float philox_half_to_u(uint32_t h16) {
+    return (float)h16 * (1.0f / 65536.0f) + (1.0f / 131072.0f);
+}
+
+}  // namespace dopt

@@ -1,0 +1,132 @@
+/*
+ * dopt.h - C ABI of the MI355X (gfx950) activation-compression library `libdopt.so`.
+ *
+ * The library replaces the device side of Deep_Optimization's activation compression:
+ *   - the Triton kernels and their `act_lib::*` ops in
+ *     Activation_Compression/act_triton_kernel.py:23-433, and
+ *   - the pybind surface of the CUDA extension in
+ *     Activation_Compression/cpp_extension/bind.cpp:44-63.
+ * Each entry point below cites the reference interface it replaces.
+ *
+ * Conventions shared by every entry point:
+ *   - Pointers are device pointers (HBM). The library never allocates, frees or synchronises;
+ *     the caller owns every buffer.
+ *   - `stream` is a hipStream_t passed as void*; NULL means the legacy default stream.
+ *     Work is enqueued asynchronously on that stream.
+ *   - Return value: DOPT_OK (0) or a negative DOPT_E* code. dopt_last_error() returns a
+ *     thread-local, human-readable message for the last failure on the calling thread.
+ *   - Packed codes form a little-endian bitstream per group: with b bits per code, element e of
+ *     a group occupies bits [e*b, e*b+b) of the group's block of group_size*b/32 uint32 words
+ *     (the word layout of act_triton_kernel.py:110-111 and :159-160).
+ *   - Groups are numbered r = 0..n_groups-1 in the order of the reference's [N, G, g] tensor.
+ */
+#ifndef DOPT_H
+#define DOPT_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define DOPT_ABI_VERSION 1
+
+/* element types */
+#define DOPT_F32 0
+#define DOPT_F16 1
+#define DOPT_BF16 2
+
+/* rounding modes */
+#define DOPT_ROUND_NEAREST 0 /* q = trunc((x-min)*inv + (0.5-1e-6)), act_triton_kernel.py:114,:155-157 */
+#define DOPT_ROUND_STOCH_NOISE 1 /* q = rint(((x-min)*inv + u) - 0.5), u read from a noise tensor */
+#define DOPT_ROUND_STOCH_PHILOX 2 /* same, u from Philox4x32-10(seed, offset), 16 bits/element */
+
+/* pre-transform flags (act_triton_kernel.py:55-58) */
+#define DOPT_FLAG_CLAMP 1 /* x = clamp(x, -alpha, alpha) */
+#define DOPT_FLAG_SQUASH 2 /* x = tanh(x / 0.5) * 0.5 (always on in the reference Triton path) */
+
+/* status codes */
+#define DOPT_OK 0
+#define DOPT_EBITS -1 /* bits not in {1,2,4,8}: the reference raises ValueError (act_triton_kernel.py:329-330) */
+#define DOPT_EINVAL -2 /* bad size, shape, dtype, layout, alignment or null pointer */
+#define DOPT_EUNSUPPORTED -3 /* a valid request this build does not implement */
+#define DOPT_EHIP -4 /* a HIP runtime error (launch failure, no device, ...) */
+
+/* Version of this ABI; bump on any signature change. */
+int dopt_abi_version(void);
+
+/* Message describing the last failure on the calling thread ("" if none). */
+const char* dopt_last_error(void);
+
+/*
+ * Per-group min/max quantize + bit-pack.
+ * Replaces act_lib::quant_pack_triton (act_triton_kernel.py:336-368, kernel :23-171) and the
+ * cpp_extension pack1..pack8 entry points (cpp_extension/bind.cpp:48-52,
+ * cpp_extension/src/quant_pack_dispatch.cpp:17-115).
+ *
+ *   x           input activations, dtype x_dtype (F32/F16/BF16), 16-byte aligned.
+ *               tile_nchw == NULL: contiguous [n_groups, group_size] (flat layout,
+ *               tensor_act_reshape_utils.py:46).
+ *               tile_nchw != NULL: a contiguous [N, C, H, W] tensor read through the s x s spatial
+ *               tile gather of tensor_act_reshape_utils.py:100-128 (s*s == group_size, H % s == 0,
+ *               W % s == 0, n_groups == N*C*(H/s)*(W/s)); the permuted copy is never materialised.
+ *   group_size  power of two in [64, 1024]
+ *   bits        1, 2, 4 or 8
+ *   rounding    DOPT_ROUND_*; noise (fp32 [n_groups, group_size] in group order, values in [0,1))
+ *               is read only for DOPT_ROUND_STOCH_NOISE; seed/offset only for DOPT_ROUND_STOCH_PHILOX.
+ *   flags       DOPT_FLAG_* bit set; clamp_alpha used with DOPT_FLAG_CLAMP.
+ *   packed      out: uint32 [n_groups, group_size*bits/32], 16-byte aligned.
+ *   scale, minv out: [n_groups] of meta_dtype (F32 or BF16): step = (max-min)/(2^b-1) (1.0 when
+ *               max == min) and the group minimum (act_triton_kernel.py:60-68).
+ */
+int dopt_quant_pack(const void* x, int x_dtype, int64_t n_groups, int group_size, int bits,
+                    const int64_t* tile_nchw, int rounding, const float* noise, uint64_t seed,
+                    uint64_t offset, int flags, float clamp_alpha, uint32_t* packed, void* scale,
+                    void* minv, int meta_dtype, void* stream);
+
+/*
+ * Unpack + dequantize: y = float(q) * scale + min, rounded once to y_dtype (F32 or BF16).
+ * Replaces act_lib::dequant_unpack_triton (act_triton_kernel.py:372-395, kernel :174-241) and
+ * the cpp_extension unpack1..unpack8 entry points (cpp_extension/bind.cpp:54-58,
+ * cpp_extension/src/dequant_unpack_dispatch.cpp:12-41).
+ *   tile_nchw == NULL: y is [n_groups, group_size]; otherwise y is the [N, C, H, W] tensor and
+ *   the inverse tile scatter of tensor_act_reshape_utils.py:131-154 is fused in.
+ */
+int dopt_dequant_unpack(const uint32_t* packed, const void* scale, const void* minv, int meta_dtype,
+                        int64_t n_groups, int group_size, int bits, const int64_t* tile_nchw,
+                        void* y, int y_dtype, void* stream);
+
+/*
+ * Code-only pack: int8 codes [n_groups, group_size] -> uint32 words [n_groups, group_size*bits/32],
+ * word = sum_j int32(code[j]) << (j*bits) with 32-bit wrap-around (identical to OR for codes in
+ * [0, 2^bits)). Replaces act_lib::pack_triton (act_triton_kernel.py:398-417, kernel :246-281).
+ */
+int dopt_pack_codes(const int8_t* codes, int64_t n_groups, int group_size, int bits,
+                    uint32_t* packed, void* stream);
+
+/*
+ * Code-only unpack: words -> int8 codes, code = (word >> (j*bits)) & (2^bits-1).
+ * Replaces act_lib::unpack_triton (act_triton_kernel.py:419-433, kernel :284-322).
+ */
+int dopt_unpack_codes(const uint32_t* packed, int64_t n_groups, int group_size, int bits,
+                      int8_t* codes, void* stream);
+
+/*
+ * FP8 (OCP e4m3) scaled GEMM, NT layout: C[m][n] = out_scale * sum_k A[m][k] * B[n][k],
+ * fp32 accumulation, C rounded once to bf16. A is [M, K] (row stride lda bytes), B is [N, K]
+ * (row stride ldb bytes), C is [M, N] bf16 (row stride ldc elements). out_scale is
+ * 1/(sA*sB) for per-tensor quantisation scales sX = 448/amax(X).
+ * The reference's counterpart is the scale-less Triton GEMM Triton_Linear
+ * (Activation_Compression/triton_kernel/linear.py:43-95, fp32 accumulate :81-86, cast :91), which
+ * has no callers; the contraction it stands for is the weight/input-gradient GEMM of
+ * _DOLinear.backward (Activation_Compression/modules/ops.py:508-512).
+ * Requires M % 256 == 0, N % 256 == 0, K % 128 == 0, 16-byte aligned rows.
+ */
+int dopt_fp8_gemm_nt(const uint8_t* A, const uint8_t* B, int64_t M, int64_t N, int64_t K,
+                     int64_t lda, int64_t ldb, float out_scale, void* C, int64_t ldc, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DOPT_H */

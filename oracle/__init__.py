@@ -1,0 +1,188 @@
+"""CPU oracle for the activation-compression hot path (TEST INFRASTRUCTURE ONLY).
+
+This package is the checker, never the product: only ``tests/``, ``__graft_entry__.smoke()`` and
+``bench.py``'s ``cpu_baseline`` leg may import it. The product path (``deep_optimization_amd``)
+never imports, links or calls anything under ``oracle/``.
+
+``liboracle.so`` is built from ``dopt_oracle.c`` (a C restatement of the reference quantizer,
+Activation_Compression/act_triton_kernel.py:23-433, with the stochastic form of
+Activation_Compression/cpp_extension/include/quant_common.h:148-156) by ``oracle/Makefile``.
+The wrappers here take and return numpy arrays and mirror the C ABI of ``include/dopt.h``.
+
+Parity status per function is listed in the header of ``dopt_oracle.c``; the squash pre-transform
+(tanh) is "parity unpinned" at bit level.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "liboracle.so")
+
+F32, F16, BF16 = 0, 1, 2
+NEAREST, STOCH_NOISE, STOCH_PHILOX = 0, 1, 2
+FLAG_CLAMP, FLAG_SQUASH = 1, 2
+
+_lib = None
+
+
+def build(force: bool = False) -> str:
+    """Compile liboracle.so with the committed Makefile (gcc + OpenMP)."""
+    if force and os.path.exists(_LIB_PATH):
+        os.remove(_LIB_PATH)
+    subprocess.run(["make", "-s", "-C", _HERE], check=True)
+    return _LIB_PATH
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            build()
+        L = ctypes.CDLL(_LIB_PATH)
+        vp, i64, i32, u64 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_uint64
+        L.oracle_quant_pack.argtypes = [vp, i32, i64, i32, i32, vp, i32, vp, u64, u64, i32,
+                                        ctypes.c_float, vp, vp, vp, i32]
+        L.oracle_quant_pack.restype = i32
+        L.oracle_dequant_unpack.argtypes = [vp, vp, vp, i32, i64, i32, i32, vp, vp, i32]
+        L.oracle_dequant_unpack.restype = i32
+        L.oracle_pack_codes.argtypes = [vp, i64, i32, i32, vp]
+        L.oracle_pack_codes.restype = i32
+        L.oracle_unpack_codes.argtypes = [vp, i64, i32, i32, vp]
+        L.oracle_unpack_codes.restype = i32
+        L.oracle_philox4x32_10.argtypes = [vp, vp, vp]
+        L.oracle_philox4x32_10.restype = None
+        L.oracle_philox_noise.argtypes = [i64, i64, u64, u64, vp]
+        L.oracle_philox_noise.restype = None
+        L.oracle_num_threads.restype = i32
+        L.oracle_set_num_threads.argtypes = [i32]
+        L.oracle_f32_to_bf16.argtypes = [ctypes.c_float]
+        L.oracle_f32_to_bf16.restype = ctypes.c_uint16
+        _lib = L
+    return _lib
+
+
+def _ptr(a):
+    return None if a is None else a.ctypes.data
+
+
+def _dtype_code(a: np.ndarray) -> int:
+    """numpy storage -> ABI dtype code. bf16 travels as uint16 bit patterns; fp16 as float16."""
+    if a.dtype == np.float32:
+        return F32
+    if a.dtype == np.float16:
+        return F16
+    if a.dtype == np.uint16:
+        return BF16
+    raise TypeError(f"unsupported oracle input dtype {a.dtype}")
+
+
+class OracleError(RuntimeError):
+    pass
+
+
+def _check(rc: int):
+    if rc == -1:
+        raise ValueError("bits must be one of (1,2,4,8)")
+    if rc != 0:
+        raise OracleError(f"oracle returned {rc}")
+
+
+def quant_pack(x: np.ndarray, group_size: int, bits: int, *, tile_nchw=None, rounding=NEAREST,
+               noise=None, seed=0, offset=0, flags=0, clamp_alpha=0.0, meta_dtype=F32):
+    """Returns (packed uint32 [NG, W], scale [NG], min [NG]); meta as float32 or uint16 (bf16)."""
+    x = np.ascontiguousarray(x)
+    if tile_nchw is not None:
+        n, c, h, w = (int(v) for v in tile_nchw)
+        s = int(round(group_size ** 0.5))
+        ng = n * c * (h // s) * (w // s)
+        tile = np.array([n, c, h, w], dtype=np.int64)
+    else:
+        ng = x.size // group_size
+        tile = None
+    nw = group_size * bits // 32
+    packed = np.zeros((ng, nw), dtype=np.uint32)
+    mdt = np.float32 if meta_dtype == F32 else np.uint16
+    scale = np.zeros(ng, dtype=mdt)
+    mn = np.zeros(ng, dtype=mdt)
+    if noise is not None:
+        noise = np.ascontiguousarray(noise, dtype=np.float32)
+    rc = lib().oracle_quant_pack(_ptr(x), _dtype_code(x), ng, group_size, bits, _ptr(tile),
+                                 rounding, _ptr(noise), seed, offset, flags, clamp_alpha,
+                                 _ptr(packed), _ptr(scale), _ptr(mn), meta_dtype)
+    _check(rc)
+    return packed, scale, mn
+
+
+def dequant_unpack(packed, scale, mn, group_size: int, bits: int, *, tile_nchw=None, y_dtype=F32):
+    """Returns y float32 (or uint16 bf16 bits): [NG, g] flat, or the [N, C, H, W] tensor."""
+    packed = np.ascontiguousarray(packed, dtype=np.uint32)
+    ng = packed.size * 32 // bits // group_size
+    meta_dtype = F32 if scale.dtype == np.float32 else BF16
+    if tile_nchw is not None:
+        shape = tuple(int(v) for v in tile_nchw)
+        tile = np.array(shape, dtype=np.int64)
+    else:
+        shape = (ng, group_size)
+        tile = None
+    y = np.zeros(shape, dtype=np.float32 if y_dtype == F32 else np.uint16)
+    rc = lib().oracle_dequant_unpack(_ptr(packed), _ptr(np.ascontiguousarray(scale)),
+                                     _ptr(np.ascontiguousarray(mn)), meta_dtype, ng, group_size,
+                                     bits, _ptr(tile), _ptr(y), y_dtype)
+    _check(rc)
+    return y
+
+
+def pack_codes(codes: np.ndarray, group_size: int, bits: int) -> np.ndarray:
+    codes = np.ascontiguousarray(codes, dtype=np.int8)
+    ng = codes.size // group_size
+    out = np.zeros((ng, group_size * bits // 32), dtype=np.uint32)
+    _check(lib().oracle_pack_codes(_ptr(codes), ng, group_size, bits, _ptr(out)))
+    return out
+
+
+def unpack_codes(packed: np.ndarray, group_size: int, bits: int) -> np.ndarray:
+    packed = np.ascontiguousarray(packed, dtype=np.uint32)
+    ng = packed.size * 32 // bits // group_size
+    out = np.zeros((ng, group_size), dtype=np.int8)
+    _check(lib().oracle_unpack_codes(_ptr(packed), ng, group_size, bits, _ptr(out)))
+    return out
+
+
+def philox4x32_10(ctr, key) -> np.ndarray:
+    c = np.array(ctr, dtype=np.uint32)
+    k = np.array(key, dtype=np.uint32)
+    out = np.zeros(4, dtype=np.uint32)
+    lib().oracle_philox4x32_10(_ptr(c), _ptr(k), _ptr(out))
+    return out
+
+
+def philox_noise(idx0: int, n: int, seed: int, offset: int) -> np.ndarray:
+    out = np.zeros(n, dtype=np.float32)
+    lib().oracle_philox_noise(idx0, n, seed, offset, _ptr(out))
+    return out
+
+
+def f32_to_bf16_bits(a: np.ndarray) -> np.ndarray:
+    """Round-to-nearest-even fp32 -> bf16 bit patterns (uint16), vectorised in numpy."""
+    u = np.ascontiguousarray(a, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    nan = (u & 0x7FFFFFFF) > 0x7F800000
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    r[nan] = ((u[nan] >> 16) | 0x40).astype(np.uint16)
+    return r
+
+
+def bf16_bits_to_f32(b: np.ndarray) -> np.ndarray:
+    return (np.ascontiguousarray(b, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def num_threads() -> int:
+    return int(lib().oracle_num_threads())
+
+
+def set_num_threads(n: int) -> None:
+    lib().oracle_set_num_threads(int(n))

@@ -1,0 +1,341 @@
+/*
+ * dopt_oracle.c - CPU restatement of Deep_Optimization's activation-compression quantizer.
+ *
+ * TEST INFRASTRUCTURE ONLY. This file is the checker for the HIP library: only tests/,
+ * __graft_entry__.smoke() and bench.py's cpu_baseline leg may load it. It is never linked into,
+ * or called by, the product path (deep_optimization_amd/).
+ *
+ * Every entry point mirrors the C ABI in include/dopt.h (same argument meaning, no stream) and
+ * cites the reference lines it restates. Paths are relative to the reference repository;
+ * AC/ = Activation_Compression/.
+ *
+ * Arithmetic contract (built with -ffp-contract=off, no -ffast-math, round-to-nearest-even):
+ *   every fp32 operation below is rounded separately, in the order written.
+ *
+ * Parity status of each function (how it is pinned; the tests in tests/test_oracle.py do it):
+ *   grouping (flat / tile gather)  pinned: brute-force index maps + torch view/permute restatement
+ *   min/max/step/inv               pinned: closed forms and known-answer groups
+ *   nearest codes                  pinned: known-answer groups, |deq-x| <= step/2 bound, numpy
+ *                                  restatement
+ *   stochastic codes (noise)       pinned: closed form with a given noise tensor, |deq-x| < step
+ *   bit packing                    pinned: numpy.packbits(bitorder='little') special case
+ *   dequant                        pinned: closed form
+ *   Philox4x32-10                  pinned: published known-answer vectors (Salmon et al., SC'11)
+ *   squash (tanh(2x)/2)            parity unpinned at bit level: the reference uses libdevice tanh
+ *                                  on an NVIDIA GPU; this oracle uses the C library's tanhf.
+ */
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+#define O_F32 0
+#define O_F16 1
+#define O_BF16 2
+
+#define O_NEAREST 0
+#define O_STOCH_NOISE 1
+#define O_STOCH_PHILOX 2
+
+#define O_FLAG_CLAMP 1
+#define O_FLAG_SQUASH 2
+
+#define O_OK 0
+#define O_EBITS -1
+#define O_EINVAL -2
+
+/* ---------------------------------------------------------------- scalar conversions */
+
+static float u2f(uint32_t u) {
+    float f;
+    memcpy(&f, &u, 4);
+    return f;
+}
+static uint32_t f2u(float f) {
+    uint32_t u;
+    memcpy(&u, &f, 4);
+    return u;
+}
+
+static float bf16_to_f32(uint16_t h) { return u2f((uint32_t)h << 16); }
+
+/* round-to-nearest-even fp32 -> bf16 (the rule of c10::BFloat16); NaN -> quiet NaN */
+static uint16_t f32_to_bf16(float f) {
+    uint32_t u = f2u(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+
+static float f16_to_f32(uint16_t h) {
+    uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+    uint32_t ex = (h >> 10) & 0x1fu, man = h & 0x3ffu;
+    if (ex == 0) {
+        float v = (float)man * (1.0f / 16777216.0f); /* man * 2^-24, exact */
+        return u2f(f2u(v) | sign);
+    }
+    if (ex == 31) return u2f(sign | 0x7f800000u | (man << 13));
+    return u2f(sign | ((ex + 112u) << 23) | (man << 13));
+}
+
+static float load_elem(const void* x, int dtype, int64_t i) {
+    if (dtype == O_F32) return ((const float*)x)[i];
+    if (dtype == O_BF16) return bf16_to_f32(((const uint16_t*)x)[i]);
+    return f16_to_f32(((const uint16_t*)x)[i]);
+}
+
+/* ---------------------------------------------------------------- Philox4x32-10
+ * Counter-based generator of Salmon, Moraes, Dror, Shaw, "Parallel random numbers: as easy as
+ * 1, 2, 3", SC'11: round (c0,c1,c2,c3) -> (hi(M1*c2)^c1^k0, lo(M1*c2), hi(M0*c0)^c3^k1, lo(M0*c0))
+ * with M0 = 0xD2511F53, M1 = 0xCD9E8D57; the key is bumped by the Weyl constants
+ * (0x9E3779B9, 0xBB67AE85) between rounds. */
+void oracle_philox4x32_10(const uint32_t ctr[4], const uint32_t key[2], uint32_t out[4]) {
+    uint32_t c0 = ctr[0], c1 = ctr[1], c2 = ctr[2], c3 = ctr[3];
+    uint32_t k0 = key[0], k1 = key[1];
+    for (int r = 0; r < 10; ++r) {
+        if (r) {
+            k0 += 0x9E3779B9u;
+            k1 += 0xBB67AE85u;
+        }
+        uint64_t p0 = (uint64_t)0xD2511F53u * c0;
+        uint64_t p1 = (uint64_t)0xCD9E8D57u * c2;
+        uint32_t n0 = (uint32_t)(p1 >> 32) ^ c1 ^ k0;
+        uint32_t n1 = (uint32_t)p1;
+        uint32_t n2 = (uint32_t)(p0 >> 32) ^ c3 ^ k1;
+        uint32_t n3 = (uint32_t)p0;
+        c0 = n0;
+        c1 = n1;
+        c2 = n2;
+        c3 = n3;
+    }
+    out[0] = c0;
+    out[1] = c1;
+    out[2] = c2;
+    out[3] = c3;
+}
+
+/* Noise for element `idx` (group-order linear index r*g + e) in Philox mode: the 8-element block
+ * idx>>3 is the counter {blk_lo, blk_hi, offset_lo, offset_hi}, the seed is the key; element k of
+ * the block takes 16-bit half (k&1) of word k>>1, and u = (h + 0.5) * 2^-16 (exact in fp32). */
+static float philox_u(int64_t idx, uint64_t seed, uint64_t offset) {
+    uint64_t blk = (uint64_t)idx >> 3;
+    uint32_t ctr[4] = {(uint32_t)blk, (uint32_t)(blk >> 32), (uint32_t)offset,
+                       (uint32_t)(offset >> 32)};
+    uint32_t key[2] = {(uint32_t)seed, (uint32_t)(seed >> 32)};
+    uint32_t w[4];
+    oracle_philox4x32_10(ctr, key, w);
+    int k = (int)(idx & 7);
+    uint32_t h = (w[k >> 1] >> ((k & 1) * 16)) & 0xffffu;
+    return (float)h * (1.0f / 65536.0f) + (1.0f / 131072.0f);
+}
+
+/* Philox noise values for n consecutive group-order indices starting at idx0 (test helper). */
+void oracle_philox_noise(int64_t idx0, int64_t n, uint64_t seed, uint64_t offset, float* u) {
+    for (int64_t i = 0; i < n; ++i) u[i] = philox_u(idx0 + i, seed, offset);
+}
+
+/* ---------------------------------------------------------------- group layout
+ * Element e of group r, as a linear index into x.
+ * Flat: r*g + e (tensor_act_reshape_utils.py:46 `X.reshape(N, -1, Group_Size)`).
+ * Tiles (tensor_act_reshape_utils.py:115-125): x viewed (N, C, H/s, s, W/s, s), permuted
+ * (0,1,2,4,3,5), reshaped (N, C*(H/s)*(W/s), s*s): group r = ((n*C + c)*(H/s) + th)*(W/s) + tw
+ * holds x[n, c, th*s + e/s, tw*s + e%s]. */
+static int64_t elem_index(int64_t r, int e, int g, const int64_t* t, int s) {
+    if (!t) return r * g + e;
+    int64_t W = t[3], nW = W / s;
+    int64_t band = r / nW, tw = r % nW;
+    return band * s * W + tw * s + (int64_t)(e / s) * W + (e % s);
+}
+
+static int check_common(int64_t n_groups, int g, int bits, const int64_t* t, int* s_out) {
+    if (bits != 1 && bits != 2 && bits != 4 && bits != 8) return O_EBITS;
+    if (n_groups < 0 || g < 64 || g > 1024 || (g & (g - 1))) return O_EINVAL;
+    *s_out = 0;
+    if (t) {
+        int s = (int)lrint(sqrt((double)g));
+        if (s * s != g) return O_EINVAL;
+        if (t[0] < 0 || t[1] < 0 || t[2] <= 0 || t[3] <= 0) return O_EINVAL;
+        if (t[2] % s || t[3] % s) return O_EINVAL;
+        if (t[0] * t[1] * (t[2] / s) * (t[3] / s) != n_groups) return O_EINVAL;
+        *s_out = s;
+    }
+    return O_OK;
+}
+
+/* ---------------------------------------------------------------- quant-pack
+ * AC/act_triton_kernel.py:53-171 per group (one Triton program per group):
+ *   x = f32(x); [clamp(x, -a, a)] (:55-56); [x = tanh(x/0.5)*0.5] (:58)
+ *   mn = min(x), mx = max(x) (:60-61); rng = mx - mn; step = rng > 0 ? rng/QMAX : 1 (:63-65)
+ *   inv = 1/step (:71)
+ *   nearest: q = clamp(trunc((x-mn)*inv + f32(0.5-1e-6)), 0, QMAX) (:114, :155-157)
+ *   stochastic (the dormant CUDA form, AC/cpp_extension/include/quant_common.h:148-156, with the
+ *   Triton step convention): q = clamp(rint_even(((x-mn)*inv + u) - 0.5), 0, QMAX)
+ *   word[w] = OR_j q[w*VPW + j] << (j*b) (:110-111, :159-160)
+ *   scale = step, min = mn (:67-68; stored in meta_dtype).
+ * Two definitions this restatement makes explicit (the reference leaves them to the hardware):
+ *   - the stored minimum is canonicalised with mn + 0.0f, so -0.0 is stored as +0.0;
+ *   - the code of a NaN is 0 (the clamp is applied in the float domain before truncation, which
+ *     equals trunc-then-clamp for every non-NaN value). */
+int oracle_quant_pack(const void* x, int x_dtype, int64_t n_groups, int g, int bits,
+                      const int64_t* tile_nchw, int rounding, const float* noise, uint64_t seed,
+                      uint64_t offset, int flags, float clamp_alpha, uint32_t* packed, void* scale,
+                      void* minv, int meta_dtype) {
+    int s = 0;
+    int rc = check_common(n_groups, g, bits, tile_nchw, &s);
+    if (rc) return rc;
+    if (x_dtype != O_F32 && x_dtype != O_F16 && x_dtype != O_BF16) return O_EINVAL;
+    if (meta_dtype != O_F32 && meta_dtype != O_BF16) return O_EINVAL;
+    if (rounding < 0 || rounding > 2) return O_EINVAL;
+    if (rounding == O_STOCH_NOISE && !noise) return O_EINVAL;
+    const int QMAX = (1 << bits) - 1;
+    const int VPW = 32 / bits, NW = g / VPW;
+    const float qmaxf = (float)QMAX;
+    const float half_m = (float)(0.5 - 1e-6); /* 0x3EFFFFDE */
+
+#pragma omp parallel
+    {
+        float* xs = (float*)malloc(sizeof(float) * g);
+        int* q = (int*)malloc(sizeof(int) * g);
+#pragma omp for schedule(static)
+        for (int64_t r = 0; r < n_groups; ++r) {
+            for (int e = 0; e < g; ++e) {
+                float v = load_elem(x, x_dtype, elem_index(r, e, g, tile_nchw, s));
+                if (flags & O_FLAG_CLAMP) v = fminf(fmaxf(v, -clamp_alpha), clamp_alpha);
+                if (flags & O_FLAG_SQUASH) v = tanhf(v / 0.5f) * 0.5f;
+                xs[e] = v;
+            }
+            float mn = xs[0], mx = xs[0];
+            for (int e = 1; e < g; ++e) {
+                mn = fminf(mn, xs[e]);
+                mx = fmaxf(mx, xs[e]);
+            }
+            mn = mn + 0.0f;
+            float rng = mx - mn;
+            float step = (rng > 0.0f) ? rng / qmaxf : 1.0f;
+            float inv = 1.0f / step;
+            for (int e = 0; e < g; ++e) {
+                float t = xs[e] - mn;
+                t = t * inv;
+                float qf;
+                if (rounding == O_NEAREST) {
+                    qf = t + half_m;
+                } else {
+                    float u = (rounding == O_STOCH_NOISE) ? noise[r * g + e]
+                                                          : philox_u(r * g + e, seed, offset);
+                    qf = t + u;
+                    qf = qf - 0.5f;
+                }
+                if (qf != qf) qf = 0.0f;
+                qf = fminf(fmaxf(qf, 0.0f), qmaxf);
+                q[e] = (rounding == O_NEAREST) ? (int)qf : (int)rintf(qf);
+            }
+            for (int w = 0; w < NW; ++w) {
+                uint32_t word = 0;
+                for (int j = 0; j < VPW; ++j) word |= (uint32_t)q[w * VPW + j] << (j * bits);
+                packed[r * NW + w] = word;
+            }
+            if (meta_dtype == O_F32) {
+                ((float*)scale)[r] = step;
+                ((float*)minv)[r] = mn;
+            } else {
+                ((uint16_t*)scale)[r] = f32_to_bf16(step);
+                ((uint16_t*)minv)[r] = f32_to_bf16(mn);
+            }
+        }
+        free(xs);
+        free(q);
+    }
+    return O_OK;
+}
+
+/* ---------------------------------------------------------------- dequant-unpack
+ * AC/act_triton_kernel.py:199-241: q = (word >> (j*b)) & QMAX (:206-210);
+ * y = f32(q)*scale + min (:223, scale/min widened to fp32 :201-204), one rounding to y_dtype
+ * (:241). With tiles the inverse layout of tensor_act_reshape_utils.py:131-154 is applied. */
+int oracle_dequant_unpack(const uint32_t* packed, const void* scale, const void* minv,
+                          int meta_dtype, int64_t n_groups, int g, int bits,
+                          const int64_t* tile_nchw, void* y, int y_dtype) {
+    int s = 0;
+    int rc = check_common(n_groups, g, bits, tile_nchw, &s);
+    if (rc) return rc;
+    if (meta_dtype != O_F32 && meta_dtype != O_BF16) return O_EINVAL;
+    if (y_dtype != O_F32 && y_dtype != O_BF16) return O_EINVAL;
+    const uint32_t QMAX = (1u << bits) - 1u;
+    const int VPW = 32 / bits, NW = g / VPW;
+#pragma omp parallel for schedule(static)
+    for (int64_t r = 0; r < n_groups; ++r) {
+        float sc, mn;
+        if (meta_dtype == O_F32) {
+            sc = ((const float*)scale)[r];
+            mn = ((const float*)minv)[r];
+        } else {
+            sc = bf16_to_f32(((const uint16_t*)scale)[r]);
+            mn = bf16_to_f32(((const uint16_t*)minv)[r]);
+        }
+        for (int e = 0; e < g; ++e) {
+            uint32_t word = packed[r * NW + e / VPW];
+            uint32_t qv = (word >> ((e % VPW) * bits)) & QMAX;
+            float v = (float)qv * sc;
+            v = v + mn;
+            int64_t o = elem_index(r, e, g, tile_nchw, s);
+            if (y_dtype == O_F32)
+                ((float*)y)[o] = v;
+            else
+                ((uint16_t*)y)[o] = f32_to_bf16(v);
+        }
+    }
+    return O_OK;
+}
+
+/* ---------------------------------------------------------------- code-only pack / unpack
+ * AC/act_triton_kernel.py:266-271: words = sum_j int32(int8 code[j]) << (j*b), int32 wrap-around.
+ * AC/act_triton_kernel.py:304-322: code = (word >> (j*b)) & QMAX, stored as int8. */
+int oracle_pack_codes(const int8_t* codes, int64_t n_groups, int g, int bits, uint32_t* packed) {
+    int s = 0;
+    int rc = check_common(n_groups, g, bits, NULL, &s);
+    if (rc) return rc;
+    const int VPW = 32 / bits;
+    const int64_t nw = n_groups * (g / VPW);
+    for (int64_t w = 0; w < nw; ++w) {
+        uint32_t acc = 0;
+        for (int j = 0; j < VPW; ++j)
+            acc += (uint32_t)(int32_t)codes[w * VPW + j] << (j * bits);
+        packed[w] = acc;
+    }
+    return O_OK;
+}
+
+int oracle_unpack_codes(const uint32_t* packed, int64_t n_groups, int g, int bits, int8_t* codes) {
+    int s = 0;
+    int rc = check_common(n_groups, g, bits, NULL, &s);
+    if (rc) return rc;
+    const int VPW = 32 / bits;
+    const uint32_t QMAX = (1u << bits) - 1u;
+    const int64_t nw = n_groups * (g / VPW);
+    for (int64_t w = 0; w < nw; ++w)
+        for (int j = 0; j < VPW; ++j)
+            codes[w * VPW + j] = (int8_t)((packed[w] >> (j * bits)) & QMAX);
+    return O_OK;
+}
+
+/* ---------------------------------------------------------------- helpers for tests / bench */
+int oracle_num_threads(void) {
+#ifdef _OPENMP
+    return omp_get_max_threads();
+#else
+    return 1;
+#endif
+}
+
+void oracle_set_num_threads(int n) {
+#ifdef _OPENMP
+    if (n > 0) omp_set_num_threads(n);
+#else
+    (void)n;
+#endif
+}
+
+uint16_t oracle_f32_to_bf16(float f) { return f32_to_bf16(f); }

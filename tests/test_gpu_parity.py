@@ -1,0 +1,346 @@
+"""GPU parity: the gfx950 kernels (through act_lib -> C ABI) against the CPU oracle.
+
+Bar: bit-exact packed words, scale, min and dequantized values for nearest rounding and for
+stochastic rounding with a given noise tensor or the Philox stream (the oracle implements the
+same generator); tolerance only for the tanh squash, whose libm/ocml tanh differ in the last
+ulp. Small ragged sizes sweep every (dtype, bits, group size, rounding) kernel; BASELINE's full
+ResNet size is checked bit-exact against the oracle and through size-independent bounds.
+"""
+import numpy as np
+import pytest
+import torch
+
+import deep_optimization_amd  # noqa: F401
+import oracle
+from deep_optimization_amd import _lib
+from tests.golden import make_golden
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+TORCH_TO_ORACLE = {torch.float32: oracle.F32, torch.float16: oracle.F16, torch.bfloat16: oracle.BF16}
+ROUNDINGS = {"nearest": oracle.NEAREST, "noise": oracle.STOCH_NOISE, "philox": oracle.STOCH_PHILOX}
+
+
+def np_view(t: torch.Tensor) -> np.ndarray:
+    """CPU numpy view with the oracle's storage convention (bf16 as uint16 bit patterns)."""
+    t = t.detach().cpu().contiguous()
+    if t.dtype == torch.bfloat16:
+        return t.view(torch.int16).numpy().view(np.uint16)
+    if t.dtype == torch.int32:
+        return t.numpy().view(np.uint32)
+    return t.numpy()
+
+
+def make_input(shape, dtype, seed):
+    gen = torch.Generator().manual_seed(seed)
+    x = torch.randn(shape, generator=gen)
+    # vary the dynamic range across the leading rows so steps differ per group
+    scale = torch.exp(torch.randn(shape[:-1] + (1,), generator=gen) * 2)
+    return (x * scale).to(dtype)
+
+
+def gpu_quant(x, bits, g, rounding, noise=None, seed=0, offset=0, scale_dtype=torch.float32, clamp=False,
+              alpha=0.0, squash=False, tile=False):
+    op = torch.ops.act_lib.quant_pack_tiles if tile else torch.ops.act_lib.quant_pack
+    out = op(x.to(DEV), bits, g, clamp, alpha, squash, ROUNDINGS[rounding], None if noise is None else noise.to(DEV),
+             seed, offset, scale_dtype)
+    torch.cuda.synchronize()
+    return out
+
+
+def oracle_quant(x, bits, g, rounding, noise=None, seed=0, offset=0, meta=oracle.F32, flags=0, alpha=0.0,
+                 tile=None):
+    xn = np_view(x)
+    return oracle.quant_pack(xn if tile else xn.reshape(-1, g), g, bits, tile_nchw=tile, rounding=ROUNDINGS[rounding],
+                             noise=None if noise is None else noise.numpy(), seed=seed, offset=offset, flags=flags,
+                             clamp_alpha=alpha, meta_dtype=meta)
+
+
+def assert_quant_equal(gpu, ref, what=""):
+    p, s, m = gpu
+    rp, rs, rm = ref
+    np.testing.assert_array_equal(np_view(p).reshape(rp.shape), rp, err_msg=f"packed {what}")
+    np.testing.assert_array_equal(np_view(s).reshape(-1), rs, err_msg=f"scale {what}")
+    np.testing.assert_array_equal(np_view(m).reshape(-1), rm, err_msg=f"min {what}")
+
+
+# ----------------------------------------------------------------------------- flat quant-pack sweep
+@pytest.mark.parametrize("rounding", ["nearest", "noise", "philox"])
+@pytest.mark.parametrize("g", [64, 128, 256, 512, 1024])
+@pytest.mark.parametrize("bits", [1, 2, 4, 8])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32], ids=["bf16", "f16", "f32"])
+def test_quant_pack_flat_parity(dtype, bits, g, rounding):
+    NG = 1 + 67 * (1024 // g)  # ragged: not a multiple of any groups-per-wave count
+    x = make_input((1, NG, g), dtype, seed=bits * 100 + g)
+    noise = torch.rand((1, NG, g), generator=torch.Generator().manual_seed(7)) if rounding == "noise" else None
+    gpu = gpu_quant(x, bits, g, rounding, noise, seed=77, offset=5)
+    ref = oracle_quant(x, bits, g, rounding, noise, seed=77, offset=5)
+    assert_quant_equal(gpu, ref, f"{dtype} b{bits} g{g} {rounding}")
+
+
+@pytest.mark.parametrize("bits", [1, 2, 4, 8])
+@pytest.mark.parametrize("g", [64, 256, 1024])
+@pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float32], ids=["bf16", "f32"])
+@pytest.mark.parametrize("meta", [torch.float32, torch.bfloat16], ids=["meta32", "meta16"])
+def test_dequant_flat_parity(bits, g, out_dtype, meta):
+    NG = 3 + 41 * (1024 // g)
+    x = make_input((1, NG, g), torch.bfloat16, seed=bits + g)
+    mo = oracle.F32 if meta == torch.float32 else oracle.BF16
+    rp, rs, rm = oracle_quant(x, bits, g, "nearest", meta=mo)
+    yo = oracle.dequant_unpack(rp, rs, rm, g, bits, y_dtype=TORCH_TO_ORACLE[out_dtype])
+    p = torch.from_numpy(rp.view(np.int32)).to(DEV)
+    if meta == torch.bfloat16:
+        s = torch.from_numpy(rs.view(np.int16)).view(torch.bfloat16).to(DEV).view(1, NG)
+        m = torch.from_numpy(rm.view(np.int16)).view(torch.bfloat16).to(DEV).view(1, NG)
+    else:
+        s = torch.from_numpy(rs).to(DEV).view(1, NG)
+        m = torch.from_numpy(rm).to(DEV).view(1, NG)
+    y = torch.ops.act_lib.dequant_unpack(p, s, m, bits, g, out_dtype)
+    np.testing.assert_array_equal(np_view(y).reshape(yo.shape), yo)
+
+
+# ----------------------------------------------------------------------------- tile layout
+TILE_CASES = [((2, 3, 32, 48), 256), ((1, 4, 16, 40), 64), ((1, 2, 64, 32), 1024), ((3, 5, 8, 8), 64),
+              ((2, 2, 48, 16), 256)]
+
+
+@pytest.mark.parametrize("shape,g", TILE_CASES)
+@pytest.mark.parametrize("rounding", ["nearest", "noise", "philox"])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=["bf16", "f32"])
+def test_quant_pack_tiles_parity(shape, g, rounding, dtype):
+    bits = 2 if g == 256 else 4
+    x = make_input(shape, dtype, seed=sum(shape) + g)
+    n_groups = shape[0] * shape[1] * (shape[2] * shape[3] // g)
+    noise = torch.rand(n_groups * g, generator=torch.Generator().manual_seed(3)) if rounding == "noise" else None
+    gpu = gpu_quant(x, bits, g, rounding, noise, seed=3, offset=11, tile=True)
+    ref = oracle_quant(x, bits, g, rounding, noise, seed=3, offset=11, tile=shape)
+    assert_quant_equal(gpu, ref, f"tiles {shape} g{g}")
+    y = torch.ops.act_lib.dequant_unpack_tiles(*gpu, bits, g, *shape, torch.bfloat16)
+    yo = oracle.dequant_unpack(*ref, g, bits, tile_nchw=shape, y_dtype=oracle.BF16)
+    np.testing.assert_array_equal(np_view(y), yo)
+
+
+# ----------------------------------------------------------------------------- committed fixtures
+@pytest.mark.parametrize("name", sorted(make_golden.CASES))
+def test_golden_fixtures(name):
+    case = make_golden.load_all()[name]
+    _, kw = make_golden.CASES[name]
+    g, bits = kw["group_size"], kw["bits"]
+    tile = kw.get("tile")
+    if name == "c1_cpu_config":
+        x = torch.from_numpy(make_golden.c1_input())
+    elif case["x"].dtype == np.uint16:
+        x = torch.from_numpy(case["x"].view(np.int16)).view(torch.bfloat16)
+    else:
+        x = torch.from_numpy(case["x"])
+    noise = torch.from_numpy(case["noise"]) if "noise" in case else None
+    rounding = {oracle.NEAREST: "nearest", oracle.STOCH_NOISE: "noise", oracle.STOCH_PHILOX: "philox"}[kw["rounding"]]
+    meta = torch.float32 if kw["meta_dtype"] == oracle.F32 else torch.bfloat16
+    flags = kw.get("flags", 0)
+    xin = x if tile else x.reshape(1, -1, g)
+    gpu = gpu_quant(xin, bits, g, rounding, noise, seed=kw.get("seed", 0), offset=kw.get("offset", 0),
+                    scale_dtype=meta, clamp=bool(flags & 1), alpha=kw.get("clamp_alpha", 0.0),
+                    squash=bool(flags & 2), tile=tile is not None)
+    if flags & 2:
+        # tanh squash: the GPU's tanhf and the C library's may differ in the last ulp
+        codes_gpu = oracle.unpack_codes(np_view(gpu[0]), g, bits).astype(int)
+        codes_ref = oracle.unpack_codes(case["packed"], g, bits).astype(int)
+        assert np.max(np.abs(codes_gpu - codes_ref)) <= 1 and np.mean(codes_gpu != codes_ref) < 1e-3
+        return
+    np.testing.assert_array_equal(np_view(gpu[0]).reshape(case["packed"].shape), case["packed"])
+    np.testing.assert_array_equal(np_view(gpu[1]).reshape(-1), case["scale"])
+    np.testing.assert_array_equal(np_view(gpu[2]).reshape(-1), case["min"])
+    out_dtype = torch.float32 if kw["y_dtype"] == oracle.F32 else torch.bfloat16
+    if tile:
+        y = torch.ops.act_lib.dequant_unpack_tiles(*gpu, bits, g, *tile, out_dtype)
+    else:
+        y = torch.ops.act_lib.dequant_unpack(*gpu, bits, g, out_dtype)
+    want = case["y"] if "y" in case else oracle.dequant_unpack(case["packed"], case["scale"], case["min"], g, bits,
+                                                                 tile_nchw=tile, y_dtype=kw["y_dtype"])
+    np.testing.assert_array_equal(np_view(y).reshape(want.shape), want)
+
+
+# ----------------------------------------------------------------------------- code-only pack
+@pytest.mark.parametrize("bits", [1, 2, 4, 8])
+@pytest.mark.parametrize("g", [64, 256, 1024])
+def test_pack_unpack_codes_parity(bits, g):
+    gen = torch.Generator().manual_seed(bits + g)
+    codes = torch.randint(-128, 128, (3, 37, g), generator=gen, dtype=torch.int8)
+    if bits == 1:
+        codes = (codes > 0).to(torch.int8)  # the masks the reference packs
+    w = torch.ops.act_lib.pack_triton(codes.to(DEV), bits, g)
+    want = oracle.pack_codes(codes.numpy().reshape(-1, g), g, bits)
+    np.testing.assert_array_equal(np_view(w), want)
+    back = torch.ops.act_lib.unpack_triton(w, bits, 3, 37, g)
+    np.testing.assert_array_equal(back.cpu().numpy().reshape(-1, g), oracle.unpack_codes(want, g, bits))
+
+
+# ----------------------------------------------------------------------------- reference-schema ops
+@pytest.mark.parametrize("bits", [1, 2, 4, 8])
+def test_reference_schema_ops(bits):
+    g = 256
+    x = make_input((4, 50, g), torch.bfloat16, seed=bits)
+    p, s, m = torch.ops.act_lib.quant_pack_triton(x.to(DEV), bits, g, False, 0, True, 3.0)
+    assert s.dtype == torch.bfloat16 and s.shape == (4, 50) and p.shape == (200, g * bits // 32)
+    rp, rs, rm = oracle_quant(x, bits, g, "nearest", meta=oracle.BF16, flags=3, alpha=3.0)
+    # squash (tanh) is tolerance-only: scale/min within 1 bf16 ulp, codes within 1 and rarely off
+    rs32 = oracle.bf16_bits_to_f32(rs)
+    np.testing.assert_allclose(s.float().cpu().numpy().reshape(-1), rs32, rtol=2 ** -7, atol=0)
+    np.testing.assert_allclose(m.float().cpu().numpy().reshape(-1), oracle.bf16_bits_to_f32(rm), rtol=2 ** -7,
+                               atol=1e-30)
+    cg = oracle.unpack_codes(np_view(p), g, bits).astype(int)
+    cr = oracle.unpack_codes(rp, g, bits).astype(int)
+    assert np.max(np.abs(cg - cr)) <= 1 and np.mean(cg != cr) < 1e-3
+    # dequant of the GPU's own packed data is bit-exact against the oracle
+    y = torch.ops.act_lib.dequant_unpack_triton(p, s, m, bits, g, False, 0)
+    assert y.dtype == torch.bfloat16 and y.shape == (4, 50, g)
+    yo = oracle.dequant_unpack(np_view(p), np_view(s).reshape(-1), np_view(m).reshape(-1), g, bits,
+                               y_dtype=oracle.BF16)
+    np.testing.assert_array_equal(np_view(y).reshape(yo.shape), yo)
+
+
+def test_avg_alam_is_rejected():
+    x = torch.zeros(1, 1, 256, dtype=torch.bfloat16, device=DEV)
+    with pytest.raises(NotImplementedError):
+        torch.ops.act_lib.quant_pack_triton(x, 2, 256, True, 2, False, 0.0)
+
+
+def test_bad_bits_raise_value_error_on_device():
+    x = torch.zeros(1, 1, 256, dtype=torch.bfloat16, device=DEV)
+    with pytest.raises(ValueError):
+        torch.ops.act_lib.quant_pack_triton(x, 3, 256, False, 0, False, 0.0)
+
+
+# ----------------------------------------------------------------------------- edge cases
+def test_special_values_bit_exact():
+    g = 256
+    x = make_input((1, 9, g), torch.float32, seed=5)
+    x[0, 0, 3] = float("inf")
+    x[0, 1, 7] = float("-inf")
+    x[0, 2, 11] = float("nan")
+    x[0, 3, :] = -0.0
+    x[0, 3, 5] = 0.0
+    x[0, 4, :] = 1e-40  # subnormal group
+    x[0, 4, 9] = 3e-40
+    x[0, 5, :] = 7.0  # constant
+    x[0, 6, :] = 3e38  # range overflows to inf
+    x[0, 6, 1] = -3e38
+    for rounding in ("nearest", "philox"):
+        gpu = gpu_quant(x, 2, g, rounding, seed=1, offset=2)
+        ref = oracle_quant(x, 2, g, rounding, seed=1, offset=2)
+        assert_quant_equal(gpu, ref, rounding)
+
+
+def test_empty_and_single_group():
+    x = torch.zeros((0, 4, 256), dtype=torch.bfloat16, device=DEV)
+    p, s, m = torch.ops.act_lib.quant_pack(x, 2, 256, False, 0.0, False, 0, None, 0, 0, torch.float32)
+    assert p.shape == (0, 16) and s.shape == (0, 4)
+    y = torch.ops.act_lib.dequant_unpack(p, s, m, 2, 256, torch.bfloat16)
+    assert y.shape == (0, 4, 256)
+    x1 = make_input((1, 1, 1024), torch.float32, seed=9)
+    assert_quant_equal(gpu_quant(x1, 8, 1024, "nearest"), oracle_quant(x1, 8, 1024, "nearest"))
+
+
+def test_misaligned_input_view():
+    base = make_input((1, 40 * 256 + 3), torch.bfloat16, seed=2)
+    x = base[:, 3:].reshape(1, 40, 256)  # storage offset of 6 bytes
+    gpu = gpu_quant(x, 2, 256, "nearest")
+    ref = oracle_quant(x.contiguous(), 2, 256, "nearest")
+    assert_quant_equal(gpu, ref)
+
+
+def test_stream_ordering_on_side_stream():
+    x = make_input((2, 300, 256), torch.bfloat16, seed=4).to(DEV)
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        p, sc, m = torch.ops.act_lib.quant_pack(x, 4, 256, False, 0.0, False, 0, None, 0, 0, torch.float32)
+        y = torch.ops.act_lib.dequant_unpack(p, sc, m, 4, 256, torch.float32)
+    s.synchronize()
+    ref = oracle_quant(x.cpu(), 4, 256, "nearest")
+    assert_quant_equal((p, sc, m), ref)
+    yo = oracle.dequant_unpack(*ref, 256, 4)
+    np.testing.assert_array_equal(y.cpu().numpy().reshape(yo.shape), yo)
+
+
+# ----------------------------------------------------------------------------- BASELINE full sizes
+@pytest.fixture(scope="module")
+def resnet_act():
+    """bf16 [256, 256, 56, 56] post-ReLU |N(0,1)|, g = 256, 2-bit."""
+    gen = torch.Generator(device=DEV).manual_seed(0)
+    x = torch.randn((256, 256, 56, 56), generator=gen, device=DEV, dtype=torch.float32).abs_().to(torch.bfloat16)
+    return x
+
+
+def test_resnet_full_size_nearest_bit_exact(resnet_act):
+    g = 256
+    x = resnet_act.view(256, -1, g)
+    p, s, m = torch.ops.act_lib.quant_pack(x, 2, g, False, 0.0, False, 0, None, 0, 0, torch.float32)
+    torch.cuda.synchronize()
+    ref = oracle.quant_pack(np_view(x).reshape(-1, g), g, 2)
+    assert_quant_equal((p, s, m), ref, "resnet nearest")
+    # round trip bound (size independent): |deq - x| <= step * (0.5 + 1e-6) + fp32 rounding
+    y = torch.ops.act_lib.dequant_unpack(p, s, m, 2, g, torch.float32)
+    err = (y - x.float()).abs()
+    step = s.view(256, -1, 1)
+    assert bool((err <= step * 0.500002 + 1e-6 * (1 + x.float().abs())).all())
+
+
+def test_resnet_full_size_stochastic(resnet_act):
+    g = 256
+    x = resnet_act.view(256, -1, g)
+    noise = torch.rand(x.shape, generator=torch.Generator(device=DEV).manual_seed(1), device=DEV)
+    p, s, m = torch.ops.act_lib.quant_pack(x, 2, g, False, 0.0, False, ROUNDINGS["noise"], noise, 0, 0,
+                                           torch.float32)
+    y = torch.ops.act_lib.dequant_unpack(p, s, m, 2, g, torch.float32)
+    step = s.view(256, -1, 1)
+    assert bool(((y - x.float()).abs() < step * (1 + 1e-5)).all())
+    # bit-exact on a slice of 2048 groups against the oracle with the same noise
+    sl = slice(0, 2048)
+    xs = np_view(x.reshape(-1, g)[sl])
+    ref = oracle.quant_pack(xs, g, 2, rounding=oracle.STOCH_NOISE, noise=noise.reshape(-1, g)[sl].cpu().numpy())
+    np.testing.assert_array_equal(np_view(p[sl]), ref[0])
+    np.testing.assert_array_equal(np_view(s).reshape(-1)[sl], ref[1])
+    # Philox: unbiased in aggregate (mean dequant error ~ 0 over 205M elements)
+    p2, s2, m2 = torch.ops.act_lib.quant_pack(x, 2, g, False, 0.0, False, ROUNDINGS["philox"], None, 1, 0,
+                                              torch.float32)
+    y2 = torch.ops.act_lib.dequant_unpack(p2, s2, m2, 2, g, torch.float32)
+    rel = float((y2.double() - x.double()).mean() / s2.double().mean())
+    assert abs(rel) < 1e-3
+
+
+# ----------------------------------------------------------------------------- FP8 GEMM
+def fp8_quantize(x):
+    s = 448.0 / x.abs().max().clamp_min(1e-12)
+    return (x * s).to(torch.float8_e4m3fn), s
+
+
+@pytest.mark.parametrize("M,N,K", [(256, 256, 128), (512, 768, 1024), (1024, 256, 4096), (4096, 11008, 4096)])
+def test_fp8_gemm_parity(M, N, K):
+    gen = torch.Generator(device=DEV).manual_seed(M + N + K)
+    a = torch.randn(M, K, generator=gen, device=DEV)
+    b = torch.randn(N, K, generator=gen, device=DEV)
+    a8, sa = fp8_quantize(a)
+    b8, sb = fp8_quantize(b)
+    out_scale = float(1.0 / (sa * sb))
+    c = torch.ops.act_lib.fp8_gemm_nt(a8, b8, out_scale)
+    ref = (a8.float() @ b8.float().t()) * out_scale
+    rel = float((c.float() - ref).norm() / ref.norm())
+    assert rel <= 1e-2, rel
+    # elementwise: within bf16 rounding of the fp32 result
+    assert bool(((c.float() - ref).abs() <= ref.abs() * 2 ** -7 + 1e-3 * ref.abs().max()).all())
+
+
+def test_fp8_gemm_rejects_bad_shapes():
+    a = torch.zeros(100, 128, dtype=torch.float8_e4m3fn, device=DEV)
+    b = torch.zeros(256, 128, dtype=torch.float8_e4m3fn, device=DEV)
+    with pytest.raises(RuntimeError, match="fp8 GEMM"):
+        torch.ops.act_lib.fp8_gemm_nt(a, b, 1.0)
+
+
+def test_native_library_is_loaded():
+    import ctypes  # noqa: F401
+
+    assert _lib.lib().dopt_abi_version() == 1
+    with open("/proc/self/maps") as f:
+        assert "libdopt.so" in f.read()
