@@ -1,12 +1,14 @@
-// gfx950 unpack-dequant kernel: y = float(q) * scale + min, one rounding to the output type.
-// Semantics follow Activation_Compression/act_triton_kernel.py:199-241; with the tile layout the
-// inverse scatter of tensor_act_reshape_utils.py:131-154 is fused into the stores.
+// gfx950 unpack-dequant kernel: y = fma(float(q), scale, min), one rounding to the output type.
+// Semantics follow Activation_Compression/act_triton_kernel.py:199-241 (`q * scale + xmin`,
+// compiled by Triton with FMA contraction); with the tile layout the inverse scatter of
+// tensor_act_reshape_utils.py:131-154 is fused into the stores.
 //
-// Work decomposition mirrors quant_pack.h: LPG lanes per group, each lane CPL 16-byte output
-// chunks c = i*LPG + li (whole-cache-line stores per instruction), P passes per iteration.
-// Per-group scale/min of the wave's GPW groups are staged once in LDS (one coalesced load per
-// array) and read back by the LPG lanes of each group; codes are read as the dword (or dword
-// pair) holding the chunk's E*BITS bits.
+// Work decomposition mirrors quant_pack.h: a lane owns units of UE output elements (UB bytes,
+// written as UB/16 consecutive 16-byte stores), a group's CPG units are spread over LPG lanes
+// (unit c = i*LPG + li), and a wave handles GPW = P*64/LPG groups. The wave's GPW scales and
+// minima are staged once in LDS (one coalesced load per array) and read back by the lanes of
+// each group; a unit's UE*BITS code bits are read as the one dword (or 2/4-dword vector) that
+// holds them.
 #pragma once
 
 #include "dopt_device.h"
@@ -26,19 +28,23 @@ struct DequantArgs {
     uint32_t meta_bf16;
 };
 
-template <int YT, int BITS, int G>
+template <int YT, int BITS, int G, int UB, int LPG_, int P, bool NT>
 struct DequantCfg {
-    static constexpr int E = DType<YT>::per16;
-    static constexpr int CPG = G / E;
-    static constexpr int CPL = CPG >= 32 ? 4 : (CPG >= 16 ? 2 : 1);
-    static constexpr int LPG = CPG / CPL;
+    static constexpr int BYTES = DType<YT>::bytes;
+    static constexpr int UE = UB / BYTES;
+    static constexpr int STORES = UB / 16;
+    static constexpr int CPG = G / UE;
+    static constexpr int LPG = LPG_ ? LPG_ : (CPG < 64 ? CPG : 64);  // lanes per group
+    static constexpr int CPL = CPG / LPG;
     static constexpr int GPP = 64 / LPG;
-    static constexpr int P = 8 / CPL;
     static constexpr int GPW = P * GPP;
     static constexpr int W = G * BITS / 32;
-    static constexpr int PW = E * BITS;
+    static constexpr int UBITS = UE * BITS;
+    static constexpr int CW = UBITS >= 32 ? UBITS / 32 : 1;  // code dwords read per unit
     static constexpr int WAVES = 4;
-    static_assert(LPG >= 4 && LPG <= 64, "group must span 4..64 lanes");
+    static_assert(UB % 16 == 0 && UE * BYTES == UB, "unit must be whole 16-byte stores");
+    static_assert(CPG * UE == G && LPG * CPL == CPG, "group must split evenly over lanes");
+    static_assert(UBITS <= 128, "a unit reads at most one 16-byte code vector");
     static_assert(GPW <= 64, "one lane per staged group");
 };
 
@@ -52,12 +58,13 @@ __device__ __forceinline__ uint64_t dq_elem_index(const DequantArgs& a, uint32_t
            (uint64_t)(e0 >> a.log2s) * a.row + (e0 & smask);
 }
 
-template <int YT, int BITS, int G>
+template <int YT, int BITS, int G, int UB, int LPG_, int P, bool NT>
 __global__ __launch_bounds__(256) void dequant_unpack_kernel(DequantArgs a) {
-    using C = DequantCfg<YT, BITS, G>;
-    constexpr int E = C::E, CPL = C::CPL, LPG = C::LPG, GPP = C::GPP, P = C::P, W = C::W;
-    constexpr int PW = C::PW;
+    using C = DequantCfg<YT, BITS, G, UB, LPG_, P, NT>;
+    constexpr int UE = C::UE, STORES = C::STORES, CPL = C::CPL, LPG = C::LPG, GPP = C::GPP, W = C::W;
+    constexpr int UBITS = C::UBITS, CW = C::CW;
     constexpr uint32_t QMAX = (1u << BITS) - 1u;
+    constexpr int E16 = DType<YT>::per16;
 
     __shared__ float s_scale[C::WAVES][C::GPW];
     __shared__ float s_min[C::WAVES][C::GPW];
@@ -85,25 +92,32 @@ __global__ __launch_bounds__(256) void dequant_unpack_kernel(DequantArgs a) {
         s_min[wv][lane] = mn;
     }
 
-    // ---- code loads: the dword(s) holding each chunk's E*BITS bits
-    uint32_t cw[P][CPL][PW > 32 ? 2 : 1];
+    // ---- code loads: the dword(s) holding each unit's UE*BITS bits
+    uint32_t cw[P][CPL][CW];
 #pragma unroll
     for (int p = 0; p < P; ++p) {
         const uint32_t r = g0 + p * GPP + slot;
         const bool ok = r < a.n_groups;
+        const uint32_t* src = a.packed + (uint64_t)r * W;
 #pragma unroll
         for (int i = 0; i < CPL; ++i) {
             const uint32_t c = (uint32_t)(i * LPG + li);
-            const uint32_t* src = a.packed + (uint64_t)r * W;
-            if constexpr (PW > 32) {
+            if constexpr (CW == 4) {
+                uint4 d = make_uint4(0u, 0u, 0u, 0u);
+                if (ok) d = *(const uint4*)(src + 4 * c);
+                cw[p][i][0] = d.x;
+                cw[p][i][1] = d.y;
+                cw[p][i][2] = d.z;
+                cw[p][i][3] = d.w;
+            } else if constexpr (CW == 2) {
                 uint2 d = make_uint2(0u, 0u);
                 if (ok) d = *(const uint2*)(src + 2 * c);
                 cw[p][i][0] = d.x;
                 cw[p][i][1] = d.y;
             } else {
                 uint32_t d = 0u;
-                if (ok) d = src[(c * PW) / 32];
-                cw[p][i][0] = d >> ((c * PW) % 32);
+                if (ok) d = src[(c * UBITS) / 32];
+                cw[p][i][0] = UBITS >= 32 ? d : d >> ((c * UBITS) % 32);
             }
         }
     }
@@ -119,26 +133,25 @@ __global__ __launch_bounds__(256) void dequant_unpack_kernel(DequantArgs a) {
 #pragma unroll
         for (int i = 0; i < CPL; ++i) {
             const uint32_t c = (uint32_t)(i * LPG + li);
-            float out[E];
+            float out[UE];
 #pragma unroll
-            for (int k = 0; k < E; ++k) {
-                uint32_t q;
-                if constexpr (PW > 32)
-                    q = (cw[p][i][(k * BITS) / 32] >> ((k * BITS) % 32)) & QMAX;
-                else
-                    q = (cw[p][i][0] >> (k * BITS)) & QMAX;
-                float t = (float)q * sc;
-                out[k] = t + mn;
+            for (int k = 0; k < UE; ++k) {
+                const uint32_t q = (cw[p][i][(k * BITS) / 32] >> ((k * BITS) % 32)) & QMAX;
+                out[k] = __builtin_fmaf((float)q, sc, mn);
             }
-            uint4 v;
-            if constexpr (YT == DT_F32) {
-                v = make_uint4(__float_as_uint(out[0]), __float_as_uint(out[1]), __float_as_uint(out[2]),
-                               __float_as_uint(out[3]));
-            } else {
-                v = make_uint4(pack_bf16x2(out[0], out[1]), pack_bf16x2(out[2], out[3]),
-                               pack_bf16x2(out[4], out[5]), pack_bf16x2(out[6], out[7]));
+#pragma unroll
+            for (int l = 0; l < STORES; ++l) {
+                const float* o = &out[l * E16];
+                uint4 v;
+                if constexpr (YT == DT_F32) {
+                    v = make_uint4(__float_as_uint(o[0]), __float_as_uint(o[1]), __float_as_uint(o[2]),
+                                   __float_as_uint(o[3]));
+                } else {
+                    v = make_uint4(pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3]), pack_bf16x2(o[4], o[5]),
+                                   pack_bf16x2(o[6], o[7]));
+                }
+                if (ok) st16<NT>(yb + dq_elem_index<G>(a, r, c * UE + l * E16) * C::BYTES, v);
             }
-            if (ok) *(uint4*)(yb + dq_elem_index<G>(a, r, c * E) * DType<YT>::bytes) = v;
         }
     }
 }

@@ -107,6 +107,8 @@ int dopt_quant_pack(const void* x, int x_dtype, int64_t n_groups, int group_size
     if (rounding < DOPT_ROUND_NEAREST || rounding > DOPT_ROUND_STOCH_PHILOX)
         return fail(DOPT_EINVAL, "unknown rounding mode %d", rounding);
     if (flags & ~(DOPT_FLAG_CLAMP | DOPT_FLAG_SQUASH)) return fail(DOPT_EINVAL, "unknown flags 0x%x", flags);
+    if (flags && rounding != DOPT_ROUND_NEAREST)
+        return fail(DOPT_EUNSUPPORTED, "the clamp/squash pre-transform is implemented with nearest rounding only");
     dopt::QuantPackArgs a{};
     if ((rc = setup_tiles(tile_nchw, n_groups, group_size, &a.tiled, &a.tiles_w, &a.log2s, &a.row))) return rc;
     if (n_groups == 0) return ok();
@@ -131,9 +133,9 @@ int dopt_quant_pack(const void* x, int x_dtype, int64_t n_groups, int group_size
     hipStream_t s = (hipStream_t)stream;
     (void)hipGetLastError();
     switch (x_dtype) {
-        case DOPT_F32: rc = dopt::launch_quant_pack_dt<dopt::DT_F32>(a, bits, group_size, rounding, s); break;
-        case DOPT_F16: rc = dopt::launch_quant_pack_dt<dopt::DT_F16>(a, bits, group_size, rounding, s); break;
-        default: rc = dopt::launch_quant_pack_dt<dopt::DT_BF16>(a, bits, group_size, rounding, s); break;
+        case DOPT_F32: rc = dopt::launch_quant_pack_dt<dopt::DT_F32>(a, bits, group_size, rounding, flags != 0, s); break;
+        case DOPT_F16: rc = dopt::launch_quant_pack_dt<dopt::DT_F16>(a, bits, group_size, rounding, flags != 0, s); break;
+        default: rc = dopt::launch_quant_pack_dt<dopt::DT_BF16>(a, bits, group_size, rounding, flags != 0, s); break;
     }
     if (rc) return fail(DOPT_EUNSUPPORTED, "no quant-pack kernel for bits=%d g=%d rounding=%d", bits, group_size, rounding);
     return hip_status("quant_pack launch");

@@ -65,6 +65,29 @@ __device__ __forceinline__ void block_minmax(float& mn, float& mx) {
     }
 }
 
+// ------------------------------------------------------------------ 16-byte global access
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+// 16-byte load / store, optionally non-temporal (streamed data touched once: the nt bit keeps
+// it from displacing reusable lines).
+template <bool NT>
+__device__ __forceinline__ uint4 ld16(const void* p) {
+    u32x4_t v;
+    if constexpr (NT)
+        v = __builtin_nontemporal_load((const u32x4_t*)p);
+    else
+        v = *(const u32x4_t*)p;
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+template <bool NT>
+__device__ __forceinline__ void st16(void* p, const uint4& d) {
+    const u32x4_t v = {d.x, d.y, d.z, d.w};
+    if constexpr (NT)
+        __builtin_nontemporal_store(v, (u32x4_t*)p);
+    else
+        *(u32x4_t*)p = v;
+}
+
 // ------------------------------------------------------------------ element conversions
 template <int DT>
 __device__ __forceinline__ void widen16(const uint4& r, float* f) {
@@ -102,7 +125,12 @@ __device__ __forceinline__ float bf16_bits_to_f32(uint16_t b) { return __uint_as
 
 // ------------------------------------------------------------------ Philox4x32-10
 // Salmon et al., SC'11: multipliers 0xD2511F53 / 0xCD9E8D57, Weyl key increments
-// 0x9E3779B9 / 0xBB67AE85, key bumped between rounds.
+// 0x9E3779B9 / 0xBB67AE85, key bumped between rounds. Each round is two 32x32->64 multiplies
+// (v_mad_u64_u32) and two 3-input XORs (v_bitop3_b32 with truth table 0x96 = a ^ b ^ c).
+__device__ __forceinline__ uint32_t xor3(uint32_t a, uint32_t b, uint32_t c) {
+    return __builtin_amdgcn_bitop3_b32(a, b, c, 0x96);
+}
+
 __device__ __forceinline__ uint4 philox4x32_10(uint32_t c0, uint32_t c1, uint32_t c2, uint32_t c3,
                                                uint32_t k0, uint32_t k1) {
 #pragma unroll
@@ -113,8 +141,8 @@ __device__ __forceinline__ uint4 philox4x32_10(uint32_t c0, uint32_t c1, uint32_
         }
         const uint64_t p0 = (uint64_t)0xD2511F53u * c0;
         const uint64_t p1 = (uint64_t)0xCD9E8D57u * c2;
-        const uint32_t n0 = (uint32_t)(p1 >> 32) ^ c1 ^ k0;
-        const uint32_t n2 = (uint32_t)(p0 >> 32) ^ c3 ^ k1;
+        const uint32_t n0 = xor3((uint32_t)(p1 >> 32), c1, k0);
+        const uint32_t n2 = xor3((uint32_t)(p0 >> 32), c3, k1);
         c1 = (uint32_t)p1;
         c3 = (uint32_t)p0;
         c0 = n0;
@@ -123,9 +151,11 @@ __device__ __forceinline__ uint4 philox4x32_10(uint32_t c0, uint32_t c1, uint32_
     return make_uint4(c0, c1, c2, c3);
 }
 
-// 16-bit half h of a Philox word -> u = (h + 0.5) * 2^-16, exact in fp32.
-__device__ __forceinline__ float philox_half_to_u(uint32_t h16) {
-    return (float)h16 * (1.0f / 65536.0f) + (1.0f / 131072.0f);
+// Byte k (0..3) of a Philox output word -> u = (b + 0.5) / 256 in (0, 1). The fma is exact
+// (b * 2^-8 + 2^-9 has at most 9 significant bits), so it equals the separately rounded form.
+__device__ __forceinline__ float philox_byte_to_u(uint32_t w, int k) {
+    const float b = (float)((w >> (8 * k)) & 0xffu);  // v_cvt_f32_ubyte<k>
+    return __builtin_fmaf(b, 1.0f / 256.0f, 1.0f / 512.0f);
 }
 
 }  // namespace dopt

@@ -1,19 +1,34 @@
 // gfx950 quant-pack kernel: per-group min/max, 1/2/4/8-bit nearest or stochastic rounding and
 // little-endian bit-packing. Semantics follow Activation_Compression/act_triton_kernel.py:53-171
 // (nearest) and the stochastic form of cpp_extension/include/quant_common.h:148-156 with the
-// Triton step convention; see include/dopt.h for the ABI.
+// Triton step convention; include/dopt.h documents the ABI.
 //
 // Work decomposition (one wavefront = 64 lanes):
-//   - a group of G elements is E*CPG values in 16-byte chunks (E = 16/sizeof(elem));
-//   - LPG consecutive lanes own one group, each lane CPL chunks: chunk c = i*LPG + li for
-//     i < CPL, so every load instruction reads LPG*16 contiguous bytes per group (>= 128 B,
-//     whole cache lines) and the wave's loads are 16-byte vector loads;
-//   - a wave handles GPP = 64/LPG groups per pass and P passes per iteration (P*CPL 16-byte
-//     loads in flight per lane), all issued before any arithmetic;
-//   - min/max: lane-local, then a DPP all-reduce over the LPG lanes (no LDS);
-//   - codes: each lane packs its chunk into a E*BITS-bit piece; pieces narrower than a dword are
-//     merged with DPP from neighbour lanes; dwords are staged in a wave-private LDS slice and
-//     written back with coalesced 128-bit stores (the wave's output block is contiguous).
+//   - a lane owns "units" of UE contiguous elements (UB bytes, read as UB/16 consecutive 16-byte
+//     loads); a group of G elements is CPG = G/UE units spread over LPG lanes, CPL units per lane
+//     (unit c = i*LPG + li), so each load instruction covers LPG*UB contiguous bytes per group;
+//   - a wave handles GPP = 64/LPG groups per pass and P passes, with every load of the wave
+//     issued before any arithmetic;
+//   - min/max: lane-local v_min3/v_max3, then a DPP all-reduce over the group's LPG lanes;
+//   - codes go straight from registers to HBM: a unit's UE*BITS code bits are one dword (or a
+//     2/4-dword vector), narrower pieces are merged across neighbouring lanes with DPP first, so
+//     consecutive lanes store consecutive dwords; per-group scale/min of all GPW groups are
+//     gathered into lanes 0..GPW-1 and written with one store per array.
+//
+// Arithmetic (the reference kernels are compiled with FMA contraction on: Triton's default
+// enable_fp_fusion and nvcc's default --fmad=true, so `a * b + c` is one rounding):
+//   nearest     q = trunc(fma(x - mn, inv, fp32(0.5 - 1e-6)))   act_triton_kernel.py:114, :155
+//   stochastic  q = rint(fma(x - mn, inv, u) - 0.5)              quant_common.h:150-151
+// Fast path and its exactness argument. For finite x in [mn, mx] with inv = 1/step finite, the
+// exact product (x - mn) * inv is at most QMAX * (1 + 2^-22), so both forms already land in
+// [0, QMAX] before the reference's clamp (u < 1): the clamp is redundant and v_cvt_u32_f32
+// (truncating, NaN -> 0) gives the exact code. An infinite input or an overflowing range gives
+// inv = 0 and a product of 0 or NaN (code 0 either way, as with the reference's clamp). The only
+// case that needs the explicit clamp is inv = +inf (step < 2^-128, a range of a few
+// subnormals); a wave containing such a group takes the clamped path. Local min/max use raw
+// v_min3/v_max3 (no NaN canonicalisation); a signalling NaN input would turn a lane's partial
+// result into NaN, so a wave with a NaN partial result recomputes min/max with IEEE fminf/fmaxf,
+// which ignore NaN operands.
 #pragma once
 
 #include "dopt_device.h"
@@ -37,28 +52,39 @@ struct QuantPackArgs {
     uint32_t meta_bf16;
 };
 
-template <int DT, int BITS, int G, int RN>
+// Philox noise layout: element idx (group-order index r*G + e) belongs to block idx / NOISE_EPC;
+// the block number is the Philox counter's low 64 bits (offset in the high 64), the seed is the
+// key, and element k of the block takes byte k of the 128-bit output (little-endian word order):
+// u = (byte + 0.5) / 256.
+constexpr int NOISE_BITS = 8;
+constexpr int NOISE_EPC = 128 / NOISE_BITS;  // elements per Philox4x32-10 call
+
+template <int DT, int BITS, int G, int RN, int UB, int LPG_, int P>
 struct QuantPackCfg {
-    static constexpr int E = DType<DT>::per16;
-    static constexpr int CPG = G / E;
-    static constexpr int CPL = CPG >= 32 ? 4 : (CPG >= 16 ? 2 : 1);
-    static constexpr int LPG = CPG / CPL;
+    static constexpr int BYTES = DType<DT>::bytes;
+    static constexpr int UE = UB / BYTES;  // elements per unit
+    static constexpr int LOADS = UB / 16;  // 16-byte loads per unit
+    static constexpr int CPG = G / UE;     // units per group
+    static constexpr int LPG = LPG_ ? LPG_ : (CPG < 64 ? CPG : 64);  // lanes per group
+    static constexpr int CPL = CPG / LPG;  // units per lane
     static constexpr int GPP = 64 / LPG;
-    static constexpr int P = RN == RN_NOISE ? (CPL >= 4 ? 1 : 4 / CPL) : 8 / CPL;
-    static constexpr int GPW = P * GPP;  // groups per wave iteration
+    static constexpr int GPW = P * GPP;    // groups per wave
     static constexpr int W = G * BITS / 32;
-    static constexpr int PW = E * BITS;  // code bits per chunk
-    static constexpr int DW = GPW * W;   // dwords staged per wave iteration
-    static constexpr int WAVES = 4;      // waves per workgroup
-    static_assert(LPG >= 4 && LPG <= 64, "group must span 4..64 lanes");
-    static_assert(DW % 4 == 0, "staged block must be whole 16-byte vectors");
+    static constexpr int UBITS = UE * BITS;  // code bits per unit
+    static constexpr int WAVES = 4;
+    static_assert(UB % 16 == 0 && UE * BYTES == UB, "unit must be whole 16-byte loads");
+    static_assert(CPG * UE == G && LPG * CPL == CPG, "group must split evenly over lanes");
+    static_assert(LPG >= 2 && LPG <= 64 && (LPG & (LPG - 1)) == 0, "2..64 lanes per group");
+    static_assert(UBITS >= 32 || (32 / UBITS) <= LPG, "narrow units merge within a group");
+    static_assert(UBITS <= 128, "a unit stores at most one 16-byte vector");
+    static_assert(GPW <= 64, "scale/min gather uses one lane per group");
 };
 
-// Linear element index of element e0 of group r (flat, or the spatial tile gather of
-// tensor_act_reshape_utils.py:115-125: group r = band*(W/s) + tw, element e = i*s + j).
 template <int G>
 __device__ __forceinline__ uint64_t group_elem_index(const QuantPackArgs& a, uint32_t r, uint32_t e0) {
     if (!a.tiled) return (uint64_t)r * G + e0;
+    // spatial tile gather of tensor_act_reshape_utils.py:115-125: group r = band*(W/s) + tw
+    // holds x[.., band's tile row * s + e/s, tw*s + e%s]
     const uint32_t band = r / a.tiles_w;
     const uint32_t tw = r - band * a.tiles_w;
     const uint32_t smask = (1u << a.log2s) - 1u;
@@ -66,42 +92,100 @@ __device__ __forceinline__ uint64_t group_elem_index(const QuantPackArgs& a, uin
            (uint64_t)(e0 >> a.log2s) * a.row + (e0 & smask);
 }
 
-template <int DT, int BITS, int G, int RN>
-__global__ __launch_bounds__(256) void quant_pack_kernel(QuantPackArgs a) {
-    using C = QuantPackCfg<DT, BITS, G, RN>;
-    constexpr int E = C::E, CPL = C::CPL, LPG = C::LPG, GPP = C::GPP, P = C::P, W = C::W;
-    constexpr int PW = C::PW;
-    constexpr int QMAX = (1 << BITS) - 1;
-    constexpr int NZ = RN == RN_NOISE ? E / 4 : 1;
-    using piece_t = typename std::conditional<(PW > 32), uint64_t, uint32_t>::type;
+// Raw v_min3/v_max3: no NaN canonicalisation of the operands (see the header comment).
+__device__ __forceinline__ float vmin3(float a, float b, float c) {
+    float d;
+    asm("v_min3_f32 %0, %1, %2, %3" : "=v"(d) : "v"(a), "v"(b), "v"(c));
+    return d;
+}
+__device__ __forceinline__ float vmax3(float a, float b, float c) {
+    float d;
+    asm("v_max3_f32 %0, %1, %2, %3" : "=v"(d) : "v"(a), "v"(b), "v"(c));
+    return d;
+}
+__device__ __forceinline__ float vmin(float a, float b) {
+    float d;
+    asm("v_min_f32 %0, %1, %2" : "=v"(d) : "v"(a), "v"(b));
+    return d;
+}
+__device__ __forceinline__ float vmax(float a, float b) {
+    float d;
+    asm("v_max_f32 %0, %1, %2" : "=v"(d) : "v"(a), "v"(b));
+    return d;
+}
 
-    __shared__ uint32_t stage[C::WAVES][C::DW];
+// min/max all-reduce over aligned blocks of LPG lanes; operands are NaN-free or quiet NaNs.
+template <int LPG>
+__device__ __forceinline__ void group_minmax(float& mn, float& mx) {
+    if constexpr (LPG >= 2) {
+        mn = vmin(mn, dpp_f32<0xB1>(mn));
+        mx = vmax(mx, dpp_f32<0xB1>(mx));
+    }
+    if constexpr (LPG >= 4) {
+        mn = vmin(mn, dpp_f32<0x4E>(mn));
+        mx = vmax(mx, dpp_f32<0x4E>(mx));
+    }
+    if constexpr (LPG >= 8) {
+        mn = vmin(mn, dpp_f32<0x141>(mn));
+        mx = vmax(mx, dpp_f32<0x141>(mx));
+    }
+    if constexpr (LPG >= 16) {
+        mn = vmin(mn, dpp_f32<0x140>(mn));
+        mx = vmax(mx, dpp_f32<0x140>(mx));
+    }
+    if constexpr (LPG >= 32) {
+        mn = vmin(mn, __shfl_xor(mn, 16, 64));
+        mx = vmax(mx, __shfl_xor(mx, 16, 64));
+    }
+    if constexpr (LPG >= 64) {
+        mn = vmin(mn, __shfl_xor(mn, 32, 64));
+        mx = vmax(mx, __shfl_xor(mx, 32, 64));
+    }
+}
+
+// v_cvt_u32_f32: truncating, saturating, NaN -> 0
+__device__ __forceinline__ uint32_t cvt_u32(float f) {
+    uint32_t d;
+    asm("v_cvt_u32_f32 %0, %1" : "=v"(d) : "v"(f));
+    return d;
+}
+
+__device__ __forceinline__ bool wave_any(bool p) { return __builtin_amdgcn_ballot_w64(p) != 0; }
+
+template <int DT, int BITS, int G, int RN, int UB, int LPG_, int P, bool PRE, bool NT>
+__global__ __launch_bounds__(256) void quant_pack_kernel(QuantPackArgs a) {
+    using C = QuantPackCfg<DT, BITS, G, RN, UB, LPG_, P>;
+    constexpr int UE = C::UE, LOADS = C::LOADS, CPL = C::CPL, LPG = C::LPG, GPP = C::GPP, W = C::W;
+    constexpr int UBITS = C::UBITS;
+    constexpr int QMAX = (1 << BITS) - 1;
+    constexpr int E16 = DType<DT>::per16;  // elements per 16-byte load
 
     const int lane = threadIdx.x & 63;
-    const int wv = threadIdx.x >> 6;
     const int slot = lane / LPG;
     const int li = lane % LPG;
-    const uint32_t g0 = (blockIdx.x * C::WAVES + wv) * (uint32_t)C::GPW;
+    const uint32_t g0 = (blockIdx.x * C::WAVES + (threadIdx.x >> 6)) * (uint32_t)C::GPW;
     const char* xb = (const char*)a.x;
 
-    // ---- issue every load of this iteration first (P*CPL 16-byte loads per lane)
-    uint4 raw[P][CPL];
-    uint4 nz[P][CPL][NZ];
-#pragma unroll
+    // ---- every load of the wave first: P*CPL units of LOADS 16-byte vectors per lane
+    uint4 raw[P][CPL][LOADS];
+    uint4 nz[P][CPL][RN == RN_NOISE ? UE / 4 : 1];
+    #pragma unroll
     for (int p = 0; p < P; ++p) {
         const uint32_t r = g0 + p * GPP + slot;
         const bool ok = r < a.n_groups;
-#pragma unroll
+        #pragma unroll
         for (int i = 0; i < CPL; ++i) {
-            const uint32_t e0 = (uint32_t)(i * LPG + li) * E;
-            raw[p][i] = make_uint4(0u, 0u, 0u, 0u);
-            if (ok)
-                raw[p][i] = *(const uint4*)(xb + group_elem_index<G>(a, r, e0) * DType<DT>::bytes);
+            const uint32_t e0 = (uint32_t)(i * LPG + li) * UE;
+            #pragma unroll
+            for (int l = 0; l < LOADS; ++l) {
+                raw[p][i][l] = make_uint4(0u, 0u, 0u, 0u);
+                if (ok) raw[p][i][l] = ld16<NT>(xb + group_elem_index<G>(a, r, e0 + l * E16) * C::BYTES);
+            }
             if constexpr (RN == RN_NOISE) {
-#pragma unroll
-                for (int k = 0; k < NZ; ++k) {
+                #pragma unroll
+                for (int k = 0; k < UE / 4; ++k) {
                     nz[p][i][k] = make_uint4(0u, 0u, 0u, 0u);
-                    if (ok) nz[p][i][k] = *(const uint4*)(a.noise + (uint64_t)r * G + e0 + 4 * k);
+                    if (ok) nz[p][i][k] = ld16<NT>(a.noise + (uint64_t)r * G + e0 + 4 * k);
                 }
             }
         }
@@ -109,125 +193,175 @@ __global__ __launch_bounds__(256) void quant_pack_kernel(QuantPackArgs a) {
 
     const float qmaxf = (float)QMAX;
     const float half_m = 0.49999899f;  // fp32(0.5 - 1e-6) = 0x3EFFFFDE
+    float step_p[P], mn_p[P];
 
-#pragma unroll
+    #pragma unroll
     for (int p = 0; p < P; ++p) {
         const uint32_t r = g0 + p * GPP + slot;
-        const bool ok = r < a.n_groups;
-        float v[CPL][E];
-#pragma unroll
-        for (int i = 0; i < CPL; ++i) widen16<DT>(raw[p][i], v[i]);
-        if (a.flags & FL_CLAMP) {
-#pragma unroll
-            for (int i = 0; i < CPL; ++i)
-#pragma unroll
-                for (int k = 0; k < E; ++k) v[i][k] = fminf(fmaxf(v[i][k], -a.clamp_alpha), a.clamp_alpha);
-        }
-        if (a.flags & FL_SQUASH) {
-#pragma unroll
-            for (int i = 0; i < CPL; ++i)
-#pragma unroll
-                for (int k = 0; k < E; ++k) v[i][k] = tanhf(v[i][k] / 0.5f) * 0.5f;
-        }
-        float mn = v[0][0], mx = v[0][0];
-#pragma unroll
+        float v[CPL][UE];
+        #pragma unroll
         for (int i = 0; i < CPL; ++i)
-#pragma unroll
-            for (int k = 0; k < E; ++k) {
-                mn = fminf(mn, v[i][k]);
-                mx = fmaxf(mx, v[i][k]);
+            #pragma unroll
+            for (int l = 0; l < LOADS; ++l) widen16<DT>(raw[p][i][l], &v[i][l * E16]);
+        if constexpr (PRE) {
+            if (a.flags & FL_CLAMP) {
+                #pragma unroll
+                for (int i = 0; i < CPL; ++i)
+                    #pragma unroll
+                    for (int k = 0; k < UE; ++k) v[i][k] = fminf(fmaxf(v[i][k], -a.clamp_alpha), a.clamp_alpha);
             }
-        block_minmax<LPG>(mn, mx);
+            if (a.flags & FL_SQUASH) {
+                #pragma unroll
+                for (int i = 0; i < CPL; ++i)
+                    #pragma unroll
+                    for (int k = 0; k < UE; ++k) v[i][k] = tanhf(v[i][k] / 0.5f) * 0.5f;
+            }
+        }
+        // lane-local min/max with raw 3-operand min/max over the lane's CPL*UE values
+        float mn = v[0][0], mx = v[0][0];
+        #pragma unroll
+        for (int j = 1; j + 1 < CPL * UE; j += 2) {
+            const float f0 = v[j / UE][j % UE], f1 = v[(j + 1) / UE][(j + 1) % UE];
+            mn = vmin3(mn, f0, f1);
+            mx = vmax3(mx, f0, f1);
+        }
+        mn = vmin(mn, v[CPL - 1][UE - 1]);  // CPL*UE is even: one value is left over
+        mx = vmax(mx, v[CPL - 1][UE - 1]);
+        if (wave_any(mn != mn || mx != mx)) {
+            // a NaN partial result (signalling NaN input, or a lane of only NaNs): IEEE
+            // fminf/fmaxf ignore NaN operands; a lane of only NaNs keeps NaN, which the
+            // cross-lane min/max below then ignore
+            mn = v[0][0];
+            mx = v[0][0];
+            #pragma unroll
+            for (int i = 0; i < CPL; ++i)
+                #pragma unroll
+                for (int k = 0; k < UE; ++k) {
+                    mn = fminf(mn, v[i][k]);
+                    mx = fmaxf(mx, v[i][k]);
+                }
+            mn = __builtin_isnan(mn) ? __uint_as_float(0x7fc00000u) : mn;  // quiet
+            mx = __builtin_isnan(mx) ? __uint_as_float(0x7fc00000u) : mx;
+        }
+        group_minmax<LPG>(mn, mx);
         mn = mn + 0.0f;  // store -0.0 as +0.0
         const float rng = mx - mn;
         const float step = rng > 0.0f ? rng / qmaxf : 1.0f;
         const float inv = 1.0f / step;
-        if (li == 0 && ok) {
-            if (a.meta_bf16) {
-                ((uint16_t*)a.scale)[r] = to_bf16(step);
-                ((uint16_t*)a.minv)[r] = to_bf16(mn);
-            } else {
-                ((float*)a.scale)[r] = step;
-                ((float*)a.minv)[r] = mn;
-            }
-        }
+        step_p[p] = step;
+        mn_p[p] = mn;
+        const bool clampq = wave_any(inv == __builtin_inff());
 
-#pragma unroll
-        for (int i = 0; i < CPL; ++i) {
-            const uint32_t c = (uint32_t)(i * LPG + li);
-            const uint32_t e0 = c * E;
-            float u[E];
-            if constexpr (RN == RN_NOISE) {
-#pragma unroll
-                for (int k = 0; k < NZ; ++k) {
-                    u[4 * k + 0] = __uint_as_float(nz[p][i][k].x);
-                    u[4 * k + 1] = __uint_as_float(nz[p][i][k].y);
-                    u[4 * k + 2] = __uint_as_float(nz[p][i][k].z);
-                    u[4 * k + 3] = __uint_as_float(nz[p][i][k].w);
+        // codes + store; the clamped variant runs only for waves holding a group with inv = +inf
+        auto emit = [&](auto clamp_tag) {
+            constexpr bool CL = decltype(clamp_tag)::value;
+            #pragma unroll
+            for (int i = 0; i < CPL; ++i) {
+                const uint32_t c = (uint32_t)(i * LPG + li);
+                const uint32_t e0 = c * UE;
+                float u[UE];
+                if constexpr (RN == RN_NOISE) {
+                    #pragma unroll
+                    for (int k = 0; k < UE / 4; ++k) {
+                        u[4 * k + 0] = __uint_as_float(nz[p][i][k].x);
+                        u[4 * k + 1] = __uint_as_float(nz[p][i][k].y);
+                        u[4 * k + 2] = __uint_as_float(nz[p][i][k].z);
+                        u[4 * k + 3] = __uint_as_float(nz[p][i][k].w);
+                    }
+                } else if constexpr (RN == RN_PHILOX) {
+                    // one Philox call per NOISE_EPC elements (a unit holds UE of them)
+                    #pragma unroll
+                    for (int b0 = 0; b0 < UE; b0 += NOISE_EPC) {
+                        const uint64_t idx = (uint64_t)r * G + e0 + b0;
+                        const uint64_t blk = idx / NOISE_EPC;
+                        const uint4 w4 = philox4x32_10((uint32_t)blk, (uint32_t)(blk >> 32), a.off_lo, a.off_hi,
+                                                       a.seed_lo, a.seed_hi);
+                        const uint32_t w[4] = {w4.x, w4.y, w4.z, w4.w};
+                        const int sub = (int)(idx % NOISE_EPC);  // 0 unless UE < NOISE_EPC
+                        #pragma unroll
+                        for (int k = 0; k < (UE < NOISE_EPC ? UE : NOISE_EPC); ++k) {
+                            const int kk = sub + k;
+                            u[b0 + k] = philox_byte_to_u(w[kk >> 2], kk & 3);
+                        }
+                    }
                 }
-            } else if constexpr (RN == RN_PHILOX) {
-                const uint64_t blk = ((uint64_t)r * G + e0) >> 3;
-                const uint4 w4 = philox4x32_10((uint32_t)blk, (uint32_t)(blk >> 32), a.off_lo, a.off_hi,
-                                               a.seed_lo, a.seed_hi);
-                const uint32_t w[4] = {w4.x, w4.y, w4.z, w4.w};
-#pragma unroll
-                for (int k = 0; k < E; ++k) {
-                    const int kk = (int)(e0 & 7u) + k;  // E == 4 chunks use half a block
-                    u[k] = philox_half_to_u((w[kk >> 1] >> ((kk & 1) * 16)) & 0xffffu);
+                uint32_t q[UE];
+                #pragma unroll
+                for (int k = 0; k < UE; ++k) {
+                    const float t = v[i][k] - mn;
+                    float qf;
+                    if constexpr (RN == RN_NEAREST) {
+                        qf = __builtin_fmaf(t, inv, half_m);
+                    } else {
+                        qf = __builtin_fmaf(t, inv, u[k]);
+                        qf = qf - 0.5f;
+                        qf = __builtin_rintf(qf);
+                    }
+                    if constexpr (CL) qf = fminf(fmaxf(qf, 0.0f), qmaxf);  // NaN -> 0, as the reference's clamp
+                    q[k] = cvt_u32(qf);
                 }
-            }
-            piece_t piece = 0;
-#pragma unroll
-            for (int k = 0; k < E; ++k) {
-                float t = v[i][k] - mn;
-                t = t * inv;
-                float qf;
-                if constexpr (RN == RN_NEAREST) {
-                    qf = t + half_m;
+                // UBITS code bits of this unit, little-endian
+                uint32_t d[UBITS >= 32 ? UBITS / 32 : 1];
+                #pragma unroll
+                for (int j = 0; j < (UBITS >= 32 ? UBITS / 32 : 1); ++j) {
+                    uint32_t acc = 0;
+                    constexpr int PER = UBITS >= 32 ? 32 / BITS : UE;
+                    #pragma unroll
+                    for (int k = 0; k < PER; ++k) acc |= q[j * PER + k] << (k * BITS);
+                    d[j] = acc;
+                }
+                uint32_t* dst = a.packed + (uint64_t)r * W;
+                const bool ok = r < a.n_groups;
+                if constexpr (UBITS >= 32) {
+                    constexpr int ND = UBITS / 32;
+                    if (ok) {
+                        if constexpr (ND == 1) dst[c] = d[0];
+                        else if constexpr (ND == 2) *(uint2*)(dst + 2 * c) = make_uint2(d[0], d[1]);
+                        else *(uint4*)(dst + 4 * c) = make_uint4(d[0], d[1], d[2], d[3]);
+                    }
                 } else {
-                    qf = t + u[k];
-                    qf = qf - 0.5f;
+                    // merge LPD = 32/UBITS neighbouring units (lanes li..li+LPD-1) into one dword
+                    uint32_t m = d[0];
+                    if constexpr (UBITS < 32) m |= dpp_u32<0xB1>(m) << UBITS;
+                    if constexpr (UBITS * 2 < 32) m |= dpp_u32<0x4E>(m) << (2 * UBITS);
+                    if constexpr (UBITS * 4 < 32) m |= dpp_u32<0x104>(m) << (4 * UBITS);
+                    constexpr int LPD = 32 / UBITS;
+                    if (ok && (li % LPD) == 0) dst[c / LPD] = m;
                 }
-                qf = fminf(fmaxf(qf, 0.0f), qmaxf);
-                const uint32_t q = RN == RN_NEAREST ? (uint32_t)qf : (uint32_t)rintf(qf);
-                piece |= (piece_t)q << (k * BITS);
             }
-            // merge narrow pieces from the next lanes (chunks c+1, c+2, ...) into a dword
-            uint32_t d0 = (uint32_t)piece;
-            if constexpr (PW < 32) d0 |= dpp_u32<0xB1>(d0) << PW;
-            if constexpr (PW * 2 < 32) d0 |= dpp_u32<0x4E>(d0) << (2 * PW);
-            if constexpr (PW * 4 < 32) d0 |= dpp_u32<0x104>(d0) << (4 * PW);
-            const int sbase = (p * GPP + slot) * W;
-            if constexpr (PW >= 32) {
-                const int di = sbase + (int)(c * (PW / 32));
-                stage[wv][di] = d0;
-                if constexpr (PW == 64) stage[wv][di + 1] = (uint32_t)((uint64_t)piece >> 32);
-            } else {
-                constexpr int LPD = 32 / PW;  // lanes merged into one dword
-                if ((li % LPD) == 0) stage[wv][sbase + (int)(c / LPD)] = d0;
-            }
+        };
+        if (clampq)
+            emit(std::true_type{});
+        else
+            emit(std::false_type{});
+    }
+
+    // ---- per-group scale / min: gather group j of the wave into lane j, one store per array
+    float sv = 0.0f, mv = 0.0f;
+    #pragma unroll
+    for (int p = 0; p < P; ++p) {
+        const int src = ((lane - p * GPP) & (GPP - 1)) * LPG;
+        const float s_ = __shfl(step_p[p], src, 64);
+        const float m_ = __shfl(mn_p[p], src, 64);
+        if (lane >= p * GPP && lane < (p + 1) * GPP) {
+            sv = s_;
+            mv = m_;
         }
     }
-    __syncthreads();
-
-    // ---- the wave's output block [g0, g0 + GPW) is contiguous: 128-bit stores
-    const uint32_t ng = g0 < a.n_groups ? min((uint32_t)C::GPW, a.n_groups - g0) : 0u;
-    const uint32_t valid = ng * W;
-    uint32_t* dst = a.packed + (uint64_t)g0 * W;
-#pragma unroll
-    for (int o = lane * 4; o < C::DW; o += 256) {
-        if ((uint32_t)o + 4 <= valid) {
-            *(uint4*)(dst + o) = *(const uint4*)&stage[wv][o];
+    const uint32_t rg = g0 + lane;
+    if (lane < C::GPW && rg < a.n_groups) {
+        if (a.meta_bf16) {
+            ((uint16_t*)a.scale)[rg] = to_bf16(sv);
+            ((uint16_t*)a.minv)[rg] = to_bf16(mv);
         } else {
-#pragma unroll
-            for (int k = 0; k < 4; ++k)
-                if ((uint32_t)(o + k) < valid) dst[o + k] = stage[wv][o + k];
+            ((float*)a.scale)[rg] = sv;
+            ((float*)a.minv)[rg] = mv;
         }
     }
 }
 
 // host-side launcher; explicitly instantiated per element type in quant_pack_<dtype>.hip
 template <int DT>
-int launch_quant_pack_dt(const QuantPackArgs& a, int bits, int g, int rn, hipStream_t s);
+int launch_quant_pack_dt(const QuantPackArgs& a, int bits, int g, int rn, bool pre, hipStream_t s);
 
 }  // namespace dopt

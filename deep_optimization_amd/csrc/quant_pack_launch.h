@@ -1,5 +1,12 @@
-// Compile-time dispatch of quant_pack_kernel over (bits, group size, rounding) for one element
-// type. Included by quant_pack_<dtype>.hip, each of which instantiates launch_quant_pack_dt<DT>.
+// Compile-time dispatch of quant_pack_kernel over (bits, group size, rounding, pre-transform) for
+// one element type, with the launch shape of each configuration. Included by
+// quant_pack_<dtype>.hip, each of which instantiates launch_quant_pack_dt<DT>.
+//
+// Launch shapes (measured on MI355X, bf16 [256, 256, 56, 56], g = 256, 2-bit): one pass per wave
+// (P = 1: a modest 32-64 bytes of loads in flight per lane across many short waves streams
+// best), two units per lane, units of 16 bytes (32 for Philox rounding, so that one
+// Philox4x32-10 call covers a lane's 16 contiguous bf16 elements), cached loads (non-temporal
+// loads measured slower here).
 #pragma once
 
 #include "quant_pack.h"
@@ -7,45 +14,66 @@
 namespace dopt {
 
 template <int DT, int BITS, int G, int RN>
+struct QuantPackShape {
+    static constexpr int BYTES = DType<DT>::bytes;
+    // unit bytes: Philox units hold NOISE_EPC elements where that is at most 64 bytes
+    static constexpr int UB = RN == RN_PHILOX ? (NOISE_EPC * BYTES <= 64 ? NOISE_EPC * BYTES : 64) : 16;
+    static constexpr int UE = UB / BYTES;
+    static constexpr int CPG = G / UE;
+    static constexpr int UBITS = UE * BITS;
+    static constexpr int LPD = UBITS >= 32 ? 1 : 32 / UBITS;  // lanes merged per code dword
+    static constexpr int L0 = RN == RN_NOISE ? CPG : CPG / 2;   // noise mode: one unit per lane
+    static constexpr int L1 = L0 < LPD ? LPD : L0;
+    static constexpr int L2 = L1 < 2 ? 2 : L1;
+    static constexpr int LPG = L2 > 64 ? 64 : L2;
+    static constexpr int P = 1;
+};
+
+template <int DT, int BITS, int G, int RN, bool PRE>
 static int qp_launch(const QuantPackArgs& a, hipStream_t s) {
-    using C = QuantPackCfg<DT, BITS, G, RN>;
+    using S = QuantPackShape<DT, BITS, G, RN>;
+    using C = QuantPackCfg<DT, BITS, G, RN, S::UB, S::LPG, S::P>;
     const uint64_t waves = ((uint64_t)a.n_groups + C::GPW - 1) / C::GPW;
     const uint64_t blocks = (waves + C::WAVES - 1) / C::WAVES;
     if (blocks == 0) return 0;
-    hipLaunchKernelGGL((quant_pack_kernel<DT, BITS, G, RN>), dim3((uint32_t)blocks), dim3(64 * C::WAVES), 0, s,
-                       a);
+    hipLaunchKernelGGL((quant_pack_kernel<DT, BITS, G, RN, S::UB, S::LPG, S::P, PRE, false>), dim3((uint32_t)blocks),
+                       dim3(64 * C::WAVES), 0, s, a);
     return 0;
 }
 
 template <int DT, int BITS, int G>
-static int qp_rn(const QuantPackArgs& a, int rn, hipStream_t s) {
+static int qp_rn(const QuantPackArgs& a, int rn, bool pre, hipStream_t s) {
+    if (pre) {  // the reference's clamp / tanh pre-transform runs with nearest rounding only
+        if (rn != RN_NEAREST) return -1;
+        return qp_launch<DT, BITS, G, RN_NEAREST, true>(a, s);
+    }
     switch (rn) {
-        case RN_NEAREST: return qp_launch<DT, BITS, G, RN_NEAREST>(a, s);
-        case RN_NOISE: return qp_launch<DT, BITS, G, RN_NOISE>(a, s);
-        case RN_PHILOX: return qp_launch<DT, BITS, G, RN_PHILOX>(a, s);
+        case RN_NEAREST: return qp_launch<DT, BITS, G, RN_NEAREST, false>(a, s);
+        case RN_NOISE: return qp_launch<DT, BITS, G, RN_NOISE, false>(a, s);
+        case RN_PHILOX: return qp_launch<DT, BITS, G, RN_PHILOX, false>(a, s);
     }
     return -1;
 }
 
 template <int DT, int BITS>
-static int qp_g(const QuantPackArgs& a, int g, int rn, hipStream_t s) {
+static int qp_g(const QuantPackArgs& a, int g, int rn, bool pre, hipStream_t s) {
     switch (g) {
-        case 64: return qp_rn<DT, BITS, 64>(a, rn, s);
-        case 128: return qp_rn<DT, BITS, 128>(a, rn, s);
-        case 256: return qp_rn<DT, BITS, 256>(a, rn, s);
-        case 512: return qp_rn<DT, BITS, 512>(a, rn, s);
-        case 1024: return qp_rn<DT, BITS, 1024>(a, rn, s);
+        case 64: return qp_rn<DT, BITS, 64>(a, rn, pre, s);
+        case 128: return qp_rn<DT, BITS, 128>(a, rn, pre, s);
+        case 256: return qp_rn<DT, BITS, 256>(a, rn, pre, s);
+        case 512: return qp_rn<DT, BITS, 512>(a, rn, pre, s);
+        case 1024: return qp_rn<DT, BITS, 1024>(a, rn, pre, s);
     }
     return -1;
 }
 
 template <int DT>
-int launch_quant_pack_dt(const QuantPackArgs& a, int bits, int g, int rn, hipStream_t s) {
+int launch_quant_pack_dt(const QuantPackArgs& a, int bits, int g, int rn, bool pre, hipStream_t s) {
     switch (bits) {
-        case 1: return qp_g<DT, 1>(a, g, rn, s);
-        case 2: return qp_g<DT, 2>(a, g, rn, s);
-        case 4: return qp_g<DT, 4>(a, g, rn, s);
-        case 8: return qp_g<DT, 8>(a, g, rn, s);
+        case 1: return qp_g<DT, 1>(a, g, rn, pre, s);
+        case 2: return qp_g<DT, 2>(a, g, rn, pre, s);
+        case 4: return qp_g<DT, 4>(a, g, rn, pre, s);
+        case 8: return qp_g<DT, 8>(a, g, rn, pre, s);
     }
     return -1;
 }

@@ -37,9 +37,13 @@ extern "C" {
 #define DOPT_BF16 2
 
 /* rounding modes */
-#define DOPT_ROUND_NEAREST 0 /* q = trunc((x-min)*inv + (0.5-1e-6)), act_triton_kernel.py:114,:155-157 */
-#define DOPT_ROUND_STOCH_NOISE 1 /* q = rint(((x-min)*inv + u) - 0.5), u read from a noise tensor */
-#define DOPT_ROUND_STOCH_PHILOX 2 /* same, u from Philox4x32-10(seed, offset), 16 bits/element */
+/* rounding modes; fma() is one correctly rounded multiply-add, matching the FMA contraction the
+ * reference's compilers apply to `a * b + c` (Triton enable_fp_fusion, nvcc --fmad=true) */
+#define DOPT_ROUND_NEAREST 0 /* q = trunc(fma(x-min, inv, 0.5-1e-6)), act_triton_kernel.py:114,:155-157 */
+#define DOPT_ROUND_STOCH_NOISE 1 /* q = rint(fma(x-min, inv, u) - 0.5), quant_common.h:150-151; u from a tensor */
+#define DOPT_ROUND_STOCH_PHILOX 2 /* same, u = (byte + 0.5)/256, one byte of Philox4x32-10 output per element:
+                                   * element i (group order) uses byte i%16 of the call with counter
+                                   * {i/16 (64 bit), offset (64 bit)} and key seed */
 
 /* pre-transform flags (act_triton_kernel.py:55-58) */
 #define DOPT_FLAG_CLAMP 1 /* x = clamp(x, -alpha, alpha) */
@@ -74,7 +78,9 @@ const char* dopt_last_error(void);
  *   bits        1, 2, 4 or 8
  *   rounding    DOPT_ROUND_*; noise (fp32 [n_groups, group_size] in group order, values in [0,1))
  *               is read only for DOPT_ROUND_STOCH_NOISE; seed/offset only for DOPT_ROUND_STOCH_PHILOX.
- *   flags       DOPT_FLAG_* bit set; clamp_alpha used with DOPT_FLAG_CLAMP.
+ *   flags       DOPT_FLAG_* bit set; clamp_alpha used with DOPT_FLAG_CLAMP. The pre-transform is
+ *               the reference's, which always rounds to nearest: flags != 0 with a stochastic
+ *               rounding mode returns DOPT_EUNSUPPORTED.
  *   packed      out: uint32 [n_groups, group_size*bits/32], 16-byte aligned.
  *   scale, minv out: [n_groups] of meta_dtype (F32 or BF16): step = (max-min)/(2^b-1) (1.0 when
  *               max == min) and the group minimum (act_triton_kernel.py:60-68).
@@ -85,7 +91,7 @@ int dopt_quant_pack(const void* x, int x_dtype, int64_t n_groups, int group_size
                     void* minv, int meta_dtype, void* stream);
 
 /*
- * Unpack + dequantize: y = float(q) * scale + min, rounded once to y_dtype (F32 or BF16).
+ * Unpack + dequantize: y = fma(float(q), scale, min), rounded once to y_dtype (F32 or BF16).
  * Replaces act_lib::dequant_unpack_triton (act_triton_kernel.py:372-395, kernel :174-241) and
  * the cpp_extension unpack1..unpack8 entry points (cpp_extension/bind.cpp:54-58,
  * cpp_extension/src/dequant_unpack_dispatch.cpp:12-41).

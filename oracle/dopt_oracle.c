@@ -10,13 +10,20 @@
  * AC/ = Activation_Compression/.
  *
  * Arithmetic contract (built with -ffp-contract=off, no -ffast-math, round-to-nearest-even):
- *   every fp32 operation below is rounded separately, in the order written.
+ *   every fp32 operation below is rounded separately, in the order written, except the three
+ *   multiply-adds written as fmaf(): the reference's kernels are compiled with FMA contraction on
+ *   (Triton's enable_fp_fusion default for AC/act_triton_kernel.py:114 `(x - xmin) * inv_scale +
+ *   (0.5 - 1e-6)` and :223 `q * scale + xmin`; nvcc's default --fmad=true for
+ *   AC/cpp_extension/include/quant_common.h:150 `(x - minv) * scale + noise - 0.5f`), so each of
+ *   those is one correctly rounded fused multiply-add (C99 fmaf).
+ *   Division (step = rng/QMAX, inv = 1/step) is IEEE correctly rounded; the reference's Triton
+ *   division on NVIDIA hardware is not pinned at bit level (no golden data exists for it).
  *
  * Parity status of each function (how it is pinned; the tests in tests/test_oracle.py do it):
  *   grouping (flat / tile gather)  pinned: brute-force index maps + torch view/permute restatement
  *   min/max/step/inv               pinned: closed forms and known-answer groups
  *   nearest codes                  pinned: known-answer groups, |deq-x| <= step/2 bound, numpy
- *                                  restatement
+ *                                  restatement, exact rational fma on boundary cases
  *   stochastic codes (noise)       pinned: closed form with a given noise tensor, |deq-x| < step
  *   bit packing                    pinned: numpy.packbits(bitorder='little') special case
  *   dequant                        pinned: closed form
@@ -117,19 +124,19 @@ void oracle_philox4x32_10(const uint32_t ctr[4], const uint32_t key[2], uint32_t
     out[3] = c3;
 }
 
-/* Noise for element `idx` (group-order linear index r*g + e) in Philox mode: the 8-element block
- * idx>>3 is the counter {blk_lo, blk_hi, offset_lo, offset_hi}, the seed is the key; element k of
- * the block takes 16-bit half (k&1) of word k>>1, and u = (h + 0.5) * 2^-16 (exact in fp32). */
+/* Noise for element `idx` (group-order linear index r*g + e) in Philox mode: the 16-element block
+ * idx>>4 is the counter {blk_lo, blk_hi, offset_lo, offset_hi}, the seed is the key; element k of
+ * the block takes byte k&3 of word k>>2, and u = (b + 0.5) * 2^-8 (exact in fp32). */
 static float philox_u(int64_t idx, uint64_t seed, uint64_t offset) {
-    uint64_t blk = (uint64_t)idx >> 3;
+    uint64_t blk = (uint64_t)idx >> 4;
     uint32_t ctr[4] = {(uint32_t)blk, (uint32_t)(blk >> 32), (uint32_t)offset,
                        (uint32_t)(offset >> 32)};
     uint32_t key[2] = {(uint32_t)seed, (uint32_t)(seed >> 32)};
     uint32_t w[4];
     oracle_philox4x32_10(ctr, key, w);
-    int k = (int)(idx & 7);
-    uint32_t h = (w[k >> 1] >> ((k & 1) * 16)) & 0xffffu;
-    return (float)h * (1.0f / 65536.0f) + (1.0f / 131072.0f);
+    int k = (int)(idx & 15);
+    uint32_t b = (w[k >> 2] >> ((k & 3) * 8)) & 0xffu;
+    return (float)b * (1.0f / 256.0f) + (1.0f / 512.0f);
 }
 
 /* Philox noise values for n consecutive group-order indices starting at idx0 (test helper). */
@@ -170,9 +177,9 @@ static int check_common(int64_t n_groups, int g, int bits, const int64_t* t, int
  *   x = f32(x); [clamp(x, -a, a)] (:55-56); [x = tanh(x/0.5)*0.5] (:58)
  *   mn = min(x), mx = max(x) (:60-61); rng = mx - mn; step = rng > 0 ? rng/QMAX : 1 (:63-65)
  *   inv = 1/step (:71)
- *   nearest: q = clamp(trunc((x-mn)*inv + f32(0.5-1e-6)), 0, QMAX) (:114, :155-157)
+ *   nearest: q = clamp(trunc(fma(x-mn, inv, f32(0.5-1e-6))), 0, QMAX) (:114, :155-157)
  *   stochastic (the dormant CUDA form, AC/cpp_extension/include/quant_common.h:148-156, with the
- *   Triton step convention): q = clamp(rint_even(((x-mn)*inv + u) - 0.5), 0, QMAX)
+ *   Triton step convention): q = clamp(rint_even(fma(x-mn, inv, u) - 0.5), 0, QMAX)
  *   word[w] = OR_j q[w*VPW + j] << (j*b) (:110-111, :159-160)
  *   scale = step, min = mn (:67-68; stored in meta_dtype).
  * Two definitions this restatement makes explicit (the reference leaves them to the hardware):
@@ -218,14 +225,13 @@ int oracle_quant_pack(const void* x, int x_dtype, int64_t n_groups, int g, int b
             float inv = 1.0f / step;
             for (int e = 0; e < g; ++e) {
                 float t = xs[e] - mn;
-                t = t * inv;
                 float qf;
                 if (rounding == O_NEAREST) {
-                    qf = t + half_m;
+                    qf = fmaf(t, inv, half_m);
                 } else {
                     float u = (rounding == O_STOCH_NOISE) ? noise[r * g + e]
                                                           : philox_u(r * g + e, seed, offset);
-                    qf = t + u;
+                    qf = fmaf(t, inv, u);
                     qf = qf - 0.5f;
                 }
                 if (qf != qf) qf = 0.0f;
@@ -253,7 +259,7 @@ int oracle_quant_pack(const void* x, int x_dtype, int64_t n_groups, int g, int b
 
 /* ---------------------------------------------------------------- dequant-unpack
  * AC/act_triton_kernel.py:199-241: q = (word >> (j*b)) & QMAX (:206-210);
- * y = f32(q)*scale + min (:223, scale/min widened to fp32 :201-204), one rounding to y_dtype
+ * y = fma(f32(q), scale, min) (:223, scale/min widened to fp32 :201-204), one rounding to y_dtype
  * (:241). With tiles the inverse layout of tensor_act_reshape_utils.py:131-154 is applied. */
 int oracle_dequant_unpack(const uint32_t* packed, const void* scale, const void* minv,
                           int meta_dtype, int64_t n_groups, int g, int bits,
@@ -278,8 +284,7 @@ int oracle_dequant_unpack(const uint32_t* packed, const void* scale, const void*
         for (int e = 0; e < g; ++e) {
             uint32_t word = packed[r * NW + e / VPW];
             uint32_t qv = (word >> ((e % VPW) * bits)) & QMAX;
-            float v = (float)qv * sc;
-            v = v + mn;
+            float v = fmaf((float)qv, sc, mn);
             int64_t o = elem_index(r, e, g, tile_nchw, s);
             if (y_dtype == O_F32)
                 ((float*)y)[o] = v;

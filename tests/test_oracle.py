@@ -52,13 +52,22 @@ def test_philox_known_answers(ctr, key, want):
 
 
 def test_philox_noise_element_mapping():
-    # block 0 (elements 0..7) of seed 0 / offset 0 is the first KAT vector; element k takes
-    # 16-bit half (k & 1) of word k >> 1, u = (h + 0.5) / 65536
+    # block 0 (elements 0..15) of seed 0 / offset 0 is the first KAT vector; element k takes
+    # byte (k & 3) of word k >> 2, u = (b + 0.5) / 256
     w = PHILOX_KAT[0][2]
-    halves = [(w[k >> 1] >> (16 * (k & 1))) & 0xFFFF for k in range(8)]
-    want = (np.array(halves, dtype=np.float64) + 0.5) / 65536.0
-    got = oracle.philox_noise(0, 8, 0, 0)
+    bts = [(w[k >> 2] >> (8 * (k & 3))) & 0xFF for k in range(16)]
+    want = (np.array(bts, dtype=np.float64) + 0.5) / 256.0
+    got = oracle.philox_noise(0, 16, 0, 0)
     np.testing.assert_array_equal(got.astype(np.float64), want)
+    # block 1 (elements 16..31) is the call with counter {1, 0, 0, 0}: a different KAT-derived stream
+    w1 = oracle.philox4x32_10([1, 0, 0, 0], [0, 0])
+    bts1 = [(int(w1[k >> 2]) >> (8 * (k & 3))) & 0xFF for k in range(16)]
+    np.testing.assert_array_equal(oracle.philox_noise(16, 16, 0, 0).astype(np.float64),
+                                  (np.array(bts1, dtype=np.float64) + 0.5) / 256.0)
+    # the offset is the high half of the counter, the seed the key
+    w2 = oracle.philox4x32_10([3, 0, 7, 0], [5, 0])
+    b2 = (int(w2[1]) >> 8) & 0xFF  # element 16*3 + 5 -> word 1, byte 1
+    assert oracle.philox_noise(16 * 3 + 5, 1, 5, 7)[0] == np.float32((b2 + 0.5) / 256.0)
 
 
 def test_philox_noise_statistics():
@@ -189,8 +198,49 @@ def test_input_widening_bf16_f16():
 
 
 # ----------------------------------------------------------------------------- independent restatement
+def fma32(a, b, c):
+    """Correctly rounded float32 fused multiply-add in numpy, independent of any libm fmaf:
+    a*b is exact in float64 (24 + 24 bits); TwoSum gives the exact error of the float64 sum;
+    rounding that sum to odd at 53 bits and then to nearest at 24 bits is correctly rounded
+    (53 >= 24 + 2, Boldo & Melquiond)."""
+    a = np.asarray(a, dtype=np.float32).astype(np.float64)
+    b = np.asarray(b, dtype=np.float32).astype(np.float64)
+    c = np.asarray(c, dtype=np.float32).astype(np.float64)
+    p = a * b
+    with np.errstate(invalid="ignore", over="ignore"):
+        s = p + c
+        bp = s - c
+        e = (p - (s - bp)) + (c - bp)  # exact: p + c == s + e (finite s)
+        bits = s.view(np.int64).copy()
+        inexact = np.isfinite(s) & (e != 0)
+        # truncate toward zero: RN went away from zero when e and s have opposite signs
+        away = inexact & (np.sign(e) != np.sign(s)) & (s != 0)
+        bits[away] -= 1
+        bits[inexact] |= 1  # round to odd
+        odd = bits.view(np.float64)
+        return odd.astype(np.float32)
+
+
+def test_fma32_emulation_is_exact():
+    from fractions import Fraction
+    rng = np.random.default_rng(99)
+    a = (rng.standard_normal(4000) * np.exp2(rng.integers(-30, 30, 4000))).astype(np.float32)
+    b = (rng.standard_normal(4000) * np.exp2(rng.integers(-30, 30, 4000))).astype(np.float32)
+    c = (rng.standard_normal(4000) * np.exp2(rng.integers(-60, 60, 4000))).astype(np.float32)
+    got = fma32(a, b, c)
+    for i in range(4000):
+        exact = Fraction(float(a[i])) * Fraction(float(b[i])) + Fraction(float(c[i]))
+        r = np.float32(float(exact))  # float(Fraction) is correctly rounded to f64 ...
+        # ... so check the f32 neighbours directly: the result must be the nearest (ties to even)
+        lo, hi = (np.nextafter(r, np.float32(-np.inf)), np.nextafter(r, np.float32(np.inf)))
+        cands = sorted([lo, r, hi], key=lambda v: (abs(Fraction(float(v)) - exact),
+                                                   int(np.float32(v).view(np.uint32)) & 1))
+        assert got[i] == cands[0], (a[i], b[i], c[i])
+
+
 def numpy_quant(x, bits, rounding=NEAREST, u=None):
-    """Vectorised numpy float32 restatement (each array op rounds once, no contraction)."""
+    """Vectorised numpy float32 restatement: each array op rounds once, fma32 for the fused
+    multiply-add of the reference's contracted `(x - mn) * inv + c`."""
     f = np.float32
     qmax = (1 << bits) - 1
     mn = x.min(axis=1) + f(0.0)
@@ -198,15 +248,78 @@ def numpy_quant(x, bits, rounding=NEAREST, u=None):
     rng = (mx - mn).astype(np.float32)
     step = np.where(rng > 0, rng / f(qmax), f(1.0)).astype(np.float32)
     inv = (f(1.0) / step).astype(np.float32)
-    t = ((x - mn[:, None]) * inv[:, None]).astype(np.float32)
+    t = (x - mn[:, None]).astype(np.float32)
     if rounding == NEAREST:
-        qf = (t + f(0.5 - 1e-6)).astype(np.float32)
+        qf = fma32(t, np.broadcast_to(inv[:, None], t.shape), np.full(t.shape, f(0.5 - 1e-6)))
         q = np.clip(qf, 0, qmax).astype(np.int64)
     else:
-        qf = ((t + u) - f(0.5)).astype(np.float32)
+        qf = (fma32(t, np.broadcast_to(inv[:, None], t.shape), u) - f(0.5)).astype(np.float32)
         q = np.rint(np.clip(qf, 0, qmax)).astype(np.int64)
     packed = packbits_reference(q, bits).view("<u4")
     return packed, step, mn
+
+
+def _fma_boundary_values(step_target, bits, per_boundary=2):
+    """Values t in [0, QMAX*step] just around the code boundaries of a group with min 0, where
+    fma(t, inv, 0.5-1e-6) and the separately rounded (t * inv) + (0.5-1e-6) truncate differently."""
+    f = np.float32
+    qmax = (1 << bits) - 1
+    mx = f(step_target * qmax)
+    step = f(mx / f(qmax))
+    inv = f(f(1) / step)
+    found = []
+    for k in range(1, qmax + 1):
+        target = f((k - f(0.5 - 1e-6)) / inv)
+        cand = np.nextafter(np.full(401, target, dtype=f), np.inf if target >= 0 else -np.inf)
+        ladder = target.view(np.uint32) + np.arange(-200, 201).astype(np.int64)
+        cand = ladder.astype(np.uint32).view(f)
+        cand = cand[(cand >= 0) & (cand <= mx)]
+        fused = fma32(cand, np.full(cand.shape, inv), np.full(cand.shape, f(0.5 - 1e-6)))
+        unfused = ((cand * inv).astype(f) + f(0.5 - 1e-6)).astype(f)
+        hit = cand[np.floor(fused) != np.floor(unfused)]
+        found.extend(hit[:per_boundary].tolist())
+    return mx, np.array(found, dtype=f), inv
+
+
+def test_nearest_uses_the_fused_multiply_add():
+    # values where fma(t, inv, c) and the separately rounded (t * inv) + c truncate to different
+    # codes: the oracle must follow the fused form (the reference's compiled arithmetic)
+    bits, g = 8, 256
+    rows = []
+    for st in (0.013, 0.37, 1.9, 7.25):
+        mx, vals, inv = _fma_boundary_values(st, bits)
+        if len(vals) == 0:
+            continue
+        for i in range(0, len(vals), g - 2):
+            chunk = vals[i:i + g - 2]
+            row = np.full(g, mx / 2, dtype=np.float32)
+            row[0], row[1] = 0.0, mx
+            row[2:2 + len(chunk)] = chunk
+            rows.append(row)
+    x = np.array(rows, dtype=np.float32)
+    assert len(x) > 0
+    p, sc, mnv = oracle.quant_pack(x, g, bits)
+    codes = oracle.unpack_codes(p, g, bits).view(np.uint8).astype(np.int64)
+    inv = (np.float32(1) / sc).astype(np.float32)
+    t = (x - mnv[:, None]).astype(np.float32)
+    fused = fma32(t, np.broadcast_to(inv[:, None], t.shape), np.full(t.shape, np.float32(0.5 - 1e-6)))
+    unfused = ((t * inv[:, None]).astype(np.float32) + np.float32(0.5 - 1e-6)).astype(np.float32)
+    differ = np.floor(fused) != np.floor(unfused)
+    assert differ.sum() >= 20, "too few distinguishing inputs"
+    np.testing.assert_array_equal(codes, np.clip(np.floor(fused), 0, 255).astype(np.int64))
+
+
+def test_dequant_uses_the_fused_multiply_add():
+    rng = np.random.default_rng(321)
+    q = rng.integers(0, 256, size=(64, 256)).astype(np.uint8)
+    packed = q.view("<u4").reshape(64, -1).copy()
+    sc = (rng.random(64) * 3).astype(np.float32)
+    mn = rng.standard_normal(64).astype(np.float32)
+    y = oracle.dequant_unpack(packed, sc, mn, 256, 8)
+    want = fma32(q.astype(np.float32), np.broadcast_to(sc[:, None], q.shape), np.broadcast_to(mn[:, None], q.shape))
+    np.testing.assert_array_equal(y, want)
+    unfused = ((q.astype(np.float32) * sc[:, None]).astype(np.float32) + mn[:, None]).astype(np.float32)
+    assert np.any(unfused != want)  # the check above can tell the two forms apart
 
 
 @pytest.mark.parametrize("bits", [1, 2, 4, 8])
@@ -222,6 +335,20 @@ def test_oracle_equals_numpy_restatement(bits, rounding):
     np.testing.assert_array_equal(s, s2)
     np.testing.assert_array_equal(m, m2)
     np.testing.assert_array_equal(p, p2)
+
+
+@pytest.mark.parametrize("bits", [1, 2, 4, 8])
+def test_philox_mode_equals_noise_mode_with_the_philox_stream(bits):
+    # Philox rounding is noise-tensor rounding with u = the element's Philox byte (pinned above by
+    # the KAT vectors and the element mapping)
+    rng = np.random.default_rng(50 + bits)
+    g = 128
+    x = rng.standard_normal((37, g)).astype(np.float32)
+    u = oracle.philox_noise(0, x.size, 77, 5).reshape(x.shape)
+    p, s, m = oracle.quant_pack(x, g, bits, rounding=PHILOX, seed=77, offset=5)
+    p2, s2, m2 = numpy_quant(x, bits, NOISE, u)
+    np.testing.assert_array_equal(p, p2)
+    np.testing.assert_array_equal(s, s2)
 
 
 # ----------------------------------------------------------------------------- layout
@@ -305,8 +432,8 @@ def test_stochastic_is_unbiased():
         acc += oracle.dequant_unpack(p, s, m, 64, 2)[0]
     mean = acc / n
     step = float(s[0])
-    # std of one sample <= step/2; 16-bit noise quantisation adds at most step/2^17 of bias
-    assert np.all(np.abs(mean - x[0]) < 5 * (step / 2) / np.sqrt(n) + step / 2 ** 16)
+    # std of one sample <= step/2; 8-bit noise quantisation adds at most step/2^9 of bias
+    assert np.all(np.abs(mean - x[0]) < 5 * (step / 2) / np.sqrt(n) + step / 2 ** 9)
 
 
 # ----------------------------------------------------------------------------- validation
