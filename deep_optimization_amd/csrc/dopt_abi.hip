@@ -207,8 +207,9 @@ int dopt_fp8_gemm_nt(const uint8_t* A, const uint8_t* B, int64_t M, int64_t N, i
     if (M < 0 || N < 0 || K < 0) return fail(DOPT_EINVAL, "negative GEMM extent");
     if (M == 0 || N == 0) return ok();
     if (!A || !B || !C) return fail(DOPT_EINVAL, "null pointer argument");
-    if (M % 256 || N % 256 || K % 128)
-        return fail(DOPT_EUNSUPPORTED, "fp8 GEMM needs M %% 256 == 0, N %% 256 == 0, K %% 128 == 0 (got %lld, %lld, %lld)",
+    if (M % 256 || N % 256 || K % 128 || K == 0)
+        return fail(DOPT_EUNSUPPORTED,
+                    "fp8 GEMM needs M %% 256 == 0, N %% 256 == 0, K %% 128 == 0 and K > 0 (got %lld, %lld, %lld)",
                     (long long)M, (long long)N, (long long)K);
     if (lda < K || ldb < K || ldc < N || lda % 16 || ldb % 16 || ldc % 8 || !aligned16(A) || !aligned16(B) ||
         !aligned16(C))

@@ -1,0 +1,267 @@
+// FP8 (OCP e4m3) scaled GEMM on CDNA4 MFMA, NT layout (A [M,K], B [N,K], both K-contiguous):
+//   C[m][n] = bf16(out_scale * sum_k A[m][k] * B[n][k]), fp32 accumulation, one rounding.
+//
+// Tiling: a workgroup of 4 waves (2 x 2) computes a BM x BN tile; each wave a (BM/2) x (BN/2)
+// sub-tile as TM x TN blocks of v_mfma_f32_32x32x64_f8f6f4 (fp8 x fp8 -> fp32, 32 x 32 x 64 per
+// instruction, 16 accumulator registers per block). At 128 x 128 per wave one 128-byte K slab
+// is 32 MFMAs fed by 16 KB of LDS operand reads per wave, half the LDS bandwidth of a CU.
+//
+// Data movement: K advances in slabs of BK = 128 bytes, double-buffered in LDS (no padding:
+// 2 * (BM + BN) * 128 bytes). Slabs go HBM/L2 -> LDS with global_load_lds_dwordx4 (no staging
+// registers): one instruction moves 64 lanes x 16 bytes into a contiguous 1 KB LDS block, i.e.
+// 8 rows of 128 bytes. The lane -> global address mapping applies an XOR swizzle, so 16-byte
+// chunk c of row r lands at chunk position c ^ ((r / 2) % 8). gfx950's LDS serves a
+// ds_read_b128 16 lanes at a time across 64 banks (256 bytes): an even and an odd row share one
+// bank row, so the 16 consecutive rows of an operand fetch hit 16 distinct 16-byte bank groups
+// (measured: the plain c ^ (r % 8) swizzle left half of all LDS cycles in bank conflicts).
+//
+// Pipeline (one barrier per slab, placed mid-slab):
+//   MFMAs of half 0 | ds_read operands of half 1 | wait LDS reads + slab k+1 loads | barrier |
+//   issue loads of slab k+2 into this buffer | ds_read half 0 of slab k+1 | MFMAs of half 1
+// so the global loads of the next-but-one slab and the operand reads of the next slab overlap
+// the second half of the MFMAs.
+//
+// MFMA operand layout (fp8, 32x32x64): lane l supplies row (l % 32) of its operand and 32
+// consecutive K bytes starting at 32*(l / 32); A and B use the same K mapping, so the dot
+// products pair matching k. Accumulator layout: lane l holds column l % 32 and, in register v,
+// row 8*(v/4) + 4*(l/32) + (v%4). The epilogue scales, rounds to bf16, transposes through LDS
+// and writes 16-byte row chunks.
+//
+// Workgroup order: the hardware hands consecutive workgroup ids to the 8 XCDs in turn, each XCD
+// with its own L2. The id is remapped so that each XCD owns a contiguous range of tiles, walked
+// in groups of GROUP_M tile rows, so the A rows and B columns one XCD streams stay in its L2.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "dopt_device.h"
+
+namespace dopt {
+
+typedef int v8i_t __attribute__((ext_vector_type(8)));
+typedef float v16f_t __attribute__((ext_vector_type(16)));
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(1))) const void gbl_void_t;
+
+__device__ __forceinline__ v16f_t mfma_fp8_32x32x64(const v8i_t& a, const v8i_t& b, const v16f_t& c) {
+    // cbsz = blgp = 0: both operands OCP fp8 e4m3; scale operands 0 select the unscaled MFMA.
+    return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
+}
+
+constexpr int GEMM_XCDS = 8;
+
+template <int BM_, int BN_, int GROUP_M_, int SCHED_ = 1>
+struct Fp8GemmCfg {
+    static constexpr int BM = BM_, BN = BN_, BK = 128, GROUP_M = GROUP_M_;
+    static constexpr int SCHED = SCHED_;  // 0: even MFMA/memory interleave, 1: LDS reads front-loaded
+    static constexpr int THREADS = 256;
+    static constexpr int WM = BM / 2, WN = BN / 2;  // wave tile
+    static constexpr int TM = WM / 32, TN = WN / 32;
+    static constexpr int LA = BM / 32, LB = BN / 32;  // global_load_lds per wave per slab
+    static constexpr int LDS_BYTES = 2 * (BM + BN) * BK;
+    static_assert(BM == BN && (BM == 128 || BM == 256), "square 128 or 256 tiles (epilogue staging)");
+    static_assert(WM * WN * 2 <= BN * BK, "a wave's bf16 tile fits one LDS array");
+    static_assert(LDS_BYTES <= 160 * 1024, "LDS budget of one CU");
+};
+
+template <class C>
+__global__ __launch_bounds__(256, 1) void fp8_gemm_nt_kernel(const uint8_t* __restrict__ A, const uint8_t* __restrict__ B,
+                                                            uint16_t* __restrict__ Cm, int64_t M, int64_t N, int64_t K,
+                                                            int64_t lda, int64_t ldb, int64_t ldc, float out_scale) {
+    constexpr int BM = C::BM, BN = C::BN, BK = C::BK, TM = C::TM, TN = C::TN, WM = C::WM, WN = C::WN;
+    // four separate LDS objects (A and B, two buffers each): the compiler can then prove that an
+    // operand read of one buffer does not alias the in-flight global_load_lds writes into the
+    // other, and does not make the read wait for those loads
+    __shared__ __attribute__((aligned(1024))) uint8_t sA0[BM * BK];
+    __shared__ __attribute__((aligned(1024))) uint8_t sA1[BM * BK];
+    __shared__ __attribute__((aligned(1024))) uint8_t sB0[BN * BK];
+    __shared__ __attribute__((aligned(1024))) uint8_t sB1[BN * BK];
+
+    // ---- XCD-aware tile order: XCD x receives ids x, x+8, x+16, ... (local index bid/8) and
+    // owns the contiguous tile range [x*per + min(x, rem), ... + per + (x < rem)), a bijection
+    const uint32_t tiles_m = (uint32_t)(M / BM), tiles_n = (uint32_t)(N / BN);
+    const uint32_t n_tiles = tiles_m * tiles_n;
+    const uint32_t bid = blockIdx.x;
+    const uint32_t xcd = bid % GEMM_XCDS, local = bid / GEMM_XCDS;
+    const uint32_t per = n_tiles / GEMM_XCDS, rem = n_tiles % GEMM_XCDS;
+    const uint32_t t = xcd * per + min(xcd, rem) + local;
+    // grouped walk: GROUP_M tile rows at a time, column-major inside the group
+    const uint32_t group = C::GROUP_M * tiles_n;
+    const uint32_t first_m = (t / group) * C::GROUP_M;
+    const uint32_t gsize = min(tiles_m - first_m, (uint32_t)C::GROUP_M);
+    const uint32_t tm = first_m + (t % group) % gsize;
+    const uint32_t tn = (t % group) / gsize;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int64_t m0 = (int64_t)tm * BM;
+    const int64_t n0 = (int64_t)tn * BN;
+
+    // ---- global -> LDS slab loads: instruction j of wave w fills the 1 KB block (j*4 + w), rows
+    // r = 8*(j*4 + w) + lane/8, chunk position lane%8 <- global chunk (lane%8) ^ ((r/2) % 8),
+    // where (r/2) % 8 = (4*(w % 2) + lane/16) % 8 does not depend on j
+    const int lrow8 = lane >> 3;
+    const int lchunk = (lane & 7) ^ ((4 * (wave & 1) + (lane >> 4)) & 7);
+    const uint8_t* ga = A + (m0 + 8 * wave + lrow8) * lda + lchunk * 16;
+    const uint8_t* gb = B + (n0 + 8 * wave + lrow8) * ldb + lchunk * 16;
+    auto issue = [&](uint8_t* sa, uint8_t* sb, int64_t k0) {
+#pragma unroll
+        for (int j = 0; j < C::LA; ++j)
+            __builtin_amdgcn_global_load_lds((gbl_void_t*)(ga + (int64_t)(32 * j) * lda + k0),
+                                             (lds_void_t*)(sa + wave * 1024 + j * 4096), 16, 0, 0);
+#pragma unroll
+        for (int j = 0; j < C::LB; ++j)
+            __builtin_amdgcn_global_load_lds((gbl_void_t*)(gb + (int64_t)(32 * j) * ldb + k0),
+                                             (lds_void_t*)(sb + wave * 1024 + j * 4096), 16, 0, 0);
+    };
+
+    // ---- operand reads: tile i of the wave = rows base + i*32 + lane%32; K half h of the slab
+    // is logical chunks 4h + 2*(lane/32) + {0, 1}, stored at chunk position c ^ ((row/2) % 8)
+    const int orow = lane & 31;
+    const int oc = 2 * (lane >> 5);
+    const int sw = (lane >> 1) & 7;  // (row/2) % 8 of this lane's operand rows (base rows are multiples of 16)
+    auto read_ops = [&](const uint8_t* sa, const uint8_t* sb, int h, v8i_t* a, v8i_t* b) {
+        const uint8_t* la = sa + (WM * wm + orow) * BK;
+        const uint8_t* lb = sb + (WN * wn + orow) * BK;
+        const int p0 = ((4 * h + oc) ^ sw) * 16, p1 = ((4 * h + oc + 1) ^ sw) * 16;
+#pragma unroll
+        for (int i = 0; i < TM; ++i) {
+            const uint4 x0 = *(const uint4*)(la + i * 32 * BK + p0);
+            const uint4 x1 = *(const uint4*)(la + i * 32 * BK + p1);
+            a[i] = v8i_t{(int)x0.x, (int)x0.y, (int)x0.z, (int)x0.w, (int)x1.x, (int)x1.y, (int)x1.z, (int)x1.w};
+        }
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+            const uint4 x0 = *(const uint4*)(lb + j * 32 * BK + p0);
+            const uint4 x1 = *(const uint4*)(lb + j * 32 * BK + p1);
+            b[j] = v8i_t{(int)x0.x, (int)x0.y, (int)x0.z, (int)x0.w, (int)x1.x, (int)x1.y, (int)x1.z, (int)x1.w};
+        }
+    };
+
+    v16f_t acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
+
+    v8i_t a0[TM], b0[TN], a1[TM], b1[TN];
+    auto mma = [&](const v8i_t* a, const v8i_t* b) {
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int j = 0; j < TN; ++j) acc[i][j] = mfma_fp8_32x32x64(a[i], b[j], acc[i][j]);
+    };
+    // one slab: (sa, sb) hold slab kt, (na, nb) slab kt+1 (loads in flight), half 0 operands of
+    // slab kt already in a0/b0. The body is branch-free: the last two slabs still issue a load
+    // (of the final slab again, an L2 hit, into a buffer nobody reads any more) and read the next
+    // buffer's half 0 (unused), so every slab is one scheduling region pair. The
+    // sched_group_barrier hints interleave one MFMA with the LDS reads / global loads that run
+    // beside it, so the in-order issue never parks a memory instruction behind a run of MFMAs.
+    const int nk = (int)(K / BK);
+    auto slab = [&](int kt, uint8_t* sa, uint8_t* sb, uint8_t* na, uint8_t* nb) {
+        constexpr int NM = TM * TN;        // MFMAs per half slab
+        constexpr int NR = 2 * (TM + TN);  // ds_read_b128 per half slab
+        read_ops(sa, sb, 1, a1, b1);
+        mma(a0, b0);
+        if constexpr (C::SCHED == 0) {
+#pragma unroll
+            for (int q = 0; q < NM; ++q) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
+            }
+        } else {
+            // LDS reads in the first half of the region, two per MFMA, so their latency is
+            // covered by the MFMAs that follow before the wait at the barrier
+#pragma unroll
+            for (int q = 0; q < NR / 2; ++q) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+            }
+            __builtin_amdgcn_sched_group_barrier(0x008, NM - NR / 2, 0);
+        }
+        // every LDS read of (sa, sb) and every load of slab kt+1 has landed, in all waves
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        issue(sa, sb, (int64_t)min(kt + 2, nk - 1) * BK);
+        read_ops(na, nb, 0, a0, b0);
+        mma(a1, b1);
+        if constexpr (C::SCHED == 0) {
+#pragma unroll
+            for (int q = 0; q < NM; ++q) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+                __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // one global load
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
+            }
+        } else {
+            // next slab's half-0 operands first (consumed at the top of the next slab), then the
+            // global loads of slab kt+2 (consumed a slab later)
+#pragma unroll
+            for (int q = 0; q < NR / 2; ++q) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+            }
+#pragma unroll
+            for (int q = 0; q < NM - NR / 2; ++q) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x020, 2, 0);
+            }
+        }
+    };
+
+    issue(sA0, sB0, 0);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    issue(sA1, sB1, (int64_t)min(1, nk - 1) * BK);
+    read_ops(sA0, sB0, 0, a0, b0);
+    int kt = 0;
+    for (; kt + 1 < nk; kt += 2) {
+        slab(kt, sA0, sB0, sA1, sB1);
+        slab(kt + 1, sA1, sB1, sA0, sB0);
+    }
+    if (kt < nk) slab(kt, sA0, sB0, sA1, sB1);
+    // the trailing loads must land before LDS is reused below
+    __builtin_amdgcn_s_waitcnt(0);
+
+    // ---- epilogue: scale, round once to bf16, transpose through LDS, 16-byte row stores.
+    // Wave w stages its WM x WN bf16 tile in one of the four LDS arrays (each >= WM*WN*2 bytes).
+    __syncthreads();
+    uint16_t* tile = (uint16_t*)(wave == 0 ? sA0 : wave == 1 ? sA1 : wave == 2 ? sB0 : sB1);
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+            const int col = j * 32 + (lane & 31);
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                const int row = i * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+                tile[row * WN + col] = to_bf16(acc[i][j][v] * out_scale);
+            }
+        }
+    __builtin_amdgcn_s_waitcnt(0);
+    __builtin_amdgcn_wave_barrier();
+    constexpr int CPR = WN / 8;  // 16-byte chunks per tile row
+    uint16_t* cbase = Cm + (m0 + WM * wm) * ldc + n0 + WN * wn;
+#pragma unroll 4
+    for (int q = lane; q < WM * CPR; q += 64) {
+        const int row = q / CPR, c = q % CPR;
+        *(uint4*)(cbase + row * ldc + c * 8) = *(const uint4*)(tile + row * WN + c * 8);
+    }
+}
+
+template <class C>
+inline int fp8_gemm_launch(const uint8_t* A, const uint8_t* B, int64_t M, int64_t N, int64_t K, int64_t lda,
+                           int64_t ldb, float out_scale, uint16_t* Cm, int64_t ldc, hipStream_t s) {
+    if (M % C::BM || N % C::BN || K % C::BK) return -1;
+    const int64_t tiles = (M / C::BM) * (N / C::BN);
+    if (tiles == 0 || K == 0) return tiles == 0 ? 0 : -1;
+    hipLaunchKernelGGL(fp8_gemm_nt_kernel<C>, dim3((uint32_t)tiles), dim3(C::THREADS), 0, s, A, B, Cm, M, N, K, lda,
+                       ldb, ldc, out_scale);
+    return 0;
+}
+
+}  // namespace dopt

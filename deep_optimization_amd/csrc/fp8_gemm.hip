@@ -1,135 +1,16 @@
-// FP8 (OCP e4m3) scaled GEMM on CDNA4 MFMA, NT layout (A [M,K], B [N,K], both K-contiguous):
-//   C[m][n] = bf16(out_scale * sum_k A[m][k] * B[n][k]), fp32 accumulation.
+// FP8 e4m3 scaled GEMM launcher (kernel and tiling in fp8_gemm.h).
 //
-// Tiling: a 256-thread workgroup (4 waves, 2 x 2) computes a BM x BN = 128 x 128 tile; each wave
-// a 64 x 64 sub-tile as 2 x 2 v_mfma_f32_32x32x64_f8f6f4 (fp8 x fp8 -> fp32, 32 x 32 x 64 per
-// instruction). K advances in BK = 128-byte slabs staged in LDS, double-buffered: the global
-// loads of slab k+1 are in flight while slab k feeds the MFMAs. LDS rows are padded by 16 B so
-// the 32 rows read by one MFMA operand fetch spread over all banks.
-//
-// MFMA operand layout (fp8, 32x32x64): lane l supplies row (l % 32) of its operand and 32
-// consecutive K bytes starting at 32*(l / 32); A and B use the same K mapping, so the dot
-// products pair matching k. Accumulator layout: lane l holds column l % 32 and, in register v,
-// row 8*(v/4) + 4*(l/32) + (v%4).
-#include <hip/hip_runtime.h>
-#include <stdint.h>
-
-#include "dopt_device.h"
+// Configuration: 256 x 256 workgroup tiles (128 x 128 per wave), GROUP_M = 4 tile rows per
+// L2 group, even MFMA / memory interleave; measured on MI355X at 8192^3 and 4096x11008x4096.
+#include "fp8_gemm.h"
 
 namespace dopt {
 
-typedef int v8i_t __attribute__((ext_vector_type(8)));
-typedef float v16f_t __attribute__((ext_vector_type(16)));
-
-namespace {
-
-constexpr int BM = 128, BN = 128, BK = 128;
-constexpr int LDK = BK + 16;  // padded LDS row (bytes)
-constexpr int THREADS = 256;
-constexpr int VEC_PER_THREAD = BM * BK / 16 / THREADS;  // 16-byte vectors per operand per slab
-
-__device__ __forceinline__ v16f_t mfma_fp8_32x32x64(const v8i_t& a, const v8i_t& b, const v16f_t& c) {
-    // cbsz = blgp = 0: both operands OCP fp8 e4m3; no block scales.
-    return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
-}
-
-__global__ __launch_bounds__(THREADS) void fp8_gemm_nt_kernel(const uint8_t* __restrict__ A,
-                                                              const uint8_t* __restrict__ B,
-                                                              uint16_t* __restrict__ C, int64_t K, int64_t lda,
-                                                              int64_t ldb, int64_t ldc, float out_scale) {
-    __shared__ __attribute__((aligned(16))) uint8_t sA[2][BM * LDK];
-    __shared__ __attribute__((aligned(16))) uint8_t sB[2][BN * LDK];
-
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = tid >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
-    const int64_t m0 = (int64_t)blockIdx.y * BM;
-    const int64_t n0 = (int64_t)blockIdx.x * BN;
-    const uint8_t* Ab = A + m0 * lda;
-    const uint8_t* Bb = B + n0 * ldb;
-
-    uint4 ra[VEC_PER_THREAD], rb[VEC_PER_THREAD];
-    auto gload = [&](int64_t k0) {
-#pragma unroll
-        for (int j = 0; j < VEC_PER_THREAD; ++j) {
-            const int q = tid + THREADS * j;
-            const int row = q / (BK / 16), c16 = q % (BK / 16);
-            ra[j] = *(const uint4*)(Ab + row * lda + k0 + c16 * 16);
-            rb[j] = *(const uint4*)(Bb + row * ldb + k0 + c16 * 16);
-        }
-    };
-    auto lstore = [&](int buf) {
-#pragma unroll
-        for (int j = 0; j < VEC_PER_THREAD; ++j) {
-            const int q = tid + THREADS * j;
-            const int row = q / (BK / 16), c16 = q % (BK / 16);
-            *(uint4*)&sA[buf][row * LDK + c16 * 16] = ra[j];
-            *(uint4*)&sB[buf][row * LDK + c16 * 16] = rb[j];
-        }
-    };
-
-    v16f_t acc[2][2];
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-#pragma unroll
-            for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
-
-    const int nk = (int)(K / BK);
-    gload(0);
-    lstore(0);
-    __syncthreads();
-
-    const int lrow = lane & 31;
-    const int lk = (lane >> 5) * 32;
-    for (int kt = 0; kt < nk; ++kt) {
-        const int cur = kt & 1;
-        if (kt + 1 < nk) gload((int64_t)(kt + 1) * BK);
-#pragma unroll
-        for (int ks = 0; ks < BK / 64; ++ks) {
-            v8i_t a[2], b[2];
-#pragma unroll
-            for (int i = 0; i < 2; ++i) {
-                const uint8_t* pa = &sA[cur][(wm * 64 + i * 32 + lrow) * LDK + ks * 64 + lk];
-                const uint8_t* pb = &sB[cur][(wn * 64 + i * 32 + lrow) * LDK + ks * 64 + lk];
-                const uint4 a0 = ((const uint4*)pa)[0], a1 = ((const uint4*)pa)[1];
-                const uint4 b0 = ((const uint4*)pb)[0], b1 = ((const uint4*)pb)[1];
-                a[i] = v8i_t{(int)a0.x, (int)a0.y, (int)a0.z, (int)a0.w, (int)a1.x, (int)a1.y, (int)a1.z, (int)a1.w};
-                b[i] = v8i_t{(int)b0.x, (int)b0.y, (int)b0.z, (int)b0.w, (int)b1.x, (int)b1.y, (int)b1.z, (int)b1.w};
-            }
-#pragma unroll
-            for (int i = 0; i < 2; ++i)
-#pragma unroll
-                for (int j = 0; j < 2; ++j) acc[i][j] = mfma_fp8_32x32x64(a[i], b[j], acc[i][j]);
-        }
-        if (kt + 1 < nk) lstore(cur ^ 1);
-        __syncthreads();
-    }
-
-    // epilogue: scale, round once to bf16, store
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const int64_t col = n0 + wn * 64 + j * 32 + (lane & 31);
-#pragma unroll
-            for (int v = 0; v < 16; ++v) {
-                const int64_t row = m0 + wm * 64 + i * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
-                C[row * ldc + col] = to_bf16(acc[i][j][v] * out_scale);
-            }
-        }
-}
-
-}  // namespace
+using Fp8GemmDefault = Fp8GemmCfg<256, 256, 4, 0>;
 
 int launch_fp8_gemm_nt(const uint8_t* A, const uint8_t* B, int64_t M, int64_t N, int64_t K, int64_t lda,
                        int64_t ldb, float out_scale, uint16_t* C, int64_t ldc, hipStream_t s) {
-    if (M % BM || N % BN || K % BK) return -1;
-    const dim3 grid((uint32_t)(N / BN), (uint32_t)(M / BM));
-    hipLaunchKernelGGL(fp8_gemm_nt_kernel, grid, dim3(THREADS), 0, s, A, B, C, K, lda, ldb, ldc, out_scale);
-    return 0;
+    return fp8_gemm_launch<Fp8GemmDefault>(A, B, M, N, K, lda, ldb, out_scale, C, ldc, s);
 }
 
 }  // namespace dopt

@@ -126,7 +126,7 @@ int dopt_unpack_codes(const uint32_t* packed, int64_t n_groups, int group_size, 
  * (Activation_Compression/triton_kernel/linear.py:43-95, fp32 accumulate :81-86, cast :91), which
  * has no callers; the contraction it stands for is the weight/input-gradient GEMM of
  * _DOLinear.backward (Activation_Compression/modules/ops.py:508-512).
- * Requires M % 256 == 0, N % 256 == 0, K % 128 == 0, 16-byte aligned rows.
+ * Requires M % 256 == 0, N % 256 == 0, K % 128 == 0, K > 0, 16-byte aligned rows.
  */
 int dopt_fp8_gemm_nt(const uint8_t* A, const uint8_t* B, int64_t M, int64_t N, int64_t K,
                      int64_t lda, int64_t ldb, float out_scale, void* C, int64_t ldc, void* stream);
