@@ -17,8 +17,9 @@ the scale/min dtype (fp32 or bf16), the output dtype, and the fused s x s spatia
 (act_lib::quant_pack_tiles / act_lib::dequant_unpack_tiles), which removes the permute copy of
 tensor_act_reshape_utils.py:128 and :152.
 
-Every operator is registered for CUDA (HIP) tensors only and has a fake (meta) implementation
-with the correct output shapes; there is no CPU implementation.
+Every operator is registered straight with the dispatcher (``torch.library.Library``: one Python
+call per op, no wrapper layers) for CUDA (HIP) tensors only, and has a fake (meta)
+implementation with the correct output shapes; there is no CPU implementation.
 """
 from __future__ import annotations
 
@@ -63,7 +64,8 @@ def rounding_code(rounding) -> int:
 
 
 def _stream(t: Tensor) -> int:
-    return torch.cuda.current_stream(t.device).cuda_stream
+    """Raw hipStream_t of torch's current stream on t's device (what the C ABI enqueues on)."""
+    return torch._C._cuda_getCurrentRawStream(t.get_device())
 
 
 def _require_cuda(*ts: Tensor) -> None:
@@ -137,11 +139,27 @@ def _dequant_launch(packed: Tensor, scale: Tensor, xmin: Tensor, n_groups: int, 
     return out
 
 
+# --------------------------------------------------------------------------- registration
+_LIB = torch.library.Library("act_lib", "DEF")
+
+
+def _op(schema: str, impl, fake):
+    """Define act_lib::<schema>, bind the HIP implementation and the fake (meta) kernel."""
+    name = schema.split("(", 1)[0]
+    _LIB.define(schema)
+    _LIB.impl(name, impl, "CUDA")
+    torch.library.register_fake(f"act_lib::{name}", fake, lib=_LIB)
+    return getattr(torch.ops.act_lib, name)
+
+
+def _meta3(x: Tensor, N: int, G: int, bits: int, group_size: int, scale_dtype: torch.dtype):
+    _, nwords, _ = _bits_consts(bits, group_size)
+    return (x.new_empty((N * G, nwords), dtype=torch.int32), x.new_empty((N, G), dtype=scale_dtype),
+            x.new_empty((N, G), dtype=scale_dtype))
+
+
 # --------------------------------------------------------------------------- general operators
-@torch.library.custom_op("act_lib::quant_pack", mutates_args=(), device_types="cuda")
-def quant_pack(x: Tensor, bits: int, group_size: int, clamp: bool, clamp_alpha: float, squash: bool,
-               rounding: int, noise: Optional[Tensor], seed: int, offset: int,
-               scale_dtype: torch.dtype) -> Tuple[Tensor, Tensor, Tensor]:
+def _quant_pack(x, bits, group_size, clamp, clamp_alpha, squash, rounding, noise, seed, offset, scale_dtype):
     """x [N, G, group_size] -> (packed int32 [N*G, W], scale [N, G], min [N, G])."""
     if x.dim() != 3 or x.shape[-1] != group_size:
         raise RuntimeError(f"quant_pack expects x of shape [N, G, {group_size}], got {tuple(x.shape)}")
@@ -151,12 +169,12 @@ def quant_pack(x: Tensor, bits: int, group_size: int, clamp: bool, clamp_alpha: 
     return packed, scale.view(N, G), xmin.view(N, G)
 
 
-@quant_pack.register_fake
-def _(x, bits, group_size, clamp, clamp_alpha, squash, rounding, noise, seed, offset, scale_dtype):
-    N, G = x.shape[0], x.shape[1]
-    _, nwords, _ = _bits_consts(bits, group_size)
-    return (x.new_empty((N * G, nwords), dtype=torch.int32), x.new_empty((N, G), dtype=scale_dtype),
-            x.new_empty((N, G), dtype=scale_dtype))
+quant_pack = _op(
+    "quant_pack(Tensor x, int bits, int group_size, bool clamp, float clamp_alpha, bool squash, int rounding, "
+    "Tensor? noise, int seed, int offset, ScalarType scale_dtype) -> (Tensor, Tensor, Tensor)",
+    _quant_pack,
+    lambda x, bits, group_size, clamp, clamp_alpha, squash, rounding, noise, seed, offset, scale_dtype:
+        _meta3(x, x.shape[0], x.shape[1], bits, group_size, scale_dtype))
 
 
 def _tile_groups(shape, group_size: int):
@@ -170,10 +188,7 @@ def _tile_groups(shape, group_size: int):
     return N, C * (H // s) * (W // s)
 
 
-@torch.library.custom_op("act_lib::quant_pack_tiles", mutates_args=(), device_types="cuda")
-def quant_pack_tiles(x: Tensor, bits: int, group_size: int, clamp: bool, clamp_alpha: float,
-                     squash: bool, rounding: int, noise: Optional[Tensor], seed: int, offset: int,
-                     scale_dtype: torch.dtype) -> Tuple[Tensor, Tensor, Tensor]:
+def _quant_pack_tiles(x, bits, group_size, clamp, clamp_alpha, squash, rounding, noise, seed, offset, scale_dtype):
     """x [N, C, H, W] grouped into s x s spatial tiles (s*s = group_size), read in place."""
     N, G = _tile_groups(x.shape, group_size)
     packed, scale, xmin = _quant_pack_launch(x, N * G, bits, group_size, tuple(x.shape), clamp,
@@ -182,17 +197,19 @@ def quant_pack_tiles(x: Tensor, bits: int, group_size: int, clamp: bool, clamp_a
     return packed, scale.view(N, G), xmin.view(N, G)
 
 
-@quant_pack_tiles.register_fake
-def _(x, bits, group_size, clamp, clamp_alpha, squash, rounding, noise, seed, offset, scale_dtype):
+def _quant_pack_tiles_fake(x, bits, group_size, clamp, clamp_alpha, squash, rounding, noise, seed, offset,
+                           scale_dtype):
     N, G = _tile_groups(x.shape, group_size)
-    _, nwords, _ = _bits_consts(bits, group_size)
-    return (x.new_empty((N * G, nwords), dtype=torch.int32), x.new_empty((N, G), dtype=scale_dtype),
-            x.new_empty((N, G), dtype=scale_dtype))
+    return _meta3(x, N, G, bits, group_size, scale_dtype)
 
 
-@torch.library.custom_op("act_lib::dequant_unpack", mutates_args=(), device_types="cuda")
-def dequant_unpack(packed: Tensor, scale: Tensor, xmin: Tensor, bits: int, group_size: int,
-                   out_dtype: torch.dtype) -> Tensor:
+quant_pack_tiles = _op(
+    "quant_pack_tiles(Tensor x, int bits, int group_size, bool clamp, float clamp_alpha, bool squash, "
+    "int rounding, Tensor? noise, int seed, int offset, ScalarType scale_dtype) -> (Tensor, Tensor, Tensor)",
+    _quant_pack_tiles, _quant_pack_tiles_fake)
+
+
+def _dequant_unpack(packed, scale, xmin, bits, group_size, out_dtype):
     """-> [N, G, group_size] of out_dtype (float32 or bfloat16)."""
     N, G = scale.shape
     if out_dtype not in _OUT_CODE:
@@ -201,15 +218,15 @@ def dequant_unpack(packed: Tensor, scale: Tensor, xmin: Tensor, bits: int, group
     return _dequant_launch(packed, scale, xmin, N * G, bits, group_size, None, y)
 
 
-@dequant_unpack.register_fake
-def _(packed, scale, xmin, bits, group_size, out_dtype):
-    N, G = scale.shape
-    return packed.new_empty((N, G, group_size), dtype=out_dtype)
+dequant_unpack = _op(
+    "dequant_unpack(Tensor packed, Tensor scale, Tensor xmin, int bits, int group_size, ScalarType out_dtype) "
+    "-> Tensor",
+    _dequant_unpack,
+    lambda packed, scale, xmin, bits, group_size, out_dtype:
+        packed.new_empty((scale.shape[0], scale.shape[1], group_size), dtype=out_dtype))
 
 
-@torch.library.custom_op("act_lib::dequant_unpack_tiles", mutates_args=(), device_types="cuda")
-def dequant_unpack_tiles(packed: Tensor, scale: Tensor, xmin: Tensor, bits: int, group_size: int,
-                         N: int, C: int, H: int, W: int, out_dtype: torch.dtype) -> Tensor:
+def _dequant_unpack_tiles(packed, scale, xmin, bits, group_size, N, C, H, W, out_dtype):
     """-> [N, C, H, W] of out_dtype: the inverse tile scatter is fused into the stores."""
     n, G = _tile_groups((N, C, H, W), group_size)
     if tuple(scale.shape) != (n, G):
@@ -220,9 +237,12 @@ def dequant_unpack_tiles(packed: Tensor, scale: Tensor, xmin: Tensor, bits: int,
     return _dequant_launch(packed, scale, xmin, n * G, bits, group_size, (N, C, H, W), y)
 
 
-@dequant_unpack_tiles.register_fake
-def _(packed, scale, xmin, bits, group_size, N, C, H, W, out_dtype):
-    return packed.new_empty((N, C, H, W), dtype=out_dtype)
+dequant_unpack_tiles = _op(
+    "dequant_unpack_tiles(Tensor packed, Tensor scale, Tensor xmin, int bits, int group_size, int N, int C, "
+    "int H, int W, ScalarType out_dtype) -> Tensor",
+    _dequant_unpack_tiles,
+    lambda packed, scale, xmin, bits, group_size, N, C, H, W, out_dtype:
+        packed.new_empty((N, C, H, W), dtype=out_dtype))
 
 
 # --------------------------------------------------------------------------- reference schemas
@@ -233,9 +253,7 @@ def _no_alam(avg_alam: bool, where: str) -> None:
             "Linear/Conv layer, controller.py:186-187, and its dequant noise uses Triton's tl.randn)")
 
 
-@torch.library.custom_op("act_lib::quant_pack_triton", mutates_args=(), device_types="cuda")
-def quant_pack_triton(x: Tensor, bits: int, group_size: int, avg_alam: bool, alam_bits: int,
-                      clamp: bool, clamp_alpha: float) -> Tuple[Tensor, Tensor, Tensor]:
+def _quant_pack_triton(x, bits, group_size, avg_alam, alam_bits, clamp, clamp_alpha):
     """Reference semantics (act_triton_kernel.py:336-368): [clamp], tanh squash, nearest
     rounding, bf16 scale and min."""
     _no_alam(avg_alam, "quant_pack_triton")
@@ -247,32 +265,32 @@ def quant_pack_triton(x: Tensor, bits: int, group_size: int, avg_alam: bool, ala
     return packed, scale.view(N, G), xmin.view(N, G)
 
 
-@quant_pack_triton.register_fake
-def _(x, bits, group_size, avg_alam, alam_bits, clamp, clamp_alpha):
-    N, G = x.shape[0], x.shape[1]
-    _, nwords, _ = _bits_consts(bits, group_size)
-    return (x.new_empty((N * G, nwords), dtype=torch.int32), x.new_empty((N, G), dtype=torch.bfloat16),
-            x.new_empty((N, G), dtype=torch.bfloat16))
+quant_pack_triton = _op(
+    "quant_pack_triton(Tensor x, int bits, int group_size, bool avg_alam, int alam_bits, bool clamp, "
+    "float clamp_alpha) -> (Tensor, Tensor, Tensor)",
+    _quant_pack_triton,
+    lambda x, bits, group_size, avg_alam, alam_bits, clamp, clamp_alpha:
+        _meta3(x, x.shape[0], x.shape[1], bits, group_size, torch.bfloat16))
 
 
-@torch.library.custom_op("act_lib::dequant_unpack_triton", mutates_args=(), device_types="cuda")
-def dequant_unpack_triton(packed: Tensor, scale: Tensor, xmin: Tensor, bits: int, group_size: int,
-                          avg_alam: bool, alam_bits: int) -> Tensor:
-    """Reference semantics (act_triton_kernel.py:372-395): bf16 output [N, G, g]."""
+def _dequant_unpack_triton(packed, scale, xmin, bits, group_size, avg_alam, alam_bits):
+    """Reference semantics (act_triton_kernel.py:372-395): bf16 output [N, G, g] whatever the
+    scale dtype (the reference allocates y as bf16, :382), one rounding from fp32."""
     _no_alam(avg_alam, "dequant_unpack_triton")
     N, G = scale.shape
     y = torch.empty((N, G, group_size), dtype=torch.bfloat16, device=packed.device)
     return _dequant_launch(packed, scale, xmin, N * G, bits, group_size, None, y)
 
 
-@dequant_unpack_triton.register_fake
-def _(packed, scale, xmin, bits, group_size, avg_alam, alam_bits):
-    N, G = scale.shape
-    return packed.new_empty((N, G, group_size), dtype=torch.bfloat16)
+dequant_unpack_triton = _op(
+    "dequant_unpack_triton(Tensor packed, Tensor scale, Tensor xmin, int bits, int group_size, bool avg_alam, "
+    "int alam_bits) -> Tensor",
+    _dequant_unpack_triton,
+    lambda packed, scale, xmin, bits, group_size, avg_alam, alam_bits:
+        packed.new_empty((scale.shape[0], scale.shape[1], group_size), dtype=torch.bfloat16))
 
 
-@torch.library.custom_op("act_lib::pack_triton", mutates_args=(), device_types="cuda")
-def pack_triton(x: Tensor, bits: int, group_size: int) -> Tensor:
+def _pack_triton(x, bits, group_size):
     """int8 codes [N, G, g] -> int32 words [N*G, W] (act_triton_kernel.py:398-417)."""
     if x.dim() != 3 or x.shape[-1] != group_size:
         raise RuntimeError(f"pack_triton expects x of shape [N, G, {group_size}], got {tuple(x.shape)}")
@@ -286,15 +304,14 @@ def pack_triton(x: Tensor, bits: int, group_size: int) -> Tensor:
     return packed
 
 
-@pack_triton.register_fake
-def _(x, bits, group_size):
-    N, G, _ = x.shape
-    _, nwords, _ = _bits_consts(bits, group_size)
-    return x.new_empty((N * G, nwords), dtype=torch.int32)
+pack_triton = _op(
+    "pack_triton(Tensor x, int bits, int group_size) -> Tensor",
+    _pack_triton,
+    lambda x, bits, group_size:
+        x.new_empty((x.shape[0] * x.shape[1], _bits_consts(bits, group_size)[1]), dtype=torch.int32))
 
 
-@torch.library.custom_op("act_lib::unpack_triton", mutates_args=(), device_types="cuda")
-def unpack_triton(packed: Tensor, bits: int, N: int, G: int, group_size: int) -> Tensor:
+def _unpack_triton(packed, bits, N, G, group_size):
     """int32 words [N*G, W] -> int8 codes [N, G, g] (act_triton_kernel.py:419-433)."""
     _bits_consts(bits, group_size)
     _require_cuda(packed)
@@ -308,14 +325,14 @@ def unpack_triton(packed: Tensor, bits: int, N: int, G: int, group_size: int) ->
     return out.view(N, G, group_size)
 
 
-@unpack_triton.register_fake
-def _(packed, bits, N, G, group_size):
-    return packed.new_empty((N, G, group_size), dtype=torch.int8)
+unpack_triton = _op(
+    "unpack_triton(Tensor packed, int bits, int N, int G, int group_size) -> Tensor",
+    _unpack_triton,
+    lambda packed, bits, N, G, group_size: packed.new_empty((N, G, group_size), dtype=torch.int8))
 
 
 # --------------------------------------------------------------------------- FP8 GEMM
-@torch.library.custom_op("act_lib::fp8_gemm_nt", mutates_args=(), device_types="cuda")
-def fp8_gemm_nt(a: Tensor, b: Tensor, out_scale: float) -> Tensor:
+def _fp8_gemm_nt(a, b, out_scale):
     """a [M, K] e4m3, b [N, K] e4m3 -> bf16 [M, N] = out_scale * a @ b.T (fp32 accumulate)."""
     if a.dtype != torch.float8_e4m3fn or b.dtype != torch.float8_e4m3fn:
         raise RuntimeError("fp8_gemm_nt expects torch.float8_e4m3fn operands")
@@ -333,6 +350,7 @@ def fp8_gemm_nt(a: Tensor, b: Tensor, out_scale: float) -> Tensor:
     return c
 
 
-@fp8_gemm_nt.register_fake
-def _(a, b, out_scale):
-    return a.new_empty((a.shape[0], b.shape[0]), dtype=torch.bfloat16)
+fp8_gemm_nt = _op(
+    "fp8_gemm_nt(Tensor a, Tensor b, float out_scale) -> Tensor",
+    _fp8_gemm_nt,
+    lambda a, b, out_scale: a.new_empty((a.shape[0], b.shape[0]), dtype=torch.bfloat16))
