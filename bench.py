@@ -244,7 +244,39 @@ def main() -> int:
                                 "packed_bytes": ve * b // 8 + vng * 8, "compression_vs_bf16": round(ve * 2 / (ve * b / 8 + vng * 8), 2),
                                 "ms_per_step": round(st * 1e3, 4)}
         extras["vit_mlp_sweep_philox_g128"] = sweep
-        del v, vgrp
+        # fused activation layers: GELU / SiLU (y + 2-bit quantized derivative, g = 128, bf16
+        # scale/min) on the ViT MLP activation, ReLU (y + 1-bit mask) on the ResNet activation;
+        # bytes per element: forward in + y + codes (+ 4 B per group), backward codes (+ 4 B per
+        # group) + dy + dx
+        fused = {}
+        vin = torch.randn((256, 197, 3072), generator=vg, device=dev).to(torch.bfloat16)
+        dyv = torch.randn_like(vin)
+        for name, fwd, bwd in (
+                ("gelu", lambda: ops.gelu_fwd_fused_quan_pack(vin, 2, 128),
+                 lambda o: ops.gelu_bwd_fused_dequan_unpack(o[1], dyv, o[2], o[3], 2, o[4], o[5], 128)),
+                ("silu", lambda: ops.silu_fwd_quan_pack(vin, 2, 128, False, 0, False),
+                 lambda o: ops.silu_bwd_fused_dequan_unpack(o[1], dyv, o[2], o[3], 2, o[4], o[5], 128, False, o[6],
+                                                            o[7], o[8], o[9], False, 0))):
+            o = fwd()
+            tf = event_avg(fwd)
+            tb = event_avg(lambda: bwd(o))
+            fb = ve * (2 + 2) + ve * 2 // 8 + vng * 4
+            bb = ve * 2 // 8 + vng * 4 + ve * (2 + 2)
+            fused[f"{name}_vit_2bit_g128"] = {"fwd_us": round(tf * 1e6, 2), "fwd_frac": round(fb / tf / 1e9 / HBM_PEAK_GBS, 4),
+                                              "bwd_us": round(tb * 1e6, 2), "bwd_frac": round(bb / tb / 1e9 / HBM_PEAK_GBS, 4)}
+            del o
+        del vin, dyv, v, vgrp
+        torch.cuda.empty_cache()
+        dyr = torch.randn_like(x)
+        o = ops.relu_fwd_fused_pack(x, True, False, 1, G_SIZE)
+        tf = event_avg(lambda: ops.relu_fwd_fused_pack(x, True, False, 1, G_SIZE))
+        tb = event_avg(lambda: ops.relu_bwd_fused_unpack(o[1], dyr, 1, o[2], o[3], G_SIZE))
+        fb = n_elem * (2 + 2) + n_elem // 8
+        bb = n_elem // 8 + n_elem * (2 + 2)
+        fused["relu_resnet_1bit"] = {"fwd_us": round(tf * 1e6, 2), "fwd_frac": round(fb / tf / 1e9 / HBM_PEAK_GBS, 4),
+                                     "bwd_us": round(tb * 1e6, 2), "bwd_frac": round(bb / tb / 1e9 / HBM_PEAK_GBS, 4)}
+        del o, dyr
+        extras["fused_activation_layers"] = fused
         torch.cuda.empty_cache()
         # config 4: FP8 e4m3 scaled GEMM, beside hipBLASLt (torch._scaled_mm) on the same operands
         gemm = {}

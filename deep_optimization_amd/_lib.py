@@ -15,6 +15,7 @@ LIB_PATH = os.path.join(_PKG, "libdopt.so")
 F32, F16, BF16 = 0, 1, 2
 ROUND_NEAREST, ROUND_STOCH_NOISE, ROUND_STOCH_PHILOX = 0, 1, 2
 FLAG_CLAMP, FLAG_SQUASH = 1, 2
+ACT_RELU, ACT_RELU6, ACT_GELU, ACT_SILU = 0, 1, 2, 3
 
 OK, EBITS, EINVAL, EUNSUPPORTED, EHIP = 0, -1, -2, -3, -4
 
@@ -26,6 +27,11 @@ EXPORTS = (
     "dopt_pack_codes",
     "dopt_unpack_codes",
     "dopt_fp8_gemm_nt",
+    "dopt_relu_pack",
+    "dopt_relu_unpack",
+    "dopt_act_forward",
+    "dopt_act_quant_pack",
+    "dopt_act_dequant_mul",
 )
 
 _lib = None
@@ -62,6 +68,16 @@ def lib() -> ctypes.CDLL:
         L.dopt_unpack_codes.restype = i32
         L.dopt_fp8_gemm_nt.argtypes = [vp, vp, i64, i64, i64, i64, i64, f32, vp, i64, vp]
         L.dopt_fp8_gemm_nt.restype = i32
+        L.dopt_relu_pack.argtypes = [vp, i32, i64, i32, i32, vp, vp, vp]
+        L.dopt_relu_pack.restype = i32
+        L.dopt_relu_unpack.argtypes = [vp, vp, i32, i64, i32, vp, vp]
+        L.dopt_relu_unpack.restype = i32
+        L.dopt_act_forward.argtypes = [vp, i32, i64, i32, vp, vp, vp]
+        L.dopt_act_forward.restype = i32
+        L.dopt_act_quant_pack.argtypes = [vp, i32, i32, i64, i32, i32, vp, vp, vp, vp, vp, i32, vp]
+        L.dopt_act_quant_pack.restype = i32
+        L.dopt_act_dequant_mul.argtypes = [vp, vp, vp, i32, i64, i32, i32, vp, vp, i32, vp, vp]
+        L.dopt_act_dequant_mul.restype = i32
         _lib = L
     return _lib
 

@@ -354,3 +354,243 @@ fp8_gemm_nt = _op(
     "fp8_gemm_nt(Tensor a, Tensor b, float out_scale) -> Tensor",
     _fp8_gemm_nt,
     lambda a, b, out_scale: a.new_empty((a.shape[0], b.shape[0]), dtype=torch.bfloat16))
+
+
+# --------------------------------------------------------------------------- fused activation layers
+# Reference: Activation_Compression/modules/activations/kernel_registration.py (op names and
+# schemas kept), kernels in kernel_implementation.py. Scale and min are bf16 [N*G] as there.
+ACT_RELU, ACT_RELU6, ACT_GELU, ACT_SILU = _lib.ACT_RELU, _lib.ACT_RELU6, _lib.ACT_GELU, _lib.ACT_SILU
+
+
+def _relu_act(relu: bool, relu6: bool) -> int:
+    if relu:
+        return ACT_RELU
+    if relu6:
+        return ACT_RELU6
+    raise RuntimeError("relu ops need relu=True or relu6=True (the reference kernel has no other branch)")
+
+
+def _relu_triton(x, relu, relu6):
+    """-> (y, int8 mask), both shaped like x (kernel_registration.py:22-39)."""
+    if x.dtype not in _DTYPE_CODE:
+        raise RuntimeError(f"relu_triton: unsupported dtype {x.dtype}")
+    _require_cuda(x)
+    x = _aligned(x)
+    y = torch.empty_like(x)
+    mask = torch.empty(x.shape, dtype=torch.int8, device=x.device)
+    rc = _lib.lib().dopt_act_forward(x.data_ptr(), _DTYPE_CODE[x.dtype], x.numel(), _relu_act(relu, relu6),
+                                     y.data_ptr(), mask.data_ptr(), _stream(x))
+    _lib.check(rc, "relu_triton")
+    return y, mask
+
+
+relu_triton = _op("relu_triton(Tensor x, bool relu, bool relu6) -> (Tensor, Tensor)", _relu_triton,
+                  lambda x, relu, relu6: (torch.empty_like(x), torch.empty_like(x, dtype=torch.int8)))
+
+
+def _flat_groups(x: Tensor, group_size: int):
+    N = x.shape[0]
+    if x.numel() % (N * group_size):
+        raise RuntimeError(f"x of shape {tuple(x.shape)} does not split into [N, G, {group_size}] groups")
+    return N, x.numel() // N // group_size
+
+
+def _relu_fwd_fused_pack(x, relu, relu6, bits, group_size):
+    """-> (y shaped like x, packed mask codes [N*G, W], N, G) (kernel_registration.py:42-72)."""
+    _, nwords, _ = _bits_consts(bits, group_size)
+    if x.dtype not in (torch.bfloat16, torch.float32):
+        raise RuntimeError(f"relu_fwd_fused_pack: input must be bfloat16 or float32, got {x.dtype}")
+    _require_cuda(x)
+    N, G = _flat_groups(x, group_size)
+    x = _aligned(x)
+    y = torch.empty_like(x)
+    packed = torch.empty((N * G, nwords), dtype=torch.int32, device=x.device)
+    rc = _lib.lib().dopt_relu_pack(x.data_ptr(), _DTYPE_CODE[x.dtype], x.numel(),
+                                   int(_relu_act(relu, relu6) == ACT_RELU6), bits, y.data_ptr(), packed.data_ptr(),
+                                   _stream(x))
+    _lib.check(rc, "relu_fwd_fused_pack")
+    return y, packed, N, G
+
+
+def _relu_fwd_fused_pack_fake(x, relu, relu6, bits, group_size):
+    N, G = _flat_groups(x, group_size)
+    return torch.empty_like(x), x.new_empty((N * G, _bits_consts(bits, group_size)[1]), dtype=torch.int32), N, G
+
+
+relu_fwd_fused_pack = _op(
+    "relu_fwd_fused_pack(Tensor x, bool relu, bool relu6, int bits, int group_size) -> (Tensor, Tensor, int, int)",
+    _relu_fwd_fused_pack, _relu_fwd_fused_pack_fake)
+
+
+def _relu_bwd_fused_unpack(packed, dy, bits, N, G, group_size):
+    """-> bf16 dx = dy * mask, shaped like dy (kernel_registration.py:74-94)."""
+    _bits_consts(bits, group_size)
+    if dy.dtype not in _DTYPE_CODE:
+        raise RuntimeError(f"relu_bwd_fused_unpack: unsupported dy dtype {dy.dtype}")
+    if dy.numel() != N * G * group_size:
+        raise RuntimeError(f"relu_bwd_fused_unpack: dy has {dy.numel()} elements, expected {N * G * group_size}")
+    _require_cuda(packed, dy)
+    packed = _aligned(packed)
+    dy = _aligned(dy)
+    dx = torch.empty(dy.shape, dtype=torch.bfloat16, device=dy.device)
+    rc = _lib.lib().dopt_relu_unpack(packed.data_ptr(), dy.data_ptr(), _DTYPE_CODE[dy.dtype], dy.numel(), bits,
+                                     dx.data_ptr(), _stream(dy))
+    _lib.check(rc, "relu_bwd_fused_unpack")
+    return dx
+
+
+relu_bwd_fused_unpack = _op(
+    "relu_bwd_fused_unpack(Tensor packed, Tensor dy, int bits, int N, int G, int group_size) -> Tensor",
+    _relu_bwd_fused_unpack,
+    lambda packed, dy, bits, N, G, group_size: torch.empty_like(dy, dtype=torch.bfloat16))
+
+
+def _act_forward(x, act):
+    if x.dtype not in _DTYPE_CODE:
+        raise RuntimeError(f"unsupported input dtype {x.dtype}")
+    _require_cuda(x)
+    x = _aligned(x)
+    y = torch.empty(x.shape, dtype=torch.bfloat16, device=x.device)
+    d = torch.empty(x.shape, dtype=torch.bfloat16, device=x.device)
+    rc = _lib.lib().dopt_act_forward(x.data_ptr(), _DTYPE_CODE[x.dtype], x.numel(), act, y.data_ptr(), d.data_ptr(),
+                                     _stream(x))
+    _lib.check(rc, "act_forward")
+    return y, d
+
+
+def _bf16_pair(x):
+    return torch.empty_like(x, dtype=torch.bfloat16), torch.empty_like(x, dtype=torch.bfloat16)
+
+
+silu_triton = _op("silu_triton(Tensor x) -> (Tensor, Tensor)", lambda x: _act_forward(x, ACT_SILU), _bf16_pair)
+gelu_triton = _op("gelu_triton(Tensor x) -> (Tensor, Tensor)", lambda x: _act_forward(x, ACT_GELU), _bf16_pair)
+
+
+def _act_quant_pack_launch(x, act, n_groups, bits, group_size, tile):
+    _, nwords, _ = _bits_consts(bits, group_size)
+    if x.dtype not in (torch.bfloat16, torch.float32):
+        raise RuntimeError(f"fused activation quant-pack: input must be bfloat16 or float32, got {x.dtype}")
+    _require_cuda(x)
+    x = _aligned(x)
+    y = torch.empty(x.shape, dtype=torch.bfloat16, device=x.device)
+    packed = torch.empty((n_groups, nwords), dtype=torch.int32, device=x.device)
+    scale = torch.zeros((n_groups,), dtype=torch.bfloat16, device=x.device)
+    xmin = torch.zeros((n_groups,), dtype=torch.bfloat16, device=x.device)
+    tile_arr = None
+    if tile is not None:
+        import ctypes
+        tile_arr = (ctypes.c_int64 * 4)(*tile)
+    rc = _lib.lib().dopt_act_quant_pack(x.data_ptr(), _DTYPE_CODE[x.dtype], act, n_groups, group_size, bits, tile_arr,
+                                        y.data_ptr(), packed.data_ptr(), scale.data_ptr(), xmin.data_ptr(), _lib.BF16,
+                                        _stream(x))
+    _lib.check(rc, "act_quant_pack")
+    return y, packed, scale, xmin
+
+
+def _act_dequant_mul_launch(packed, dy, scale, xmin, n_groups, bits, group_size, tile):
+    _bits_consts(bits, group_size)
+    if dy.dtype not in (torch.bfloat16, torch.float32):
+        raise RuntimeError(f"fused activation backward: dy must be bfloat16 or float32, got {dy.dtype}")
+    if scale.dtype not in _META_CODE or xmin.dtype != scale.dtype:
+        raise RuntimeError("fused activation backward: scale and min must both be float32 or both bfloat16")
+    if dy.numel() != n_groups * group_size:
+        raise RuntimeError(f"fused activation backward: dy has {dy.numel()} elements, expected {n_groups * group_size}")
+    _require_cuda(packed, dy, scale, xmin)
+    packed = _aligned(packed)
+    dy = _aligned(dy)
+    dx = torch.empty(dy.shape, dtype=torch.bfloat16, device=dy.device)
+    tile_arr = None
+    if tile is not None:
+        import ctypes
+        tile_arr = (ctypes.c_int64 * 4)(*tile)
+    rc = _lib.lib().dopt_act_dequant_mul(packed.data_ptr(), scale.contiguous().data_ptr(), xmin.contiguous().data_ptr(),
+                                         _META_CODE[scale.dtype], n_groups, group_size, bits, tile_arr, dy.data_ptr(),
+                                         _DTYPE_CODE[dy.dtype], dx.data_ptr(), _stream(dy))
+    _lib.check(rc, "act_dequant_mul")
+    return dx
+
+
+def _gelu_fwd_fused_quan_pack(x, bits, group_size):
+    """-> (bf16 y shaped like x, packed [N*G, W], bf16 scale [N*G], bf16 min [N*G], N, G); flat
+    [N, -1, g] grouping (kernel_registration.py:261-292)."""
+    N, G = _flat_groups(x, group_size)
+    y, packed, scale, xmin = _act_quant_pack_launch(x, ACT_GELU, N * G, bits, group_size, None)
+    return y, packed, scale, xmin, N, G
+
+
+def _gelu_fwd_fused_quan_pack_fake(x, bits, group_size):
+    N, G = _flat_groups(x, group_size)
+    nw = _bits_consts(bits, group_size)[1]
+    return (torch.empty_like(x, dtype=torch.bfloat16), x.new_empty((N * G, nw), dtype=torch.int32),
+            x.new_empty((N * G,), dtype=torch.bfloat16), x.new_empty((N * G,), dtype=torch.bfloat16), N, G)
+
+
+gelu_fwd_fused_quan_pack = _op(
+    "gelu_fwd_fused_quan_pack(Tensor x, int bits, int group_size) -> (Tensor, Tensor, Tensor, Tensor, int, int)",
+    _gelu_fwd_fused_quan_pack, _gelu_fwd_fused_quan_pack_fake)
+
+
+def _gelu_bwd_fused_dequan_unpack(packed, dy, scale, min, bits, N, G, group_size):
+    """-> bf16 dx = dy * dequant(packed), shaped like dy (kernel_registration.py:295-319)."""
+    return _act_dequant_mul_launch(packed, dy, scale, min, N * G, bits, group_size, None)
+
+
+gelu_bwd_fused_dequan_unpack = _op(
+    "gelu_bwd_fused_dequan_unpack(Tensor packed, Tensor dy, Tensor scale, Tensor min, int bits, int N, int G, "
+    "int group_size) -> Tensor",
+    _gelu_bwd_fused_dequan_unpack,
+    lambda packed, dy, scale, min, bits, N, G, group_size: torch.empty_like(dy, dtype=torch.bfloat16))
+
+
+def _silu_layout(x, group_size):
+    """(N, G, new_H, new_W, pad_elig, reshape_elig, tile) of the reference's spatial-aware grouping
+    (tensor_act_reshape_utils.py:100-128), without materialising it."""
+    from .modules.tensor_act_reshape_utils import tile_layout_applies
+
+    if tile_layout_applies(x, group_size, False):
+        n, c, h, w = (int(v) for v in x.shape)
+        s = int(round(group_size ** 0.5))
+        return n, c * (h // s) * (w // s), h // s, w // s, False, True, (n, c, h, w)
+    N, G = _flat_groups(x, group_size)
+    return N, G, 0, 0, False, False, None
+
+
+def _silu_fwd_quan_pack(x, bits, group_size, avg_alam, alam_bits, pack_only):
+    """-> (bf16 y shaped like x, packed, bf16 scale [N*G], bf16 min [N*G], N, G, new_H, new_W,
+    padding eligibility, reshape eligibility) (kernel_registration.py:148-198); the spatial-tile
+    grouping is read and written in place."""
+    _no_alam(avg_alam, "silu_fwd_quan_pack")
+    N, G, nh, nw, pad_e, rs_e, tile = _silu_layout(x, group_size)
+    y, packed, scale, xmin = _act_quant_pack_launch(x, ACT_SILU, N * G, bits, group_size, tile)
+    return y, packed, scale, xmin, N, G, nh, nw, pad_e, rs_e
+
+
+def _silu_fwd_quan_pack_fake(x, bits, group_size, avg_alam, alam_bits, pack_only):
+    N, G, nh, nw, pad_e, rs_e, _ = _silu_layout(x, group_size)
+    nwords = _bits_consts(bits, group_size)[1]
+    return (torch.empty_like(x, dtype=torch.bfloat16), x.new_empty((N * G, nwords), dtype=torch.int32),
+            x.new_empty((N * G,), dtype=torch.bfloat16), x.new_empty((N * G,), dtype=torch.bfloat16), N, G, nh, nw,
+            pad_e, rs_e)
+
+
+silu_fwd_quan_pack = _op(
+    "silu_fwd_quan_pack(Tensor x, int bits, int group_size, bool avg_alam, int alam_bits, bool pack_only) -> "
+    "(Tensor, Tensor, Tensor, Tensor, int, int, int, int, bool, bool)",
+    _silu_fwd_quan_pack, _silu_fwd_quan_pack_fake)
+
+
+def _silu_bwd_fused_dequan_unpack(packed, dy, scale, min, bits, N, G, group_size, pack_only, new_H, new_W,
+                                  spatical_padding_eligibility, spatical_reshape_eligibility, avg_alam, alam_bits):
+    """-> bf16 dx = dy * dequant(packed), shaped like dy (kernel_registration.py:202-237)."""
+    _no_alam(avg_alam, "silu_bwd_fused_dequan_unpack")
+    tile = tuple(int(v) for v in dy.shape) if spatical_reshape_eligibility else None
+    return _act_dequant_mul_launch(packed, dy, scale, min, N * G, bits, group_size, tile)
+
+
+silu_bwd_fused_dequan_unpack = _op(
+    "silu_bwd_fused_dequan_unpack(Tensor packed, Tensor dy, Tensor scale, Tensor min, int bits, int N, int G, "
+    "int group_size, bool pack_only, int new_H, int new_W, bool spatical_padding_eligibility, "
+    "bool spatical_reshape_eligibility, bool avg_alam, int alam_bits) -> Tensor",
+    _silu_bwd_fused_dequan_unpack,
+    lambda packed, dy, scale, min, bits, N, G, group_size, pack_only, new_H, new_W, pe, re, aa, ab:
+        torch.empty_like(dy, dtype=torch.bfloat16))

@@ -24,6 +24,7 @@ SOURCES = [
     "dequant_unpack.hip",
     "pack_codes.hip",
     "fp8_gemm.hip",
+    "act_fused.hip",
 ]
 
 ARCH = "gfx950"

@@ -15,7 +15,14 @@
 
 namespace dopt {
 
+// DYT (template parameter of dequant_unpack_kernel): DY_NONE writes the dequantized values; DT_BF16
+// / DT_F32 multiply them by an incoming gradient dy of that type (same layout as the output) and
+// write dx = dy * dequant(q), the backward of the fused GELU / SiLU layers
+// (AC/modules/activations/kernel_implementation.py:392-395, :620-640).
+enum { DY_NONE = -1 };
+
 struct DequantArgs {
+    const void* dy;
     const uint32_t* packed;
     const void* scale;
     const void* minv;
@@ -58,7 +65,7 @@ __device__ __forceinline__ uint64_t dq_elem_index(const DequantArgs& a, uint32_t
            (uint64_t)(e0 >> a.log2s) * a.row + (e0 & smask);
 }
 
-template <int YT, int BITS, int G, int UB, int LPG_, int P, bool NT>
+template <int YT, int BITS, int G, int UB, int LPG_, int P, bool NT, int DYT>
 __global__ __launch_bounds__(256) void dequant_unpack_kernel(DequantArgs a) {
     using C = DequantCfg<YT, BITS, G, UB, LPG_, P, NT>;
     constexpr int UE = C::UE, STORES = C::STORES, CPL = C::CPL, LPG = C::LPG, GPP = C::GPP, W = C::W;
@@ -139,6 +146,22 @@ __global__ __launch_bounds__(256) void dequant_unpack_kernel(DequantArgs a) {
                 const uint32_t q = (cw[p][i][(k * BITS) / 32] >> ((k * BITS) % 32)) & QMAX;
                 out[k] = __builtin_fmaf((float)q, sc, mn);
             }
+            if constexpr (DYT != DY_NONE) {
+                constexpr int DB = DType<DYT>::bytes;
+                constexpr int DE = DType<DYT>::per16;
+                float g[UE];
+                if (ok) {
+#pragma unroll
+                    for (int l = 0; l < UE / DE; ++l)
+                        widen16<DYT>(ld16<false>((const char*)a.dy + dq_elem_index<G>(a, r, c * UE + l * DE) * DB),
+                                     &g[l * DE]);
+                } else {
+#pragma unroll
+                    for (int k = 0; k < UE; ++k) g[k] = 0.0f;
+                }
+#pragma unroll
+                for (int k = 0; k < UE; ++k) out[k] = g[k] * out[k];
+            }
 #pragma unroll
             for (int l = 0; l < STORES; ++l) {
                 const float* o = &out[l * E16];
@@ -157,6 +180,6 @@ __global__ __launch_bounds__(256) void dequant_unpack_kernel(DequantArgs a) {
 }
 
 template <int YT>
-int launch_dequant_unpack_dt(const DequantArgs& a, int bits, int g, hipStream_t s);
+int launch_dequant_unpack_dt(const DequantArgs& a, int bits, int g, int dyt, hipStream_t s);
 
 }  // namespace dopt

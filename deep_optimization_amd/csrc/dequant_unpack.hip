@@ -17,42 +17,52 @@ struct DequantShape {
     static constexpr int P = CPL >= 4 ? 1 : 4 / CPL;
 };
 
-template <int YT, int BITS, int G>
+template <int YT, int BITS, int G, int DYT>
 static int dq_launch(const DequantArgs& a, hipStream_t s) {
     using S = DequantShape<YT, G>;
-    using C = DequantCfg<YT, BITS, G, S::UB, S::LPG, S::P, true>;
+    using C = DequantCfg<YT, BITS, G, S::UB, S::LPG, S::P, true>;  // shape of every DYT variant
     const uint64_t waves = ((uint64_t)a.n_groups + C::GPW - 1) / C::GPW;
     const uint64_t blocks = (waves + C::WAVES - 1) / C::WAVES;
     if (blocks == 0) return 0;
-    hipLaunchKernelGGL((dequant_unpack_kernel<YT, BITS, G, S::UB, S::LPG, S::P, true>), dim3((uint32_t)blocks),
+    hipLaunchKernelGGL((dequant_unpack_kernel<YT, BITS, G, S::UB, S::LPG, S::P, true, DYT>), dim3((uint32_t)blocks),
                        dim3(64 * C::WAVES), 0, s, a);
     return 0;
 }
 
+template <int YT, int BITS, int G>
+static int dq_dy(const DequantArgs& a, int dyt, hipStream_t s) {
+    if (dyt == DY_NONE) return dq_launch<YT, BITS, G, DY_NONE>(a, s);
+    if constexpr (YT == DT_BF16) {  // the fused activation backward writes bf16 dx
+        if (dyt == DT_BF16) return dq_launch<YT, BITS, G, DT_BF16>(a, s);
+        if (dyt == DT_F32) return dq_launch<YT, BITS, G, DT_F32>(a, s);
+    }
+    return -1;
+}
+
 template <int YT, int BITS>
-static int dq_g(const DequantArgs& a, int g, hipStream_t s) {
+static int dq_g(const DequantArgs& a, int g, int dyt, hipStream_t s) {
     switch (g) {
-        case 64: return dq_launch<YT, BITS, 64>(a, s);
-        case 128: return dq_launch<YT, BITS, 128>(a, s);
-        case 256: return dq_launch<YT, BITS, 256>(a, s);
-        case 512: return dq_launch<YT, BITS, 512>(a, s);
-        case 1024: return dq_launch<YT, BITS, 1024>(a, s);
+        case 64: return dq_dy<YT, BITS, 64>(a, dyt, s);
+        case 128: return dq_dy<YT, BITS, 128>(a, dyt, s);
+        case 256: return dq_dy<YT, BITS, 256>(a, dyt, s);
+        case 512: return dq_dy<YT, BITS, 512>(a, dyt, s);
+        case 1024: return dq_dy<YT, BITS, 1024>(a, dyt, s);
     }
     return -1;
 }
 
 template <int YT>
-int launch_dequant_unpack_dt(const DequantArgs& a, int bits, int g, hipStream_t s) {
+int launch_dequant_unpack_dt(const DequantArgs& a, int bits, int g, int dyt, hipStream_t s) {
     switch (bits) {
-        case 1: return dq_g<YT, 1>(a, g, s);
-        case 2: return dq_g<YT, 2>(a, g, s);
-        case 4: return dq_g<YT, 4>(a, g, s);
-        case 8: return dq_g<YT, 8>(a, g, s);
+        case 1: return dq_g<YT, 1>(a, g, dyt, s);
+        case 2: return dq_g<YT, 2>(a, g, dyt, s);
+        case 4: return dq_g<YT, 4>(a, g, dyt, s);
+        case 8: return dq_g<YT, 8>(a, g, dyt, s);
     }
     return -1;
 }
 
-template int launch_dequant_unpack_dt<DT_F32>(const DequantArgs&, int, int, hipStream_t);
-template int launch_dequant_unpack_dt<DT_BF16>(const DequantArgs&, int, int, hipStream_t);
+template int launch_dequant_unpack_dt<DT_F32>(const DequantArgs&, int, int, int, hipStream_t);
+template int launch_dequant_unpack_dt<DT_BF16>(const DequantArgs&, int, int, int, hipStream_t);
 
 }  // namespace dopt

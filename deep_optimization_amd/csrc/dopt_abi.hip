@@ -13,6 +13,9 @@ int launch_pack_codes(const int8_t* codes, uint32_t* out, uint64_t n_words, int 
 int launch_unpack_codes(const uint32_t* packed, int8_t* codes, uint64_t n_words, int bits, hipStream_t s);
 int launch_fp8_gemm_nt(const uint8_t* A, const uint8_t* B, int64_t M, int64_t N, int64_t K, int64_t lda,
                        int64_t ldb, float out_scale, uint16_t* C, int64_t ldc, hipStream_t s);
+int launch_relu_pack(const void* x, int dt, void* y, uint32_t* packed, uint64_t n, int bits, bool relu6, hipStream_t s);
+int launch_relu_unpack(const uint32_t* packed, const void* dy, int dyt, void* dx, uint64_t n, int bits, hipStream_t s);
+int launch_act_forward(const void* x, int dt, void* y, void* aux, uint64_t n, int act, hipStream_t s);
 }  // namespace dopt
 
 namespace {
@@ -133,9 +136,9 @@ int dopt_quant_pack(const void* x, int x_dtype, int64_t n_groups, int group_size
     hipStream_t s = (hipStream_t)stream;
     (void)hipGetLastError();
     switch (x_dtype) {
-        case DOPT_F32: rc = dopt::launch_quant_pack_dt<dopt::DT_F32>(a, bits, group_size, rounding, flags != 0, s); break;
-        case DOPT_F16: rc = dopt::launch_quant_pack_dt<dopt::DT_F16>(a, bits, group_size, rounding, flags != 0, s); break;
-        default: rc = dopt::launch_quant_pack_dt<dopt::DT_BF16>(a, bits, group_size, rounding, flags != 0, s); break;
+        case DOPT_F32: rc = dopt::launch_quant_pack_dt<dopt::DT_F32>(a, bits, group_size, rounding, flags ? dopt::PRE_REF : dopt::PRE_NONE, s); break;
+        case DOPT_F16: rc = dopt::launch_quant_pack_dt<dopt::DT_F16>(a, bits, group_size, rounding, flags ? dopt::PRE_REF : dopt::PRE_NONE, s); break;
+        default: rc = dopt::launch_quant_pack_dt<dopt::DT_BF16>(a, bits, group_size, rounding, flags ? dopt::PRE_REF : dopt::PRE_NONE, s); break;
     }
     if (rc) return fail(DOPT_EUNSUPPORTED, "no quant-pack kernel for bits=%d g=%d rounding=%d", bits, group_size, rounding);
     return hip_status("quant_pack launch");
@@ -167,9 +170,9 @@ int dopt_dequant_unpack(const uint32_t* packed, const void* scale, const void* m
     hipStream_t s = (hipStream_t)stream;
     (void)hipGetLastError();
     if (y_dtype == DOPT_F32)
-        rc = dopt::launch_dequant_unpack_dt<dopt::DT_F32>(a, bits, group_size, s);
+        rc = dopt::launch_dequant_unpack_dt<dopt::DT_F32>(a, bits, group_size, dopt::DY_NONE, s);
     else
-        rc = dopt::launch_dequant_unpack_dt<dopt::DT_BF16>(a, bits, group_size, s);
+        rc = dopt::launch_dequant_unpack_dt<dopt::DT_BF16>(a, bits, group_size, dopt::DY_NONE, s);
     if (rc) return fail(DOPT_EUNSUPPORTED, "no dequant kernel for bits=%d g=%d", bits, group_size);
     return hip_status("dequant_unpack launch");
 }
@@ -218,6 +221,121 @@ int dopt_fp8_gemm_nt(const uint8_t* A, const uint8_t* B, int64_t M, int64_t N, i
     const int rc = dopt::launch_fp8_gemm_nt(A, B, M, N, K, lda, ldb, out_scale, (uint16_t*)C, ldc, (hipStream_t)stream);
     if (rc) return fail(DOPT_EUNSUPPORTED, "fp8 GEMM launch configuration unsupported");
     return hip_status("fp8_gemm launch");
+}
+
+int dopt_relu_pack(const void* x, int x_dtype, int64_t n, int relu6, int bits, void* y, uint32_t* packed, void* stream) {
+    int rc;
+    if ((rc = check_bits(bits))) return rc;
+    if (x_dtype != DOPT_F32 && x_dtype != DOPT_BF16)
+        return fail(DOPT_EINVAL, "relu_pack: input dtype must be F32 or BF16, got code %d", x_dtype);
+    if (n < 0 || n % 64) return fail(DOPT_EINVAL, "relu_pack: n must be a non-negative multiple of 64, got %lld", (long long)n);
+    if (n == 0) return ok();
+    if (!x || !y || !packed) return fail(DOPT_EINVAL, "null pointer argument");
+    if (!aligned16(x) || !aligned16(y) || !aligned16(packed)) return fail(DOPT_EINVAL, "x, y and packed must be 16-byte aligned");
+    (void)hipGetLastError();
+    if (dopt::launch_relu_pack(x, x_dtype, y, packed, (uint64_t)n, bits, relu6 != 0, (hipStream_t)stream))
+        return fail(DOPT_EUNSUPPORTED, "no relu_pack kernel for dtype %d bits %d", x_dtype, bits);
+    return hip_status("relu_pack launch");
+}
+
+int dopt_relu_unpack(const uint32_t* packed, const void* dy, int dy_dtype, int64_t n, int bits, void* dx, void* stream) {
+    int rc;
+    if ((rc = check_bits(bits))) return rc;
+    if (dy_dtype != DOPT_F32 && dy_dtype != DOPT_F16 && dy_dtype != DOPT_BF16)
+        return fail(DOPT_EINVAL, "relu_unpack: unsupported dy dtype code %d", dy_dtype);
+    if (n < 0 || n % 64) return fail(DOPT_EINVAL, "relu_unpack: n must be a non-negative multiple of 64, got %lld", (long long)n);
+    if (n == 0) return ok();
+    if (!packed || !dy || !dx) return fail(DOPT_EINVAL, "null pointer argument");
+    if (!aligned16(dy) || !aligned16(dx) || ((uintptr_t)packed & 7u))
+        return fail(DOPT_EINVAL, "dy and dx must be 16-byte and packed 8-byte aligned");
+    (void)hipGetLastError();
+    if (dopt::launch_relu_unpack(packed, dy, dy_dtype, dx, (uint64_t)n, bits, (hipStream_t)stream))
+        return fail(DOPT_EUNSUPPORTED, "no relu_unpack kernel for dtype %d bits %d", dy_dtype, bits);
+    return hip_status("relu_unpack launch");
+}
+
+int dopt_act_forward(const void* x, int x_dtype, int64_t n, int act, void* y, void* aux, void* stream) {
+    if (x_dtype != DOPT_F32 && x_dtype != DOPT_F16 && x_dtype != DOPT_BF16)
+        return fail(DOPT_EINVAL, "act_forward: unsupported input dtype code %d", x_dtype);
+    if (act < DOPT_ACT_RELU || act > DOPT_ACT_SILU) return fail(DOPT_EINVAL, "act_forward: unknown activation %d", act);
+    if (n < 0) return fail(DOPT_EINVAL, "act_forward: negative n");
+    if (n == 0) return ok();
+    if (!x || !y || !aux) return fail(DOPT_EINVAL, "null pointer argument");
+    if (!aligned16(x) || !aligned16(y) || !aligned16(aux)) return fail(DOPT_EINVAL, "x, y and aux must be 16-byte aligned");
+    (void)hipGetLastError();
+    if (dopt::launch_act_forward(x, x_dtype, y, aux, (uint64_t)n, act, (hipStream_t)stream))
+        return fail(DOPT_EUNSUPPORTED, "no act_forward kernel for dtype %d act %d", x_dtype, act);
+    return hip_status("act_forward launch");
+}
+
+int dopt_act_quant_pack(const void* x, int x_dtype, int act, int64_t n_groups, int group_size, int bits,
+                        const int64_t* tile_nchw, void* y, uint32_t* packed, void* scale, void* minv, int meta_dtype,
+                        void* stream) {
+    int rc;
+    if ((rc = check_bits(bits))) return rc;
+    if ((rc = check_group(group_size))) return rc;
+    if (n_groups < 0 || n_groups >= (int64_t)1 << 31)
+        return fail(DOPT_EINVAL, "n_groups must be in [0, 2^31), got %lld", (long long)n_groups);
+    if (x_dtype != DOPT_F32 && x_dtype != DOPT_BF16)
+        return fail(DOPT_EINVAL, "act_quant_pack: input dtype must be F32 or BF16, got code %d", x_dtype);
+    if (act != DOPT_ACT_GELU && act != DOPT_ACT_SILU)
+        return fail(DOPT_EINVAL, "act_quant_pack: activation must be GELU or SILU, got %d", act);
+    if (meta_dtype != DOPT_F32 && meta_dtype != DOPT_BF16)
+        return fail(DOPT_EINVAL, "scale/min dtype must be F32 or BF16, got code %d", meta_dtype);
+    dopt::QuantPackArgs a{};
+    if ((rc = setup_tiles(tile_nchw, n_groups, group_size, &a.tiled, &a.tiles_w, &a.log2s, &a.row))) return rc;
+    if (n_groups == 0) return ok();
+    if (!x || !y || !packed || !scale || !minv) return fail(DOPT_EINVAL, "null pointer argument");
+    if (!aligned16(x) || !aligned16(y) || !aligned16(packed)) return fail(DOPT_EINVAL, "x, y and packed must be 16-byte aligned");
+    a.x = x;
+    a.y = y;
+    a.packed = packed;
+    a.scale = scale;
+    a.minv = minv;
+    a.n_groups = (uint32_t)n_groups;
+    a.meta_bf16 = meta_dtype == DOPT_BF16;
+    const int pre = act == DOPT_ACT_GELU ? dopt::PRE_GELU : dopt::PRE_SILU;
+    hipStream_t s = (hipStream_t)stream;
+    (void)hipGetLastError();
+    if (x_dtype == DOPT_F32)
+        rc = dopt::launch_quant_pack_dt<dopt::DT_F32>(a, bits, group_size, dopt::RN_NEAREST, pre, s);
+    else
+        rc = dopt::launch_quant_pack_dt<dopt::DT_BF16>(a, bits, group_size, dopt::RN_NEAREST, pre, s);
+    if (rc) return fail(DOPT_EUNSUPPORTED, "no act_quant_pack kernel for bits=%d g=%d act=%d", bits, group_size, act);
+    return hip_status("act_quant_pack launch");
+}
+
+int dopt_act_dequant_mul(const uint32_t* packed, const void* scale, const void* minv, int meta_dtype, int64_t n_groups,
+                         int group_size, int bits, const int64_t* tile_nchw, const void* dy, int dy_dtype, void* dx,
+                         void* stream) {
+    int rc;
+    if ((rc = check_bits(bits))) return rc;
+    if ((rc = check_group(group_size))) return rc;
+    if (n_groups < 0 || n_groups >= (int64_t)1 << 31)
+        return fail(DOPT_EINVAL, "n_groups must be in [0, 2^31), got %lld", (long long)n_groups);
+    if (meta_dtype != DOPT_F32 && meta_dtype != DOPT_BF16)
+        return fail(DOPT_EINVAL, "scale/min dtype must be F32 or BF16, got code %d", meta_dtype);
+    if (dy_dtype != DOPT_F32 && dy_dtype != DOPT_BF16)
+        return fail(DOPT_EINVAL, "act_dequant_mul: dy dtype must be F32 or BF16, got code %d", dy_dtype);
+    dopt::DequantArgs a{};
+    if ((rc = setup_tiles(tile_nchw, n_groups, group_size, &a.tiled, &a.tiles_w, &a.log2s, &a.row))) return rc;
+    if (n_groups == 0) return ok();
+    if (!packed || !scale || !minv || !dy || !dx) return fail(DOPT_EINVAL, "null pointer argument");
+    if (!aligned16(dx) || !aligned16(dy) || ((uintptr_t)packed & 7u))
+        return fail(DOPT_EINVAL, "dx and dy must be 16-byte and packed 8-byte aligned");
+    a.dy = dy;
+    a.packed = packed;
+    a.scale = scale;
+    a.minv = minv;
+    a.y = dx;
+    a.n_groups = (uint32_t)n_groups;
+    a.meta_bf16 = meta_dtype == DOPT_BF16;
+    (void)hipGetLastError();
+    rc = dopt::launch_dequant_unpack_dt<dopt::DT_BF16>(a, bits, group_size,
+                                                       dy_dtype == DOPT_F32 ? dopt::DT_F32 : dopt::DT_BF16,
+                                                       (hipStream_t)stream);
+    if (rc) return fail(DOPT_EUNSUPPORTED, "no act_dequant_mul kernel for bits=%d g=%d", bits, group_size);
+    return hip_status("act_dequant_mul launch");
 }
 
 }  // extern "C"

@@ -123,6 +123,39 @@ __device__ __forceinline__ uint16_t to_bf16(float v) { return (uint16_t)(pack_bf
 
 __device__ __forceinline__ float bf16_bits_to_f32(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
 
+// ------------------------------------------------------------------ activation math
+// Fast fp32 transcendentals for the fused activation kernels (v_exp_f32 / v_rcp_f32 based; the
+// reference's own are Triton's exp and libdevice tanh, so these are tolerance-level anyway).
+// tanh(u) = sign(u) * (1 - e) / (1 + e), e = 2^(-2|u| log2 e): absolute error ~2e-7, exact 0 at 0.
+__device__ __forceinline__ float fast_tanh(float u) {
+    const float e = __builtin_amdgcn_exp2f(-2.8853900817779268f * fabsf(u));  // -2 log2(e) |u|
+    const float r = (1.0f - e) * __builtin_amdgcn_rcpf(1.0f + e);
+    return copysignf(r, u);
+}
+__device__ __forceinline__ float fast_sigmoid(float x) {
+    return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-1.4426950408889634f * x));
+}
+// GELU (tanh form) value and derivative of act_triton kernels
+// (AC/modules/activations/kernel_implementation.py:496-519): u = a (x + b x^3), t = tanh(u),
+// y = x (1 + t) / 2, dy/dx = (1 + t)/2 + x (1 - t^2) a (1 + 3 b x^2) / 2. Evaluated through
+// s = (1 + t)/2 = sigmoid(2u) and 1 - t^2 = 4 s (1 - s), the same function without the
+// cancellation of 1 + t for x below about -4 (where an fp32 tanh is already -1).
+__device__ __forceinline__ void gelu_and_grad(float x, float& y, float& d) {
+    const float a = 0.7978845608028654f, b = 0.044715f, b3 = 0.134145f;
+    const float x2 = x * x;
+    const float u = a * __builtin_fmaf(b * x2, x, x);
+    const float s = fast_sigmoid(2.0f * u);
+    y = x * s;
+    d = __builtin_fmaf(2.0f * x * s * (1.0f - s), a * __builtin_fmaf(b3, x2, 1.0f), s);
+}
+// SiLU value and derivative (kernel_implementation.py:225-229): s = sigmoid(x), y = x s,
+// dy/dx = s + x s (1 - s)
+__device__ __forceinline__ void silu_and_grad(float x, float& y, float& d) {
+    const float s = fast_sigmoid(x);
+    y = x * s;
+    d = __builtin_fmaf(x * s, 1.0f - s, s);
+}
+
 // ------------------------------------------------------------------ Philox4x32-10
 // Salmon et al., SC'11: multipliers 0xD2511F53 / 0xCD9E8D57, Weyl key increments
 // 0x9E3779B9 / 0xBB67AE85, key bumped between rounds. Each round is two 32x32->64 multiplies

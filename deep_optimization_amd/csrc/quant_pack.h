@@ -35,8 +35,18 @@
 
 namespace dopt {
 
+// Pre-transform applied before min/max (template parameter PRE of quant_pack_kernel):
+//   PRE_NONE  codes of x itself
+//   PRE_REF   the reference quantizer's optional clamp(x, +-alpha) and tanh(x/0.5)*0.5 (runtime flags)
+//   PRE_GELU  fused GELU layer: y = gelu(x) is written as bf16, the codes are of
+//             tanh(clamp(gelu'(x), -3, 3)/0.5)*0.5 with the range floored at 1e-4
+//             (AC/modules/activations/kernel_implementation.py:496-535)
+//   PRE_SILU  the same for SiLU (kernel_implementation.py:225-243)
+enum { PRE_NONE = 0, PRE_REF = 1, PRE_GELU = 2, PRE_SILU = 3 };
+
 struct QuantPackArgs {
     const void* x;
+    void* y;  // activation output (PRE_GELU / PRE_SILU): bf16, same layout as x
     const float* noise;
     uint32_t* packed;
     void* scale;
@@ -152,7 +162,7 @@ __device__ __forceinline__ uint32_t cvt_u32(float f) {
 
 __device__ __forceinline__ bool wave_any(bool p) { return __builtin_amdgcn_ballot_w64(p) != 0; }
 
-template <int DT, int BITS, int G, int RN, int UB, int LPG_, int P, bool PRE, bool NT>
+template <int DT, int BITS, int G, int RN, int UB, int LPG_, int P, int PRE, bool NT>
 __global__ __launch_bounds__(256) void quant_pack_kernel(QuantPackArgs a) {
     using C = QuantPackCfg<DT, BITS, G, RN, UB, LPG_, P>;
     constexpr int UE = C::UE, LOADS = C::LOADS, CPL = C::CPL, LPG = C::LPG, GPP = C::GPP, W = C::W;
@@ -203,18 +213,47 @@ __global__ __launch_bounds__(256) void quant_pack_kernel(QuantPackArgs a) {
         for (int i = 0; i < CPL; ++i)
             #pragma unroll
             for (int l = 0; l < LOADS; ++l) widen16<DT>(raw[p][i][l], &v[i][l * E16]);
-        if constexpr (PRE) {
+        if constexpr (PRE == PRE_REF) {
             if (a.flags & FL_CLAMP) {
-                #pragma unroll
+#pragma unroll
                 for (int i = 0; i < CPL; ++i)
-                    #pragma unroll
+#pragma unroll
                     for (int k = 0; k < UE; ++k) v[i][k] = fminf(fmaxf(v[i][k], -a.clamp_alpha), a.clamp_alpha);
             }
             if (a.flags & FL_SQUASH) {
-                #pragma unroll
+#pragma unroll
                 for (int i = 0; i < CPL; ++i)
-                    #pragma unroll
+#pragma unroll
                     for (int k = 0; k < UE; ++k) v[i][k] = tanhf(v[i][k] / 0.5f) * 0.5f;
+            }
+        } else if constexpr (PRE == PRE_GELU || PRE == PRE_SILU) {
+            // activation value (stored bf16) and its squashed derivative (quantized)
+#pragma unroll
+            for (int i = 0; i < CPL; ++i) {
+                const uint32_t e0 = (uint32_t)(i * LPG + li) * UE;
+                float yv[UE];
+#pragma unroll
+                for (int k = 0; k < UE; ++k) {
+                    float d;
+                    if constexpr (PRE == PRE_GELU)
+                        gelu_and_grad(v[i][k], yv[k], d);
+                    else
+                        silu_and_grad(v[i][k], yv[k], d);
+                    d = fminf(fmaxf(d, -3.0f), 3.0f);
+                    v[i][k] = fast_tanh(d * 2.0f) * 0.5f;
+                }
+                if (r < a.n_groups) {
+#pragma unroll
+                    for (int l = 0; l < LOADS; ++l) {
+                        const float* o = &yv[l * E16];
+                        char* yb = (char*)a.y + group_elem_index<G>(a, r, e0 + l * E16) * 2;
+                        if constexpr (E16 == 8)
+                            *(uint4*)yb = make_uint4(pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3]),
+                                                     pack_bf16x2(o[4], o[5]), pack_bf16x2(o[6], o[7]));
+                        else
+                            *(uint2*)yb = make_uint2(pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3]));
+                    }
+                }
             }
         }
         // lane-local min/max with raw 3-operand min/max over the lane's CPL*UE values
@@ -245,7 +284,8 @@ __global__ __launch_bounds__(256) void quant_pack_kernel(QuantPackArgs a) {
         }
         group_minmax<LPG>(mn, mx);
         mn = mn + 0.0f;  // store -0.0 as +0.0
-        const float rng = mx - mn;
+        float rng = mx - mn;
+        if constexpr (PRE == PRE_GELU || PRE == PRE_SILU) rng = fmaxf(rng, 1e-4f);  // kernel_implementation.py:236, :529
         const float step = rng > 0.0f ? rng / qmaxf : 1.0f;
         const float inv = 1.0f / step;
         step_p[p] = step;
@@ -362,6 +402,6 @@ __global__ __launch_bounds__(256) void quant_pack_kernel(QuantPackArgs a) {
 
 // host-side launcher; explicitly instantiated per element type in quant_pack_<dtype>.hip
 template <int DT>
-int launch_quant_pack_dt(const QuantPackArgs& a, int bits, int g, int rn, bool pre, hipStream_t s);
+int launch_quant_pack_dt(const QuantPackArgs& a, int bits, int g, int rn, int pre, hipStream_t s);
 
 }  // namespace dopt

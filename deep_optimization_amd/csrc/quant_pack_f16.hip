@@ -2,5 +2,5 @@
 #include "quant_pack_launch.h"
 
 namespace dopt {
-template int launch_quant_pack_dt<DT_F16>(const QuantPackArgs&, int, int, int, bool, hipStream_t);
+template int launch_quant_pack_dt<DT_F16>(const QuantPackArgs&, int, int, int, int, hipStream_t);
 }  // namespace dopt

@@ -13,7 +13,7 @@
 
 namespace dopt {
 
-template <int DT, int BITS, int G, int RN>
+template <int DT, int BITS, int G, int RN, int PRE>
 struct QuantPackShape {
     static constexpr int BYTES = DType<DT>::bytes;
     // unit bytes: Philox units hold NOISE_EPC elements where that is at most 64 bytes
@@ -22,16 +22,18 @@ struct QuantPackShape {
     static constexpr int CPG = G / UE;
     static constexpr int UBITS = UE * BITS;
     static constexpr int LPD = UBITS >= 32 ? 1 : 32 / UBITS;  // lanes merged per code dword
-    static constexpr int L0 = RN == RN_NOISE ? CPG : CPG / 2;   // noise mode: one unit per lane
+    // noise mode: one unit per lane; the VALU-heavy activation pre-transforms: four (more
+    // independent work per lane); otherwise two
+    static constexpr int L0 = RN == RN_NOISE ? CPG : (PRE == PRE_GELU || PRE == PRE_SILU) ? CPG / 4 : CPG / 2;
     static constexpr int L1 = L0 < LPD ? LPD : L0;
     static constexpr int L2 = L1 < 2 ? 2 : L1;
     static constexpr int LPG = L2 > 64 ? 64 : L2;
     static constexpr int P = 1;
 };
 
-template <int DT, int BITS, int G, int RN, bool PRE>
+template <int DT, int BITS, int G, int RN, int PRE>
 static int qp_launch(const QuantPackArgs& a, hipStream_t s) {
-    using S = QuantPackShape<DT, BITS, G, RN>;
+    using S = QuantPackShape<DT, BITS, G, RN, PRE>;
     using C = QuantPackCfg<DT, BITS, G, RN, S::UB, S::LPG, S::P>;
     const uint64_t waves = ((uint64_t)a.n_groups + C::GPW - 1) / C::GPW;
     const uint64_t blocks = (waves + C::WAVES - 1) / C::WAVES;
@@ -42,21 +44,30 @@ static int qp_launch(const QuantPackArgs& a, hipStream_t s) {
 }
 
 template <int DT, int BITS, int G>
-static int qp_rn(const QuantPackArgs& a, int rn, bool pre, hipStream_t s) {
-    if (pre) {  // the reference's clamp / tanh pre-transform runs with nearest rounding only
+static int qp_rn(const QuantPackArgs& a, int rn, int pre, hipStream_t s) {
+    if (pre != PRE_NONE) {  // the pre-transforms (reference quantizer, fused activations) round to nearest
         if (rn != RN_NEAREST) return -1;
-        return qp_launch<DT, BITS, G, RN_NEAREST, true>(a, s);
+        switch (pre) {
+            case PRE_REF: return qp_launch<DT, BITS, G, RN_NEAREST, PRE_REF>(a, s);
+            case PRE_GELU:
+                if constexpr (DT == DT_F16) return -1;
+                else return qp_launch<DT, BITS, G, RN_NEAREST, PRE_GELU>(a, s);
+            case PRE_SILU:
+                if constexpr (DT == DT_F16) return -1;
+                else return qp_launch<DT, BITS, G, RN_NEAREST, PRE_SILU>(a, s);
+        }
+        return -1;
     }
     switch (rn) {
-        case RN_NEAREST: return qp_launch<DT, BITS, G, RN_NEAREST, false>(a, s);
-        case RN_NOISE: return qp_launch<DT, BITS, G, RN_NOISE, false>(a, s);
-        case RN_PHILOX: return qp_launch<DT, BITS, G, RN_PHILOX, false>(a, s);
+        case RN_NEAREST: return qp_launch<DT, BITS, G, RN_NEAREST, PRE_NONE>(a, s);
+        case RN_NOISE: return qp_launch<DT, BITS, G, RN_NOISE, PRE_NONE>(a, s);
+        case RN_PHILOX: return qp_launch<DT, BITS, G, RN_PHILOX, PRE_NONE>(a, s);
     }
     return -1;
 }
 
 template <int DT, int BITS>
-static int qp_g(const QuantPackArgs& a, int g, int rn, bool pre, hipStream_t s) {
+static int qp_g(const QuantPackArgs& a, int g, int rn, int pre, hipStream_t s) {
     switch (g) {
         case 64: return qp_rn<DT, BITS, 64>(a, rn, pre, s);
         case 128: return qp_rn<DT, BITS, 128>(a, rn, pre, s);
@@ -68,7 +79,7 @@ static int qp_g(const QuantPackArgs& a, int g, int rn, bool pre, hipStream_t s) 
 }
 
 template <int DT>
-int launch_quant_pack_dt(const QuantPackArgs& a, int bits, int g, int rn, bool pre, hipStream_t s) {
+int launch_quant_pack_dt(const QuantPackArgs& a, int bits, int g, int rn, int pre, hipStream_t s) {
     switch (bits) {
         case 1: return qp_g<DT, 1>(a, g, rn, pre, s);
         case 2: return qp_g<DT, 2>(a, g, rn, pre, s);

@@ -131,6 +131,63 @@ int dopt_unpack_codes(const uint32_t* packed, int64_t n_groups, int group_size, 
 int dopt_fp8_gemm_nt(const uint8_t* A, const uint8_t* B, int64_t M, int64_t N, int64_t K,
                      int64_t lda, int64_t ldb, float out_scale, void* C, int64_t ldc, void* stream);
 
+/* ---------------------------------------------------------------- fused activation layers
+ * The compressed ReLU / GELU / SiLU layers of Activation_Compression/modules/activations/ save the
+ * layer's mask (ReLU) or its quantized derivative (GELU, SiLU) in the forward pass and apply it to
+ * the incoming gradient in the backward pass. */
+#define DOPT_ACT_RELU 0
+#define DOPT_ACT_RELU6 1 /* mask = 0 < x < 6 */
+#define DOPT_ACT_GELU 2  /* tanh form: x (1 + tanh(a (x + b x^3))) / 2, a = sqrt(2/pi), b = 0.044715 */
+#define DOPT_ACT_SILU 3  /* x sigmoid(x) */
+
+/*
+ * y = relu(x) (x where the mask holds, else 0; fp32 inputs come out rounded to bf16 as in the
+ * reference) and the mask packed as `bits`-bit codes (0 or 1) in the quantizer's bitstream.
+ * x, y: n elements of x_dtype (F32 or BF16); packed: n*bits/32 uint32; n % 64 == 0.
+ * Replaces act_lib::relu_fwd_fused_pack (modules/activations/kernel_registration.py:42-72,
+ * kernel modules/activations/kernel_implementation.py:34-90).
+ */
+int dopt_relu_pack(const void* x, int x_dtype, int64_t n, int relu6, int bits, void* y, uint32_t* packed,
+                   void* stream);
+
+/*
+ * dx = bf16(dy * mask), mask = lowest bit of each `bits`-bit code. dy: n elements of dy_dtype
+ * (F32, F16 or BF16); dx: n bf16; n % 64 == 0.
+ * Replaces act_lib::relu_bwd_fused_unpack (kernel_registration.py:74-94, kernel_implementation.py:93-143).
+ */
+int dopt_relu_unpack(const uint32_t* packed, const void* dy, int dy_dtype, int64_t n, int bits, void* dx,
+                     void* stream);
+
+/*
+ * Unfused activation forward over n elements (any n): RELU/RELU6 -> y in x's type and an int8
+ * mask in aux; GELU/SILU -> bf16 y and the bf16 derivative in aux.
+ * Replaces act_lib::relu_triton, silu_triton, gelu_triton (kernel_registration.py:22-39,
+ * :132-146, :245-259).
+ */
+int dopt_act_forward(const void* x, int x_dtype, int64_t n, int act, void* y, void* aux, void* stream);
+
+/*
+ * Fused GELU / SiLU forward: y = act(x) written as bf16, and per group the derivative
+ * d = tanh(clamp(act'(x), -3, 3) / 0.5) * 0.5 quantized like dopt_quant_pack with nearest rounding,
+ * the range floored at 1e-4 (kernel_implementation.py:225-243, :496-535). Layout arguments as in
+ * dopt_quant_pack (tile_nchw != NULL: x and y are [N, C, H, W] read/written through the tile map).
+ * x_dtype F32 or BF16; act DOPT_ACT_GELU or DOPT_ACT_SILU.
+ * Replaces act_lib::gelu_fwd_fused_quan_pack (kernel_registration.py:261-292) and
+ * act_lib::silu_fwd_quan_pack (:148-198).
+ */
+int dopt_act_quant_pack(const void* x, int x_dtype, int act, int64_t n_groups, int group_size, int bits,
+                        const int64_t* tile_nchw, void* y, uint32_t* packed, void* scale, void* minv, int meta_dtype,
+                        void* stream);
+
+/*
+ * Fused GELU / SiLU backward: dx = bf16(dy * fma(float(q), scale, min)) with dy (F32 or BF16) in
+ * the output's layout. Replaces act_lib::gelu_bwd_fused_dequan_unpack (kernel_registration.py:295-319)
+ * and act_lib::silu_bwd_fused_dequan_unpack (:202-237).
+ */
+int dopt_act_dequant_mul(const uint32_t* packed, const void* scale, const void* minv, int meta_dtype, int64_t n_groups,
+                         int group_size, int bits, const int64_t* tile_nchw, const void* dy, int dy_dtype, void* dx,
+                         void* stream);
+
 #ifdef __cplusplus
 }
 #endif

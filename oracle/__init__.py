@@ -26,6 +26,7 @@ _LIB_PATH = os.path.join(_HERE, "liboracle.so")
 F32, F16, BF16 = 0, 1, 2
 NEAREST, STOCH_NOISE, STOCH_PHILOX = 0, 1, 2
 FLAG_CLAMP, FLAG_SQUASH = 1, 2
+ACT_RELU, ACT_RELU6, ACT_GELU, ACT_SILU = 0, 1, 2, 3
 
 _lib = None
 
@@ -62,6 +63,16 @@ def lib():
         L.oracle_set_num_threads.argtypes = [i32]
         L.oracle_f32_to_bf16.argtypes = [ctypes.c_float]
         L.oracle_f32_to_bf16.restype = ctypes.c_uint16
+        L.oracle_relu_pack.argtypes = [vp, i32, i64, i32, i32, vp, vp]
+        L.oracle_relu_pack.restype = i32
+        L.oracle_relu_unpack.argtypes = [vp, vp, i32, i64, i32, vp]
+        L.oracle_relu_unpack.restype = i32
+        L.oracle_act_forward.argtypes = [vp, i32, i64, i32, vp, vp]
+        L.oracle_act_forward.restype = i32
+        L.oracle_act_quant_pack.argtypes = [vp, i32, i32, i64, i32, i32, vp, vp, vp, vp, vp, i32]
+        L.oracle_act_quant_pack.restype = i32
+        L.oracle_act_dequant_mul.argtypes = [vp, vp, vp, i32, i64, i32, i32, vp, vp, i32, vp]
+        L.oracle_act_dequant_mul.restype = i32
         _lib = L
     return _lib
 
@@ -165,6 +176,63 @@ def philox_noise(idx0: int, n: int, seed: int, offset: int) -> np.ndarray:
     out = np.zeros(n, dtype=np.float32)
     lib().oracle_philox_noise(idx0, n, seed, offset, _ptr(out))
     return out
+
+
+def relu_pack(x: np.ndarray, bits: int, relu6: bool = False):
+    """-> (y in x's storage type, packed uint32 mask codes); x float32 or uint16 (bf16 bits)."""
+    x = np.ascontiguousarray(x)
+    y = np.zeros_like(x)
+    packed = np.zeros(x.size * bits // 32, dtype=np.uint32)
+    _check(lib().oracle_relu_pack(_ptr(x), _dtype_code(x), x.size, int(relu6), bits, _ptr(y), _ptr(packed)))
+    return y, packed
+
+
+def relu_unpack(packed: np.ndarray, dy: np.ndarray, bits: int) -> np.ndarray:
+    """-> dx as bf16 bit patterns (uint16), same shape as dy."""
+    packed = np.ascontiguousarray(packed, dtype=np.uint32)
+    dy = np.ascontiguousarray(dy)
+    dx = np.zeros(dy.shape, dtype=np.uint16)
+    _check(lib().oracle_relu_unpack(_ptr(packed), _ptr(dy), _dtype_code(dy), dy.size, bits, _ptr(dx)))
+    return dx
+
+
+def act_forward(x: np.ndarray, act: int):
+    """Unfused helpers: relu/relu6 -> (y in x's type, int8 mask); gelu/silu -> (bf16 y, bf16 dy/dx)."""
+    x = np.ascontiguousarray(x)
+    if act in (ACT_RELU, ACT_RELU6):
+        y, aux = np.zeros_like(x), np.zeros(x.shape, dtype=np.int8)
+    else:
+        y, aux = np.zeros(x.shape, dtype=np.uint16), np.zeros(x.shape, dtype=np.uint16)
+    _check(lib().oracle_act_forward(_ptr(x), _dtype_code(x), x.size, act, _ptr(y), _ptr(aux)))
+    return y, aux
+
+
+def act_quant_pack(x: np.ndarray, act: int, group_size: int, bits: int, *, tile_nchw=None, meta_dtype=BF16):
+    """Fused GELU/SiLU forward -> (bf16 y shaped like x, packed [NG, W], scale [NG], min [NG])."""
+    x = np.ascontiguousarray(x)
+    ng = x.size // group_size
+    tile = None if tile_nchw is None else np.array([int(v) for v in tile_nchw], dtype=np.int64)
+    y = np.zeros(x.shape, dtype=np.uint16)
+    packed = np.zeros((ng, group_size * bits // 32), dtype=np.uint32)
+    mdt = np.float32 if meta_dtype == F32 else np.uint16
+    scale, mn = np.zeros(ng, dtype=mdt), np.zeros(ng, dtype=mdt)
+    _check(lib().oracle_act_quant_pack(_ptr(x), _dtype_code(x), act, ng, group_size, bits, _ptr(tile), _ptr(y),
+                                       _ptr(packed), _ptr(scale), _ptr(mn), meta_dtype))
+    return y, packed, scale, mn
+
+
+def act_dequant_mul(packed, scale, mn, group_size: int, bits: int, dy: np.ndarray, *, tile_nchw=None):
+    """Fused GELU/SiLU backward -> dx = bf16(dy * dequant) as uint16, shaped like dy."""
+    packed = np.ascontiguousarray(packed, dtype=np.uint32)
+    dy = np.ascontiguousarray(dy)
+    ng = packed.size * 32 // bits // group_size
+    meta_dtype = F32 if scale.dtype == np.float32 else BF16
+    tile = None if tile_nchw is None else np.array([int(v) for v in tile_nchw], dtype=np.int64)
+    dx = np.zeros(dy.shape, dtype=np.uint16)
+    _check(lib().oracle_act_dequant_mul(_ptr(packed), _ptr(np.ascontiguousarray(scale)), _ptr(np.ascontiguousarray(mn)),
+                                        meta_dtype, ng, group_size, bits, _ptr(tile), _ptr(dy), _dtype_code(dy),
+                                        _ptr(dx)))
+    return dx
 
 
 def f32_to_bf16_bits(a: np.ndarray) -> np.ndarray:

@@ -30,6 +30,13 @@
  *   Philox4x32-10                  pinned: published known-answer vectors (Salmon et al., SC'11)
  *   squash (tanh(2x)/2)            parity unpinned at bit level: the reference uses libdevice tanh
  *                                  on an NVIDIA GPU; this oracle uses the C library's tanhf.
+ *   ReLU mask pack / unpack        pinned: known answers, numpy.packbits, closed form dy * mask
+ *   GELU / SiLU value, derivative  parity unpinned at bit level (Triton exp, libdevice tanh);
+ *                                  pinned to tolerance against torch's float64 gelu / silu and
+ *                                  their autograd derivatives
+ *   fused activation quant-pack    pinned: equals the quantizer above applied to the squashed
+ *                                  derivative with the range floored at 1e-4
+ *   fused activation backward      pinned: closed form bf16(dy * dequant)
  */
 #include <math.h>
 #include <stdint.h>
@@ -323,6 +330,194 @@ int oracle_unpack_codes(const uint32_t* packed, int64_t n_groups, int g, int bit
     for (int64_t w = 0; w < nw; ++w)
         for (int j = 0; j < VPW; ++j)
             codes[w * VPW + j] = (int8_t)((packed[w] >> (j * bits)) & QMAX);
+    return O_OK;
+}
+
+/* ---------------------------------------------------------------- fused activation layers
+ * AC/modules/activations/kernel_implementation.py. Transcendentals use the C library's tanhf /
+ * expf in fp32 (the reference uses Triton's exp and libdevice tanh): "parity unpinned" at bit
+ * level for the GELU / SiLU values and derivatives; everything downstream of them (min/max,
+ * codes, packing, the backward multiply) follows the quantizer's exact arithmetic. */
+#define O_ACT_RELU 0
+#define O_ACT_RELU6 1
+#define O_ACT_GELU 2
+#define O_ACT_SILU 3
+
+static void store_elem(void* y, int dtype, int64_t i, float v) {
+    if (dtype == O_F32)
+        ((float*)y)[i] = v;
+    else
+        ((uint16_t*)y)[i] = f32_to_bf16(v);
+}
+
+/* GELU, tanh form (:496-519): u = a (x + b x^3), t = tanh(u), y = 0.5 x (1 + t),
+ * dy/dx = 0.5 (1 + t) + 0.5 x (1 - t^2) a (1 + 3 b x^2) */
+static void gelu_and_grad(float x, float* y, float* d) {
+    const float a = 0.7978845608028654f, b = 0.044715f, b3 = 0.134145f;
+    float x2 = x * x;
+    float x3 = x * x2;
+    float u = a * (x + b * x3);
+    float t = tanhf(u);
+    *y = 0.5f * x * (1.0f + t);
+    float dt = 1.0f - t * t;
+    float du = a * (1.0f + b3 * x2);
+    *d = 0.5f * (1.0f + t) + 0.5f * x * dt * du;
+}
+
+/* SiLU (:225-229): s = 1 / (1 + exp(-x)), y = x s, dy/dx = s + x s (1 - s) */
+static void silu_and_grad(float x, float* y, float* d) {
+    float s = 1.0f / (1.0f + expf(-x));
+    *y = x * s;
+    *d = s + x * s * (1.0f - s);
+}
+
+/* relu_variance_fwd_fused_pack_kernel (:34-90): mask = x > 0 (relu6: 0 < x < 6),
+ * y = mask ? bf16(x) : 0 stored in x's type, mask codes (0/1) packed b bits each. */
+int oracle_relu_pack(const void* x, int x_dtype, int64_t n, int relu6, int bits, void* y, uint32_t* packed) {
+    if (bits != 1 && bits != 2 && bits != 4 && bits != 8) return O_EBITS;
+    if (x_dtype != O_F32 && x_dtype != O_BF16) return O_EINVAL;
+    if (n < 0 || n % 64) return O_EINVAL;
+    const int VPW = 32 / bits;
+    for (int64_t w = 0; w < n / VPW; ++w) packed[w] = 0;
+    for (int64_t i = 0; i < n; ++i) {
+        float v = load_elem(x, x_dtype, i);
+        int m = relu6 ? (v > 0.0f && v < 6.0f) : (v > 0.0f);
+        float o = m ? bf16_to_f32(f32_to_bf16(v)) : 0.0f;
+        store_elem(y, x_dtype, i, o);
+        packed[i / VPW] |= (uint32_t)m << ((i % VPW) * bits);
+    }
+    return O_OK;
+}
+
+/* relu_bwd_fused_unpack_kernel (:93-143): dx = bf16(dy * float(code & 1)) */
+int oracle_relu_unpack(const uint32_t* packed, const void* dy, int dy_dtype, int64_t n, int bits, uint16_t* dx) {
+    if (bits != 1 && bits != 2 && bits != 4 && bits != 8) return O_EBITS;
+    if (n < 0 || n % 64) return O_EINVAL;
+    const int VPW = 32 / bits;
+    for (int64_t i = 0; i < n; ++i) {
+        uint32_t m = (packed[i / VPW] >> ((i % VPW) * bits)) & 1u;
+        float g = load_elem(dy, dy_dtype, i);
+        dx[i] = f32_to_bf16(g * (float)m);
+    }
+    return O_OK;
+}
+
+/* the unfused helpers relu_variance_kernel (:9-31), silu_triton (:154-175), gelu_triton (:437-466) */
+int oracle_act_forward(const void* x, int x_dtype, int64_t n, int act, void* y, void* aux) {
+    if (n < 0 || act < 0 || act > 3) return O_EINVAL;
+    for (int64_t i = 0; i < n; ++i) {
+        float v = load_elem(x, x_dtype, i);
+        if (act == O_ACT_RELU || act == O_ACT_RELU6) {
+            int m = act == O_ACT_RELU6 ? (v > 0.0f && v < 6.0f) : (v > 0.0f);
+            if (x_dtype == O_F32)
+                ((float*)y)[i] = m ? v : 0.0f;
+            else
+                ((uint16_t*)y)[i] = m ? ((const uint16_t*)x)[i] : 0;
+            ((int8_t*)aux)[i] = (int8_t)m;
+        } else {
+            float yv, dv;
+            if (act == O_ACT_GELU)
+                gelu_and_grad(v, &yv, &dv);
+            else
+                silu_and_grad(v, &yv, &dv);
+            ((uint16_t*)y)[i] = f32_to_bf16(yv);
+            ((uint16_t*)aux)[i] = f32_to_bf16(dv);
+        }
+    }
+    return O_OK;
+}
+
+/* gelu_fwd_fused_quan_pack_triton (:468-535) / silu_fwd_fused_quan_pack_triton (:180-243):
+ * y = act(x) as bf16; d = tanh(clamp(act'(x), -3, 3) / 0.5) * 0.5; per group mn, mx,
+ * rng = max(mx - mn, 1e-4), step = rng / QMAX, inv = 1 / step,
+ * q = clamp(trunc(fma(d - mn, inv, 0.5 - 1e-6)), 0, QMAX), packed as the quantizer does. */
+int oracle_act_quant_pack(const void* x, int x_dtype, int act, int64_t n_groups, int g, int bits,
+                          const int64_t* tile_nchw, uint16_t* y, uint32_t* packed, void* scale, void* minv,
+                          int meta_dtype) {
+    int s = 0;
+    int rc = check_common(n_groups, g, bits, tile_nchw, &s);
+    if (rc) return rc;
+    if (x_dtype != O_F32 && x_dtype != O_BF16) return O_EINVAL;
+    if (act != O_ACT_GELU && act != O_ACT_SILU) return O_EINVAL;
+    if (meta_dtype != O_F32 && meta_dtype != O_BF16) return O_EINVAL;
+    const int QMAX = (1 << bits) - 1;
+    const int VPW = 32 / bits, NW = g / VPW;
+    const float qmaxf = (float)QMAX;
+    const float half_m = (float)(0.5 - 1e-6);
+#pragma omp parallel
+    {
+        float* ds = (float*)malloc(sizeof(float) * g);
+#pragma omp for schedule(static)
+        for (int64_t r = 0; r < n_groups; ++r) {
+            for (int e = 0; e < g; ++e) {
+                int64_t idx = elem_index(r, e, g, tile_nchw, s);
+                float v = load_elem(x, x_dtype, idx), yv, dv;
+                if (act == O_ACT_GELU)
+                    gelu_and_grad(v, &yv, &dv);
+                else
+                    silu_and_grad(v, &yv, &dv);
+                y[idx] = f32_to_bf16(yv);
+                dv = fminf(fmaxf(dv, -3.0f), 3.0f);
+                ds[e] = tanhf(dv / 0.5f) * 0.5f;
+            }
+            float mn = ds[0], mx = ds[0];
+            for (int e = 1; e < g; ++e) {
+                mn = fminf(mn, ds[e]);
+                mx = fmaxf(mx, ds[e]);
+            }
+            mn = mn + 0.0f;
+            float rng = fmaxf(mx - mn, 1e-4f);
+            float step = rng / qmaxf;
+            float inv = 1.0f / step;
+            for (int w = 0; w < NW; ++w) {
+                uint32_t word = 0;
+                for (int j = 0; j < VPW; ++j) {
+                    float qf = fmaf(ds[w * VPW + j] - mn, inv, half_m);
+                    if (qf != qf) qf = 0.0f;
+                    qf = fminf(fmaxf(qf, 0.0f), qmaxf);
+                    word |= (uint32_t)(int)qf << (j * bits);
+                }
+                packed[r * NW + w] = word;
+            }
+            if (meta_dtype == O_F32) {
+                ((float*)scale)[r] = step;
+                ((float*)minv)[r] = mn;
+            } else {
+                ((uint16_t*)scale)[r] = f32_to_bf16(step);
+                ((uint16_t*)minv)[r] = f32_to_bf16(mn);
+            }
+        }
+        free(ds);
+    }
+    return O_OK;
+}
+
+/* gelu_bwd / silu_bwd_fused_dequan_unpack (:360-395): dx = bf16(dy * fma(float(q), scale, min)) */
+int oracle_act_dequant_mul(const uint32_t* packed, const void* scale, const void* minv, int meta_dtype,
+                           int64_t n_groups, int g, int bits, const int64_t* tile_nchw, const void* dy,
+                           int dy_dtype, uint16_t* dx) {
+    int s = 0;
+    int rc = check_common(n_groups, g, bits, tile_nchw, &s);
+    if (rc) return rc;
+    const uint32_t QMAX = (1u << bits) - 1u;
+    const int VPW = 32 / bits, NW = g / VPW;
+#pragma omp parallel for schedule(static)
+    for (int64_t r = 0; r < n_groups; ++r) {
+        float sc, mn;
+        if (meta_dtype == O_F32) {
+            sc = ((const float*)scale)[r];
+            mn = ((const float*)minv)[r];
+        } else {
+            sc = bf16_to_f32(((const uint16_t*)scale)[r]);
+            mn = bf16_to_f32(((const uint16_t*)minv)[r]);
+        }
+        for (int e = 0; e < g; ++e) {
+            uint32_t qv = (packed[r * NW + e / VPW] >> ((e % VPW) * bits)) & QMAX;
+            int64_t o = elem_index(r, e, g, tile_nchw, s);
+            float act = fmaf((float)qv, sc, mn);
+            dx[o] = f32_to_bf16(load_elem(dy, dy_dtype, o) * act);
+        }
+    }
     return O_OK;
 }
 

@@ -226,3 +226,41 @@ def test_padding_zero_fills():
     groups, N, G, *_ = tr.spatical_aware_act_tensor_reshape(x, 64, True, False)
     assert G == 1 and groups.shape == (2, 1, 64)
     assert torch.equal(groups[:, 0, :15], torch.ones(2, 15)) and torch.count_nonzero(groups[:, 0, 15:]) == 0
+
+
+# ----------------------------------------------------------------------------- per-layer group meta
+class TestLayerGroupMeta:
+    """Known answers worked out by hand from the rule of controller.py:364-378 (first of
+    [512, 256, 128, 64], or [1024, ...] for BatchNorm, dividing the grouped extent; else 256 with
+    padding) and the N/G arithmetic of controller.py:127-177."""
+
+    def test_find_group_size_known_answers(self):
+        from deep_optimization_amd.controller import find_group_size
+
+        assert find_group_size(256 * 56 * 56, 2) == (512, False)  # ResNet conv2 activation per sample
+        assert find_group_size(197 * 3072, 2) == (512, False)  # ViT MLP activation per sample
+        assert find_group_size(64 * 3 * 3 * 2, 4) == (128, False)  # 1152 = 2^7 * 9
+        assert find_group_size(64 * 3, 8) == (64, False)
+        assert find_group_size(100, 1) == (256, True)  # no power of two >= 64 divides 100
+        assert find_group_size(1024 * 7, 2, special=True) == (1024, False)
+        assert find_group_size(1024 * 7, 2) == (512, False)
+        assert find_group_size(512, 3) == (256, True)  # bits outside {1,2,4,8} fall through
+
+    def test_layer_group_meta_shapes(self):
+        from deep_optimization_amd.controller import layer_group_meta
+
+        m = layer_group_meta((256, 256, 56, 56), 2)
+        assert m == {"group_size": 512, "act_padding": False, "N": 256, "NG": 256 * 1568}
+        m = layer_group_meta((256, 197, 3072), 2)
+        assert m == {"group_size": 512, "act_padding": False, "N": 256, "NG": 256 * 1182}
+        m = layer_group_meta((256, 64, 56, 56), 2, batchnorm=True)  # per channel: N*H*W = 802816
+        assert m == {"group_size": 1024, "act_padding": False, "N": 64, "NG": 64 * 784}
+        m = layer_group_meta((32, 100), 1)
+        assert m == {"group_size": 256, "act_padding": True, "N": 32, "NG": 32}
+        m = layer_group_meta((8, 64, 32, 32), 2)  # BASELINE config 1 shape
+        assert m["group_size"] == 512 and m["NG"] == 8 * 128
+
+    def test_activation_size(self):
+        from deep_optimization_amd.controller import compute_activation_size_in_bytes
+
+        assert compute_activation_size_in_bytes((256, 256, 56, 56), torch.bfloat16) == 256 * 256 * 56 * 56 * 2 / 2 ** 20

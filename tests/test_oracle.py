@@ -455,3 +455,107 @@ def test_golden_fixtures_regenerate():
         fresh = make_golden.compute_case(name)
         for key in case:
             np.testing.assert_array_equal(case[key], fresh[key], err_msg=f"{name}:{key}")
+
+
+# ----------------------------------------------------------------------------- fused activation layers
+def _bf16(a):
+    return oracle.f32_to_bf16_bits(np.asarray(a, dtype=np.float32))
+
+
+def _f32(b):
+    return oracle.bf16_bits_to_f32(b)
+
+
+@pytest.mark.parametrize("bits", [1, 2, 4, 8])
+@pytest.mark.parametrize("relu6", [False, True])
+@pytest.mark.parametrize("storage", ["f32", "bf16"])
+def test_relu_pack_known_answers(bits, relu6, storage):
+    rng = np.random.default_rng(60 + bits)
+    x = (rng.standard_normal(1024) * 4).astype(np.float32)
+    x[:8] = [0.0, -0.0, 6.0, 5.999, 1e-30, -1e-30, np.inf, -np.inf]
+    xin = x if storage == "f32" else _bf16(x)
+    xv = x if storage == "f32" else _f32(xin)
+    y, packed = oracle.relu_pack(xin, bits, relu6)
+    mask = ((xv > 0) & (xv < 6)) if relu6 else (xv > 0)
+    want_y = np.where(mask, _f32(_bf16(xv)), 0.0).astype(np.float32)  # bf16-rounded as the reference stores it
+    got_y = y if storage == "f32" else _f32(y)
+    np.testing.assert_array_equal(got_y, want_y)
+    assert np.all(got_y.view(np.uint32)[~mask] == 0)  # +0.0, not -0.0
+    codes = mask.astype(np.int64).reshape(1, -1)
+    np.testing.assert_array_equal(words_to_bytes(packed), packbits_reference(codes, bits)[0])
+
+
+@pytest.mark.parametrize("bits", [1, 4])
+def test_relu_unpack_closed_form(bits):
+    rng = np.random.default_rng(70 + bits)
+    mask = rng.random(512) < 0.5
+    packed = packbits_reference(mask.astype(np.int64).reshape(1, -1), bits)[0].view("<u4")
+    dy = (rng.standard_normal(512) * 3).astype(np.float32)
+    dy[:3] = [-2.0, np.inf, -np.inf]
+    mask[:3] = False
+    packed = packbits_reference(mask.astype(np.int64).reshape(1, -1), bits)[0].view("<u4")
+    dx = oracle.relu_unpack(packed, dy, bits)
+    with np.errstate(invalid="ignore"):
+        want = _bf16((dy * mask.astype(np.float32)).astype(np.float32))  # -2*0 = -0.0, inf*0 = NaN
+    np.testing.assert_array_equal(dx[3:], want[3:])
+    assert dx[0] == 0x8000 and np.isnan(_f32(dx[1:3])).all()
+
+
+def _torch_act_and_grad(x, act):
+    xt = torch.tensor(x, dtype=torch.float64, requires_grad=True)
+    y = torch.nn.functional.gelu(xt, approximate="tanh") if act == oracle.ACT_GELU else torch.nn.functional.silu(xt)
+    (g,) = torch.autograd.grad(y.sum(), xt)
+    return y.detach().numpy(), g.numpy()
+
+
+@pytest.mark.parametrize("act", [oracle.ACT_GELU, oracle.ACT_SILU])
+def test_act_forward_matches_torch_float64(act):
+    rng = np.random.default_rng(80 + act)
+    x = np.concatenate([rng.standard_normal(4000) * 3, [0.0, -0.0, 10.0, -10.0, 30.0, -30.0]]).astype(np.float32)
+    y, d = oracle.act_forward(x, act)
+    ty, td = _torch_act_and_grad(x.astype(np.float64), act)
+    # fp32 evaluation then one bf16 rounding: within one bf16 ulp of the float64 value
+    for got, want in ((_f32(y), ty), (_f32(d), td)):
+        err = np.abs(got.astype(np.float64) - want)
+        assert np.all(err <= np.abs(want) * 2 ** -8 + 1e-6), float(err.max())
+
+
+@pytest.mark.parametrize("act", [oracle.ACT_GELU, oracle.ACT_SILU])
+@pytest.mark.parametrize("bits", [1, 2, 4, 8])
+def test_act_quant_pack_is_the_quantizer_of_the_squashed_derivative(act, bits):
+    rng = np.random.default_rng(90 + bits + 10 * act)
+    g = 128
+    x = (rng.standard_normal((40, g)) * 2).astype(np.float32)
+    y, packed, scale, mn = oracle.act_quant_pack(x, act, g, bits, meta_dtype=oracle.F32)
+    y0, _ = oracle.act_forward(x, act)
+    np.testing.assert_array_equal(y, y0)  # the activation output is the unfused one
+    # the squashed derivative, float64: dequantized codes must lie within step/2 (+fp32 slack) of it
+    _, td = _torch_act_and_grad(x.astype(np.float64), act)
+    sq = np.tanh(np.clip(td, -3, 3) / 0.5) * 0.5
+    deq = oracle.dequant_unpack(packed, scale, mn, g, bits)
+    assert np.all(np.abs(deq - sq) <= scale[:, None] * 0.5 + 1e-5)
+    # the range floor: max(mx - mn, 1e-4) / QMAX
+    assert np.all(scale >= np.float32(1e-4) / np.float32((1 << bits) - 1))
+
+
+def test_act_quant_pack_range_floor_known_answer():
+    # a constant group has mx == mn: the range is floored at 1e-4, so step = 1e-4/QMAX and every code is 0
+    x = np.full((2, 64), 0.7, dtype=np.float32)
+    for act in (oracle.ACT_GELU, oracle.ACT_SILU):
+        _, packed, scale, mn = oracle.act_quant_pack(x, act, 64, 2, meta_dtype=oracle.F32)
+        assert np.all(packed == 0)
+        assert np.all(scale == np.float32(np.float32(1e-4) / np.float32(3)))
+
+
+@pytest.mark.parametrize("bits", [2, 8])
+def test_act_dequant_mul_closed_form(bits):
+    rng = np.random.default_rng(100 + bits)
+    g, ng = 256, 24
+    q = rng.integers(0, 1 << bits, size=(ng, g))
+    packed = packbits_reference(q, bits).view("<u4").reshape(ng, -1)
+    sc = _bf16(rng.random(ng) * 0.1)
+    mn = _bf16(rng.standard_normal(ng) * 0.2)
+    dy = _bf16(rng.standard_normal((ng, g)))
+    dx = oracle.act_dequant_mul(packed, sc, mn, g, bits, dy)
+    act = fma32(q.astype(np.float32), np.broadcast_to(_f32(sc)[:, None], q.shape), np.broadcast_to(_f32(mn)[:, None], q.shape))
+    np.testing.assert_array_equal(dx, _bf16((_f32(dy) * act).astype(np.float32)))
