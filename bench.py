@@ -93,6 +93,60 @@ def pmc_probe() -> int:
     return 0
 
 
+def vit_train_step(torch, dev, batch=128, steps=6, warmup=3):
+    """one ViT-B/16 train step (forward, cross-entropy, backward, fused AdamW step)
+    on a fixed synthetic batch (N(0,1) images 224x224x3, random labels over 1000 classes, bf16
+    autocast, random-init weights), plain and rewritten by the Controller with every selected saved
+    activation 2-bit. Reports ms per step and the peak HBM allocated during the timed steps."""
+    import torch.nn.functional as F
+
+    from deep_optimization_amd.controller import Controller
+    from deep_optimization_amd.vit import vit_base_patch16_224
+
+    res = {}
+    g = torch.Generator(device=dev).manual_seed(5)
+    xb = torch.randn((batch, 3, 224, 224), generator=g, device=dev)
+    yb = torch.randint(0, 1000, (batch,), generator=g, device=dev)
+    for name in ("plain", "compressed_2bit"):
+        torch.manual_seed(0)
+        model = vit_base_patch16_224().to(dev).train()
+        if name != "plain":
+            ctl = Controller(model, {"batch_size": batch, "default_bits": 2}, input_shape=(3, 224, 224))
+            model = ctl.warp_model()
+        opt = torch.optim.AdamW(model.parameters(), lr=3e-3, fused=True)
+
+        def one():
+            opt.zero_grad(set_to_none=True)
+            with torch.autocast("cuda", dtype=torch.bfloat16):
+                loss = F.cross_entropy(model(xb), yb)
+            loss.backward()
+            opt.step()
+            return loss
+
+        for _ in range(warmup):
+            one()
+        torch.cuda.synchronize()
+        torch.cuda.reset_peak_memory_stats()
+        base_alloc = torch.cuda.memory_allocated()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            loss = one()
+        torch.cuda.synchronize()
+        dt = (time.perf_counter() - t0) / steps
+        res[name] = {"ms_per_step": round(dt * 1e3, 2), "samples_per_s": round(batch / dt, 1),
+                     "peak_hbm_GiB": round(torch.cuda.max_memory_allocated() / 2 ** 30, 3),
+                     "peak_above_resident_GiB": round((torch.cuda.max_memory_allocated() - base_alloc) / 2 ** 30, 3),
+                     "loss": round(float(loss.detach()), 4)}
+        if name != "plain":
+            res[name]["layers_compressed"] = sum(1 for v in ctl.meta.values() if isinstance(v, dict))
+        del model, opt
+        torch.cuda.empty_cache()
+    p, c = res["plain"], res["compressed_2bit"]
+    res["compressed_vs_plain"] = {"step_time_ratio": round(c["ms_per_step"] / p["ms_per_step"], 3),
+                                  "peak_hbm_ratio": round(c["peak_hbm_GiB"] / p["peak_hbm_GiB"], 3)}
+    return res
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -307,6 +361,8 @@ def main() -> int:
             gemm[f"{M}x{Nn}x{K}"] = entry
             del a8, b8, cm
         extras["fp8_gemm_nt"] = gemm
+        torch.cuda.empty_cache()
+        extras["vit_b16_train_step_bs128"] = vit_train_step(torch, dev)
         out["extras"] = extras
 
     if not args.no_cpu:

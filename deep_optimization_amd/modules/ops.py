@@ -1,0 +1,163 @@
+"""Compressed Linear / Conv autograd Functions: the forward saves the layer input quantized
+(per-group min/max, b bits, packed) instead of the input itself; the backward dequantizes it and
+computes the weight and input gradients.
+
+Mirrors Activation_Compression/modules/ops.py: ``_DOConvnd.run_forward`` / ``run_backward``
+(:200-387), ``_DOConv1d/2d/3d`` (:390-435) and ``_DOLinear`` (:438-540), with the same ``apply``
+arguments and ``meta`` keys (bits, group_size, act_padding, pack_only, AVG_ALAM, ALAM_BITS,
+DIVISION and the optional rounding keys of module_utils). As in the reference, the saved input is
+quantized with ``clamp=True`` and the layer's ``clamp_alpha`` (the tanh squash of the quantizer
+applies), an optional DIVISION low-pass (average pool) is stored beside it and added back when
+the input is restored, and under autocast the computation runs in the autocast dtype.
+
+Differences from the reference:
+  * ``_DOLinear`` takes the bias and applies it (the reference calls ``F.linear(input, W, None)``
+    and never trains the bias, ops.py:481); its gradient is ``dy`` summed over the rows;
+  * the Conv Functions take an optional bias the same way (the reference's DOConv layers are
+    built with ``bias=False``).
+"""
+from __future__ import annotations
+
+import torch
+import torch.nn.functional as F
+from torch.amp import custom_bwd, custom_fwd
+from torch.autograd import Function
+from torch.nn.grad import conv1d_input, conv1d_weight, conv2d_input, conv2d_weight, conv3d_input, conv3d_weight
+from torch.nn.modules.utils import _pair, _single, _triple
+
+from .module_utils import unified_dequantize, unified_quantize
+
+
+def _compute_dtype():
+    return torch.get_autocast_dtype("cuda") if torch.is_autocast_enabled("cuda") else None
+
+
+class _DOConvnd(Function):
+    @staticmethod
+    def run_forward(ctx, forward_op, input, weight, learnable_scale, stride=1, padding=0, dilation=1, groups=1,
+                    clamp_alpha=3.0, target_name=None, meta=None, ema_grad_meta=None, bias=None):
+        """ops.py:200-270."""
+        dt = _compute_dtype()
+        if dt is not None:
+            input = input.to(dt)
+            weight_compute = weight.to(dt)
+            bias_compute = None if bias is None else bias.to(dt)
+        else:
+            weight_compute, bias_compute = weight, bias
+        m = meta[f"{target_name}"]
+        input_l = None
+        if m.get("DIVISION") is not None and not m["pack_only"]:
+            k = min(input.shape[-2], input.shape[-1], m["DIVISION"]["pool_kernel_size"])
+            input_l = F.avg_pool2d(input.to(torch.bfloat16), k, stride=k, padding=0)
+        q_tensor, q_meta, input_l = unified_quantize(input.to(torch.bfloat16), input_l, target_name, meta, clamp=True,
+                                                     clamp_alpha=clamp_alpha)
+        ctx.meta = stride, padding, dilation, groups, ema_grad_meta, clamp_alpha, bias is not None
+        ctx.save_for_backward(weight, q_tensor[0], q_tensor[1], q_tensor[2], input_l, learnable_scale)
+        ctx.q_inputs_meta = q_meta
+        return forward_op(input, weight_compute, bias=bias_compute, stride=stride, padding=padding, dilation=dilation,
+                          groups=groups)
+
+    @staticmethod
+    def run_backward(ctx, dy, dim, pad_fn):
+        """ops.py:273-387: restores the input, then the input and weight gradients by conv*_input /
+        conv*_weight."""
+        stride, padding, dilation, groups, _, _, has_bias = ctx.meta
+        weight, q0, q1, q2, input_l, _ = ctx.saved_tensors
+        dt = _compute_dtype()
+        if dt is not None:
+            dy = dy.to(dt)
+            weight_compute = weight.to(torch.bfloat16)
+        else:
+            weight_compute = weight
+        stride, padding, dilation = pad_fn(stride), pad_fn(padding), pad_fn(dilation)
+        input = unified_dequantize((q0, q1, q2), ctx.q_inputs_meta, input_l)
+        if dt is None:
+            input = input.to(dy.dtype)
+        grad_input = {1: conv1d_input, 2: conv2d_input, 3: conv3d_input}[dim]
+        grad_weight = {1: conv1d_weight, 2: conv2d_weight, 3: conv3d_weight}[dim]
+        dx = dw = db = None
+        if ctx.needs_input_grad[0]:
+            dx = grad_input(input.shape, weight_compute.to(dy.dtype), dy, stride=stride, padding=padding,
+                            dilation=dilation, groups=groups)
+        if ctx.needs_input_grad[1]:
+            dw = grad_weight(input.to(dy.dtype), weight_compute.shape, dy, stride=stride, padding=padding,
+                             dilation=dilation, groups=groups)
+        if has_bias:
+            db = dy.sum(dim=[0] + list(range(2, dy.dim())))
+        if dx is not None and dt is not None:
+            dx = dx.to(torch.bfloat16)
+        if dw is not None and dt is not None:
+            dw = dw.to(torch.bfloat16)
+        return dx, dw, None, None, None, None, None, None, None, None, None, db
+
+
+def _conv_function(dim, op, pad_fn, name):
+    class _Fn(Function):
+        @staticmethod
+        @custom_fwd(device_type="cuda")
+        def forward(ctx, input, weight, learnable_scale, stride=1, padding=0, dilation=1, groups=1, clamp_alpha=3.0,
+                    target_name=None, meta=None, ema_grad_meta=None, bias=None):
+            return _DOConvnd.run_forward(ctx, op, input, weight, learnable_scale, stride=stride, padding=padding,
+                                         dilation=dilation, groups=groups, clamp_alpha=clamp_alpha,
+                                         target_name=target_name, meta=meta, ema_grad_meta=ema_grad_meta, bias=bias)
+
+        @staticmethod
+        @custom_bwd(device_type="cuda")
+        def backward(ctx, dy):
+            return _DOConvnd.run_backward(ctx, dy, dim, pad_fn)
+
+    _Fn.__name__ = _Fn.__qualname__ = name
+    return _Fn
+
+
+_DOConv1d = _conv_function(1, F.conv1d, _single, "_DOConv1d")  # ops.py:390-403
+_DOConv2d = _conv_function(2, F.conv2d, _pair, "_DOConv2d")  # ops.py:406-419
+_DOConv3d = _conv_function(3, F.conv3d, _triple, "_DOConv3d")  # ops.py:422-435
+
+
+class _DOLinear(Function):
+    """ops.py:438-540 (plus the bias, see the module docstring)."""
+
+    @staticmethod
+    @custom_fwd(device_type="cuda")
+    def forward(ctx, input, weight, clamp_alpha, target_name, meta, ema_grad_meta, bias=None):
+        dt = _compute_dtype()
+        if dt is not None:
+            input = input.to(dt)
+            weight_compute = weight.to(dt)
+            bias_compute = None if bias is None else bias.to(dt)
+        else:
+            weight_compute, bias_compute = weight, bias
+        m = meta[f"{target_name}"]
+        input_l = None
+        if m.get("DIVISION") is not None and input.ndim not in (1, 2) and not m["pack_only"]:
+            k = min(input.shape[2], m["DIVISION"]["pool_kernel_size"])
+            input_l = F.avg_pool1d(input.to(torch.bfloat16), k, stride=k, padding=0)
+        q_tensor, q_meta, input_l = unified_quantize(input, input_l, target_name, meta, clamp=True,
+                                                     clamp_alpha=clamp_alpha)
+        ctx.q_inputs_meta = q_meta
+        ctx.meta = input.shape, ema_grad_meta, clamp_alpha, bias is not None
+        ctx.save_for_backward(weight, q_tensor[0], q_tensor[1], q_tensor[2], input_l)
+        return F.linear(input, weight_compute, bias_compute)
+
+    @staticmethod
+    @custom_bwd(device_type="cuda")
+    def backward(ctx, dy):
+        input_shape, _, _, has_bias = ctx.meta
+        weight, q0, q1, q2, input_l = ctx.saved_tensors
+        dt = _compute_dtype()
+        if dt is not None:
+            weight_compute = weight.to(dt)
+            dy = dy.to(dt)
+        else:
+            weight_compute = weight
+        input = unified_dequantize((q0, q1, q2), ctx.q_inputs_meta, input_l).to(dy.dtype)
+        C_in, C_out = input.shape[-1], dy.shape[-1]
+        dy_flat = dy.reshape(-1, C_out)
+        dw = dy_flat.t().mm(input.reshape(-1, C_in))
+        dx = dy_flat.mm(weight_compute.to(dy.dtype))
+        db = dy_flat.sum(0) if has_bias else None
+        return dx.view(*input_shape), dw, None, None, None, None, db
+
+
+__all__ = ["_DOConvnd", "_DOConv1d", "_DOConv2d", "_DOConv3d", "_DOLinear"]

@@ -1,0 +1,168 @@
+"""Compressed Linear / Conv layers and the Controller-rewritten model on the GPU.
+
+What is pinned and how:
+  * forward outputs: bit-exact against the same torch product (F.linear / F.conv*) on the same
+    bf16 operands: the compressed layers change only what is saved;
+  * the saved input: the layer's weight gradient must equal dy^T . x_hat (Linear) or
+    conv*_weight(x_hat, dy) (Conv) computed in fp32, where x_hat is the reference operator chain
+    act_lib::quant_pack_triton(clamp=True, alpha=3) -> act_lib::dequant_unpack_triton on the
+    reference's grouping (Activation_Compression/modules/ops.py:262-264, :472-474, :508-512). That
+    chain is pinned bit-exactly against the CPU oracle by the parity tests. Bar: relative
+    Frobenius error <= 1e-2 (bf16 GEMM over up to 25k rows);
+  * input and bias gradients: fp32 references of dy . W and sum(dy), same bar;
+  * the model rewrite: a 2-block ViT-B/16 trains (loss falls on a fixed batch), and the bytes its
+    autograd graph saves drop by the factor the 2-bit format predicts.
+"""
+import pytest
+import torch
+import torch.nn.functional as F
+from torch.nn.grad import conv2d_input, conv2d_weight
+
+import deep_optimization_amd  # noqa: F401
+from deep_optimization_amd.controller import Controller, layer_group_meta
+from deep_optimization_amd.layers import DOConv2d, DOLinear
+from deep_optimization_amd.vit import VisionTransformer
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def rel_err(got, want):
+    got, want = got.double(), want.double()
+    return ((got - want).norm() / want.norm().clamp_min(1e-30)).item()
+
+
+def meta_for(name, shape, bits, **over):
+    m = {"pack_only": False, "bits": bits, "AVG_ALAM": False, "ALAM_BITS": 0, "DIVISION": None}
+    m.update(layer_group_meta(shape, bits))
+    m.update(over)
+    return {name: m}
+
+
+def x_hat_reference(x, bits, g, act_padding):
+    """Reference chain: flat [N, -1, g] grouping, clamp + squash quantize, bf16 dequantize."""
+    assert not act_padding
+    N = x.shape[0]
+    groups = x.reshape(N, -1, g)
+    packed, scale, xmin = torch.ops.act_lib.quant_pack_triton(groups, bits, g, False, 0, True, 3.0)
+    return torch.ops.act_lib.dequant_unpack_triton(packed, scale, xmin, bits, g, False, 0).reshape(x.shape)
+
+
+@pytest.mark.parametrize("bits", [2, 4, 8])
+@pytest.mark.parametrize("shape,autocast", [((4, 197, 768), True), ((512, 1024), True), ((4, 197, 768), False)],
+                         ids=["3d-bf16", "2d-bf16", "3d-fp32"])
+def test_do_linear(bits, shape, autocast):
+    torch.manual_seed(bits)
+    cin, cout = shape[-1], 384
+    layer = DOLinear(cin, cout, target_name="fc", meta=meta_for("fc", shape, bits)).to(DEV).train()
+    x = (torch.randn(shape, device=DEV) * 2).requires_grad_(True)
+    dy = torch.randn(*shape[:-1], cout, device=DEV)
+    with torch.autocast("cuda", dtype=torch.bfloat16, enabled=autocast):
+        y = layer(x)
+        want_y = F.linear(x.detach().to(y.dtype), layer.weight.to(y.dtype), layer.bias.to(y.dtype))
+    assert y.dtype == (torch.bfloat16 if autocast else torch.float32)
+    assert torch.equal(y, want_y)
+    y.backward(dy.to(y.dtype))
+    g = layer.meta["fc"]["group_size"]
+    xin = x.detach().to(torch.bfloat16) if autocast else x.detach()
+    x_hat = x_hat_reference(xin, bits, g, layer.meta["fc"]["act_padding"]).float()
+    dyf = dy.to(y.dtype).float().reshape(-1, cout)
+    wf = layer.weight.detach().to(y.dtype).float()
+    assert rel_err(layer.weight.grad, dyf.t() @ x_hat.reshape(-1, cin)) <= 1e-2
+    assert rel_err(x.grad, (dyf @ wf).reshape(x.shape)) <= 1e-2
+    assert rel_err(layer.bias.grad, dyf.sum(0)) <= 1e-2
+
+
+@pytest.mark.parametrize("bits", [2, 4])
+@pytest.mark.parametrize("case", ["flat512", "tile256", "stride2"])
+def test_do_conv2d(bits, case):
+    torch.manual_seed(10 + bits)
+    if case == "flat512":  # meta as the Controller picks it: S = 64*56*56 = 392 * 512, flat groups
+        shape, k, stride, pad, over = (4, 64, 56, 56), 3, 1, 1, {}
+    elif case == "tile256":  # hand-set 16 x 16 spatial tiles on 32 x 32 maps
+        shape, k, stride, pad, over = (4, 64, 32, 32), 3, 1, 1, {"group_size": 256, "NG": 4 * 64 * 4}
+    else:
+        shape, k, stride, pad, over = (4, 32, 64, 64), 3, 2, 1, {}
+    meta = meta_for("conv", shape, bits, **over)
+    layer = DOConv2d(shape[1], 96, k, stride=stride, padding=pad, target_name="conv", meta=meta).to(DEV).train()
+    x = torch.randn(shape, device=DEV).requires_grad_(True)
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        y = layer(x)
+        want_y = F.conv2d(x.detach().bfloat16(), layer.weight.bfloat16(), None, stride, pad)
+    assert torch.equal(y, want_y)
+    dy = torch.randn_like(y)
+    y.backward(dy)
+    g = meta["conv"]["group_size"]
+    xb = x.detach().bfloat16()
+    if case == "tile256":
+        packed, scale, xmin = torch.ops.act_lib.quant_pack_tiles(xb, bits, g, True, 3.0, True, 0, None, 0, 0,
+                                                                  torch.bfloat16)
+        n, c, h, w = shape
+        x_hat = torch.ops.act_lib.dequant_unpack_tiles(packed, scale, xmin, bits, g, n, c, h, w, torch.bfloat16)
+    else:
+        x_hat = x_hat_reference(xb, bits, g, False)
+    dyf = dy.float()
+    want_dw = conv2d_weight(x_hat.float(), layer.weight.shape, dyf, stride=stride, padding=pad)
+    assert rel_err(layer.weight.grad, want_dw) <= 1e-2
+    want_dx = conv2d_input(x.shape, layer.weight.detach().bfloat16().float(), dyf, stride=stride, padding=pad)
+    assert rel_err(x.grad, want_dx) <= 1e-2
+
+
+def test_tile_layout_reference_chain_matches_flat_permutation():
+    """The in-place tile operators equal the reference's permuted copy
+    (tensor_act_reshape_utils.py:115-125) followed by the flat operators."""
+    torch.manual_seed(5)
+    n, c, h, w, g, s = 2, 8, 32, 32, 256, 16
+    x = torch.randn(n, c, h, w, device=DEV).bfloat16()
+    tiles = x.reshape(n, c, h // s, s, w // s, s).permute(0, 1, 2, 4, 3, 5).reshape(n, -1, g)
+    want = torch.ops.act_lib.quant_pack_triton(tiles, 2, g, False, 0, True, 3.0)
+    got = torch.ops.act_lib.quant_pack_tiles(x, 2, g, True, 3.0, True, 0, None, 0, 0, torch.bfloat16)
+    for a, b in zip(got, want):
+        assert torch.equal(a.reshape(-1), b.reshape(-1))
+
+
+def _saved_bytes(model, x):
+    seen, total = set(), [0]
+
+    def pack(t):
+        key = (t.untyped_storage().data_ptr(), t.dtype)
+        if key not in seen and not isinstance(t, torch.nn.Parameter):
+            seen.add(key)
+            total[0] += t.untyped_storage().nbytes()
+        return t
+
+    with torch.autograd.graph.saved_tensors_hooks(pack, lambda t: t):
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            model(x)
+    return total[0]
+
+
+def test_controller_vit_trains_and_saves_less():
+    torch.manual_seed(7)
+    B = 64
+    base = VisionTransformer(depth=2, num_classes=100).to(DEV)
+    x = torch.randn(B, 3, 224, 224, device=DEV)
+    y = torch.randint(0, 100, (B,), device=DEV)
+    plain_bytes = _saved_bytes(base.train(), x)
+    c = Controller(base, {"batch_size": B, "default_bits": 2}, input_shape=(3, 224, 224))
+    model = c.warp_model()
+    assert "blocks.1.mlp.fc1" in c.meta and "blocks.1.mlp.act" in c.meta
+    comp_bytes = _saved_bytes(model, x)
+    # Per block and per token, in units of 768 bf16 values, the plain model saves about 17 (two
+    # LayerNorm inputs, qkv / proj / fc1 inputs, q k v and the attention output, 4 + 4 for the GELU
+    # and fc2 inputs); 2 bits per value leaves 1/8 of the 11 compressed units: about 7.4 of 17.
+    print(f"saved activation bytes: plain {plain_bytes}, compressed {comp_bytes}")
+    assert comp_bytes < 0.6 * plain_bytes, (comp_bytes, plain_bytes)
+    opt = torch.optim.AdamW(model.parameters(), lr=1e-3, fused=True)
+    losses = []
+    for _ in range(8):
+        opt.zero_grad(set_to_none=True)
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            loss = F.cross_entropy(model(x), y)
+        loss.backward()
+        for n_, p in model.named_parameters():
+            assert p.grad is not None and torch.isfinite(p.grad).all(), n_
+        opt.step()
+        losses.append(loss.item())
+    assert all(torch.isfinite(torch.tensor(losses)))
+    assert losses[-1] < 0.8 * losses[0], losses
