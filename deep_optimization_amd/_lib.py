@@ -16,6 +16,7 @@ F32, F16, BF16 = 0, 1, 2
 ROUND_NEAREST, ROUND_STOCH_NOISE, ROUND_STOCH_PHILOX = 0, 1, 2
 FLAG_CLAMP, FLAG_SQUASH = 1, 2
 ACT_RELU, ACT_RELU6, ACT_GELU, ACT_SILU = 0, 1, 2, 3
+BN_NORM, BN_QUANT, BN_RELU_QUANT, BN_RELU6_QUANT = 0, 1, 2, 3
 
 OK, EBITS, EINVAL, EUNSUPPORTED, EHIP = 0, -1, -2, -3, -4
 
@@ -32,6 +33,11 @@ EXPORTS = (
     "dopt_act_forward",
     "dopt_act_quant_pack",
     "dopt_act_dequant_mul",
+    "dopt_bn_workspace_floats",
+    "dopt_bn_reduce",
+    "dopt_bn_norm_quant",
+    "dopt_bn_bwd_reduce",
+    "dopt_bn_bwd_dx",
 )
 
 _lib = None
@@ -78,6 +84,19 @@ def lib() -> ctypes.CDLL:
         L.dopt_act_quant_pack.restype = i32
         L.dopt_act_dequant_mul.argtypes = [vp, vp, vp, i32, i64, i32, i32, vp, vp, i32, vp, vp]
         L.dopt_act_dequant_mul.restype = i32
+        L.dopt_bn_workspace_floats.argtypes = [i64, i64, i64]
+        L.dopt_bn_workspace_floats.restype = i64
+        L.dopt_bn_reduce.argtypes = [vp, i32, i64, i64, i64, i64, i64, vp, vp, vp, vp]
+        L.dopt_bn_reduce.restype = i32
+        L.dopt_bn_norm_quant.argtypes = [vp, i32, i64, i64, i64, i64, i64, vp, vp, vp, vp, i32, vp, vp, f32, i32, i32,
+                                         i32, vp, vp, vp, vp, vp, vp, vp, vp, vp]
+        L.dopt_bn_norm_quant.restype = i32
+        L.dopt_bn_bwd_reduce.argtypes = [i32, vp, vp, vp, vp, vp, vp, i32, i64, i64, i64, i64, i64, i32, i32, vp, vp, vp,
+                                         vp]
+        L.dopt_bn_bwd_reduce.restype = i32
+        L.dopt_bn_bwd_dx.argtypes = [i32, vp, vp, vp, vp, vp, vp, i32, i64, i64, i64, i64, i64, i32, i32, vp, vp, vp, vp,
+                                     f32, i32, vp, vp]
+        L.dopt_bn_bwd_dx.restype = i32
         _lib = L
     return _lib
 

@@ -25,6 +25,7 @@ SOURCES = [
     "pack_codes.hip",
     "fp8_gemm.hip",
     "act_fused.hip",
+    "bn_fused.hip",
 ]
 
 ARCH = "gfx950"

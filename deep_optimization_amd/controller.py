@@ -77,7 +77,8 @@ def _node_input_meta(node):
     return None
 
 
-_SELECTED = (nn.Linear, nn.Conv1d, nn.Conv2d, nn.Conv3d, nn.ReLU, nn.SiLU, nn.GELU)
+_SELECTED = (nn.Linear, nn.Conv1d, nn.Conv2d, nn.Conv3d, nn.BatchNorm2d, nn.SyncBatchNorm, nn.ReLU, nn.SiLU, nn.GELU)
+_BATCHNORM = (nn.BatchNorm2d, nn.SyncBatchNorm)
 
 
 class Controller:
@@ -89,7 +90,10 @@ class Controller:
     outside this library: every selected layer gets ``default_bits`` unless ``config['bits']``
     (a {target: bits} dict) names it, and ``DIVISION`` is None (a caller may set a layer's
     ``meta[target]['DIVISION']`` by hand; the layer Functions honour it). ReLU layers are
-    mask-only (``pack_only``, 1 bit) as in the reference.
+    mask-only (``pack_only``, 1 bit) as in the reference. BatchNorm and SyncBatchNorm layers get
+    the per-channel group layout (the reference applies it to BatchNorm2d only, controller.py:
+    131-135, and gives SyncBatchNorm the per-sample one its kernels do not use) and keep their
+    bias and running statistics (the reference copies the weight only, controller.py:330-332).
 
     ``input_shape`` (per sample) replaces the reference's peek at the first batch of
     ``train_loader``; either may be given. ``device`` is where the model runs ('cuda' as in the
@@ -151,6 +155,7 @@ class Controller:
     def _new_module(self, target, mod):
         from .layers import DOConv1d, DOConv2d, DOConv3d, DOLinear
         from .modules.activations import DOGELU, DOReLU_Variance, DOSiLU
+        from .modules.normalization import DOBatchNorm2d, DOSyncBatchNorm2d
 
         kw = dict(target_name=target, meta=self.meta)
         clamp = self.layer_clamp
@@ -161,6 +166,14 @@ class Controller:
                 next(c for c in (nn.Conv1d, nn.Conv2d, nn.Conv3d) if isinstance(mod, c))]
             new = cls(mod.in_channels, mod.out_channels, mod.kernel_size, mod.stride, mod.padding, mod.dilation,
                       mod.groups, mod.padding_mode, clamp_alpha=clamp, bias=mod.bias is not None, **kw)
+        elif isinstance(mod, _BATCHNORM):
+            if isinstance(mod, nn.SyncBatchNorm):
+                new = DOSyncBatchNorm2d(mod.num_features, mod.eps, mod.momentum, mod.affine, mod.track_running_stats,
+                                        mod.process_group, **kw)
+            else:
+                new = DOBatchNorm2d(mod.num_features, mod.eps, mod.momentum, mod.affine, mod.track_running_stats, **kw)
+            new.load_state_dict(mod.state_dict())
+            return new.to(self.device)
         elif isinstance(mod, nn.ReLU):
             new = DOReLU_Variance(inplace=False, relu=True, relu6=False, **kw)
         elif isinstance(mod, nn.SiLU):
@@ -189,7 +202,7 @@ class Controller:
                 bits = self._bits_for(target)
                 relu = isinstance(mod, nn.ReLU)
                 entry = {"tensor_meta": tm, "pack_only": relu, "bits": 1 if relu else bits}
-                entry.update(layer_group_meta(tm.shape, bits))
+                entry.update(layer_group_meta(tm.shape, bits, batchnorm=isinstance(mod, _BATCHNORM)))
                 if self.config.get("AVG_ALAM") is not None:
                     entry.update({"AVG_ALAM": self.config["AVG_ALAM"], "ALAM_BITS": self.config["AVG_ALAM_BTS"]})
                 else:

@@ -1,0 +1,489 @@
+// BatchNorm kernels for gfx950: per-channel statistics, normalize + quant-pack (plain, squashed
+// or fused with ReLU / ReLU6) and the backward pair (dequant + reduce, then the input gradient).
+//
+// Restates Activation_Compression/modules/normalization/kernel_implementation.py (the live
+// DOBatchNorm2d path) and Activation_Compression/triton_kernel/norm_act_fusion/bn_act_fusion.py
+// (the BatchNorm + ReLU fusion):
+//   stats     sum, sum of squares per channel (kernel_implementation.py:12-35)
+//   BN_NORM   y = x_hat * w + b and x_hat, both bf16; invstd from eps (:38-91)
+//   BN_QUANT  y, and x_hat squashed to 2 tanh(clamp(x_hat, -3, 3) / 2) quantized per group
+//             (:94-201)
+//   BN_RELU*  y = relu(x_hat * w + b) (or relu6), a 1-bit mask, x_hat quantized per group with
+//             no squash and codes (x_hat - min) / scale + (0.5 - 1e-6) (bn_act_fusion.py:8-118)
+//   backward  sum(dy [* mask]) and sum(dy [* mask] * x_hat') with x_hat' the dequantized codes
+//             (or the bf16 x_hat), then dx = (dy - db/M - x_hat' dw/M) w invstd (bf16)
+//             (kernel_implementation.py:204-481, bn_act_fusion.py:121-278)
+//
+// Floating-point order (the reference kernels compile with FMA contraction): mean = sum / M,
+// var = max(fma(-mean, mean, sumsq / M), 0), invstd = 1 / sqrt(var + eps) (IEEE division and
+// square root), x_hat = (x - mean) * invstd, y = fma(x_hat, w, b), codes trunc(fma(t - min,
+// 1/scale, 0.5 - 1e-6)) (squashed modes) or trunc((x_hat - min) / scale + (0.5 - 1e-6)) (ReLU
+// modes), x_hat' = fma(q, scale, min), dx = ((fma(-x_hat', dw/M, dy - db/M)) * w) * invstd.
+//
+// Mapping: a workgroup of 256 lanes covers 2048 consecutive elements of one channel, 8 per lane
+// (one 16-byte access for 2-byte types when HW is a multiple of 8, element by element
+// otherwise). A group of G elements spans G/8 aligned lanes (4..64), so group min/max and the
+// code merge stay inside a wave. Reductions are two-stage and ordered (workgroup partials, then
+// one thread per channel), so sums are deterministic and need no zeroed buffer or atomics.
+#include "bn_fused.h"
+#include "dopt_device.h"
+
+namespace dopt {
+namespace {
+
+constexpr int TPB = 256;
+constexpr int EPL = 8;
+constexpr int64_t WG_ELEMS = TPB * EPL;
+
+__device__ __forceinline__ int64_t bn_off(const BnGeom& g, int64_t c, int64_t e) {
+    const int64_t n = e / g.HW;
+    return n * g.stride_n + c * g.stride_c + (e - n * g.HW);
+}
+
+template <int DT>
+__device__ __forceinline__ float load1(const void* base, int64_t off) {
+    if constexpr (DT == DT_F32) return ((const float*)base)[off];
+    else if constexpr (DT == DT_BF16) return bf16_bits_to_f32(((const uint16_t*)base)[off]);
+    else return (float)__builtin_bit_cast(_Float16, ((const uint16_t*)base)[off]);
+}
+
+// 8 elements e0..e0+7 of channel c (VEC: one row, contiguous; else each bounded by M, 0 beyond)
+template <int DT, bool VEC>
+__device__ __forceinline__ void load8(const void* base, const BnGeom& g, int64_t c, int64_t e0, int64_t M,
+                                      float* v) {
+    if constexpr (VEC) {
+        const char* p = (const char*)base + bn_off(g, c, e0) * DType<DT>::bytes;
+        widen16<DT>(ld16<false>(p), v);
+        if constexpr (DT == DT_F32) widen16<DT>(ld16<false>(p + 16), v + 4);
+    } else {
+#pragma unroll
+        for (int k = 0; k < EPL; ++k) v[k] = (e0 + k < M) ? load1<DT>(base, bn_off(g, c, e0 + k)) : 0.0f;
+    }
+}
+
+template <bool VEC>
+__device__ __forceinline__ void store8_bf16(uint16_t* base, const BnGeom& g, int64_t c, int64_t e0, int64_t M,
+                                            const float* v) {
+    if constexpr (VEC) {
+        st16<false>(base + bn_off(g, c, e0), make_uint4(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]),
+                                                       pack_bf16x2(v[4], v[5]), pack_bf16x2(v[6], v[7])));
+    } else {
+#pragma unroll
+        for (int k = 0; k < EPL; ++k)
+            if (e0 + k < M) base[bn_off(g, c, e0 + k)] = to_bf16(v[k]);
+    }
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+    v += dpp_f32<0xB1>(v);
+    v += dpp_f32<0x4E>(v);
+    v += dpp_f32<0x141>(v);
+    v += dpp_f32<0x140>(v);
+    v += __shfl_xor(v, 16, 64);
+    v += __shfl_xor(v, 32, 64);
+    return v;
+}
+
+// sums of a and b over the workgroup, in lane 0 of wave 0 (fixed order: waves 0..3)
+__device__ __forceinline__ void block_sum2(float& a, float& b) {
+    __shared__ float red[2][TPB / 64];
+    a = wave_sum(a);
+    b = wave_sum(b);
+    const int w = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) {
+        red[0][w] = a;
+        red[1][w] = b;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        a = ((red[0][0] + red[0][1]) + red[0][2]) + red[0][3];
+        b = ((red[1][0] + red[1][1]) + red[1][2]) + red[1][3];
+    }
+}
+
+// min / max over aligned blocks of lpg lanes (lpg in 4..64, wave-uniform)
+__device__ __forceinline__ void group_minmax(float& mn, float& mx, int lpg) {
+    mn = fminf(mn, dpp_f32<0xB1>(mn));
+    mx = fmaxf(mx, dpp_f32<0xB1>(mx));
+    mn = fminf(mn, dpp_f32<0x4E>(mn));
+    mx = fmaxf(mx, dpp_f32<0x4E>(mx));
+    if (lpg >= 8) {
+        mn = fminf(mn, dpp_f32<0x141>(mn));
+        mx = fmaxf(mx, dpp_f32<0x141>(mx));
+    }
+    if (lpg >= 16) {
+        mn = fminf(mn, dpp_f32<0x140>(mn));
+        mx = fmaxf(mx, dpp_f32<0x140>(mx));
+    }
+    if (lpg >= 32) {
+        mn = fminf(mn, __shfl_xor(mn, 16, 64));
+        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    }
+    if (lpg >= 64) {
+        mn = fminf(mn, __shfl_xor(mn, 32, 64));
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    }
+}
+
+// Writes the lane's 8 codes (bits each) into the channel bitstream at element e0: 1-bit codes
+// merge over 4 lanes, 2-bit over 2, 4-bit fill one word, 8-bit two.
+__device__ __forceinline__ void store_codes(uint32_t* chan, int64_t e0, const int* q, int bits, bool active) {
+    const int lane = threadIdx.x & 63;
+    if (bits == 8) {
+        const uint32_t lo = (uint32_t)q[0] | ((uint32_t)q[1] << 8) | ((uint32_t)q[2] << 16) | ((uint32_t)q[3] << 24);
+        const uint32_t hi = (uint32_t)q[4] | ((uint32_t)q[5] << 8) | ((uint32_t)q[6] << 16) | ((uint32_t)q[7] << 24);
+        if (active) *(uint2*)(chan + e0 / 4) = make_uint2(lo, hi);
+        return;
+    }
+    uint32_t v = 0;
+#pragma unroll
+    for (int k = 0; k < EPL; ++k) v |= (uint32_t)q[k] << (k * bits);
+    if (bits == 4) {
+        if (active) chan[e0 / 8] = v;
+    } else if (bits == 2) {
+        v <<= 16 * (lane & 1);
+        v |= dpp_u32<0xB1>(v);
+        if (active && (lane & 1) == 0) chan[e0 / 16] = v;
+    } else {
+        v <<= 8 * (lane & 3);
+        v |= dpp_u32<0xB1>(v);
+        v |= dpp_u32<0x4E>(v);
+        if (active && (lane & 3) == 0) chan[e0 / 32] = v;
+    }
+}
+
+// 8 mask bits of a lane -> one word over 4 lanes
+__device__ __forceinline__ void store_mask(uint32_t* chan, int64_t e0, uint32_t m8, bool active) {
+    const int lane = threadIdx.x & 63;
+    uint32_t v = m8 << (8 * (lane & 3));
+    v |= dpp_u32<0xB1>(v);
+    v |= dpp_u32<0x4E>(v);
+    if (active && (lane & 3) == 0) chan[e0 / 32] = v;
+}
+
+// the lane's 8 codes read back from the channel bitstream
+__device__ __forceinline__ void load_codes(const uint32_t* chan, int64_t e0, int bits, int* q) {
+    if (bits == 8) {
+        const uint2 w = *(const uint2*)(chan + e0 / 4);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            q[k] = (w.x >> (8 * k)) & 0xff;
+            q[k + 4] = (w.y >> (8 * k)) & 0xff;
+        }
+        return;
+    }
+    const int64_t bit0 = e0 * bits;
+    const uint32_t w = chan[bit0 >> 5] >> (bit0 & 31);
+    const uint32_t qm = (1u << bits) - 1u;
+#pragma unroll
+    for (int k = 0; k < EPL; ++k) q[k] = (w >> (k * bits)) & qm;
+}
+
+// ------------------------------------------------------------------ statistics
+template <int DT, bool VEC>
+__global__ __launch_bounds__(TPB) void bn_stats_kernel(const void* __restrict__ x, BnGeom g,
+                                                       float* __restrict__ partial, int64_t nchunks) {
+    const int64_t c = blockIdx.y, chunk = blockIdx.x;
+    const int64_t M = g.N * g.HW;
+    const int64_t e_end = min(M, (chunk + 1) * BN_CHUNK);
+    float s = 0.0f, s2 = 0.0f;
+    for (int64_t e0 = chunk * BN_CHUNK + (int64_t)threadIdx.x * EPL; e0 < e_end; e0 += WG_ELEMS) {
+        float v[EPL];
+        load8<DT, VEC>(x, g, c, e0, M, v);
+#pragma unroll
+        for (int k = 0; k < EPL; ++k) {
+            s += v[k];
+            s2 = fmaf(v[k], v[k], s2);
+        }
+    }
+    block_sum2(s, s2);
+    if (threadIdx.x == 0) {
+        partial[c * nchunks + chunk] = s;
+        partial[(g.C + c) * nchunks + chunk] = s2;
+    }
+}
+
+// one thread per channel: the partials in chunk order
+__global__ __launch_bounds__(TPB) void bn_finalize_kernel(const float* __restrict__ partial, int64_t C,
+                                                          int64_t nchunks, float* __restrict__ out0,
+                                                          float* __restrict__ out1) {
+    const int64_t c = (int64_t)blockIdx.x * TPB + threadIdx.x;
+    if (c >= C) return;
+    float a = 0.0f, b = 0.0f;
+    for (int64_t k = 0; k < nchunks; ++k) {
+        a += partial[c * nchunks + k];
+        b += partial[(C + c) * nchunks + k];
+    }
+    out0[c] = a;
+    out1[c] = b;
+}
+
+// per-channel mean and inverse std as the forward kernels derive them
+__device__ __forceinline__ void channel_stats(const BnFwdArgs& a, int64_t c, int64_t M, float& mean, float& inv) {
+    if (a.sync) {
+        mean = a.mean_in[c];
+        inv = a.invstd_in[c];
+        return;
+    }
+    const float Mf = (float)M;
+    mean = a.sum[c] / Mf;
+    float var = fmaf(-mean, mean, a.sumsq[c] / Mf);
+    var = fmaxf(var, 0.0f);
+    inv = 1.0f / sqrtf(var + a.eps);
+    if (blockIdx.x == 0 && threadIdx.x == 0) {
+        a.mean_out[c] = mean;
+        a.var_out[c] = var;
+    }
+}
+
+// ------------------------------------------------------------------ forward
+template <int DT, int MODE, bool VEC>
+__global__ __launch_bounds__(TPB) void bn_fwd_kernel(BnFwdArgs a, int group, int bits, int relu6) {
+    const BnGeom g = a.g;
+    const int64_t c = blockIdx.y;
+    const int64_t M = g.N * g.HW;
+    const int64_t e0 = (int64_t)blockIdx.x * WG_ELEMS + (int64_t)threadIdx.x * EPL;
+    const bool active = e0 < M;
+    float mean, inv;
+    channel_stats(a, c, M, mean, inv);
+    const float w = a.w[c], b = a.b[c];
+
+    float v[EPL] = {};
+    if (active) load8<DT, VEC>(a.x, g, c, e0, M, v);
+    float xh[EPL], y[EPL];
+#pragma unroll
+    for (int k = 0; k < EPL; ++k) {
+        xh[k] = (v[k] - mean) * inv;
+        y[k] = fmaf(xh[k], w, b);
+    }
+    if constexpr (MODE == BN_NORM) {
+        if (active) {
+            store8_bf16<VEC>(a.y, g, c, e0, M, y);
+            store8_bf16<VEC>(a.xhat, g, c, e0, M, xh);
+        }
+        return;
+    } else {
+        uint32_t m8 = 0;
+        if constexpr (MODE == BN_RELU_QUANT) {
+#pragma unroll
+            for (int k = 0; k < EPL; ++k) {
+                const bool on = relu6 ? (y[k] > 0.0f && y[k] < 6.0f) : (y[k] > 0.0f);
+                m8 |= (uint32_t)on << k;
+                y[k] = relu6 ? fminf(fmaxf(y[k], 0.0f), 6.0f) : (on ? y[k] : 0.0f);
+            }
+        }
+        if (active) store8_bf16<VEC>(a.y, g, c, e0, M, y);
+        if constexpr (MODE == BN_RELU_QUANT) store_mask(a.relu_packed + c * (M / 32), e0, m8, active);
+
+        // values quantized: the squashed x_hat (BN_QUANT) or x_hat itself (ReLU modes)
+        float t[EPL];
+        float mn = __builtin_huge_valf(), mx = -__builtin_huge_valf();
+#pragma unroll
+        for (int k = 0; k < EPL; ++k) {
+            if constexpr (MODE == BN_QUANT) {
+                const float cl = fminf(fmaxf(xh[k], -3.0f), 3.0f);
+                t[k] = tanhf(cl * 0.5f) / 0.5f;
+            } else {
+                t[k] = xh[k];
+            }
+            if (active) {
+                mn = fminf(mn, t[k]);
+                mx = fmaxf(mx, t[k]);
+            }
+        }
+        const int lpg = group / EPL;
+        group_minmax(mn, mx, lpg);
+        const float qmaxf = (float)((1 << bits) - 1);
+        const float rng = mx - mn;
+        const float step = rng > 0.0f ? rng / qmaxf : 1.0f;
+        const float half_m = 0.49999899f;  // fp32(0.5 - 1e-6) = 0x3EFFFFDE
+        int q[EPL];
+        if constexpr (MODE == BN_QUANT) {
+            const float invs = 1.0f / step;
+#pragma unroll
+            for (int k = 0; k < EPL; ++k) {
+                const float qf = fminf(fmaxf(fmaf(t[k] - mn, invs, half_m), 0.0f), qmaxf);
+                q[k] = (int)qf;
+            }
+        } else {
+#pragma unroll
+            for (int k = 0; k < EPL; ++k) {
+                const float qf = fminf(fmaxf((t[k] - mn) / step + half_m, 0.0f), qmaxf);
+                q[k] = (int)qf;
+            }
+        }
+        store_codes(a.packed + c * (M * bits / 32), e0, q, bits, active);
+        if (active && ((threadIdx.x & 63) & (lpg - 1)) == 0) {
+            const int64_t gi = c * (M / group) + e0 / group;
+            a.scale[gi] = to_bf16(step);
+            a.minv[gi] = to_bf16(mn);
+        }
+    }
+}
+
+// ------------------------------------------------------------------ backward
+// x_hat' and dy (times the ReLU mask) of the lane's 8 elements
+template <int DYT, int MODE, bool VEC>
+__device__ __forceinline__ void bwd_operands(const BnBwdArgs& a, int64_t c, int64_t e0, int64_t M, int group,
+                                             int bits, float* xh, float* dy) {
+    load8<DYT, VEC>(a.dy, a.g, c, e0, M, dy);
+    if constexpr (MODE == BN_NORM) {
+        load8<DT_BF16, VEC>(a.xhat, a.g, c, e0, M, xh);
+    } else {
+        int q[EPL];
+        load_codes(a.packed + c * (M * bits / 32), e0, bits, q);
+        const int64_t gi = c * (M / group) + e0 / group;
+        const float sc = bf16_bits_to_f32(a.scale[gi]);
+        const float mn = bf16_bits_to_f32(a.minv[gi]);
+#pragma unroll
+        for (int k = 0; k < EPL; ++k) xh[k] = fmaf((float)q[k], sc, mn);
+        if constexpr (MODE == BN_RELU_QUANT) {
+            const uint32_t m = a.relu_packed[c * (M / 32) + e0 / 32] >> (e0 & 31);
+#pragma unroll
+            for (int k = 0; k < EPL; ++k) dy[k] = dy[k] * (float)((m >> k) & 1u);
+        }
+    }
+}
+
+template <int DYT, int MODE, bool VEC>
+__global__ __launch_bounds__(TPB) void bn_bwd_reduce_kernel(BnBwdArgs a, int group, int bits, int64_t nchunks) {
+    const int64_t c = blockIdx.y, chunk = blockIdx.x;
+    const int64_t M = a.g.N * a.g.HW;
+    const int64_t e_end = min(M, (chunk + 1) * BN_CHUNK);
+    float sdy = 0.0f, sdyx = 0.0f;
+    for (int64_t e0 = chunk * BN_CHUNK + (int64_t)threadIdx.x * EPL; e0 < e_end; e0 += WG_ELEMS) {
+        float xh[EPL], dy[EPL];
+        bwd_operands<DYT, MODE, VEC>(a, c, e0, M, group, bits, xh, dy);
+#pragma unroll
+        for (int k = 0; k < EPL; ++k) {
+            sdy += dy[k];
+            sdyx = fmaf(dy[k], xh[k], sdyx);
+        }
+    }
+    block_sum2(sdy, sdyx);
+    if (threadIdx.x == 0) {
+        a.partial[c * nchunks + chunk] = sdyx;            // -> dw
+        a.partial[(a.g.C + c) * nchunks + chunk] = sdy;   // -> db
+    }
+}
+
+template <int DYT, int MODE, bool VEC>
+__global__ __launch_bounds__(TPB) void bn_bwd_dx_kernel(BnBwdArgs a, int group, int bits) {
+    const int64_t c = blockIdx.y;
+    const int64_t M = a.g.N * a.g.HW;
+    const int64_t e0 = (int64_t)blockIdx.x * WG_ELEMS + (int64_t)threadIdx.x * EPL;
+    if (e0 >= M) return;
+    const float Mf = (float)M;
+    const float dwm = a.dw_in[c] / Mf, dbm = a.db_in[c] / Mf;
+    const float w = a.w[c];
+    const float inv = a.var_is_invstd ? a.var[c] : 1.0f / sqrtf(a.var[c] + a.eps);
+    float xh[EPL], dy[EPL], dx[EPL];
+    bwd_operands<DYT, MODE, VEC>(a, c, e0, M, group, bits, xh, dy);
+#pragma unroll
+    for (int k = 0; k < EPL; ++k) dx[k] = (fmaf(-xh[k], dwm, dy[k] - dbm) * w) * inv;
+    store8_bf16<VEC>(a.dx, a.g, c, e0, M, dx);
+}
+
+template <int DT>
+int fwd_dt(const BnFwdArgs& a, int mode, int group, int bits, bool vec, hipStream_t s) {
+    const int64_t M = a.g.N * a.g.HW;
+    const dim3 grid((unsigned)((M + WG_ELEMS - 1) / WG_ELEMS), (unsigned)a.g.C);
+    const int relu6 = mode == BN_RELU6_QUANT;
+#define DOPT_BN_FWD(MODE_, VEC_) hipLaunchKernelGGL((bn_fwd_kernel<DT, MODE_, VEC_>), grid, dim3(TPB), 0, s, a, group, bits, relu6)
+    if (mode == BN_NORM) {
+        if (vec) DOPT_BN_FWD(BN_NORM, true); else DOPT_BN_FWD(BN_NORM, false);
+    } else if (mode == BN_QUANT) {
+        if (vec) DOPT_BN_FWD(BN_QUANT, true); else DOPT_BN_FWD(BN_QUANT, false);
+    } else {
+        if (vec) DOPT_BN_FWD(BN_RELU_QUANT, true); else DOPT_BN_FWD(BN_RELU_QUANT, false);
+    }
+#undef DOPT_BN_FWD
+    return 0;
+}
+
+template <int DYT>
+int bwd_dt(const BnBwdArgs& a, int mode, int group, int bits, bool vec, bool reduce, hipStream_t s) {
+    const int64_t M = a.g.N * a.g.HW;
+    const int64_t nch = bn_nchunks(M);
+    const int m = mode == BN_RELU6_QUANT ? BN_RELU_QUANT : mode;
+    if (reduce) {
+        const dim3 grid((unsigned)nch, (unsigned)a.g.C);
+#define DOPT_BN_RED(MODE_, VEC_) hipLaunchKernelGGL((bn_bwd_reduce_kernel<DYT, MODE_, VEC_>), grid, dim3(TPB), 0, s, a, group, bits, nch)
+        if (nch == 0) {
+        } else if (m == BN_NORM) {
+            if (vec) DOPT_BN_RED(BN_NORM, true); else DOPT_BN_RED(BN_NORM, false);
+        } else if (m == BN_QUANT) {
+            if (vec) DOPT_BN_RED(BN_QUANT, true); else DOPT_BN_RED(BN_QUANT, false);
+        } else {
+            if (vec) DOPT_BN_RED(BN_RELU_QUANT, true); else DOPT_BN_RED(BN_RELU_QUANT, false);
+        }
+#undef DOPT_BN_RED
+        hipLaunchKernelGGL(bn_finalize_kernel, dim3((unsigned)((a.g.C + TPB - 1) / TPB)), dim3(TPB), 0, s,
+                           (const float*)a.partial, a.g.C, nch, a.dw, a.db);
+    } else {
+        const dim3 grid((unsigned)((M + WG_ELEMS - 1) / WG_ELEMS), (unsigned)a.g.C);
+#define DOPT_BN_DX(MODE_, VEC_) hipLaunchKernelGGL((bn_bwd_dx_kernel<DYT, MODE_, VEC_>), grid, dim3(TPB), 0, s, a, group, bits)
+        if (m == BN_NORM) {
+            if (vec) DOPT_BN_DX(BN_NORM, true); else DOPT_BN_DX(BN_NORM, false);
+        } else if (m == BN_QUANT) {
+            if (vec) DOPT_BN_DX(BN_QUANT, true); else DOPT_BN_DX(BN_QUANT, false);
+        } else {
+            if (vec) DOPT_BN_DX(BN_RELU_QUANT, true); else DOPT_BN_DX(BN_RELU_QUANT, false);
+        }
+#undef DOPT_BN_DX
+    }
+    return 0;
+}
+
+}  // namespace
+
+int64_t bn_nchunks(int64_t M) { return (M + BN_CHUNK - 1) / BN_CHUNK; }
+
+int launch_bn_reduce(const void* x, int dt, const BnGeom& g, float* partial, float* sum, float* sumsq, bool vec,
+                     hipStream_t s) {
+    const int64_t M = g.N * g.HW;
+    const int64_t nch = bn_nchunks(M);
+    const dim3 grid((unsigned)nch, (unsigned)g.C);
+#define DOPT_BN_STATS(DT_)                                                                                   \
+    do {                                                                                                     \
+        if (vec) hipLaunchKernelGGL((bn_stats_kernel<DT_, true>), grid, dim3(TPB), 0, s, x, g, partial, nch);  \
+        else hipLaunchKernelGGL((bn_stats_kernel<DT_, false>), grid, dim3(TPB), 0, s, x, g, partial, nch);     \
+    } while (0)
+    if (nch > 0) {
+        switch (dt) {
+            case DT_F32: DOPT_BN_STATS(DT_F32); break;
+            case DT_F16: DOPT_BN_STATS(DT_F16); break;
+            default: DOPT_BN_STATS(DT_BF16); break;
+        }
+    }
+#undef DOPT_BN_STATS
+    hipLaunchKernelGGL(bn_finalize_kernel, dim3((unsigned)((g.C + TPB - 1) / TPB)), dim3(TPB), 0, s,
+                       (const float*)partial, g.C, nch, sum, sumsq);
+    return 0;
+}
+
+int launch_bn_fwd(const BnFwdArgs& a, int dt, int mode, int group, int bits, bool vec, hipStream_t s) {
+    switch (dt) {
+        case DT_F32: return fwd_dt<DT_F32>(a, mode, group, bits, vec, s);
+        case DT_F16: return fwd_dt<DT_F16>(a, mode, group, bits, vec, s);
+        default: return fwd_dt<DT_BF16>(a, mode, group, bits, vec, s);
+    }
+}
+
+int launch_bn_bwd_reduce(const BnBwdArgs& a, int dyt, int mode, int group, int bits, bool vec, hipStream_t s) {
+    switch (dyt) {
+        case DT_F32: return bwd_dt<DT_F32>(a, mode, group, bits, vec, true, s);
+        case DT_F16: return bwd_dt<DT_F16>(a, mode, group, bits, vec, true, s);
+        default: return bwd_dt<DT_BF16>(a, mode, group, bits, vec, true, s);
+    }
+}
+
+int launch_bn_bwd_dx(const BnBwdArgs& a, int dyt, int mode, int group, int bits, bool vec, hipStream_t s) {
+    switch (dyt) {
+        case DT_F32: return bwd_dt<DT_F32>(a, mode, group, bits, vec, false, s);
+        case DT_F16: return bwd_dt<DT_F16>(a, mode, group, bits, vec, false, s);
+        default: return bwd_dt<DT_BF16>(a, mode, group, bits, vec, false, s);
+    }
+}
+
+}  // namespace dopt

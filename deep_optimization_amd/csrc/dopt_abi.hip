@@ -2,9 +2,11 @@
 // layout set-up and dispatch to the templated gfx950 kernels. No entry point allocates,
 // frees or synchronises; all work is enqueued on the caller's stream.
 #include <stdarg.h>
+#include <initializer_list>
 #include <stdio.h>
 
 #include "../../include/dopt.h"
+#include "bn_fused.h"
 #include "dequant_unpack.h"
 #include "quant_pack.h"
 
@@ -78,6 +80,47 @@ int setup_tiles(const int64_t* t, int64_t n_groups, int g, uint32_t* tiled, uint
     *tiles_w = (uint32_t)(W / s);
     *log2s = (uint32_t)ilog2(s);
     *row = (uint64_t)W;
+    return DOPT_OK;
+}
+
+// Validates a BatchNorm geometry; fills g and whether 16-byte vector access applies.
+int bn_geom(int64_t N, int64_t C, int64_t HW, int64_t stride_n, int64_t stride_c, dopt::BnGeom* g) {
+    if (N < 0 || C < 0 || HW < 0 || C > 65535)
+        return fail(DOPT_EINVAL, "BatchNorm shape must have N, HW >= 0 and 0 <= C <= 65535, got N=%lld C=%lld HW=%lld",
+                    (long long)N, (long long)C, (long long)HW);
+    if (N * HW >= ((int64_t)1 << 40)) return fail(DOPT_EINVAL, "BatchNorm channel too large: N*HW=%lld", (long long)(N * HW));
+    if (stride_n < 0 || stride_c < 0) return fail(DOPT_EINVAL, "BatchNorm strides must be non-negative");
+    *g = dopt::BnGeom{N, C, HW, stride_n, stride_c};
+    return DOPT_OK;
+}
+
+bool bn_vec(const dopt::BnGeom& g, std::initializer_list<const void*> ptrs) {
+    if (g.HW % 8 || g.stride_n % 8 || g.stride_c % 8) return false;
+    for (const void* p : ptrs)
+        if (p && !aligned16(p)) return false;
+    return true;
+}
+
+int bn_dtype(int dt, const char* what) {
+    if (dt != DOPT_F32 && dt != DOPT_F16 && dt != DOPT_BF16)
+        return fail(DOPT_EINVAL, "%s dtype must be F32, F16 or BF16, got code %d", what, dt);
+    return DOPT_OK;
+}
+
+int bn_quant_checks(int mode, int64_t M, int group_size, int bits, const void* packed, const void* scale,
+                    const void* minv, const void* relu_packed) {
+    int rc;
+    if (mode < DOPT_BN_NORM || mode > DOPT_BN_RELU6_QUANT) return fail(DOPT_EINVAL, "unknown BatchNorm mode %d", mode);
+    if (mode == DOPT_BN_NORM) return DOPT_OK;
+    if ((rc = check_bits(bits))) return rc;
+    if (group_size < 32 || group_size > 512 || (group_size & (group_size - 1)))
+        return fail(DOPT_EINVAL, "BatchNorm group_size must be a power of two in [32, 512], got %d", group_size);
+    if (M % group_size)
+        return fail(DOPT_EINVAL, "BatchNorm quant-pack needs N*HW %% group_size == 0 (N*HW=%lld, group_size=%d)",
+                    (long long)M, group_size);
+    if (!packed || !scale || !minv) return fail(DOPT_EINVAL, "null packed/scale/min pointer");
+    if ((uintptr_t)packed & 7u) return fail(DOPT_EINVAL, "packed must be 8-byte aligned");
+    if (mode != DOPT_BN_QUANT && !relu_packed) return fail(DOPT_EINVAL, "null relu_packed pointer");
     return DOPT_OK;
 }
 
@@ -336,6 +379,130 @@ int dopt_act_dequant_mul(const uint32_t* packed, const void* scale, const void* 
                                                        (hipStream_t)stream);
     if (rc) return fail(DOPT_EUNSUPPORTED, "no act_dequant_mul kernel for bits=%d g=%d", bits, group_size);
     return hip_status("act_dequant_mul launch");
+}
+
+int64_t dopt_bn_workspace_floats(int64_t N, int64_t C, int64_t HW) {
+    if (N < 0 || C < 0 || HW < 0) return 0;
+    return 2 * C * dopt::bn_nchunks(N * HW);
+}
+
+int dopt_bn_reduce(const void* x, int x_dtype, int64_t N, int64_t C, int64_t HW, int64_t stride_n, int64_t stride_c,
+                   float* workspace, float* sum, float* sumsq, void* stream) {
+    int rc;
+    dopt::BnGeom g;
+    if ((rc = bn_geom(N, C, HW, stride_n, stride_c, &g))) return rc;
+    if ((rc = bn_dtype(x_dtype, "bn_reduce: x"))) return rc;
+    if (C == 0) return ok();
+    if (!sum || !sumsq || (N * HW > 0 && (!x || !workspace))) return fail(DOPT_EINVAL, "null pointer argument");
+    (void)hipGetLastError();
+    dopt::launch_bn_reduce(x, x_dtype, g, workspace, sum, sumsq, bn_vec(g, {x}), (hipStream_t)stream);
+    return hip_status("bn_reduce launch");
+}
+
+int dopt_bn_norm_quant(const void* x, int x_dtype, int64_t N, int64_t C, int64_t HW, int64_t stride_n,
+                       int64_t stride_c, const float* sum, const float* sumsq, const float* mean_in,
+                       const float* invstd_in, int sync, const float* weight, const float* bias, float eps, int mode,
+                       int group_size, int bits, void* y, void* x_hat, uint32_t* packed, uint32_t* relu_packed,
+                       void* scale, void* minv, float* mean_out, float* var_out, void* stream) {
+    int rc;
+    dopt::BnGeom g;
+    if ((rc = bn_geom(N, C, HW, stride_n, stride_c, &g))) return rc;
+    if ((rc = bn_dtype(x_dtype, "bn_norm_quant: x"))) return rc;
+    const int64_t M = N * HW;
+    if ((rc = bn_quant_checks(mode, M, group_size, bits, packed, scale, minv, relu_packed))) return rc;
+    if (C == 0 || M == 0) return ok();
+    if (!x || !y || !weight || !bias) return fail(DOPT_EINVAL, "null x/y/weight/bias pointer");
+    if (sync ? (!mean_in || !invstd_in) : (!sum || !sumsq || !mean_out || !var_out))
+        return fail(DOPT_EINVAL, "null statistics pointer (sync=%d)", sync);
+    if (mode == DOPT_BN_NORM && !x_hat) return fail(DOPT_EINVAL, "null x_hat pointer");
+    dopt::BnFwdArgs a{};
+    a.g = g;
+    a.x = x;
+    a.sum = sum;
+    a.sumsq = sumsq;
+    a.mean_in = mean_in;
+    a.invstd_in = invstd_in;
+    a.w = weight;
+    a.b = bias;
+    a.eps = eps;
+    a.sync = sync != 0;
+    a.y = (uint16_t*)y;
+    a.xhat = (uint16_t*)x_hat;
+    a.packed = packed;
+    a.relu_packed = relu_packed;
+    a.scale = (uint16_t*)scale;
+    a.minv = (uint16_t*)minv;
+    a.mean_out = mean_out;
+    a.var_out = var_out;
+    (void)hipGetLastError();
+    dopt::launch_bn_fwd(a, x_dtype, mode, group_size, bits, bn_vec(g, {x, y, x_hat}), (hipStream_t)stream);
+    return hip_status("bn_norm_quant launch");
+}
+
+int dopt_bn_bwd_reduce(int mode, const void* x_hat, const uint32_t* packed, const uint32_t* relu_packed,
+                       const void* scale, const void* minv, const void* dy, int dy_dtype, int64_t N, int64_t C,
+                       int64_t HW, int64_t stride_n, int64_t stride_c, int group_size, int bits, float* workspace,
+                       float* dweight, float* dbias, void* stream) {
+    int rc;
+    dopt::BnGeom g;
+    if ((rc = bn_geom(N, C, HW, stride_n, stride_c, &g))) return rc;
+    if ((rc = bn_dtype(dy_dtype, "bn_bwd_reduce: dy"))) return rc;
+    const int64_t M = N * HW;
+    if ((rc = bn_quant_checks(mode, M, group_size, bits, packed, scale, minv, relu_packed))) return rc;
+    if (C == 0) return ok();
+    if (!dweight || !dbias) return fail(DOPT_EINVAL, "null dweight/dbias pointer");
+    if (M > 0 && (!dy || !workspace || (mode == DOPT_BN_NORM && !x_hat)))
+        return fail(DOPT_EINVAL, "null dy/workspace/x_hat pointer");
+    dopt::BnBwdArgs a{};
+    a.g = g;
+    a.xhat = (const uint16_t*)x_hat;
+    a.packed = packed;
+    a.relu_packed = relu_packed;
+    a.scale = (const uint16_t*)scale;
+    a.minv = (const uint16_t*)minv;
+    a.dy = dy;
+    a.partial = workspace;
+    a.dw = dweight;
+    a.db = dbias;
+    (void)hipGetLastError();
+    dopt::launch_bn_bwd_reduce(a, dy_dtype, mode, group_size, bits,
+                               bn_vec(g, {dy, mode == DOPT_BN_NORM ? x_hat : nullptr}), (hipStream_t)stream);
+    return hip_status("bn_bwd_reduce launch");
+}
+
+int dopt_bn_bwd_dx(int mode, const void* x_hat, const uint32_t* packed, const uint32_t* relu_packed,
+                   const void* scale, const void* minv, const void* dy, int dy_dtype, int64_t N, int64_t C, int64_t HW,
+                   int64_t stride_n, int64_t stride_c, int group_size, int bits, const float* dweight,
+                   const float* dbias, const float* weight, const float* var, float eps, int var_is_invstd, void* dx,
+                   void* stream) {
+    int rc;
+    dopt::BnGeom g;
+    if ((rc = bn_geom(N, C, HW, stride_n, stride_c, &g))) return rc;
+    if ((rc = bn_dtype(dy_dtype, "bn_bwd_dx: dy"))) return rc;
+    const int64_t M = N * HW;
+    if ((rc = bn_quant_checks(mode, M, group_size, bits, packed, scale, minv, relu_packed))) return rc;
+    if (C == 0 || M == 0) return ok();
+    if (!dy || !dx || !dweight || !dbias || !weight || !var || (mode == DOPT_BN_NORM && !x_hat))
+        return fail(DOPT_EINVAL, "null pointer argument");
+    dopt::BnBwdArgs a{};
+    a.g = g;
+    a.xhat = (const uint16_t*)x_hat;
+    a.packed = packed;
+    a.relu_packed = relu_packed;
+    a.scale = (const uint16_t*)scale;
+    a.minv = (const uint16_t*)minv;
+    a.dy = dy;
+    a.dw_in = dweight;
+    a.db_in = dbias;
+    a.w = weight;
+    a.var = var;
+    a.eps = eps;
+    a.var_is_invstd = var_is_invstd != 0;
+    a.dx = (uint16_t*)dx;
+    (void)hipGetLastError();
+    dopt::launch_bn_bwd_dx(a, dy_dtype, mode, group_size, bits,
+                           bn_vec(g, {dy, dx, mode == DOPT_BN_NORM ? x_hat : nullptr}), (hipStream_t)stream);
+    return hip_status("bn_bwd_dx launch");
 }
 
 }  // extern "C"

@@ -188,6 +188,64 @@ int dopt_act_dequant_mul(const uint32_t* packed, const void* scale, const void* 
                          int group_size, int bits, const int64_t* tile_nchw, const void* dy, int dy_dtype, void* dx,
                          void* stream);
 
+/* ---------------------------------------------------------------- BatchNorm
+ * An activation [N, C, HW] with element strides (stride_n, stride_c, 1): channel c is the flat
+ * sequence e = n*HW + s of M = N*HW elements. Every element tensor of a call (x, y, x_hat, dy,
+ * dx) has that geometry; all of them 16-byte aligned. Per channel, groups are runs of group_size
+ * consecutive elements, and
+ *   packed       uint32 [C, M*bits/32]   the little-endian code bitstream of the channel
+ *   relu_packed  uint32 [C, M/32]        bit e = ReLU mask of element e
+ *   scale, minv  bf16   [C, M/group_size]
+ * Sums are two-stage (per-workgroup partials in `workspace`, then per channel in a fixed order):
+ * deterministic, no atomics, nothing to zero. `workspace` holds dopt_bn_workspace_floats() floats.
+ *
+ * Modes: */
+#define DOPT_BN_NORM 0        /* y, x_hat (bf16), kernel_implementation.py:38-91 */
+#define DOPT_BN_QUANT 1       /* y, codes of 2 tanh(clamp(x_hat, -3, 3)/2), kernel_implementation.py:94-201 */
+#define DOPT_BN_RELU_QUANT 2  /* relu(y), mask, codes of x_hat, bn_act_fusion.py:8-118 */
+#define DOPT_BN_RELU6_QUANT 3 /* min(max(y, 0), 6), mask 0 < y < 6, codes of x_hat */
+
+/* Floats of workspace the BatchNorm reductions need for this shape. */
+int64_t dopt_bn_workspace_floats(int64_t N, int64_t C, int64_t HW);
+
+/* sum[c], sumsq[c] over the channel (fp32). Replaces act_lib::bn_fwd_reduce
+ * (AC/modules/normalization/kernel_registration.py:13-39, kernel_implementation.py:12-35). */
+int dopt_bn_reduce(const void* x, int x_dtype, int64_t N, int64_t C, int64_t HW, int64_t stride_n, int64_t stride_c,
+                   float* workspace, float* sum, float* sumsq, void* stream);
+
+/* Normalize (+ ReLU) (+ quant-pack). sync = 0: mean = sum/M, var = max(fma(-mean, mean, sumsq/M), 0),
+ * invstd = 1/sqrt(var + eps), mean_out/var_out written; sync = 1: mean_in and invstd_in are used
+ * (SyncBatchNorm). x_hat = (x - mean)*invstd, y = fma(x_hat, weight, bias) -> bf16.
+ * DOPT_BN_QUANT codes: t = 2 tanh(clamp(x_hat, -3, 3)/2), q = trunc(fma(t - min, 1/scale, 0.5-1e-6));
+ * ReLU modes: q = trunc((x_hat - min)/scale + (0.5-1e-6)); scale = (max-min)/QMAX or 1.
+ * M % group_size == 0 for the quant modes. Replaces act_lib::bn_fwd_norm (kernel_registration.py:42-80),
+ * act_lib::bn_fwd_norm_quant_pack_fused (:83-150) and act_lib::bn_relu_fwd_norm_fused_quant_pack
+ * (AC/triton_kernel/norm_act_fusion/kernel_registration.py:19-74). */
+int dopt_bn_norm_quant(const void* x, int x_dtype, int64_t N, int64_t C, int64_t HW, int64_t stride_n,
+                       int64_t stride_c, const float* sum, const float* sumsq, const float* mean_in,
+                       const float* invstd_in, int sync, const float* weight, const float* bias, float eps, int mode,
+                       int group_size, int bits, void* y, void* x_hat, uint32_t* packed, uint32_t* relu_packed,
+                       void* scale, void* minv, float* mean_out, float* var_out, void* stream);
+
+/* dweight[c] = sum(dy*m * x_hat'), dbias[c] = sum(dy*m), with x_hat' = fma(q, scale, min) (or the bf16
+ * x_hat for DOPT_BN_NORM) and m the ReLU mask (ReLU modes) or 1. Replaces act_lib::bn_bwd_reduce
+ * (kernel_registration.py:153-178), act_lib::bn_bwd_reduce_dequant_unpack_fused (:211-240) and
+ * act_lib::bn_relu_bwd_reduce_fused_dequant_unpack (norm_act_fusion/kernel_registration.py:77-119). */
+int dopt_bn_bwd_reduce(int mode, const void* x_hat, const uint32_t* packed, const uint32_t* relu_packed,
+                       const void* scale, const void* minv, const void* dy, int dy_dtype, int64_t N, int64_t C,
+                       int64_t HW, int64_t stride_n, int64_t stride_c, int group_size, int bits, float* workspace,
+                       float* dweight, float* dbias, void* stream);
+
+/* dx = (fma(-x_hat', dweight/M, dy*m - dbias/M) * weight) * invstd -> bf16, invstd = var_is_invstd ? var :
+ * 1/sqrt(var + eps). Replaces act_lib::bn_bwd_dx (kernel_registration.py:181-208),
+ * act_lib::bn_bwd_dx_dequant_unpack_fused (:243-276) and act_lib::bn_relu_bwd_dx_fused_dequant_unpack
+ * (norm_act_fusion/kernel_registration.py:122-166). */
+int dopt_bn_bwd_dx(int mode, const void* x_hat, const uint32_t* packed, const uint32_t* relu_packed,
+                   const void* scale, const void* minv, const void* dy, int dy_dtype, int64_t N, int64_t C, int64_t HW,
+                   int64_t stride_n, int64_t stride_c, int group_size, int bits, const float* dweight,
+                   const float* dbias, const float* weight, const float* var, float eps, int var_is_invstd, void* dx,
+                   void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -73,6 +73,17 @@ def lib():
         L.oracle_act_quant_pack.restype = i32
         L.oracle_act_dequant_mul.argtypes = [vp, vp, vp, i32, i64, i32, i32, vp, vp, i32, vp]
         L.oracle_act_dequant_mul.restype = i32
+        f32 = ctypes.c_float
+        L.oracle_bn_reduce.argtypes = [vp, i32, i64, i64, i64, i64, i64, vp, vp]
+        L.oracle_bn_reduce.restype = i32
+        L.oracle_bn_norm_quant.argtypes = [vp, i32, i64, i64, i64, i64, i64, vp, vp, vp, vp, i32, vp, vp, f32, i32,
+                                           i32, i32, vp, vp, vp, vp, vp, vp, vp, vp, vp]
+        L.oracle_bn_norm_quant.restype = i32
+        L.oracle_bn_bwd_reduce.argtypes = [i32, vp, vp, vp, vp, vp, vp, i32, i64, i64, i64, i64, i64, i32, i32, vp, vp]
+        L.oracle_bn_bwd_reduce.restype = i32
+        L.oracle_bn_bwd_dx.argtypes = [i32, vp, vp, vp, vp, vp, vp, i32, i64, i64, i64, i64, i64, i32, i32, vp, vp,
+                                       vp, vp, f32, i32, vp]
+        L.oracle_bn_bwd_dx.restype = i32
         _lib = L
     return _lib
 
@@ -232,6 +243,88 @@ def act_dequant_mul(packed, scale, mn, group_size: int, bits: int, dy: np.ndarra
     _check(lib().oracle_act_dequant_mul(_ptr(packed), _ptr(np.ascontiguousarray(scale)), _ptr(np.ascontiguousarray(mn)),
                                         meta_dtype, ng, group_size, bits, _ptr(tile), _ptr(dy), _dtype_code(dy),
                                         _ptr(dx)))
+    return dx
+
+
+BN_NORM, BN_QUANT, BN_RELU_QUANT, BN_RELU6_QUANT = 0, 1, 2, 3
+
+
+def _bn_geom(x: np.ndarray):
+    """[N, C, *spatial] contiguous -> (N, C, HW, stride_n, stride_c)."""
+    N, C = int(x.shape[0]), int(x.shape[1])
+    HW = int(np.prod(x.shape[2:], dtype=np.int64)) if x.ndim > 2 else 1
+    return N, C, HW, C * HW, HW
+
+
+def bn_reduce(x: np.ndarray):
+    """-> (sum, sumsq) float64 [C] over each channel of a contiguous [N, C, ...] array."""
+    x = np.ascontiguousarray(x)
+    N, C, HW, sn, sc = _bn_geom(x)
+    s, q = np.zeros(C), np.zeros(C)
+    _check(lib().oracle_bn_reduce(_ptr(x), _dtype_code(x), N, C, HW, sn, sc, _ptr(s), _ptr(q)))
+    return s, q
+
+
+def bn_norm_quant(x: np.ndarray, weight, bias, *, mode, group_size=0, bits=2, eps=1e-5, sum=None, sumsq=None,
+                  mean=None, invstd=None):
+    """Normalize (+ ReLU) (+ quant-pack) of a contiguous [N, C, ...] array. Statistics: fp32 sum /
+    sumsq (non-sync) or fp32 mean / invstd (sync). Returns a dict with y (bf16 bits, x's shape),
+    x_hat (BN_NORM), packed [C, M*bits/32], relu_packed [C, M/32], scale / min (bf16 bits
+    [C, M/g]), mean / var (non-sync) and t (fp32 [C, M], the quantized values)."""
+    x = np.ascontiguousarray(x)
+    N, C, HW, sn, sc = _bn_geom(x)
+    M = N * HW
+    sync = mean is not None
+    f = lambda a: None if a is None else np.ascontiguousarray(a, dtype=np.float32)  # noqa: E731
+    w, b = f(weight), f(bias)
+    sum, sumsq, mean, invstd = f(sum), f(sumsq), f(mean), f(invstd)
+    out = {"y": np.zeros(x.shape, dtype=np.uint16)}
+    quant = mode != BN_NORM
+    out["x_hat"] = np.zeros(x.shape, dtype=np.uint16) if not quant else None
+    out["packed"] = np.zeros((C, M * bits // 32), dtype=np.uint32) if quant else None
+    out["relu_packed"] = np.zeros((C, M // 32), dtype=np.uint32) if mode in (BN_RELU_QUANT, BN_RELU6_QUANT) else None
+    ng = M // group_size if quant else 0
+    out["scale"] = np.zeros((C, ng), dtype=np.uint16) if quant else None
+    out["min"] = np.zeros((C, ng), dtype=np.uint16) if quant else None
+    out["mean"] = np.zeros(C, dtype=np.float32)
+    out["var"] = np.zeros(C, dtype=np.float32)
+    out["t"] = np.zeros((C, M), dtype=np.float32) if quant else None
+    _check(lib().oracle_bn_norm_quant(_ptr(x), _dtype_code(x), N, C, HW, sn, sc, _ptr(sum), _ptr(sumsq), _ptr(mean),
+                                      _ptr(invstd), int(sync), _ptr(w), _ptr(b), float(eps), mode, group_size, bits,
+                                      _ptr(out["y"]), _ptr(out["x_hat"]), _ptr(out["packed"]),
+                                      _ptr(out["relu_packed"]), _ptr(out["scale"]), _ptr(out["min"]),
+                                      _ptr(out["mean"]), _ptr(out["var"]), _ptr(out["t"])))
+    return out
+
+
+def _bn_bwd_args(mode, x_hat, packed, relu_packed, scale, mn, dy):
+    c = lambda a, dt: None if a is None else np.ascontiguousarray(a, dtype=dt)  # noqa: E731
+    return (c(x_hat, np.uint16), c(packed, np.uint32), c(relu_packed, np.uint32), c(scale, np.uint16),
+            c(mn, np.uint16), np.ascontiguousarray(dy))
+
+
+def bn_bwd_reduce(dy: np.ndarray, *, mode, x_hat=None, packed=None, relu_packed=None, scale=None, min=None,
+                  group_size=0, bits=2):
+    """-> (dweight, dbias) float64 [C]: sum(dy*m * x_hat'), sum(dy*m)."""
+    xh, p, rp, s, mn, dy = _bn_bwd_args(mode, x_hat, packed, relu_packed, scale, min, dy)
+    N, C, HW, sn, sc = _bn_geom(dy)
+    dw, db = np.zeros(C), np.zeros(C)
+    _check(lib().oracle_bn_bwd_reduce(mode, _ptr(xh), _ptr(p), _ptr(rp), _ptr(s), _ptr(mn), _ptr(dy), _dtype_code(dy),
+                                      N, C, HW, sn, sc, group_size, bits, _ptr(dw), _ptr(db)))
+    return dw, db
+
+
+def bn_bwd_dx(dy: np.ndarray, dweight, dbias, weight, var, *, mode, eps=1e-7, var_is_invstd=False, x_hat=None,
+              packed=None, relu_packed=None, scale=None, min=None, group_size=0, bits=2):
+    """-> dx as bf16 bits (uint16), dy's shape; dweight / dbias / weight / var fp32 [C]."""
+    xh, p, rp, s, mn, dy = _bn_bwd_args(mode, x_hat, packed, relu_packed, scale, min, dy)
+    N, C, HW, sn, sc = _bn_geom(dy)
+    f = lambda a: np.ascontiguousarray(a, dtype=np.float32)  # noqa: E731
+    dw, db, w, v = f(dweight), f(dbias), f(weight), f(var)
+    dx = np.zeros(dy.shape, dtype=np.uint16)
+    _check(lib().oracle_bn_bwd_dx(mode, _ptr(xh), _ptr(p), _ptr(rp), _ptr(s), _ptr(mn), _ptr(dy), _dtype_code(dy), N,
+                                  C, HW, sn, sc, group_size, bits, _ptr(dw), _ptr(db), _ptr(w), _ptr(v), float(eps),
+                                  int(var_is_invstd), _ptr(dx)))
     return dx
 
 

@@ -37,6 +37,13 @@
  *   fused activation quant-pack    pinned: equals the quantizer above applied to the squashed
  *                                  derivative with the range floored at 1e-4
  *   fused activation backward      pinned: closed form bf16(dy * dequant)
+ *   BatchNorm statistics           pinned: float64 sums; the normalization against torch's float64
+ *                                  batch_norm (mean, biased variance, eps, affine)
+ *   BatchNorm codes / mask / pack  pinned: known-answer ramps through the sync path (mean 0,
+ *                                  invstd 1 makes x_hat = x), the pinned quantizer applied to the
+ *                                  quantized values (squashed mode), bounds |x_hat' - t| <= scale/2
+ *   BatchNorm squash (2 tanh(x/2)) parity unpinned at bit level (libdevice tanh in the reference)
+ *   BatchNorm backward             pinned: against torch's float64 batch_norm autograd on x_hat
  */
 #include <math.h>
 #include <stdint.h>
@@ -516,6 +523,209 @@ int oracle_act_dequant_mul(const uint32_t* packed, const void* scale, const void
             int64_t o = elem_index(r, e, g, tile_nchw, s);
             float act = fmaf((float)qv, sc, mn);
             dx[o] = f32_to_bf16(load_elem(dy, dy_dtype, o) * act);
+        }
+    }
+    return O_OK;
+}
+
+/* ---------------------------------------------------------------- BatchNorm
+ * AC/modules/normalization/kernel_implementation.py (DOBatchNorm2d's kernels) and
+ * AC/triton_kernel/norm_act_fusion/bn_act_fusion.py (BatchNorm + ReLU). Channel c is the flat
+ * sequence e = n*HW + s (offset n*stride_n + c*stride_c + s); groups are runs of g consecutive
+ * elements of a channel; packed [C, M*bits/32], relu_packed [C, M/32], scale/min bf16 [C, M/g].
+ * The statistics here are double-precision sums (the GPU's fp32 sums differ only in rounding
+ * order; the tests compare them with a tolerance and feed the GPU's sums back in), everything
+ * downstream of them is the kernels' fp32 operation sequence. */
+#define O_BN_NORM 0
+#define O_BN_QUANT 1
+#define O_BN_RELU_QUANT 2
+#define O_BN_RELU6_QUANT 3
+
+static int64_t bn_off(int64_t HW, int64_t sn, int64_t sc, int64_t c, int64_t e) {
+    int64_t n = e / HW;
+    return n * sn + c * sc + (e - n * HW);
+}
+
+/* sum and sum of squares per channel (kernel_implementation.py:12-35), in double */
+int oracle_bn_reduce(const void* x, int x_dtype, int64_t N, int64_t C, int64_t HW, int64_t sn, int64_t sc,
+                     double* sum, double* sumsq) {
+    if (N < 0 || C < 0 || HW < 0) return O_EINVAL;
+    const int64_t M = N * HW;
+#pragma omp parallel for schedule(static)
+    for (int64_t c = 0; c < C; ++c) {
+        double a = 0.0, b = 0.0;
+        for (int64_t e = 0; e < M; ++e) {
+            double v = load_elem(x, x_dtype, bn_off(HW, sn, sc, c, e));
+            a += v;
+            b += v * v;
+        }
+        sum[c] = a;
+        sumsq[c] = b;
+    }
+    return O_OK;
+}
+
+/* Normalize (+ ReLU) (+ quant-pack), one fp32 rounding per operation:
+ *   mean = sum/M; var = max(fma(-mean, mean, sumsq/M), 0); invstd = 1/sqrtf(var + eps)
+ *     (kernel_implementation.py:66-71, :138-143; bn_act_fusion.py:55-60), or mean_in / invstd_in (sync)
+ *   x_hat = (x - mean)*invstd; y = fma(x_hat, w, b) (:76-77, :150-151)
+ *   BN_NORM: y, x_hat -> bf16 (:78-79)
+ *   BN_QUANT: t = tanhf(clamp(x_hat, -3, 3)*0.5)/0.5 (:155-156); per group min/max,
+ *     scale = rng > 0 ? rng/QMAX : 1, inv = 1/scale, q = trunc(fma(t - min, inv, 0.5-1e-6)),
+ *     clamped to [0, QMAX] (:157-177)
+ *   BN_RELU*: m = y > 0 (relu6: 0 < y < 6); y = m ? y : 0 (relu6: min(max(y, 0), 6)); codes of
+ *     t = x_hat with q = trunc((t - min)/scale + (0.5-1e-6)) (bn_act_fusion.py:63-101)
+ *   t_out (optional, fp32 [C, M]): the values the codes quantize */
+int oracle_bn_norm_quant(const void* x, int x_dtype, int64_t N, int64_t C, int64_t HW, int64_t sn, int64_t sc,
+                         const float* sum, const float* sumsq, const float* mean_in, const float* invstd_in,
+                         int sync, const float* w, const float* b, float eps, int mode, int g, int bits,
+                         uint16_t* y, uint16_t* x_hat, uint32_t* packed, uint32_t* relu_packed, uint16_t* scale,
+                         uint16_t* minv, float* mean_out, float* var_out, float* t_out) {
+    if (N < 0 || C < 0 || HW < 0 || mode < 0 || mode > 3) return O_EINVAL;
+    const int64_t M = N * HW;
+    if (mode != O_BN_NORM) {
+        if (bits != 1 && bits != 2 && bits != 4 && bits != 8) return O_EBITS;
+        if (g < 32 || g > 512 || (g & (g - 1)) || M % g) return O_EINVAL;
+    }
+    const int QMAX = (1 << bits) - 1;
+    const float qmaxf = (float)QMAX;
+    const float half_m = (float)(0.5 - 1e-6);
+    const int64_t TW = M * bits / 32, NG = mode == O_BN_NORM ? 0 : M / g;
+#pragma omp parallel
+    {
+        float* t = (float*)malloc(sizeof(float) * (g > 0 ? g : 1));
+#pragma omp for schedule(static)
+        for (int64_t c = 0; c < C; ++c) {
+            float mean, inv;
+            if (sync) {
+                mean = mean_in[c];
+                inv = invstd_in[c];
+            } else {
+                const float Mf = (float)M;
+                mean = sum[c] / Mf;
+                float var = fmaf(-mean, mean, sumsq[c] / Mf);
+                var = fmaxf(var, 0.0f);
+                inv = 1.0f / sqrtf(var + eps);
+                mean_out[c] = mean;
+                var_out[c] = var;
+            }
+            const float wc = w[c], bc = b[c];
+            if (mode == O_BN_NORM) {
+                for (int64_t e = 0; e < M; ++e) {
+                    const int64_t o = bn_off(HW, sn, sc, c, e);
+                    float xh = (load_elem(x, x_dtype, o) - mean) * inv;
+                    y[o] = f32_to_bf16(fmaf(xh, wc, bc));
+                    x_hat[o] = f32_to_bf16(xh);
+                }
+                continue;
+            }
+            if (mode != O_BN_QUANT)
+                for (int64_t k = 0; k < M / 32; ++k) relu_packed[c * (M / 32) + k] = 0;
+            for (int64_t r = 0; r < NG; ++r) {
+                float mn = INFINITY, mx = -INFINITY;
+                for (int e = 0; e < g; ++e) {
+                    const int64_t ee = r * g + e;
+                    const int64_t o = bn_off(HW, sn, sc, c, ee);
+                    float xh = (load_elem(x, x_dtype, o) - mean) * inv;
+                    float yv = fmaf(xh, wc, bc);
+                    if (mode == O_BN_QUANT) {
+                        float cl = fminf(fmaxf(xh, -3.0f), 3.0f);
+                        t[e] = tanhf(cl * 0.5f) / 0.5f;
+                    } else {
+                        int m = mode == O_BN_RELU6_QUANT ? (yv > 0.0f && yv < 6.0f) : (yv > 0.0f);
+                        relu_packed[c * (M / 32) + ee / 32] |= (uint32_t)m << (ee % 32);
+                        yv = mode == O_BN_RELU6_QUANT ? fminf(fmaxf(yv, 0.0f), 6.0f) : (m ? yv : 0.0f);
+                        t[e] = xh;
+                    }
+                    y[o] = f32_to_bf16(yv);
+                    if (t_out) t_out[c * M + ee] = t[e];
+                    mn = fminf(mn, t[e]);
+                    mx = fmaxf(mx, t[e]);
+                }
+                float rng = mx - mn;
+                float step = rng > 0.0f ? rng / qmaxf : 1.0f;
+                float invs = 1.0f / step;
+                uint32_t* words = packed + c * TW + r * (g * bits / 32);
+                for (int k = 0; k < g * bits / 32; ++k) words[k] = 0;
+                for (int e = 0; e < g; ++e) {
+                    float qf = mode == O_BN_QUANT ? fmaf(t[e] - mn, invs, half_m) : (t[e] - mn) / step + half_m;
+                    if (qf != qf) qf = 0.0f;
+                    qf = fminf(fmaxf(qf, 0.0f), qmaxf);
+                    int q = (int)qf;
+                    words[(e * bits) / 32] |= (uint32_t)q << ((e * bits) % 32);
+                }
+                scale[c * NG + r] = f32_to_bf16(step);
+                minv[c * NG + r] = f32_to_bf16(mn);
+            }
+        }
+        free(t);
+    }
+    return O_OK;
+}
+
+/* x_hat' and dy*m of element e of channel c for the backward (kernel_implementation.py:392-403,
+ * :463-470; bn_act_fusion.py:160-172, :247-255): x_hat' = fma(q, scale, min) or the bf16 x_hat */
+static void bn_bwd_elem(int mode, const uint16_t* x_hat, const uint32_t* packed, const uint32_t* relu_packed,
+                        const uint16_t* scale, const uint16_t* minv, const void* dy, int dy_dtype, int64_t M,
+                        int64_t HW, int64_t sn, int64_t sc, int g, int bits, int64_t c, int64_t e, float* xh,
+                        float* dyv) {
+    const int64_t o = bn_off(HW, sn, sc, c, e);
+    float d = load_elem(dy, dy_dtype, o);
+    if (mode == O_BN_NORM) {
+        *xh = bf16_to_f32(x_hat[o]);
+    } else {
+        const int64_t bit = e * bits;
+        uint32_t q = (packed[c * (M * bits / 32) + bit / 32] >> (bit % 32)) & ((1u << bits) - 1u);
+        const int64_t gi = c * (M / g) + e / g;
+        *xh = fmaf((float)q, bf16_to_f32(scale[gi]), bf16_to_f32(minv[gi]));
+        if (mode != O_BN_QUANT) {
+            uint32_t m = (relu_packed[c * (M / 32) + e / 32] >> (e % 32)) & 1u;
+            d = d * (float)m;
+        }
+    }
+    *dyv = d;
+}
+
+/* dweight = sum(dy*m * x_hat'), dbias = sum(dy*m) per channel, in double */
+int oracle_bn_bwd_reduce(int mode, const uint16_t* x_hat, const uint32_t* packed, const uint32_t* relu_packed,
+                         const uint16_t* scale, const uint16_t* minv, const void* dy, int dy_dtype, int64_t N,
+                         int64_t C, int64_t HW, int64_t sn, int64_t sc, int g, int bits, double* dw, double* db) {
+    if (N < 0 || C < 0 || HW < 0 || mode < 0 || mode > 3) return O_EINVAL;
+    const int64_t M = N * HW;
+#pragma omp parallel for schedule(static)
+    for (int64_t c = 0; c < C; ++c) {
+        double a = 0.0, s = 0.0;
+        for (int64_t e = 0; e < M; ++e) {
+            float xh, d;
+            bn_bwd_elem(mode, x_hat, packed, relu_packed, scale, minv, dy, dy_dtype, M, HW, sn, sc, g, bits, c, e,
+                        &xh, &d);
+            a += (double)d * (double)xh;
+            s += d;
+        }
+        dw[c] = a;
+        db[c] = s;
+    }
+    return O_OK;
+}
+
+/* dx = ((fma(-x_hat', dw/M, dy*m - db/M)) * w) * invstd -> bf16, invstd = var_is_invstd ? var :
+ * 1/sqrtf(var + eps) (kernel_implementation.py:252-255, :471-481; bn_act_fusion.py:256-278) */
+int oracle_bn_bwd_dx(int mode, const uint16_t* x_hat, const uint32_t* packed, const uint32_t* relu_packed,
+                     const uint16_t* scale, const uint16_t* minv, const void* dy, int dy_dtype, int64_t N, int64_t C,
+                     int64_t HW, int64_t sn, int64_t sc, int g, int bits, const float* dw, const float* db,
+                     const float* w, const float* var, float eps, int var_is_invstd, uint16_t* dx) {
+    if (N < 0 || C < 0 || HW < 0 || mode < 0 || mode > 3) return O_EINVAL;
+    const int64_t M = N * HW;
+    const float Mf = (float)M;
+#pragma omp parallel for schedule(static)
+    for (int64_t c = 0; c < C; ++c) {
+        const float dwm = dw[c] / Mf, dbm = db[c] / Mf, wc = w[c];
+        const float inv = var_is_invstd ? var[c] : 1.0f / sqrtf(var[c] + eps);
+        for (int64_t e = 0; e < M; ++e) {
+            float xh, d;
+            bn_bwd_elem(mode, x_hat, packed, relu_packed, scale, minv, dy, dy_dtype, M, HW, sn, sc, g, bits, c, e,
+                        &xh, &d);
+            dx[bn_off(HW, sn, sc, c, e)] = f32_to_bf16((fmaf(-xh, dwm, d - dbm) * wc) * inv);
         }
     }
     return O_OK;

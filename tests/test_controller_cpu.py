@@ -15,6 +15,7 @@ from torch import nn
 from deep_optimization_amd.controller import Controller
 from deep_optimization_amd.layers import DOConv1d, DOConv2d, DOConv3d, DOLinear
 from deep_optimization_amd.modules.activations import DOGELU, DOReLU_Variance, DOSiLU
+from deep_optimization_amd.modules.normalization import DOBatchNorm2d
 from deep_optimization_amd.vit import vit_base_patch16_224
 
 
@@ -98,21 +99,22 @@ def test_cnn_relu_mask_only_and_bits_override():
     c = Controller(model, {"batch_size": 32, "default_bits": 2, "bits": {"conv2": 4}}, input_shape=(3, 64, 64),
                    device="cpu")
     c.warp_model()
-    # outputs: conv1 / bn1 / relu / conv2 / silu [32, 32, 64, 64] bf16 = 8 MiB (bf16) -> not selected;
-    # at batch 32 nothing exceeds 10 MiB except the fp32 BatchNorm output (16 MiB), which is not a
-    # selected type here.
+    # outputs: conv1 / bn1 / relu / conv2 / silu [32, 32, 64, 64] bf16 = 8 MiB -> none selected
     assert _targets(c) == []
     c = Controller(_Cnn(), {"batch_size": 64, "default_bits": 2, "bits": {"conv2": 4}}, input_shape=(3, 64, 64),
                    device="cpu")
     c.warp_model()
-    assert _targets(c) == ["act1", "act2", "conv1", "conv2"]
+    assert _targets(c) == ["act1", "act2", "bn1", "conv1", "conv2"]
     assert c.meta["act1"]["pack_only"] and c.meta["act1"]["bits"] == 1
+    # BatchNorm groups per channel: S = N*H*W = 64*64*64 = 256 * 1024, N = C = 32
+    m = c.meta["bn1"]
+    assert (m["group_size"], m["act_padding"], m["N"], m["NG"]) == (1024, False, 32, 32 * 256)
     assert c.meta["conv2"]["bits"] == 4 and c.meta["act2"]["bits"] == 2
     mods = dict(c.traced_model.named_modules())
     assert type(mods["act1"]) is DOReLU_Variance and type(mods["act2"]) is DOSiLU
     assert type(mods["conv2"]) is DOConv2d and mods["conv2"].padding_mode == "reflect"
     assert mods["conv1"].bias is None and mods["conv2"].bias is not None
-    assert type(mods["bn1"]) is nn.BatchNorm2d  # BatchNorm is not rewritten (no DOBatchNorm2d yet)
+    assert type(mods["bn1"]) is DOBatchNorm2d and mods["bn1"].target_name == "bn1"
 
 
 def test_eval_forward_equals_original():
@@ -133,7 +135,7 @@ def test_quantizer_false_traces_without_swapping():
     c = Controller(_Cnn(), {"batch_size": 64, "default_bits": 2}, input_shape=(3, 64, 64), device="cpu")
     tm = c.warp_model(quantizer=False)
     assert not any(isinstance(m, (DOLinear, DOConv2d, DOReLU_Variance)) for m in tm.modules())
-    assert set(c.target_dict) == {"act1", "act2", "conv1", "conv2"}
+    assert set(c.target_dict) == {"act1", "act2", "bn1", "conv1", "conv2"}
 
 
 def test_conv_layers_construct_like_torch():
@@ -157,3 +159,34 @@ def test_controller_needs_an_input_shape():
     loader = [(torch.zeros(4, 3, 64, 64), torch.zeros(4, dtype=torch.long))]
     c = Controller(_Cnn(), {"batch_size": 4, "default_bits": 2}, train_loader=loader, device="cpu")
     assert c.input_shape == (3, 64, 64)
+
+
+def test_batchnorm_swap_keeps_state_and_fuse_bn_act():
+    from deep_optimization_amd.fusion import DOBatchNormReLU2d, fuse_bn_act
+
+    torch.manual_seed(4)
+    model = _Cnn()
+    with torch.no_grad():
+        model.bn1.weight.uniform_(0.5, 1.5)
+        model.bn1.bias.uniform_(-0.5, 0.5)
+        model.bn1.running_mean.uniform_(-1, 1)
+        model.bn1.running_var.uniform_(0.5, 2)
+    ref = {k: v.clone() for k, v in model.bn1.state_dict().items()}
+    x = torch.randn(2, 3, 64, 64)
+    model.eval()
+    with torch.no_grad():
+        want = model(x)
+    c = Controller(model, {"batch_size": 64, "default_bits": 2}, input_shape=(3, 64, 64), device="cpu")
+    tm = c.warp_model()
+    for k, v in ref.items():
+        assert torch.equal(tm.bn1.state_dict()[k], v), k
+    fused = fuse_bn_act(tm)
+    mods = dict(fused.named_modules())
+    assert type(mods["bn1_bnact"]) is DOBatchNormReLU2d and "bn1" not in mods and "act1" not in mods
+    assert "bn1_bnact" in c.meta and "bn1" not in c.meta
+    assert mods["bn1_bnact"].target_name == "bn1_bnact" and c.meta["bn1_bnact"]["group_size"] == 1024
+    for k, v in ref.items():
+        assert torch.equal(mods["bn1_bnact"].state_dict()[k], v), k
+    fused.eval()
+    with torch.no_grad():
+        torch.testing.assert_close(fused(x), want, rtol=0, atol=0)

@@ -1,0 +1,289 @@
+"""GPU parity of the BatchNorm kernels (statistics, normalize + quant-pack, backward reduce and
+input gradient) against the CPU oracle, through the act_lib operators -> the C ABI.
+
+Bar:
+  * sums (forward statistics, backward dweight / dbias): fp32 reductions in a fixed order, within
+    1e-5 of the sum of the terms' magnitudes (a bound of fp32 summation error) of the float64
+    oracle sums;
+  * everything downstream of the sums, given the GPU's sums: bit-exact (mean, var, y, x_hat,
+    ReLU mask, codes, scale, min, dx), except the squashed mode's codes, which go through tanh
+    (libdevice in the reference, ocml here, the C library in the oracle): within one code on under
+    1% of the elements, scale and min within one bf16 ulp.
+Shapes cover the 16-byte path (HW a multiple of 8) and the element path (HW = 49, 196), group
+sizes 32..512 (BLOCK_M 64..1024), bits 1/2/4/8, bf16 / fp32 / fp16 inputs, and the sync path.
+"""
+import numpy as np
+import pytest
+import torch
+
+import deep_optimization_amd  # noqa: F401
+import oracle
+from deep_optimization_amd.fusion import DOBatchNormReLU2d
+from deep_optimization_amd.modules.normalization import DOBatchNorm2d
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+ops = torch.ops.act_lib
+
+
+def npv(t):
+    t = t.detach().cpu().contiguous()
+    if t.dtype in (torch.bfloat16,):
+        return t.view(torch.int16).numpy().view(np.uint16)
+    if t.dtype == torch.float16:
+        return t.numpy()
+    if t.dtype == torch.int32:
+        return t.numpy().view(np.uint32)
+    return t.numpy()
+
+
+def make(shape, dtype, seed, shift=0.5, scale=1.7):
+    g = torch.Generator().manual_seed(seed)
+    x = (torch.randn(shape, generator=g) * scale + shift).to(dtype)
+    C = shape[1]
+    w = torch.rand(C, generator=g) + 0.5
+    b = torch.randn(C, generator=g) * 0.3
+    return x, w, b
+
+
+def geo(x):
+    N, C = x.shape[0], x.shape[1]
+    HW = x.numel() // (N * C)
+    return dict(M=N * HW, HW=HW, stride_n=C * HW, stride_c=HW)
+
+
+def codes_of(packed, bits):
+    """codes of a little-endian code bitstream (numpy.unpackbits)"""
+    b = np.unpackbits(np.ascontiguousarray(packed).reshape(-1).view(np.uint8), bitorder="little")
+    return (b.reshape(-1, bits).astype(np.int64) << np.arange(bits)).sum(axis=1)
+
+
+def sums_close(got, want_f64, mag):
+    return np.all(np.abs(got.astype(np.float64) - want_f64) <= 1e-5 * mag + 1e-30)
+
+
+def check_stats(x, s, q):
+    rs, rq = oracle.bn_reduce(npv(x))
+    xa = np.abs(npv(x).astype(np.float32) if x.dtype != torch.bfloat16 else oracle.bf16_bits_to_f32(npv(x)))
+    mag = xa.astype(np.float64).sum(axis=tuple(i for i in range(xa.ndim) if i != 1))
+    mag2 = (xa.astype(np.float64) ** 2).sum(axis=tuple(i for i in range(xa.ndim) if i != 1))
+    assert sums_close(npv(s), rs, mag)
+    assert sums_close(npv(q), rq, mag2)
+
+
+SHAPES = [(4, 16, 16, 16), (8, 32, 14, 14), (16, 8, 7, 7), (32, 16, 28, 28)]
+DTYPES = [torch.bfloat16, torch.float32, torch.float16]
+
+
+@pytest.mark.parametrize("shape", SHAPES, ids=lambda s: "x".join(map(str, s)))
+@pytest.mark.parametrize("dtype", DTYPES, ids=["bf16", "f32", "f16"])
+def test_reduce_and_plain_normalize(shape, dtype):
+    x, w, b = make(shape, dtype, 1)
+    xd = x.to(DEV)
+    g = geo(x)
+    s, q = ops.bn_fwd_reduce(xd.view(shape[0], shape[1], -1), **g, BLOCK_M=256, num_warps=8, num_stages=5)
+    torch.cuda.synchronize()
+    check_stats(x, s, q)
+    y, xh, mean, var = ops.bn_fwd_norm(xd.view(shape[0], shape[1], -1), s, q, w.to(DEV), b.to(DEV), None, None, **g,
+                                       BLOCK_M=256, sync=False, num_warps=8, num_stages=5)
+    ref = oracle.bn_norm_quant(npv(x), w.numpy(), b.numpy(), mode=oracle.BN_NORM, eps=1e-7, sum=npv(s),
+                               sumsq=npv(q))
+    np.testing.assert_array_equal(npv(mean), ref["mean"])
+    np.testing.assert_array_equal(npv(var), ref["var"])
+    np.testing.assert_array_equal(npv(y).reshape(-1), ref["y"].reshape(-1))
+    np.testing.assert_array_equal(npv(xh).reshape(-1), ref["x_hat"].reshape(-1))
+
+
+# (shape, BLOCK_M): M = N*HW is a multiple of the group BLOCK_M // 2
+QCASES = [((4, 16, 16, 16), 64), ((4, 16, 16, 16), 1024), ((8, 32, 14, 14), 64), ((16, 32, 14, 14), 128),
+          ((32, 16, 28, 28), 512), ((32, 8, 7, 7), 64)]
+
+
+@pytest.mark.parametrize("case", QCASES, ids=lambda c: "x".join(map(str, c[0])) + f"-B{c[1]}")
+@pytest.mark.parametrize("bits", [1, 2, 4, 8])
+@pytest.mark.parametrize("mode", ["relu", "relu6", "squash"])
+def test_fused_forward_and_backward(case, bits, mode):
+    shape, BLOCK = case
+    dtype = torch.bfloat16 if bits != 4 else torch.float32
+    x, w, b = make(shape, dtype, 100 + bits)
+    N, C = shape[0], shape[1]
+    g = geo(x)
+    x3 = x.to(DEV).view(N, C, -1)
+    wd, bd = w.to(DEV), b.to(DEV)
+    s, q = ops.bn_fwd_reduce(x3, **g, BLOCK_M=BLOCK, num_warps=8, num_stages=5)
+    if mode == "squash":
+        y, packed, scale, xmin, mean, var = ops.bn_fwd_norm_quant_pack_fused(
+            x3, s, q, wd, bd, None, None, **g, BLOCK_M=BLOCK, bits=bits, sync=False, avg_alam=False, alam_bits=0,
+            num_warps=8, num_stages=5)
+        rp = None
+        omode = oracle.BN_QUANT
+    else:
+        y, packed, rp, scale, xmin, mean, var = ops.bn_relu_fwd_norm_fused_quant_pack(
+            x3, s, q, wd, bd, None, None, **g, relu=mode == "relu", relu6=mode == "relu6", BLOCK_SIZE=BLOCK,
+            BITS=bits, sync=False)
+        omode = oracle.BN_RELU_QUANT if mode == "relu" else oracle.BN_RELU6_QUANT
+    torch.cuda.synchronize()
+    check_stats(x, s, q)
+    grp = BLOCK // 2
+    ref = oracle.bn_norm_quant(npv(x), w.numpy(), b.numpy(), mode=omode, group_size=grp, bits=bits, eps=1e-5,
+                               sum=npv(s), sumsq=npv(q))
+    np.testing.assert_array_equal(npv(mean), ref["mean"])
+    np.testing.assert_array_equal(npv(var), ref["var"])
+    np.testing.assert_array_equal(npv(y).reshape(-1), ref["y"].reshape(-1))
+    if rp is not None:
+        np.testing.assert_array_equal(npv(rp), ref["relu_packed"])
+    if mode == "squash":
+        d = np.abs(codes_of(npv(packed), bits) - codes_of(ref["packed"], bits))
+        assert d.max() <= 1 and (d > 0).mean() < 0.01
+        for a, r in ((npv(scale), ref["scale"]), (npv(xmin), ref["min"])):
+            assert np.abs(a.astype(np.int64) - r.astype(np.int64)).max() <= 1
+    else:
+        np.testing.assert_array_equal(npv(packed), ref["packed"])
+        np.testing.assert_array_equal(npv(scale), ref["scale"])
+        np.testing.assert_array_equal(npv(xmin), ref["min"])
+
+    # backward on the GPU's own saved tensors
+    gdy = torch.Generator().manual_seed(7)
+    dy = torch.randn(shape, generator=gdy).to(torch.bfloat16)
+    dy3 = dy.to(DEV).view(N, C, -1)
+    if mode == "squash":
+        dw, db = ops.bn_bwd_reduce_dequant_unpack_fused(packed, dy3, scale, xmin, **g, BLOCK_M=BLOCK, bits=bits,
+                                                        avg_alam=False, alam_bits=0)
+        dx = ops.bn_bwd_dx_dequant_unpack_fused(packed, dy3, scale, xmin, dw, db, wd, var, **g, BLOCK_M=BLOCK,
+                                                bits=bits, sync=False, avg_alam=False, alam_bits=0)
+        eps = 1e-7
+    else:
+        dw, db = ops.bn_relu_bwd_reduce_fused_dequant_unpack(packed, rp, dy3, scale, xmin, **g, BLOCK_SIZE=BLOCK,
+                                                             BITS=bits)
+        dx = ops.bn_relu_bwd_dx_fused_dequant_unpack(packed, rp, dy3, dw, db, wd, var, scale, xmin, **g,
+                                                     BLOCK_SIZE=BLOCK, BITS=bits)
+        eps = 1e-5
+    torch.cuda.synchronize()
+    kw = dict(mode=omode, packed=npv(packed), relu_packed=None if rp is None else npv(rp), scale=npv(scale),
+              min=npv(xmin), group_size=grp, bits=bits)
+    rdw, rdb = oracle.bn_bwd_reduce(npv(dy), **kw)
+    dyf = np.abs(oracle.bf16_bits_to_f32(npv(dy))).astype(np.float64)
+    assert sums_close(npv(db), rdb, dyf.sum(axis=(0, 2, 3)))
+    assert sums_close(npv(dw), rdw, 8.0 * dyf.sum(axis=(0, 2, 3)))  # |x_hat'| < 8 for this data
+    rdx = oracle.bn_bwd_dx(npv(dy), npv(dw), npv(db), w.numpy(), npv(var), eps=eps, **kw)
+    np.testing.assert_array_equal(npv(dx).reshape(-1), rdx.reshape(-1))
+
+
+@pytest.mark.parametrize("mode", ["plain", "squash", "relu"])
+def test_sync_path_bit_exact(mode):
+    shape = (8, 16, 14, 14)
+    x, w, b = make(shape, torch.bfloat16, 9)
+    N, C = shape[0], shape[1]
+    g = geo(x)
+    gen = torch.Generator().manual_seed(3)
+    mean = torch.randn(C, generator=gen) * 0.3
+    inv = torch.rand(C, generator=gen) + 0.5
+    x3 = x.to(DEV).view(N, C, -1)
+    args = (x3, None, None, w.to(DEV), b.to(DEV), mean.to(DEV), inv.to(DEV))
+    if mode == "plain":
+        y, xh, mo, vo = ops.bn_fwd_norm(*args, **g, BLOCK_M=64, sync=True, num_warps=8, num_stages=5)
+        assert mo is None and vo is None
+        ref = oracle.bn_norm_quant(npv(x), w.numpy(), b.numpy(), mode=oracle.BN_NORM, mean=mean.numpy(),
+                                   invstd=inv.numpy())
+        np.testing.assert_array_equal(npv(xh).reshape(-1), ref["x_hat"].reshape(-1))
+        # backward with the inverse std in place of the variance
+        dy = torch.randn(shape, generator=gen).to(torch.bfloat16)
+        dy3 = dy.to(DEV).view(N, C, -1)
+        dg, dbt = ops.bn_bwd_reduce(xh, dy3, **g, BLOCK_M=64, num_warps=8, num_stages=5)
+        dx = ops.bn_bwd_dx(xh, dy3, inv.to(DEV), w.to(DEV), dbt, dg, **g, BLOCK_M=64, sync=True, num_warps=8,
+                           num_stages=5)
+        rdx = oracle.bn_bwd_dx(npv(dy), npv(dg), npv(dbt), w.numpy(), inv.numpy(), mode=oracle.BN_NORM,
+                               var_is_invstd=True, x_hat=npv(xh))
+        np.testing.assert_array_equal(npv(dx).reshape(-1), rdx.reshape(-1))
+    elif mode == "squash":
+        y, packed, scale, xmin, mo, vo = ops.bn_fwd_norm_quant_pack_fused(
+            *args, **g, BLOCK_M=64, bits=2, sync=True, avg_alam=False, alam_bits=0, num_warps=8, num_stages=5)
+        ref = oracle.bn_norm_quant(npv(x), w.numpy(), b.numpy(), mode=oracle.BN_QUANT, group_size=32, bits=2,
+                                   mean=mean.numpy(), invstd=inv.numpy())
+    else:
+        y, packed, rp, scale, xmin, mo, vo = ops.bn_relu_fwd_norm_fused_quant_pack(
+            *args, **g, relu=True, relu6=False, BLOCK_SIZE=64, BITS=2, sync=True)
+        ref = oracle.bn_norm_quant(npv(x), w.numpy(), b.numpy(), mode=oracle.BN_RELU_QUANT, group_size=32, bits=2,
+                                   mean=mean.numpy(), invstd=inv.numpy())
+        np.testing.assert_array_equal(npv(packed), ref["packed"])
+        np.testing.assert_array_equal(npv(rp), ref["relu_packed"])
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(npv(y).reshape(-1), ref["y"].reshape(-1))
+
+
+def test_errors():
+    x = torch.randn(2, 4, 10, 10, device=DEV).to(torch.bfloat16)
+    x3 = x.view(2, 4, 100)
+    g = geo(x)
+    s, q = ops.bn_fwd_reduce(x3, **g, BLOCK_M=64, num_warps=8, num_stages=5)
+    w = torch.ones(4, device=DEV)
+    with pytest.raises(RuntimeError, match="group_size == 0"):  # M = 200 is not a multiple of 32
+        ops.bn_fwd_norm_quant_pack_fused(x3, s, q, w, w, None, None, **g, BLOCK_M=64, bits=2, sync=False,
+                                         avg_alam=False, alam_bits=0, num_warps=8, num_stages=5)
+    with pytest.raises(ValueError):
+        ops.bn_relu_fwd_norm_fused_quant_pack(x3, s, q, w, w, None, None, **g, relu=True, relu6=False, BLOCK_SIZE=64,
+                                              BITS=3, sync=False)
+    with pytest.raises(NotImplementedError):
+        ops.bn_fwd_norm_quant_pack_fused(x3, s, q, w, w, None, None, **g, BLOCK_M=64, bits=2, sync=False,
+                                         avg_alam=True, alam_bits=2, num_warps=8, num_stages=5)
+
+
+# ----------------------------------------------------------------------------- layers
+def _layer_case(layer_cls, shape, BLOCK, act_padding=False, **kw):
+    torch.manual_seed(11)
+    C = shape[1]
+    meta = {"bn": {"group_size": BLOCK, "bits": 2, "act_padding": act_padding, "AVG_ALAM": False, "ALAM_BITS": 0,
+                   "pack_only": False, "N": C, "DIVISION": None}}
+    layer = layer_cls(C, target_name="bn", meta=meta, **kw).to(DEV).train()
+    ref = torch.nn.BatchNorm2d(C).to(DEV).train()
+    with torch.no_grad():
+        layer.weight.uniform_(0.5, 1.5)
+        layer.bias.uniform_(-0.5, 0.5)
+        ref.load_state_dict(layer.state_dict())
+    x = (torch.randn(shape, device=DEV) * 1.5 + 0.3).requires_grad_(True)
+    return layer, ref, x, meta
+
+
+@pytest.mark.parametrize("act_padding", [False, True])
+def test_do_batchnorm2d_layer(act_padding):
+    shape = (8, 16, 28, 28)
+    layer, ref, x, meta = _layer_case(DOBatchNorm2d, shape, 256, act_padding)
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        y = layer(x)
+    yr = ref(x.detach().float().requires_grad_(True))
+    assert y.dtype == torch.bfloat16
+    torch.testing.assert_close(y.float(), yr, rtol=2 ** -7, atol=2e-2)
+    # running statistics: the reference's update with the biased batch variance
+    xd = x.detach().double()
+    var_b = xd.var(dim=(0, 2, 3), unbiased=False)
+    torch.testing.assert_close(layer.running_mean.double(), 0.1 * xd.mean(dim=(0, 2, 3)), rtol=1e-5, atol=1e-6)
+    torch.testing.assert_close(layer.running_var.double(), 0.9 + 0.1 * var_b, rtol=1e-5, atol=1e-6)
+    assert int(layer.num_batches_tracked) == 1
+    dy = torch.randn_like(y)
+    y.backward(dy)
+    assert layer.weight.grad.dtype == torch.float32 and torch.isfinite(x.grad).all()
+    # the gradient follows the saved, squashed and quantized x_hat: close to exact BN's in direction
+    xr = x.detach().float().requires_grad_(True)
+    ref.zero_grad()
+    ref(xr).backward(dy.float())
+    cos = torch.nn.functional.cosine_similarity(x.grad.float().flatten(), xr.grad.flatten(), dim=0)
+    assert cos > 0.9, float(cos)
+    torch.testing.assert_close(layer.bias.grad, ref.bias.grad, rtol=1e-3, atol=1e-3)
+
+
+def test_do_batchnorm_relu_layer():
+    shape = (8, 16, 28, 28)
+    layer, ref, x, meta = _layer_case(DOBatchNormReLU2d, shape, 256)
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        y = layer(x)
+    yr = torch.relu(ref(x.detach().float()))
+    torch.testing.assert_close(y.float(), yr, rtol=2 ** -7, atol=2e-2)
+    dy = torch.randn_like(y)
+    y.backward(dy)
+    xr = x.detach().float().requires_grad_(True)
+    ref.zero_grad()
+    torch.relu(ref(xr)).backward(dy.float())
+    cos = torch.nn.functional.cosine_similarity(x.grad.float().flatten(), xr.grad.flatten(), dim=0)
+    assert cos > 0.9, float(cos)
+    # dbias = sum(dy * mask) exactly as autograd's (the mask is y > 0 on the same fp32 y)
+    torch.testing.assert_close(layer.bias.grad, ref.bias.grad, rtol=1e-3, atol=1e-2)

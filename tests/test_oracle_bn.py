@@ -1,0 +1,186 @@
+"""Pins the BatchNorm part of the CPU oracle (oracle_bn_*) before it is trusted as the checker
+of the HIP kernels.
+
+  * normalization: against torch's float64 batch_norm (training statistics: mean, biased
+    variance, eps inside the square root, affine), and the backward against torch's float64
+    autograd of batch_norm;
+  * codes, ReLU mask and packing: known answers through the sync path (mean 0, invstd 1 makes
+    x_hat = x exactly): integer ramps whose codes have the closed form round(x * QMAX / 31), no
+    value lying near a rounding boundary; the packed words from numpy.packbits;
+  * the squashed mode equals the already pinned quantizer (oracle_quant_pack, nearest, bf16
+    scale/min) applied per channel to the values it quantizes;
+  * the ReLU modes' division form keeps |x_hat' - x_hat| <= scale/2 and is monotone.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+
+
+def bf16(a):
+    return oracle.bf16_bits_to_f32(a).astype(np.float64)
+
+
+def rnd(shape, seed, scale=1.0, shift=0.0):
+    r = np.random.default_rng(seed)
+    return (r.standard_normal(shape) * scale + shift).astype(np.float32)
+
+
+def stats32(x):
+    s, q = oracle.bn_reduce(x)
+    return s.astype(np.float32), q.astype(np.float32)
+
+
+@pytest.mark.parametrize("shape", [(4, 8, 6, 6), (3, 5, 7, 9), (16, 4, 8, 8)])
+def test_normalize_matches_torch_float64(shape):
+    x = rnd(shape, 1, scale=2.0, shift=0.7)
+    C = shape[1]
+    w, b = rnd((C,), 2), rnd((C,), 3)
+    s, q = oracle.bn_reduce(x)
+    xd = x.astype(np.float64)
+    np.testing.assert_allclose(s, xd.sum(axis=(0, 2, 3)), rtol=1e-12)
+    np.testing.assert_allclose(q, (xd ** 2).sum(axis=(0, 2, 3)), rtol=1e-12)
+    out = oracle.bn_norm_quant(x, w, b, mode=oracle.BN_NORM, eps=1e-5, sum=s.astype(np.float32),
+                               sumsq=q.astype(np.float32))
+    mean = xd.mean(axis=(0, 2, 3))
+    var = xd.var(axis=(0, 2, 3))  # biased, as the kernels compute it
+    np.testing.assert_allclose(out["mean"], mean, rtol=1e-6, atol=1e-6)
+    np.testing.assert_allclose(out["var"], var, rtol=1e-5, atol=1e-6)
+    want = torch.nn.functional.batch_norm(torch.from_numpy(xd), None, None, torch.from_numpy(w.astype(np.float64)),
+                                          torch.from_numpy(b.astype(np.float64)), training=True, eps=1e-5).numpy()
+    y = bf16(out["y"])
+    assert np.all(np.abs(y - want) <= 2.0 ** -8 * np.abs(want) + 2e-5)
+    xh_want = (xd - mean[None, :, None, None]) / np.sqrt(var + 1e-5)[None, :, None, None]
+    assert np.all(np.abs(bf16(out["x_hat"]) - xh_want) <= 2.0 ** -8 * np.abs(xh_want) + 2e-5)
+
+
+def _sync(x, bits, mode, g, w=None, b=None):
+    C = x.shape[1]
+    w = np.ones(C, np.float32) if w is None else w
+    b = np.zeros(C, np.float32) if b is None else b
+    return oracle.bn_norm_quant(x, w, b, mode=mode, group_size=g, bits=bits, mean=np.zeros(C, np.float32),
+                                invstd=np.ones(C, np.float32))
+
+
+def _packbits(codes, bits):
+    """little-endian bitstream of codes (numpy.packbits over the per-code bit planes)"""
+    planes = ((codes[:, None] >> np.arange(bits)[None, :]) & 1).astype(np.uint8).reshape(-1)
+    return np.packbits(planes, bitorder="little").view(np.uint32)
+
+
+@pytest.mark.parametrize("bits", [1, 2, 4, 8])
+@pytest.mark.parametrize("mode", [oracle.BN_RELU_QUANT, oracle.BN_RELU6_QUANT])
+def test_relu_modes_known_answer_ramp(bits, mode):
+    # one channel, two groups of 32: the ramp 0..31 and the same ramp minus 16 (mask bits vary)
+    ramp = np.arange(32, dtype=np.float32)
+    x = np.concatenate([ramp, ramp - 16.0]).reshape(1, 1, 64)
+    out = _sync(x, bits, mode, 32)
+    qmax = (1 << bits) - 1
+    want_q = np.floor(ramp.astype(np.float64) * qmax / 31 + 0.5).astype(np.uint32)
+    codes = np.concatenate([want_q, want_q])
+    np.testing.assert_array_equal(out["packed"].reshape(-1), _packbits(codes, bits))
+    np.testing.assert_array_equal(bf16(out["scale"]).reshape(-1), bf16(oracle.f32_to_bf16_bits(
+        np.full(2, np.float32(31.0) / np.float32(qmax)))))
+    np.testing.assert_array_equal(bf16(out["min"]).reshape(-1), [0.0, -16.0])
+    xv = x.reshape(-1).astype(np.float64)
+    mask = (xv > 0) & ((xv < 6) if mode == oracle.BN_RELU6_QUANT else True)
+    np.testing.assert_array_equal(out["relu_packed"].reshape(-1), _packbits(mask.astype(np.uint32), 1))
+    y_want = np.minimum(np.maximum(xv, 0), 6) if mode == oracle.BN_RELU6_QUANT else np.where(mask, xv, 0)
+    np.testing.assert_array_equal(bf16(out["y"]).reshape(-1), y_want)
+
+
+@pytest.mark.parametrize("bits", [1, 2, 4, 8])
+def test_squash_mode_known_answer_ramp(bits):
+    # x_hat on an evenly spaced ramp over [-3, 3]; codes of t = 2 tanh(x_hat / 2) worked out in
+    # float64, each value at least 1e-4 (in code units) away from a rounding boundary
+    xh = (-3.0 + 6.0 * np.arange(32) / 31).astype(np.float32)
+    x = xh.reshape(1, 1, 32)
+    out = _sync(x, bits, oracle.BN_QUANT, 32)
+    t = 2.0 * np.tanh(xh.astype(np.float64) / 2.0)
+    qmax = (1 << bits) - 1
+    u = (t - t.min()) / (t.max() - t.min()) * qmax + 0.5
+    assert np.all(np.abs(u - np.round(u)) > 1e-4)
+    np.testing.assert_array_equal(out["packed"].reshape(-1), _packbits(np.floor(u).astype(np.uint32), bits))
+    np.testing.assert_allclose(out["t"].reshape(-1), t, rtol=2e-7, atol=1e-7)
+
+
+@pytest.mark.parametrize("bits", [1, 2, 4, 8])
+@pytest.mark.parametrize("g", [64, 128, 256])  # the pinned quantizer takes g >= 64; g = 32 is pinned by the ramps
+def test_squash_mode_equals_pinned_quantizer(bits, g):
+    x = rnd((4, 3, 8, 8), 10 + bits, scale=1.5, shift=0.3)
+    C, M = 3, 4 * 64
+    w, b = rnd((C,), 4), rnd((C,), 5)
+    s, q = stats32(x)
+    out = oracle.bn_norm_quant(x, w, b, mode=oracle.BN_QUANT, group_size=g, bits=bits, eps=1e-5, sum=s, sumsq=q)
+    t = out["t"]  # [C, M], channel-major flat order n*HW + s
+    xd = x.astype(np.float64)
+    xh = (xd - out["mean"][None, :, None, None]) / np.sqrt(out["var"].astype(np.float64) + 1e-5)[None, :, None, None]
+    t_want = 2.0 * np.tanh(np.clip(xh, -3, 3) / 2.0)
+    np.testing.assert_allclose(t, t_want.transpose(1, 0, 2, 3).reshape(C, M), rtol=1e-5, atol=1e-6)
+    rp, rs, rm = oracle.quant_pack(t.reshape(-1, g), g, bits, meta_dtype=oracle.BF16)
+    np.testing.assert_array_equal(out["packed"].reshape(-1), rp.reshape(-1))
+    np.testing.assert_array_equal(out["scale"].reshape(-1), rs)
+    np.testing.assert_array_equal(out["min"].reshape(-1), rm)
+
+
+@pytest.mark.parametrize("bits", [2, 4, 8])
+def test_relu_mode_division_bound_and_monotone(bits):
+    x = rnd((8, 2, 4, 8), 30 + bits, scale=1.0)
+    C, M, g = 2, 8 * 32, 64
+    w, b = rnd((C,), 6), rnd((C,), 7)
+    s, q = stats32(x)
+    out = oracle.bn_norm_quant(x, w, b, mode=oracle.BN_RELU_QUANT, group_size=g, bits=bits, eps=1e-5, sum=s, sumsq=q)
+    t = out["t"].reshape(-1, g).astype(np.float64)
+    codes = oracle.unpack_codes(out["packed"].reshape(-1, g * bits // 32), g, bits).view(np.uint8).astype(np.float64)
+    # the step kept in fp32 by the kernel is the unrounded rng / QMAX; the stored bf16 is its rounding
+    step = (t.max(axis=1) - t.min(axis=1)) / ((1 << bits) - 1)
+    deq = codes * step[:, None] + t.min(axis=1)[:, None]
+    assert np.all(np.abs(deq - t) <= step[:, None] * (0.5 + 1e-5))
+    order = np.argsort(t, axis=1, kind="stable")
+    assert np.all(np.diff(np.take_along_axis(codes, order, axis=1), axis=1) >= 0)
+
+
+@pytest.mark.parametrize("eps", [1e-7, 1e-5])
+def test_backward_matches_torch_autograd(eps):
+    shape = (6, 4, 5, 8)
+    x = rnd(shape, 40, scale=1.3, shift=-0.2)
+    C = shape[1]
+    w, b = rnd((C,), 8) + 1.0, rnd((C,), 9)
+    dy = rnd(shape, 41)
+    s, q = stats32(x)
+    fw = oracle.bn_norm_quant(x, w, b, mode=oracle.BN_NORM, eps=eps, sum=s, sumsq=q)
+    dw, db = oracle.bn_bwd_reduce(dy, mode=oracle.BN_NORM, x_hat=fw["x_hat"])
+    dx = oracle.bn_bwd_dx(dy, dw.astype(np.float32), db.astype(np.float32), w, fw["var"], mode=oracle.BN_NORM,
+                          eps=eps, x_hat=fw["x_hat"])
+    xt = torch.from_numpy(x.astype(np.float64)).requires_grad_(True)
+    wt = torch.from_numpy(w.astype(np.float64)).requires_grad_(True)
+    bt = torch.from_numpy(b.astype(np.float64)).requires_grad_(True)
+    torch.nn.functional.batch_norm(xt, None, None, wt, bt, training=True, eps=eps).backward(
+        torch.from_numpy(dy.astype(np.float64)))
+    # x_hat is kept in bf16 (relative error 2^-9), the sums and dx follow it
+    np.testing.assert_allclose(db, bt.grad.numpy(), rtol=1e-6, atol=1e-6)
+    xh = bf16(fw["x_hat"])
+    assert np.all(np.abs(dw - wt.grad.numpy()) <= 2.0 ** -8 * np.abs(dy * xh).sum(axis=(0, 2, 3)) + 1e-6)
+    got = bf16(dx)
+    want = xt.grad.numpy()
+    assert np.sqrt(((got - want) ** 2).mean()) <= 1e-2 * np.sqrt((want ** 2).mean())
+
+
+def test_relu_backward_masks_dy():
+    """With the ReLU mask all zero the reduce sums are zero and dx is -(0 + x_hat' * 0) * ... = 0."""
+    x = -np.abs(rnd((2, 1, 8, 8), 50)) - 1.0
+    C = 1
+    w, b = np.ones(C, np.float32), np.zeros(C, np.float32)
+    out = oracle.bn_norm_quant(x, w, b, mode=oracle.BN_RELU_QUANT, group_size=32, bits=2,
+                               mean=np.zeros(C, np.float32), invstd=np.ones(C, np.float32))
+    assert not out["relu_packed"].any()
+    dy = rnd(x.shape, 51)
+    dw, db = oracle.bn_bwd_reduce(dy, mode=oracle.BN_RELU_QUANT, packed=out["packed"],
+                                  relu_packed=out["relu_packed"], scale=out["scale"], min=out["min"], group_size=32,
+                                  bits=2)
+    assert dw[0] == 0.0 and db[0] == 0.0
+    dx = oracle.bn_bwd_dx(dy, dw.astype(np.float32), db.astype(np.float32), w, np.ones(C, np.float32),
+                          mode=oracle.BN_RELU_QUANT, eps=1e-5, packed=out["packed"], relu_packed=out["relu_packed"],
+                          scale=out["scale"], min=out["min"], group_size=32, bits=2)
+    assert not np.any(bf16(dx))
