@@ -93,6 +93,76 @@ def pmc_probe() -> int:
     return 0
 
 
+def batchnorm_layer(torch, dev, event_avg, shape=(256, 256, 56, 56), block=1024, bits=2):
+    """The compressed BatchNorm on a ResNet-50 stage-1 activation (bf16, per-channel groups of
+    block // 2, 2-bit): statistics, normalize + quant-pack (squashed, and fused with ReLU), the
+    backward reduce and input gradient, each against its algorithmic bytes; beside torch's
+    BatchNorm (MIOpen) forward + backward on the same tensor, which saves the full input."""
+    ops = torch.ops.act_lib
+    N, C, H, W = shape
+    HW, M = H * W, N * H * W
+    E = N * C * HW
+    g = dict(M=M, HW=HW, stride_n=C * HW, stride_c=HW)
+    gen = torch.Generator(device=dev).manual_seed(11)
+    x = torch.randn((N, C, HW), generator=gen, device=dev).to(torch.bfloat16)
+    dy = torch.randn((N, C, HW), generator=gen, device=dev).to(torch.bfloat16)
+    w = torch.rand(C, generator=gen, device=dev) + 0.5
+    b = torch.randn(C, generator=gen, device=dev)
+    ng = E // (block // 2)
+    frac = lambda nbytes, t: round(nbytes / t / 1e9 / HBM_PEAK_GBS, 4)  # noqa: E731
+    s_, q_ = ops.bn_fwd_reduce(x, **g, BLOCK_M=block, num_warps=8, num_stages=5)
+    t_st = event_avg(lambda: ops.bn_fwd_reduce(x, **g, BLOCK_M=block, num_warps=8, num_stages=5))
+    res = {"shape": list(shape), "group": block // 2, "bits": bits,
+           "stats": {"us": round(t_st * 1e6, 1), "frac": frac(2 * E, t_st)}}
+    for mode in ("squash", "relu"):
+        if mode == "squash":
+            def fwd():
+                return ops.bn_fwd_norm_quant_pack_fused(x, s_, q_, w, b, None, None, **g, BLOCK_M=block, bits=bits,
+                                                        sync=False, avg_alam=False, alam_bits=0, num_warps=8,
+                                                        num_stages=5)
+            o = fwd()
+            packed, scale, mn, var = o[1], o[2], o[3], o[5]
+
+            def red():
+                return ops.bn_bwd_reduce_dequant_unpack_fused(packed, dy, scale, mn, **g, BLOCK_M=block, bits=bits,
+                                                              avg_alam=False, alam_bits=0)
+            dw, db = red()
+
+            def dx():
+                return ops.bn_bwd_dx_dequant_unpack_fused(packed, dy, scale, mn, dw, db, w, var, **g, BLOCK_M=block,
+                                                          bits=bits, sync=False, avg_alam=False, alam_bits=0)
+            side = E * bits / 8 + ng * 4
+        else:
+            def fwd():
+                return ops.bn_relu_fwd_norm_fused_quant_pack(x, s_, q_, w, b, None, None, **g, relu=True, relu6=False,
+                                                             BLOCK_SIZE=block, BITS=bits, sync=False)
+            o = fwd()
+            packed, rp, scale, mn, var = o[1], o[2], o[3], o[4], o[6]
+
+            def red():
+                return ops.bn_relu_bwd_reduce_fused_dequant_unpack(packed, rp, dy, scale, mn, **g, BLOCK_SIZE=block,
+                                                                   BITS=bits)
+            dw, db = red()
+
+            def dx():
+                return ops.bn_relu_bwd_dx_fused_dequant_unpack(packed, rp, dy, dw, db, w, var, scale, mn, **g,
+                                                               BLOCK_SIZE=block, BITS=bits)
+            side = E * bits / 8 + E / 8 + ng * 4
+        tf, tr, tx = event_avg(fwd), event_avg(red), event_avg(dx)
+        res[mode] = {"fwd_us": round(tf * 1e6, 1), "fwd_frac": frac(4 * E + side, tf),
+                     "bwd_reduce_us": round(tr * 1e6, 1), "bwd_reduce_frac": frac(2 * E + side, tr),
+                     "bwd_dx_us": round(tx * 1e6, 1), "bwd_dx_frac": frac(4 * E + side, tx),
+                     "layer_fwd_bwd_us": round((t_st + tf + tr + tx) * 1e6, 1)}
+        del o
+    xx = x.view(N, C, H, W).clone().requires_grad_(True)
+    dy4 = dy.view(N, C, H, W)
+
+    def torch_bn():
+        torch.nn.functional.batch_norm(xx, None, None, w, b, True, 0.1, 1e-5).backward(dy4)
+    res["torch_batchnorm_fwd_bwd_us"] = round(event_avg(torch_bn) * 1e6, 1)
+    return res
+
+
 def vit_train_step(torch, dev, batch=128, steps=6, warmup=3):
     """one ViT-B/16 train step (forward, cross-entropy, backward, fused AdamW step)
     on a fixed synthetic batch (N(0,1) images 224x224x3, random labels over 1000 classes, bf16
@@ -361,6 +431,8 @@ def main() -> int:
             gemm[f"{M}x{Nn}x{K}"] = entry
             del a8, b8, cm
         extras["fp8_gemm_nt"] = gemm
+        torch.cuda.empty_cache()
+        extras["batchnorm_resnet_2bit"] = batchnorm_layer(torch, dev, event_avg)
         torch.cuda.empty_cache()
         extras["vit_b16_train_step_bs128"] = vit_train_step(torch, dev)
         out["extras"] = extras

@@ -20,11 +20,11 @@
 // 1/scale, 0.5 - 1e-6)) (squashed modes) or trunc((x_hat - min) / scale + (0.5 - 1e-6)) (ReLU
 // modes), x_hat' = fma(q, scale, min), dx = ((fma(-x_hat', dw/M, dy - db/M)) * w) * invstd.
 //
-// Mapping: a workgroup of 256 lanes covers 2048 consecutive elements of one channel, 8 per lane
-// (one 16-byte access for 2-byte types when HW is a multiple of 8, element by element
-// otherwise). A group of G elements spans G/8 aligned lanes (4..64), so group min/max and the
+// Mapping: a workgroup of 256 lanes covers 4 blocks of 2048 consecutive elements of one channel,
+// 8 per lane per block (one 16-byte access for 2-byte types when HW is a multiple of 8, element
+// by element otherwise), with every block's loads issued before the first is used. A group of G elements spans G/8 aligned lanes (4..64), so group min/max and the
 // code merge stay inside a wave. Reductions are two-stage and ordered (workgroup partials, then
-// one thread per channel), so sums are deterministic and need no zeroed buffer or atomics.
+// one wave per channel), so sums are deterministic and need no zeroed buffer or atomics.
 #include "bn_fused.h"
 #include "dopt_device.h"
 
@@ -34,10 +34,14 @@ namespace {
 constexpr int TPB = 256;
 constexpr int EPL = 8;
 constexpr int64_t WG_ELEMS = TPB * EPL;
+constexpr int ITER = (int)(BN_CHUNK / WG_ELEMS);  // 2048-element blocks per workgroup (loads issued together)
 
+// element offset of channel c's element e; e < M < 2^31 (checked by the host), so the divide is
+// a 32-bit one
 __device__ __forceinline__ int64_t bn_off(const BnGeom& g, int64_t c, int64_t e) {
-    const int64_t n = e / g.HW;
-    return n * g.stride_n + c * g.stride_c + (e - n * g.HW);
+    const uint32_t hw = (uint32_t)g.HW, ee = (uint32_t)e;
+    const uint32_t n = ee / hw;
+    return (int64_t)n * g.stride_n + c * g.stride_c + (int64_t)(ee - n * hw);
 }
 
 template <int DT>
@@ -61,12 +65,13 @@ __device__ __forceinline__ void load8(const void* base, const BnGeom& g, int64_t
     }
 }
 
+// bf16 outputs are streamed (non-temporal: written once, read by another kernel much later)
 template <bool VEC>
 __device__ __forceinline__ void store8_bf16(uint16_t* base, const BnGeom& g, int64_t c, int64_t e0, int64_t M,
                                             const float* v) {
     if constexpr (VEC) {
-        st16<false>(base + bn_off(g, c, e0), make_uint4(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]),
-                                                       pack_bf16x2(v[4], v[5]), pack_bf16x2(v[6], v[7])));
+        st16<true>(base + bn_off(g, c, e0), make_uint4(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]),
+                                                      pack_bf16x2(v[4], v[5]), pack_bf16x2(v[6], v[7])));
     } else {
 #pragma unroll
         for (int k = 0; k < EPL; ++k)
@@ -148,7 +153,7 @@ __device__ __forceinline__ void store_codes(uint32_t* chan, int64_t e0, const in
         v <<= 8 * (lane & 3);
         v |= dpp_u32<0xB1>(v);
         v |= dpp_u32<0x4E>(v);
-        if (active && (lane & 3) == 0) chan[e0 / 32] = v;
+        if (active && (lane & 3) == 0) chan[e0 >> 5] = v;
     }
 }
 
@@ -158,7 +163,7 @@ __device__ __forceinline__ void store_mask(uint32_t* chan, int64_t e0, uint32_t 
     uint32_t v = m8 << (8 * (lane & 3));
     v |= dpp_u32<0xB1>(v);
     v |= dpp_u32<0x4E>(v);
-    if (active && (lane & 3) == 0) chan[e0 / 32] = v;
+    if (active && (lane & 3) == 0) chan[e0 >> 5] = v;
 }
 
 // the lane's 8 codes read back from the channel bitstream
@@ -185,17 +190,26 @@ __global__ __launch_bounds__(TPB) void bn_stats_kernel(const void* __restrict__ 
                                                        float* __restrict__ partial, int64_t nchunks) {
     const int64_t c = blockIdx.y, chunk = blockIdx.x;
     const int64_t M = g.N * g.HW;
-    const int64_t e_end = min(M, (chunk + 1) * BN_CHUNK);
-    float s = 0.0f, s2 = 0.0f;
-    for (int64_t e0 = chunk * BN_CHUNK + (int64_t)threadIdx.x * EPL; e0 < e_end; e0 += WG_ELEMS) {
-        float v[EPL];
-        load8<DT, VEC>(x, g, c, e0, M, v);
+    const int64_t base = chunk * BN_CHUNK + (int64_t)threadIdx.x * EPL;
+    float v[ITER][EPL];
 #pragma unroll
-        for (int k = 0; k < EPL; ++k) {
-            s += v[k];
-            s2 = fmaf(v[k], v[k], s2);
+    for (int it = 0; it < ITER; ++it) {
+        const int64_t e0 = base + it * WG_ELEMS;
+        if (e0 < M) {
+            load8<DT, VEC>(x, g, c, e0, M, v[it]);
+        } else {
+#pragma unroll
+            for (int k = 0; k < EPL; ++k) v[it][k] = 0.0f;
         }
     }
+    float s = 0.0f, s2 = 0.0f;
+#pragma unroll
+    for (int it = 0; it < ITER; ++it)
+#pragma unroll
+        for (int k = 0; k < EPL; ++k) {
+            s += v[it][k];
+            s2 = fmaf(v[it][k], v[it][k], s2);
+        }
     block_sum2(s, s2);
     if (threadIdx.x == 0) {
         partial[c * nchunks + chunk] = s;
@@ -203,19 +217,24 @@ __global__ __launch_bounds__(TPB) void bn_stats_kernel(const void* __restrict__ 
     }
 }
 
-// one thread per channel: the partials in chunk order
-__global__ __launch_bounds__(TPB) void bn_finalize_kernel(const float* __restrict__ partial, int64_t C,
-                                                          int64_t nchunks, float* __restrict__ out0,
-                                                          float* __restrict__ out1) {
-    const int64_t c = (int64_t)blockIdx.x * TPB + threadIdx.x;
-    if (c >= C) return;
+// one wave per channel: lane l sums partials l, l+64, ... in order, then the wave tree (fixed
+// order, so the result is deterministic); the loads of a lane are independent and overlap
+__global__ __launch_bounds__(64) void bn_finalize_kernel(const float* __restrict__ partial, int64_t C,
+                                                         int64_t nchunks, float* __restrict__ out0,
+                                                         float* __restrict__ out1) {
+    const int64_t c = blockIdx.x;
     float a = 0.0f, b = 0.0f;
-    for (int64_t k = 0; k < nchunks; ++k) {
+#pragma unroll 4
+    for (int64_t k = threadIdx.x; k < nchunks; k += 64) {
         a += partial[c * nchunks + k];
         b += partial[(C + c) * nchunks + k];
     }
-    out0[c] = a;
-    out1[c] = b;
+    a = wave_sum(a);
+    b = wave_sum(b);
+    if (threadIdx.x == 0) {
+        out0[c] = a;
+        out1[c] = b;
+    }
 }
 
 // per-channel mean and inverse std as the forward kernels derive them
@@ -237,19 +256,13 @@ __device__ __forceinline__ void channel_stats(const BnFwdArgs& a, int64_t c, int
 }
 
 // ------------------------------------------------------------------ forward
-template <int DT, int MODE, bool VEC>
-__global__ __launch_bounds__(TPB) void bn_fwd_kernel(BnFwdArgs a, int group, int bits, int relu6) {
-    const BnGeom g = a.g;
-    const int64_t c = blockIdx.y;
-    const int64_t M = g.N * g.HW;
-    const int64_t e0 = (int64_t)blockIdx.x * WG_ELEMS + (int64_t)threadIdx.x * EPL;
-    const bool active = e0 < M;
-    float mean, inv;
-    channel_stats(a, c, M, mean, inv);
-    const float w = a.w[c], b = a.b[c];
-
-    float v[EPL] = {};
-    if (active) load8<DT, VEC>(a.x, g, c, e0, M, v);
+// One 2048-element block of the forward: y (and the mask / codes / scale / min) from the lane's 8
+// loaded values. Whole groups are active or not (M % group == 0), so the group's lanes agree.
+template <int MODE, bool VEC>
+__device__ __forceinline__ void fwd_block(const BnFwdArgs& a, int64_t c, int64_t e0, int64_t M, bool active,
+                                          const float* v, float mean, float inv, float w, float b, int lg,
+                                          int bits, int relu6) {
+    const BnGeom& g = a.g;
     float xh[EPL], y[EPL];
 #pragma unroll
     for (int k = 0; k < EPL; ++k) {
@@ -261,7 +274,6 @@ __global__ __launch_bounds__(TPB) void bn_fwd_kernel(BnFwdArgs a, int group, int
             store8_bf16<VEC>(a.y, g, c, e0, M, y);
             store8_bf16<VEC>(a.xhat, g, c, e0, M, xh);
         }
-        return;
     } else {
         uint32_t m8 = 0;
         if constexpr (MODE == BN_RELU_QUANT) {
@@ -273,7 +285,7 @@ __global__ __launch_bounds__(TPB) void bn_fwd_kernel(BnFwdArgs a, int group, int
             }
         }
         if (active) store8_bf16<VEC>(a.y, g, c, e0, M, y);
-        if constexpr (MODE == BN_RELU_QUANT) store_mask(a.relu_packed + c * (M / 32), e0, m8, active);
+        if constexpr (MODE == BN_RELU_QUANT) store_mask(a.relu_packed + c * (M >> 5), e0, m8, active);
 
         // values quantized: the squashed x_hat (BN_QUANT) or x_hat itself (ReLU modes)
         float t[EPL];
@@ -282,16 +294,14 @@ __global__ __launch_bounds__(TPB) void bn_fwd_kernel(BnFwdArgs a, int group, int
         for (int k = 0; k < EPL; ++k) {
             if constexpr (MODE == BN_QUANT) {
                 const float cl = fminf(fmaxf(xh[k], -3.0f), 3.0f);
-                t[k] = tanhf(cl * 0.5f) / 0.5f;
+                t[k] = fast_tanh(cl * 0.5f) * 2.0f;
             } else {
                 t[k] = xh[k];
             }
-            if (active) {
-                mn = fminf(mn, t[k]);
-                mx = fmaxf(mx, t[k]);
-            }
+            mn = fminf(mn, t[k]);
+            mx = fmaxf(mx, t[k]);
         }
-        const int lpg = group / EPL;
+        const int lpg = 1 << (lg - 3);  // group / EPL
         group_minmax(mn, mx, lpg);
         const float qmaxf = (float)((1 << bits) - 1);
         const float rng = mx - mn;
@@ -312,33 +322,61 @@ __global__ __launch_bounds__(TPB) void bn_fwd_kernel(BnFwdArgs a, int group, int
                 q[k] = (int)qf;
             }
         }
-        store_codes(a.packed + c * (M * bits / 32), e0, q, bits, active);
+        store_codes(a.packed + c * ((M * bits) >> 5), e0, q, bits, active);
         if (active && ((threadIdx.x & 63) & (lpg - 1)) == 0) {
-            const int64_t gi = c * (M / group) + e0 / group;
+            const int64_t gi = c * (M >> lg) + (e0 >> lg);
             a.scale[gi] = to_bf16(step);
             a.minv[gi] = to_bf16(mn);
         }
     }
 }
 
+// A workgroup covers ITER consecutive 2048-element blocks of one channel; all loads are issued
+// before the first block is processed.
+template <int DT, int MODE, bool VEC>
+__global__ __launch_bounds__(TPB) void bn_fwd_kernel(BnFwdArgs a, int lg, int bits, int relu6) {
+    const int64_t c = blockIdx.y;
+    const int64_t M = a.g.N * a.g.HW;
+    const int64_t base = (int64_t)blockIdx.x * BN_CHUNK + (int64_t)threadIdx.x * EPL;
+    float v[ITER][EPL];
+#pragma unroll
+    for (int it = 0; it < ITER; ++it) {
+        const int64_t e0 = base + it * WG_ELEMS;
+        if (e0 < M) {
+            load8<DT, VEC>(a.x, a.g, c, e0, M, v[it]);
+        } else {
+#pragma unroll
+            for (int k = 0; k < EPL; ++k) v[it][k] = 0.0f;
+        }
+    }
+    float mean, inv;
+    channel_stats(a, c, M, mean, inv);
+    const float w = a.w[c], b = a.b[c];
+#pragma unroll
+    for (int it = 0; it < ITER; ++it) {
+        const int64_t e0 = base + it * WG_ELEMS;
+        fwd_block<MODE, VEC>(a, c, e0, M, e0 < M, v[it], mean, inv, w, b, lg, bits, relu6);
+    }
+}
+
 // ------------------------------------------------------------------ backward
-// x_hat' and dy (times the ReLU mask) of the lane's 8 elements
+// dy (times the ReLU mask) and x_hat' of the lane's 8 elements
 template <int DYT, int MODE, bool VEC>
-__device__ __forceinline__ void bwd_operands(const BnBwdArgs& a, int64_t c, int64_t e0, int64_t M, int group,
+__device__ __forceinline__ void bwd_operands(const BnBwdArgs& a, int64_t c, int64_t e0, int64_t M, int lg,
                                              int bits, float* xh, float* dy) {
     load8<DYT, VEC>(a.dy, a.g, c, e0, M, dy);
     if constexpr (MODE == BN_NORM) {
         load8<DT_BF16, VEC>(a.xhat, a.g, c, e0, M, xh);
     } else {
         int q[EPL];
-        load_codes(a.packed + c * (M * bits / 32), e0, bits, q);
-        const int64_t gi = c * (M / group) + e0 / group;
+        load_codes(a.packed + c * ((M * bits) >> 5), e0, bits, q);
+        const int64_t gi = c * (M >> lg) + (e0 >> lg);
         const float sc = bf16_bits_to_f32(a.scale[gi]);
         const float mn = bf16_bits_to_f32(a.minv[gi]);
 #pragma unroll
         for (int k = 0; k < EPL; ++k) xh[k] = fmaf((float)q[k], sc, mn);
         if constexpr (MODE == BN_RELU_QUANT) {
-            const uint32_t m = a.relu_packed[c * (M / 32) + e0 / 32] >> (e0 & 31);
+            const uint32_t m = a.relu_packed[c * (M >> 5) + (e0 >> 5)] >> (e0 & 31);
 #pragma unroll
             for (int k = 0; k < EPL; ++k) dy[k] = dy[k] * (float)((m >> k) & 1u);
         }
@@ -346,20 +384,29 @@ __device__ __forceinline__ void bwd_operands(const BnBwdArgs& a, int64_t c, int6
 }
 
 template <int DYT, int MODE, bool VEC>
-__global__ __launch_bounds__(TPB) void bn_bwd_reduce_kernel(BnBwdArgs a, int group, int bits, int64_t nchunks) {
+__global__ __launch_bounds__(TPB) void bn_bwd_reduce_kernel(BnBwdArgs a, int lg, int bits, int64_t nchunks) {
     const int64_t c = blockIdx.y, chunk = blockIdx.x;
     const int64_t M = a.g.N * a.g.HW;
-    const int64_t e_end = min(M, (chunk + 1) * BN_CHUNK);
-    float sdy = 0.0f, sdyx = 0.0f;
-    for (int64_t e0 = chunk * BN_CHUNK + (int64_t)threadIdx.x * EPL; e0 < e_end; e0 += WG_ELEMS) {
-        float xh[EPL], dy[EPL];
-        bwd_operands<DYT, MODE, VEC>(a, c, e0, M, group, bits, xh, dy);
+    const int64_t base = chunk * BN_CHUNK + (int64_t)threadIdx.x * EPL;
+    float xh[ITER][EPL], dy[ITER][EPL];
 #pragma unroll
-        for (int k = 0; k < EPL; ++k) {
-            sdy += dy[k];
-            sdyx = fmaf(dy[k], xh[k], sdyx);
+    for (int it = 0; it < ITER; ++it) {
+        const int64_t e0 = base + it * WG_ELEMS;
+        if (e0 < M) {
+            bwd_operands<DYT, MODE, VEC>(a, c, e0, M, lg, bits, xh[it], dy[it]);
+        } else {
+#pragma unroll
+            for (int k = 0; k < EPL; ++k) xh[it][k] = dy[it][k] = 0.0f;
         }
     }
+    float sdy = 0.0f, sdyx = 0.0f;
+#pragma unroll
+    for (int it = 0; it < ITER; ++it)
+#pragma unroll
+        for (int k = 0; k < EPL; ++k) {
+            sdy += dy[it][k];
+            sdyx = fmaf(dy[it][k], xh[it][k], sdyx);
+        }
     block_sum2(sdy, sdyx);
     if (threadIdx.x == 0) {
         a.partial[c * nchunks + chunk] = sdyx;            // -> dw
@@ -368,28 +415,44 @@ __global__ __launch_bounds__(TPB) void bn_bwd_reduce_kernel(BnBwdArgs a, int gro
 }
 
 template <int DYT, int MODE, bool VEC>
-__global__ __launch_bounds__(TPB) void bn_bwd_dx_kernel(BnBwdArgs a, int group, int bits) {
+__global__ __launch_bounds__(TPB) void bn_bwd_dx_kernel(BnBwdArgs a, int lg, int bits) {
     const int64_t c = blockIdx.y;
     const int64_t M = a.g.N * a.g.HW;
-    const int64_t e0 = (int64_t)blockIdx.x * WG_ELEMS + (int64_t)threadIdx.x * EPL;
-    if (e0 >= M) return;
+    const int64_t base = (int64_t)blockIdx.x * BN_CHUNK + (int64_t)threadIdx.x * EPL;
+    float xh[ITER][EPL], dy[ITER][EPL];
+#pragma unroll
+    for (int it = 0; it < ITER; ++it) {
+        const int64_t e0 = base + it * WG_ELEMS;
+        if (e0 < M) bwd_operands<DYT, MODE, VEC>(a, c, e0, M, lg, bits, xh[it], dy[it]);
+    }
     const float Mf = (float)M;
     const float dwm = a.dw_in[c] / Mf, dbm = a.db_in[c] / Mf;
     const float w = a.w[c];
     const float inv = a.var_is_invstd ? a.var[c] : 1.0f / sqrtf(a.var[c] + a.eps);
-    float xh[EPL], dy[EPL], dx[EPL];
-    bwd_operands<DYT, MODE, VEC>(a, c, e0, M, group, bits, xh, dy);
 #pragma unroll
-    for (int k = 0; k < EPL; ++k) dx[k] = (fmaf(-xh[k], dwm, dy[k] - dbm) * w) * inv;
-    store8_bf16<VEC>(a.dx, a.g, c, e0, M, dx);
+    for (int it = 0; it < ITER; ++it) {
+        const int64_t e0 = base + it * WG_ELEMS;
+        if (e0 >= M) break;
+        float dx[EPL];
+#pragma unroll
+        for (int k = 0; k < EPL; ++k) dx[k] = (fmaf(-xh[it][k], dwm, dy[it][k] - dbm) * w) * inv;
+        store8_bf16<VEC>(a.dx, a.g, c, e0, M, dx);
+    }
+}
+
+int log2i(int v) {
+    int l = 0;
+    while ((1 << l) < v) ++l;
+    return l;
 }
 
 template <int DT>
 int fwd_dt(const BnFwdArgs& a, int mode, int group, int bits, bool vec, hipStream_t s) {
     const int64_t M = a.g.N * a.g.HW;
-    const dim3 grid((unsigned)((M + WG_ELEMS - 1) / WG_ELEMS), (unsigned)a.g.C);
+    const int lg = mode == BN_NORM ? 3 : log2i(group);
+    const dim3 grid((unsigned)bn_nchunks(M), (unsigned)a.g.C);
     const int relu6 = mode == BN_RELU6_QUANT;
-#define DOPT_BN_FWD(MODE_, VEC_) hipLaunchKernelGGL((bn_fwd_kernel<DT, MODE_, VEC_>), grid, dim3(TPB), 0, s, a, group, bits, relu6)
+#define DOPT_BN_FWD(MODE_, VEC_) hipLaunchKernelGGL((bn_fwd_kernel<DT, MODE_, VEC_>), grid, dim3(TPB), 0, s, a, lg, bits, relu6)
     if (mode == BN_NORM) {
         if (vec) DOPT_BN_FWD(BN_NORM, true); else DOPT_BN_FWD(BN_NORM, false);
     } else if (mode == BN_QUANT) {
@@ -404,11 +467,12 @@ int fwd_dt(const BnFwdArgs& a, int mode, int group, int bits, bool vec, hipStrea
 template <int DYT>
 int bwd_dt(const BnBwdArgs& a, int mode, int group, int bits, bool vec, bool reduce, hipStream_t s) {
     const int64_t M = a.g.N * a.g.HW;
+    const int lg = mode == BN_NORM ? 3 : log2i(group);
     const int64_t nch = bn_nchunks(M);
     const int m = mode == BN_RELU6_QUANT ? BN_RELU_QUANT : mode;
     if (reduce) {
         const dim3 grid((unsigned)nch, (unsigned)a.g.C);
-#define DOPT_BN_RED(MODE_, VEC_) hipLaunchKernelGGL((bn_bwd_reduce_kernel<DYT, MODE_, VEC_>), grid, dim3(TPB), 0, s, a, group, bits, nch)
+#define DOPT_BN_RED(MODE_, VEC_) hipLaunchKernelGGL((bn_bwd_reduce_kernel<DYT, MODE_, VEC_>), grid, dim3(TPB), 0, s, a, lg, bits, nch)
         if (nch == 0) {
         } else if (m == BN_NORM) {
             if (vec) DOPT_BN_RED(BN_NORM, true); else DOPT_BN_RED(BN_NORM, false);
@@ -418,11 +482,11 @@ int bwd_dt(const BnBwdArgs& a, int mode, int group, int bits, bool vec, bool red
             if (vec) DOPT_BN_RED(BN_RELU_QUANT, true); else DOPT_BN_RED(BN_RELU_QUANT, false);
         }
 #undef DOPT_BN_RED
-        hipLaunchKernelGGL(bn_finalize_kernel, dim3((unsigned)((a.g.C + TPB - 1) / TPB)), dim3(TPB), 0, s,
-                           (const float*)a.partial, a.g.C, nch, a.dw, a.db);
+        hipLaunchKernelGGL(bn_finalize_kernel, dim3((unsigned)a.g.C), dim3(64), 0, s, (const float*)a.partial,
+                           a.g.C, nch, a.dw, a.db);
     } else {
-        const dim3 grid((unsigned)((M + WG_ELEMS - 1) / WG_ELEMS), (unsigned)a.g.C);
-#define DOPT_BN_DX(MODE_, VEC_) hipLaunchKernelGGL((bn_bwd_dx_kernel<DYT, MODE_, VEC_>), grid, dim3(TPB), 0, s, a, group, bits)
+        const dim3 grid((unsigned)nch, (unsigned)a.g.C);
+#define DOPT_BN_DX(MODE_, VEC_) hipLaunchKernelGGL((bn_bwd_dx_kernel<DYT, MODE_, VEC_>), grid, dim3(TPB), 0, s, a, lg, bits)
         if (m == BN_NORM) {
             if (vec) DOPT_BN_DX(BN_NORM, true); else DOPT_BN_DX(BN_NORM, false);
         } else if (m == BN_QUANT) {
@@ -457,8 +521,8 @@ int launch_bn_reduce(const void* x, int dt, const BnGeom& g, float* partial, flo
         }
     }
 #undef DOPT_BN_STATS
-    hipLaunchKernelGGL(bn_finalize_kernel, dim3((unsigned)((g.C + TPB - 1) / TPB)), dim3(TPB), 0, s,
-                       (const float*)partial, g.C, nch, sum, sumsq);
+    hipLaunchKernelGGL(bn_finalize_kernel, dim3((unsigned)g.C), dim3(64), 0, s, (const float*)partial, g.C, nch,
+                       sum, sumsq);
     return 0;
 }
 
