@@ -6,6 +6,7 @@ library ``libdopt.so`` is loaded on the first operator call and must have been b
 """
 from . import act_lib  # noqa: F401  (registers torch.ops.act_lib.*)
 from . import bn_lib  # noqa: F401  (registers the BatchNorm act_lib operators)
+from . import dw_lib  # noqa: F401  (registers act_lib::dw_gemm)
 from .act_lib import _bits_consts  # noqa: F401
 
-__all__ = ["act_lib", "bn_lib"]
+__all__ = ["act_lib", "bn_lib", "dw_lib"]

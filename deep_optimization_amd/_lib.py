@@ -38,6 +38,8 @@ EXPORTS = (
     "dopt_bn_norm_quant",
     "dopt_bn_bwd_reduce",
     "dopt_bn_bwd_dx",
+    "dopt_dw_gemm_workspace_floats",
+    "dopt_dw_gemm",
 )
 
 _lib = None
@@ -97,6 +99,10 @@ def lib() -> ctypes.CDLL:
         L.dopt_bn_bwd_dx.argtypes = [i32, vp, vp, vp, vp, vp, vp, i32, i64, i64, i64, i64, i64, i32, i32, vp, vp, vp, vp,
                                      f32, i32, vp, vp]
         L.dopt_bn_bwd_dx.restype = i32
+        L.dopt_dw_gemm_workspace_floats.argtypes = [i64, i64, i64]
+        L.dopt_dw_gemm_workspace_floats.restype = i64
+        L.dopt_dw_gemm.argtypes = [vp, i64, vp, i64, vp, vp, vp, i32, i32, i64, i64, i64, vp, vp, vp, vp, vp]
+        L.dopt_dw_gemm.restype = i32
         _lib = L
     return _lib
 

@@ -26,6 +26,7 @@ SOURCES = [
     "fp8_gemm.hip",
     "act_fused.hip",
     "bn_fused.hip",
+    "dw_gemm.hip",
 ]
 
 ARCH = "gfx950"

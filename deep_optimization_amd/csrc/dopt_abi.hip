@@ -8,6 +8,7 @@
 #include "../../include/dopt.h"
 #include "bn_fused.h"
 #include "dequant_unpack.h"
+#include "dw_gemm.h"
 #include "quant_pack.h"
 
 namespace dopt {
@@ -504,6 +505,56 @@ int dopt_bn_bwd_dx(int mode, const void* x_hat, const uint32_t* packed, const ui
     dopt::launch_bn_bwd_dx(a, dy_dtype, mode, group_size, bits,
                            bn_vec(g, {dy, dx, mode == DOPT_BN_NORM ? x_hat : nullptr}), (hipStream_t)stream);
     return hip_status("bn_bwd_dx launch");
+}
+
+int64_t dopt_dw_gemm_workspace_floats(int64_t M, int64_t N, int64_t K) {
+    if (M <= 0 || N <= 0 || K < 0 || M % 256 || N % 256) return 0;  // unsupported shapes need none
+    return dopt::dw_workspace_floats(M, N, K);
+}
+
+int dopt_dw_gemm(const void* dy, int64_t ldd, const void* x_hat, int64_t ldx, const uint32_t* packed,
+                 const void* scale, const void* minv, int group_size, int bits, int64_t M, int64_t N, int64_t K,
+                 float* workspace, float* dw_f32, void* dw_bf16, float* db, void* stream) {
+    int rc;
+    if (M <= 0 || N <= 0 || K < 0 || M % 256 || N % 256)
+        return fail(DOPT_EUNSUPPORTED, "dw_gemm needs M and N positive multiples of 256 (got M=%lld N=%lld K=%lld)",
+                    (long long)M, (long long)N, (long long)K);
+    if (M * N >= ((int64_t)1 << 40) || K >= ((int64_t)1 << 31))
+        return fail(DOPT_EINVAL, "dw_gemm shape too large");
+    if ((K > 0 && !dy) || !workspace || (!dw_f32 && !dw_bf16))
+        return fail(DOPT_EINVAL, "null dy/workspace/output pointer");
+    if (ldd < M || ldd % 8 || !aligned16(dy)) return fail(DOPT_EINVAL, "dy must be 16-byte aligned with ldd >= M, ldd %% 8 == 0");
+    if (((uintptr_t)workspace & 15u) || (dw_f32 && ((uintptr_t)dw_f32 & 15u)) || (dw_bf16 && ((uintptr_t)dw_bf16 & 7u)))
+        return fail(DOPT_EINVAL, "workspace / dw_f32 must be 16-byte and dw_bf16 8-byte aligned");
+    dopt::DwArgs a{};
+    a.dy = (const uint16_t*)dy;
+    a.ldd = ldd;
+    a.M = M;
+    a.N = N;
+    a.K = K;
+    a.partial = workspace;
+    int mode;
+    if (x_hat || (K == 0 && !packed)) {
+        if (ldx < N || ldx % 8 || !aligned16(x_hat))
+            return fail(DOPT_EINVAL, "x_hat must be 16-byte aligned with ldx >= N, ldx %% 8 == 0");
+        a.xh = (const uint16_t*)x_hat;
+        a.ldx = ldx;
+        mode = dopt::DW_B_BF16;
+    } else {
+        if ((rc = check_bits(bits))) return rc;
+        if ((rc = check_group(group_size))) return rc;
+        if (!packed || !scale || !minv) return fail(DOPT_EINVAL, "null packed/scale/min pointer");
+        if ((uintptr_t)packed & 7u) return fail(DOPT_EINVAL, "packed must be 8-byte aligned");
+        a.packed = packed;
+        a.scale = (const uint16_t*)scale;
+        a.minv = (const uint16_t*)minv;
+        a.bits = bits;
+        a.lg = ilog2(group_size);
+        mode = dopt::DW_B_PACKED;
+    }
+    (void)hipGetLastError();
+    dopt::launch_dw_gemm(a, mode, db != nullptr, dw_f32, (uint16_t*)dw_bf16, db, (hipStream_t)stream);
+    return hip_status("dw_gemm launch");
 }
 
 }  // extern "C"

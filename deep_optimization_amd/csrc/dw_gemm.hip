@@ -1,0 +1,327 @@
+// Weight gradient of a Linear layer from its saved activation, on CDNA4 bf16 MFMA:
+//   dW[m][n] = sum_k dy[k][m] * x_hat[k][n]      (M = out features, N = in features, K = tokens)
+//   db[m]    = sum_k dy[k][m]                     (optional, fused)
+// with x_hat either a bf16 tensor or decoded inside the kernel from the quantizer's packed codes
+// (x_hat = bf16(fma(q, scale, min)), the value act_lib::dequant_unpack_triton writes), so the
+// dequantized activation never goes through HBM.
+//
+// Both operands arrive K-outer ([K][M] and [K][N], row-major), which MFMA cannot read directly:
+// a lane's MFMA operand is 8 consecutive K values of one row/column. Each K tile (64 tokens) is
+// therefore staged through registers: a lane loads an 8 x 8 block (8 token rows x 16 bytes),
+// transposes it with byte permutes (v_perm_b32) and writes 8 K-contiguous 16-byte chunks to LDS
+// ([m][k] and [n][k], 128-byte rows, chunk c of row r at position c ^ ((r / 2) % 8) so a
+// ds_read_b128 of 16 consecutive rows hits 16 distinct bank groups). For packed x the lane reads
+// the 8 rows' codes (8 * bits bits per row) and their group's bf16 scale and min, and decodes
+// straight into the transposed chunks.
+//
+// Tiling: 256 x 256 output tile per workgroup of 4 waves (2 x 2), each wave 128 x 128 as 4 x 4
+// blocks of v_mfma_f32_32x32x16_bf16 (fp32 accumulators). The K range is split S ways so the
+// small M x N of a weight gradient still fills the GPU; each split writes an fp32 partial tile
+// and a second kernel sums the S partials in order (deterministic) into fp32 and/or bf16. K
+// tiles are double-buffered: the global loads of tile k+1 are issued before the MFMAs of tile k,
+// and their transpose/decode into the other LDS buffer follows them.
+//
+// MFMA layout (32x32x16 bf16): lane l supplies row (or column) l % 32 and 8 consecutive K values
+// starting at 8 * (l / 32) of the 16; A and B use the same K mapping. Accumulator register v of
+// lane l holds row 8*(v/4) + 4*(l/32) + (v%4), column l % 32.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <algorithm>
+
+#include "dopt_device.h"
+#include "dw_gemm.h"
+
+namespace dopt {
+namespace {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+
+constexpr int BM = 256, BN = 256, BK = 64, THREADS = 256;
+constexpr int DW_XCDS = 8;
+constexpr int TM = 4, TN = 4;          // 32 x 32 blocks per wave
+constexpr int ROWB = BK * 2;           // LDS row pitch in bytes (64 bf16)
+
+__device__ __forceinline__ f32x16_t mfma_bf16(const uint4& a, const uint4& b, const f32x16_t& c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b),
+                                                   c, 0, 0, 0);
+}
+
+// byte offset of 16-byte chunk `ch` of LDS row `r`
+__device__ __forceinline__ int lds_off(int r, int ch) { return r * ROWB + ((ch ^ ((r >> 1) & 7)) << 4); }
+
+// one K tile's worth of a lane's producer inputs (registers between the global load and the LDS write)
+struct Stage {
+    uint4 a[8];      // dy rows k..k+7, 8 m values each
+    uint4 b[8];      // x_hat rows (bf16 mode)
+    uint32_t w[8];   // codes of 8 x 8 (packed mode; bits == 8 uses w and w2)
+    uint32_t w2[8];
+    uint32_t sm[8];  // bf16 scale (low) | min (high) per row (packed mode)
+};
+
+template <int MODE, int BITS>
+__device__ __forceinline__ void load_stage(const DwArgs& a, Stage& s, int64_t k0, int kb, int mb, int64_t m0,
+                                           int64_t n0) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const int64_t k = k0 + kb * 8 + j;
+        const bool in = k < a.K;
+        s.a[j] = in ? *(const uint4*)(a.dy + k * a.ldd + m0 + mb * 8) : make_uint4(0, 0, 0, 0);
+        if constexpr (MODE == DW_B_BF16) {
+            s.b[j] = in ? *(const uint4*)(a.xh + k * a.ldx + n0 + mb * 8) : make_uint4(0, 0, 0, 0);
+        } else {
+            // element e = k * N + n of the flat activation: codes at bit e * bits, group e >> lg
+            // (e % 8 == 0, so the 8 codes of bits <= 4 lie in one word; bits == 8 takes two)
+            const int64_t e = k * a.N + n0 + mb * 8;
+            const int64_t bit = e * BITS;
+            if (in) {
+                const uint32_t* wp = a.packed + (bit >> 5);
+                s.w[j] = BITS == 8 ? wp[0] : (wp[0] >> (bit & 31));
+                s.w2[j] = BITS == 8 ? wp[1] : 0u;
+                const int64_t gi = e >> a.lg;
+                s.sm[j] = (uint32_t)a.scale[gi] | ((uint32_t)a.minv[gi] << 16);
+            } else {
+                s.w[j] = s.w2[j] = 0u;
+                s.sm[j] = 0u;  // scale 0, min 0: rows past K decode to 0
+            }
+        }
+    }
+}
+
+// Part p (0..3) of writing a staged K tile to LDS: columns 2p and 2p+1 of the lane's 8 x 8 A block
+// (transposed) and of its B block (transposed or decoded); with DB also dy rows 2p, 2p+1 into db[].
+template <int MODE, int BITS, bool DB>
+__device__ __forceinline__ void write_part(const DwArgs& a, const Stage& s, char* sa, char* sb, int kb, int mb,
+                                           float* db, int p) {
+    if constexpr (DB) {
+        // column sums of dy rows 2p, 2p+1 (dword q of a row holds columns 2q, 2q+1); fenced so the
+        // scheduler does not widen every row early (register pressure)
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int j = 2 * p; j < 2 * p + 2; ++j) {
+            const uint32_t* d = (const uint32_t*)&s.a[j];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                db[2 * q] += __uint_as_float(d[q] << 16);
+                db[2 * q + 1] += __uint_as_float(d[q] & 0xffff0000u);
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int c = 2 * p; c < 2 * p + 2; ++c) {
+        const uint32_t sel = (c & 1) ? 0x07060302u : 0x05040100u;
+        uint32_t d[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const uint32_t* lo = (const uint32_t*)&s.a[2 * r];
+            const uint32_t* hi = (const uint32_t*)&s.a[2 * r + 1];
+            d[r] = __builtin_amdgcn_perm(hi[c >> 1], lo[c >> 1], sel);
+        }
+        *(uint4*)(sa + lds_off(mb * 8 + c, kb)) = make_uint4(d[0], d[1], d[2], d[3]);
+        if constexpr (MODE == DW_B_BF16) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const uint32_t* lo = (const uint32_t*)&s.b[2 * r];
+                const uint32_t* hi = (const uint32_t*)&s.b[2 * r + 1];
+                d[r] = __builtin_amdgcn_perm(hi[c >> 1], lo[c >> 1], sel);
+            }
+            *(uint4*)(sb + lds_off(mb * 8 + c, kb)) = make_uint4(d[0], d[1], d[2], d[3]);
+        } else {
+            // value (row j, column c) = bf16(fma(q, scale_j, min_j)), rows 2r, 2r+1 in dword r
+            constexpr uint32_t qm = (1u << BITS) - 1u;
+            float v[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const uint32_t q = BITS == 8 ? (((c < 4 ? s.w[j] : s.w2[j]) >> (8 * (c & 3))) & 0xffu)
+                                             : ((s.w[j] >> (c * BITS)) & qm);
+                v[j] = fmaf((float)q, __uint_as_float(s.sm[j] << 16), __uint_as_float(s.sm[j] & 0xffff0000u));
+            }
+            *(uint4*)(sb + lds_off(mb * 8 + c, kb)) = make_uint4(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]),
+                                                               pack_bf16x2(v[4], v[5]), pack_bf16x2(v[6], v[7]));
+        }
+    }
+}
+
+template <int MODE, int BITS, bool DB>
+__device__ __forceinline__ void write_stage(const DwArgs& a, const Stage& s, char* sa, char* sb, int kb, int mb,
+                                            float* db) {
+#pragma unroll
+    for (int p = 0; p < 4; ++p) write_part<MODE, BITS, DB>(a, s, sa, sb, kb, mb, db, p);
+}
+
+// The MFMAs of one K tile (4 steps of 16 K) from LDS buffers (ra, rb).
+__device__ __forceinline__ void mma_tile(f32x16_t (&acc)[TM][TN], const char* ra, const char* rb, int wm, int wn,
+                                         int lane) {
+    const int orow = lane & 31, och = lane >> 5;
+#pragma unroll
+    for (int kk = 0; kk < BK / 16; ++kk) {
+        uint4 fa[TM], fb[TN];
+#pragma unroll
+        for (int i = 0; i < TM; ++i) fa[i] = *(const uint4*)(ra + lds_off(wm * 128 + i * 32 + orow, 2 * kk + och));
+#pragma unroll
+        for (int j = 0; j < TN; ++j) fb[j] = *(const uint4*)(rb + lds_off(wn * 128 + j * 32 + orow, 2 * kk + och));
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int j = 0; j < TN; ++j) acc[i][j] = mfma_bf16(fa[i], fb[j], acc[i][j]);
+    }
+}
+
+// K tiles kt0..kt1-1 of one split: the global loads of tile k+1 go out before the MFMAs of tile k
+// (LDS buffer k % 2); after them the staged tile is transposed / decoded into buffer (k+1) % 2.
+template <int MODE, int BITS, bool DB>
+__global__ __launch_bounds__(THREADS, 1) void dw_gemm_kernel(DwArgs a) {
+    __shared__ __attribute__((aligned(1024))) char sA[2][BM * ROWB];
+    __shared__ __attribute__((aligned(1024))) char sB[2][BN * ROWB];
+
+    // workgroup ids go to the 8 XCDs round-robin (id % 8). Work items are numbered
+    // L = (split * tiles_m + tm) * tiles_n + tn and each XCD takes a contiguous range of L, so the
+    // workgroups of one XCD share dy tiles (same split, tm) and x tiles (same split, tn) in its L2.
+    const int tiles_n = (int)(a.N / BN), tiles = (int)(a.M / BM) * tiles_n;
+    const int W = tiles * a.splits, per = (W + DW_XCDS - 1) / DW_XCDS;
+    const int xcd = blockIdx.x % DW_XCDS, local = blockIdx.x / DW_XCDS;
+    if (local >= per) return;
+    const int L = xcd * per + local;
+    if (L >= W) return;
+    const int split = L / tiles, t = L % tiles;
+    const int tm = t / tiles_n, tn = t % tiles_n;
+    const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
+    const int64_t kt0 = (int64_t)split * a.kt_per_split;
+    const int64_t kt1 = min(kt0 + a.kt_per_split, (a.K + BK - 1) / BK);
+    // every workgroup of a DB launch sums its dy tile (a runtime tn == 0 test doubles the
+    // kernel's live registers); the tn == 0 ones store the sums
+    constexpr bool with_db = DB;
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int kb = wave * 2 + (lane >> 5), mb = lane & 31;  // this lane's 8 x 8 producer block
+
+    f32x16_t acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
+    float db[8] = {};
+
+    Stage st;
+    const int64_t nk = kt1 - kt0;
+    if (nk > 0) {
+        load_stage<MODE, BITS>(a, st, kt0 * BK, kb, mb, m0, n0);
+        write_stage<MODE, BITS, with_db>(a, st, sA[0], sB[0], kb, mb, db);
+    }
+    __syncthreads();
+    int cur = 0;
+    for (int64_t k = kt0; k < kt1; ++k) {
+        const bool more = k + 1 < kt1;
+        if (more) load_stage<MODE, BITS>(a, st, (k + 1) * BK, kb, mb, m0, n0);
+        mma_tile(acc, sA[cur], sB[cur], wm, wn, lane);
+        if (more) write_stage<MODE, BITS, with_db>(a, st, sA[cur ^ 1], sB[cur ^ 1], kb, mb, db);
+        __syncthreads();
+        cur ^= 1;
+    }
+
+    // fp32 partial tile of this split
+    float* P = a.partial + (int64_t)split * a.M * a.N;
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+            const int64_t col = n0 + wn * 128 + j * 32 + (lane & 31);
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                const int64_t row = m0 + wm * 128 + i * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+                P[row * a.N + col] = acc[i][j][v];
+            }
+        }
+    if (with_db && tn == 0) {
+        // per-lane sums of its 8 m columns over its k rows -> fixed-order sum over the 8 k blocks
+        float* red = (float*)sA[0];
+#pragma unroll
+        for (int c = 0; c < 8; ++c) red[kb * BM + mb * 8 + c] = db[c];
+        __syncthreads();
+        float sum = 0.0f;
+#pragma unroll
+        for (int q = 0; q < 8; ++q) sum += red[q * BM + tid];
+        a.db_partial[(int64_t)split * a.M + m0 + tid] = sum;
+    }
+}
+
+// out[m][n] = sum over splits, in split order; fp32 and/or bf16; db likewise
+__global__ __launch_bounds__(256) void dw_reduce_kernel(const float* __restrict__ partial, int splits, int64_t MN,
+                                                        float* __restrict__ out32, uint16_t* __restrict__ out16,
+                                                        const float* __restrict__ dbp, int64_t M,
+                                                        float* __restrict__ db) {
+    const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+    if (i < MN) {
+        // splits == 0 (no K) writes zeros
+        float4 s = splits > 0 ? *(const float4*)(partial + i) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        for (int k = 1; k < splits; ++k) {
+            const float4 p = *(const float4*)(partial + (int64_t)k * MN + i);
+            s.x += p.x;
+            s.y += p.y;
+            s.z += p.z;
+            s.w += p.w;
+        }
+        if (out32) *(float4*)(out32 + i) = s;
+        if (out16) *(uint2*)(out16 + i) = make_uint2(pack_bf16x2(s.x, s.y), pack_bf16x2(s.z, s.w));
+    }
+    if (db && dbp && blockIdx.x == 0) {
+        for (int64_t m = threadIdx.x; m < M; m += 256) {
+            float s = splits > 0 ? dbp[m] : 0.0f;
+            for (int k = 1; k < splits; ++k) s += dbp[(int64_t)k * M + m];
+            db[m] = s;
+        }
+    }
+}
+
+}  // namespace
+
+int dw_splits(int64_t M, int64_t N, int64_t K) {
+    const int64_t tiles = std::max<int64_t>((M / BM) * (N / BN), 1);
+    const int64_t kts = (K + BK - 1) / BK;
+    // one round of at most 256 workgroups (one per CU: 128 KB of LDS each)
+    int64_t s = std::max<int64_t>(256 / tiles, 1);
+    s = std::min(s, kts);
+    return (int)std::max<int64_t>(s, 1);
+}
+
+int64_t dw_workspace_floats(int64_t M, int64_t N, int64_t K) {
+    const int s = dw_splits(M, N, K);
+    return (int64_t)s * M * N + (int64_t)s * M;
+}
+
+int launch_dw_gemm(DwArgs a, int mode, bool with_db, float* out32, uint16_t* out16, float* db, hipStream_t st) {
+    const int splits = dw_splits(a.M, a.N, a.K);
+    const int64_t kts = (a.K + BK - 1) / BK;
+    a.kt_per_split = std::max<int64_t>((kts + splits - 1) / splits, 1);
+    const int used = kts ? (int)((kts + a.kt_per_split - 1) / a.kt_per_split) : 0;  // splits with work
+    a.splits = used;
+    a.db_partial = a.partial + (int64_t)splits * a.M * a.N;
+    const int tiles = (int)((a.M / BM) * (a.N / BN));
+    // ids: 8 XCDs x ceil(W / 8) slots; slots past W exit at once
+    const int64_t W = (int64_t)tiles * used;
+    const dim3 grid((unsigned)(DW_XCDS * ((W + DW_XCDS - 1) / DW_XCDS)));
+    if (used > 0) {
+#define DOPT_DW(MODE_, BITS_, DB_) hipLaunchKernelGGL((dw_gemm_kernel<MODE_, BITS_, DB_>), grid, dim3(THREADS), 0, st, a)
+#define DOPT_DW_DB(MODE_, BITS_) \
+    do { if (with_db) DOPT_DW(MODE_, BITS_, true); else DOPT_DW(MODE_, BITS_, false); } while (0)
+    if (mode == DW_B_BF16) DOPT_DW_DB(DW_B_BF16, 0);
+    else if (a.bits == 1) DOPT_DW_DB(DW_B_PACKED, 1);
+    else if (a.bits == 2) DOPT_DW_DB(DW_B_PACKED, 2);
+    else if (a.bits == 4) DOPT_DW_DB(DW_B_PACKED, 4);
+    else DOPT_DW_DB(DW_B_PACKED, 8);
+#undef DOPT_DW_DB
+#undef DOPT_DW
+    }
+    const int64_t MN = a.M * a.N;
+    hipLaunchKernelGGL(dw_reduce_kernel, dim3((unsigned)((MN / 4 + 255) / 256)), dim3(256), 0, st,
+                       (const float*)a.partial, used, MN, out32, out16, (const float*)a.db_partial, a.M,
+                       with_db ? db : nullptr);
+    return 0;
+}
+
+}  // namespace dopt

@@ -10,9 +10,16 @@ quantized with ``clamp=True`` and the layer's ``clamp_alpha`` (the tanh squash o
 applies), an optional DIVISION low-pass (average pool) is stored beside it and added back when
 the input is restored, and under autocast the computation runs in the autocast dtype.
 
+The Linear weight gradient ``dy^T . x_hat`` (and the bias gradient) runs on the gfx950 kernel
+behind ``act_lib::dw_gemm`` when dy is bf16 and both feature counts are multiples of 256; the
+per-layer meta key ``dw_fused_unpack`` (default False) makes that kernel decode the packed codes
+itself instead of reading the dequantized x_hat.
+
 Differences from the reference:
   * ``_DOLinear`` takes the bias and applies it (the reference calls ``F.linear(input, W, None)``
     and never trains the bias, ops.py:481); its gradient is ``dy`` summed over the rows;
+  * on the dw_gemm path the weight gradient comes back in the weight's dtype (fp32 master
+    weights get an fp32 gradient; the reference's is bf16 under autocast);
   * the Conv Functions take an optional bias the same way (the reference's DOConv layers are
     built with ``bias=False``).
 """
@@ -25,6 +32,7 @@ from torch.autograd import Function
 from torch.nn.grad import conv1d_input, conv1d_weight, conv2d_input, conv2d_weight, conv3d_input, conv3d_weight
 from torch.nn.modules.utils import _pair, _single, _triple
 
+from ..dw_lib import dw_gemm_supported
 from .module_utils import unified_dequantize, unified_quantize
 
 
@@ -137,6 +145,11 @@ class _DOLinear(Function):
                                                      clamp_alpha=clamp_alpha)
         ctx.q_inputs_meta = q_meta
         ctx.meta = input.shape, ema_grad_meta, clamp_alpha, bias is not None
+        # the packed codes can feed the weight-gradient GEMM directly when they are the flat
+        # [tokens * in_features] bitstream (no padding, no low-pass, no ALAM)
+        (bits, pack_only, group_size, act_padding, _, _, _, _, _, reshape_elig, _, avg_alam, _, _) = q_meta
+        ctx.fused_unpack = (bool(m.get("dw_fused_unpack", False)) and not (pack_only or act_padding or reshape_elig
+                                                                             or avg_alam) and input_l is None)
         ctx.save_for_backward(weight, q_tensor[0], q_tensor[1], q_tensor[2], input_l)
         return F.linear(input, weight_compute, bias_compute)
 
@@ -151,12 +164,26 @@ class _DOLinear(Function):
             dy = dy.to(dt)
         else:
             weight_compute = weight
-        input = unified_dequantize((q0, q1, q2), ctx.q_inputs_meta, input_l).to(dy.dtype)
-        C_in, C_out = input.shape[-1], dy.shape[-1]
+        C_in, C_out = input_shape[-1], dy.shape[-1]
         dy_flat = dy.reshape(-1, C_out)
-        dw = dy_flat.t().mm(input.reshape(-1, C_in))
+        if dy.dtype == torch.bfloat16 and dw_gemm_supported(C_out, C_in):
+            # weight (and bias) gradient on the gfx950 split-K GEMM for K-outer operands, in the
+            # weight's precision; x_hat is either dequantized first or decoded inside the GEMM
+            out_dtype = weight.dtype if weight.dtype in (torch.float32, torch.bfloat16) else torch.float32
+            if ctx.fused_unpack and q1.dtype == torch.bfloat16:
+                bits, group_size = ctx.q_inputs_meta[0], ctx.q_inputs_meta[2]
+                dw, db = torch.ops.act_lib.dw_gemm(dy_flat, None, q0, q1, q2, C_in, bits, group_size, has_bias,
+                                                   out_dtype)
+                input = None
+            else:
+                input = unified_dequantize((q0, q1, q2), ctx.q_inputs_meta, input_l)
+                dw, db = torch.ops.act_lib.dw_gemm(dy_flat, input.reshape(-1, C_in), None, None, None, C_in, 0, 0,
+                                                   has_bias, out_dtype)
+        else:
+            input = unified_dequantize((q0, q1, q2), ctx.q_inputs_meta, input_l).to(dy.dtype)
+            dw = dy_flat.t().mm(input.reshape(-1, C_in))
+            db = dy_flat.sum(0) if has_bias else None
         dx = dy_flat.mm(weight_compute.to(dy.dtype))
-        db = dy_flat.sum(0) if has_bias else None
         return dx.view(*input_shape), dw, None, None, None, None, db
 
 

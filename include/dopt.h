@@ -246,6 +246,23 @@ int dopt_bn_bwd_dx(int mode, const void* x_hat, const uint32_t* packed, const ui
                    const float* dbias, const float* weight, const float* var, float eps, int var_is_invstd, void* dx,
                    void* stream);
 
+/* ---------------------------------------------------------------- Linear weight gradient
+ * dW[m][n] = sum_k dy[k][m] * x_hat[k][n] (bf16 MFMA, fp32 accumulation) and, when db is not NULL,
+ * db[m] = sum_k dy[k][m]: the weight and bias gradients of a Linear layer with K tokens, M out and
+ * N in features. dy: bf16 [K, ldd] (M columns used). x_hat either bf16 [K, ldx] (x_hat != NULL) or
+ * the quantizer's packed codes of the flat [K*N] activation (packed, scale, minv bf16 per group of
+ * group_size consecutive elements, b bits), decoded in the kernel to bf16(fma(q, scale, min)), the
+ * value dequant_unpack writes. Outputs fp32 dw_f32 and/or bf16 dw_bf16 [M, N] row-major, fp32 db.
+ * The K range is split across workgroups; the fp32 partials go through `workspace`
+ * (dopt_dw_gemm_workspace_floats(M, N, K) floats) and are summed in a fixed order (deterministic).
+ * Requires M % 256 == 0, N % 256 == 0, ldd % 8 == 0, ldx % 8 == 0, 16-byte aligned dy / x_hat.
+ * Replaces, for the compressed Linear layer, the dequantize + `dy_flatten.T.mm(input_flatten)` of
+ * AC/modules/ops.py:508-512 (the reference's Triton fused attempt lives only in test2.ipynb). */
+int64_t dopt_dw_gemm_workspace_floats(int64_t M, int64_t N, int64_t K);
+int dopt_dw_gemm(const void* dy, int64_t ldd, const void* x_hat, int64_t ldx, const uint32_t* packed,
+                 const void* scale, const void* minv, int group_size, int bits, int64_t M, int64_t N, int64_t K,
+                 float* workspace, float* dw_f32, void* dw_bf16, float* db, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -49,12 +49,16 @@ def x_hat_reference(x, bits, g, act_padding):
 
 
 @pytest.mark.parametrize("bits", [2, 4, 8])
-@pytest.mark.parametrize("shape,autocast", [((4, 197, 768), True), ((512, 1024), True), ((4, 197, 768), False)],
-                         ids=["3d-bf16", "2d-bf16", "3d-fp32"])
-def test_do_linear(bits, shape, autocast):
+@pytest.mark.parametrize("shape,autocast,cout,fused", [
+    ((4, 197, 768), True, 384, False), ((512, 1024), True, 384, False), ((4, 197, 768), False, 384, False),
+    ((4, 197, 768), True, 512, False), ((4, 197, 768), True, 512, True), ((600, 256), True, 256, True)],
+    ids=["3d-bf16", "2d-bf16", "3d-fp32", "3d-bf16-dwgemm", "3d-bf16-dwgemm-fused", "2d-bf16-dwgemm-fused"])
+def test_do_linear(bits, shape, autocast, cout, fused):
+    """Shapes with in/out features multiples of 256 run the weight gradient on act_lib::dw_gemm (fp32
+    result), with the packed codes decoded inside the GEMM when ``dw_fused_unpack`` is set."""
     torch.manual_seed(bits)
-    cin, cout = shape[-1], 384
-    layer = DOLinear(cin, cout, target_name="fc", meta=meta_for("fc", shape, bits)).to(DEV).train()
+    cin = shape[-1]
+    layer = DOLinear(cin, cout, target_name="fc", meta=meta_for("fc", shape, bits, dw_fused_unpack=fused)).to(DEV).train()
     x = (torch.randn(shape, device=DEV) * 2).requires_grad_(True)
     dy = torch.randn(*shape[:-1], cout, device=DEV)
     with torch.autocast("cuda", dtype=torch.bfloat16, enabled=autocast):
