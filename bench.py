@@ -213,7 +213,9 @@ def vit_train_step(torch, dev, batch=128, steps=6, warmup=3):
         torch.cuda.empty_cache()
     p, c = res["plain"], res["compressed_2bit"]
     res["compressed_vs_plain"] = {"step_time_ratio": round(c["ms_per_step"] / p["ms_per_step"], 3),
-                                  "peak_hbm_ratio": round(c["peak_hbm_GiB"] / p["peak_hbm_GiB"], 3)}
+                                  "peak_hbm_ratio": round(c["peak_hbm_GiB"] / p["peak_hbm_GiB"], 3),
+                                  "peak_above_resident_ratio": round(c["peak_above_resident_GiB"]
+                                                                     / p["peak_above_resident_GiB"], 3)}
     return res
 
 
