@@ -250,6 +250,177 @@ __global__ __launch_bounds__(THREADS, 1) void dw_gemm_kernel(DwArgs a) {
     }
 }
 
+// ------------------------------------------------------------------ v2: bf16 operands, no transposes
+// Tiles go HBM -> LDS with global_load_lds (no registers, no VALU) in their natural [k][m] /
+// [k][n] layout, through a ring of V2_STAGES stages of V2_BK tokens, V2_STAGES - 1 tiles ahead.
+// The MFMA operands are read with ds_read_b64_tr_b16, whose 16-lane groups transpose a 4 x 16
+// block: lane 4p+q of a group receives element q of the 8-byte reads of lanes p, p+4, p+8, p+12.
+// Source lane 4u+v of group g reads row (k0 + 8*(g/2) + 4h + u), 4 columns at 16*(g%2) + 4v of the
+// fragment, so MFMA lane l receives column l % 32 at 4 consecutive k; reads h = 0, 1 give its 8.
+// LDS rows are 512 bytes (256 bf16); 16-byte chunk c of row r sits at position c ^ (4 * (r % 4)),
+// which puts the 4 rows of a transposing read on 4 distinct 64-byte bank groups.
+constexpr int V2_BK = 32, V2_STAGES = 4;
+constexpr int V2_ROWB = 512;                    // bytes per LDS row (256 bf16)
+constexpr int V2_TILE = V2_BK * V2_ROWB;        // bytes of one operand tile (16 KB)
+
+typedef short v4i16_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) v4i16_t lds_v4i16_t;
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(1))) const void gbl_void_t;
+
+__device__ __forceinline__ int v2_pos(int r, int c) { return (c ^ ((r & 3) << 2)) << 4; }
+
+// s_waitcnt vmcnt(n) (expcnt / lgkmcnt left at their maxima: no wait on them)
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+// 8 bf16 of one MFMA operand: column `col` of the stage tile (lane's column within the 32-wide
+// fragment applied by the transpose), rows kk*16 + 8*(g/2) + {0..7}
+__device__ __forceinline__ uint4 v2_frag(const char* tile, int kk, int col0, int lane) {
+    const int g = lane >> 4, t = lane & 15, u = t >> 2, v = t & 3;
+    const int colw = col0 + 16 * (g & 1) + 4 * v;  // first of the 4 columns this lane reads
+    uint4 out;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const int r = kk * 16 + 8 * (g >> 1) + 4 * h + u;
+        const char* p = tile + r * V2_ROWB + v2_pos(r, colw >> 3) + ((colw & 4) << 1);
+        const v4i16_t x = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t*)p);
+        const uint32_t lo = (uint32_t)(uint16_t)x[0] | ((uint32_t)(uint16_t)x[1] << 16);
+        const uint32_t hi = (uint32_t)(uint16_t)x[2] | ((uint32_t)(uint16_t)x[3] << 16);
+        if (h == 0) {
+            out.x = lo;
+            out.y = hi;
+        } else {
+            out.z = lo;
+            out.w = hi;
+        }
+    }
+    return out;
+}
+
+template <bool DB>
+__global__ __launch_bounds__(THREADS, 1) void dw_gemm_v2_kernel(DwArgs a) {
+    __shared__ __attribute__((aligned(1024))) char sm[V2_STAGES * 2 * V2_TILE];
+
+    const int tiles_n = (int)(a.N / BN), tiles = (int)(a.M / BM) * tiles_n;
+    const int W = tiles * a.splits, per = (W + DW_XCDS - 1) / DW_XCDS;
+    const int xcd = blockIdx.x % DW_XCDS, local = blockIdx.x / DW_XCDS;
+    if (local >= per) return;
+    const int L = xcd * per + local;
+    if (L >= W) return;
+    const int split = L / tiles, t = L % tiles;
+    const int tm = t / tiles_n, tn = t % tiles_n;
+    const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
+    const int64_t kt0 = (int64_t)split * a.kt_per_split;
+    const int64_t kt1 = min(kt0 + a.kt_per_split, a.K / V2_BK);
+    const int nk = (int)(kt1 - kt0);
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+
+    // global -> LDS: instruction j of wave w fills 1 KB block b = 4j + w of a tile = rows 2b, 2b+1;
+    // lane l -> row 2b + l/32, position l % 32 <- global chunk (l % 32) ^ (4 * (row % 4))
+    auto issue = [&](int stage, int64_t kt) {
+        char* sa = sm + stage * 2 * V2_TILE;
+        char* sb = sa + V2_TILE;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int b = 4 * j + wave, r = 2 * b + (lane >> 5), c = (lane & 31) ^ ((r & 3) << 2);
+            const int64_t k = kt * V2_BK + r;
+            __builtin_amdgcn_global_load_lds((gbl_void_t*)(a.dy + k * a.ldd + m0 + c * 8),
+                                             (lds_void_t*)(sa + b * 1024), 16, 0, 0);
+            __builtin_amdgcn_global_load_lds((gbl_void_t*)(a.xh + k * a.ldx + n0 + c * 8),
+                                             (lds_void_t*)(sb + b * 1024), 16, 0, 0);
+        }
+    };
+
+    f32x16_t acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
+    // bias gradient: thread t sums rows 4*(t/32) .. +3 of the dy tile in its 8 columns 8*(t%32) ..
+    // +7; column block t % 32 belongs to the workgroup with tn == (t % 32) % tiles_n, so the
+    // workgroups sharing a dy tile split its columns between them
+    float dbs[8] = {};
+    const int dcb = tid & 31, drg = tid >> 5;
+    const bool db_owner = DB && (dcb % tiles_n) == tn;
+
+#pragma unroll
+    for (int s = 0; s < V2_STAGES - 1; ++s)
+        if (s < nk) issue(s, kt0 + s);
+    for (int i = 0; i < nk; ++i) {
+        // tile i's loads (issued V2_STAGES - 1 tiles ago) done; later tiles' may stay in flight
+        const int ahead = min(nk - 1 - i, V2_STAGES - 2);
+        if (ahead >= 2) wait_vm<16>();
+        else if (ahead == 1) wait_vm<8>();
+        else wait_vm<0>();
+        __syncthreads();  // every wave's loads of tile i landed; every wave done with tile i-1
+        if (i + V2_STAGES - 1 < nk) issue((i + V2_STAGES - 1) % V2_STAGES, kt0 + i + V2_STAGES - 1);
+        const char* sa = sm + (i % V2_STAGES) * 2 * V2_TILE;
+        const char* sb = sa + V2_TILE;
+#pragma unroll
+        for (int kk = 0; kk < V2_BK / 16; ++kk) {
+            uint4 fa[TM], fb[TN];
+#pragma unroll
+            for (int ii = 0; ii < TM; ++ii) fa[ii] = v2_frag(sa, kk, wm * 128 + ii * 32, lane);
+#pragma unroll
+            for (int jj = 0; jj < TN; ++jj) fb[jj] = v2_frag(sb, kk, wn * 128 + jj * 32, lane);
+#pragma unroll
+            for (int ii = 0; ii < TM; ++ii)
+#pragma unroll
+                for (int jj = 0; jj < TN; ++jj) acc[ii][jj] = mfma_bf16(fa[ii], fb[jj], acc[ii][jj]);
+        }
+        if constexpr (DB) {
+            if (db_owner) {
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const int r = 4 * drg + q;
+                    const uint4 x = *(const uint4*)(sa + r * V2_ROWB + v2_pos(r, dcb));
+                    const uint32_t w[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) {
+                        dbs[2 * c] += __uint_as_float(w[c] << 16);
+                        dbs[2 * c + 1] += __uint_as_float(w[c] & 0xffff0000u);
+                    }
+                }
+            }
+        }
+    }
+
+    float* P = a.partial + (int64_t)split * a.M * a.N;
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+            const int64_t col = n0 + wn * 128 + j * 32 + (lane & 31);
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                const int64_t row = m0 + wm * 128 + i * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+                P[row * a.N + col] = acc[i][j][v];
+            }
+        }
+    if constexpr (DB) {
+        // fixed-order sum over the 8 row groups, through LDS (the stages are no longer read)
+        __syncthreads();
+        float* red = (float*)sm;
+#pragma unroll
+        for (int c = 0; c < 8; ++c) red[drg * BM + dcb * 8 + c] = dbs[c];
+        __syncthreads();
+        if (((tid >> 3) % tiles_n) == tn) {
+            float sum = 0.0f;
+#pragma unroll
+            for (int q = 0; q < 8; ++q) sum += red[q * BM + tid];
+            a.db_partial[(int64_t)split * a.M + m0 + tid] = sum;
+        }
+    }
+}
+
 // out[m][n] = sum over splits, in split order; fp32 and/or bf16; db likewise
 __global__ __launch_bounds__(256) void dw_reduce_kernel(const float* __restrict__ partial, int splits, int64_t MN,
                                                         float* __restrict__ out32, uint16_t* __restrict__ out16,
@@ -296,6 +467,25 @@ int64_t dw_workspace_floats(int64_t M, int64_t N, int64_t K) {
 
 int launch_dw_gemm(DwArgs a, int mode, bool with_db, float* out32, uint16_t* out16, float* db, hipStream_t st) {
     const int splits = dw_splits(a.M, a.N, a.K);
+    if (mode == DW_B_BF16 && a.K > 0 && a.K % V2_BK == 0) {
+        // the transpose-free kernel: 32-token tiles, split at the same token boundaries as the
+        // 64-token kernel, so both accumulate the same 16-token MFMA steps in the same order
+        const int64_t kts = a.K / V2_BK;
+        const int64_t kts64 = (a.K + BK - 1) / BK;
+        a.kt_per_split = std::max<int64_t>((kts64 + splits - 1) / splits, 1) * (BK / V2_BK);
+        const int used = (int)((kts + a.kt_per_split - 1) / a.kt_per_split);
+        a.splits = used;
+        a.db_partial = a.partial + (int64_t)splits * a.M * a.N;
+        const int64_t W = (a.M / BM) * (a.N / BN) * used;
+        const dim3 grid((unsigned)(DW_XCDS * ((W + DW_XCDS - 1) / DW_XCDS)));
+        if (with_db) hipLaunchKernelGGL((dw_gemm_v2_kernel<true>), grid, dim3(THREADS), 0, st, a);
+        else hipLaunchKernelGGL((dw_gemm_v2_kernel<false>), grid, dim3(THREADS), 0, st, a);
+        const int64_t MN = a.M * a.N;
+        hipLaunchKernelGGL(dw_reduce_kernel, dim3((unsigned)((MN / 4 + 255) / 256)), dim3(256), 0, st,
+                           (const float*)a.partial, used, MN, out32, out16, (const float*)a.db_partial, a.M,
+                           with_db ? db : nullptr);
+        return 0;
+    }
     const int64_t kts = (a.K + BK - 1) / BK;
     a.kt_per_split = std::max<int64_t>((kts + splits - 1) / splits, 1);
     const int used = kts ? (int)((kts + a.kt_per_split - 1) / a.kt_per_split) : 0;  // splits with work

@@ -6,7 +6,9 @@ Bar:
     terms' magnitudes (fp32 accumulation over up to 25k terms) plus 1e-6;
   * the packed path bit-exact equal to the bf16 path fed with act_lib::dequant_unpack_triton's
     x_hat (itself bit-exact against the CPU oracle): the in-kernel decode produces the same bf16
-    values and the kernel sums in the same order;
+    values, and both kernels (register-transposing with in-kernel decode, and LDS-transposing for
+    bf16 operands) split K at the same token boundaries and accumulate the same 16-token MFMA
+    steps in the same order;
   * the bf16 output is the round-to-nearest-even of the fp32 output; repeated calls are bit-equal.
 """
 import pytest
@@ -60,7 +62,8 @@ def test_packed_operand_equals_dequantized(bits, g, K, M, N):
     got, gdb = ops.dw_gemm(dy, None, packed, scale, xmin, N, bits, g, True, torch.float32)
     torch.cuda.synchronize()
     assert torch.equal(got, want)
-    assert torch.equal(gdb, wdb)
+    # db: both sum the same dy, in the two kernels' own orders
+    assert bool(((gdb.double() - wdb.double()).abs() <= 1e-4 * dy.double().abs().sum(0) + 1e-6).all())
     check_close(got, dy, x_hat)
 
 
