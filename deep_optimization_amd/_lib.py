@@ -40,6 +40,8 @@ EXPORTS = (
     "dopt_bn_bwd_dx",
     "dopt_dw_gemm_workspace_floats",
     "dopt_dw_gemm",
+    "dopt_graph_node_counts",
+    "dopt_graph_replace_memsets",
 )
 
 _lib = None
@@ -103,6 +105,10 @@ def lib() -> ctypes.CDLL:
         L.dopt_dw_gemm_workspace_floats.restype = i64
         L.dopt_dw_gemm.argtypes = [vp, i64, vp, i64, vp, vp, vp, i32, i32, i64, i64, i64, vp, vp, vp, vp, vp]
         L.dopt_dw_gemm.restype = i32
+        L.dopt_graph_node_counts.argtypes = [vp, vp, i32]
+        L.dopt_graph_node_counts.restype = i32
+        L.dopt_graph_replace_memsets.argtypes = [vp, vp]
+        L.dopt_graph_replace_memsets.restype = i32
         _lib = L
     return _lib
 

@@ -27,6 +27,7 @@ SOURCES = [
     "act_fused.hip",
     "bn_fused.hip",
     "dw_gemm.hip",
+    "graph_tools.hip",
 ]
 
 ARCH = "gfx950"

@@ -19,6 +19,8 @@ int launch_fp8_gemm_nt(const uint8_t* A, const uint8_t* B, int64_t M, int64_t N,
 int launch_relu_pack(const void* x, int dt, void* y, uint32_t* packed, uint64_t n, int bits, bool relu6, hipStream_t s);
 int launch_relu_unpack(const uint32_t* packed, const void* dy, int dyt, void* dx, uint64_t n, int bits, hipStream_t s);
 int launch_act_forward(const void* x, int dt, void* y, void* aux, uint64_t n, int act, hipStream_t s);
+const char* graph_node_counts(hipGraph_t g, int64_t* counts, int n_counts);
+const char* graph_replace_memsets(hipGraph_t g, int64_t* replaced);
 }  // namespace dopt
 
 namespace {
@@ -558,3 +560,19 @@ int dopt_dw_gemm(const void* dy, int64_t ldd, const void* x_hat, int64_t ldx, co
 }
 
 }  // extern "C"
+
+int dopt_graph_node_counts(void* graph, int64_t* counts, int n_counts) {
+    if (!graph || (!counts && n_counts > 0) || n_counts < 0) return fail(DOPT_EINVAL, "null graph or counts");
+    for (int i = 0; i < n_counts; ++i) counts[i] = 0;
+    if (const char* e = dopt::graph_node_counts((hipGraph_t)graph, counts, n_counts))
+        return fail(DOPT_EHIP, "graph_node_counts: %s failed", e);
+    return ok();
+}
+
+int dopt_graph_replace_memsets(void* graph, int64_t* n_replaced) {
+    if (!graph || !n_replaced) return fail(DOPT_EINVAL, "null graph or n_replaced");
+    *n_replaced = 0;
+    if (const char* e = dopt::graph_replace_memsets((hipGraph_t)graph, n_replaced))
+        return fail(DOPT_EHIP, "graph_replace_memsets: %s failed after %lld replacements", e, (long long)*n_replaced);
+    return ok();
+}

@@ -263,6 +263,24 @@ int dopt_dw_gemm(const void* dy, int64_t ldd, const void* x_hat, int64_t ldx, co
                  const void* scale, const void* minv, int group_size, int bits, int64_t M, int64_t N, int64_t K,
                  float* workspace, float* dw_f32, void* dw_bf16, float* db, void* stream);
 
+/*
+ * HIP graph tools for capturing a whole training step (forward, backward, optimizer step) as
+ * Activation_Compression/cuda_graph_utils.py:82-120 (`Graph.capture_cuda_graph_qdrop`) does.
+ * `graph` is a captured, not yet instantiated hipGraph_t passed as void* (torch:
+ * `torch.cuda.CUDAGraph(keep_graph=True).raw_cuda_graph()` after capture).
+ *
+ * dopt_graph_node_counts: counts[t] = number of nodes of hipGraphNodeType t (child graphs' nodes
+ * included) for t < n_counts; other types are not counted.
+ *
+ * dopt_graph_replace_memsets: replaces every memset node (the record of a hipMemsetAsync made
+ * during capture, by this library's caller or by any library it calls) with a kernel node that
+ * writes the same bytes, with the same dependencies and dependents; *n_replaced = number
+ * replaced. Call it before the graph is instantiated. (Memset nodes in replayed graphs are
+ * avoided on this platform; this library's own entry points issue none.)
+ */
+int dopt_graph_node_counts(void* graph, int64_t* counts, int n_counts);
+int dopt_graph_replace_memsets(void* graph, int64_t* n_replaced);
+
 #ifdef __cplusplus
 }
 #endif
