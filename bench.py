@@ -9,8 +9,11 @@ public torch operators. `value` is algorithmic bytes per step / wall time per st
     unpack = 2/8 B + 8 B per group + 2 B (bf16 out) per element
 The JSON line also carries the dominant kernel's roofline (quant-pack, HIP-event timed on the
 stream it is launched on), the CPU oracle timed on the host cores (cpu_baseline), and extras:
-the Philox and nearest rounding modes of the same step, the ViT MLP bit-width sweep (config 3),
-the FP8 GEMM (config 4) beside hipBLASLt on the same data, and a HIP-graph replay of the step.
+the Philox and nearest rounding modes of the same step, a HIP-graph replay of the step, the ViT
+MLP bit-width sweep (config 3), the fused activation layers, the FP8 GEMM (config 4) beside
+hipBLASLt on the same data, the compressed Linear layers' weight-gradient GEMM at the ViT-B/16
+shapes, the compressed BatchNorm layer, and the ViT-B/16 train step (config 5): plain vs 2-bit,
+and the captured weight-noise step replayed from one HIP graph vs run eagerly.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-extras] [--no-cpu]
        python bench.py --pmc-probe   (one copy kernel + the dominant kernel, for rocprofv3 --pmc)
@@ -31,11 +34,17 @@ if ROOT not in sys.path:
 
 HBM_PEAK_GBS = 8000.0
 FP8_PEAK_TFLOPS = 5000.0
+BF16_PEAK_TFLOPS = 2500.0
 METRIC = "quant-pack+unpack GB/s (% HBM peak) at 2-bit; FP8 GEMM TFLOPS (% peak)"
 PMC_SUMMARY = os.path.join(ROOT, "profiles", "quant_pack_resnet_noise_pmc.md")
 N, C, H, W = 256, 256, 56, 56
 G_SIZE, BITS = 256, 2
 NEAREST, NOISE, PHILOX = 0, 1, 2
+
+
+def progress(msg: str) -> None:
+    """A progress line on stderr (the JSON result is the only stdout line)."""
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
 def pack_bytes(n_elem, n_groups, in_bytes, bits, noise=False):
@@ -384,6 +393,7 @@ def main() -> int:
                                         "ms_per_step": round(s_ * 1e3, 4), "bytes_per_step": b_,
                                         "pack_kernel_us": round(t_k * 1e6, 2),
                                         "pack_kernel_frac": round(pb_plain / t_k / 1e9 / HBM_PEAK_GBS, 4)}
+        progress("graph replay of the step")
         # the same step replayed from a HIP graph (host dispatch removed)
         try:
             gs = torch.cuda.Stream()
@@ -405,6 +415,7 @@ def main() -> int:
             extras["resnet_noise_graph_replay"] = {"error": str(e)[:200]}
         del packed, scale, xmin, y
         torch.cuda.empty_cache()
+        progress("ViT MLP sweep")
         # config 3: ViT-B/16 MLP activation, GELU(N(0,1)) bf16 [256,197,3072], group 128, 1/2/4/8 bits,
         # stochastic rounding from the Philox stream
         vg = torch.Generator(device=dev).manual_seed(2)
@@ -422,6 +433,7 @@ def main() -> int:
                                 "packed_bytes": ve * b // 8 + vng * 8, "compression_vs_bf16": round(ve * 2 / (ve * b / 8 + vng * 8), 2),
                                 "ms_per_step": round(st * 1e3, 4)}
         extras["vit_mlp_sweep_philox_g128"] = sweep
+        progress("fused activation layers")
         # fused activation layers: GELU / SiLU (y + 2-bit quantized derivative, g = 128, bf16
         # scale/min) on the ViT MLP activation, ReLU (y + 1-bit mask) on the ResNet activation;
         # bytes per element: forward in + y + codes (+ 4 B per group), backward codes (+ 4 B per
@@ -456,6 +468,7 @@ def main() -> int:
         del o, dyr
         extras["fused_activation_layers"] = fused
         torch.cuda.empty_cache()
+        progress("FP8 GEMM")
         # config 4: FP8 e4m3 scaled GEMM, beside hipBLASLt (torch._scaled_mm) on the same operands
         gemm = {}
         for (M, Nn, K) in ((8192, 8192, 8192), (4096, 11008, 4096)):
@@ -485,15 +498,55 @@ def main() -> int:
             gemm[f"{M}x{Nn}x{K}"] = entry
             del a8, b8, cm
         extras["fp8_gemm_nt"] = gemm
+        progress("weight-gradient GEMM")
+        # the compressed Linear layers' weight gradient dW = dy^T x_hat (+ db = sum dy) at the ViT-B/16
+        # bs-128 shapes (K = 25216 tokens), 2-bit activations: the reference chain (dequantize, then
+        # torch's GEMM and bias sum), hipBLASLt alone on x_hat, act_lib::dw_gemm on x_hat (with and
+        # without the fused bias gradient) and on the packed codes (decoded inside the GEMM)
+        dwx = {}
+        Kt = 128 * 197
+        for lname, cin, cout, gsz in (("qkv", 768, 2304, 256), ("proj", 768, 768, 256), ("fc1", 768, 3072, 256),
+                                      ("fc2", 3072, 768, 512)):
+            gd = torch.Generator(device=dev).manual_seed(7)
+            xa = torch.randn((128, 197, cin), generator=gd, device=dev).to(torch.bfloat16)
+            dyd = torch.randn((Kt, cout), generator=gd, device=dev).to(torch.bfloat16)
+            pk, sc, mn = ops.quant_pack_triton(xa.view(128, -1, gsz), 2, gsz, False, 0, True, 3.0)
+            xh = ops.dequant_unpack_triton(pk, sc, mn, 2, gsz, False, 0).view(Kt, cin)
+            fl = 2.0 * Kt * cin * cout
+            t = {"reference_chain": event_avg(lambda: (dyd.t().mm(ops.dequant_unpack_triton(pk, sc, mn, 2, gsz, False, 0)
+                                                                   .view(Kt, cin)), dyd.sum(0)), reps=10),
+                 "hipblaslt_mm": event_avg(lambda: dyd.t().mm(xh), reps=10),
+                 "dw_gemm": event_avg(lambda: ops.dw_gemm(dyd, xh, None, None, None, cin, 0, 0, False, torch.bfloat16),
+                                      reps=10),
+                 "dw_gemm_db": event_avg(lambda: ops.dw_gemm(dyd, xh, None, None, None, cin, 0, 0, True, torch.bfloat16),
+                                         reps=10),
+                 "layer_dequant_dw_gemm_db": event_avg(
+                     lambda: ops.dw_gemm(dyd, ops.dequant_unpack_triton(pk, sc, mn, 2, gsz, False, 0).view(Kt, cin), None,
+                                         None, None, cin, 0, 0, True, torch.bfloat16), reps=10),
+                 "packed_dw_gemm_db": event_avg(lambda: ops.dw_gemm(dyd, None, pk, sc, mn, cin, 2, gsz, True,
+                                                                    torch.bfloat16), reps=10)}
+            dwx[f"{lname}_{cout}x{cin}x{Kt}"] = {
+                **{f"{k}_us": round(v * 1e6, 1) for k, v in t.items()},
+                "dw_gemm_TFLOP/s": round(fl / t["dw_gemm"] / 1e12, 1),
+                "dw_gemm_frac_bf16_peak": round(fl / t["dw_gemm"] / 1e12 / BF16_PEAK_TFLOPS, 4),
+                "hipblaslt_TFLOP/s": round(fl / t["hipblaslt_mm"] / 1e12, 1),
+                "layer_vs_reference_chain": round(t["reference_chain"] / t["layer_dequant_dw_gemm_db"], 3)}
+            del xa, dyd, pk, sc, mn, xh
+        extras["dw_gemm_vit_b16_bs128_2bit"] = dwx
         torch.cuda.empty_cache()
+        torch.cuda.empty_cache()
+        progress("BatchNorm layer")
         extras["batchnorm_resnet_2bit"] = batchnorm_layer(torch, dev, event_avg)
         torch.cuda.empty_cache()
+        progress("ViT-B/16 train step")
         extras["vit_b16_train_step_bs128"] = vit_train_step(torch, dev)
         torch.cuda.empty_cache()
+        progress("ViT-B/16 captured qdrop step")
         extras["vit_b16_qdrop_step_bs128_graph"] = vit_qdrop_graph_step(torch, dev)
         out["extras"] = extras
 
     if not args.no_cpu:
+        progress("CPU baseline")
         import numpy as np
 
         import oracle

@@ -421,32 +421,83 @@ __global__ __launch_bounds__(THREADS, 1) void dw_gemm_v2_kernel(DwArgs a) {
     }
 }
 
-// out[m][n] = sum over splits, in split order; fp32 and/or bf16; db likewise
+// out[m][n] = sum of the split partials; fp32 and/or bf16; db likewise. SUB consecutive lanes
+// share one 4-wide output: lane j sums splits [j*per, (j+1)*per) in order, 4 loads in flight,
+// and the SUB partial sums are combined by an xor butterfly, which gives every lane the same
+// value (fp32 addition is commutative) and fixes the order: the result depends on the split
+// count only, never on timing. Thread t < M also sums db[t] over the splits in order.
+__device__ __forceinline__ void add4(float4& s, const float4& p) {
+    s.x += p.x;
+    s.y += p.y;
+    s.z += p.z;
+    s.w += p.w;
+}
+
+template <int SUB>
 __global__ __launch_bounds__(256) void dw_reduce_kernel(const float* __restrict__ partial, int splits, int64_t MN,
                                                         float* __restrict__ out32, uint16_t* __restrict__ out16,
                                                         const float* __restrict__ dbp, int64_t M,
                                                         float* __restrict__ db) {
-    const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+    const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int64_t i = (t / SUB) * 4;
+    const int j = (int)(t % SUB);
+    const int per = (splits + SUB - 1) / SUB;
+    const int k0 = min(j * per, splits), k1 = min(k0 + per, splits);
+    float4 s = make_float4(0.0f, 0.0f, 0.0f, 0.0f);  // splits == 0 (no K) writes zeros
     if (i < MN) {
-        // splits == 0 (no K) writes zeros
-        float4 s = splits > 0 ? *(const float4*)(partial + i) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        for (int k = 1; k < splits; ++k) {
-            const float4 p = *(const float4*)(partial + (int64_t)k * MN + i);
-            s.x += p.x;
-            s.y += p.y;
-            s.z += p.z;
-            s.w += p.w;
+        int k = k0;
+        for (; k + 3 < k1; k += 4) {
+            const float4 p0 = *(const float4*)(partial + (int64_t)k * MN + i);
+            const float4 p1 = *(const float4*)(partial + (int64_t)(k + 1) * MN + i);
+            const float4 p2 = *(const float4*)(partial + (int64_t)(k + 2) * MN + i);
+            const float4 p3 = *(const float4*)(partial + (int64_t)(k + 3) * MN + i);
+            add4(s, p0);
+            add4(s, p1);
+            add4(s, p2);
+            add4(s, p3);
         }
+        for (; k < k1; ++k) add4(s, *(const float4*)(partial + (int64_t)k * MN + i));
+    }
+    // all lanes of the wave take part in the butterfly (SUB divides 64 and the grid is whole waves)
+#pragma unroll
+    for (int m = 1; m < SUB; m <<= 1) {
+        s.x += __shfl_xor(s.x, m);
+        s.y += __shfl_xor(s.y, m);
+        s.z += __shfl_xor(s.z, m);
+        s.w += __shfl_xor(s.w, m);
+    }
+    if (i < MN && j == 0) {
         if (out32) *(float4*)(out32 + i) = s;
         if (out16) *(uint2*)(out16 + i) = make_uint2(pack_bf16x2(s.x, s.y), pack_bf16x2(s.z, s.w));
     }
-    if (db && dbp && blockIdx.x == 0) {
-        for (int64_t m = threadIdx.x; m < M; m += 256) {
-            float s = splits > 0 ? dbp[m] : 0.0f;
-            for (int k = 1; k < splits; ++k) s += dbp[(int64_t)k * M + m];
-            db[m] = s;
+    if (db && t < M) {
+        float d = splits > 0 ? dbp[t] : 0.0f;
+        int k = 1;
+        for (; k + 3 < splits; k += 4) {
+            const float p0 = dbp[(int64_t)k * M + t], p1 = dbp[(int64_t)(k + 1) * M + t];
+            const float p2 = dbp[(int64_t)(k + 2) * M + t], p3 = dbp[(int64_t)(k + 3) * M + t];
+            d += p0;
+            d += p1;
+            d += p2;
+            d += p3;
         }
+        for (; k < splits; ++k) d += dbp[(int64_t)k * M + t];
+        db[t] = d;
     }
+}
+
+// one launch of the reduce: SUB lanes per output for a wide split count (more loads in flight)
+void launch_dw_reduce(const float* partial, int used, int64_t MN, float* out32, uint16_t* out16, const float* dbp,
+                      int64_t M, float* db, hipStream_t st) {
+    const int sub = used > 16 ? 8 : used > 8 ? 4 : used > 4 ? 2 : 1;
+    const int64_t threads = std::max<int64_t>(MN / 4 * sub, M);
+    const dim3 grid((unsigned)((threads + 255) / 256));
+#define DOPT_RED(S_) hipLaunchKernelGGL(dw_reduce_kernel<S_>, grid, dim3(256), 0, st, partial, used, MN, out32, out16, dbp, M, db)
+    if (sub == 8) DOPT_RED(8);
+    else if (sub == 4) DOPT_RED(4);
+    else if (sub == 2) DOPT_RED(2);
+    else DOPT_RED(1);
+#undef DOPT_RED
 }
 
 }  // namespace
@@ -480,10 +531,7 @@ int launch_dw_gemm(DwArgs a, int mode, bool with_db, float* out32, uint16_t* out
         const dim3 grid((unsigned)(DW_XCDS * ((W + DW_XCDS - 1) / DW_XCDS)));
         if (with_db) hipLaunchKernelGGL((dw_gemm_v2_kernel<true>), grid, dim3(THREADS), 0, st, a);
         else hipLaunchKernelGGL((dw_gemm_v2_kernel<false>), grid, dim3(THREADS), 0, st, a);
-        const int64_t MN = a.M * a.N;
-        hipLaunchKernelGGL(dw_reduce_kernel, dim3((unsigned)((MN / 4 + 255) / 256)), dim3(256), 0, st,
-                           (const float*)a.partial, used, MN, out32, out16, (const float*)a.db_partial, a.M,
-                           with_db ? db : nullptr);
+        launch_dw_reduce(a.partial, used, a.M * a.N, out32, out16, a.db_partial, a.M, with_db ? db : nullptr, st);
         return 0;
     }
     const int64_t kts = (a.K + BK - 1) / BK;
@@ -507,10 +555,7 @@ int launch_dw_gemm(DwArgs a, int mode, bool with_db, float* out32, uint16_t* out
 #undef DOPT_DW_DB
 #undef DOPT_DW
     }
-    const int64_t MN = a.M * a.N;
-    hipLaunchKernelGGL(dw_reduce_kernel, dim3((unsigned)((MN / 4 + 255) / 256)), dim3(256), 0, st,
-                       (const float*)a.partial, used, MN, out32, out16, (const float*)a.db_partial, a.M,
-                       with_db ? db : nullptr);
+    launch_dw_reduce(a.partial, used, a.M * a.N, out32, out16, a.db_partial, a.M, with_db ? db : nullptr, st);
     return 0;
 }
 

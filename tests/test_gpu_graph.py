@@ -14,7 +14,6 @@ What is pinned and how:
     weights come back to their values (one fp32 add and subtract).
 """
 import ctypes
-import os
 
 import pytest
 import torch
