@@ -259,11 +259,12 @@ __global__ __launch_bounds__(THREADS, 1) void dw_gemm_kernel(DwArgs a) {
 // fragment, so MFMA lane l receives column l % 32 at 4 consecutive k; reads h = 0, 1 give its 8.
 // LDS rows are 512 bytes (256 bf16); 16-byte chunk c of row r sits at position c ^ (4 * (r % 4)),
 // which puts the 4 rows of a transposing read on 4 distinct 64-byte bank groups.
-constexpr int V2_BK = 32, V2_STAGES = 4;
+constexpr int V2_BK = 32;
 constexpr int V2_ROWB = 512;                    // bytes per LDS row (256 bf16)
 constexpr int V2_TILE = V2_BK * V2_ROWB;        // bytes of one operand tile (16 KB)
 
 typedef short v4i16_t __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef __attribute__((address_space(3))) v4i16_t lds_v4i16_t;
 typedef __attribute__((address_space(3))) void lds_void_t;
 typedef __attribute__((address_space(1))) const void gbl_void_t;
@@ -301,9 +302,38 @@ __device__ __forceinline__ uint4 v2_frag(const char* tile, int kk, int col0, int
     return out;
 }
 
+// s_waitcnt vmcnt(n) lgkmcnt(0): this wave's loads older than the n most recent have landed and
+// its LDS reads have returned
+template <int N>
+__device__ __forceinline__ void wait_vm_lds() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4));
+}
+
+// workgroup barrier without the memory fence of __syncthreads (whose release would wait for every
+// in-flight global -> LDS load); the asm's memory clobber keeps the compiler from moving memory
+// operations across it, the waits before it are explicit
+__device__ __forceinline__ void barrier_only() { asm volatile("s_barrier" ::: "memory"); }
+
+// Pipeline, per 32-token slab i (stage i % 4: one LDS object for its A tile, one for its B tile):
+//   operand reads of slab i, second 16 tokens | MFMAs of slab i, first 16 tokens (read one step
+//   earlier) | wait: own loads of slab i+1 landed, own LDS reads returned | barrier |
+//   issue loads of slab i+4 into stage i % 4 | operand reads of slab i+1, first 16 tokens |
+//   MFMAs of slab i, second 16 tokens
+// Three slabs stay in flight behind the one being multiplied; every step issues exactly one slab
+// (indices past the split's last slab reload the last one, which nobody reads), so the wait count
+// is the same in every step. Each stage's A and B tiles are separate LDS objects, so the compiler
+// can tell which in-flight load an operand read depends on and waits for that one only.
 template <bool DB>
 __global__ __launch_bounds__(THREADS, 1) void dw_gemm_v2_kernel(DwArgs a) {
-    __shared__ __attribute__((aligned(1024))) char sm[V2_STAGES * 2 * V2_TILE];
+    __shared__ __attribute__((aligned(1024))) char sa0[V2_TILE];
+    __shared__ __attribute__((aligned(1024))) char sa1[V2_TILE];
+    __shared__ __attribute__((aligned(1024))) char sa2[V2_TILE];
+    __shared__ __attribute__((aligned(1024))) char sa3[V2_TILE];
+    __shared__ __attribute__((aligned(1024))) char sb0[V2_TILE];
+    __shared__ __attribute__((aligned(1024))) char sb1[V2_TILE];
+    __shared__ __attribute__((aligned(1024))) char sb2[V2_TILE];
+    __shared__ __attribute__((aligned(1024))) char sb3[V2_TILE];
 
     const int tiles_n = (int)(a.N / BN), tiles = (int)(a.M / BM) * tiles_n;
     const int W = tiles * a.splits, per = (W + DW_XCDS - 1) / DW_XCDS;
@@ -322,18 +352,31 @@ __global__ __launch_bounds__(THREADS, 1) void dw_gemm_v2_kernel(DwArgs a) {
     const int wm = wave >> 1, wn = wave & 1;
 
     // global -> LDS: instruction j of wave w fills 1 KB block b = 4j + w of a tile = rows 2b, 2b+1;
-    // lane l -> row 2b + l/32, position l % 32 <- global chunk (l % 32) ^ (4 * (row % 4))
-    auto issue = [&](int stage, int64_t kt) {
-        char* sa = sm + stage * 2 * V2_TILE;
-        char* sb = sa + V2_TILE;
+    // lane l -> row 2b + l/32, position l % 32 <- global chunk (l % 32) ^ (4 * (row % 4)).
+    // The LDS offsets carry `opaque0`, a zero the compiler cannot see through: its wait insertion
+    // checks an operand read against one recorded load per LDS object, and a read it can prove
+    // disjoint from that load's bytes would otherwise wait for every load in flight.
+    // The global address is a wave-uniform slab base plus a loop-invariant 32-bit lane offset.
+    int opaque0;
+    asm volatile("s_mov_b32 %0, 0" : "=s"(opaque0));
+    uint32_t offa[4], offb[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int r = 2 * (4 * j + wave) + (lane >> 5), c = (lane & 31) ^ ((r & 3) << 2);
+        offa[j] = (uint32_t)(r * a.ldd + c * 8) * 2u;
+        offb[j] = (uint32_t)(r * a.ldx + c * 8) * 2u;
+    }
+    auto issue = [&](char* sa, char* sb, int64_t kt) {
+        kt = min(kt, kt1 - 1);
+        const char* ga = (const char*)(a.dy + kt * V2_BK * a.ldd + m0);
+        const char* gb = (const char*)(a.xh + kt * V2_BK * a.ldx + n0);
+        char* da = sa + opaque0;
+        char* db = sb + opaque0;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            const int b = 4 * j + wave, r = 2 * b + (lane >> 5), c = (lane & 31) ^ ((r & 3) << 2);
-            const int64_t k = kt * V2_BK + r;
-            __builtin_amdgcn_global_load_lds((gbl_void_t*)(a.dy + k * a.ldd + m0 + c * 8),
-                                             (lds_void_t*)(sa + b * 1024), 16, 0, 0);
-            __builtin_amdgcn_global_load_lds((gbl_void_t*)(a.xh + k * a.ldx + n0 + c * 8),
-                                             (lds_void_t*)(sb + b * 1024), 16, 0, 0);
+            const int b = 4 * j + wave;
+            __builtin_amdgcn_global_load_lds((gbl_void_t*)(ga + offa[j]), (lds_void_t*)(da + b * 1024), 16, 0, 0);
+            __builtin_amdgcn_global_load_lds((gbl_void_t*)(gb + offb[j]), (lds_void_t*)(db + b * 1024), 16, 0, 0);
         }
     };
 
@@ -344,54 +387,78 @@ __global__ __launch_bounds__(THREADS, 1) void dw_gemm_v2_kernel(DwArgs a) {
         for (int j = 0; j < TN; ++j)
 #pragma unroll
             for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
-    // bias gradient: thread t sums rows 4*(t/32) .. +3 of the dy tile in its 8 columns 8*(t%32) ..
-    // +7; column block t % 32 belongs to the workgroup with tn == (t % 32) % tiles_n, so the
-    // workgroups sharing a dy tile split its columns between them
-    float dbs[8] = {};
-    const int dcb = tid & 31, drg = tid >> 5;
-    const bool db_owner = DB && (dcb % tiles_n) == tn;
-
+    // bias gradient from the dy fragments already in registers: lane l of fragment ii holds
+    // column (l % 32) at 8 consecutive tokens as 4 bf16 pairs, and one v_dot2 with (1, 1) adds a
+    // pair. Only the waves with wn == 0 of the workgroups with tn == 0 (one per dy tile) sum.
+    float dbacc[TM] = {};
+    const bool db_wave = DB && tn == 0 && wn == 0;
+    uint4 fa0[TM], fb0[TN], fa1[TM], fb1[TN];
+    auto read_frags = [&](const char* sa, const char* sb, int kk, uint4* fa, uint4* fb) {
 #pragma unroll
-    for (int s = 0; s < V2_STAGES - 1; ++s)
-        if (s < nk) issue(s, kt0 + s);
-    for (int i = 0; i < nk; ++i) {
-        // tile i's loads (issued V2_STAGES - 1 tiles ago) done; later tiles' may stay in flight
-        const int ahead = min(nk - 1 - i, V2_STAGES - 2);
-        if (ahead >= 2) wait_vm<16>();
-        else if (ahead == 1) wait_vm<8>();
-        else wait_vm<0>();
-        __syncthreads();  // every wave's loads of tile i landed; every wave done with tile i-1
-        if (i + V2_STAGES - 1 < nk) issue((i + V2_STAGES - 1) % V2_STAGES, kt0 + i + V2_STAGES - 1);
-        const char* sa = sm + (i % V2_STAGES) * 2 * V2_TILE;
-        const char* sb = sa + V2_TILE;
+        for (int ii = 0; ii < TM; ++ii) fa[ii] = v2_frag(sa, kk, wm * 128 + ii * 32, lane);
 #pragma unroll
-        for (int kk = 0; kk < V2_BK / 16; ++kk) {
-            uint4 fa[TM], fb[TN];
+        for (int jj = 0; jj < TN; ++jj) fb[jj] = v2_frag(sb, kk, wn * 128 + jj * 32, lane);
+    };
+    auto mma = [&](const uint4* fa, const uint4* fb) {
 #pragma unroll
-            for (int ii = 0; ii < TM; ++ii) fa[ii] = v2_frag(sa, kk, wm * 128 + ii * 32, lane);
+        for (int ii = 0; ii < TM; ++ii)
 #pragma unroll
-            for (int jj = 0; jj < TN; ++jj) fb[jj] = v2_frag(sb, kk, wn * 128 + jj * 32, lane);
+            for (int jj = 0; jj < TN; ++jj) acc[ii][jj] = mfma_bf16(fa[ii], fb[jj], acc[ii][jj]);
+        if (db_wave) {
+            const bf16x2_t one = __builtin_bit_cast(bf16x2_t, 0x3f803f80u);
 #pragma unroll
-            for (int ii = 0; ii < TM; ++ii)
+            for (int ii = 0; ii < TM; ++ii) {
+                const uint32_t w[4] = {fa[ii].x, fa[ii].y, fa[ii].z, fa[ii].w};
 #pragma unroll
-                for (int jj = 0; jj < TN; ++jj) acc[ii][jj] = mfma_bf16(fa[ii], fb[jj], acc[ii][jj]);
-        }
-        if constexpr (DB) {
-            if (db_owner) {
-#pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    const int r = 4 * drg + q;
-                    const uint4 x = *(const uint4*)(sa + r * V2_ROWB + v2_pos(r, dcb));
-                    const uint32_t w[4] = {x.x, x.y, x.z, x.w};
-#pragma unroll
-                    for (int c = 0; c < 4; ++c) {
-                        dbs[2 * c] += __uint_as_float(w[c] << 16);
-                        dbs[2 * c + 1] += __uint_as_float(w[c] & 0xffff0000u);
-                    }
-                }
+                for (int q = 0; q < 4; ++q)
+                    dbacc[ii] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, w[q]), one, dbacc[ii], false);
             }
         }
+    };
+    constexpr int NM = TM * TN;            // MFMAs per 16 tokens
+    constexpr int NR = 2 * (TM + TN);      // transposing reads per 16 tokens
+    auto step = [&](char* ca, char* cb, char* na, char* nb, int i) {
+        read_frags(ca, cb, 1, fa1, fb1);
+        mma(fa0, fb0);
+#pragma unroll
+        for (int q = 0; q < NR; ++q) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
+        }
+        wait_vm_lds<16>();
+        barrier_only();
+        issue(ca, cb, kt0 + i + 4);
+        read_frags(na, nb, 0, fa0, fb0);
+        mma(fa1, fb1);
+#pragma unroll
+        for (int q = 0; q < NM; ++q) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
+            if (q < 8) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // one global load
+        }
+    };
+
+    if (nk > 0) {
+        issue(sa0, sb0, kt0);
+        issue(sa1, sb1, kt0 + 1);
+        issue(sa2, sb2, kt0 + 2);
+        issue(sa3, sb3, kt0 + 3);
+        wait_vm_lds<24>();
+        barrier_only();
+        read_frags(sa0, sb0, 0, fa0, fb0);
+        int i = 0;
+        for (; i + 4 <= nk; i += 4) {
+            step(sa0, sb0, sa1, sb1, i);
+            step(sa1, sb1, sa2, sb2, i + 1);
+            step(sa2, sb2, sa3, sb3, i + 2);
+            step(sa3, sb3, sa0, sb0, i + 3);
+        }
+        if (i < nk) step(sa0, sb0, sa1, sb1, i);
+        if (i + 1 < nk) step(sa1, sb1, sa2, sb2, i + 1);
+        if (i + 2 < nk) step(sa2, sb2, sa3, sb3, i + 2);
     }
+    // the trailing (unused) loads land before LDS is reused below
+    __builtin_amdgcn_s_waitcnt(0);
 
     float* P = a.partial + (int64_t)split * a.M * a.N;
 #pragma unroll
@@ -405,18 +472,12 @@ __global__ __launch_bounds__(THREADS, 1) void dw_gemm_v2_kernel(DwArgs a) {
                 P[row * a.N + col] = acc[i][j][v];
             }
         }
-    if constexpr (DB) {
-        // fixed-order sum over the 8 row groups, through LDS (the stages are no longer read)
-        __syncthreads();
-        float* red = (float*)sm;
+    if (db_wave) {
+        // lanes l and l + 32 hold the two token halves of column l % 32
 #pragma unroll
-        for (int c = 0; c < 8; ++c) red[drg * BM + dcb * 8 + c] = dbs[c];
-        __syncthreads();
-        if (((tid >> 3) % tiles_n) == tn) {
-            float sum = 0.0f;
-#pragma unroll
-            for (int q = 0; q < 8; ++q) sum += red[q * BM + tid];
-            a.db_partial[(int64_t)split * a.M + m0 + tid] = sum;
+        for (int ii = 0; ii < TM; ++ii) {
+            const float other = __shfl_xor(dbacc[ii], 32);
+            if (lane < 32) a.db_partial[(int64_t)split * a.M + m0 + wm * 128 + ii * 32 + lane] = dbacc[ii] + other;
         }
     }
 }
