@@ -17,6 +17,7 @@ and the captured weight-noise step replayed from one HIP graph vs run eagerly.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-extras] [--no-cpu]
        python bench.py --pmc-probe   (one copy kernel + the dominant kernel, for rocprofv3 --pmc)
+       python bench.py --fp8-probe random|constant   (the 8192^3 FP8 GEMM alone, for rocprofv3 --pmc)
 """
 from __future__ import annotations
 
@@ -99,6 +100,50 @@ def pmc_probe() -> int:
                                               xmin.data_ptr(), _lib.F32, stream), "quant_pack")
     torch.cuda.synchronize()
     print(f"pmc probe: copy {x.numel() * 2} B, then 3 x quant_pack (noise, bf16, g={G_SIZE}, {BITS}-bit)")
+    return 0
+
+
+def fp8_probe(mode: str) -> int:
+    """The 8192^3 FP8 GEMM, 3 + 10 launches, on the bench's N(0,1) -> e4m3 operands ("random") or on
+    constant operands ("constant": every A byte 0x38 = 1.0, every B byte 0x30 = 0.5), for
+    rocprofv3 --pmc runs that compare clock (GRBM_GUI_ACTIVE) and MFMA occupancy between the two."""
+    import torch
+
+    import deep_optimization_amd  # noqa: F401
+    from deep_optimization_amd import _lib
+
+    dev = torch.device("cuda:0")
+    M = Nn = K = 8192
+    if mode == "constant":
+        a8 = torch.full((M, K), 0x38, dtype=torch.uint8, device=dev)
+        b8 = torch.full((Nn, K), 0x30, dtype=torch.uint8, device=dev)
+        osc = 1.0
+    else:
+        gg = torch.Generator(device=dev).manual_seed(3)
+        a = torch.randn((M, K), generator=gg, device=dev)
+        bm = torch.randn((Nn, K), generator=gg, device=dev)
+        sa, sb = 448.0 / a.abs().max(), 448.0 / bm.abs().max()
+        a8 = (a * sa).to(torch.float8_e4m3fn).view(torch.uint8)
+        b8 = (bm * sb).to(torch.float8_e4m3fn).view(torch.uint8)
+        osc = float(1.0 / (sa * sb))
+        del a, bm
+    cm = torch.empty((M, Nn), dtype=torch.bfloat16, device=dev)
+    L = _lib.lib()
+    stream = torch.cuda.current_stream(dev)
+
+    def launch():
+        _lib.check(L.dopt_fp8_gemm_nt(a8.data_ptr(), b8.data_ptr(), M, Nn, K, K, K, osc, cm.data_ptr(), Nn,
+                                      stream.cuda_stream), "fp8_gemm")
+    for _ in range(3):
+        launch()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(10):
+        launch()
+    e1.record(stream)
+    e1.synchronize()
+    us = e0.elapsed_time(e1) / 10 * 1e3
+    print(f"fp8 probe ({mode}): {us:.1f} us per launch, {2.0 * M * Nn * K / us / 1e6:.0f} TFLOP/s")
     return 0
 
 
@@ -285,6 +330,7 @@ def main() -> int:
     ap.add_argument("--no-extras", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--pmc-probe", action="store_true")
+    ap.add_argument("--fp8-probe", choices=("random", "constant"))
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}). "
@@ -293,6 +339,8 @@ def main() -> int:
         return 2
     if args.pmc_probe:
         return pmc_probe()
+    if args.fp8_probe:
+        return fp8_probe(args.fp8_probe)
 
     import torch
 
