@@ -215,16 +215,26 @@ __global__ __launch_bounds__(256) void quant_pack_kernel(QuantPackArgs a) {
             for (int l = 0; l < LOADS; ++l) widen16<DT>(raw[p][i][l], &v[i][l * E16]);
         if constexpr (PRE == PRE_REF) {
             if (a.flags & FL_CLAMP) {
+                // one v_med3 per element equals fminf(fmaxf(x, -alpha), alpha) for alpha >= 0,
+                // NaN x included (med3 of a NaN and two numbers is their minimum, here -alpha)
+                const float al = a.clamp_alpha;
+                if (al >= 0.0f) {
 #pragma unroll
-                for (int i = 0; i < CPL; ++i)
+                    for (int i = 0; i < CPL; ++i)
 #pragma unroll
-                    for (int k = 0; k < UE; ++k) v[i][k] = fminf(fmaxf(v[i][k], -a.clamp_alpha), a.clamp_alpha);
+                        for (int k = 0; k < UE; ++k) v[i][k] = __builtin_amdgcn_fmed3f(v[i][k], -al, al);
+                } else {
+#pragma unroll
+                    for (int i = 0; i < CPL; ++i)
+#pragma unroll
+                        for (int k = 0; k < UE; ++k) v[i][k] = fminf(fmaxf(v[i][k], -al), al);
+                }
             }
             if (a.flags & FL_SQUASH) {
 #pragma unroll
                 for (int i = 0; i < CPL; ++i)
 #pragma unroll
-                    for (int k = 0; k < UE; ++k) v[i][k] = tanhf(v[i][k] / 0.5f) * 0.5f;
+                    for (int k = 0; k < UE; ++k) v[i][k] = squash_half_tanh2(v[i][k]);
             }
         } else if constexpr (PRE == PRE_GELU || PRE == PRE_SILU) {
             // activation value (stored bf16) and its squashed derivative (quantized)
