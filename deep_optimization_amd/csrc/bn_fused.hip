@@ -281,7 +281,7 @@ __device__ __forceinline__ void fwd_block(const BnFwdArgs& a, int64_t c, int64_t
             for (int k = 0; k < EPL; ++k) {
                 const bool on = relu6 ? (y[k] > 0.0f && y[k] < 6.0f) : (y[k] > 0.0f);
                 m8 |= (uint32_t)on << k;
-                y[k] = relu6 ? fminf(fmaxf(y[k], 0.0f), 6.0f) : (on ? y[k] : 0.0f);
+                y[k] = relu6 ? __builtin_amdgcn_fmed3f(y[k], 0.0f, 6.0f) : (on ? y[k] : 0.0f);
             }
         }
         if (active) store8_bf16<VEC>(a.y, g, c, e0, M, y);
@@ -293,8 +293,7 @@ __device__ __forceinline__ void fwd_block(const BnFwdArgs& a, int64_t c, int64_t
 #pragma unroll
         for (int k = 0; k < EPL; ++k) {
             if constexpr (MODE == BN_QUANT) {
-                const float cl = fminf(fmaxf(xh[k], -3.0f), 3.0f);
-                t[k] = fast_tanh(cl * 0.5f) * 2.0f;
+                t[k] = two_tanh_half_fast(__builtin_amdgcn_fmed3f(xh[k], -3.0f, 3.0f));
             } else {
                 t[k] = xh[k];
             }
@@ -312,13 +311,13 @@ __device__ __forceinline__ void fwd_block(const BnFwdArgs& a, int64_t c, int64_t
             const float invs = 1.0f / step;
 #pragma unroll
             for (int k = 0; k < EPL; ++k) {
-                const float qf = fminf(fmaxf(fmaf(t[k] - mn, invs, half_m), 0.0f), qmaxf);
+                const float qf = __builtin_amdgcn_fmed3f(fmaf(t[k] - mn, invs, half_m), 0.0f, qmaxf);
                 q[k] = (int)qf;
             }
         } else {
 #pragma unroll
             for (int k = 0; k < EPL; ++k) {
-                const float qf = fminf(fmaxf((t[k] - mn) / step + half_m, 0.0f), qmaxf);
+                const float qf = __builtin_amdgcn_fmed3f((t[k] - mn) / step + half_m, 0.0f, qmaxf);
                 q[k] = (int)qf;
             }
         }

@@ -151,21 +151,35 @@ __device__ __forceinline__ float fast_sigmoid(float x) {
 // (AC/modules/activations/kernel_implementation.py:496-519): u = a (x + b x^3), t = tanh(u),
 // y = x (1 + t) / 2, dy/dx = (1 + t)/2 + x (1 - t^2) a (1 + 3 b x^2) / 2. Evaluated through
 // s = (1 + t)/2 = sigmoid(2u) and 1 - t^2 = 4 s (1 - s), the same function without the
-// cancellation of 1 + t for x below about -4 (where an fp32 tanh is already -1).
+// cancellation of 1 + t for x below about -4 (where an fp32 tanh is already -1):
+// u = x (a + a b x^2), s = 1 / (1 + 2^(-2 log2(e) u)), dy/dx = s + x s (1 - s) (2a + 6ab x^2).
 __device__ __forceinline__ void gelu_and_grad(float x, float& y, float& d) {
-    const float a = 0.7978845608028654f, b = 0.044715f, b3 = 0.134145f;
+    const float a = 0.7978845608028654f, ab = 0.7978845608028654f * 0.044715f;
     const float x2 = x * x;
-    const float u = a * __builtin_fmaf(b * x2, x, x);
-    const float s = fast_sigmoid(2.0f * u);
+    const float u = x * __builtin_fmaf(ab, x2, a);
+    const float s = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-2.8853900817779268f * u));
     y = x * s;
-    d = __builtin_fmaf(2.0f * x * s * (1.0f - s), a * __builtin_fmaf(b3, x2, 1.0f), s);
+    const float c = __builtin_fmaf(6.0f * ab, x2, 2.0f * a);
+    d = __builtin_fmaf(y * (1.0f - s), c, s);
 }
 // SiLU value and derivative (kernel_implementation.py:225-229): s = sigmoid(x), y = x s,
 // dy/dx = s + x s (1 - s)
 __device__ __forceinline__ void silu_and_grad(float x, float& y, float& d) {
     const float s = fast_sigmoid(x);
     y = x * s;
-    d = __builtin_fmaf(x * s, 1.0f - s, s);
+    d = __builtin_fmaf(y, 1.0f - s, s);
+}
+// 2 tanh(x / 2) of BatchNorm's squash, the exp form of fast_tanh with the two scalings folded in
+// (bit-identical to fast_tanh(x * 0.5) * 2)
+__device__ __forceinline__ float two_tanh_half_fast(float x) {
+    const float e = __builtin_amdgcn_exp2f(-1.4426950408889634f * fabsf(x));
+    return copysignf(__builtin_fmaf(-2.0f, e, 2.0f) * __builtin_amdgcn_rcpf(1.0f + e), x);
+}
+// tanh(2d) / 2 of a clamped activation derivative, the exp form of fast_tanh with the two
+// scalings folded in (bit-identical to fast_tanh(2d) * 0.5: both scalings are powers of two)
+__device__ __forceinline__ float half_tanh2_fast(float d) {
+    const float e = __builtin_amdgcn_exp2f(-5.7707801635558535f * fabsf(d));
+    return copysignf(__builtin_fmaf(-0.5f, e, 0.5f) * __builtin_amdgcn_rcpf(1.0f + e), d);
 }
 
 // ------------------------------------------------------------------ Philox4x32-10

@@ -249,8 +249,7 @@ __global__ __launch_bounds__(256) void quant_pack_kernel(QuantPackArgs a) {
                         gelu_and_grad(v[i][k], yv[k], d);
                     else
                         silu_and_grad(v[i][k], yv[k], d);
-                    d = fminf(fmaxf(d, -3.0f), 3.0f);
-                    v[i][k] = fast_tanh(d * 2.0f) * 0.5f;
+                    v[i][k] = half_tanh2_fast(__builtin_amdgcn_fmed3f(d, -3.0f, 3.0f));
                 }
                 if (r < a.n_groups) {
 #pragma unroll
@@ -347,7 +346,7 @@ __global__ __launch_bounds__(256) void quant_pack_kernel(QuantPackArgs a) {
                         qf = qf - 0.5f;
                         qf = __builtin_rintf(qf);
                     }
-                    if constexpr (CL) qf = fminf(fmaxf(qf, 0.0f), qmaxf);  // NaN -> 0, as the reference's clamp
+                    if constexpr (CL) qf = __builtin_amdgcn_fmed3f(qf, 0.0f, qmaxf);  // NaN -> 0, as the reference's clamp
                     q[k] = cvt_u32(qf);
                 }
                 // UBITS code bits of this unit, little-endian

@@ -232,6 +232,31 @@ def test_special_values_bit_exact():
         assert_quant_equal(gpu, ref, rounding)
 
 
+@pytest.mark.parametrize("alpha", [3.0, 0.0, -1.0])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=["bf16", "f32"])
+def test_special_values_clamped_bit_exact(alpha, dtype):
+    """The clamp pre-transform (clamp(x, -alpha, alpha), then nearest codes) on NaN, +-inf,
+    signed zeros, subnormals and values beyond alpha: bit-exact against the oracle's
+    fminf(fmaxf(x, -alpha), alpha), which sends NaN to -alpha (the kernel's v_med3 path for
+    alpha >= 0, its min/max path for a negative alpha)."""
+    g = 256
+    x = make_input((1, 8, g), torch.float32, seed=6) * 4
+    x[0, 0, 3] = float("inf")
+    x[0, 1, 7] = float("-inf")
+    x[0, 2, 11] = float("nan")
+    x[0, 2, 12] = float("nan")
+    x[0, 3, :] = -0.0
+    x[0, 3, 5] = 0.0
+    x[0, 4, :] = 1e-40
+    x[0, 4, 9] = -3e-40
+    x[0, 5, :] = float("nan")  # a group of NaN only: every value becomes -alpha
+    x = x.to(dtype)
+    for bits in (2, 8):
+        gpu = gpu_quant(x, bits, g, "nearest", clamp=True, alpha=alpha)
+        ref = oracle_quant(x, bits, g, "nearest", flags=1, alpha=alpha)
+        assert_quant_equal(gpu, ref, f"{bits}-bit alpha={alpha}")
+
+
 def test_empty_and_single_group():
     x = torch.zeros((0, 4, 256), dtype=torch.bfloat16, device=DEV)
     p, s, m = torch.ops.act_lib.quant_pack(x, 2, 256, False, 0.0, False, 0, None, 0, 0, torch.float32)
