@@ -324,8 +324,28 @@ __device__ __forceinline__ void barrier_only() { asm volatile("s_barrier" ::: "m
 // (indices past the split's last slab reload the last one, which nobody reads), so the wait count
 // is the same in every step. Each stage's A and B tiles are separate LDS objects, so the compiler
 // can tell which in-flight load an operand read depends on and waits for that one only.
-template <bool DB>
+//
+// BITS = 0: x_hat is bf16 and its tiles arrive by DMA like dy's. BITS = 1, 2, 4: x_hat is the
+// quantizer's packed codes. A slab's codes (32 rows x 256 columns x BITS bits) and, per decoding
+// thread, the dwords holding its group's bf16 scale and min arrive by DMA into a ring of 4 code
+// slots with the slab's dy. Each step's wait covers the loads issued two steps before, and in the
+// step before a slab is multiplied every thread decodes its 32 values of it, bf16(fma(q, scale,
+// min)) as dequant_unpack writes them, into the slab's B stage, beside that step's MFMAs; the
+// step's barrier publishes the stage.
+// Thread t decodes row t / 8, columns 32 (t % 8) .. +31: 32 consecutive elements of the flat
+// activation, inside one group (g >= 64), whose codes are BITS consecutive words.
+template <int BITS>
+struct V2Codes {
+    static constexpr int NC = BITS == 2 ? 2 : 1;             // code DMAs per thread per slab
+    static constexpr int CODE_BYTES = BITS ? 1024 * BITS : 0;  // codes of one slab
+    static constexpr int SLOT = BITS ? CODE_BYTES + 2048 : 16;  // + scale and min dwords (4 B per thread each)
+    static constexpr int LOADS = BITS ? 4 + NC + 2 : 8;        // DMAs per thread per step
+};
+
+template <int BITS, bool DB>
 __global__ __launch_bounds__(THREADS, 1) void dw_gemm_v2_kernel(DwArgs a) {
+    static_assert(BITS == 0 || BITS == 1 || BITS == 2 || BITS == 4, "bf16, or 1/2/4-bit codes");
+    using CS = V2Codes<BITS>;
     __shared__ __attribute__((aligned(1024))) char sa0[V2_TILE];
     __shared__ __attribute__((aligned(1024))) char sa1[V2_TILE];
     __shared__ __attribute__((aligned(1024))) char sa2[V2_TILE];
@@ -334,6 +354,10 @@ __global__ __launch_bounds__(THREADS, 1) void dw_gemm_v2_kernel(DwArgs a) {
     __shared__ __attribute__((aligned(1024))) char sb1[V2_TILE];
     __shared__ __attribute__((aligned(1024))) char sb2[V2_TILE];
     __shared__ __attribute__((aligned(1024))) char sb3[V2_TILE];
+    __shared__ __attribute__((aligned(1024))) char sc0[CS::SLOT];
+    __shared__ __attribute__((aligned(1024))) char sc1[CS::SLOT];
+    __shared__ __attribute__((aligned(1024))) char sc2[CS::SLOT];
+    __shared__ __attribute__((aligned(1024))) char sc3[CS::SLOT];
 
     const int tiles_n = (int)(a.N / BN), tiles = (int)(a.M / BM) * tiles_n;
     const int W = tiles * a.splits, per = (W + DW_XCDS - 1) / DW_XCDS;
@@ -353,10 +377,10 @@ __global__ __launch_bounds__(THREADS, 1) void dw_gemm_v2_kernel(DwArgs a) {
 
     // global -> LDS: instruction j of wave w fills 1 KB block b = 4j + w of a tile = rows 2b, 2b+1;
     // lane l -> row 2b + l/32, position l % 32 <- global chunk (l % 32) ^ (4 * (row % 4)).
+    // The global address is a wave-uniform slab base plus a loop-invariant 32-bit lane offset.
     // The LDS offsets carry `opaque0`, a zero the compiler cannot see through: its wait insertion
     // checks an operand read against one recorded load per LDS object, and a read it can prove
     // disjoint from that load's bytes would otherwise wait for every load in flight.
-    // The global address is a wave-uniform slab base plus a loop-invariant 32-bit lane offset.
     int opaque0;
     asm volatile("s_mov_b32 %0, 0" : "=s"(opaque0));
     uint32_t offa[4], offb[4];
@@ -366,17 +390,85 @@ __global__ __launch_bounds__(THREADS, 1) void dw_gemm_v2_kernel(DwArgs a) {
         offa[j] = (uint32_t)(r * a.ldd + c * 8) * 2u;
         offb[j] = (uint32_t)(r * a.ldx + c * 8) * 2u;
     }
-    auto issue = [&](char* sa, char* sb, int64_t kt) {
+    // packed x_hat: this thread's decode row and column run, and its flat element offset in a slab
+    const int br = tid >> 3, bj = tid & 7;
+    const int64_t e_lane = (int64_t)br * a.N + 32 * bj;
+    const uint32_t offc = (uint32_t)((e_lane >> 5) * BITS * 4);  // byte offset of its code words
+    auto issue = [&](char* sa, char* sb, char* sc, int64_t kt) {
         kt = min(kt, kt1 - 1);
         const char* ga = (const char*)(a.dy + kt * V2_BK * a.ldd + m0);
-        const char* gb = (const char*)(a.xh + kt * V2_BK * a.ldx + n0);
         char* da = sa + opaque0;
-        char* db = sb + opaque0;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int b = 4 * j + wave;
-            __builtin_amdgcn_global_load_lds((gbl_void_t*)(ga + offa[j]), (lds_void_t*)(da + b * 1024), 16, 0, 0);
-            __builtin_amdgcn_global_load_lds((gbl_void_t*)(gb + offb[j]), (lds_void_t*)(db + b * 1024), 16, 0, 0);
+        for (int j = 0; j < 4; ++j)
+            __builtin_amdgcn_global_load_lds((gbl_void_t*)(ga + offa[j]), (lds_void_t*)(da + (4 * j + wave) * 1024), 16,
+                                             0, 0);
+        if constexpr (BITS == 0) {
+            const char* gb = (const char*)(a.xh + kt * V2_BK * a.ldx + n0);
+            char* db = sb + opaque0;
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                __builtin_amdgcn_global_load_lds((gbl_void_t*)(gb + offb[j]), (lds_void_t*)(db + (4 * j + wave) * 1024),
+                                                 16, 0, 0);
+        } else {
+            const int64_t e0 = kt * V2_BK * a.N + n0;  // a multiple of 256
+            const char* gc = (const char*)a.packed + (e0 >> 5) * BITS * 4;
+            char* dc = sc + opaque0;
+            if constexpr (BITS == 4) {
+                __builtin_amdgcn_global_load_lds((gbl_void_t*)(gc + offc), (lds_void_t*)(dc + wave * 1024), 16, 0, 0);
+            } else {
+#pragma unroll
+                for (int d = 0; d < CS::NC; ++d)
+                    __builtin_amdgcn_global_load_lds((gbl_void_t*)(gc + offc + 4 * d),
+                                                     (lds_void_t*)(dc + d * 1024 + wave * 256), 4, 0, 0);
+            }
+            // the dwords holding this thread's group's bf16 scale and min
+            const int64_t gi = (e0 + e_lane) >> a.lg;
+            __builtin_amdgcn_global_load_lds((gbl_void_t*)((const char*)a.scale + (gi >> 1) * 4),
+                                             (lds_void_t*)(dc + CS::CODE_BYTES + wave * 256), 4, 0, 0);
+            __builtin_amdgcn_global_load_lds((gbl_void_t*)((const char*)a.minv + (gi >> 1) * 4),
+                                             (lds_void_t*)(dc + CS::CODE_BYTES + 1024 + wave * 256), 4, 0, 0);
+        }
+    };
+    // packed x_hat: slab kt's codes, scale and min from slot sc (LDS reads), then chunk c (8
+    // values, one 16-byte LDS chunk) decoded into its B stage sb
+    struct DecodeIn {
+        uint32_t w[BITS ? BITS : 1];
+        float scl, mnv;
+    };
+    auto decode_load = [&](const char* sc, int64_t kt) {
+        DecodeIn d{};
+        if constexpr (BITS != 0) {
+            kt = min(kt, kt1 - 1);
+            const int hi = (int)(((kt * V2_BK * a.N + n0 + e_lane) >> a.lg) & 1);
+            const uint32_t sw = *(const uint32_t*)(sc + CS::CODE_BYTES + tid * 4);
+            const uint32_t mw = *(const uint32_t*)(sc + CS::CODE_BYTES + 1024 + tid * 4);
+            d.scl = __uint_as_float(hi ? (sw & 0xffff0000u) : (sw << 16));
+            d.mnv = __uint_as_float(hi ? (mw & 0xffff0000u) : (mw << 16));
+            if constexpr (BITS == 4) {
+                const uint4 x = *(const uint4*)(sc + tid * 16);
+                d.w[0] = x.x;
+                d.w[1] = x.y;
+                d.w[2] = x.z;
+                d.w[3] = x.w;
+            } else {
+#pragma unroll
+                for (int q = 0; q < BITS; ++q) d.w[q] = *(const uint32_t*)(sc + q * 1024 + tid * 4);
+            }
+        }
+        return d;
+    };
+    auto decode_chunk = [&](const DecodeIn& d, char* sb, int c) {
+        if constexpr (BITS != 0) {
+            constexpr uint32_t qm = (1u << BITS) - 1u;
+            uint32_t o[4];
+#pragma unroll
+            for (int h = 0; h < 4; ++h) {
+                const int e = 8 * c + 2 * h;
+                const uint32_t q0 = (d.w[(e * BITS) >> 5] >> ((e * BITS) & 31)) & qm;
+                const uint32_t q1 = (d.w[((e + 1) * BITS) >> 5] >> (((e + 1) * BITS) & 31)) & qm;
+                o[h] = pack_bf16x2(fmaf((float)q0, d.scl, d.mnv), fmaf((float)q1, d.scl, d.mnv));
+            }
+            *(uint4*)(sb + br * V2_ROWB + v2_pos(br, 4 * bj + c)) = make_uint4(o[0], o[1], o[2], o[3]);
         }
     };
 
@@ -392,6 +484,7 @@ __global__ __launch_bounds__(THREADS, 1) void dw_gemm_v2_kernel(DwArgs a) {
     // pair. Only the waves with wn == 0 of the workgroups with tn == 0 (one per dy tile) sum.
     float dbacc[TM] = {};
     const bool db_wave = DB && tn == 0 && wn == 0;
+
     uint4 fa0[TM], fb0[TN], fa1[TM], fb1[TN];
     auto read_frags = [&](const char* sa, const char* sb, int kk, uint4* fa, uint4* fb) {
 #pragma unroll
@@ -399,65 +492,100 @@ __global__ __launch_bounds__(THREADS, 1) void dw_gemm_v2_kernel(DwArgs a) {
 #pragma unroll
         for (int jj = 0; jj < TN; ++jj) fb[jj] = v2_frag(sb, kk, wn * 128 + jj * 32, lane);
     };
-    auto mma = [&](const uint4* fa, const uint4* fb) {
-#pragma unroll
-        for (int ii = 0; ii < TM; ++ii)
-#pragma unroll
-            for (int jj = 0; jj < TN; ++jj) acc[ii][jj] = mfma_bf16(fa[ii], fb[jj], acc[ii][jj]);
+    // bias-gradient pairs of fragment row ii
+    auto db_row = [&](const uint4* fa, int ii) {
         if (db_wave) {
             const bf16x2_t one = __builtin_bit_cast(bf16x2_t, 0x3f803f80u);
+            const uint32_t w[4] = {fa[ii].x, fa[ii].y, fa[ii].z, fa[ii].w};
 #pragma unroll
-            for (int ii = 0; ii < TM; ++ii) {
-                const uint32_t w[4] = {fa[ii].x, fa[ii].y, fa[ii].z, fa[ii].w};
-#pragma unroll
-                for (int q = 0; q < 4; ++q)
-                    dbacc[ii] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, w[q]), one, dbacc[ii], false);
-            }
+            for (int q = 0; q < 4; ++q)
+                dbacc[ii] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, w[q]), one, dbacc[ii], false);
         }
+    };
+    // the MFMAs of fragment row ii
+    auto mma_row = [&](const uint4* fa, const uint4* fb, int ii) {
+#pragma unroll
+        for (int jj = 0; jj < TN; ++jj) acc[ii][jj] = mfma_bf16(fa[ii], fb[jj], acc[ii][jj]);
+    };
+    auto mma = [&](const uint4* fa, const uint4* fb) {
+#pragma unroll
+        for (int ii = 0; ii < TM; ++ii) mma_row(fa, fb, ii);
+#pragma unroll
+        for (int ii = 0; ii < TM; ++ii) db_row(fa, ii);
     };
     constexpr int NM = TM * TN;            // MFMAs per 16 tokens
     constexpr int NR = 2 * (TM + TN);      // transposing reads per 16 tokens
-    auto step = [&](char* ca, char* cb, char* na, char* nb, int i) {
-        read_frags(ca, cb, 1, fa1, fb1);
-        mma(fa0, fb0);
+    // step i: slab i in stage (ca, cb), its code slot cc; slab i+1 in (na, nb), its codes in slot
+    // nc (packed x_hat: decoded into nb here, before the barrier that publishes it)
+    auto step = [&](char* ca, char* cb, char* cc, char* na, char* nb, const char* nc, int i) {
+        if constexpr (BITS == 0) {
+            read_frags(ca, cb, 1, fa1, fb1);
+            mma(fa0, fb0);
 #pragma unroll
-        for (int q = 0; q < NR; ++q) {
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
-            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
+            for (int q = 0; q < NR; ++q) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
+            }
+        } else {
+            // codes first (their wait then leaves the operand reads in flight), and the decode
+            // of slab i+1 in four pieces between the four MFMA rows, fenced so that the VALU work
+            // runs beside the matrix pipe instead of before it
+            const DecodeIn din = decode_load(nc, kt0 + i + 1);
+            read_frags(ca, cb, 1, fa1, fb1);
+#pragma unroll
+            for (int ii = 0; ii < TM; ++ii) {
+                mma_row(fa0, fb0, ii);
+                __builtin_amdgcn_sched_barrier(0);
+                decode_chunk(din, nb, ii);
+                db_row(fa0, ii);
+                __builtin_amdgcn_sched_barrier(0);
+            }
         }
-        wait_vm_lds<16>();
+        if constexpr (BITS == 0)
+            wait_vm_lds<16>();  // slab i+1 landed (slabs i+2, i+3 may stay in flight)
+        else
+            wait_vm_lds<CS::LOADS>();  // slab i+2 landed (slab i+3 may stay in flight)
         barrier_only();
-        issue(ca, cb, kt0 + i + 4);
+        issue(ca, cb, cc, kt0 + i + 4);
         read_frags(na, nb, 0, fa0, fb0);
         mma(fa1, fb1);
 #pragma unroll
         for (int q = 0; q < NM; ++q) {
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
             __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
-            if (q < 8) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // one global load
+            if (q < CS::LOADS) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // one global load
         }
     };
 
     if (nk > 0) {
-        issue(sa0, sb0, kt0);
-        issue(sa1, sb1, kt0 + 1);
-        issue(sa2, sb2, kt0 + 2);
-        issue(sa3, sb3, kt0 + 3);
-        wait_vm_lds<24>();
+        issue(sa0, sb0, sc0, kt0);
+        issue(sa1, sb1, sc1, kt0 + 1);
+        issue(sa2, sb2, sc2, kt0 + 2);
+        issue(sa3, sb3, sc3, kt0 + 3);
+        if constexpr (BITS == 0) {
+            wait_vm_lds<3 * CS::LOADS>();
+        } else {
+            // slab 0 is decoded here, slab i+1 in step i (its loads landed by step i-1's wait)
+            wait_vm_lds<2 * CS::LOADS>();
+            const DecodeIn din = decode_load(sc0, kt0);
+#pragma unroll
+            for (int c = 0; c < 4; ++c) decode_chunk(din, sb0, c);
+            wait_vm_lds<2 * CS::LOADS>();
+        }
         barrier_only();
         read_frags(sa0, sb0, 0, fa0, fb0);
         int i = 0;
         for (; i + 4 <= nk; i += 4) {
-            step(sa0, sb0, sa1, sb1, i);
-            step(sa1, sb1, sa2, sb2, i + 1);
-            step(sa2, sb2, sa3, sb3, i + 2);
-            step(sa3, sb3, sa0, sb0, i + 3);
+            step(sa0, sb0, sc0, sa1, sb1, sc1, i);
+            step(sa1, sb1, sc1, sa2, sb2, sc2, i + 1);
+            step(sa2, sb2, sc2, sa3, sb3, sc3, i + 2);
+            step(sa3, sb3, sc3, sa0, sb0, sc0, i + 3);
         }
-        if (i < nk) step(sa0, sb0, sa1, sb1, i);
-        if (i + 1 < nk) step(sa1, sb1, sa2, sb2, i + 1);
-        if (i + 2 < nk) step(sa2, sb2, sa3, sb3, i + 2);
+        if (i < nk) step(sa0, sb0, sc0, sa1, sb1, sc1, i);
+        if (i + 1 < nk) step(sa1, sb1, sc1, sa2, sb2, sc2, i + 1);
+        if (i + 2 < nk) step(sa2, sb2, sc2, sa3, sb3, sc3, i + 2);
     }
-    // the trailing (unused) loads land before LDS is reused below
+    // the trailing (unused) loads land before the kernel ends
     __builtin_amdgcn_s_waitcnt(0);
 
     float* P = a.partial + (int64_t)split * a.M * a.N;
@@ -579,9 +707,16 @@ int64_t dw_workspace_floats(int64_t M, int64_t N, int64_t K) {
 
 int launch_dw_gemm(DwArgs a, int mode, bool with_db, float* out32, uint16_t* out16, float* db, hipStream_t st) {
     const int splits = dw_splits(a.M, a.N, a.K);
-    if (mode == DW_B_BF16 && a.K > 0 && a.K % V2_BK == 0) {
+    // the packed codes go through the pipelined kernel for 1/2/4 bits with DMA-aligned arrays
+    // (codes 16-byte, scale/min 4-byte aligned); 8-bit codes through the register-decoding kernel
+    const bool v2_packed = mode == DW_B_PACKED && (a.bits == 1 || a.bits == 2 || a.bits == 4) &&
+                           ((uintptr_t)a.packed & 15u) == 0 && ((uintptr_t)a.scale & 3u) == 0 &&
+                           ((uintptr_t)a.minv & 3u) == 0;
+    if ((mode == DW_B_BF16 || v2_packed) && a.K > 0 && a.K % V2_BK == 0) {
         // the transpose-free kernel: 32-token tiles, split at the same token boundaries as the
         // 64-token kernel, so both accumulate the same 16-token MFMA steps in the same order
+        // (K % 32 == 0 and N % 256 == 0 make the group count K N / g even, so the scale/min dword
+        // loads stay inside their arrays)
         const int64_t kts = a.K / V2_BK;
         const int64_t kts64 = (a.K + BK - 1) / BK;
         a.kt_per_split = std::max<int64_t>((kts64 + splits - 1) / splits, 1) * (BK / V2_BK);
@@ -590,8 +725,16 @@ int launch_dw_gemm(DwArgs a, int mode, bool with_db, float* out32, uint16_t* out
         a.db_partial = a.partial + (int64_t)splits * a.M * a.N;
         const int64_t W = (a.M / BM) * (a.N / BN) * used;
         const dim3 grid((unsigned)(DW_XCDS * ((W + DW_XCDS - 1) / DW_XCDS)));
-        if (with_db) hipLaunchKernelGGL((dw_gemm_v2_kernel<true>), grid, dim3(THREADS), 0, st, a);
-        else hipLaunchKernelGGL((dw_gemm_v2_kernel<false>), grid, dim3(THREADS), 0, st, a);
+#define DOPT_DW2(BITS_)                                                                              \
+    do {                                                                                             \
+        if (with_db) hipLaunchKernelGGL((dw_gemm_v2_kernel<BITS_, true>), grid, dim3(THREADS), 0, st, a);  \
+        else hipLaunchKernelGGL((dw_gemm_v2_kernel<BITS_, false>), grid, dim3(THREADS), 0, st, a);         \
+    } while (0)
+        if (mode == DW_B_BF16) DOPT_DW2(0);
+        else if (a.bits == 1) DOPT_DW2(1);
+        else if (a.bits == 2) DOPT_DW2(2);
+        else DOPT_DW2(4);
+#undef DOPT_DW2
         launch_dw_reduce(a.partial, used, a.M * a.N, out32, out16, a.db_partial, a.M, with_db ? db : nullptr, st);
         return 0;
     }
