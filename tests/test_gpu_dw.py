@@ -6,9 +6,9 @@ Bar:
     terms' magnitudes (fp32 accumulation over up to 25k terms) plus 1e-6;
   * the packed path bit-exact equal to the bf16 path fed with act_lib::dequant_unpack_triton's
     x_hat (itself bit-exact against the CPU oracle): the in-kernel decode produces the same bf16
-    values, and both kernels (register-transposing with in-kernel decode, and LDS-transposing for
-    bf16 operands) split K at the same token boundaries and accumulate the same 16-token MFMA
-    steps in the same order;
+    values, and every kernel (the pipelined one for bf16 and for 1/2/4-bit codes, the
+    register-decoding one for 8-bit codes) splits K at the same token boundaries and accumulates
+    the same 16-token MFMA steps in the same order;
   * the bf16 output is the round-to-nearest-even of the fp32 output; repeated calls are bit-equal.
 """
 import pytest
