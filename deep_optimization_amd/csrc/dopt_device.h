@@ -124,14 +124,9 @@ __device__ __forceinline__ uint16_t to_bf16(float v) { return (uint16_t)(pack_bf
 __device__ __forceinline__ float bf16_bits_to_f32(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
 
 // ------------------------------------------------------------------ activation math
-// Fast fp32 transcendentals for the fused activation kernels (v_exp_f32 / v_rcp_f32 based; the
-// reference's own are Triton's exp and libdevice tanh, so these are tolerance-level anyway).
-// tanh(u) = sign(u) * (1 - e) / (1 + e), e = 2^(-2|u| log2 e): absolute error ~2e-7, exact 0 at 0.
-__device__ __forceinline__ float fast_tanh(float u) {
-    const float e = __builtin_amdgcn_exp2f(-2.8853900817779268f * fabsf(u));  // -2 log2(e) |u|
-    const float r = (1.0f - e) * __builtin_amdgcn_rcpf(1.0f + e);
-    return copysignf(r, u);
-}
+// Fast fp32 transcendentals for the fused kernels (v_exp_f32 / v_rcp_f32 based; the reference's
+// own are Triton's exp and libdevice tanh, so these are tolerance-level anyway).
+//
 // The quantizer's squash tanh(x / 0.5) * 0.5 = tanh(2x) / 2, with the two scalings folded in: for
 // |x| >= 1/16 the exp form (1 - e) / (2 (1 + e)), e = 2^(-4 log2(e) |x|), where 1 - e keeps at
 // least 2 leading bits; below that the odd Taylor polynomial x (1 - 4x^2/3 + 32x^4/15 - 272x^6/315)
@@ -169,17 +164,15 @@ __device__ __forceinline__ void silu_and_grad(float x, float& y, float& d) {
     y = x * s;
     d = __builtin_fmaf(y, 1.0f - s, s);
 }
-// 2 tanh(x / 2) of BatchNorm's squash, the exp form of fast_tanh with the two scalings folded in
-// (bit-identical to fast_tanh(x * 0.5) * 2)
+// 2 tanh(x / 2) of BatchNorm's squash, as 4 sigmoid(x) - 2 (two transcendentals, two other
+// instructions; absolute error ~2e-7)
 __device__ __forceinline__ float two_tanh_half_fast(float x) {
-    const float e = __builtin_amdgcn_exp2f(-1.4426950408889634f * fabsf(x));
-    return copysignf(__builtin_fmaf(-2.0f, e, 2.0f) * __builtin_amdgcn_rcpf(1.0f + e), x);
+    const float r = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-1.4426950408889634f * x));
+    return __builtin_fmaf(4.0f, r, -2.0f);
 }
-// tanh(2d) / 2 of a clamped activation derivative, the exp form of fast_tanh with the two
-// scalings folded in (bit-identical to fast_tanh(2d) * 0.5: both scalings are powers of two)
+// tanh(2d) / 2 of a clamped activation derivative, as sigmoid(4d) - 1/2 (absolute error ~1e-7)
 __device__ __forceinline__ float half_tanh2_fast(float d) {
-    const float e = __builtin_amdgcn_exp2f(-5.7707801635558535f * fabsf(d));
-    return copysignf(__builtin_fmaf(-0.5f, e, 0.5f) * __builtin_amdgcn_rcpf(1.0f + e), d);
+    return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-5.7707801635558535f * d)) - 0.5f;
 }
 
 // ------------------------------------------------------------------ Philox4x32-10
