@@ -712,7 +712,10 @@ int launch_dw_gemm(DwArgs a, int mode, bool with_db, float* out32, uint16_t* out
     const bool v2_packed = mode == DW_B_PACKED && (a.bits == 1 || a.bits == 2 || a.bits == 4) &&
                            ((uintptr_t)a.packed & 15u) == 0 && ((uintptr_t)a.scale & 3u) == 0 &&
                            ((uintptr_t)a.minv & 3u) == 0;
-    if ((mode == DW_B_BF16 || v2_packed) && a.K > 0 && a.K % V2_BK == 0) {
+    // (the pipelined kernel keeps a slab's lane offsets in 32 bits: 32 rows of either operand
+    // must span less than 4 GiB)
+    const bool v2_offsets = a.ldd < ((int64_t)1 << 26) && a.ldx < ((int64_t)1 << 26) && a.N < ((int64_t)1 << 26);
+    if ((mode == DW_B_BF16 || v2_packed) && v2_offsets && a.K > 0 && a.K % V2_BK == 0) {
         // the transpose-free kernel: 32-token tiles, split at the same token boundaries as the
         // 64-token kernel, so both accumulate the same 16-token MFMA steps in the same order
         // (K % 32 == 0 and N % 256 == 0 make the group count K N / g even, so the scale/min dword
