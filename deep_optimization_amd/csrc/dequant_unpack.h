@@ -5,10 +5,11 @@
 //
 // Work decomposition mirrors quant_pack.h: a lane owns units of UE output elements (UB bytes,
 // written as UB/16 consecutive 16-byte stores), a group's CPG units are spread over LPG lanes
-// (unit c = i*LPG + li), and a wave handles GPW = P*64/LPG groups. The wave's GPW scales and
-// minima are staged once in LDS (one coalesced load per array) and read back by the lanes of
-// each group; a unit's UE*BITS code bits are read as the one dword (or 2/4-dword vector) that
-// holds them.
+// (unit c = i*LPG + li), and a wave handles GPW = P*64/LPG groups. Each lane loads its groups'
+// scale and minimum itself (the LPG lanes of a group share one request) and a unit's UE*BITS
+// code bits as the one dword (or 2/4-dword vector) that holds them; nothing is staged in LDS and
+// no wave waits for another. (Staging them in LDS behind a workgroup barrier cost 12 us of the
+// 81 us the kernel took on config 2 when its inputs came cold from HBM right after quant-pack.)
 #pragma once
 
 #include "dopt_device.h"
@@ -52,7 +53,6 @@ struct DequantCfg {
     static_assert(UB % 16 == 0 && UE * BYTES == UB, "unit must be whole 16-byte stores");
     static_assert(CPG * UE == G && LPG * CPL == CPG, "group must split evenly over lanes");
     static_assert(UBITS <= 128, "a unit reads at most one 16-byte code vector");
-    static_assert(GPW <= 64, "one lane per staged group");
 };
 
 template <int G>
@@ -73,30 +73,28 @@ __global__ __launch_bounds__(256) void dequant_unpack_kernel(DequantArgs a) {
     constexpr uint32_t QMAX = (1u << BITS) - 1u;
     constexpr int E16 = DType<YT>::per16;
 
-    __shared__ float s_scale[C::WAVES][C::GPW];
-    __shared__ float s_min[C::WAVES][C::GPW];
-
     const int lane = threadIdx.x & 63;
     const int wv = threadIdx.x >> 6;
     const int slot = lane / LPG;
     const int li = lane % LPG;
     const uint32_t g0 = (blockIdx.x * C::WAVES + wv) * (uint32_t)C::GPW;
 
-    // ---- stage the wave's per-group scale/min (one coalesced load per array)
-    if (lane < C::GPW) {
-        const uint32_t r = g0 + lane;
-        float sc = 0.0f, mn = 0.0f;
+    // ---- each lane loads its groups' scale and min itself (the LPG lanes of a group read the
+    // same address, one request); no staging, so the waves of a workgroup never wait for each other
+    float scs[P], mns[P];
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+        const uint32_t r = g0 + p * GPP + slot;
+        scs[p] = mns[p] = 0.0f;
         if (r < a.n_groups) {
             if (a.meta_bf16) {
-                sc = bf16_bits_to_f32(((const uint16_t*)a.scale)[r]);
-                mn = bf16_bits_to_f32(((const uint16_t*)a.minv)[r]);
+                scs[p] = bf16_bits_to_f32(((const uint16_t*)a.scale)[r]);
+                mns[p] = bf16_bits_to_f32(((const uint16_t*)a.minv)[r]);
             } else {
-                sc = ((const float*)a.scale)[r];
-                mn = ((const float*)a.minv)[r];
+                scs[p] = ((const float*)a.scale)[r];
+                mns[p] = ((const float*)a.minv)[r];
             }
         }
-        s_scale[wv][lane] = sc;
-        s_min[wv][lane] = mn;
     }
 
     // ---- code loads: the dword(s) holding each unit's UE*BITS bits
@@ -128,15 +126,13 @@ __global__ __launch_bounds__(256) void dequant_unpack_kernel(DequantArgs a) {
             }
         }
     }
-    __syncthreads();
-
     char* yb = (char*)a.y;
 #pragma unroll
     for (int p = 0; p < P; ++p) {
         const uint32_t r = g0 + p * GPP + slot;
         const bool ok = r < a.n_groups;
-        const float sc = s_scale[wv][p * GPP + slot];
-        const float mn = s_min[wv][p * GPP + slot];
+        const float sc = scs[p];
+        const float mn = mns[p];
 #pragma unroll
         for (int i = 0; i < CPL; ++i) {
             const uint32_t c = (uint32_t)(i * LPG + li);
