@@ -127,17 +127,15 @@ __device__ __forceinline__ float bf16_bits_to_f32(uint16_t b) { return __uint_as
 // Fast fp32 transcendentals for the fused kernels (v_exp_f32 / v_rcp_f32 based; the reference's
 // own are Triton's exp and libdevice tanh, so these are tolerance-level anyway).
 //
-// The quantizer's squash tanh(x / 0.5) * 0.5 = tanh(2x) / 2, with the two scalings folded in: for
-// |x| >= 1/16 the exp form (1 - e) / (2 (1 + e)), e = 2^(-4 log2(e) |x|), where 1 - e keeps at
-// least 2 leading bits; below that the odd Taylor polynomial x (1 - 4x^2/3 + 32x^4/15 - 272x^6/315)
-// (truncation error < 1e-10 there). Absolute error ~3e-8 over the whole line, exact 0 at 0.
+// The quantizer's squash tanh(x / 0.5) * 0.5 = tanh(2x) / 2: for |x| >= 1/16 as sigmoid(4x) - 1/2
+// (absolute error ~6e-8), below that the odd Taylor polynomial x (1 - 4x^2/3 + 32x^4/15 -
+// 272x^6/315) (truncation error < 1e-10 there), which keeps small values accurate relative to
+// their own size: a group whose values are all tiny still gets a faithful range. Exact 0 at 0.
 __device__ __forceinline__ float squash_half_tanh2(float x) {
-    const float ax = fabsf(x);
-    const float e = __builtin_amdgcn_exp2f(-5.7707801635558535f * ax);
-    const float r = fmaf(-0.5f, e, 0.5f) * __builtin_amdgcn_rcpf(1.0f + e);
-    const float s = ax * ax;
-    const float p = ax * fmaf(s, fmaf(s, fmaf(s, -272.0f / 315.0f, 32.0f / 15.0f), -4.0f / 3.0f), 1.0f);
-    return copysignf(ax < 0.0625f ? p : r, x);
+    const float r = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-5.7707801635558535f * x)) - 0.5f;
+    const float s = x * x;
+    const float p = x * fmaf(s, fmaf(s, fmaf(s, -272.0f / 315.0f, 32.0f / 15.0f), -4.0f / 3.0f), 1.0f);
+    return fabsf(x) < 0.0625f ? p : r;
 }
 __device__ __forceinline__ float fast_sigmoid(float x) {
     return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-1.4426950408889634f * x));
