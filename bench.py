@@ -18,6 +18,7 @@ and the captured weight-noise step replayed from one HIP graph vs run eagerly.
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-extras] [--no-cpu]
        python bench.py --pmc-probe   (one copy kernel + the dominant kernel, for rocprofv3 --pmc)
        python bench.py --fp8-probe random|constant   (the 8192^3 FP8 GEMM alone, for rocprofv3 --pmc)
+       python bench.py --dw-probe   (three weight-gradient GEMMs at the ViT fc1 shape, for rocprofv3 --pmc)
 """
 from __future__ import annotations
 
@@ -144,6 +145,25 @@ def fp8_probe(mode: str) -> int:
     e1.synchronize()
     us = e0.elapsed_time(e1) / 10 * 1e3
     print(f"fp8 probe ({mode}): {us:.1f} us per launch, {2.0 * M * Nn * K / us / 1e6:.0f} TFLOP/s")
+    return 0
+
+
+def dw_probe() -> int:
+    """Three weight-gradient GEMMs at the ViT-B/16 bs-128 fc1 shape (dy bf16 [25216, 3072], x_hat
+    bf16 [25216, 768], no bias gradient), for rocprofv3 --pmc runs."""
+    import torch
+
+    import deep_optimization_amd  # noqa: F401
+
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(7)
+    K, cin, cout = 128 * 197, 768, 3072
+    dy = torch.randn((K, cout), generator=g, device=dev).to(torch.bfloat16)
+    xh = torch.randn((K, cin), generator=g, device=dev).to(torch.bfloat16)
+    for _ in range(3):
+        torch.ops.act_lib.dw_gemm(dy, xh, None, None, None, cin, 0, 0, False, torch.bfloat16)
+    torch.cuda.synchronize()
+    print(f"dw probe: 3 x dw_gemm M={cout} N={cin} K={K}")
     return 0
 
 
@@ -331,6 +351,7 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--pmc-probe", action="store_true")
     ap.add_argument("--fp8-probe", choices=("random", "constant"))
+    ap.add_argument("--dw-probe", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}). "
@@ -341,6 +362,8 @@ def main() -> int:
         return pmc_probe()
     if args.fp8_probe:
         return fp8_probe(args.fp8_probe)
+    if args.dw_probe:
+        return dw_probe()
 
     import torch
 
