@@ -106,27 +106,28 @@ __device__ __forceinline__ void block_sum2(float& a, float& b) {
     }
 }
 
-// min / max over aligned blocks of lpg lanes (lpg in 4..64, wave-uniform)
+// min / max over aligned blocks of lpg lanes (lpg in 4..64, wave-uniform); raw v_min / v_max
+// (the operands are computed values: numbers or quiet NaNs)
 __device__ __forceinline__ void group_minmax(float& mn, float& mx, int lpg) {
-    mn = fminf(mn, dpp_f32<0xB1>(mn));
-    mx = fmaxf(mx, dpp_f32<0xB1>(mx));
-    mn = fminf(mn, dpp_f32<0x4E>(mn));
-    mx = fmaxf(mx, dpp_f32<0x4E>(mx));
+    mn = vmin(mn, dpp_f32<0xB1>(mn));
+    mx = vmax(mx, dpp_f32<0xB1>(mx));
+    mn = vmin(mn, dpp_f32<0x4E>(mn));
+    mx = vmax(mx, dpp_f32<0x4E>(mx));
     if (lpg >= 8) {
-        mn = fminf(mn, dpp_f32<0x141>(mn));
-        mx = fmaxf(mx, dpp_f32<0x141>(mx));
+        mn = vmin(mn, dpp_f32<0x141>(mn));
+        mx = vmax(mx, dpp_f32<0x141>(mx));
     }
     if (lpg >= 16) {
-        mn = fminf(mn, dpp_f32<0x140>(mn));
-        mx = fmaxf(mx, dpp_f32<0x140>(mx));
+        mn = vmin(mn, dpp_f32<0x140>(mn));
+        mx = vmax(mx, dpp_f32<0x140>(mx));
     }
     if (lpg >= 32) {
-        mn = fminf(mn, __shfl_xor(mn, 16, 64));
-        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+        mn = vmin(mn, __shfl_xor(mn, 16, 64));
+        mx = vmax(mx, __shfl_xor(mx, 16, 64));
     }
     if (lpg >= 64) {
-        mn = fminf(mn, __shfl_xor(mn, 32, 64));
-        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        mn = vmin(mn, __shfl_xor(mn, 32, 64));
+        mx = vmax(mx, __shfl_xor(mx, 32, 64));
     }
 }
 
@@ -297,8 +298,8 @@ __device__ __forceinline__ void fwd_block(const BnFwdArgs& a, int64_t c, int64_t
             } else {
                 t[k] = xh[k];
             }
-            mn = fminf(mn, t[k]);
-            mx = fmaxf(mx, t[k]);
+            mn = vmin(mn, t[k]);
+            mx = vmax(mx, t[k]);
         }
         const int lpg = 1 << (lg - 3);  // group / EPL
         group_minmax(mn, mx, lpg);

@@ -65,6 +65,30 @@ __device__ __forceinline__ void block_minmax(float& mn, float& mx) {
     }
 }
 
+// Raw v_min/v_max (and 3-operand forms): no NaN canonicalisation of the operands, which fminf /
+// fmaxf would add in IEEE mode. Equal to fminf / fmaxf for operands that are numbers or quiet NaNs
+// (every arithmetic result and every bit copy of one), the only operands these kernels pass.
+__device__ __forceinline__ float vmin3(float a, float b, float c) {
+    float d;
+    asm("v_min3_f32 %0, %1, %2, %3" : "=v"(d) : "v"(a), "v"(b), "v"(c));
+    return d;
+}
+__device__ __forceinline__ float vmax3(float a, float b, float c) {
+    float d;
+    asm("v_max3_f32 %0, %1, %2, %3" : "=v"(d) : "v"(a), "v"(b), "v"(c));
+    return d;
+}
+__device__ __forceinline__ float vmin(float a, float b) {
+    float d;
+    asm("v_min_f32 %0, %1, %2" : "=v"(d) : "v"(a), "v"(b));
+    return d;
+}
+__device__ __forceinline__ float vmax(float a, float b) {
+    float d;
+    asm("v_max_f32 %0, %1, %2" : "=v"(d) : "v"(a), "v"(b));
+    return d;
+}
+
 // ------------------------------------------------------------------ 16-byte global access
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 

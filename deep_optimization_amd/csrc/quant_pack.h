@@ -102,28 +102,6 @@ __device__ __forceinline__ uint64_t group_elem_index(const QuantPackArgs& a, uin
            (uint64_t)(e0 >> a.log2s) * a.row + (e0 & smask);
 }
 
-// Raw v_min3/v_max3: no NaN canonicalisation of the operands (see the header comment).
-__device__ __forceinline__ float vmin3(float a, float b, float c) {
-    float d;
-    asm("v_min3_f32 %0, %1, %2, %3" : "=v"(d) : "v"(a), "v"(b), "v"(c));
-    return d;
-}
-__device__ __forceinline__ float vmax3(float a, float b, float c) {
-    float d;
-    asm("v_max3_f32 %0, %1, %2, %3" : "=v"(d) : "v"(a), "v"(b), "v"(c));
-    return d;
-}
-__device__ __forceinline__ float vmin(float a, float b) {
-    float d;
-    asm("v_min_f32 %0, %1, %2" : "=v"(d) : "v"(a), "v"(b));
-    return d;
-}
-__device__ __forceinline__ float vmax(float a, float b) {
-    float d;
-    asm("v_max_f32 %0, %1, %2" : "=v"(d) : "v"(a), "v"(b));
-    return d;
-}
-
 // min/max all-reduce over aligned blocks of LPG lanes; operands are NaN-free or quiet NaNs.
 template <int LPG>
 __device__ __forceinline__ void group_minmax(float& mn, float& mx) {
