@@ -316,9 +316,26 @@ __device__ __forceinline__ void fwd_block(const BnFwdArgs& a, int64_t c, int64_t
                 q[k] = (int)qf;
             }
         } else {
+            // (t - mn) / step, correctly rounded, without a division per element: with y = 1/step
+            // correctly rounded (one division per group), q0 = RN(a y) and the exact remainder
+            // r = fma(-q0, step, a), RN(q0 + r y) is the correctly rounded a / step (Markstein's
+            // theorem, the IA-64 division), given no overflow and a normal remainder. With
+            // 2^-60 <= step < inf and a in [0, rng] the quotient lies in [0, qmax], and whenever it
+            // can reach a rounding boundary of the code (q >= ~1e-7) the remainder is normal.
+            // (Checked bit-for-bit against fp32 division on 4e8 random and quantizer-shaped pairs.)
+            const float invs = 1.0f / step;
+            const bool fastdiv = step >= 0x1p-60f && step < __builtin_huge_valf();
 #pragma unroll
             for (int k = 0; k < EPL; ++k) {
-                const float qf = __builtin_amdgcn_fmed3f((t[k] - mn) / step + half_m, 0.0f, qmaxf);
+                const float num = t[k] - mn;
+                float quo;
+                if (fastdiv) {
+                    const float q0 = num * invs;
+                    quo = fmaf(fmaf(-q0, step, num), invs, q0);
+                } else {
+                    quo = num / step;
+                }
+                const float qf = __builtin_amdgcn_fmed3f(quo + half_m, 0.0f, qmaxf);
                 q[k] = (int)qf;
             }
         }
