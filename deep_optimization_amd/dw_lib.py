@@ -57,10 +57,16 @@ def _dw_gemm(dy: Tensor, x_hat: Optional[Tensor], packed: Optional[Tensor], scal
             raise RuntimeError("dw_gemm: give x_hat or packed, scale and min")
         if packed.numel() * 32 != K * N * bits:
             raise RuntimeError(f"dw_gemm: packed holds {packed.numel()} words, expected {K * N * bits // 32}")
+        if (K * N) % group_size:
+            raise RuntimeError(f"dw_gemm: K*N = {K * N} is not a whole number of groups of {group_size}")
         p = _aligned16(packed)
         sc, mn = scale.contiguous(), min.contiguous()
         if sc.dtype != torch.bfloat16 or mn.dtype != torch.bfloat16:
             raise RuntimeError("dw_gemm: scale and min must be bf16 (the reference quantizer's)")
+        n_groups = K * N // group_size
+        if sc.numel() != n_groups or mn.numel() != n_groups:
+            raise RuntimeError(f"dw_gemm: scale and min must hold one value per group ({n_groups}), got "
+                               f"{sc.numel()} and {mn.numel()}")
         rc = L.dopt_dw_gemm(dy.data_ptr(), M, None, 0, p.data_ptr(), sc.data_ptr(), mn.data_ptr(), group_size, bits,
                             M, N, K, ws.data_ptr(), d32, d16, None if db is None else db.data_ptr(), _stream(dy))
     _lib.check(rc, "dw_gemm")

@@ -76,3 +76,11 @@ def test_no_tokens_and_errors():
     x = torch.randn((64, 256), device=DEV).to(torch.bfloat16)
     with pytest.raises(RuntimeError, match="multiples of 256"):
         ops.dw_gemm(dy, x, None, None, None, 256, 0, 0, False, torch.float32)
+    # packed operands: the per-group scale/min must cover every group (the kernel reads them unchecked)
+    dy = torch.randn((64, 256), device=DEV).to(torch.bfloat16)
+    x = torch.randn((1, 64 * 256 // 128, 128), device=DEV).to(torch.bfloat16)
+    p, sc, mn = ops.quant_pack_triton(x, 2, 128, False, 0, True, 3.0)
+    with pytest.raises(RuntimeError, match="one value per group"):
+        ops.dw_gemm(dy, None, p, sc.reshape(-1)[:-2], mn, 256, 2, 128, False, torch.float32)
+    with pytest.raises(RuntimeError, match="packed holds"):
+        ops.dw_gemm(dy, None, p.reshape(-1)[:-1], sc, mn, 256, 2, 128, False, torch.float32)
