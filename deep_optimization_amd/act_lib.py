@@ -121,9 +121,16 @@ def _quant_pack_launch(x: Tensor, n_groups: int, bits: int, group_size: int, til
 
 def _dequant_launch(packed: Tensor, scale: Tensor, xmin: Tensor, n_groups: int, bits: int,
                     group_size: int, tile, out: Tensor):
-    _bits_consts(bits, group_size)
+    _, nwords, _ = _bits_consts(bits, group_size)
     if scale.dtype not in _META_CODE or xmin.dtype != scale.dtype:
         raise RuntimeError("dequant_unpack: scale and min must both be float32 or both bfloat16")
+    # the kernel reads these unchecked: every size must match the group count
+    if scale.numel() != n_groups or xmin.numel() != n_groups:
+        raise RuntimeError(f"dequant_unpack: scale and min must hold {n_groups} values, got {scale.numel()} "
+                           f"and {xmin.numel()}")
+    if packed.numel() * packed.element_size() != n_groups * nwords * 4:
+        raise RuntimeError(f"dequant_unpack: packed holds {packed.numel() * packed.element_size()} bytes, "
+                           f"expected {n_groups * nwords * 4} ({n_groups} groups of {nwords} words)")
     _require_cuda(packed, scale, xmin)
     packed = _aligned(packed)
     scale = scale.contiguous()
@@ -429,6 +436,9 @@ def _relu_bwd_fused_unpack(packed, dy, bits, N, G, group_size):
         raise RuntimeError(f"relu_bwd_fused_unpack: unsupported dy dtype {dy.dtype}")
     if dy.numel() != N * G * group_size:
         raise RuntimeError(f"relu_bwd_fused_unpack: dy has {dy.numel()} elements, expected {N * G * group_size}")
+    if packed.numel() * packed.element_size() * 8 < dy.numel() * bits:
+        raise RuntimeError(f"relu_bwd_fused_unpack: packed holds {packed.numel() * packed.element_size()} bytes, "
+                           f"too few for {dy.numel()} {bits}-bit masks")
     _require_cuda(packed, dy)
     packed = _aligned(packed)
     dy = _aligned(dy)
@@ -495,6 +505,10 @@ def _act_dequant_mul_launch(packed, dy, scale, xmin, n_groups, bits, group_size,
         raise RuntimeError("fused activation backward: scale and min must both be float32 or both bfloat16")
     if dy.numel() != n_groups * group_size:
         raise RuntimeError(f"fused activation backward: dy has {dy.numel()} elements, expected {n_groups * group_size}")
+    _, nwords, _ = _bits_consts(bits, group_size)
+    if scale.numel() != n_groups or xmin.numel() != n_groups or \
+            packed.numel() * packed.element_size() != n_groups * nwords * 4:
+        raise RuntimeError(f"fused activation backward: packed / scale / min do not hold {n_groups} groups")
     _require_cuda(packed, dy, scale, xmin)
     packed = _aligned(packed)
     dy = _aligned(dy)
