@@ -215,8 +215,24 @@ def _bwd_common(mode, DY, M, HW, x_hat=None, packed=None, relu_packed=None, scal
     return DY3, N, C, xh, c(packed), c(relu_packed), c(scale), c(xmin)
 
 
+def _check_saved(C, M, group, bits, p, rp, sc, mn, *vecs):
+    """The kernels read the saved tensors unchecked: their sizes must match the channel layout."""
+    if p is not None and p.numel() * p.element_size() * 8 != C * M * bits:
+        raise RuntimeError(f"BatchNorm backward: packed codes hold {p.numel() * p.element_size()} bytes, "
+                           f"expected {C * M * bits // 8}")
+    if rp is not None and rp.numel() * rp.element_size() * 8 < C * M:
+        raise RuntimeError("BatchNorm backward: the ReLU mask is too small for the tensor")
+    for t in (sc, mn):
+        if t is not None and t.numel() != C * (M // group):
+            raise RuntimeError(f"BatchNorm backward: scale/min hold {t.numel()} values, expected {C * (M // group)}")
+    for t in vecs:
+        if t is not None and t.numel() != C:
+            raise RuntimeError(f"BatchNorm backward: per-channel vectors must hold {C} values, got {t.numel()}")
+
+
 def _bwd_reduce(mode, DY, M, HW, group, bits, **kw):
     DY3, N, C, xh, p, rp, sc, mn = _bwd_common(mode, DY, M, HW, **kw)
+    _check_saved(C, M, group, bits, p, rp, sc, mn)
     dw = torch.empty(C, dtype=torch.float32, device=DY.device)
     db = torch.empty_like(dw)
     ws = _workspace(DY, N, C, HW)
@@ -231,6 +247,7 @@ def _bwd_dx(mode, DY, M, HW, group, bits, DW, DB, W, VAR, eps, var_is_invstd, **
     DY3, N, C, xh, p, rp, sc, mn = _bwd_common(mode, DY, M, HW, **kw)
     dx = torch.empty(DY3.shape, dtype=torch.bfloat16, device=DY.device)
     dw, db, w, v = _f32(DW), _f32(DB), _f32(W), _f32(VAR)
+    _check_saved(C, M, group, bits, p, rp, sc, mn, dw, db, w, v)
     rc = _lib.lib().dopt_bn_bwd_dx(mode, _ptr(xh), _ptr(p), _ptr(rp), _ptr(sc), _ptr(mn), DY3.data_ptr(),
                                    _DTYPE_CODE[DY3.dtype], N, C, HW, C * HW, HW, group, bits, dw.data_ptr(),
                                    db.data_ptr(), w.data_ptr(), v.data_ptr(), float(eps), int(bool(var_is_invstd)),
