@@ -12,7 +12,8 @@ stream it is launched on), the CPU oracle timed on the host cores (cpu_baseline)
 the Philox and nearest rounding modes of the same step, a HIP-graph replay of the step, the ViT
 MLP bit-width sweep (config 3), the fused activation layers, the FP8 GEMM (config 4) beside
 hipBLASLt on the same data, the compressed Linear layers' weight-gradient GEMM at the ViT-B/16
-shapes, the compressed BatchNorm layer, and the ViT-B/16 train step (config 5): plain vs 2-bit,
+shapes, the compressed BatchNorm layer, the ViT-B/16 train step (config 5): plain vs 2-bit,
+the ResNet-50 train step (plain vs compressed Conv/BatchNorm/ReLU, eager and graph-replayed),
 and the captured weight-noise step replayed from one HIP graph vs run eagerly.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-extras] [--no-cpu]
@@ -29,6 +30,11 @@ import re
 import statistics
 import sys
 import time
+
+# MIOpen's default find mode benchmarks every convolution solver on a layer's first call (seconds
+# per shape for the ResNet-50 leg); the heuristic mode keeps the run within minutes. Both the
+# plain and the compressed models run under the same mode.
+os.environ.setdefault("MIOPEN_FIND_MODE", "FAST")
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
 if ROOT not in sys.path:
@@ -342,6 +348,90 @@ def vit_qdrop_graph_step(torch, dev, batch=128, steps=6, warmup=2):
     return res
 
 
+def resnet_train_step(torch, dev, batch=64, steps=6, warmup=3):
+    """ResNet-50 train step (forward, cross-entropy, backward, SGD with momentum) on a fixed
+    synthetic batch (N(0,1) 224x224x3 images, random labels over 1000 classes, bf16 autocast,
+    random init), plain and rewritten by the Controller (every selected Conv / BatchNorm input 2-bit,
+    ReLU masks 1-bit), each run eagerly and replayed from one memset-free HIP graph."""
+    import torch.nn.functional as F
+
+    from deep_optimization_amd.controller import Controller
+    from deep_optimization_amd.graph import finalize
+    from deep_optimization_amd.resnet import resnet50
+
+    g = torch.Generator(device=dev).manual_seed(5)
+    xb = torch.randn((batch, 3, 224, 224), generator=g, device=dev)
+    yb = torch.randint(0, 1000, (batch,), generator=g, device=dev)
+    res = {}
+    for name in ("plain", "compressed_2bit"):
+        torch.manual_seed(0)
+        model = resnet50().to(dev).train()
+        n_layers = None
+        if name != "plain":
+            ctl = Controller(model, {"batch_size": batch, "default_bits": 2}, input_shape=(3, 224, 224))
+            model = ctl.warp_model()
+            n_layers = sum(1 for v in ctl.meta.values() if isinstance(v, dict))
+        opt = torch.optim.SGD(model.parameters(), lr=0.01, momentum=0.9)
+
+        def step():
+            with torch.autocast("cuda", dtype=torch.bfloat16):
+                loss = F.cross_entropy(model(xb), yb)
+            loss.backward()
+            opt.step()
+            return loss
+
+        def eager():
+            opt.zero_grad(set_to_none=False)
+            return step()
+
+        first = float(eager().detach())
+        for _ in range(warmup - 1):
+            eager()
+        torch.cuda.synchronize()
+        torch.cuda.reset_peak_memory_stats()
+        base_alloc = torch.cuda.memory_allocated()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            eager()
+        torch.cuda.synchronize()
+        t_eager = (time.perf_counter() - t0) / steps
+        peak = torch.cuda.max_memory_allocated() - base_alloc
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            eager()
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph(keep_graph=True)
+        opt.zero_grad(set_to_none=False)
+        with torch.cuda.graph(graph, stream=side):
+            loss = step()
+        finalize(graph)
+        for _ in range(warmup):
+            opt.zero_grad(set_to_none=False)
+            graph.replay()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            opt.zero_grad(set_to_none=False)
+            graph.replay()
+        torch.cuda.synchronize()
+        t_graph = (time.perf_counter() - t0) / steps
+        res[name] = {"eager_ms_per_step": round(t_eager * 1e3, 2), "graph_replay_ms_per_step": round(t_graph * 1e3, 2),
+                     "peak_above_resident_GiB": round(peak / 2 ** 30, 3), "loss_first_step": round(first, 4),
+                     "loss_last_step": round(float(loss.detach()), 4)}
+        if n_layers is not None:
+            res[name]["layers_compressed"] = n_layers
+        del graph, model, opt
+        torch.cuda.empty_cache()
+    p, c = res["plain"], res["compressed_2bit"]
+    res["compressed_vs_plain"] = {
+        "graph_step_time_ratio": round(c["graph_replay_ms_per_step"] / p["graph_replay_ms_per_step"], 3),
+        "eager_step_time_ratio": round(c["eager_ms_per_step"] / p["eager_ms_per_step"], 3),
+        "peak_above_resident_ratio": round(c["peak_above_resident_GiB"] / p["peak_above_resident_GiB"], 3)}
+    return res
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -612,6 +702,9 @@ def main() -> int:
         progress("ViT-B/16 train step")
         extras["vit_b16_train_step_bs128"] = vit_train_step(torch, dev)
         torch.cuda.empty_cache()
+        torch.cuda.empty_cache()
+        progress("ResNet-50 train step")
+        extras["resnet50_train_step_bs64"] = resnet_train_step(torch, dev)
         progress("ViT-B/16 captured qdrop step")
         extras["vit_b16_qdrop_step_bs128_graph"] = vit_qdrop_graph_step(torch, dev)
         out["extras"] = extras

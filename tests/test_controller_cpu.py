@@ -190,3 +190,34 @@ def test_batchnorm_swap_keeps_state_and_fuse_bn_act():
     fused.eval()
     with torch.no_grad():
         torch.testing.assert_close(fused(x), want, rtol=0, atol=0)
+
+
+def test_resnet50_selection_and_swap():
+    """ResNet-50 at batch 64: every Conv / BatchNorm / ReLU whose output exceeds 10 MiB
+    (controller.py's threshold) becomes its DO* counterpart: 37 convolutions, 37 BatchNorms and
+    33 ReLUs; ReLUs keep 1-bit masks only, the others 2-bit codes of their saved input; small
+    late-stage layers stay torch's."""
+    from deep_optimization_amd.resnet import resnet50
+
+    torch.manual_seed(0)
+    c = Controller(resnet50(), {"batch_size": 64, "default_bits": 2}, input_shape=(3, 224, 224), device="cpu")
+    model = c.warp_model()
+    kinds = {}
+    for name, mod in model.named_modules():
+        if name in c.meta:
+            kinds[type(mod).__name__] = kinds.get(type(mod).__name__, 0) + 1
+    assert kinds == {"DOConv2d": 37, "DOBatchNorm2d": 37, "DOReLU_Variance": 33}
+    for k in _targets(c):
+        m = c.meta[k]
+        assert m["tensor_meta"].shape[0] == 64
+        if k.split(".")[-1].startswith("relu"):
+            assert m["pack_only"] and m["bits"] == 1
+        else:
+            assert not m["pack_only"] and m["bits"] == 2
+    # output sizes decide: layer3.0.conv3 writes [64, 1024, 14, 14] (25.7 MB, selected), its 3x3
+    # conv2 [64, 256, 14, 14] (6.4 MB, not), and so on down to layer4's [64, 512, 7, 7]
+    assert "conv1" in c.meta and "bn1" in c.meta and "layer1.0.conv1" in c.meta
+    assert "layer3.0.conv3" in c.meta and tuple(c.meta["layer3.0.conv3"]["tensor_meta"].shape) == (64, 256, 14, 14)
+    assert "layer3.0.conv2" not in c.meta and "layer4.2.conv2" not in c.meta
+    assert isinstance(model.get_submodule("layer1.0.bn1"), DOBatchNorm2d)
+    assert isinstance(model.get_submodule("layer4.2.conv2"), nn.Conv2d)
