@@ -42,6 +42,7 @@ EXPORTS = (
     "dopt_dw_gemm",
     "dopt_graph_node_counts",
     "dopt_graph_replace_memsets",
+    "dopt_stream_probe",
 )
 
 _lib = None
@@ -109,6 +110,8 @@ def lib() -> ctypes.CDLL:
         L.dopt_graph_node_counts.restype = i32
         L.dopt_graph_replace_memsets.argtypes = [vp, vp]
         L.dopt_graph_replace_memsets.restype = i32
+        L.dopt_stream_probe.argtypes = [vp, vp, vp, vp, i64, i32, vp]
+        L.dopt_stream_probe.restype = i32
         _lib = L
     return _lib
 

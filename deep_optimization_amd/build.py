@@ -28,6 +28,7 @@ SOURCES = [
     "bn_fused.hip",
     "dw_gemm.hip",
     "graph_tools.hip",
+    "stream_probe.hip",
 ]
 
 ARCH = "gfx950"

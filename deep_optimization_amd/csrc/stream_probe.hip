@@ -1,0 +1,74 @@
+// Bandwidth-ceiling probe for the quant-pack kernel's byte mix: the same reads and writes with
+// no arithmetic, so a benchmark can report how close the real kernel comes to what the memory
+// system delivers for that mix (reads of two streams interleaved with a small write stream).
+//
+// Unit u = 8 elements: reads 16 bytes of x (8 bf16) and, with noise, 32 bytes of noise (8 fp32);
+// with BITS > 0 writes BITS bytes of "codes" (8 codes of BITS bits) and, every 32 units (one
+// 256-element group), 8 bytes of "scale/min". Consecutive lanes take consecutive units, as the
+// quant-pack kernel's lanes take consecutive 16-byte pieces of a group. The bytes written are a
+// hash of the bytes read: they only keep the loads alive.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace dopt {
+namespace {
+
+constexpr int PROBE_THREADS = 256;
+
+template <int BITS, bool NOISE>
+__global__ __launch_bounds__(PROBE_THREADS) void stream_mix_kernel(const uint4* __restrict__ x,
+                                                                   const uint4* __restrict__ noise,
+                                                                   uint8_t* __restrict__ codes,
+                                                                   uint32_t* __restrict__ meta, uint64_t n_units) {
+    const uint64_t u = (uint64_t)blockIdx.x * PROBE_THREADS + threadIdx.x;
+    if (u >= n_units) return;
+    const uint4 a = x[u];
+    uint32_t h = a.x ^ a.y ^ a.z ^ a.w;
+    if constexpr (NOISE) {
+        const uint4 b = noise[2 * u], c = noise[2 * u + 1];
+        h ^= b.x ^ b.y ^ b.z ^ b.w ^ c.x ^ c.y ^ c.z ^ c.w;
+    }
+    if constexpr (BITS == 0) {
+        if (h == 0x9E3779B9u) codes[0] = 1;  // practically never taken; keeps the loads
+    } else {
+        if constexpr (BITS == 1) codes[u] = (uint8_t)h;
+        if constexpr (BITS == 2) ((uint16_t*)codes)[u] = (uint16_t)h;
+        if constexpr (BITS == 4) ((uint32_t*)codes)[u] = h;
+        if constexpr (BITS == 8) ((uint2*)codes)[u] = make_uint2(h, h >> 7);
+        if ((u & 31) == 0) ((uint2*)meta)[u >> 5] = make_uint2(h, h >> 3);
+    }
+}
+
+template <int BITS, bool NOISE>
+hipError_t launch(const void* x, const void* noise, void* codes, void* meta, uint64_t n, hipStream_t s) {
+    const uint64_t blocks = (n + PROBE_THREADS - 1) / PROBE_THREADS;
+    hipLaunchKernelGGL((stream_mix_kernel<BITS, NOISE>), dim3((uint32_t)blocks), dim3(PROBE_THREADS), 0, s,
+                       (const uint4*)x, (const uint4*)noise, (uint8_t*)codes, (uint32_t*)meta, n);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+// bits in {0, 1, 2, 4, 8}; 0 = reads only. Returns nullptr or the name of what failed.
+const char* launch_stream_mix(const void* x, const void* noise, void* codes, void* meta, uint64_t n_units, int bits,
+                              hipStream_t s) {
+    hipError_t e = hipSuccess;
+#define DOPT_SM(B)                                                                               \
+    case B:                                                                                      \
+        e = noise ? launch<B, true>(x, noise, codes, meta, n_units, s)                           \
+                  : launch<B, false>(x, noise, codes, meta, n_units, s);                          \
+        break;
+    switch (bits) {
+        DOPT_SM(0)
+        DOPT_SM(1)
+        DOPT_SM(2)
+        DOPT_SM(4)
+        DOPT_SM(8)
+        default:
+            return "bits";
+    }
+#undef DOPT_SM
+    return e == hipSuccess ? nullptr : hipGetErrorString(e);
+}
+
+}  // namespace dopt

@@ -125,7 +125,9 @@ class Graph:
 
     def capture_cuda_graph_qdrop(self):
         """:82-120. Returns (graphs, compute_stream, static_x, static_y, logits, loss); the last two
-        are the static outputs of the last graph captured."""
+        are the static outputs of the last graph captured, detached: they share the graph's output
+        memory, so every replay refreshes them, but hold no reference to the captured autograd graph
+        (which would keep its AccumulateGrad nodes, bound to the capture stream, alive)."""
         self.init_graph()
         self.warmup(empty=True)
         self.warmup()
@@ -139,6 +141,7 @@ class Graph:
                 with cuda.graph(g):
                     with torch.amp.autocast(device_type="cuda", dtype=torch.bfloat16):
                         logits, loss = self._step(clip=True)
+            logits, loss = logits.detach(), loss.detach()
             self.memsets_replaced[i] = finalize(g)
             cuda.synchronize()
         return self.graphs, self.compute_stream, self.static_x, self.static_y, logits, loss

@@ -281,6 +281,17 @@ int dopt_dw_gemm(const void* dy, int64_t ldd, const void* x_hat, int64_t ldx, co
 int dopt_graph_node_counts(void* graph, int64_t* counts, int n_counts);
 int dopt_graph_replace_memsets(void* graph, int64_t* n_replaced);
 
+/*
+ * Diagnostic, no counterpart in the reference: the memory system's ceiling for the quant-pack
+ * kernel's byte mix, measured with the same reads and writes and no arithmetic. n_units units of
+ * 8 elements; per unit it reads 16 bytes of x and, when noise != NULL, 32 bytes of noise, and for
+ * bits > 0 writes `bits` bytes to codes plus, every 32 units (a 256-element group), 8 bytes to
+ * meta. bits = 0 reads only (codes must still point to one writable byte). The bytes written are
+ * meaningless. Sizes: x 16*n_units, noise 32*n_units, codes bits*n_units, meta 8*ceil(n_units/32).
+ */
+int dopt_stream_probe(const void* x, const void* noise, void* codes, void* meta, int64_t n_units, int bits,
+                      void* stream);
+
 #ifdef __cplusplus
 }
 #endif

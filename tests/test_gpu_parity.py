@@ -369,3 +369,44 @@ def test_native_library_is_loaded():
     assert _lib.lib().dopt_abi_version() == 1
     with open("/proc/self/maps") as f:
         assert "libdopt.so" in f.read()
+
+
+@pytest.mark.parametrize("bits", [0, 1, 2, 4, 8])
+@pytest.mark.parametrize("with_noise", [True, False])
+def test_stream_probe_writes_hash_of_reads(bits, with_noise):
+    """dopt_stream_probe (the same-mix bandwidth ceiling the benchmark reports) reads every byte
+    it claims to: its outputs are the XOR of each unit's 16 x bytes (and 32 noise bytes) as
+    documented, checked against numpy, for a unit count that ends mid-group."""
+    L = _lib.lib()
+    n = 1000
+    gen = torch.Generator().manual_seed(bits * 2 + with_noise)
+    x = torch.randint(-2 ** 31, 2 ** 31 - 1, (n, 4), generator=gen, dtype=torch.int64).to(torch.int32)
+    nz = torch.randint(-2 ** 31, 2 ** 31 - 1, (n, 8), generator=gen, dtype=torch.int64).to(torch.int32)
+    h = np.bitwise_xor.reduce(x.numpy().view(np.uint32), axis=1)
+    if with_noise:
+        h = h ^ np.bitwise_xor.reduce(nz.numpy().view(np.uint32), axis=1)
+    codes = torch.full((max(bits, 1) * n,), 0x5A, dtype=torch.uint8, device="cuda")
+    meta = torch.zeros(2 * ((n + 31) // 32), dtype=torch.int32, device="cuda")
+    xd, nd = x.cuda(), nz.cuda()
+    rc = L.dopt_stream_probe(xd.data_ptr(), nd.data_ptr() if with_noise else None, codes.data_ptr(), meta.data_ptr(),
+                             n, bits, torch.cuda.current_stream().cuda_stream)
+    _lib.check(rc, "stream_probe")
+    got = codes.cpu().numpy()
+    if bits == 0:
+        assert (got[1:] == 0x5A).all() and got[0] in (0x5A, 1)
+        assert (got[0] == 1) == bool((h == 0x9E3779B9).any())
+        return
+    want = {1: h.astype(np.uint8), 2: h.astype(np.uint16), 4: h,
+            8: np.stack([h, h >> np.uint32(7)], axis=1).reshape(-1)}[bits]
+    np.testing.assert_array_equal(got.view(want.dtype), want)
+    want_meta = np.stack([h[::32], h[::32] >> np.uint32(3)], axis=1).reshape(-1)
+    np.testing.assert_array_equal(meta.cpu().numpy().view(np.uint32), want_meta)
+
+
+def test_stream_probe_rejects_bad_arguments():
+    L = _lib.lib()
+    buf = torch.zeros(64, dtype=torch.int32, device="cuda")
+    s = torch.cuda.current_stream().cuda_stream
+    assert L.dopt_stream_probe(buf.data_ptr(), None, buf.data_ptr(), buf.data_ptr(), 4, 3, s) == _lib.EINVAL
+    assert L.dopt_stream_probe(buf.data_ptr() + 4, None, buf.data_ptr(), buf.data_ptr(), 4, 2, s) == _lib.EINVAL
+    assert L.dopt_stream_probe(buf.data_ptr(), None, buf.data_ptr(), buf.data_ptr(), -1, 2, s) == _lib.EINVAL
