@@ -31,11 +31,6 @@ import statistics
 import sys
 import time
 
-# MIOpen's default find mode benchmarks every convolution solver on a layer's first call (seconds
-# per shape for the ResNet-50 leg); the heuristic mode keeps the run within minutes. Both the
-# plain and the compressed models run under the same mode.
-os.environ.setdefault("MIOPEN_FIND_MODE", "FAST")
-
 ROOT = os.path.dirname(os.path.abspath(__file__))
 if ROOT not in sys.path:
     sys.path.insert(0, ROOT)

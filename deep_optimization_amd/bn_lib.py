@@ -45,7 +45,9 @@ def _geom(X: Tensor, M: int, HW: int):
 
 
 def _f32(t: Optional[Tensor]) -> Optional[Tensor]:
-    return None if t is None else t.detach().contiguous().to(torch.float32)
+    if t is None or (t.dtype == torch.float32 and t.is_contiguous()):
+        return t
+    return t.detach().contiguous().to(torch.float32)
 
 
 def _ptr(t: Optional[Tensor]):

@@ -34,10 +34,13 @@ _NW, _NS = 8, 5  # launch-tuning arguments of the reference's operators (ignored
 
 
 def _update_running(running_mean, running_var, mean, var, momentum):
-    if running_mean is not None and mean is not None:
-        running_mean.mul_(1.0 - momentum).add_(mean, alpha=momentum)
-    if running_var is not None and var is not None:
-        running_var.mul_(1.0 - momentum).add_(var, alpha=momentum)
+    """running = running * (1 - momentum) + momentum * batch statistic (normalization_ops.py:56-57),
+    both buffers in one multi-tensor kernel per step."""
+    run = [t for t, b in ((running_mean, mean), (running_var, var)) if t is not None and b is not None]
+    new = [b for t, b in ((running_mean, mean), (running_var, var)) if t is not None and b is not None]
+    if run:
+        torch._foreach_mul_(run, 1.0 - momentum)
+        torch._foreach_add_(run, new, alpha=momentum)
 
 
 class _DOBatchNorm(Function):

@@ -29,7 +29,6 @@ import torch
 import torch.nn.functional as F
 from torch.amp import custom_bwd, custom_fwd
 from torch.autograd import Function
-from torch.nn.grad import conv1d_input, conv1d_weight, conv2d_input, conv2d_weight, conv3d_input, conv3d_weight
 from torch.nn.modules.utils import _pair, _single, _triple
 
 from ..dw_lib import dw_gemm_supported
@@ -60,36 +59,32 @@ class _DOConvnd(Function):
         q_tensor, q_meta, input_l = unified_quantize(input.to(torch.bfloat16), input_l, target_name, meta, clamp=True,
                                                      clamp_alpha=clamp_alpha)
         ctx.meta = stride, padding, dilation, groups, ema_grad_meta, clamp_alpha, bias is not None
-        ctx.save_for_backward(weight, q_tensor[0], q_tensor[1], q_tensor[2], input_l, learnable_scale)
+        # the backward computes with the weight in bf16 under autocast: keep the forward's cast
+        # (as autograd does for a plain convolution) instead of casting again
+        w_saved = weight if dt is None else (weight_compute if dt == torch.bfloat16 else weight.to(torch.bfloat16))
+        ctx.save_for_backward(w_saved, q_tensor[0], q_tensor[1], q_tensor[2], input_l, learnable_scale)
         ctx.q_inputs_meta = q_meta
         return forward_op(input, weight_compute, bias=bias_compute, stride=stride, padding=padding, dilation=dilation,
                           groups=groups)
 
     @staticmethod
     def run_backward(ctx, dy, dim, pad_fn):
-        """ops.py:273-387: restores the input, then the input and weight gradients by conv*_input /
-        conv*_weight."""
+        """ops.py:273-387: restores the input, then the input and weight gradients (the
+        conv*_input / conv*_weight pair of the reference, computed by one convolution_backward
+        call: the same two products, one dispatch)."""
         stride, padding, dilation, groups, _, _, has_bias = ctx.meta
-        weight, q0, q1, q2, input_l, _ = ctx.saved_tensors
+        weight_compute, q0, q1, q2, input_l, _ = ctx.saved_tensors  # bf16 under autocast (see run_forward)
         dt = _compute_dtype()
         if dt is not None:
             dy = dy.to(dt)
-            weight_compute = weight.to(torch.bfloat16)
-        else:
-            weight_compute = weight
         stride, padding, dilation = pad_fn(stride), pad_fn(padding), pad_fn(dilation)
         input = unified_dequantize((q0, q1, q2), ctx.q_inputs_meta, input_l)
-        if dt is None:
-            input = input.to(dy.dtype)
-        grad_input = {1: conv1d_input, 2: conv2d_input, 3: conv3d_input}[dim]
-        grad_weight = {1: conv1d_weight, 2: conv2d_weight, 3: conv3d_weight}[dim]
         dx = dw = db = None
-        if ctx.needs_input_grad[0]:
-            dx = grad_input(input.shape, weight_compute.to(dy.dtype), dy, stride=stride, padding=padding,
-                            dilation=dilation, groups=groups)
-        if ctx.needs_input_grad[1]:
-            dw = grad_weight(input.to(dy.dtype), weight_compute.shape, dy, stride=stride, padding=padding,
-                             dilation=dilation, groups=groups)
+        need_dx, need_dw = bool(ctx.needs_input_grad[0]), bool(ctx.needs_input_grad[1])
+        if need_dx or need_dw:
+            dx, dw, _ = torch.ops.aten.convolution_backward(
+                dy, input.to(dy.dtype), weight_compute.to(dy.dtype), None, list(stride), list(padding),
+                list(dilation), False, [0] * dim, groups, [need_dx, need_dw, False])
         if has_bias:
             db = dy.sum(dim=[0] + list(range(2, dy.dim())))
         if dx is not None and dt is not None:
