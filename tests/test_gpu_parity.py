@@ -410,3 +410,37 @@ def test_stream_probe_rejects_bad_arguments():
     assert L.dopt_stream_probe(buf.data_ptr(), None, buf.data_ptr(), buf.data_ptr(), 4, 3, s) == _lib.EINVAL
     assert L.dopt_stream_probe(buf.data_ptr() + 4, None, buf.data_ptr(), buf.data_ptr(), 4, 2, s) == _lib.EINVAL
     assert L.dopt_stream_probe(buf.data_ptr(), None, buf.data_ptr(), buf.data_ptr(), -1, 2, s) == _lib.EINVAL
+
+
+def test_beyond_2pow32_elements():
+    """A bf16 activation of 2^32 + 2^24 elements (8.6 GB; g = 1024, 4,210,688 groups): element
+    offsets past 2^32 take the kernels' 64-bit address arithmetic, and the Philox counter (the
+    element index / 16) passes 2^28. Three windows of groups (the first, the 64 on either side of
+    element 2^32, the last) match the oracle bit for bit, nearest and Philox, packed codes,
+    scale, min and the dequantized bf16 values."""
+    g, bits = 1024, 2
+    n_el = (1 << 32) + (1 << 24)
+    ng = n_el // g
+    x = torch.randn((n_el,), generator=torch.Generator(device=DEV).manual_seed(11), device=DEV,
+                    dtype=torch.bfloat16).view(1, ng, g)
+    b = (1 << 32) // g
+    windows = [slice(0, 64), slice(b - 64, b + 64), slice(ng - 64, ng)]
+    for rounding, seed, offset in (("nearest", 0, 0), ("philox", 7, 3)):
+        print(f"[>2^32] {rounding}", flush=True)
+        p, s, m = torch.ops.act_lib.quant_pack(x, bits, g, False, 0.0, False, ROUNDINGS[rounding], None, seed, offset,
+                                               torch.float32)
+        y = torch.ops.act_lib.dequant_unpack(p, s, m, bits, g, torch.bfloat16)
+        torch.cuda.synchronize()
+        for w in windows:
+            xs = np_view(x[0, w])
+            if rounding == "nearest":
+                ref = oracle.quant_pack(xs, g, bits)
+            else:  # the Philox stream at these element indices, through the oracle's noise-tensor path
+                u = oracle.philox_noise(w.start * g, (w.stop - w.start) * g, seed, offset).reshape(-1, g)
+                ref = oracle.quant_pack(xs, g, bits, rounding=oracle.STOCH_NOISE, noise=u)
+            assert_quant_equal((p[w], s.view(-1)[w], m.view(-1)[w]), ref, f"{rounding} groups {w}")
+            yo = oracle.dequant_unpack(*ref, g, bits, y_dtype=oracle.BF16)
+            np.testing.assert_array_equal(np_view(y.view(-1, g)[w]), yo, err_msg=f"{rounding} dequant {w}")
+        del p, s, m, y
+    del x
+    torch.cuda.empty_cache()
