@@ -45,9 +45,12 @@ G_SIZE, BITS = 256, 2
 NEAREST, NOISE, PHILOX = 0, 1, 2
 
 
+_T0 = time.perf_counter()
+
+
 def progress(msg: str) -> None:
-    """A progress line on stderr (the JSON result is the only stdout line)."""
-    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+    """A progress line on stderr (the JSON result is the only stdout line), with the seconds elapsed."""
+    print(f"[bench {time.perf_counter() - _T0:6.1f}s] {msg}", file=sys.stderr, flush=True)
 
 
 def pack_bytes(n_elem, n_groups, in_bytes, bits, noise=False):

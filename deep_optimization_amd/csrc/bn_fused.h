@@ -66,11 +66,13 @@ struct BnBwdArgs {
     uint16_t* dx;            // bf16
 };
 
+// vw: elements per vector access (8, 4, 2 or 1); it divides HW, stride_n and stride_c, and every
+// element pointer is aligned to vw elements (bn_width in the C ABI picks it)
 int64_t bn_nchunks(int64_t M);
-int launch_bn_reduce(const void* x, int dt, const BnGeom& g, float* partial, float* sum, float* sumsq, bool vec,
+int launch_bn_reduce(const void* x, int dt, const BnGeom& g, float* partial, float* sum, float* sumsq, int vw,
                      hipStream_t s);
-int launch_bn_fwd(const BnFwdArgs& a, int dt, int mode, int group, int bits, bool vec, hipStream_t s);
-int launch_bn_bwd_reduce(const BnBwdArgs& a, int dyt, int mode, int group, int bits, bool vec, hipStream_t s);
-int launch_bn_bwd_dx(const BnBwdArgs& a, int dyt, int mode, int group, int bits, bool vec, hipStream_t s);
+int launch_bn_fwd(const BnFwdArgs& a, int dt, int mode, int group, int bits, int vw, hipStream_t s);
+int launch_bn_bwd_reduce(const BnBwdArgs& a, int dyt, int mode, int group, int bits, int vw, hipStream_t s);
+int launch_bn_bwd_dx(const BnBwdArgs& a, int dyt, int mode, int group, int bits, int vw, hipStream_t s);
 
 }  // namespace dopt

@@ -21,8 +21,11 @@
 // modes), x_hat' = fma(q, scale, min), dx = ((fma(-x_hat', dw/M, dy - db/M)) * w) * invstd.
 //
 // Mapping: a workgroup of 256 lanes covers 4 blocks of 2048 consecutive elements of one channel,
-// 8 per lane per block (one 16-byte access for 2-byte types when HW is a multiple of 8, element
-// by element otherwise), with every block's loads issued before the first is used. A group of G elements spans G/8 aligned lanes (4..64), so group min/max and the
+// 8 per lane per block, read and written as 8 / V row-contiguous accesses of V elements, V the
+// largest of 8, 4, 2, 1 that divides HW and both strides and fits the pointers' alignment (so an
+// access never crosses a row: one 16-byte access for 2-byte types at HW = 56 x 56, two 8-byte
+// ones at 14 x 14, eight 2-byte ones at 7 x 7), with every block's loads issued before the first
+// is used. A group of G elements spans G/8 aligned lanes (4..64), so group min/max and the
 // code merge stay inside a wave. Reductions are two-stage and ordered (workgroup partials, then
 // one wave per channel), so sums are deterministic and need no zeroed buffer or atomics.
 #include "bn_fused.h"
@@ -36,46 +39,117 @@ constexpr int EPL = 8;
 constexpr int64_t WG_ELEMS = TPB * EPL;
 constexpr int ITER = (int)(BN_CHUNK / WG_ELEMS);  // 2048-element blocks per workgroup (loads issued together)
 
-// element offset of channel c's element e; e < M < 2^31 (checked by the host), so the divide is
-// a 32-bit one
-__device__ __forceinline__ int64_t bn_off(const BnGeom& g, int64_t c, int64_t e) {
+// Position of element e of channel c: row n = e / HW, column r = e % HW, at offset
+// row + r with row = n * stride_n + c * stride_c. A lane finds its first element's position with
+// one 32-bit division (e < M + BN_CHUNK < 2^32, the host checks M < 2^31) and walks from there:
+// V elements to the next chunk of its 8, WG_ELEMS to its next block, each a remainder step
+// below HW plus whole rows, so one conditional wrap per step.
+struct RowCursor {
+    int64_t row;
+    uint32_t r;
+};
+
+__device__ __forceinline__ RowCursor cursor_at(const BnGeom& g, int64_t c, int64_t e) {
     const uint32_t hw = (uint32_t)g.HW, ee = (uint32_t)e;
     const uint32_t n = ee / hw;
-    return (int64_t)n * g.stride_n + c * g.stride_c + (int64_t)(ee - n * hw);
+    return {(int64_t)n * g.stride_n + c * g.stride_c, ee - n * hw};
 }
 
-template <int DT>
-__device__ __forceinline__ float load1(const void* base, int64_t off) {
-    if constexpr (DT == DT_F32) return ((const float*)base)[off];
-    else if constexpr (DT == DT_BF16) return bf16_bits_to_f32(((const uint16_t*)base)[off]);
-    else return (float)__builtin_bit_cast(_Float16, ((const uint16_t*)base)[off]);
+// advance by dr < HW elements plus the whole rows folded into drow (= rows * stride_n)
+__device__ __forceinline__ void cursor_step(RowCursor& p, const BnGeom& g, uint32_t dr, int64_t drow) {
+    p.r += dr;
+    p.row += drow;
+    if (p.r >= (uint32_t)g.HW) {
+        p.r -= (uint32_t)g.HW;
+        p.row += g.stride_n;
+    }
 }
 
-// 8 elements e0..e0+7 of channel c (VEC: one row, contiguous; else each bounded by M, 0 beyond)
-template <int DT, bool VEC>
-__device__ __forceinline__ void load8(const void* base, const BnGeom& g, int64_t c, int64_t e0, int64_t M,
-                                      float* v) {
-    if constexpr (VEC) {
-        const char* p = (const char*)base + bn_off(g, c, e0) * DType<DT>::bytes;
-        widen16<DT>(ld16<false>(p), v);
-        if constexpr (DT == DT_F32) widen16<DT>(ld16<false>(p + 16), v + 4);
-    } else {
+// cursors of the lane's ITER blocks (elements base + it * WG_ELEMS)
+__device__ __forceinline__ void block_cursors(const BnGeom& g, int64_t c, int64_t base, RowCursor* cur) {
+    const uint32_t hw = (uint32_t)g.HW;
+    const uint32_t bq = (uint32_t)WG_ELEMS / hw, br = (uint32_t)WG_ELEMS - bq * hw;
+    const int64_t brow = (int64_t)bq * g.stride_n;
+    cur[0] = cursor_at(g, c, base);
 #pragma unroll
-        for (int k = 0; k < EPL; ++k) v[k] = (e0 + k < M) ? load1<DT>(base, bn_off(g, c, e0 + k)) : 0.0f;
+    for (int it = 1; it < ITER; ++it) {
+        cur[it] = cur[it - 1];
+        cursor_step(cur[it], g, br, brow);
+    }
+}
+
+// V consecutive elements of one row at element offset off (aligned to V elements)
+template <int DT, int V>
+__device__ __forceinline__ void ldv(const void* base, int64_t off, float* v) {
+    const char* p = (const char*)base + off * DType<DT>::bytes;
+    if constexpr (V * DType<DT>::bytes >= 16) {
+#pragma unroll
+        for (int h = 0; h < V * DType<DT>::bytes / 16; ++h) widen16<DT>(ld16<false>(p + 16 * h), v + h * DType<DT>::per16);
+    } else if constexpr (DT == DT_F32) {
+        if constexpr (V == 2) {
+            const uint2 u = *(const uint2*)p;
+            v[0] = __uint_as_float(u.x);
+            v[1] = __uint_as_float(u.y);
+        } else {
+            v[0] = *(const float*)p;
+        }
+    } else {
+        uint32_t w[2] = {0u, 0u};
+        if constexpr (V == 4) {
+            const uint2 u = *(const uint2*)p;
+            w[0] = u.x;
+            w[1] = u.y;
+        } else if constexpr (V == 2) {
+            w[0] = *(const uint32_t*)p;
+        } else {
+            w[0] = *(const uint16_t*)p;
+        }
+#pragma unroll
+        for (int k = 0; k < V; ++k) {
+            const uint32_t b = (w[k >> 1] >> (16 * (k & 1))) & 0xffffu;
+            if constexpr (DT == DT_BF16) v[k] = __uint_as_float(b << 16);
+            else v[k] = (float)__builtin_bit_cast(_Float16, (uint16_t)b);
+        }
+    }
+}
+
+// the lane's 8 elements e0..e0+7 (cursor p at e0) as EPL / V row-contiguous loads; chunks at or
+// past M read as 0 (M is a multiple of V, so a chunk is all in or all out)
+template <int DT, int V>
+__device__ __forceinline__ void load8(const void* base, const BnGeom& g, RowCursor p, int64_t e0, int64_t M,
+                                      float* v) {
+#pragma unroll
+    for (int j = 0; j < EPL / V; ++j) {
+        if (j) cursor_step(p, g, V, 0);
+        if (V == EPL || e0 + j * V < M) {
+            ldv<DT, V>(base, p.row + p.r, v + j * V);
+        } else {
+#pragma unroll
+            for (int k = 0; k < V; ++k) v[j * V + k] = 0.0f;
+        }
     }
 }
 
 // bf16 outputs are streamed (non-temporal: written once, read by another kernel much later)
-template <bool VEC>
-__device__ __forceinline__ void store8_bf16(uint16_t* base, const BnGeom& g, int64_t c, int64_t e0, int64_t M,
+template <int V>
+__device__ __forceinline__ void store8_bf16(uint16_t* base, const BnGeom& g, RowCursor p, int64_t e0, int64_t M,
                                             const float* v) {
-    if constexpr (VEC) {
-        st16<true>(base + bn_off(g, c, e0), make_uint4(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]),
-                                                      pack_bf16x2(v[4], v[5]), pack_bf16x2(v[6], v[7])));
-    } else {
 #pragma unroll
-        for (int k = 0; k < EPL; ++k)
-            if (e0 + k < M) base[bn_off(g, c, e0 + k)] = to_bf16(v[k]);
+    for (int j = 0; j < EPL / V; ++j) {
+        if (j) cursor_step(p, g, V, 0);
+        if (V < EPL && e0 + j * V >= M) continue;
+        uint16_t* q = base + p.row + p.r;
+        const float* u = v + j * V;
+        if constexpr (V == 8) {
+            st16<true>(q, make_uint4(pack_bf16x2(u[0], u[1]), pack_bf16x2(u[2], u[3]), pack_bf16x2(u[4], u[5]),
+                                     pack_bf16x2(u[6], u[7])));
+        } else if constexpr (V == 4) {
+            *(uint2*)q = make_uint2(pack_bf16x2(u[0], u[1]), pack_bf16x2(u[2], u[3]));
+        } else if constexpr (V == 2) {
+            *(uint32_t*)q = pack_bf16x2(u[0], u[1]);
+        } else {
+            *q = to_bf16(u[0]);
+        }
     }
 }
 
@@ -186,18 +260,20 @@ __device__ __forceinline__ void load_codes(const uint32_t* chan, int64_t e0, int
 }
 
 // ------------------------------------------------------------------ statistics
-template <int DT, bool VEC>
+template <int DT, int V>
 __global__ __launch_bounds__(TPB) void bn_stats_kernel(const void* __restrict__ x, BnGeom g,
                                                        float* __restrict__ partial, int64_t nchunks) {
     const int64_t c = blockIdx.y, chunk = blockIdx.x;
     const int64_t M = g.N * g.HW;
     const int64_t base = chunk * BN_CHUNK + (int64_t)threadIdx.x * EPL;
+    RowCursor cur[ITER];
+    block_cursors(g, c, base, cur);
     float v[ITER][EPL];
 #pragma unroll
     for (int it = 0; it < ITER; ++it) {
         const int64_t e0 = base + it * WG_ELEMS;
         if (e0 < M) {
-            load8<DT, VEC>(x, g, c, e0, M, v[it]);
+            load8<DT, V>(x, g, cur[it], e0, M, v[it]);
         } else {
 #pragma unroll
             for (int k = 0; k < EPL; ++k) v[it][k] = 0.0f;
@@ -259,10 +335,10 @@ __device__ __forceinline__ void channel_stats(const BnFwdArgs& a, int64_t c, int
 // ------------------------------------------------------------------ forward
 // One 2048-element block of the forward: y (and the mask / codes / scale / min) from the lane's 8
 // loaded values. Whole groups are active or not (M % group == 0), so the group's lanes agree.
-template <int MODE, bool VEC>
-__device__ __forceinline__ void fwd_block(const BnFwdArgs& a, int64_t c, int64_t e0, int64_t M, bool active,
-                                          const float* v, float mean, float inv, float w, float b, int lg,
-                                          int bits, int relu6) {
+template <int MODE, int V>
+__device__ __forceinline__ void fwd_block(const BnFwdArgs& a, int64_t c, RowCursor pos, int64_t e0, int64_t M,
+                                          bool active, const float* v, float mean, float inv, float w, float b,
+                                          int lg, int bits, int relu6) {
     const BnGeom& g = a.g;
     float xh[EPL], y[EPL];
 #pragma unroll
@@ -272,8 +348,8 @@ __device__ __forceinline__ void fwd_block(const BnFwdArgs& a, int64_t c, int64_t
     }
     if constexpr (MODE == BN_NORM) {
         if (active) {
-            store8_bf16<VEC>(a.y, g, c, e0, M, y);
-            store8_bf16<VEC>(a.xhat, g, c, e0, M, xh);
+            store8_bf16<V>(a.y, g, pos, e0, M, y);
+            store8_bf16<V>(a.xhat, g, pos, e0, M, xh);
         }
     } else {
         uint32_t m8 = 0;
@@ -285,7 +361,7 @@ __device__ __forceinline__ void fwd_block(const BnFwdArgs& a, int64_t c, int64_t
                 y[k] = relu6 ? __builtin_amdgcn_fmed3f(y[k], 0.0f, 6.0f) : (on ? y[k] : 0.0f);
             }
         }
-        if (active) store8_bf16<VEC>(a.y, g, c, e0, M, y);
+        if (active) store8_bf16<V>(a.y, g, pos, e0, M, y);
         if constexpr (MODE == BN_RELU_QUANT) store_mask(a.relu_packed + c * (M >> 5), e0, m8, active);
 
         // values quantized: the squashed x_hat (BN_QUANT) or x_hat itself (ReLU modes)
@@ -350,17 +426,19 @@ __device__ __forceinline__ void fwd_block(const BnFwdArgs& a, int64_t c, int64_t
 
 // A workgroup covers ITER consecutive 2048-element blocks of one channel; all loads are issued
 // before the first block is processed.
-template <int DT, int MODE, bool VEC>
+template <int DT, int MODE, int V>
 __global__ __launch_bounds__(TPB) void bn_fwd_kernel(BnFwdArgs a, int lg, int bits, int relu6) {
     const int64_t c = blockIdx.y;
     const int64_t M = a.g.N * a.g.HW;
     const int64_t base = (int64_t)blockIdx.x * BN_CHUNK + (int64_t)threadIdx.x * EPL;
+    RowCursor cur[ITER];
+    block_cursors(a.g, c, base, cur);
     float v[ITER][EPL];
 #pragma unroll
     for (int it = 0; it < ITER; ++it) {
         const int64_t e0 = base + it * WG_ELEMS;
         if (e0 < M) {
-            load8<DT, VEC>(a.x, a.g, c, e0, M, v[it]);
+            load8<DT, V>(a.x, a.g, cur[it], e0, M, v[it]);
         } else {
 #pragma unroll
             for (int k = 0; k < EPL; ++k) v[it][k] = 0.0f;
@@ -372,18 +450,18 @@ __global__ __launch_bounds__(TPB) void bn_fwd_kernel(BnFwdArgs a, int lg, int bi
 #pragma unroll
     for (int it = 0; it < ITER; ++it) {
         const int64_t e0 = base + it * WG_ELEMS;
-        fwd_block<MODE, VEC>(a, c, e0, M, e0 < M, v[it], mean, inv, w, b, lg, bits, relu6);
+        fwd_block<MODE, V>(a, c, cur[it], e0, M, e0 < M, v[it], mean, inv, w, b, lg, bits, relu6);
     }
 }
 
 // ------------------------------------------------------------------ backward
 // dy (times the ReLU mask) and x_hat' of the lane's 8 elements
-template <int DYT, int MODE, bool VEC>
-__device__ __forceinline__ void bwd_operands(const BnBwdArgs& a, int64_t c, int64_t e0, int64_t M, int lg,
-                                             int bits, float* xh, float* dy) {
-    load8<DYT, VEC>(a.dy, a.g, c, e0, M, dy);
+template <int DYT, int MODE, int V>
+__device__ __forceinline__ void bwd_operands(const BnBwdArgs& a, int64_t c, RowCursor pos, int64_t e0, int64_t M,
+                                             int lg, int bits, float* xh, float* dy) {
+    load8<DYT, V>(a.dy, a.g, pos, e0, M, dy);
     if constexpr (MODE == BN_NORM) {
-        load8<DT_BF16, VEC>(a.xhat, a.g, c, e0, M, xh);
+        load8<DT_BF16, V>(a.xhat, a.g, pos, e0, M, xh);
     } else {
         int q[EPL];
         load_codes(a.packed + c * ((M * bits) >> 5), e0, bits, q);
@@ -400,17 +478,19 @@ __device__ __forceinline__ void bwd_operands(const BnBwdArgs& a, int64_t c, int6
     }
 }
 
-template <int DYT, int MODE, bool VEC>
+template <int DYT, int MODE, int V>
 __global__ __launch_bounds__(TPB) void bn_bwd_reduce_kernel(BnBwdArgs a, int lg, int bits, int64_t nchunks) {
     const int64_t c = blockIdx.y, chunk = blockIdx.x;
     const int64_t M = a.g.N * a.g.HW;
     const int64_t base = chunk * BN_CHUNK + (int64_t)threadIdx.x * EPL;
+    RowCursor cur[ITER];
+    block_cursors(a.g, c, base, cur);
     float xh[ITER][EPL], dy[ITER][EPL];
 #pragma unroll
     for (int it = 0; it < ITER; ++it) {
         const int64_t e0 = base + it * WG_ELEMS;
         if (e0 < M) {
-            bwd_operands<DYT, MODE, VEC>(a, c, e0, M, lg, bits, xh[it], dy[it]);
+            bwd_operands<DYT, MODE, V>(a, c, cur[it], e0, M, lg, bits, xh[it], dy[it]);
         } else {
 #pragma unroll
             for (int k = 0; k < EPL; ++k) xh[it][k] = dy[it][k] = 0.0f;
@@ -431,16 +511,18 @@ __global__ __launch_bounds__(TPB) void bn_bwd_reduce_kernel(BnBwdArgs a, int lg,
     }
 }
 
-template <int DYT, int MODE, bool VEC>
+template <int DYT, int MODE, int V>
 __global__ __launch_bounds__(TPB) void bn_bwd_dx_kernel(BnBwdArgs a, int lg, int bits) {
     const int64_t c = blockIdx.y;
     const int64_t M = a.g.N * a.g.HW;
     const int64_t base = (int64_t)blockIdx.x * BN_CHUNK + (int64_t)threadIdx.x * EPL;
+    RowCursor cur[ITER];
+    block_cursors(a.g, c, base, cur);
     float xh[ITER][EPL], dy[ITER][EPL];
 #pragma unroll
     for (int it = 0; it < ITER; ++it) {
         const int64_t e0 = base + it * WG_ELEMS;
-        if (e0 < M) bwd_operands<DYT, MODE, VEC>(a, c, e0, M, lg, bits, xh[it], dy[it]);
+        if (e0 < M) bwd_operands<DYT, MODE, V>(a, c, cur[it], e0, M, lg, bits, xh[it], dy[it]);
     }
     const float Mf = (float)M;
     const float dwm = a.dw_in[c] / Mf, dbm = a.db_in[c] / Mf;
@@ -453,7 +535,7 @@ __global__ __launch_bounds__(TPB) void bn_bwd_dx_kernel(BnBwdArgs a, int lg, int
         float dx[EPL];
 #pragma unroll
         for (int k = 0; k < EPL; ++k) dx[k] = (fmaf(-xh[it][k], dwm, dy[it][k] - dbm) * w) * inv;
-        store8_bf16<VEC>(a.dx, a.g, c, e0, M, dx);
+        store8_bf16<V>(a.dx, a.g, cur[it], e0, M, dx);
     }
 }
 
@@ -463,54 +545,74 @@ int log2i(int v) {
     return l;
 }
 
+// kernel template for the vector width vw (8, 4, 2 or 1 elements per access)
+#define DOPT_BN_BY_WIDTH(vw, LAUNCH) \
+    do {                             \
+        switch (vw) {                \
+            case 8: LAUNCH(8); break; \
+            case 4: LAUNCH(4); break; \
+            case 2: LAUNCH(2); break; \
+            default: LAUNCH(1); break; \
+        }                            \
+    } while (0)
+
 template <int DT>
-int fwd_dt(const BnFwdArgs& a, int mode, int group, int bits, bool vec, hipStream_t s) {
+int fwd_dt(const BnFwdArgs& a, int mode, int group, int bits, int vw, hipStream_t s) {
     const int64_t M = a.g.N * a.g.HW;
     const int lg = mode == BN_NORM ? 3 : log2i(group);
     const dim3 grid((unsigned)bn_nchunks(M), (unsigned)a.g.C);
     const int relu6 = mode == BN_RELU6_QUANT;
-#define DOPT_BN_FWD(MODE_, VEC_) hipLaunchKernelGGL((bn_fwd_kernel<DT, MODE_, VEC_>), grid, dim3(TPB), 0, s, a, lg, bits, relu6)
-    if (mode == BN_NORM) {
-        if (vec) DOPT_BN_FWD(BN_NORM, true); else DOPT_BN_FWD(BN_NORM, false);
-    } else if (mode == BN_QUANT) {
-        if (vec) DOPT_BN_FWD(BN_QUANT, true); else DOPT_BN_FWD(BN_QUANT, false);
-    } else {
-        if (vec) DOPT_BN_FWD(BN_RELU_QUANT, true); else DOPT_BN_FWD(BN_RELU_QUANT, false);
-    }
+#define DOPT_BN_FWD(MODE_, V_) hipLaunchKernelGGL((bn_fwd_kernel<DT, MODE_, V_>), grid, dim3(TPB), 0, s, a, lg, bits, relu6)
+#define DOPT_BN_FWD_NORM(V_) DOPT_BN_FWD(BN_NORM, V_)
+#define DOPT_BN_FWD_QUANT(V_) DOPT_BN_FWD(BN_QUANT, V_)
+#define DOPT_BN_FWD_RELU(V_) DOPT_BN_FWD(BN_RELU_QUANT, V_)
+    if (mode == BN_NORM) DOPT_BN_BY_WIDTH(vw, DOPT_BN_FWD_NORM);
+    else if (mode == BN_QUANT) DOPT_BN_BY_WIDTH(vw, DOPT_BN_FWD_QUANT);
+    else DOPT_BN_BY_WIDTH(vw, DOPT_BN_FWD_RELU);
+#undef DOPT_BN_FWD_RELU
+#undef DOPT_BN_FWD_QUANT
+#undef DOPT_BN_FWD_NORM
 #undef DOPT_BN_FWD
     return 0;
 }
 
 template <int DYT>
-int bwd_dt(const BnBwdArgs& a, int mode, int group, int bits, bool vec, bool reduce, hipStream_t s) {
+int bwd_dt(const BnBwdArgs& a, int mode, int group, int bits, int vw, bool reduce, hipStream_t s) {
     const int64_t M = a.g.N * a.g.HW;
     const int lg = mode == BN_NORM ? 3 : log2i(group);
     const int64_t nch = bn_nchunks(M);
     const int m = mode == BN_RELU6_QUANT ? BN_RELU_QUANT : mode;
+    const dim3 grid((unsigned)nch, (unsigned)a.g.C);
     if (reduce) {
-        const dim3 grid((unsigned)nch, (unsigned)a.g.C);
-#define DOPT_BN_RED(MODE_, VEC_) hipLaunchKernelGGL((bn_bwd_reduce_kernel<DYT, MODE_, VEC_>), grid, dim3(TPB), 0, s, a, lg, bits, nch)
+#define DOPT_BN_RED(MODE_, V_) hipLaunchKernelGGL((bn_bwd_reduce_kernel<DYT, MODE_, V_>), grid, dim3(TPB), 0, s, a, lg, bits, nch)
+#define DOPT_BN_RED_NORM(V_) DOPT_BN_RED(BN_NORM, V_)
+#define DOPT_BN_RED_QUANT(V_) DOPT_BN_RED(BN_QUANT, V_)
+#define DOPT_BN_RED_RELU(V_) DOPT_BN_RED(BN_RELU_QUANT, V_)
         if (nch == 0) {
         } else if (m == BN_NORM) {
-            if (vec) DOPT_BN_RED(BN_NORM, true); else DOPT_BN_RED(BN_NORM, false);
+            DOPT_BN_BY_WIDTH(vw, DOPT_BN_RED_NORM);
         } else if (m == BN_QUANT) {
-            if (vec) DOPT_BN_RED(BN_QUANT, true); else DOPT_BN_RED(BN_QUANT, false);
+            DOPT_BN_BY_WIDTH(vw, DOPT_BN_RED_QUANT);
         } else {
-            if (vec) DOPT_BN_RED(BN_RELU_QUANT, true); else DOPT_BN_RED(BN_RELU_QUANT, false);
+            DOPT_BN_BY_WIDTH(vw, DOPT_BN_RED_RELU);
         }
+#undef DOPT_BN_RED_RELU
+#undef DOPT_BN_RED_QUANT
+#undef DOPT_BN_RED_NORM
 #undef DOPT_BN_RED
         hipLaunchKernelGGL(bn_finalize_kernel, dim3((unsigned)a.g.C), dim3(64), 0, s, (const float*)a.partial,
                            a.g.C, nch, a.dw, a.db);
     } else {
-        const dim3 grid((unsigned)nch, (unsigned)a.g.C);
-#define DOPT_BN_DX(MODE_, VEC_) hipLaunchKernelGGL((bn_bwd_dx_kernel<DYT, MODE_, VEC_>), grid, dim3(TPB), 0, s, a, lg, bits)
-        if (m == BN_NORM) {
-            if (vec) DOPT_BN_DX(BN_NORM, true); else DOPT_BN_DX(BN_NORM, false);
-        } else if (m == BN_QUANT) {
-            if (vec) DOPT_BN_DX(BN_QUANT, true); else DOPT_BN_DX(BN_QUANT, false);
-        } else {
-            if (vec) DOPT_BN_DX(BN_RELU_QUANT, true); else DOPT_BN_DX(BN_RELU_QUANT, false);
-        }
+#define DOPT_BN_DX(MODE_, V_) hipLaunchKernelGGL((bn_bwd_dx_kernel<DYT, MODE_, V_>), grid, dim3(TPB), 0, s, a, lg, bits)
+#define DOPT_BN_DX_NORM(V_) DOPT_BN_DX(BN_NORM, V_)
+#define DOPT_BN_DX_QUANT(V_) DOPT_BN_DX(BN_QUANT, V_)
+#define DOPT_BN_DX_RELU(V_) DOPT_BN_DX(BN_RELU_QUANT, V_)
+        if (m == BN_NORM) DOPT_BN_BY_WIDTH(vw, DOPT_BN_DX_NORM);
+        else if (m == BN_QUANT) DOPT_BN_BY_WIDTH(vw, DOPT_BN_DX_QUANT);
+        else DOPT_BN_BY_WIDTH(vw, DOPT_BN_DX_RELU);
+#undef DOPT_BN_DX_RELU
+#undef DOPT_BN_DX_QUANT
+#undef DOPT_BN_DX_NORM
 #undef DOPT_BN_DX
     }
     return 0;
@@ -520,50 +622,52 @@ int bwd_dt(const BnBwdArgs& a, int mode, int group, int bits, bool vec, bool red
 
 int64_t bn_nchunks(int64_t M) { return (M + BN_CHUNK - 1) / BN_CHUNK; }
 
-int launch_bn_reduce(const void* x, int dt, const BnGeom& g, float* partial, float* sum, float* sumsq, bool vec,
+int launch_bn_reduce(const void* x, int dt, const BnGeom& g, float* partial, float* sum, float* sumsq, int vw,
                      hipStream_t s) {
     const int64_t M = g.N * g.HW;
     const int64_t nch = bn_nchunks(M);
     const dim3 grid((unsigned)nch, (unsigned)g.C);
-#define DOPT_BN_STATS(DT_)                                                                                   \
-    do {                                                                                                     \
-        if (vec) hipLaunchKernelGGL((bn_stats_kernel<DT_, true>), grid, dim3(TPB), 0, s, x, g, partial, nch);  \
-        else hipLaunchKernelGGL((bn_stats_kernel<DT_, false>), grid, dim3(TPB), 0, s, x, g, partial, nch);     \
-    } while (0)
+#define DOPT_BN_STATS(DT_, V_) hipLaunchKernelGGL((bn_stats_kernel<DT_, V_>), grid, dim3(TPB), 0, s, x, g, partial, nch)
+#define DOPT_BN_STATS_F32(V_) DOPT_BN_STATS(DT_F32, V_)
+#define DOPT_BN_STATS_F16(V_) DOPT_BN_STATS(DT_F16, V_)
+#define DOPT_BN_STATS_BF16(V_) DOPT_BN_STATS(DT_BF16, V_)
     if (nch > 0) {
         switch (dt) {
-            case DT_F32: DOPT_BN_STATS(DT_F32); break;
-            case DT_F16: DOPT_BN_STATS(DT_F16); break;
-            default: DOPT_BN_STATS(DT_BF16); break;
+            case DT_F32: DOPT_BN_BY_WIDTH(vw, DOPT_BN_STATS_F32); break;
+            case DT_F16: DOPT_BN_BY_WIDTH(vw, DOPT_BN_STATS_F16); break;
+            default: DOPT_BN_BY_WIDTH(vw, DOPT_BN_STATS_BF16); break;
         }
     }
+#undef DOPT_BN_STATS_BF16
+#undef DOPT_BN_STATS_F16
+#undef DOPT_BN_STATS_F32
 #undef DOPT_BN_STATS
     hipLaunchKernelGGL(bn_finalize_kernel, dim3((unsigned)g.C), dim3(64), 0, s, (const float*)partial, g.C, nch,
                        sum, sumsq);
     return 0;
 }
 
-int launch_bn_fwd(const BnFwdArgs& a, int dt, int mode, int group, int bits, bool vec, hipStream_t s) {
+int launch_bn_fwd(const BnFwdArgs& a, int dt, int mode, int group, int bits, int vw, hipStream_t s) {
     switch (dt) {
-        case DT_F32: return fwd_dt<DT_F32>(a, mode, group, bits, vec, s);
-        case DT_F16: return fwd_dt<DT_F16>(a, mode, group, bits, vec, s);
-        default: return fwd_dt<DT_BF16>(a, mode, group, bits, vec, s);
+        case DT_F32: return fwd_dt<DT_F32>(a, mode, group, bits, vw, s);
+        case DT_F16: return fwd_dt<DT_F16>(a, mode, group, bits, vw, s);
+        default: return fwd_dt<DT_BF16>(a, mode, group, bits, vw, s);
     }
 }
 
-int launch_bn_bwd_reduce(const BnBwdArgs& a, int dyt, int mode, int group, int bits, bool vec, hipStream_t s) {
+int launch_bn_bwd_reduce(const BnBwdArgs& a, int dyt, int mode, int group, int bits, int vw, hipStream_t s) {
     switch (dyt) {
-        case DT_F32: return bwd_dt<DT_F32>(a, mode, group, bits, vec, true, s);
-        case DT_F16: return bwd_dt<DT_F16>(a, mode, group, bits, vec, true, s);
-        default: return bwd_dt<DT_BF16>(a, mode, group, bits, vec, true, s);
+        case DT_F32: return bwd_dt<DT_F32>(a, mode, group, bits, vw, true, s);
+        case DT_F16: return bwd_dt<DT_F16>(a, mode, group, bits, vw, true, s);
+        default: return bwd_dt<DT_BF16>(a, mode, group, bits, vw, true, s);
     }
 }
 
-int launch_bn_bwd_dx(const BnBwdArgs& a, int dyt, int mode, int group, int bits, bool vec, hipStream_t s) {
+int launch_bn_bwd_dx(const BnBwdArgs& a, int dyt, int mode, int group, int bits, int vw, hipStream_t s) {
     switch (dyt) {
-        case DT_F32: return bwd_dt<DT_F32>(a, mode, group, bits, vec, false, s);
-        case DT_F16: return bwd_dt<DT_F16>(a, mode, group, bits, vec, false, s);
-        default: return bwd_dt<DT_BF16>(a, mode, group, bits, vec, false, s);
+        case DT_F32: return bwd_dt<DT_F32>(a, mode, group, bits, vw, false, s);
+        case DT_F16: return bwd_dt<DT_F16>(a, mode, group, bits, vw, false, s);
+        default: return bwd_dt<DT_BF16>(a, mode, group, bits, vw, false, s);
     }
 }
 

@@ -100,12 +100,27 @@ int bn_geom(int64_t N, int64_t C, int64_t HW, int64_t stride_n, int64_t stride_c
     return DOPT_OK;
 }
 
-bool bn_vec(const dopt::BnGeom& g, std::initializer_list<const void*> ptrs) {
-    if (g.HW % 8 || g.stride_n % 8 || g.stride_c % 8) return false;
-    for (const void* p : ptrs)
-        if (p && !aligned16(p)) return false;
-    return true;
+// Elements per vector access of the BatchNorm kernels: the largest of 8, 4, 2 that divides HW and
+// both strides (so no access crosses a row) with every tensor (pointer, element bytes) aligned
+// for it; else 1.
+struct BnTensor {
+    const void* p;
+    int bytes;
+};
+int bn_width(const dopt::BnGeom& g, std::initializer_list<BnTensor> ts) {
+    for (int v : {8, 4, 2}) {
+        if (g.HW % v || g.stride_n % v || g.stride_c % v) continue;
+        bool ok = true;
+        for (const BnTensor& t : ts) {
+            const uintptr_t align = (uintptr_t)(v * t.bytes < 16 ? v * t.bytes : 16);
+            if (t.p && ((uintptr_t)t.p % align)) ok = false;
+        }
+        if (ok) return v;
+    }
+    return 1;
 }
+
+int bn_bytes(int dt) { return dt == DOPT_F32 ? 4 : 2; }
 
 int bn_dtype(int dt, const char* what) {
     if (dt != DOPT_F32 && dt != DOPT_F16 && dt != DOPT_BF16)
@@ -401,7 +416,8 @@ int dopt_bn_reduce(const void* x, int x_dtype, int64_t N, int64_t C, int64_t HW,
     if (C == 0) return ok();
     if (!sum || !sumsq || (N * HW > 0 && (!x || !workspace))) return fail(DOPT_EINVAL, "null pointer argument");
     (void)hipGetLastError();
-    dopt::launch_bn_reduce(x, x_dtype, g, workspace, sum, sumsq, bn_vec(g, {x}), (hipStream_t)stream);
+    dopt::launch_bn_reduce(x, x_dtype, g, workspace, sum, sumsq, bn_width(g, {{x, bn_bytes(x_dtype)}}),
+                           (hipStream_t)stream);
     return hip_status("bn_reduce launch");
 }
 
@@ -441,7 +457,8 @@ int dopt_bn_norm_quant(const void* x, int x_dtype, int64_t N, int64_t C, int64_t
     a.mean_out = mean_out;
     a.var_out = var_out;
     (void)hipGetLastError();
-    dopt::launch_bn_fwd(a, x_dtype, mode, group_size, bits, bn_vec(g, {x, y, x_hat}), (hipStream_t)stream);
+    dopt::launch_bn_fwd(a, x_dtype, mode, group_size, bits,
+                        bn_width(g, {{x, bn_bytes(x_dtype)}, {y, 2}, {x_hat, 2}}), (hipStream_t)stream);
     return hip_status("bn_norm_quant launch");
 }
 
@@ -472,7 +489,8 @@ int dopt_bn_bwd_reduce(int mode, const void* x_hat, const uint32_t* packed, cons
     a.db = dbias;
     (void)hipGetLastError();
     dopt::launch_bn_bwd_reduce(a, dy_dtype, mode, group_size, bits,
-                               bn_vec(g, {dy, mode == DOPT_BN_NORM ? x_hat : nullptr}), (hipStream_t)stream);
+                               bn_width(g, {{dy, bn_bytes(dy_dtype)}, {mode == DOPT_BN_NORM ? x_hat : nullptr, 2}}),
+                               (hipStream_t)stream);
     return hip_status("bn_bwd_reduce launch");
 }
 
@@ -507,7 +525,8 @@ int dopt_bn_bwd_dx(int mode, const void* x_hat, const uint32_t* packed, const ui
     a.dx = (uint16_t*)dx;
     (void)hipGetLastError();
     dopt::launch_bn_bwd_dx(a, dy_dtype, mode, group_size, bits,
-                           bn_vec(g, {dy, dx, mode == DOPT_BN_NORM ? x_hat : nullptr}), (hipStream_t)stream);
+                           bn_width(g, {{dy, bn_bytes(dy_dtype)}, {dx, 2}, {mode == DOPT_BN_NORM ? x_hat : nullptr, 2}}),
+                           (hipStream_t)stream);
     return hip_status("bn_bwd_dx launch");
 }
 

@@ -145,26 +145,26 @@ class _DOLinear(Function):
         (bits, pack_only, group_size, act_padding, _, _, _, _, _, reshape_elig, _, avg_alam, _, _) = q_meta
         ctx.fused_unpack = (bool(m.get("dw_fused_unpack", False)) and not (pack_only or act_padding or reshape_elig
                                                                              or avg_alam) and input_l is None)
-        ctx.save_for_backward(weight, q_tensor[0], q_tensor[1], q_tensor[2], input_l)
+        # the backward's input gradient uses the weight in the autocast dtype: keep the forward's cast
+        ctx.w_dtype = weight.dtype
+        ctx.save_for_backward(weight_compute, q_tensor[0], q_tensor[1], q_tensor[2], input_l)
         return F.linear(input, weight_compute, bias_compute)
 
     @staticmethod
     @custom_bwd(device_type="cuda")
     def backward(ctx, dy):
         input_shape, _, _, has_bias = ctx.meta
-        weight, q0, q1, q2, input_l = ctx.saved_tensors
+        weight_compute, q0, q1, q2, input_l = ctx.saved_tensors  # the forward's (autocast-dtype) weight
         dt = _compute_dtype()
         if dt is not None:
-            weight_compute = weight.to(dt)
+            weight_compute = weight_compute.to(dt)
             dy = dy.to(dt)
-        else:
-            weight_compute = weight
         C_in, C_out = input_shape[-1], dy.shape[-1]
         dy_flat = dy.reshape(-1, C_out)
         if dy.dtype == torch.bfloat16 and dw_gemm_supported(C_out, C_in):
             # weight (and bias) gradient on the gfx950 split-K GEMM for K-outer operands, in the
             # weight's precision; x_hat is either dequantized first or decoded inside the GEMM
-            out_dtype = weight.dtype if weight.dtype in (torch.float32, torch.bfloat16) else torch.float32
+            out_dtype = ctx.w_dtype if ctx.w_dtype in (torch.float32, torch.bfloat16) else torch.float32
             if ctx.fused_unpack and q1.dtype == torch.bfloat16:
                 bits, group_size = ctx.q_inputs_meta[0], ctx.q_inputs_meta[2]
                 dw, db = torch.ops.act_lib.dw_gemm(dy_flat, None, q0, q1, q2, C_in, bits, group_size, has_bias,
