@@ -9,8 +9,9 @@ Bar:
     ReLU mask, codes, scale, min, dx), except the squashed mode's codes, which go through tanh
     (libdevice in the reference, ocml here, the C library in the oracle): within one code on under
     1% of the elements, scale and min within one bf16 ulp.
-Shapes cover the 16-byte path (HW a multiple of 8) and the element path (HW = 49, 196), group
-sizes 32..512 (BLOCK_M 64..1024), bits 1/2/4/8, bf16 / fp32 / fp16 inputs, and the sync path.
+Shapes cover every access width of the kernels (8 elements per access at HW = 256, 784; 4 at
+HW = 196; 2 at HW = 50; 1 at HW = 49 and for a misaligned input view), group sizes 32..512
+(BLOCK_M 64..1024), bits 1/2/4/8, bf16 / fp32 / fp16 inputs, and the sync path.
 """
 import numpy as np
 import pytest
@@ -71,7 +72,7 @@ def check_stats(x, s, q):
     assert sums_close(npv(q), rq, mag2)
 
 
-SHAPES = [(4, 16, 16, 16), (8, 32, 14, 14), (16, 8, 7, 7), (32, 16, 28, 28)]
+SHAPES = [(4, 16, 16, 16), (8, 32, 14, 14), (16, 8, 7, 7), (32, 16, 28, 28), (8, 16, 5, 10)]
 DTYPES = [torch.bfloat16, torch.float32, torch.float16]
 
 
@@ -96,7 +97,7 @@ def test_reduce_and_plain_normalize(shape, dtype):
 
 # (shape, BLOCK_M): M = N*HW is a multiple of the group BLOCK_M // 2
 QCASES = [((4, 16, 16, 16), 64), ((4, 16, 16, 16), 1024), ((8, 32, 14, 14), 64), ((16, 32, 14, 14), 128),
-          ((32, 16, 28, 28), 512), ((32, 8, 7, 7), 64)]
+          ((32, 16, 28, 28), 512), ((32, 8, 7, 7), 64), ((32, 8, 5, 10), 64)]
 
 
 @pytest.mark.parametrize("case", QCASES, ids=lambda c: "x".join(map(str, c[0])) + f"-B{c[1]}")
@@ -287,3 +288,46 @@ def test_do_batchnorm_relu_layer():
     assert cos > 0.9, float(cos)
     # dbias = sum(dy * mask) exactly as autograd's (the mask is y > 0 on the same fp32 y)
     torch.testing.assert_close(layer.bias.grad, ref.bias.grad, rtol=1e-3, atol=1e-2)
+
+
+@pytest.mark.parametrize("mode", ["squash", "relu"])
+def test_misaligned_input_view_matches_aligned(mode):
+    """An input view one element past an aligned base (HW = 784 would take 16-byte accesses) runs
+    the element-wise access path: outputs equal the aligned run's bit for bit, forward and
+    backward."""
+    shape, BLOCK, bits = (8, 16, 28, 28), 256, 2
+    N, C = shape[0], shape[1]
+    HW = shape[2] * shape[3]
+    x, w, b = make(shape, torch.bfloat16, 21)
+    g = dict(M=N * HW, HW=HW, stride_n=C * HW, stride_c=HW)
+    base = torch.zeros(x.numel() + 1, dtype=torch.bfloat16, device=DEV)
+    base[1:].copy_(x.reshape(-1).to(DEV))
+    outs = []
+    for xd in (x.to(DEV).view(N, C, HW), base[1:].view(N, C, HW)):
+        assert xd.data_ptr() % 16 == (2 if xd.storage_offset() else 0)
+        s, q = ops.bn_fwd_reduce(xd, **g, BLOCK_M=BLOCK, num_warps=8, num_stages=5)
+        if mode == "squash":
+            y, packed, scale, mn, mean, var = ops.bn_fwd_norm_quant_pack_fused(
+                xd, s, q, w.to(DEV), b.to(DEV), None, None, **g, BLOCK_M=BLOCK, bits=bits, sync=False, avg_alam=False,
+                alam_bits=0, num_warps=8, num_stages=5)
+            rp = None
+        else:
+            y, packed, rp, scale, mn, mean, var = ops.bn_relu_fwd_norm_fused_quant_pack(
+                xd, s, q, w.to(DEV), b.to(DEV), None, None, **g, relu=True, relu6=False, BLOCK_SIZE=BLOCK, BITS=bits,
+                sync=False)
+        dyf = torch.zeros(x.numel() + 1, dtype=torch.bfloat16, device=DEV)
+        dyf[1:].copy_(torch.randn(x.numel(), generator=torch.Generator().manual_seed(5)).to(torch.bfloat16).to(DEV))
+        dy = dyf[1:].view(N, C, HW) if xd.storage_offset() else dyf[1:].clone().view(N, C, HW)
+        if mode == "squash":
+            dw, db = ops.bn_bwd_reduce_dequant_unpack_fused(packed, dy, scale, mn, **g, BLOCK_M=BLOCK, bits=bits,
+                                                            avg_alam=False, alam_bits=0)
+            dx = ops.bn_bwd_dx_dequant_unpack_fused(packed, dy, scale, mn, dw, db, w.to(DEV), var, **g, BLOCK_M=BLOCK,
+                                                    bits=bits, sync=False, avg_alam=False, alam_bits=0)
+        else:
+            dw, db = ops.bn_relu_bwd_reduce_fused_dequant_unpack(packed, rp, dy, scale, mn, **g, BLOCK_SIZE=BLOCK,
+                                                                 BITS=bits)
+            dx = ops.bn_relu_bwd_dx_fused_dequant_unpack(packed, rp, dy, dw, db, w.to(DEV), var, scale, mn, **g,
+                                                         BLOCK_SIZE=BLOCK, BITS=bits)
+        outs.append([t for t in (s, q, y, packed, rp, scale, mn, mean, var, dw, db, dx) if t is not None])
+    for a, b_ in zip(*outs):
+        assert torch.equal(a.cpu(), b_.cpu())
