@@ -64,8 +64,13 @@ def rounding_code(rounding) -> int:
 
 
 def _stream(t: Tensor) -> int:
-    """Raw hipStream_t of torch's current stream on t's device (what the C ABI enqueues on)."""
-    return torch._C._cuda_getCurrentRawStream(t.get_device())
+    """Raw hipStream_t of torch's current stream on t's device (what the C ABI enqueues on). The
+    C ABI launches on the calling thread's current device, so t must live there."""
+    dev = t.get_device()
+    if dev != torch.cuda.current_device():
+        raise RuntimeError(f"act_lib operators launch on the current device ({torch.cuda.current_device()}); "
+                           f"the tensors are on cuda:{dev}: call under torch.cuda.device({dev})")
+    return torch._C._cuda_getCurrentRawStream(dev)
 
 
 def _require_cuda(*ts: Tensor) -> None:
@@ -264,8 +269,8 @@ def _quant_pack_triton(x, bits, group_size, avg_alam, alam_bits, clamp, clamp_al
     """Reference semantics (act_triton_kernel.py:336-368): [clamp], tanh squash, nearest
     rounding, bf16 scale and min."""
     _no_alam(avg_alam, "quant_pack_triton")
-    if x.dim() != 3:
-        raise RuntimeError(f"quant_pack_triton expects x of shape [N, G, g], got {tuple(x.shape)}")
+    if x.dim() != 3 or x.shape[-1] != group_size:  # the reference's x.view(N * G, group_size)
+        raise RuntimeError(f"quant_pack_triton expects x of shape [N, G, {group_size}], got {tuple(x.shape)}")
     N, G, _ = x.shape
     packed, scale, xmin = _quant_pack_launch(x, N * G, bits, group_size, None, clamp, clamp_alpha,
                                              True, ROUND_NEAREST, None, 0, 0, torch.bfloat16)
@@ -320,11 +325,14 @@ pack_triton = _op(
 
 def _unpack_triton(packed, bits, N, G, group_size):
     """int32 words [N*G, W] -> int8 codes [N, G, g] (act_triton_kernel.py:419-433)."""
-    _bits_consts(bits, group_size)
+    _, nwords, _ = _bits_consts(bits, group_size)
     _require_cuda(packed)
     NG = packed.shape[0]
     if NG != N * G:
         raise RuntimeError(f"unpack_triton: packed has {NG} groups, expected N*G = {N * G}")
+    if packed.numel() * packed.element_size() != NG * nwords * 4:
+        raise RuntimeError(f"unpack_triton: packed holds {packed.numel() * packed.element_size()} bytes, expected "
+                           f"{NG * nwords * 4} ({NG} groups of {nwords} words)")
     packed = _aligned(packed)
     out = torch.empty((NG, group_size), dtype=torch.int8, device=packed.device)
     rc = _lib.lib().dopt_unpack_codes(packed.data_ptr(), NG, group_size, bits, out.data_ptr(), _stream(packed))
@@ -484,8 +492,8 @@ def _act_quant_pack_launch(x, act, n_groups, bits, group_size, tile):
     x = _aligned(x)
     y = torch.empty(x.shape, dtype=torch.bfloat16, device=x.device)
     packed = torch.empty((n_groups, nwords), dtype=torch.int32, device=x.device)
-    scale = torch.zeros((n_groups,), dtype=torch.bfloat16, device=x.device)
-    xmin = torch.zeros((n_groups,), dtype=torch.bfloat16, device=x.device)
+    scale = torch.empty((n_groups,), dtype=torch.bfloat16, device=x.device)  # every group's written
+    xmin = torch.empty((n_groups,), dtype=torch.bfloat16, device=x.device)
     tile_arr = None
     if tile is not None:
         import ctypes

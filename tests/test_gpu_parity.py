@@ -206,6 +206,32 @@ def test_avg_alam_is_rejected():
         torch.ops.act_lib.quant_pack_triton(x, 2, 256, True, 2, False, 0.0)
 
 
+def test_mismatched_sizes_are_rejected_before_launch():
+    """Inputs whose sizes disagree with the group geometry raise instead of reaching a kernel that
+    would read past them: a last dim other than group_size (the reference's x.view(N*G, g)
+    raises), packed words short of N*G groups' worth."""
+    x = torch.randn((2, 4, 128), device=DEV).to(torch.bfloat16)
+    with pytest.raises(RuntimeError):
+        torch.ops.act_lib.quant_pack_triton(x, 2, 256, False, 0, True, 3.0)
+    with pytest.raises(RuntimeError):
+        torch.ops.act_lib.quant_pack(x, 2, 256, False, 0.0, False, 0, None, 0, 0, torch.float32)
+    packed = torch.zeros((8, 4), dtype=torch.int32, device=DEV)  # 2-bit g=256 needs 16 words per group
+    with pytest.raises(RuntimeError):
+        torch.ops.act_lib.unpack_triton(packed, 2, 2, 4, 256)
+    with pytest.raises(RuntimeError):
+        torch.ops.act_lib.dequant_unpack_triton(packed, torch.ones((2, 4), dtype=torch.bfloat16, device=DEV),
+                                                torch.zeros((2, 4), dtype=torch.bfloat16, device=DEV), 2, 256, False, 0)
+
+
+def test_tensors_off_the_current_device_are_rejected(monkeypatch):
+    """The C ABI launches on the current device; a tensor elsewhere raises (simulated by making
+    the current-device query answer another index)."""
+    x = torch.randn((2, 4, 256), device=DEV).to(torch.bfloat16)
+    monkeypatch.setattr(torch.cuda, "current_device", lambda: x.get_device() + 1)
+    with pytest.raises(RuntimeError, match="current device"):
+        torch.ops.act_lib.quant_pack(x, 2, 256, False, 0.0, False, 0, None, 0, 0, torch.float32)
+
+
 def test_bad_bits_raise_value_error_on_device():
     x = torch.zeros(1, 1, 256, dtype=torch.bfloat16, device=DEV)
     with pytest.raises(ValueError):
