@@ -104,6 +104,11 @@ def _norm_launch(X, SUM, SUM_SQUARE, GAMMA, BETA, mean, var, M, HW, sync, mode, 
         xmin = torch.empty_like(scale)
         if mode in (_lib.BN_RELU_QUANT, _lib.BN_RELU6_QUANT):
             relu_packed = torch.empty((C, M // 32), dtype=torch.int32, device=dev)
+    used = (("weight", GAMMA), ("bias", BETA)) + ((("mean", mean), ("var", var)) if sync else
+                                                   (("sum", SUM), ("sum of squares", SUM_SQUARE)))
+    for name, t in used:
+        if t is not None and t.numel() != C:  # the kernels read one value per channel
+            raise RuntimeError(f"BatchNorm forward: {name} must hold {C} values (one per channel), got {t.numel()}")
     w, b = _f32(GAMMA), _f32(BETA)
     if sync:
         if mean is None or var is None:

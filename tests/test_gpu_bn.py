@@ -331,3 +331,18 @@ def test_misaligned_input_view_matches_aligned(mode):
         outs.append([t for t in (s, q, y, packed, rp, scale, mn, mean, var, dw, db, dx) if t is not None])
     for a, b_ in zip(*outs):
         assert torch.equal(a.cpu(), b_.cpu())
+
+
+def test_forward_rejects_short_per_channel_vectors():
+    """weight / bias / sums with fewer values than channels raise before a kernel reads past them."""
+    shape = (4, 16, 16, 16)
+    x, w, b = make(shape, torch.bfloat16, 3)
+    g = geo(x)
+    xd = x.to(DEV).view(shape[0], shape[1], -1)
+    s, q = ops.bn_fwd_reduce(xd, **g, BLOCK_M=256, num_warps=8, num_stages=5)
+    with pytest.raises(RuntimeError, match="one per channel"):
+        ops.bn_fwd_norm_quant_pack_fused(xd, s, q, w[:8].to(DEV), b.to(DEV), None, None, **g, BLOCK_M=256, bits=2,
+                                         sync=False, avg_alam=False, alam_bits=0, num_warps=8, num_stages=5)
+    with pytest.raises(RuntimeError, match="one per channel"):
+        ops.bn_fwd_norm(xd, s[:8], q, w.to(DEV), b.to(DEV), None, None, **g, BLOCK_M=256, sync=False, num_warps=8,
+                        num_stages=5)
