@@ -360,8 +360,114 @@ bn_relu_bwd_dx_fused_dequant_unpack = _op(
     BLOCK_SIZE, BITS: DY.new_empty((DY.shape[0], DY.shape[1], HW), dtype=torch.bfloat16))
 
 
+# ------------------------------------------------------------------ layer operators
+# Not in the reference: the compressed BatchNorm layers' training forward and backward, each one
+# operator call. The reference's layers issue two operators per pass and update the running
+# statistics with four tensor ops (normalization_ops.py:45-57 and :95-157, fused_ops.py:19-86);
+# these run the same kernels, the running statistics updated inside the normalize kernel.
+_LAYER_EPS = {_lib.BN_QUANT: (EPS_FUSED, EPS_PLAIN), _lib.BN_RELU_QUANT: (EPS_FUSED, EPS_FUSED),
+              _lib.BN_RELU6_QUANT: (EPS_FUSED, EPS_FUSED)}  # (forward, backward) as the operators above
+
+
+def _layer_mode(kind: int) -> int:
+    """The kernels' mode for a layer kind (BN_QUANT, BN_RELU_QUANT or BN_RELU6_QUANT; the ReLU6 backward
+    is the ReLU one, its mask already marks 0 < y < 6)."""
+    if kind not in _LAYER_EPS:
+        raise RuntimeError(f"BatchNorm layer operators take kind BN_QUANT, BN_RELU_QUANT or BN_RELU6_QUANT, got {kind}")
+    return _lib.BN_RELU_QUANT if kind == _lib.BN_RELU6_QUANT else kind
+
+
+def _bn_train_fwd(X, weight, bias, running_mean, running_var, momentum, BLOCK_M, bits, kind):
+    """X [N, C, ...] -> (y bf16 [N, C, HW], packed [C, M*bits/32], ReLU mask [C, M/32] ([C, 0] without ReLU), scale, min
+    bf16 [C, M/g], batch mean, biased batch variance); the running statistics are updated in place:
+    run = run * (1 - momentum) + momentum * statistic (an empty tensor stands for no statistic)."""
+    _layer_mode(kind)
+    running_mean = running_mean if running_mean is not None and running_mean.numel() else None
+    running_var = running_var if running_var is not None and running_var.numel() else None
+    g = _group(BLOCK_M)
+    _bits_consts(bits, g)
+    _require_cuda(X, weight, bias, running_mean, running_var)
+    if X.dim() < 2 or X.dtype not in _DTYPE_CODE:
+        raise RuntimeError(f"bn_train_fwd: X must be an [N, C, ...] float tensor, got {tuple(X.shape)} {X.dtype}")
+    N, C = int(X.shape[0]), int(X.shape[1])
+    HW = X.numel() // (N * C) if N * C else 0
+    X3 = X.contiguous().view(N, C, HW)
+    M, dev = N * HW, X.device
+    for name, t in (("weight", weight), ("bias", bias), ("running_mean", running_mean), ("running_var", running_var)):
+        if t is not None and t.numel() != C:
+            raise RuntimeError(f"bn_train_fwd: {name} must hold {C} values (one per channel), got {t.numel()}")
+    in_kernel = all(t is None or (t.dtype == torch.float32 and t.is_contiguous()) for t in (running_mean, running_var))
+    y = torch.empty((N, C, HW), dtype=torch.bfloat16, device=dev)
+    packed = torch.empty((C, M * bits // 32), dtype=torch.int32, device=dev)
+    scale = torch.empty((C, M // g), dtype=torch.bfloat16, device=dev)
+    xmin = torch.empty_like(scale)
+    rp = torch.empty((C, M // 32 if kind != _lib.BN_QUANT else 0), dtype=torch.int32, device=dev)
+    sums = torch.empty((2, C), dtype=torch.float32, device=dev)  # sum, sum of squares
+    mean = torch.empty(C, dtype=torch.float32, device=dev)
+    var = torch.empty_like(mean)
+    ws = _workspace(X3, N, C, HW)
+    w, b = _f32(weight), _f32(bias)
+    rm, rv = (running_mean, running_var) if in_kernel else (None, None)
+    rc = _lib.lib().dopt_bn_train_forward(
+        X3.data_ptr(), _DTYPE_CODE[X3.dtype], N, C, HW, C * HW, HW, ws.data_ptr(), sums[0].data_ptr(),
+        sums[1].data_ptr(), w.data_ptr(), b.data_ptr(), _LAYER_EPS[kind][0], kind, g, bits, y.data_ptr(), None,
+        packed.data_ptr(), rp.data_ptr() if rp.numel() else None, scale.data_ptr(), xmin.data_ptr(), mean.data_ptr(),
+        var.data_ptr(),
+        _ptr(rm), _ptr(rv), float(momentum), _stream(X))
+    _lib.check(rc, "bn_train_fwd")
+    if not in_kernel:
+        for run, stat in ((running_mean, mean), (running_var, var)):
+            if run is not None:
+                run.mul_(1.0 - momentum).add_(stat, alpha=momentum)
+    return y, packed, rp, scale, xmin, mean, var
+
+
+def _bn_train_fwd_fake(X, weight, bias, running_mean, running_var, momentum, BLOCK_M, bits, kind):
+    N, C = X.shape[0], X.shape[1]
+    HW = X.numel() // (N * C) if N * C else 0
+    M, g = N * HW, BLOCK_M // 2
+    rp = X.new_empty((C, M // 32 if kind != _lib.BN_QUANT else 0), dtype=torch.int32)
+    scale = X.new_empty((C, M // g), dtype=torch.bfloat16)
+    return (X.new_empty((N, C, HW), dtype=torch.bfloat16), X.new_empty((C, M * bits // 32), dtype=torch.int32), rp,
+            scale, torch.empty_like(scale), X.new_empty((C,), dtype=torch.float32),
+            X.new_empty((C,), dtype=torch.float32))
+
+
+bn_train_fwd = _op(
+    "bn_train_fwd(Tensor X, Tensor weight, Tensor bias, Tensor(a!) running_mean, Tensor(b!) running_var, "
+    "float momentum, int BLOCK_M, int bits, int kind) -> (Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor)",
+    _bn_train_fwd, _bn_train_fwd_fake)
+
+
+def _bn_train_bwd(packed, relu_packed, dy, scale, min, weight, var, BLOCK_M, bits, kind):
+    """dy [N, C, ...] -> (bf16 dx [N, C, HW], dweight, dbias) of the layer whose forward was bn_train_fwd."""
+    m = _layer_mode(kind)
+    g = _group(BLOCK_M)
+    _bits_consts(bits, g)
+    if dy.dim() < 2:
+        raise RuntimeError(f"bn_train_bwd: dy must be [N, C, ...], got {tuple(dy.shape)}")
+    N, C = int(dy.shape[0]), int(dy.shape[1])
+    HW = dy.numel() // (N * C) if N * C else 0
+    kw = dict(packed=packed, relu_packed=relu_packed if m == _lib.BN_RELU_QUANT else None, scale=scale, xmin=min)
+    dw, db = _bwd_reduce(m, dy, N * HW, HW, g, bits, **kw)
+    dx = _bwd_dx(m, dy, N * HW, HW, g, bits, dw, db, weight, var, _LAYER_EPS[kind][1], False, **kw)
+    return dx, dw, db
+
+
+def _bn_train_bwd_fake(packed, relu_packed, dy, scale, min, weight, var, BLOCK_M, bits, kind):
+    N, C = dy.shape[0], dy.shape[1]
+    HW = dy.numel() // (N * C) if N * C else 0
+    return (dy.new_empty((N, C, HW), dtype=torch.bfloat16), dy.new_empty((C,), dtype=torch.float32),
+            dy.new_empty((C,), dtype=torch.float32))
+
+
+bn_train_bwd = _op(
+    "bn_train_bwd(Tensor packed, Tensor? relu_packed, Tensor dy, Tensor scale, Tensor min, Tensor weight, Tensor var, "
+    "int BLOCK_M, int bits, int kind) -> (Tensor, Tensor, Tensor)", _bn_train_bwd, _bn_train_bwd_fake)
+
+
 __all__ = [
-    "bn_fwd_reduce", "bn_fwd_norm", "bn_fwd_norm_quant_pack_fused", "bn_relu_fwd_norm_fused_quant_pack",
+    "bn_train_fwd", "bn_train_bwd", "bn_fwd_reduce", "bn_fwd_norm", "bn_fwd_norm_quant_pack_fused", "bn_relu_fwd_norm_fused_quant_pack",
     "bn_bwd_reduce", "bn_bwd_dx", "bn_bwd_reduce_dequant_unpack_fused", "bn_bwd_dx_dequant_unpack_fused",
     "bn_relu_bwd_reduce_fused_dequant_unpack", "bn_relu_bwd_dx_fused_dequant_unpack",
 ]

@@ -44,6 +44,9 @@ struct BnFwdArgs {
     uint16_t* minv;
     float* mean_out;         // written when sync == 0
     float* var_out;
+    float* run_mean;         // when set (sync == 0): run = run * run_keep + run_mom * batch statistic
+    float* run_var;
+    float run_keep, run_mom;
 };
 
 struct BnBwdArgs {

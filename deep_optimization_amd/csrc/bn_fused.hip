@@ -329,6 +329,10 @@ __device__ __forceinline__ void channel_stats(const BnFwdArgs& a, int64_t c, int
     if (blockIdx.x == 0 && threadIdx.x == 0) {
         a.mean_out[c] = mean;
         a.var_out[c] = var;
+        // the running statistics (biased variance, as the reference's layer updates them with
+        // mul_(1 - momentum).add_(stat, alpha=momentum), normalization_ops.py:56-57)
+        if (a.run_mean) a.run_mean[c] = fmaf(a.run_mom, mean, a.run_mean[c] * a.run_keep);
+        if (a.run_var) a.run_var[c] = fmaf(a.run_mom, var, a.run_var[c] * a.run_keep);
     }
 }
 

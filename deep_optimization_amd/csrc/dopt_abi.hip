@@ -462,6 +462,47 @@ int dopt_bn_norm_quant(const void* x, int x_dtype, int64_t N, int64_t C, int64_t
     return hip_status("bn_norm_quant launch");
 }
 
+int dopt_bn_train_forward(const void* x, int x_dtype, int64_t N, int64_t C, int64_t HW, int64_t stride_n,
+                          int64_t stride_c, float* workspace, float* sum, float* sumsq, const float* weight,
+                          const float* bias, float eps, int mode, int group_size, int bits, void* y, void* x_hat,
+                          uint32_t* packed, uint32_t* relu_packed, void* scale, void* minv, float* mean_out,
+                          float* var_out, float* running_mean, float* running_var, float momentum, void* stream) {
+    int rc;
+    if ((rc = dopt_bn_reduce(x, x_dtype, N, C, HW, stride_n, stride_c, workspace, sum, sumsq, stream))) return rc;
+    dopt::BnGeom g;
+    if ((rc = bn_geom(N, C, HW, stride_n, stride_c, &g))) return rc;
+    const int64_t M = N * HW;
+    if ((rc = bn_quant_checks(mode, M, group_size, bits, packed, scale, minv, relu_packed))) return rc;
+    if (C == 0 || M == 0) return ok();
+    if (!x || !y || !weight || !bias || !mean_out || !var_out) return fail(DOPT_EINVAL, "null pointer argument");
+    if (mode == DOPT_BN_NORM && !x_hat) return fail(DOPT_EINVAL, "null x_hat pointer");
+    dopt::BnFwdArgs a{};
+    a.g = g;
+    a.x = x;
+    a.sum = sum;
+    a.sumsq = sumsq;
+    a.w = weight;
+    a.b = bias;
+    a.eps = eps;
+    a.sync = 0;
+    a.y = (uint16_t*)y;
+    a.xhat = (uint16_t*)x_hat;
+    a.packed = packed;
+    a.relu_packed = relu_packed;
+    a.scale = (uint16_t*)scale;
+    a.minv = (uint16_t*)minv;
+    a.mean_out = mean_out;
+    a.var_out = var_out;
+    a.run_mean = running_mean;
+    a.run_var = running_var;
+    a.run_mom = momentum;
+    a.run_keep = (float)(1.0 - (double)momentum);
+    (void)hipGetLastError();
+    dopt::launch_bn_fwd(a, x_dtype, mode, group_size, bits,
+                        bn_width(g, {{x, bn_bytes(x_dtype)}, {y, 2}, {x_hat, 2}}), (hipStream_t)stream);
+    return hip_status("bn_train_forward launch");
+}
+
 int dopt_bn_bwd_reduce(int mode, const void* x_hat, const uint32_t* packed, const uint32_t* relu_packed,
                        const void* scale, const void* minv, const void* dy, int dy_dtype, int64_t N, int64_t C,
                        int64_t HW, int64_t stride_n, int64_t stride_c, int group_size, int bits, float* workspace,

@@ -23,9 +23,9 @@ from torch import nn
 from torch.amp import custom_bwd, custom_fwd
 from torch.autograd import Function
 
-from . import bn_lib  # noqa: F401  (registers the BatchNorm act_lib operators)
+from . import _lib, bn_lib  # noqa: F401  (bn_lib registers the BatchNorm act_lib operators)
 from .modules.activations import DOReLU_Variance
-from .modules.normalization import DOBatchNorm2d, _ema_factor, _update_running
+from .modules.normalization import DOBatchNorm2d, _ema_factor, _stat
 
 
 class _DOBatchNormReLU2d(Function):
@@ -41,29 +41,27 @@ class _DOBatchNormReLU2d(Function):
         N, C, H, W = x.shape
         HW = H * W
         x3 = x.contiguous().view(N, C, HW)
-        geo = dict(M=N * HW, HW=HW, stride_n=C * HW, stride_c=HW)
-        s, q = torch.ops.act_lib.bn_fwd_reduce(x3, **geo, BLOCK_M=BLOCK, num_warps=8, num_stages=5)
-        y, packed, relu_packed, scale, xmin, mean, var = torch.ops.act_lib.bn_relu_fwd_norm_fused_quant_pack(
-            x3, s, q, weight, bias, None, None, **geo, relu=relu, relu6=relu6, BLOCK_SIZE=BLOCK, BITS=BITS,
-            sync=False)
-        _update_running(running_mean, running_var, mean, var, exponential_average_factor)
-        ctx.other_meta = BLOCK, BITS
+        if not (relu or relu6):
+            raise RuntimeError("DOBatchNormReLU2d needs relu or relu6")
+        mode = _lib.BN_RELU_QUANT if relu else _lib.BN_RELU6_QUANT
+        # statistics, normalize + ReLU + quant-pack and the running-statistics update in one
+        # operator call (the reference's bn_fwd_reduce + bn_relu_fwd_norm_fused_quant_pack + update)
+        y, packed, relu_packed, scale, xmin, mean, var = torch.ops.act_lib.bn_train_fwd(
+            x3, weight, bias, _stat(running_mean, x3), _stat(running_var, x3), exponential_average_factor, BLOCK,
+            BITS, mode)
+        ctx.other_meta = BLOCK, BITS, mode
         ctx.save_for_backward(weight, packed, relu_packed, var, scale, xmin)
         return y.view(N, C, H, W)
 
     @staticmethod
     @custom_bwd(device_type="cuda")
     def backward(ctx, dy):
-        BLOCK, BITS = ctx.other_meta
+        BLOCK, BITS, mode = ctx.other_meta
         weight, packed, relu_packed, var, scale, xmin = ctx.saved_tensors
         N, C, H, W = dy.shape
-        HW = H * W
-        dy3 = dy.contiguous().view(N, C, HW)
-        geo = dict(M=N * HW, HW=HW, stride_n=C * HW, stride_c=HW)
-        DW, DB = torch.ops.act_lib.bn_relu_bwd_reduce_fused_dequant_unpack(packed, relu_packed, dy3, scale, xmin,
-                                                                          **geo, BLOCK_SIZE=BLOCK, BITS=BITS)
-        DX = torch.ops.act_lib.bn_relu_bwd_dx_fused_dequant_unpack(packed, relu_packed, dy3, DW, DB, weight, var,
-                                                                  scale, xmin, **geo, BLOCK_SIZE=BLOCK, BITS=BITS)
+        dy3 = dy.contiguous().view(N, C, H * W)
+        DX, DW, DB = torch.ops.act_lib.bn_train_bwd(packed, relu_packed, dy3, scale, xmin, weight, var, BLOCK, BITS,
+                                                    mode)
         return DX.view(N, C, H, W), DW, DB, None, None, None, None, None, None, None, None
 
 

@@ -6,9 +6,11 @@ Mirrors Activation_Compression/modules/normalization/normalization_ops.py (``_DO
 :8-157; ``_DOSyncBatchNorm``, :160-340) and normalization_layers.py (``DOBatchNorm2d``,
 ``DOSyncBatchNorm2d``): same ``apply`` arguments, the same per-layer ``meta`` keys (group_size =
 BLOCK_M, bits, act_padding, AVG_ALAM, ALAM_BITS) and the same two paths:
-  * act_padding False: act_lib::bn_fwd_norm_quant_pack_fused saves 2 tanh(clamp(x_hat)/2) codes
-    (groups of group_size // 2 per channel), and the backward runs
-    bn_bwd_reduce_dequant_unpack_fused + bn_bwd_dx_dequant_unpack_fused on them;
+  * act_padding False: the forward saves 2 tanh(clamp(x_hat)/2) codes (groups of group_size // 2
+    per channel) and the backward restores them inside its reduction and input-gradient kernels;
+    each pass is one operator call (act_lib::bn_train_fwd / bn_train_bwd: the kernels of the
+    reference's bn_fwd_reduce + bn_fwd_norm_quant_pack_fused and bn_bwd_reduce_dequant_unpack_fused
+    + bn_bwd_dx_dequant_unpack_fused, with the running statistics updated in the normalize kernel);
   * act_padding True: act_lib::bn_fwd_norm, then the generic quantizer on x_hat; the backward
     dequantizes and runs bn_bwd_reduce + bn_bwd_dx.
 As in the reference, the running variance is updated with the biased batch variance, the
@@ -27,10 +29,16 @@ from torch import nn
 from torch.amp import custom_bwd, custom_fwd
 from torch.autograd import Function
 
-from .. import bn_lib  # noqa: F401  (registers the BatchNorm act_lib operators)
+from .. import _lib, bn_lib  # noqa: F401  (bn_lib registers the BatchNorm act_lib operators)
+from ..act_lib import _no_alam
 from .module_utils import unified_dequantize, unified_quantize
 
 _NW, _NS = 8, 5  # launch-tuning arguments of the reference's operators (ignored by the kernels)
+
+
+def _stat(t, like):
+    """A running-statistics buffer for act_lib::bn_train_fwd (an empty tensor when the module keeps none)."""
+    return t if t is not None else like.new_empty((0,), dtype=torch.float32)
 
 
 def _update_running(running_mean, running_var, mean, var, momentum):
@@ -59,8 +67,8 @@ class _DOBatchNorm(Function):
         x3 = input.contiguous().view(N, C, HW)
         M = N * HW
         geo = dict(M=M, HW=HW, stride_n=C * HW, stride_c=HW)
-        sum_, sumsq_ = torch.ops.act_lib.bn_fwd_reduce(x3, **geo, BLOCK_M=BLOCK_M, num_warps=_NW, num_stages=_NS)
         if m["act_padding"]:
+            sum_, sumsq_ = torch.ops.act_lib.bn_fwd_reduce(x3, **geo, BLOCK_M=BLOCK_M, num_warps=_NW, num_stages=_NS)
             y3, x_hat, mean, var = torch.ops.act_lib.bn_fwd_norm(x3, sum_, sumsq_, weight, bias, None, None, **geo,
                                                                  BLOCK_M=BLOCK_M, sync=False, num_warps=_NW,
                                                                  num_stages=_NS)
@@ -71,10 +79,12 @@ class _DOBatchNorm(Function):
             ctx.meta = (BLOCK_M, meta, target_name, None, None, True)
             return y3.view(N, C, H, W)
         avg_alam, alam_bits = m["AVG_ALAM"], m["ALAM_BITS"]
-        y, packed, scale, xmin, mean, var = torch.ops.act_lib.bn_fwd_norm_quant_pack_fused(
-            x3, sum_, sumsq_, weight, bias, None, None, **geo, BLOCK_M=BLOCK_M, bits=m["bits"], sync=False,
-            avg_alam=avg_alam, alam_bits=alam_bits, num_warps=_NW, num_stages=_NS)
-        _update_running(running_mean, running_var, mean, var, momentum)
+        _no_alam(avg_alam, "DOBatchNorm2d")
+        # statistics, normalize + quant-pack and the running-statistics update in one operator
+        # call (the reference's bn_fwd_reduce + bn_fwd_norm_quant_pack_fused + update)
+        y, packed, _, scale, xmin, mean, var = torch.ops.act_lib.bn_train_fwd(
+            x3, weight, bias, _stat(running_mean, x3), _stat(running_var, x3), momentum, BLOCK_M, m["bits"],
+            _lib.BN_QUANT)
         ctx.save_for_backward(weight, packed, scale, xmin, var)
         ctx.meta = (BLOCK_M, meta, target_name, avg_alam, alam_bits, False)
         return y.view(N, C, H, W)
@@ -98,11 +108,8 @@ class _DOBatchNorm(Function):
         else:
             weight, packed, scale, xmin, var = ctx.saved_tensors
             bits = meta[f"{target_name}"]["bits"]
-            dgamma, dbeta = torch.ops.act_lib.bn_bwd_reduce_dequant_unpack_fused(
-                packed, dy3, scale, xmin, **geo, BLOCK_M=BLOCK_M, bits=bits, avg_alam=avg_alam, alam_bits=alam_bits)
-            dx = torch.ops.act_lib.bn_bwd_dx_dequant_unpack_fused(
-                packed, dy3, scale, xmin, dgamma, dbeta, weight, var, **geo, BLOCK_M=BLOCK_M, bits=bits, sync=False,
-                avg_alam=avg_alam, alam_bits=alam_bits)
+            dx, dgamma, dbeta = torch.ops.act_lib.bn_train_bwd(packed, None, dy3, scale, xmin, weight, var, BLOCK_M,
+                                                              bits, _lib.BN_QUANT)
         return dx.view(N, C, H, W), dgamma, dbeta, None, None, None, None, None, None, None
 
 

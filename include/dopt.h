@@ -227,6 +227,18 @@ int dopt_bn_norm_quant(const void* x, int x_dtype, int64_t N, int64_t C, int64_t
                        int group_size, int bits, void* y, void* x_hat, uint32_t* packed, uint32_t* relu_packed,
                        void* scale, void* minv, float* mean_out, float* var_out, void* stream);
 
+/* The training forward of the compressed BatchNorm layer in one call: dopt_bn_reduce into sum/sumsq,
+ * then dopt_bn_norm_quant (sync = 0), which also updates running_mean / running_var (when not NULL)
+ * with run = fma(momentum, stat, run * (1 - momentum)), stat the batch mean and biased variance.
+ * Replaces the act_lib::bn_fwd_reduce + act_lib::bn_fwd_norm_quant_pack_fused (or
+ * bn_relu_fwd_norm_fused_quant_pack) pair and the running-statistics update of _DOBatchNorm.forward
+ * (AC/modules/normalization/normalization_ops.py:45-57). */
+int dopt_bn_train_forward(const void* x, int x_dtype, int64_t N, int64_t C, int64_t HW, int64_t stride_n,
+                          int64_t stride_c, float* workspace, float* sum, float* sumsq, const float* weight,
+                          const float* bias, float eps, int mode, int group_size, int bits, void* y, void* x_hat,
+                          uint32_t* packed, uint32_t* relu_packed, void* scale, void* minv, float* mean_out,
+                          float* var_out, float* running_mean, float* running_var, float momentum, void* stream);
+
 /* dweight[c] = sum(dy*m * x_hat'), dbias[c] = sum(dy*m), with x_hat' = fma(q, scale, min) (or the bf16
  * x_hat for DOPT_BN_NORM) and m the ReLU mask (ReLU modes) or 1. Replaces act_lib::bn_bwd_reduce
  * (kernel_registration.py:153-178), act_lib::bn_bwd_reduce_dequant_unpack_fused (:211-240) and

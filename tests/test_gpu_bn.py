@@ -346,3 +346,71 @@ def test_forward_rejects_short_per_channel_vectors():
     with pytest.raises(RuntimeError, match="one per channel"):
         ops.bn_fwd_norm(xd, s[:8], q, w.to(DEV), b.to(DEV), None, None, **g, BLOCK_M=256, sync=False, num_warps=8,
                         num_stages=5)
+
+
+@pytest.mark.parametrize("mode", ["squash", "relu", "relu6"])
+@pytest.mark.parametrize("shape,BLOCK", [((8, 16, 28, 28), 256), ((16, 32, 14, 14), 64)],
+                         ids=["8x16x28x28", "16x32x14x14"])
+def test_layer_operators_equal_the_reference_operator_pairs(mode, shape, BLOCK):
+    """act_lib::bn_train_fwd / bn_train_bwd (one call per pass, running statistics updated in the
+    normalize kernel) give bit for bit what the reference's operator pairs give, and the running
+    statistics of the torch update (mul_(1 - m).add_(stat, alpha=m)) within one fp32 rounding."""
+    from deep_optimization_amd import _lib
+    bits, mom = 2, 0.1
+    N, C = shape[0], shape[1]
+    x, w, b = make(shape, torch.bfloat16, 31)
+    g = geo(x)
+    xd = x.to(DEV).view(N, C, -1)
+    wd, bd = w.to(DEV), b.to(DEV)
+    dy = torch.randn(xd.shape, generator=torch.Generator().manual_seed(6)).to(torch.bfloat16).to(DEV)
+    rm0 = torch.randn(C, device=DEV)
+    rv0 = torch.rand(C, device=DEV) + 0.5
+    # the reference operator pairs
+    s, q = ops.bn_fwd_reduce(xd, **g, BLOCK_M=BLOCK, num_warps=8, num_stages=5)
+    if mode == "squash":
+        y, packed, scale, mn, mean, var = ops.bn_fwd_norm_quant_pack_fused(
+            xd, s, q, wd, bd, None, None, **g, BLOCK_M=BLOCK, bits=bits, sync=False, avg_alam=False, alam_bits=0,
+            num_warps=8, num_stages=5)
+        rp = None
+        dw, db = ops.bn_bwd_reduce_dequant_unpack_fused(packed, dy, scale, mn, **g, BLOCK_M=BLOCK, bits=bits,
+                                                        avg_alam=False, alam_bits=0)
+        dx = ops.bn_bwd_dx_dequant_unpack_fused(packed, dy, scale, mn, dw, db, wd, var, **g, BLOCK_M=BLOCK, bits=bits,
+                                                sync=False, avg_alam=False, alam_bits=0)
+        lmode = _lib.BN_QUANT
+    else:
+        relu6 = mode == "relu6"
+        y, packed, rp, scale, mn, mean, var = ops.bn_relu_fwd_norm_fused_quant_pack(
+            xd, s, q, wd, bd, None, None, **g, relu=not relu6, relu6=relu6, BLOCK_SIZE=BLOCK, BITS=bits, sync=False)
+        dw, db = ops.bn_relu_bwd_reduce_fused_dequant_unpack(packed, rp, dy, scale, mn, **g, BLOCK_SIZE=BLOCK, BITS=bits)
+        dx = ops.bn_relu_bwd_dx_fused_dequant_unpack(packed, rp, dy, dw, db, wd, var, scale, mn, **g, BLOCK_SIZE=BLOCK,
+                                                     BITS=bits)
+        lmode = _lib.BN_RELU6_QUANT if relu6 else _lib.BN_RELU_QUANT
+    # the layer operators
+    rm, rv = rm0.clone(), rv0.clone()
+    y2, packed2, rp2, scale2, mn2, mean2, var2 = ops.bn_train_fwd(xd, wd, bd, rm, rv, mom, BLOCK, bits, lmode)
+    dx2, dw2, db2 = ops.bn_train_bwd(packed2, rp2, dy, scale2, mn2, wd, var2, BLOCK, bits, lmode)
+    assert (rp is None) == (rp2.numel() == 0)
+    for a, b_ in ((y, y2), (packed, packed2), (rp, rp2), (scale, scale2), (mn, mn2), (mean, mean2), (var, var2),
+                  (dw, dw2), (db, db2), (dx, dx2)):
+        if a is not None:
+            assert torch.equal(a, b_)
+    ref_m = rm0.clone().mul_(1.0 - mom).add_(mean, alpha=mom)
+    ref_v = rv0.clone().mul_(1.0 - mom).add_(var, alpha=mom)
+    torch.testing.assert_close(rm, ref_m, rtol=2 ** -23, atol=1e-7)
+    torch.testing.assert_close(rv, ref_v, rtol=2 ** -23, atol=1e-7)
+
+
+def test_layer_operator_opcheck():
+    from deep_optimization_amd import _lib
+    shape, BLOCK = (4, 16, 16, 16), 256
+    x, w, b = make(shape, torch.bfloat16, 2)
+    xd = x.to(DEV).view(4, 16, -1)
+    rm, rv = torch.zeros(16, device=DEV), torch.ones(16, device=DEV)
+    tests = ("test_schema", "test_faketensor", "test_aot_dispatch_static", "test_aot_dispatch_dynamic")
+    torch.library.opcheck(ops.bn_train_fwd.default, (xd, w.to(DEV), b.to(DEV), rm, rv, 0.1, BLOCK, 2, _lib.BN_QUANT),
+                          test_utils=tests)
+    y, packed, rp, scale, mn, mean, var = ops.bn_train_fwd(xd, w.to(DEV), b.to(DEV), rm, rv, 0.1, BLOCK, 2,
+                                                           _lib.BN_RELU_QUANT)
+    dy = torch.randn(xd.shape, device=DEV).to(torch.bfloat16)
+    torch.library.opcheck(ops.bn_train_bwd.default, (packed, rp, dy, scale, mn, w.to(DEV), var, BLOCK, 2,
+                                                     _lib.BN_RELU_QUANT), test_utils=tests)
