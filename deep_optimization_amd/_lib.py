@@ -37,6 +37,7 @@ EXPORTS = (
     "dopt_bn_reduce",
     "dopt_bn_norm_quant",
     "dopt_bn_train_forward",
+    "dopt_bn_train_backward",
     "dopt_bn_bwd_reduce",
     "dopt_bn_bwd_dx",
     "dopt_dw_gemm_workspace_floats",
@@ -97,11 +98,16 @@ def lib() -> ctypes.CDLL:
         L.dopt_bn_norm_quant.argtypes = [vp, i32, i64, i64, i64, i64, i64, vp, vp, vp, vp, i32, vp, vp, f32, i32, i32,
                                          i32, vp, vp, vp, vp, vp, vp, vp, vp, vp]
         L.dopt_bn_norm_quant.restype = i32
-        # x, dt, N, C, HW, stride_n, stride_c, workspace, sum, sumsq, weight, bias, eps, mode, group, bits,
+        # x, dt, N, C, HW, stride_n, stride_c, workspace, weight, bias, eps, mode, group, bits,
         # y, x_hat, packed, relu_packed, scale, min, mean_out, var_out, running_mean, running_var, momentum, stream
-        L.dopt_bn_train_forward.argtypes = [vp, i32, i64, i64, i64, i64, i64, vp, vp, vp, vp, vp, f32, i32, i32, i32,
+        L.dopt_bn_train_forward.argtypes = [vp, i32, i64, i64, i64, i64, i64, vp, vp, vp, f32, i32, i32, i32,
                                             vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, f32, vp]
         L.dopt_bn_train_forward.restype = i32
+        # mode, packed, relu_packed, scale, min, dy, dy_dt, N, C, HW, stride_n, stride_c, group, bits, workspace,
+        # weight, var, eps, dweight, dbias, dx, stream
+        L.dopt_bn_train_backward.argtypes = [i32, vp, vp, vp, vp, vp, i32, i64, i64, i64, i64, i64, i32, i32, vp,
+                                             vp, vp, f32, vp, vp, vp, vp]
+        L.dopt_bn_train_backward.restype = i32
         L.dopt_bn_bwd_reduce.argtypes = [i32, vp, vp, vp, vp, vp, vp, i32, i64, i64, i64, i64, i64, i32, i32, vp, vp, vp,
                                          vp]
         L.dopt_bn_bwd_reduce.restype = i32

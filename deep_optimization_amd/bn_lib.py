@@ -402,15 +402,14 @@ def _bn_train_fwd(X, weight, bias, running_mean, running_var, momentum, BLOCK_M,
     scale = torch.empty((C, M // g), dtype=torch.bfloat16, device=dev)
     xmin = torch.empty_like(scale)
     rp = torch.empty((C, M // 32 if kind != _lib.BN_QUANT else 0), dtype=torch.int32, device=dev)
-    sums = torch.empty((2, C), dtype=torch.float32, device=dev)  # sum, sum of squares
     mean = torch.empty(C, dtype=torch.float32, device=dev)
     var = torch.empty_like(mean)
     ws = _workspace(X3, N, C, HW)
     w, b = _f32(weight), _f32(bias)
     rm, rv = (running_mean, running_var) if in_kernel else (None, None)
     rc = _lib.lib().dopt_bn_train_forward(
-        X3.data_ptr(), _DTYPE_CODE[X3.dtype], N, C, HW, C * HW, HW, ws.data_ptr(), sums[0].data_ptr(),
-        sums[1].data_ptr(), w.data_ptr(), b.data_ptr(), _LAYER_EPS[kind][0], kind, g, bits, y.data_ptr(), None,
+        X3.data_ptr(), _DTYPE_CODE[X3.dtype], N, C, HW, C * HW, HW, ws.data_ptr(), w.data_ptr(), b.data_ptr(),
+        _LAYER_EPS[kind][0], kind, g, bits, y.data_ptr(), None,
         packed.data_ptr(), rp.data_ptr() if rp.numel() else None, scale.data_ptr(), xmin.data_ptr(), mean.data_ptr(),
         var.data_ptr(),
         _ptr(rm), _ptr(rv), float(momentum), _stream(X))
@@ -448,9 +447,25 @@ def _bn_train_bwd(packed, relu_packed, dy, scale, min, weight, var, BLOCK_M, bit
         raise RuntimeError(f"bn_train_bwd: dy must be [N, C, ...], got {tuple(dy.shape)}")
     N, C = int(dy.shape[0]), int(dy.shape[1])
     HW = dy.numel() // (N * C) if N * C else 0
-    kw = dict(packed=packed, relu_packed=relu_packed if m == _lib.BN_RELU_QUANT else None, scale=scale, xmin=min)
-    dw, db = _bwd_reduce(m, dy, N * HW, HW, g, bits, **kw)
-    dx = _bwd_dx(m, dy, N * HW, HW, g, bits, dw, db, weight, var, _LAYER_EPS[kind][1], False, **kw)
+    M = N * HW
+    DY3, _, _, _, p, rp, sc, mn = _bwd_common(m, dy, M, HW, packed=packed,
+                                              relu_packed=relu_packed if m == _lib.BN_RELU_QUANT else None,
+                                              scale=scale, xmin=min)
+    if p is None or sc is None or mn is None:
+        raise RuntimeError("bn_train_bwd: packed codes, scale and min are required")
+    w, v = _f32(weight), _f32(var)
+    _check_saved(C, M, g, bits, p, rp, sc, mn, w, v)
+    if m == _lib.BN_RELU_QUANT and rp is None:
+        raise RuntimeError("bn_train_bwd: the ReLU kinds need the saved ReLU mask")
+    dx = torch.empty(DY3.shape, dtype=torch.bfloat16, device=dy.device)
+    dw = torch.empty(C, dtype=torch.float32, device=dy.device)
+    db = torch.empty_like(dw)
+    ws = _workspace(DY3, N, C, HW)
+    rc = _lib.lib().dopt_bn_train_backward(m, p.data_ptr(), _ptr(rp), sc.data_ptr(), mn.data_ptr(), DY3.data_ptr(),
+                                           _DTYPE_CODE[DY3.dtype], N, C, HW, C * HW, HW, g, bits, ws.data_ptr(),
+                                           w.data_ptr(), v.data_ptr(), _LAYER_EPS[kind][1], dw.data_ptr(),
+                                           db.data_ptr(), dx.data_ptr(), _stream(dy))
+    _lib.check(rc, "bn_train_bwd")
     return dx, dw, db
 
 

@@ -47,6 +47,8 @@ struct BnFwdArgs {
     float* run_mean;         // when set (sync == 0): run = run * run_keep + run_mom * batch statistic
     float* run_var;
     float run_keep, run_mom;
+    const float* partial;    // when set (sync == 0): the statistics kernel's [2, C, nchunks] partials,
+    int64_t nchunks;         // summed here instead of reading sum / sumsq
 };
 
 struct BnBwdArgs {
@@ -60,8 +62,9 @@ struct BnBwdArgs {
     float* partial;          // [2, C, nchunks] workspace of the reduce
     float* dw;               // reduce outputs: sum(dy * x_hat), sum(dy)
     float* db;
-    const float* dw_in;      // dx inputs
-    const float* db_in;
+    const float* dw_in;      // dx inputs; when NULL the dx kernel sums the reduce kernel's partials
+    const float* db_in;      // itself and writes dw / db (no separate finalize launch)
+    int64_t nchunks;
     const float* w;
     const float* var;        // variance, or the inverse std when var_is_invstd
     float eps;
@@ -72,10 +75,12 @@ struct BnBwdArgs {
 // vw: elements per vector access (8, 4, 2 or 1); it divides HW, stride_n and stride_c, and every
 // element pointer is aligned to vw elements (bn_width in the C ABI picks it)
 int64_t bn_nchunks(int64_t M);
+// finalize = false: only the workgroup partials (for a consumer that sums them itself)
 int launch_bn_reduce(const void* x, int dt, const BnGeom& g, float* partial, float* sum, float* sumsq, int vw,
-                     hipStream_t s);
+                     hipStream_t s, bool finalize = true);
 int launch_bn_fwd(const BnFwdArgs& a, int dt, int mode, int group, int bits, int vw, hipStream_t s);
-int launch_bn_bwd_reduce(const BnBwdArgs& a, int dyt, int mode, int group, int bits, int vw, hipStream_t s);
+int launch_bn_bwd_reduce(const BnBwdArgs& a, int dyt, int mode, int group, int bits, int vw, hipStream_t s,
+                         bool finalize = true);
 int launch_bn_bwd_dx(const BnBwdArgs& a, int dyt, int mode, int group, int bits, int vw, hipStream_t s);
 
 }  // namespace dopt

@@ -314,6 +314,16 @@ __global__ __launch_bounds__(64) void bn_finalize_kernel(const float* __restrict
     }
 }
 
+// One channel's sum over its workgroup partials p[0..n), computed by a whole wave exactly as
+// bn_finalize_kernel does (lane l adds p[l], p[l + 64], ... in order, then the same wave tree), so
+// the result is bit-identical to the finalized value; every lane returns it.
+__device__ __forceinline__ float partial_sum(const float* __restrict__ p, int64_t n) {
+    float a = 0.0f;
+#pragma unroll 4
+    for (int64_t k = threadIdx.x & 63; k < n; k += 64) a += p[k];
+    return wave_sum(a);
+}
+
 // per-channel mean and inverse std as the forward kernels derive them
 __device__ __forceinline__ void channel_stats(const BnFwdArgs& a, int64_t c, int64_t M, float& mean, float& inv) {
     if (a.sync) {
@@ -322,8 +332,16 @@ __device__ __forceinline__ void channel_stats(const BnFwdArgs& a, int64_t c, int
         return;
     }
     const float Mf = (float)M;
-    mean = a.sum[c] / Mf;
-    float var = fmaf(-mean, mean, a.sumsq[c] / Mf);
+    float sum, sumsq;
+    if (a.partial) {
+        sum = partial_sum(a.partial + c * a.nchunks, a.nchunks);
+        sumsq = partial_sum(a.partial + (a.g.C + c) * a.nchunks, a.nchunks);
+    } else {
+        sum = a.sum[c];
+        sumsq = a.sumsq[c];
+    }
+    mean = sum / Mf;
+    float var = fmaf(-mean, mean, sumsq / Mf);
     var = fmaxf(var, 0.0f);
     inv = 1.0f / sqrtf(var + a.eps);
     if (blockIdx.x == 0 && threadIdx.x == 0) {
@@ -529,7 +547,19 @@ __global__ __launch_bounds__(TPB) void bn_bwd_dx_kernel(BnBwdArgs a, int lg, int
         if (e0 < M) bwd_operands<DYT, MODE, V>(a, c, cur[it], e0, M, lg, bits, xh[it], dy[it]);
     }
     const float Mf = (float)M;
-    const float dwm = a.dw_in[c] / Mf, dbm = a.db_in[c] / Mf;
+    float dws, dbs;
+    if (a.dw_in) {
+        dws = a.dw_in[c];
+        dbs = a.db_in[c];
+    } else {
+        dws = partial_sum(a.partial + c * a.nchunks, a.nchunks);
+        dbs = partial_sum(a.partial + (a.g.C + c) * a.nchunks, a.nchunks);
+        if (blockIdx.x == 0 && threadIdx.x == 0) {
+            a.dw[c] = dws;
+            a.db[c] = dbs;
+        }
+    }
+    const float dwm = dws / Mf, dbm = dbs / Mf;
     const float w = a.w[c];
     const float inv = a.var_is_invstd ? a.var[c] : 1.0f / sqrtf(a.var[c] + a.eps);
 #pragma unroll
@@ -581,7 +611,7 @@ int fwd_dt(const BnFwdArgs& a, int mode, int group, int bits, int vw, hipStream_
 }
 
 template <int DYT>
-int bwd_dt(const BnBwdArgs& a, int mode, int group, int bits, int vw, bool reduce, hipStream_t s) {
+int bwd_dt(const BnBwdArgs& a, int mode, int group, int bits, int vw, bool reduce, hipStream_t s, bool finalize) {
     const int64_t M = a.g.N * a.g.HW;
     const int lg = mode == BN_NORM ? 3 : log2i(group);
     const int64_t nch = bn_nchunks(M);
@@ -604,8 +634,9 @@ int bwd_dt(const BnBwdArgs& a, int mode, int group, int bits, int vw, bool reduc
 #undef DOPT_BN_RED_QUANT
 #undef DOPT_BN_RED_NORM
 #undef DOPT_BN_RED
-        hipLaunchKernelGGL(bn_finalize_kernel, dim3((unsigned)a.g.C), dim3(64), 0, s, (const float*)a.partial,
-                           a.g.C, nch, a.dw, a.db);
+        if (finalize)
+            hipLaunchKernelGGL(bn_finalize_kernel, dim3((unsigned)a.g.C), dim3(64), 0, s, (const float*)a.partial,
+                               a.g.C, nch, a.dw, a.db);
     } else {
 #define DOPT_BN_DX(MODE_, V_) hipLaunchKernelGGL((bn_bwd_dx_kernel<DYT, MODE_, V_>), grid, dim3(TPB), 0, s, a, lg, bits)
 #define DOPT_BN_DX_NORM(V_) DOPT_BN_DX(BN_NORM, V_)
@@ -627,7 +658,7 @@ int bwd_dt(const BnBwdArgs& a, int mode, int group, int bits, int vw, bool reduc
 int64_t bn_nchunks(int64_t M) { return (M + BN_CHUNK - 1) / BN_CHUNK; }
 
 int launch_bn_reduce(const void* x, int dt, const BnGeom& g, float* partial, float* sum, float* sumsq, int vw,
-                     hipStream_t s) {
+                     hipStream_t s, bool finalize) {
     const int64_t M = g.N * g.HW;
     const int64_t nch = bn_nchunks(M);
     const dim3 grid((unsigned)nch, (unsigned)g.C);
@@ -646,8 +677,9 @@ int launch_bn_reduce(const void* x, int dt, const BnGeom& g, float* partial, flo
 #undef DOPT_BN_STATS_F16
 #undef DOPT_BN_STATS_F32
 #undef DOPT_BN_STATS
-    hipLaunchKernelGGL(bn_finalize_kernel, dim3((unsigned)g.C), dim3(64), 0, s, (const float*)partial, g.C, nch,
-                       sum, sumsq);
+    if (finalize)
+        hipLaunchKernelGGL(bn_finalize_kernel, dim3((unsigned)g.C), dim3(64), 0, s, (const float*)partial, g.C, nch,
+                           sum, sumsq);
     return 0;
 }
 
@@ -659,19 +691,20 @@ int launch_bn_fwd(const BnFwdArgs& a, int dt, int mode, int group, int bits, int
     }
 }
 
-int launch_bn_bwd_reduce(const BnBwdArgs& a, int dyt, int mode, int group, int bits, int vw, hipStream_t s) {
+int launch_bn_bwd_reduce(const BnBwdArgs& a, int dyt, int mode, int group, int bits, int vw, hipStream_t s,
+                         bool finalize) {
     switch (dyt) {
-        case DT_F32: return bwd_dt<DT_F32>(a, mode, group, bits, vw, true, s);
-        case DT_F16: return bwd_dt<DT_F16>(a, mode, group, bits, vw, true, s);
-        default: return bwd_dt<DT_BF16>(a, mode, group, bits, vw, true, s);
+        case DT_F32: return bwd_dt<DT_F32>(a, mode, group, bits, vw, true, s, finalize);
+        case DT_F16: return bwd_dt<DT_F16>(a, mode, group, bits, vw, true, s, finalize);
+        default: return bwd_dt<DT_BF16>(a, mode, group, bits, vw, true, s, finalize);
     }
 }
 
 int launch_bn_bwd_dx(const BnBwdArgs& a, int dyt, int mode, int group, int bits, int vw, hipStream_t s) {
     switch (dyt) {
-        case DT_F32: return bwd_dt<DT_F32>(a, mode, group, bits, vw, false, s);
-        case DT_F16: return bwd_dt<DT_F16>(a, mode, group, bits, vw, false, s);
-        default: return bwd_dt<DT_BF16>(a, mode, group, bits, vw, false, s);
+        case DT_F32: return bwd_dt<DT_F32>(a, mode, group, bits, vw, false, s, false);
+        case DT_F16: return bwd_dt<DT_F16>(a, mode, group, bits, vw, false, s, false);
+        default: return bwd_dt<DT_BF16>(a, mode, group, bits, vw, false, s, false);
     }
 }
 

@@ -463,24 +463,30 @@ int dopt_bn_norm_quant(const void* x, int x_dtype, int64_t N, int64_t C, int64_t
 }
 
 int dopt_bn_train_forward(const void* x, int x_dtype, int64_t N, int64_t C, int64_t HW, int64_t stride_n,
-                          int64_t stride_c, float* workspace, float* sum, float* sumsq, const float* weight,
-                          const float* bias, float eps, int mode, int group_size, int bits, void* y, void* x_hat,
-                          uint32_t* packed, uint32_t* relu_packed, void* scale, void* minv, float* mean_out,
-                          float* var_out, float* running_mean, float* running_var, float momentum, void* stream) {
+                          int64_t stride_c, float* workspace, const float* weight, const float* bias, float eps,
+                          int mode, int group_size, int bits, void* y, void* x_hat, uint32_t* packed,
+                          uint32_t* relu_packed, void* scale, void* minv, float* mean_out, float* var_out,
+                          float* running_mean, float* running_var, float momentum, void* stream) {
     int rc;
-    if ((rc = dopt_bn_reduce(x, x_dtype, N, C, HW, stride_n, stride_c, workspace, sum, sumsq, stream))) return rc;
     dopt::BnGeom g;
     if ((rc = bn_geom(N, C, HW, stride_n, stride_c, &g))) return rc;
+    if ((rc = bn_dtype(x_dtype, "bn_train_forward: x"))) return rc;
     const int64_t M = N * HW;
     if ((rc = bn_quant_checks(mode, M, group_size, bits, packed, scale, minv, relu_packed))) return rc;
     if (C == 0 || M == 0) return ok();
-    if (!x || !y || !weight || !bias || !mean_out || !var_out) return fail(DOPT_EINVAL, "null pointer argument");
+    if (!x || !y || !weight || !bias || !mean_out || !var_out || !workspace)
+        return fail(DOPT_EINVAL, "null pointer argument");
     if (mode == DOPT_BN_NORM && !x_hat) return fail(DOPT_EINVAL, "null x_hat pointer");
+    const int vw = bn_width(g, {{x, bn_bytes(x_dtype)}, {y, 2}, {x_hat, 2}});
+    (void)hipGetLastError();
+    // workgroup partials only: the normalize kernel sums them itself (no finalize launch)
+    dopt::launch_bn_reduce(x, x_dtype, g, workspace, nullptr, nullptr, bn_width(g, {{x, bn_bytes(x_dtype)}}),
+                           (hipStream_t)stream, false);
     dopt::BnFwdArgs a{};
     a.g = g;
     a.x = x;
-    a.sum = sum;
-    a.sumsq = sumsq;
+    a.partial = workspace;
+    a.nchunks = dopt::bn_nchunks(M);
     a.w = weight;
     a.b = bias;
     a.eps = eps;
@@ -497,10 +503,48 @@ int dopt_bn_train_forward(const void* x, int x_dtype, int64_t N, int64_t C, int6
     a.run_var = running_var;
     a.run_mom = momentum;
     a.run_keep = (float)(1.0 - (double)momentum);
-    (void)hipGetLastError();
-    dopt::launch_bn_fwd(a, x_dtype, mode, group_size, bits,
-                        bn_width(g, {{x, bn_bytes(x_dtype)}, {y, 2}, {x_hat, 2}}), (hipStream_t)stream);
+    dopt::launch_bn_fwd(a, x_dtype, mode, group_size, bits, vw, (hipStream_t)stream);
     return hip_status("bn_train_forward launch");
+}
+
+int dopt_bn_train_backward(int mode, const uint32_t* packed, const uint32_t* relu_packed, const void* scale,
+                           const void* minv, const void* dy, int dy_dtype, int64_t N, int64_t C, int64_t HW,
+                           int64_t stride_n, int64_t stride_c, int group_size, int bits, float* workspace,
+                           const float* weight, const float* var, float eps, float* dweight, float* dbias, void* dx,
+                           void* stream) {
+    int rc;
+    dopt::BnGeom g;
+    if ((rc = bn_geom(N, C, HW, stride_n, stride_c, &g))) return rc;
+    if ((rc = bn_dtype(dy_dtype, "bn_train_backward: dy"))) return rc;
+    if (mode == DOPT_BN_NORM) return fail(DOPT_EINVAL, "bn_train_backward takes the quantized modes");
+    const int64_t M = N * HW;
+    if ((rc = bn_quant_checks(mode, M, group_size, bits, packed, scale, minv, relu_packed))) return rc;
+    if (C == 0 || M == 0) return ok();
+    if (!dy || !dx || !dweight || !dbias || !weight || !var || !workspace) return fail(DOPT_EINVAL, "null pointer argument");
+    dopt::BnBwdArgs a{};
+    a.g = g;
+    a.packed = packed;
+    a.relu_packed = relu_packed;
+    a.scale = (const uint16_t*)scale;
+    a.minv = (const uint16_t*)minv;
+    a.dy = dy;
+    a.partial = workspace;
+    a.nchunks = dopt::bn_nchunks(M);
+    a.dw = dweight;
+    a.db = dbias;
+    a.dw_in = nullptr;  // the dx kernel sums the partials and writes dweight / dbias
+    a.db_in = nullptr;
+    a.w = weight;
+    a.var = var;
+    a.eps = eps;
+    a.var_is_invstd = 0;
+    a.dx = (uint16_t*)dx;
+    (void)hipGetLastError();
+    dopt::launch_bn_bwd_reduce(a, dy_dtype, mode, group_size, bits, bn_width(g, {{dy, bn_bytes(dy_dtype)}}),
+                               (hipStream_t)stream, false);
+    dopt::launch_bn_bwd_dx(a, dy_dtype, mode, group_size, bits, bn_width(g, {{dy, bn_bytes(dy_dtype)}, {dx, 2}}),
+                           (hipStream_t)stream);
+    return hip_status("bn_train_backward launch");
 }
 
 int dopt_bn_bwd_reduce(int mode, const void* x_hat, const uint32_t* packed, const uint32_t* relu_packed,

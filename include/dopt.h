@@ -227,17 +227,30 @@ int dopt_bn_norm_quant(const void* x, int x_dtype, int64_t N, int64_t C, int64_t
                        int group_size, int bits, void* y, void* x_hat, uint32_t* packed, uint32_t* relu_packed,
                        void* scale, void* minv, float* mean_out, float* var_out, void* stream);
 
-/* The training forward of the compressed BatchNorm layer in one call: dopt_bn_reduce into sum/sumsq,
- * then dopt_bn_norm_quant (sync = 0), which also updates running_mean / running_var (when not NULL)
- * with run = fma(momentum, stat, run * (1 - momentum)), stat the batch mean and biased variance.
- * Replaces the act_lib::bn_fwd_reduce + act_lib::bn_fwd_norm_quant_pack_fused (or
- * bn_relu_fwd_norm_fused_quant_pack) pair and the running-statistics update of _DOBatchNorm.forward
- * (AC/modules/normalization/normalization_ops.py:45-57). */
+/* The training forward of the compressed BatchNorm layer in one call: the statistics kernel's
+ * workgroup partials (into workspace, dopt_bn_workspace_floats() floats), then the normalize (+ ReLU)
+ * + quant-pack kernel of dopt_bn_norm_quant (sync = 0), which sums the partials itself in the
+ * finalize order (bit-identical to dopt_bn_reduce's sums), writes mean_out / var_out and updates
+ * running_mean / running_var (when not NULL) with run = fma(momentum, stat, run * (1 - momentum)),
+ * stat the batch mean and biased variance. Replaces the act_lib::bn_fwd_reduce +
+ * act_lib::bn_fwd_norm_quant_pack_fused (or bn_relu_fwd_norm_fused_quant_pack) pair and the
+ * running-statistics update of _DOBatchNorm.forward (AC/modules/normalization/normalization_ops.py:45-57). */
 int dopt_bn_train_forward(const void* x, int x_dtype, int64_t N, int64_t C, int64_t HW, int64_t stride_n,
-                          int64_t stride_c, float* workspace, float* sum, float* sumsq, const float* weight,
-                          const float* bias, float eps, int mode, int group_size, int bits, void* y, void* x_hat,
-                          uint32_t* packed, uint32_t* relu_packed, void* scale, void* minv, float* mean_out,
-                          float* var_out, float* running_mean, float* running_var, float momentum, void* stream);
+                          int64_t stride_c, float* workspace, const float* weight, const float* bias, float eps,
+                          int mode, int group_size, int bits, void* y, void* x_hat, uint32_t* packed,
+                          uint32_t* relu_packed, void* scale, void* minv, float* mean_out, float* var_out,
+                          float* running_mean, float* running_var, float momentum, void* stream);
+
+/* The backward of that layer in one call (quantized modes): the reduce kernel's partials into
+ * workspace, then the dx kernel, which sums them (bit-identical to dopt_bn_bwd_reduce's dweight /
+ * dbias), writes dweight / dbias and dx. Replaces the act_lib::bn_bwd_reduce_dequant_unpack_fused +
+ * bn_bwd_dx_dequant_unpack_fused (or the bn_relu_* pair) of the reference's layers
+ * (normalization_ops.py:95-157, AC/fusion/fused_ops.py:60-86). */
+int dopt_bn_train_backward(int mode, const uint32_t* packed, const uint32_t* relu_packed, const void* scale,
+                           const void* minv, const void* dy, int dy_dtype, int64_t N, int64_t C, int64_t HW,
+                           int64_t stride_n, int64_t stride_c, int group_size, int bits, float* workspace,
+                           const float* weight, const float* var, float eps, float* dweight, float* dbias, void* dx,
+                           void* stream);
 
 /* dweight[c] = sum(dy*m * x_hat'), dbias[c] = sum(dy*m), with x_hat' = fma(q, scale, min) (or the bf16
  * x_hat for DOPT_BN_NORM) and m the ReLU mask (ReLU modes) or 1. Replaces act_lib::bn_bwd_reduce
