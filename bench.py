@@ -81,7 +81,8 @@ def resnet_inputs(torch, dev):
 
 
 def pmc_probe() -> int:
-    """A plain copy of known size (the counter calibration), then the dominant kernel three times."""
+    """A plain copy of known size (the counter calibration), then the dominant kernel three times and
+    the unpack-dequant kernel three times."""
     import torch
 
     import deep_optimization_amd  # noqa: F401
@@ -103,8 +104,13 @@ def pmc_probe() -> int:
         _lib.check(_lib.lib().dopt_quant_pack(xg.data_ptr(), _lib.BF16, n_groups, G_SIZE, BITS, None, NOISE,
                                               noise.data_ptr(), 0, 0, 0, 0.0, packed.data_ptr(), scale.data_ptr(),
                                               xmin.data_ptr(), _lib.F32, stream), "quant_pack")
+    for _ in range(3):
+        _lib.check(_lib.lib().dopt_dequant_unpack(packed.data_ptr(), scale.data_ptr(), xmin.data_ptr(), _lib.F32,
+                                                  n_groups, G_SIZE, BITS, None, y.data_ptr(), _lib.BF16, stream),
+                   "dequant_unpack")
     torch.cuda.synchronize()
-    print(f"pmc probe: copy {x.numel() * 2} B, then 3 x quant_pack (noise, bf16, g={G_SIZE}, {BITS}-bit)")
+    print(f"pmc probe: copy {x.numel() * 2} B, then 3 x quant_pack (noise, bf16, g={G_SIZE}, {BITS}-bit), "
+          "3 x dequant_unpack (bf16 out)")
     return 0
 
 
