@@ -23,7 +23,7 @@ implementation with the correct output shapes; there is no CPU implementation.
 """
 from __future__ import annotations
 
-from typing import Optional, Tuple
+from typing import Optional
 
 import torch
 from torch import Tensor

@@ -26,7 +26,6 @@ from functools import reduce
 import operator
 from typing import Tuple
 
-import torch
 import torch.nn.functional as F
 from torch import Tensor
 

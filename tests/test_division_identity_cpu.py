@@ -4,7 +4,6 @@ RN(q0 + r y), which Markstein's theorem (the IA-64 division) makes the correctly
 quotient. The kernel uses it for 2^-60 <= step < inf. This test pins the identity bit-for-bit
 against fp32 division on random and quantizer-shaped pairs in that range, in C with fmaf (gcc),
 for every quotient that can reach a rounding boundary of a code (q >= 1e-7)."""
-import os
 import shutil
 import subprocess
 
