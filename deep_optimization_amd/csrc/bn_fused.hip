@@ -500,6 +500,22 @@ __device__ __forceinline__ void bwd_operands(const BnBwdArgs& a, int64_t c, RowC
     }
 }
 
+// dy (times the ReLU mask), the codes and the group's scale / min of the lane's 8 elements
+template <int DYT, int MODE, int V>
+__device__ __forceinline__ void bwd_codes(const BnBwdArgs& a, int64_t c, RowCursor pos, int64_t e0, int64_t M, int lg,
+                                          int bits, int* q, float& sc, float& mn, float* dy) {
+    load8<DYT, V>(a.dy, a.g, pos, e0, M, dy);
+    load_codes(a.packed + c * ((M * bits) >> 5), e0, bits, q);
+    const int64_t gi = c * (M >> lg) + (e0 >> lg);
+    sc = bf16_bits_to_f32(a.scale[gi]);
+    mn = bf16_bits_to_f32(a.minv[gi]);
+    if constexpr (MODE == BN_RELU_QUANT) {
+        const uint32_t m = a.relu_packed[c * (M >> 5) + (e0 >> 5)] >> (e0 & 31);
+#pragma unroll
+        for (int k = 0; k < EPL; ++k) dy[k] = dy[k] * (float)((m >> k) & 1u);
+    }
+}
+
 template <int DYT, int MODE, int V>
 __global__ __launch_bounds__(TPB) void bn_bwd_reduce_kernel(BnBwdArgs a, int lg, int bits, int64_t nchunks) {
     const int64_t c = blockIdx.y, chunk = blockIdx.x;
@@ -507,25 +523,47 @@ __global__ __launch_bounds__(TPB) void bn_bwd_reduce_kernel(BnBwdArgs a, int lg,
     const int64_t base = chunk * BN_CHUNK + (int64_t)threadIdx.x * EPL;
     RowCursor cur[ITER];
     block_cursors(a.g, c, base, cur);
-    float xh[ITER][EPL], dy[ITER][EPL];
+    float sdy = 0.0f, sdyx = 0.0f;
+    if constexpr (MODE == BN_NORM) {
+        float xh[ITER][EPL], dy[ITER][EPL];
 #pragma unroll
-    for (int it = 0; it < ITER; ++it) {
-        const int64_t e0 = base + it * WG_ELEMS;
-        if (e0 < M) {
-            bwd_operands<DYT, MODE, V>(a, c, cur[it], e0, M, lg, bits, xh[it], dy[it]);
-        } else {
+        for (int it = 0; it < ITER; ++it) {
+            const int64_t e0 = base + it * WG_ELEMS;
+            if (e0 < M) bwd_operands<DYT, MODE, V>(a, c, cur[it], e0, M, lg, bits, xh[it], dy[it]);
+        }
 #pragma unroll
-            for (int k = 0; k < EPL; ++k) xh[it][k] = dy[it][k] = 0.0f;
+        for (int it = 0; it < ITER; ++it) {
+            if (base + it * WG_ELEMS >= M) continue;
+#pragma unroll
+            for (int k = 0; k < EPL; ++k) {
+                sdy += dy[it][k];
+                sdyx = fmaf(dy[it][k], xh[it][k], sdyx);
+            }
+        }
+    } else {
+        // a lane's 8 elements of a block lie in one group, so sum(dy * x_hat') over them is
+        // scale * sum(dy * q) + min * sum(dy): no dequantized value per element
+        float dy[ITER][EPL];
+        int q[ITER][EPL];
+        float sc[ITER], mn[ITER];
+#pragma unroll
+        for (int it = 0; it < ITER; ++it) {
+            const int64_t e0 = base + it * WG_ELEMS;
+            if (e0 < M) bwd_codes<DYT, MODE, V>(a, c, cur[it], e0, M, lg, bits, q[it], sc[it], mn[it], dy[it]);
+        }
+#pragma unroll
+        for (int it = 0; it < ITER; ++it) {
+            if (base + it * WG_ELEMS >= M) continue;
+            float gdy = 0.0f, gdyq = 0.0f;
+#pragma unroll
+            for (int k = 0; k < EPL; ++k) {
+                gdy += dy[it][k];
+                gdyq = fmaf(dy[it][k], (float)q[it][k], gdyq);
+            }
+            sdy += gdy;
+            sdyx = fmaf(sc[it], gdyq, fmaf(mn[it], gdy, sdyx));
         }
     }
-    float sdy = 0.0f, sdyx = 0.0f;
-#pragma unroll
-    for (int it = 0; it < ITER; ++it)
-#pragma unroll
-        for (int k = 0; k < EPL; ++k) {
-            sdy += dy[it][k];
-            sdyx = fmaf(dy[it][k], xh[it][k], sdyx);
-        }
     block_sum2(sdy, sdyx);
     if (threadIdx.x == 0) {
         a.partial[c * nchunks + chunk] = sdyx;            // -> dw
