@@ -174,8 +174,6 @@ int dopt_quant_pack(const void* x, int x_dtype, int64_t n_groups, int group_size
     if (rounding < DOPT_ROUND_NEAREST || rounding > DOPT_ROUND_STOCH_PHILOX)
         return fail(DOPT_EINVAL, "unknown rounding mode %d", rounding);
     if (flags & ~(DOPT_FLAG_CLAMP | DOPT_FLAG_SQUASH)) return fail(DOPT_EINVAL, "unknown flags 0x%x", flags);
-    if (flags && rounding != DOPT_ROUND_NEAREST)
-        return fail(DOPT_EUNSUPPORTED, "the clamp/squash pre-transform is implemented with nearest rounding only");
     dopt::QuantPackArgs a{};
     if ((rc = setup_tiles(tile_nchw, n_groups, group_size, &a.tiled, &a.tiles_w, &a.log2s, &a.row))) return rc;
     if (n_groups == 0) return ok();

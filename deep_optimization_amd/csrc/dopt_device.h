@@ -151,15 +151,29 @@ __device__ __forceinline__ float bf16_bits_to_f32(uint16_t b) { return __uint_as
 // Fast fp32 transcendentals for the fused kernels (v_exp_f32 / v_rcp_f32 based; the reference's
 // own are Triton's exp and libdevice tanh, so these are tolerance-level anyway).
 //
-// The quantizer's squash tanh(x / 0.5) * 0.5 = tanh(2x) / 2: for |x| >= 1/16 as sigmoid(4x) - 1/2
-// (absolute error ~6e-8), below that the odd Taylor polynomial x (1 - 4x^2/3 + 32x^4/15 -
-// 272x^6/315) (truncation error < 1e-10 there), which keeps small values accurate relative to
-// their own size: a group whose values are all tiny still gets a faithful range. Exact 0 at 0.
+// The quantizer's squash tanh(x / 0.5) * 0.5 = tanh(2x) / 2, within about 2 fp32 ulps of the
+// exact value everywhere (the reference evaluates it with libdevice tanh):
+//   |x| < 0.45:  x + x^3 Q(x^2), Q of degree 5: a weighted minimax fit of (tanh(2x)/2 - x)/x^3
+//                over x^2 in [0, 0.2025] whose relative error is 1.6e-8; evaluated in fp32 the
+//                branch is within 1.01 ulp, and tiny values keep their relative accuracy (exact
+//                0 at 0, -0 at -0);
+//   |x| >= 0.45: 1/2 - 1/(e^{4|x|} + 1) with the sign of x (v_exp_f32, v_rcp_f32). The result is
+//                >= 0.358 there and the subtracted term <= 0.142, so nothing cancels: within 1.3
+//                ulps with a correctly rounded exp, 1.7 with one ulp of exp error. +-inf gives
+//                +-1/2 and NaN stays NaN.
+// (a float64 emulation of both branches over 7 million arguments gave a 1.80 ulp maximum.)
 __device__ __forceinline__ float squash_half_tanh2(float x) {
-    const float r = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-5.7707801635558535f * x)) - 0.5f;
-    const float s = x * x;
-    const float p = x * fmaf(s, fmaf(s, fmaf(s, -272.0f / 315.0f, 32.0f / 15.0f), -4.0f / 3.0f), 1.0f);
-    return fabsf(x) < 0.0625f ? p : r;
+    const float a = fabsf(x);
+    const float e = __builtin_amdgcn_exp2f(5.7707801635558535f * a);  // e^{4|x|} = 2^{4|x|/ln 2}
+    const float r = __builtin_copysignf(0.5f - __builtin_amdgcn_rcpf(e + 1.0f), x);
+    const float t = x * x;
+    float q = __builtin_fmaf(t, 5.341052532196045f, -7.024715423583984f);
+    q = __builtin_fmaf(q, t, 5.351459980010986f);
+    q = __builtin_fmaf(q, t, -3.438175678253174f);
+    q = __builtin_fmaf(q, t, 2.13285756111145f);
+    q = __builtin_fmaf(q, t, -1.3333284854888916f);
+    const float p = __builtin_fmaf(x * t, q, x);
+    return a < 0.45f ? p : r;
 }
 __device__ __forceinline__ float fast_sigmoid(float x) {
     return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-1.4426950408889634f * x));

@@ -19,16 +19,20 @@
 // enable_fp_fusion and nvcc's default --fmad=true, so `a * b + c` is one rounding):
 //   nearest     q = trunc(fma(x - mn, inv, fp32(0.5 - 1e-6)))   act_triton_kernel.py:114, :155
 //   stochastic  q = rint(fma(x - mn, inv, u) - 0.5)              quant_common.h:150-151
-// Fast path and its exactness argument. For finite x in [mn, mx] with inv = 1/step finite, the
-// exact product (x - mn) * inv is at most QMAX * (1 + 2^-22), so both forms already land in
-// [0, QMAX] before the reference's clamp (u < 1): the clamp is redundant and v_cvt_u32_f32
-// (truncating, NaN -> 0) gives the exact code. An infinite input or an overflowing range gives
-// inv = 0 and a product of 0 or NaN (code 0 either way, as with the reference's clamp). The only
-// case that needs the explicit clamp is inv = +inf (step < 2^-128, a range of a few
-// subnormals); a wave containing such a group takes the clamped path. Local min/max use raw
-// v_min3/v_max3 (no NaN canonicalisation); a signalling NaN input would turn a lane's partial
-// result into NaN, so a wave with a NaN partial result recomputes min/max with IEEE fminf/fmaxf,
-// which ignore NaN operands.
+// Clamp and its exactness argument. For finite x in [mn, mx] with inv = 1/step finite, the exact
+// product (x - mn) * inv is at most QMAX * (1 + 2^-22). Nearest rounding adds 0.5 - 1e-6 and
+// Philox noise adds u <= 255.5/256, so those two forms stay below QMAX + 1/2 before the
+// reference's clamp: the clamp is redundant there and v_cvt_u32_f32 (truncating, NaN -> 0) gives
+// the exact code. A caller's noise tensor is different: torch.rand can return u = 1 - 2^-24, and
+// fma(t, inv, u) with t * inv = QMAX then rounds to QMAX + 1 (the spacing of fp32 near QMAX + 1 is
+// coarser than 2^-24), whose rint is QMAX + 1; noise-tensor rounding therefore always applies the
+// reference's clamp (quant_common.h:152, one v_med3 per element). An infinite input or an
+// overflowing range gives inv = 0 and a product of 0 or NaN (code 0 either way, as with the
+// reference's clamp). The remaining case that needs the clamp is inv = +inf (step < 2^-128, a
+// range of a few subnormals); a wave containing such a group takes the clamped path. Local
+// min/max use raw v_min3/v_max3 (no NaN canonicalisation); a signalling NaN input would turn a
+// lane's partial result into NaN, so a wave with a NaN partial result recomputes min/max with
+// IEEE fminf/fmaxf, which ignore NaN operands.
 #pragma once
 
 #include "dopt_device.h"
@@ -324,7 +328,8 @@ __global__ __launch_bounds__(256) void quant_pack_kernel(QuantPackArgs a) {
                         qf = qf - 0.5f;
                         qf = __builtin_rintf(qf);
                     }
-                    if constexpr (CL) qf = __builtin_amdgcn_fmed3f(qf, 0.0f, qmaxf);  // NaN -> 0, as the reference's clamp
+                    // NaN -> 0, as the reference's clamp; always on for a caller's noise tensor
+                    if constexpr (CL || RN == RN_NOISE) qf = __builtin_amdgcn_fmed3f(qf, 0.0f, qmaxf);
                     q[k] = cvt_u32(qf);
                 }
                 // UBITS code bits of this unit, little-endian

@@ -45,10 +45,17 @@ static int qp_launch(const QuantPackArgs& a, hipStream_t s) {
 
 template <int DT, int BITS, int G>
 static int qp_rn(const QuantPackArgs& a, int rn, int pre, hipStream_t s) {
-    if (pre != PRE_NONE) {  // the pre-transforms (reference quantizer, fused activations) round to nearest
+    if (pre == PRE_REF) {  // the reference quantizer's clamp / squash, with any rounding
+        switch (rn) {
+            case RN_NEAREST: return qp_launch<DT, BITS, G, RN_NEAREST, PRE_REF>(a, s);
+            case RN_NOISE: return qp_launch<DT, BITS, G, RN_NOISE, PRE_REF>(a, s);
+            case RN_PHILOX: return qp_launch<DT, BITS, G, RN_PHILOX, PRE_REF>(a, s);
+        }
+        return -1;
+    }
+    if (pre != PRE_NONE) {  // the fused activations round to nearest
         if (rn != RN_NEAREST) return -1;
         switch (pre) {
-            case PRE_REF: return qp_launch<DT, BITS, G, RN_NEAREST, PRE_REF>(a, s);
             case PRE_GELU:
                 if constexpr (DT == DT_F16) return -1;
                 else return qp_launch<DT, BITS, G, RN_NEAREST, PRE_GELU>(a, s);

@@ -78,9 +78,8 @@ const char* dopt_last_error(void);
  *   bits        1, 2, 4 or 8
  *   rounding    DOPT_ROUND_*; noise (fp32 [n_groups, group_size] in group order, values in [0,1))
  *               is read only for DOPT_ROUND_STOCH_NOISE; seed/offset only for DOPT_ROUND_STOCH_PHILOX.
- *   flags       DOPT_FLAG_* bit set; clamp_alpha used with DOPT_FLAG_CLAMP. The pre-transform is
- *               the reference's, which always rounds to nearest: flags != 0 with a stochastic
- *               rounding mode returns DOPT_EUNSUPPORTED.
+ *   flags       DOPT_FLAG_* bit set; clamp_alpha used with DOPT_FLAG_CLAMP. The pre-transform
+ *               (the reference's, act_triton_kernel.py:55-58) combines with every rounding mode.
  *   packed      out: uint32 [n_groups, group_size*bits/32], 16-byte aligned.
  *   scale, minv out: [n_groups] of meta_dtype (F32 or BF16): step = (max-min)/(2^b-1) (1.0 when
  *               max == min) and the group minimum (act_triton_kernel.py:60-68).

@@ -77,6 +77,38 @@ def test_do_linear(bits, shape, autocast, cout, fused):
     assert rel_err(layer.bias.grad, dyf.sum(0)) <= 1e-2
 
 
+@pytest.mark.parametrize("rounding", ["stochastic", "stochastic_noise"])
+def test_do_linear_stochastic_rounding_meta(rounding):
+    """The per-layer meta keys 'rounding' = 'stochastic' (Philox) / 'stochastic_noise' reach the
+    layer's clamp + squash quantizer. 8-bit codes: the weight gradient is within 1e-2 of
+    dy^T . squash(clamp(x)) in fp32; with a noise tensor it also equals (1e-2) the operator chain
+    quant_pack(clamp, squash, the same noise) -> dequant_unpack."""
+    torch.manual_seed(3)
+    shape, cout, bits = (4, 197, 768), 512, 8
+    over = {"rounding": rounding, "seed": 5}
+    meta = meta_for("fc", shape, bits, **over)
+    g = meta["fc"]["group_size"]
+    n_el = shape[0] * shape[1] * shape[2]
+    noise = torch.rand((shape[0], n_el // shape[0] // g, g), device=DEV)
+    if rounding == "stochastic_noise":
+        meta["fc"]["noise"] = noise
+    layer = DOLinear(shape[-1], cout, target_name="fc", meta=meta).to(DEV).train()
+    x = (torch.randn(shape, device=DEV) * 2).requires_grad_(True)
+    dy = torch.randn(*shape[:-1], cout, device=DEV)
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        y = layer(x)
+    y.backward(dy.to(y.dtype))
+    xb = x.detach().to(torch.bfloat16).float()
+    sq = torch.tanh(2.0 * xb.clamp(-3.0, 3.0)) / 2.0
+    dyf = dy.to(torch.bfloat16).float().reshape(-1, cout)
+    assert rel_err(layer.weight.grad, dyf.t() @ sq.reshape(-1, shape[-1])) <= 1e-2
+    if rounding == "stochastic_noise":
+        groups = x.detach().to(torch.bfloat16).reshape(shape[0], -1, g)
+        p, sc, mn = torch.ops.act_lib.quant_pack(groups, bits, g, True, 3.0, True, 1, noise, 0, 0, torch.bfloat16)
+        x_hat = torch.ops.act_lib.dequant_unpack(p, sc, mn, bits, g, torch.bfloat16).float()
+        assert rel_err(layer.weight.grad, dyf.t() @ x_hat.reshape(-1, shape[-1])) <= 1e-2
+
+
 @pytest.mark.parametrize("bits", [2, 4])
 @pytest.mark.parametrize("case", ["flat512", "tile256", "stride2"])
 def test_do_conv2d(bits, case):

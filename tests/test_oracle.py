@@ -13,6 +13,8 @@ import pytest
 import torch
 
 import oracle
+from tests.restate import (_ulp32, f64_pretransform, fma32, numpy_quant, packbits_reference, squash_inputs,  # noqa: F401
+                           squash_mismatch)
 
 F32, BF16 = oracle.F32, oracle.BF16
 NEAREST, NOISE, PHILOX = oracle.NEAREST, oracle.STOCH_NOISE, oracle.STOCH_PHILOX
@@ -25,14 +27,6 @@ def _lib(oracle_lib):
 
 def words_to_bytes(packed):
     return np.ascontiguousarray(packed, dtype="<u4").view(np.uint8)
-
-
-def packbits_reference(codes, bits):
-    """Little-endian bitstream of b-bit codes via numpy.packbits (library routine)."""
-    codes = np.asarray(codes, dtype=np.int64)
-    expanded = ((codes[..., None] >> np.arange(bits)) & 1).astype(np.uint8)
-    flat = expanded.reshape(codes.shape[0], -1)
-    return np.packbits(flat, axis=1, bitorder="little")
 
 
 # ----------------------------------------------------------------------------- Philox
@@ -198,29 +192,6 @@ def test_input_widening_bf16_f16():
 
 
 # ----------------------------------------------------------------------------- independent restatement
-def fma32(a, b, c):
-    """Correctly rounded float32 fused multiply-add in numpy, independent of any libm fmaf:
-    a*b is exact in float64 (24 + 24 bits); TwoSum gives the exact error of the float64 sum;
-    rounding that sum to odd at 53 bits and then to nearest at 24 bits is correctly rounded
-    (53 >= 24 + 2, Boldo & Melquiond)."""
-    a = np.asarray(a, dtype=np.float32).astype(np.float64)
-    b = np.asarray(b, dtype=np.float32).astype(np.float64)
-    c = np.asarray(c, dtype=np.float32).astype(np.float64)
-    p = a * b
-    with np.errstate(invalid="ignore", over="ignore"):
-        s = p + c
-        bp = s - c
-        e = (p - (s - bp)) + (c - bp)  # exact: p + c == s + e (finite s)
-        bits = s.view(np.int64).copy()
-        inexact = np.isfinite(s) & (e != 0)
-        # truncate toward zero: RN went away from zero when e and s have opposite signs
-        away = inexact & (np.sign(e) != np.sign(s)) & (s != 0)
-        bits[away] -= 1
-        bits[inexact] |= 1  # round to odd
-        odd = bits.view(np.float64)
-        return odd.astype(np.float32)
-
-
 def test_fma32_emulation_is_exact():
     from fractions import Fraction
     rng = np.random.default_rng(99)
@@ -236,27 +207,6 @@ def test_fma32_emulation_is_exact():
         cands = sorted([lo, r, hi], key=lambda v: (abs(Fraction(float(v)) - exact),
                                                    int(np.float32(v).view(np.uint32)) & 1))
         assert got[i] == cands[0], (a[i], b[i], c[i])
-
-
-def numpy_quant(x, bits, rounding=NEAREST, u=None):
-    """Vectorised numpy float32 restatement: each array op rounds once, fma32 for the fused
-    multiply-add of the reference's contracted `(x - mn) * inv + c`."""
-    f = np.float32
-    qmax = (1 << bits) - 1
-    mn = x.min(axis=1) + f(0.0)
-    mx = x.max(axis=1)
-    rng = (mx - mn).astype(np.float32)
-    step = np.where(rng > 0, rng / f(qmax), f(1.0)).astype(np.float32)
-    inv = (f(1.0) / step).astype(np.float32)
-    t = (x - mn[:, None]).astype(np.float32)
-    if rounding == NEAREST:
-        qf = fma32(t, np.broadcast_to(inv[:, None], t.shape), np.full(t.shape, f(0.5 - 1e-6)))
-        q = np.clip(qf, 0, qmax).astype(np.int64)
-    else:
-        qf = (fma32(t, np.broadcast_to(inv[:, None], t.shape), u) - f(0.5)).astype(np.float32)
-        q = np.rint(np.clip(qf, 0, qmax)).astype(np.int64)
-    packed = packbits_reference(q, bits).view("<u4")
-    return packed, step, mn
 
 
 def _fma_boundary_values(step_target, bits, per_boundary=2):
@@ -559,3 +509,53 @@ def test_act_dequant_mul_closed_form(bits):
     dx = oracle.act_dequant_mul(packed, sc, mn, g, bits, dy)
     act = fma32(q.astype(np.float32), np.broadcast_to(_f32(sc)[:, None], q.shape), np.broadcast_to(_f32(mn)[:, None], q.shape))
     np.testing.assert_array_equal(dx, _bf16((_f32(dy) * act).astype(np.float32)))
+
+
+# ----------------------------------------------------------------------------- clamp + tanh squash
+@pytest.mark.parametrize("alpha", [3.0, 0.3])
+@pytest.mark.parametrize("bits", [2, 8])
+def test_clamp_squash_equals_float64(bits, alpha):
+    x = squash_inputs(bits + int(alpha * 10))
+    got = oracle.quant_pack(x, 256, bits, flags=oracle.FLAG_CLAMP | oracle.FLAG_SQUASH, clamp_alpha=alpha)
+    assert squash_mismatch(got, x, bits, alpha) == []
+
+
+@pytest.mark.parametrize("plant", [{"form": "2tanh(x/2)"}, {"clamp_first": False}])
+def test_clamp_squash_check_catches_planted_mistakes(plant):
+    """The comparison above must reject a restatement with BatchNorm's squash 2 tanh(x/2) in place of
+    tanh(2x)/2, and one that clamps after squashing (which clamps nothing at alpha = 3 but lets
+    values beyond alpha move the group's extremes)."""
+    x = squash_inputs(5)
+    alpha = 3.0
+    got = oracle.quant_pack(x, 256, 2, flags=oracle.FLAG_CLAMP | oracle.FLAG_SQUASH, clamp_alpha=alpha)
+    assert squash_mismatch(got, x, 2, alpha, **plant) != []
+
+
+def test_clamp_alone_is_bit_exact_against_numpy():
+    x = squash_inputs(6)
+    for bits in (1, 4):
+        got = oracle.quant_pack(x, 256, bits, flags=oracle.FLAG_CLAMP, clamp_alpha=0.75)
+        want = numpy_quant(np.clip(x, np.float32(-0.75), np.float32(0.75)), bits)
+        for a, b in zip(got, want):
+            np.testing.assert_array_equal(a, b)
+
+
+def test_noise_near_one_is_clamped_to_qmax():
+    """u = 1 - 2^-24 (torch.rand's largest value) on a group's maximum: fma(t, inv, u) rounds up to
+    QMAX + 1 and rint(QMAX + 1/2) is QMAX + 1, so only the clamp keeps the code in range."""
+    rng = np.random.default_rng(8)
+    for bits in (1, 2, 4, 8):
+        qmax = (1 << bits) - 1
+        x = rng.standard_normal((64, 128)).astype(np.float32)
+        u = rng.random((64, 128), dtype=np.float32)
+        imax = x.argmax(axis=1)
+        u[np.arange(64), imax] = np.float32(1 - 2 ** -24)
+        p, s, m = oracle.quant_pack(x, 128, bits, rounding=NOISE, noise=u)
+        codes = oracle.unpack_codes(p, 128, bits).view(np.uint8 if bits == 8 else np.int8).astype(np.int64)
+        assert (codes[np.arange(64), imax] == qmax).all()
+        # the case is real: before the clamp a good share of these maxima round to QMAX + 1
+        inv = (np.float32(1) / s).astype(np.float32)
+        t = (x[np.arange(64), imax] - m).astype(np.float32)
+        pre = np.rint((fma32(t, inv, u[np.arange(64), imax]) - np.float32(0.5)).astype(np.float32))
+        assert (pre == qmax + 1).mean() > 0.3
+        np.testing.assert_array_equal(p, numpy_quant(x, bits, NOISE, u)[0])
