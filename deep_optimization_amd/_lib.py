@@ -37,6 +37,7 @@ EXPORTS = (
     "dopt_bn_reduce",
     "dopt_bn_norm_quant",
     "dopt_bn_train_forward",
+    "dopt_bn_train_forward_noalloc",
     "dopt_bn_train_backward",
     "dopt_bn_bwd_reduce",
     "dopt_bn_bwd_dx",
@@ -103,6 +104,9 @@ def lib() -> ctypes.CDLL:
         L.dopt_bn_train_forward.argtypes = [vp, i32, i64, i64, i64, i64, i64, vp, vp, vp, f32, i32, i32, i32,
                                             vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, f32, vp]
         L.dopt_bn_train_forward.restype = i32
+        L.dopt_bn_train_forward_noalloc.argtypes = [vp, i32, i64, i64, i64, i64, i64, vp, vp, f32, i32, i32, i32,
+                                                    vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, f32, vp]
+        L.dopt_bn_train_forward_noalloc.restype = i32
         # mode, packed, relu_packed, scale, min, dy, dy_dt, N, C, HW, stride_n, stride_c, group, bits, workspace,
         # weight, var, eps, dweight, dbias, dx, stream
         L.dopt_bn_train_backward.argtypes = [i32, vp, vp, vp, vp, vp, i32, i64, i64, i64, i64, i64, i32, i32, vp,

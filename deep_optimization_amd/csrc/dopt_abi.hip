@@ -3,6 +3,7 @@
 // frees or synchronises; all work is enqueued on the caller's stream.
 #include <stdarg.h>
 #include <initializer_list>
+#include <mutex>
 #include <stdio.h>
 
 #include "../../include/dopt.h"
@@ -142,6 +143,34 @@ int bn_quant_checks(int mode, int64_t M, int group_size, int bits, const void* p
     if (!packed || !scale || !minv) return fail(DOPT_EINVAL, "null packed/scale/min pointer");
     if ((uintptr_t)packed & 7u) return fail(DOPT_EINVAL, "packed must be 8-byte aligned");
     if (mode != DOPT_BN_QUANT && !relu_packed) return fail(DOPT_EINVAL, "null relu_packed pointer");
+    return DOPT_OK;
+}
+
+// Static per-device scratch of dopt_bn_train_forward_noalloc: the statistics kernel's workgroup
+// partials, which the normalize kernel sums. Each partial slot is written before it is read in
+// the same call, so nothing needs clearing between calls. In host code `scratch` is only a
+// host-side handle: kernels get the device address that hipGetSymbolAddress returns for the
+// current device, looked up on the entry point's first call on that device and kept.
+static __device__ __align__(256) float scratch[DOPT_BN_SCRATCH_FLOATS];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+float* g_scratch_ptr[kMaxDevices] = {};
+
+int scratch_of_current_device(float** out) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return fail(DOPT_EHIP, "hipGetDevice: %s", hipGetErrorString(e));
+    if (dev < 0 || dev >= kMaxDevices) return fail(DOPT_EINVAL, "device index %d beyond %d", dev, kMaxDevices);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p)
+            return fail(DOPT_EHIP, "hipGetSymbolAddress(scratch) on device %d: %s", dev, hipGetErrorString(e));
+        g_scratch_ptr[dev] = (float*)p;
+    }
+    *out = g_scratch_ptr[dev];
     return DOPT_OK;
 }
 
@@ -460,20 +489,36 @@ int dopt_bn_norm_quant(const void* x, int x_dtype, int64_t N, int64_t C, int64_t
     return hip_status("bn_norm_quant launch");
 }
 
-int dopt_bn_train_forward(const void* x, int x_dtype, int64_t N, int64_t C, int64_t HW, int64_t stride_n,
-                          int64_t stride_c, float* workspace, const float* weight, const float* bias, float eps,
-                          int mode, int group_size, int bits, void* y, void* x_hat, uint32_t* packed,
+}  // extern "C"
+
+namespace {
+
+// dopt_bn_train_forward with the workspace either the caller's (noalloc = false) or this device's
+// static scratch (noalloc = true, looked up after the arguments are validated).
+int bn_train_forward_impl(bool noalloc, const void* x, int x_dtype, int64_t N, int64_t C, int64_t HW,
+                          int64_t stride_n, int64_t stride_c, float* workspace, const float* weight, const float* bias,
+                          float eps, int mode, int group_size, int bits, void* y, void* x_hat, uint32_t* packed,
                           uint32_t* relu_packed, void* scale, void* minv, float* mean_out, float* var_out,
                           float* running_mean, float* running_var, float momentum, void* stream) {
     int rc;
+    const char* name = noalloc ? "bn_train_forward_noalloc" : "bn_train_forward";
     dopt::BnGeom g;
     if ((rc = bn_geom(N, C, HW, stride_n, stride_c, &g))) return rc;
-    if ((rc = bn_dtype(x_dtype, "bn_train_forward: x"))) return rc;
+    if ((rc = bn_dtype(x_dtype, noalloc ? "bn_train_forward_noalloc: x" : "bn_train_forward: x"))) return rc;
     const int64_t M = N * HW;
     if ((rc = bn_quant_checks(mode, M, group_size, bits, packed, scale, minv, relu_packed))) return rc;
+    if (noalloc) {
+        const int64_t need = 2 * C * dopt::bn_nchunks(M);
+        if (need > DOPT_BN_SCRATCH_FLOATS)
+            return fail(DOPT_EINVAL,
+                        "%s: N=%lld C=%lld HW=%lld needs %lld floats of scratch, more than the %d the static "
+                        "scratch holds (use dopt_bn_train_forward with a workspace)",
+                        name, (long long)N, (long long)C, (long long)HW, (long long)need, DOPT_BN_SCRATCH_FLOATS);
+    }
     if (C == 0 || M == 0) return ok();
-    if (!x || !y || !weight || !bias || !mean_out || !var_out || !workspace)
-        return fail(DOPT_EINVAL, "null pointer argument");
+    if (!x || !y || !weight || !bias || !mean_out || !var_out || (!noalloc && !workspace))
+        return fail(DOPT_EINVAL, "%s: null pointer argument", name);
+    if (noalloc && (rc = scratch_of_current_device(&workspace))) return rc;
     if (mode == DOPT_BN_NORM && !x_hat) return fail(DOPT_EINVAL, "null x_hat pointer");
     const int vw = bn_width(g, {{x, bn_bytes(x_dtype)}, {y, 2}, {x_hat, 2}});
     (void)hipGetLastError();
@@ -502,7 +547,31 @@ int dopt_bn_train_forward(const void* x, int x_dtype, int64_t N, int64_t C, int6
     a.run_mom = momentum;
     a.run_keep = (float)(1.0 - (double)momentum);
     dopt::launch_bn_fwd(a, x_dtype, mode, group_size, bits, vw, (hipStream_t)stream);
-    return hip_status("bn_train_forward launch");
+    return hip_status(noalloc ? "bn_train_forward_noalloc launch" : "bn_train_forward launch");
+}
+
+}  // namespace
+
+extern "C" {
+
+int dopt_bn_train_forward(const void* x, int x_dtype, int64_t N, int64_t C, int64_t HW, int64_t stride_n,
+                          int64_t stride_c, float* workspace, const float* weight, const float* bias, float eps,
+                          int mode, int group_size, int bits, void* y, void* x_hat, uint32_t* packed,
+                          uint32_t* relu_packed, void* scale, void* minv, float* mean_out, float* var_out,
+                          float* running_mean, float* running_var, float momentum, void* stream) {
+    return bn_train_forward_impl(false, x, x_dtype, N, C, HW, stride_n, stride_c, workspace, weight, bias, eps, mode,
+                                 group_size, bits, y, x_hat, packed, relu_packed, scale, minv, mean_out, var_out,
+                                 running_mean, running_var, momentum, stream);
+}
+
+int dopt_bn_train_forward_noalloc(const void* x, int x_dtype, int64_t N, int64_t C, int64_t HW, int64_t stride_n,
+                                  int64_t stride_c, const float* weight, const float* bias, float eps, int mode,
+                                  int group_size, int bits, void* y, void* x_hat, uint32_t* packed,
+                                  uint32_t* relu_packed, void* scale, void* minv, float* mean_out, float* var_out,
+                                  float* running_mean, float* running_var, float momentum, void* stream) {
+    return bn_train_forward_impl(true, x, x_dtype, N, C, HW, stride_n, stride_c, nullptr, weight, bias, eps, mode,
+                                 group_size, bits, y, x_hat, packed, relu_packed, scale, minv, mean_out, var_out,
+                                 running_mean, running_var, momentum, stream);
 }
 
 int dopt_bn_train_backward(int mode, const uint32_t* packed, const uint32_t* relu_packed, const void* scale,

@@ -240,6 +240,21 @@ int dopt_bn_train_forward(const void* x, int x_dtype, int64_t N, int64_t C, int6
                           uint32_t* relu_packed, void* scale, void* minv, float* mean_out, float* var_out,
                           float* running_mean, float* running_var, float momentum, void* stream);
 
+/* No counterpart in the reference. dopt_bn_train_forward for callers that cannot allocate device
+ * memory (code under HIP graph capture that may not call hipMalloc, tight serving loops, harnesses
+ * that forbid allocation): the same arguments without `workspace`, the same outputs bit for bit.
+ * The statistics kernel's partials go to a static per-device scratch array of
+ * DOPT_BN_SCRATCH_FLOATS floats (4 MiB, held on each GPU the library runs on until the process
+ * ends); a shape with dopt_bn_workspace_floats(N, C, HW) > DOPT_BN_SCRATCH_FLOATS returns
+ * DOPT_EINVAL. No allocation of any kind. Every call on one GPU shares that GPU's scratch, so calls
+ * that overlap on one GPU (e.g. on two streams at once) race; calls ordered on one stream do not. */
+#define DOPT_BN_SCRATCH_FLOATS (1 << 20)
+int dopt_bn_train_forward_noalloc(const void* x, int x_dtype, int64_t N, int64_t C, int64_t HW, int64_t stride_n,
+                                  int64_t stride_c, const float* weight, const float* bias, float eps, int mode,
+                                  int group_size, int bits, void* y, void* x_hat, uint32_t* packed,
+                                  uint32_t* relu_packed, void* scale, void* minv, float* mean_out, float* var_out,
+                                  float* running_mean, float* running_var, float momentum, void* stream);
+
 /* The backward of that layer in one call (quantized modes): the reduce kernel's partials into
  * workspace, then the dx kernel, which sums them (bit-identical to dopt_bn_bwd_reduce's dweight /
  * dbias), writes dweight / dbias and dx. Replaces the act_lib::bn_bwd_reduce_dequant_unpack_fused +

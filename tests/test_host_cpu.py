@@ -100,6 +100,17 @@ class TestValidationWithoutDevice:
         assert L.dopt_pack_codes(16, 4, 64, 5, 16, None) == _lib.EBITS
         assert L.dopt_unpack_codes(16, 4, 48, 2, 16, None) == _lib.EINVAL
 
+    def test_bn_noalloc_rejects_shapes_beyond_the_scratch(self):
+        L = _lib.lib()
+        N, C, HW = 1024, 2048, 56 * 56  # 2 * 2048 * 392 partials: more than the 2^20 floats of scratch
+        assert L.dopt_bn_workspace_floats(N, C, HW) > (1 << 20)
+        assert L.dopt_bn_workspace_floats(128, C, HW) <= (1 << 20)
+        rc = L.dopt_bn_train_forward_noalloc(16, _lib.BF16, N, C, HW, C * HW, HW, 16, 16, 1e-5, _lib.BN_QUANT, 256, 2,
+                                             16, None, 16, None, 16, 16, 16, 16, None, None, 0.1, None)
+        assert rc == _lib.EINVAL
+        msg = L.dopt_last_error().decode()
+        assert "scratch" in msg and "1048576" in msg, msg
+
     def test_gemm_shape_checks(self):
         L = _lib.lib()
         assert L.dopt_fp8_gemm_nt(16, 16, 100, 256, 128, 128, 128, 1.0, 16, 256, None) == _lib.EUNSUPPORTED
