@@ -300,14 +300,21 @@ int dopt_fp8_gemm_nt(const uint8_t* A, const uint8_t* B, int64_t M, int64_t N, i
                      float out_scale, void* C, int64_t ldc, void* stream) {
     if (M < 0 || N < 0 || K < 0) return fail(DOPT_EINVAL, "negative GEMM extent");
     if (M == 0 || N == 0) return ok();
-    if (!A || !B || !C) return fail(DOPT_EINVAL, "null pointer argument");
-    if (M % 256 || N % 256 || K % 128 || K == 0)
-        return fail(DOPT_EUNSUPPORTED,
-                    "fp8 GEMM needs M %% 256 == 0, N %% 256 == 0, K %% 128 == 0 and K > 0 (got %lld, %lld, %lld)",
-                    (long long)M, (long long)N, (long long)K);
-    if (lda < K || ldb < K || ldc < N || lda % 16 || ldb % 16 || ldc % 8 || !aligned16(A) || !aligned16(B) ||
-        !aligned16(C))
-        return fail(DOPT_EINVAL, "fp8 GEMM needs 16-byte aligned rows with lda, ldb >= K and ldc >= N");
+    if (!C || (K > 0 && (!A || !B))) return fail(DOPT_EINVAL, "null pointer argument");
+    if (K % 16)
+        return fail(DOPT_EUNSUPPORTED, "fp8 GEMM needs K %% 16 == 0 (one 16-byte load per lane), got K=%lld",
+                    (long long)K);
+    if (lda < K || ldb < K || ldc < N || lda % 16 || ldb % 16 || (K > 0 && (!aligned16(A) || !aligned16(B))) ||
+        ((uintptr_t)C & 1))
+        return fail(DOPT_EINVAL,
+                    "fp8 GEMM needs 16-byte aligned A and B, lda and ldb multiples of 16 and >= K, a 2-byte aligned C "
+                    "and ldc >= N (got lda=%lld ldb=%lld ldc=%lld K=%lld N=%lld)",
+                    (long long)lda, (long long)ldb, (long long)ldc, (long long)K, (long long)N);
+    if (lda > (1 << 23) || ldb > (1 << 23))
+        return fail(DOPT_EINVAL, "fp8 GEMM row strides must be at most 2^23 bytes (32-bit tile offsets), got %lld, %lld",
+                    (long long)lda, (long long)ldb);
+    if ((M + 255) / 256 * ((N + 255) / 256) >= ((int64_t)1 << 31))
+        return fail(DOPT_EINVAL, "fp8 GEMM output too large: %lld x %lld", (long long)M, (long long)N);
     (void)hipGetLastError();
     const int rc = dopt::launch_fp8_gemm_nt(A, B, M, N, K, lda, ldb, out_scale, (uint16_t*)C, ldc, (hipStream_t)stream);
     if (rc) return fail(DOPT_EUNSUPPORTED, "fp8 GEMM launch configuration unsupported");

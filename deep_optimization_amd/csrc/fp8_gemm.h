@@ -1,5 +1,6 @@
 // FP8 (OCP e4m3) scaled GEMM on CDNA4 MFMA, NT layout (A [M,K], B [N,K], both K-contiguous):
 //   C[m][n] = bf16(out_scale * sum_k A[m][k] * B[n][k]), fp32 accumulation, one rounding.
+// Any M, N >= 0; K a multiple of 16 (one 16-byte load per lane); A, B rows 16-byte aligned.
 //
 // Tiling: a workgroup of 4 waves (2 x 2) computes a BM x BN tile; each wave a (BM/2) x (BN/2)
 // sub-tile as TM x TN blocks of v_mfma_f32_32x32x64_f8f6f4 (fp8 x fp8 -> fp32, 32 x 32 x 64 per
@@ -7,13 +8,17 @@
 // is 32 MFMAs fed by 16 KB of LDS operand reads per wave, half the LDS bandwidth of a CU.
 //
 // Data movement: K advances in slabs of BK = 128 bytes, double-buffered in LDS (no padding:
-// 2 * (BM + BN) * 128 bytes). Slabs go HBM/L2 -> LDS with global_load_lds_dwordx4 (no staging
-// registers): one instruction moves 64 lanes x 16 bytes into a contiguous 1 KB LDS block, i.e.
-// 8 rows of 128 bytes. The lane -> global address mapping applies an XOR swizzle, so 16-byte
-// chunk c of row r lands at chunk position c ^ ((r / 2) % 8). gfx950's LDS serves a
-// ds_read_b128 16 lanes at a time across 64 banks (256 bytes): an even and an odd row share one
-// bank row, so the 16 consecutive rows of an operand fetch hit 16 distinct 16-byte bank groups
-// (measured: the plain c ^ (r % 8) swizzle left half of all LDS cycles in bank conflicts).
+// 2 * (BM + BN) * 128 bytes). Slabs go HBM/L2 -> LDS with buffer_load_dwordx4 ... lds (no
+// staging registers): one instruction moves 64 lanes x 16 bytes into a contiguous 1 KB LDS
+// block, i.e. 8 rows of 128 bytes (whole cache lines). The lane -> global address mapping
+// applies an XOR swizzle, so 16-byte chunk c of row r lands at chunk position c ^ ((r / 2) % 8).
+// gfx950's LDS serves a ds_read_b128 16 lanes at a time across 64 banks (256 bytes): an even
+// and an odd row share one bank row, so the 16 consecutive rows of an operand fetch hit 16
+// distinct 16-byte bank groups (measured: the plain c ^ (r % 8) swizzle left half of all LDS
+// cycles in bank conflicts). The loads go through a range-checked buffer resource: a lane whose
+// row lies beyond M (or N) or whose 16 bytes lie beyond K gets an offset past the resource's
+// range, which the hardware turns into zeros without a memory access, so edge tiles need no
+// other masking until the stores, and slabs past the end load nothing.
 //
 // Pipeline (one barrier per slab, placed mid-slab):
 //   MFMAs of half 0 | ds_read operands of half 1 | wait LDS reads + slab k+1 loads | barrier |
@@ -25,7 +30,8 @@
 // consecutive K bytes starting at 32*(l / 32); A and B use the same K mapping, so the dot
 // products pair matching k. Accumulator layout: lane l holds column l % 32 and, in register v,
 // row 8*(v/4) + 4*(l/32) + (v%4). The epilogue scales, rounds to bf16, transposes through LDS
-// and writes 16-byte row chunks.
+// and writes 16-byte row chunks inside M x N (element stores for a ragged last chunk or an
+// unaligned C).
 //
 // Workgroup order: the hardware hands consecutive workgroup ids to the 8 XCDs in turn, each XCD
 // with its own L2. The id is remapped so that each XCD owns a contiguous range of tiles, walked
@@ -35,6 +41,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "dopt_device.h"
 
 namespace dopt {
@@ -42,7 +50,6 @@ namespace dopt {
 typedef int v8i_t __attribute__((ext_vector_type(8)));
 typedef float v16f_t __attribute__((ext_vector_type(16)));
 typedef __attribute__((address_space(3))) void lds_void_t;
-typedef __attribute__((address_space(1))) const void gbl_void_t;
 
 __device__ __forceinline__ v16f_t mfma_fp8_32x32x64(const v8i_t& a, const v8i_t& b, const v16f_t& c) {
     // cbsz = blgp = 0: both operands OCP fp8 e4m3; scale operands 0 select the unscaled MFMA.
@@ -50,6 +57,18 @@ __device__ __forceinline__ v16f_t mfma_fp8_32x32x64(const v8i_t& a, const v8i_t&
 }
 
 constexpr int GEMM_XCDS = 8;
+constexpr uint32_t GEMM_OOB = 0x80000000u;    // buffer offset past the range: the load returns zeros
+constexpr uint32_t GEMM_RANGE = 0x7FFFFF00u;  // num_records of the operand resources
+
+struct Fp8GemmArgs {
+    const uint8_t* A;
+    const uint8_t* B;
+    uint16_t* C;
+    int64_t M, N, K, lda, ldb, ldc;
+    float out_scale;
+    uint32_t tiles_m, tiles_n;
+    uint32_t vec_store;  // C 16-byte aligned with ldc % 8 == 0: whole chunks go out as 16-byte stores
+};
 
 template <int BM_, int BN_, int GROUP_M_, int SCHED_ = 1>
 struct Fp8GemmCfg {
@@ -65,11 +84,10 @@ struct Fp8GemmCfg {
     static_assert(LDS_BYTES <= 160 * 1024, "LDS budget of one CU");
 };
 
-template <class C>
-__global__ __launch_bounds__(256, 1) void fp8_gemm_nt_kernel(const uint8_t* __restrict__ A, const uint8_t* __restrict__ B,
-                                                            uint16_t* __restrict__ Cm, int64_t M, int64_t N, int64_t K,
-                                                            int64_t lda, int64_t ldb, int64_t ldc, float out_scale) {
+template <class C, bool EDGE>
+__global__ __launch_bounds__(256, 1) void fp8_gemm_nt_kernel(Fp8GemmArgs p) {
     constexpr int BM = C::BM, BN = C::BN, BK = C::BK, TM = C::TM, TN = C::TN, WM = C::WM, WN = C::WN;
+    const int64_t M = p.M, N = p.N, K = p.K, lda = p.lda, ldb = p.ldb, ldc = p.ldc;
     // four separate LDS objects (A and B, two buffers each): the compiler can then prove that an
     // operand read of one buffer does not alias the in-flight global_load_lds writes into the
     // other, and does not make the read wait for those loads
@@ -80,7 +98,7 @@ __global__ __launch_bounds__(256, 1) void fp8_gemm_nt_kernel(const uint8_t* __re
 
     // ---- XCD-aware tile order: XCD x receives ids x, x+8, x+16, ... (local index bid/8) and
     // owns the contiguous tile range [x*per + min(x, rem), ... + per + (x < rem)), a bijection
-    const uint32_t tiles_m = (uint32_t)(M / BM), tiles_n = (uint32_t)(N / BN);
+    const uint32_t tiles_m = p.tiles_m, tiles_n = p.tiles_n;
     const uint32_t n_tiles = tiles_m * tiles_n;
     const uint32_t bid = blockIdx.x;
     const uint32_t xcd = bid % GEMM_XCDS, local = bid / GEMM_XCDS;
@@ -105,17 +123,36 @@ __global__ __launch_bounds__(256, 1) void fp8_gemm_nt_kernel(const uint8_t* __re
     // where (r/2) % 8 = (4*(w % 2) + lane/16) % 8 does not depend on j
     const int lrow8 = lane >> 3;
     const int lchunk = (lane & 7) ^ ((4 * (wave & 1) + (lane >> 4)) & 7);
-    const uint8_t* ga = A + (m0 + 8 * wave + lrow8) * lda + lchunk * 16;
-    const uint8_t* gb = B + (n0 + 8 * wave + lrow8) * ldb + lchunk * 16;
-    auto issue = [&](uint8_t* sa, uint8_t* sb, int64_t k0) {
+    const __amdgpu_buffer_rsrc_t ra =
+        __builtin_amdgcn_make_buffer_rsrc((void*)(p.A + m0 * lda), (short)0, (int)GEMM_RANGE, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rb =
+        __builtin_amdgcn_make_buffer_rsrc((void*)(p.B + n0 * ldb), (short)0, (int)GEMM_RANGE, 0x00020000);
+    const int r0 = 8 * wave + lrow8;  // row of instruction j: 32 j + r0
+    const int rows_a = (int)min((int64_t)BM, M - m0) - r0, rows_b = (int)min((int64_t)BN, N - n0) - r0;
+    const uint32_t offa0 = (uint32_t)(r0 * lda + lchunk * 16), offb0 = (uint32_t)(r0 * ldb + lchunk * 16);
+    const uint32_t stepa = (uint32_t)(32 * lda), stepb = (uint32_t)(32 * ldb);
+    // EDGE = false (M, N multiples of the tile and K of BK, the common case): only the slabs past
+    // K are out of range, a wave-uniform test. EDGE = true: lanes past K and rows past M (N) get
+    // GEMM_OOB (selects, no branches; about 2% slower at 8192^3).
+    auto issue = [&](uint8_t* sa, uint8_t* sb, int64_t k0, auto edge) __attribute__((always_inline)) {
+        constexpr bool E = decltype(edge)::value;
+        int la = C::BM, lb = C::BN;
+        if constexpr (E) {
+            const bool k_ok = k0 + lchunk * 16 < K;
+            la = k_ok ? rows_a : 0;
+            lb = k_ok ? rows_b : 0;
+        }
+        const uint32_t kk = k0 < K ? (uint32_t)k0 : GEMM_OOB;
 #pragma unroll
         for (int j = 0; j < C::LA; ++j)
-            __builtin_amdgcn_global_load_lds((gbl_void_t*)(ga + (int64_t)(32 * j) * lda + k0),
-                                             (lds_void_t*)(sa + wave * 1024 + j * 4096), 16, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_void_t*)(sa + wave * 1024 + j * 4096), 16,
+                                                     !E || 32 * j < la ? offa0 + j * stepa + kk : GEMM_OOB, 0, 0,
+                                                     0);
 #pragma unroll
         for (int j = 0; j < C::LB; ++j)
-            __builtin_amdgcn_global_load_lds((gbl_void_t*)(gb + (int64_t)(32 * j) * ldb + k0),
-                                             (lds_void_t*)(sb + wave * 1024 + j * 4096), 16, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_void_t*)(sb + wave * 1024 + j * 4096), 16,
+                                                     !E || 32 * j < lb ? offb0 + j * stepb + kk : GEMM_OOB, 0, 0,
+                                                     0);
     };
 
     // ---- operand reads: tile i of the wave = rows base + i*32 + lane%32; K half h of the slab
@@ -123,7 +160,7 @@ __global__ __launch_bounds__(256, 1) void fp8_gemm_nt_kernel(const uint8_t* __re
     const int orow = lane & 31;
     const int oc = 2 * (lane >> 5);
     const int sw = (lane >> 1) & 7;  // (row/2) % 8 of this lane's operand rows (base rows are multiples of 16)
-    auto read_ops = [&](const uint8_t* sa, const uint8_t* sb, int h, v8i_t* a, v8i_t* b) {
+    auto read_ops = [&](const uint8_t* sa, const uint8_t* sb, int h, v8i_t* a, v8i_t* b) __attribute__((always_inline)) {
         const uint8_t* la = sa + (WM * wm + orow) * BK;
         const uint8_t* lb = sb + (WN * wn + orow) * BK;
         const int p0 = ((4 * h + oc) ^ sw) * 16, p1 = ((4 * h + oc + 1) ^ sw) * 16;
@@ -150,7 +187,7 @@ __global__ __launch_bounds__(256, 1) void fp8_gemm_nt_kernel(const uint8_t* __re
             for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
 
     v8i_t a0[TM], b0[TN], a1[TM], b1[TN];
-    auto mma = [&](const v8i_t* a, const v8i_t* b) {
+    auto mma = [&](const v8i_t* a, const v8i_t* b) __attribute__((always_inline)) {
 #pragma unroll
         for (int i = 0; i < TM; ++i)
 #pragma unroll
@@ -158,12 +195,12 @@ __global__ __launch_bounds__(256, 1) void fp8_gemm_nt_kernel(const uint8_t* __re
     };
     // one slab: (sa, sb) hold slab kt, (na, nb) slab kt+1 (loads in flight), half 0 operands of
     // slab kt already in a0/b0. The body is branch-free: the last two slabs still issue a load
-    // (of the final slab again, an L2 hit, into a buffer nobody reads any more) and read the next
-    // buffer's half 0 (unused), so every slab is one scheduling region pair. The
+    // (past K: every lane out of range, so zeros into a buffer nobody reads any more) and read
+    // the next buffer's half 0 (unused), so every slab is one scheduling region pair. The
     // sched_group_barrier hints interleave one MFMA with the LDS reads / global loads that run
     // beside it, so the in-order issue never parks a memory instruction behind a run of MFMAs.
-    const int nk = (int)(K / BK);
-    auto slab = [&](int kt, uint8_t* sa, uint8_t* sb, uint8_t* na, uint8_t* nb) {
+    const int nk = (int)((K + BK - 1) / BK);
+    auto slab = [&](int kt, uint8_t* sa, uint8_t* sb, uint8_t* na, uint8_t* nb, auto edge) __attribute__((always_inline)) {
         constexpr int NM = TM * TN;        // MFMAs per half slab
         constexpr int NR = 2 * (TM + TN);  // ds_read_b128 per half slab
         read_ops(sa, sb, 1, a1, b1);
@@ -187,7 +224,7 @@ __global__ __launch_bounds__(256, 1) void fp8_gemm_nt_kernel(const uint8_t* __re
         // every LDS read of (sa, sb) and every load of slab kt+1 has landed, in all waves
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
-        issue(sa, sb, (int64_t)min(kt + 2, nk - 1) * BK);
+        issue(sa, sb, (int64_t)(kt + 2) * BK, edge);
         read_ops(na, nb, 0, a0, b0);
         mma(a1, b1);
         if constexpr (C::SCHED == 0) {
@@ -213,17 +250,18 @@ __global__ __launch_bounds__(256, 1) void fp8_gemm_nt_kernel(const uint8_t* __re
         }
     };
 
-    issue(sA0, sB0, 0);
+    const std::integral_constant<bool, EDGE> edge{};
+    issue(sA0, sB0, 0, edge);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    issue(sA1, sB1, (int64_t)min(1, nk - 1) * BK);
+    issue(sA1, sB1, (int64_t)BK, edge);
     read_ops(sA0, sB0, 0, a0, b0);
     int kt = 0;
     for (; kt + 1 < nk; kt += 2) {
-        slab(kt, sA0, sB0, sA1, sB1);
-        slab(kt + 1, sA1, sB1, sA0, sB0);
+        slab(kt, sA0, sB0, sA1, sB1, edge);
+        slab(kt + 1, sA1, sB1, sA0, sB0, edge);
     }
-    if (kt < nk) slab(kt, sA0, sB0, sA1, sB1);
+    if (kt < nk) slab(kt, sA0, sB0, sA1, sB1, edge);
     // the trailing loads must land before LDS is reused below
     __builtin_amdgcn_s_waitcnt(0);
 
@@ -239,28 +277,38 @@ __global__ __launch_bounds__(256, 1) void fp8_gemm_nt_kernel(const uint8_t* __re
 #pragma unroll
             for (int v = 0; v < 16; ++v) {
                 const int row = i * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
-                tile[row * WN + col] = to_bf16(acc[i][j][v] * out_scale);
+                tile[row * WN + col] = to_bf16(acc[i][j][v] * p.out_scale);
             }
         }
     __builtin_amdgcn_s_waitcnt(0);
     __builtin_amdgcn_wave_barrier();
     constexpr int CPR = WN / 8;  // 16-byte chunks per tile row
-    uint16_t* cbase = Cm + (m0 + WM * wm) * ldc + n0 + WN * wn;
+    const int64_t row0 = m0 + WM * wm, col0 = n0 + WN * wn;
+    uint16_t* cbase = p.C + row0 * ldc + col0;
 #pragma unroll 4
     for (int q = lane; q < WM * CPR; q += 64) {
         const int row = q / CPR, c = q % CPR;
-        *(uint4*)(cbase + row * ldc + c * 8) = *(const uint4*)(tile + row * WN + c * 8);
+        if (row0 + row >= M) continue;
+        const int64_t n = col0 + c * 8;
+        if (p.vec_store && n + 8 <= N) {
+            *(uint4*)(cbase + row * ldc + c * 8) = *(const uint4*)(tile + row * WN + c * 8);
+        } else {
+            for (int e = 0; e < 8 && n + e < N; ++e) cbase[row * ldc + c * 8 + e] = tile[row * WN + c * 8 + e];
+        }
     }
 }
 
 template <class C>
 inline int fp8_gemm_launch(const uint8_t* A, const uint8_t* B, int64_t M, int64_t N, int64_t K, int64_t lda,
                            int64_t ldb, float out_scale, uint16_t* Cm, int64_t ldc, hipStream_t s) {
-    if (M % C::BM || N % C::BN || K % C::BK) return -1;
-    const int64_t tiles = (M / C::BM) * (N / C::BN);
-    if (tiles == 0 || K == 0) return tiles == 0 ? 0 : -1;
-    hipLaunchKernelGGL(fp8_gemm_nt_kernel<C>, dim3((uint32_t)tiles), dim3(C::THREADS), 0, s, A, B, Cm, M, N, K, lda,
-                       ldb, ldc, out_scale);
+    Fp8GemmArgs p{A, B, Cm, M, N, K, lda, ldb, ldc, out_scale, (uint32_t)((M + C::BM - 1) / C::BM),
+                  (uint32_t)((N + C::BN - 1) / C::BN), (uint32_t)(ldc % 8 == 0 && ((uintptr_t)Cm & 15) == 0)};
+    const uint64_t tiles = (uint64_t)p.tiles_m * p.tiles_n;
+    if (tiles == 0) return 0;
+    if (M % C::BM == 0 && N % C::BN == 0 && K % C::BK == 0)
+        hipLaunchKernelGGL((fp8_gemm_nt_kernel<C, false>), dim3((uint32_t)tiles), dim3(C::THREADS), 0, s, p);
+    else
+        hipLaunchKernelGGL((fp8_gemm_nt_kernel<C, true>), dim3((uint32_t)tiles), dim3(C::THREADS), 0, s, p);
     return 0;
 }
 

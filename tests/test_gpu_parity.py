@@ -463,9 +463,52 @@ def test_fp8_gemm_parity(M, N, K):
     assert bool(((c.float() - ref).abs() <= ref.abs() * 2 ** -7 + 1e-3 * ref.abs().max()).all())
 
 
+@pytest.mark.parametrize("M,N,K", [(1, 1, 16), (100, 300, 48), (257, 255, 144), (1000, 777, 1040), (33, 4099, 2064),
+                                   (4095, 4097, 4112), (300, 200, 0)])
+def test_fp8_gemm_ragged_shapes(M, N, K):
+    """Edge tiles (M, N not multiples of 256, K a multiple of 16 but not of 64; K = 0 gives zeros),
+    through the C ABI with padded row strides: lda, ldb > K, ldc > N (odd, so element stores), and a
+    sentinel around the M x N block of C that must stay untouched."""
+    gen = torch.Generator(device=DEV).manual_seed(M * 7 + N + K)
+    lda, ldb, ldc = K + 32, K + 48, N + 3
+    a_buf = torch.randn(M, lda, generator=gen, device=DEV)
+    b_buf = torch.randn(N, ldb, generator=gen, device=DEV)
+    a8 = (a_buf * 40).clamp(-448, 448).to(torch.float8_e4m3fn)
+    b8 = (b_buf * 40).clamp(-448, 448).to(torch.float8_e4m3fn)
+    # the padding columns hold NaN encodings: a kernel that read past K would turn rows NaN
+    a8.view(torch.uint8)[:, K:] = 0x7F
+    b8.view(torch.uint8)[:, K:] = 0xFF
+    c = torch.full((M + 2, ldc), 77.0, dtype=torch.bfloat16, device=DEV)
+    out_scale = 1.0 / 1600.0
+    rc = _lib.lib().dopt_fp8_gemm_nt(a8.data_ptr(), b8.data_ptr(), M, N, K, lda, ldb, out_scale, c.data_ptr(), ldc,
+                                     torch.cuda.current_stream().cuda_stream)
+    _lib.check(rc, "fp8_gemm_nt")
+    torch.cuda.synchronize()
+    ref = (a8[:, :K].float() @ b8[:, :K].float().t()) * out_scale
+    got = c[:M, :N].float()
+    assert bool(torch.isfinite(got).all())
+    if K == 0:
+        assert bool((got == 0).all())
+    else:
+        rel = float((got - ref).norm() / ref.norm())
+        assert rel <= 1e-2, rel
+        assert bool(((got - ref).abs() <= ref.abs() * 2 ** -7 + 1e-3 * ref.abs().max()).all())
+    assert bool((c[:M, N:] == 77.0).all()) and bool((c[M:] == 77.0).all())
+
+
+def test_fp8_gemm_operator_odd_n():
+    """act_lib::fp8_gemm_nt with N % 8 != 0 (ldc = N: element stores) equals the fp32 matmul."""
+    gen = torch.Generator(device=DEV).manual_seed(3)
+    a8, sa = fp8_quantize(torch.randn(130, 96, generator=gen, device=DEV))
+    b8, sb = fp8_quantize(torch.randn(67, 96, generator=gen, device=DEV))
+    c = torch.ops.act_lib.fp8_gemm_nt(a8, b8, float(1.0 / (sa * sb)))
+    ref = (a8.float() @ b8.float().t()) / (sa * sb)
+    assert float((c.float() - ref).norm() / ref.norm()) <= 1e-2
+
+
 def test_fp8_gemm_rejects_bad_shapes():
-    a = torch.zeros(100, 128, dtype=torch.float8_e4m3fn, device=DEV)
-    b = torch.zeros(256, 128, dtype=torch.float8_e4m3fn, device=DEV)
+    a = torch.zeros(100, 120, dtype=torch.float8_e4m3fn, device=DEV)
+    b = torch.zeros(256, 120, dtype=torch.float8_e4m3fn, device=DEV)
     with pytest.raises(RuntimeError, match="fp8 GEMM"):
         torch.ops.act_lib.fp8_gemm_nt(a, b, 1.0)
 

@@ -113,8 +113,12 @@ class TestValidationWithoutDevice:
 
     def test_gemm_shape_checks(self):
         L = _lib.lib()
-        assert L.dopt_fp8_gemm_nt(16, 16, 100, 256, 128, 128, 128, 1.0, 16, 256, None) == _lib.EUNSUPPORTED
-        assert L.dopt_fp8_gemm_nt(16, 16, 256, 256, 128, 64, 128, 1.0, 16, 256, None) == _lib.EINVAL
+        assert L.dopt_fp8_gemm_nt(16, 16, 100, 256, 120, 128, 128, 1.0, 16, 256, None) == _lib.EUNSUPPORTED  # K % 16
+        assert L.dopt_fp8_gemm_nt(16, 16, 256, 256, 128, 64, 128, 1.0, 16, 256, None) == _lib.EINVAL  # lda < K
+        assert L.dopt_fp8_gemm_nt(16, 16, 256, 256, 128, 136, 128, 1.0, 16, 256, None) == _lib.EINVAL  # lda % 16
+        assert L.dopt_fp8_gemm_nt(8, 16, 256, 256, 128, 128, 128, 1.0, 16, 256, None) == _lib.EINVAL  # A unaligned
+        assert L.dopt_fp8_gemm_nt(16, 16, 256, 250, 128, 128, 128, 1.0, 16, 249, None) == _lib.EINVAL  # ldc < N
+        assert L.dopt_fp8_gemm_nt(16, 16, 256, 256, 128, 1 << 24, 128, 1.0, 16, 256, None) == _lib.EINVAL  # lda > 2^23
 
 
 def test_bits_consts_contract():
