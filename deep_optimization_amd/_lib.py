@@ -28,6 +28,7 @@ EXPORTS = (
     "dopt_pack_codes",
     "dopt_unpack_codes",
     "dopt_fp8_gemm_nt",
+    "dopt_fp8_pack_kmajor",
     "dopt_relu_pack",
     "dopt_relu_unpack",
     "dopt_act_forward",
@@ -82,6 +83,8 @@ def lib() -> ctypes.CDLL:
         L.dopt_unpack_codes.restype = i32
         L.dopt_fp8_gemm_nt.argtypes = [vp, vp, i64, i64, i64, i64, i64, f32, vp, i64, vp]
         L.dopt_fp8_gemm_nt.restype = i32
+        L.dopt_fp8_pack_kmajor.argtypes = [vp, i64, i64, i64, i64, vp, i64, vp]
+        L.dopt_fp8_pack_kmajor.restype = i32
         L.dopt_relu_pack.argtypes = [vp, i32, i64, i32, i32, vp, vp, vp]
         L.dopt_relu_pack.restype = i32
         L.dopt_relu_unpack.argtypes = [vp, vp, i32, i64, i32, vp, vp]

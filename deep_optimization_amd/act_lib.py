@@ -371,6 +371,51 @@ fp8_gemm_nt = _op(
     lambda a, b, out_scale: a.new_empty((a.shape[0], b.shape[0]), dtype=torch.bfloat16))
 
 
+def _kmajor(t: Tensor, rows: int, k: int, stride_r: int, stride_k: int, k_pad: int):
+    """(tensor, row stride) of an e4m3 operand as the GEMM reads it: rows K-contiguous, row stride a
+    multiple of 16, 16-byte aligned. Used in place when it already is; otherwise packed by
+    dopt_fp8_pack_kmajor into a fresh [rows, k_pad] buffer whose padding columns are zero."""
+    if stride_k == 1 and k == k_pad and stride_r % 16 == 0 and k <= stride_r <= (1 << 23) and t.data_ptr() % 16 == 0:
+        return t, stride_r
+    out = (torch.zeros if k_pad != k else torch.empty)((rows, k_pad), dtype=torch.uint8, device=t.device)
+    rc = _lib.lib().dopt_fp8_pack_kmajor(t.data_ptr(), rows, k, stride_r, stride_k, out.data_ptr(), k_pad, _stream(t))
+    _lib.check(rc, "fp8_pack_kmajor")
+    return out, k_pad
+
+
+def _fp8_linear(a, b, out_scale):
+    """Triton_Linear's contraction (Activation_Compression/triton_kernel/linear.py:43-95) in e4m3:
+    a [M, K] @ b [K, N] with any strides -> bf16 [M, N] = out_scale * a @ b, fp32 accumulate. The
+    GEMM reads both operands K-contiguous: an operand in another layout (b in its row-major [K, N]
+    layout, a transposed view, unaligned rows, K not a multiple of 16) is first packed by
+    dopt_fp8_pack_kmajor (zero-padding K to a multiple of 16), the rest is read in place."""
+    if a.dtype != torch.float8_e4m3fn or b.dtype != torch.float8_e4m3fn:
+        raise RuntimeError("fp8_linear expects torch.float8_e4m3fn operands")
+    if a.dim() != 2 or b.dim() != 2 or a.shape[1] != b.shape[0]:
+        raise RuntimeError(f"fp8_linear: shapes {tuple(a.shape)} x {tuple(b.shape)} do not contract")
+    _require_cuda(a, b)
+    M, K = a.shape
+    N = b.shape[1]
+    c = torch.empty((M, N), dtype=torch.bfloat16, device=a.device)
+    if M == 0 or N == 0:
+        return c
+    if K == 0:
+        return c.zero_()
+    k_pad = (K + 15) // 16 * 16
+    ta, lda = _kmajor(a.view(torch.uint8), M, K, a.stride(0), a.stride(1), k_pad)
+    tb, ldb = _kmajor(b.view(torch.uint8), N, K, b.stride(1), b.stride(0), k_pad)
+    rc = _lib.lib().dopt_fp8_gemm_nt(ta.data_ptr(), tb.data_ptr(), M, N, k_pad, lda, ldb, float(out_scale),
+                                     c.data_ptr(), N, _stream(a))
+    _lib.check(rc, "fp8_linear")
+    return c
+
+
+fp8_linear = _op(
+    "fp8_linear(Tensor a, Tensor b, float out_scale) -> Tensor",
+    _fp8_linear,
+    lambda a, b, out_scale: a.new_empty((a.shape[0], b.shape[1]), dtype=torch.bfloat16))
+
+
 # --------------------------------------------------------------------------- fused activation layers
 # Reference: Activation_Compression/modules/activations/kernel_registration.py (op names and
 # schemas kept), kernels in kernel_implementation.py. Scale and min are bf16 [N*G] as there.

@@ -24,6 +24,7 @@ SOURCES = [
     "dequant_unpack.hip",
     "pack_codes.hip",
     "fp8_gemm.hip",
+    "fp8_pack.hip",
     "act_fused.hip",
     "bn_fused.hip",
     "dw_gemm.hip",

@@ -17,6 +17,8 @@ int launch_pack_codes(const int8_t* codes, uint32_t* out, uint64_t n_words, int 
 int launch_unpack_codes(const uint32_t* packed, int8_t* codes, uint64_t n_words, int bits, hipStream_t s);
 int launch_fp8_gemm_nt(const uint8_t* A, const uint8_t* B, int64_t M, int64_t N, int64_t K, int64_t lda,
                        int64_t ldb, float out_scale, uint16_t* C, int64_t ldc, hipStream_t s);
+int launch_fp8_pack(const uint8_t* src, int64_t rows, int64_t cols, int64_t stride_r, int64_t stride_c, uint8_t* dst,
+                    int64_t ld_dst, hipStream_t s);
 int launch_relu_pack(const void* x, int dt, void* y, uint32_t* packed, uint64_t n, int bits, bool relu6, hipStream_t s);
 int launch_relu_unpack(const uint32_t* packed, const void* dy, int dyt, void* dx, uint64_t n, int bits, hipStream_t s);
 int launch_act_forward(const void* x, int dt, void* y, void* aux, uint64_t n, int act, hipStream_t s);
@@ -319,6 +321,19 @@ int dopt_fp8_gemm_nt(const uint8_t* A, const uint8_t* B, int64_t M, int64_t N, i
     const int rc = dopt::launch_fp8_gemm_nt(A, B, M, N, K, lda, ldb, out_scale, (uint16_t*)C, ldc, (hipStream_t)stream);
     if (rc) return fail(DOPT_EUNSUPPORTED, "fp8 GEMM launch configuration unsupported");
     return hip_status("fp8_gemm launch");
+}
+
+int dopt_fp8_pack_kmajor(const uint8_t* src, int64_t rows, int64_t cols, int64_t stride_r, int64_t stride_c, uint8_t* dst,
+                         int64_t ld_dst, void* stream) {
+    if (rows < 0 || cols < 0 || stride_r < 0 || stride_c < 0)
+        return fail(DOPT_EINVAL, "fp8 pack: negative extent or stride");
+    if (rows == 0 || cols == 0) return ok();
+    if (!src || !dst) return fail(DOPT_EINVAL, "null pointer argument");
+    if (ld_dst < cols) return fail(DOPT_EINVAL, "fp8 pack: ld_dst (%lld) < cols (%lld)", (long long)ld_dst, (long long)cols);
+    (void)hipGetLastError();
+    if (dopt::launch_fp8_pack(src, rows, cols, stride_r, stride_c, dst, ld_dst, (hipStream_t)stream))
+        return fail(DOPT_EINVAL, "fp8 pack: %lld x %lld is too large for one launch", (long long)rows, (long long)cols);
+    return hip_status("fp8_pack launch");
 }
 
 int dopt_relu_pack(const void* x, int x_dtype, int64_t n, int relu6, int bits, void* y, uint32_t* packed, void* stream) {

@@ -133,6 +133,17 @@ int dopt_unpack_codes(const uint32_t* packed, int64_t n_groups, int group_size, 
 int dopt_fp8_gemm_nt(const uint8_t* A, const uint8_t* B, int64_t M, int64_t N, int64_t K,
                      int64_t lda, int64_t ldb, float out_scale, void* C, int64_t ldc, void* stream);
 
+/*
+ * Layout conversion for dopt_fp8_gemm_nt: dst[r * ld_dst + c] = src[r * stride_r + c * stride_c]
+ * (byte matrices, element strides in bytes). The reference's Triton_Linear
+ * (Activation_Compression/triton_kernel/linear.py:43-95) takes A [M, K] and B [K, N] with arbitrary
+ * strides (:52-55); operands that are not K-contiguous with 16-byte aligned rows are packed with
+ * this first (rows = M or N, cols = K). stride_r == 1 (B in its row-major [K, N] layout) runs a
+ * tiled transpose, anything else a byte gather.
+ */
+int dopt_fp8_pack_kmajor(const uint8_t* src, int64_t rows, int64_t cols, int64_t stride_r, int64_t stride_c,
+                         uint8_t* dst, int64_t ld_dst, void* stream);
+
 /* ---------------------------------------------------------------- fused activation layers
  * The compressed ReLU / GELU / SiLU layers of Activation_Compression/modules/activations/ save the
  * layer's mask (ReLU) or its quantized derivative (GELU, SiLU) in the forward pass and apply it to

@@ -24,7 +24,7 @@ TESTS = ("test_schema", "test_faketensor", "test_aot_dispatch_static", "test_aot
 
 @pytest.mark.parametrize("case", [
     "quant_pack", "quant_pack_triton", "dequant_unpack", "dequant_unpack_triton", "quant_pack_tiles",
-    "pack_triton", "unpack_triton", "fp8_gemm_nt", "relu_fwd_fused_pack", "dw_gemm"])
+    "pack_triton", "unpack_triton", "fp8_gemm_nt", "fp8_linear", "relu_fwd_fused_pack", "dw_gemm"])
 def test_opcheck(case):
     x = _x((2, 8, 256))
     if case == "quant_pack":
@@ -45,12 +45,14 @@ def test_opcheck(case):
         args = (ops.pack_triton((x > 0).to(torch.int8), 1, 256), 1, 2, 8, 256)
     elif case == "fp8_gemm_nt":
         args = (_x((256, 128), 1).to(torch.float8_e4m3fn), _x((256, 128), 2).to(torch.float8_e4m3fn), 0.5)
+    elif case == "fp8_linear":
+        args = (_x((200, 100), 1).to(torch.float8_e4m3fn), _x((100, 72), 2).to(torch.float8_e4m3fn), 0.5)
     elif case == "relu_fwd_fused_pack":
         args = (_x((4, 8, 16, 16)), True, False, 1, 256)
     else:
         args = (_x((512, 256), 3), _x((512, 256), 4), None, None, None, 256, 0, 0, True, torch.float32)
     # test_schema mutates-and-compares its inputs with arithmetic torch lacks for fp8 tensors
-    tests = TESTS[1:] if case == "fp8_gemm_nt" else TESTS
+    tests = TESTS[1:] if case.startswith("fp8") else TESTS
     torch.library.opcheck(getattr(ops, case).default, args, test_utils=tests)
 
 

@@ -506,6 +506,49 @@ def test_fp8_gemm_operator_odd_n():
     assert float((c.float() - ref).norm() / ref.norm()) <= 1e-2
 
 
+@pytest.mark.parametrize("case", ["nn", "nn_ragged_k", "a_transposed", "b_colmajor", "both_views"])
+def test_fp8_linear_any_strides(case):
+    """act_lib::fp8_linear, Triton_Linear's contraction (linear.py:43-95: a [M, K] @ b [K, N] with any
+    strides), against the fp32 matmul of the same e4m3 operands: b in its row-major [K, N] layout
+    (the transposing pack), K not a multiple of 16 (zero-padded), a as a transposed view, b
+    column-major (read in place), and both views at once."""
+    M, K, N = {"nn": (1024, 2048, 768), "nn_ragged_k": (300, 100, 200), "a_transposed": (520, 272, 260),
+               "b_colmajor": (512, 512, 1000), "both_views": (257, 1040, 129)}[case]
+    gen = torch.Generator(device=DEV).manual_seed(M + K + N)
+    a8, sa = fp8_quantize(torch.randn(M, K, generator=gen, device=DEV))
+    b8, sb = fp8_quantize(torch.randn(K, N, generator=gen, device=DEV))
+    a_in, b_in = a8, b8
+    if case in ("a_transposed", "both_views"):
+        a_in = a8.t().contiguous().t()  # strides (1, M)
+    if case in ("b_colmajor", "both_views"):
+        b_in = b8.t().contiguous().t()  # strides (1, K)
+    assert torch.equal(a_in.view(torch.uint8), a8.view(torch.uint8)) and torch.equal(b_in.view(torch.uint8),
+                                                                                       b8.view(torch.uint8))
+    out_scale = float(1.0 / (sa * sb))
+    c = torch.ops.act_lib.fp8_linear(a_in, b_in, out_scale)
+    ref = (a8.float() @ b8.float()) * out_scale
+    rel = float((c.float() - ref).norm() / ref.norm())
+    assert c.shape == (M, N) and rel <= 1e-2, rel
+    assert bool(((c.float() - ref).abs() <= ref.abs() * 2 ** -7 + 1e-3 * ref.abs().max()).all())
+
+
+def test_fp8_pack_kmajor_is_the_strided_copy():
+    """dopt_fp8_pack_kmajor against torch's strided indexing: the transposing path (stride_r == 1) and
+    the gather path, ragged extents, a destination row stride past cols."""
+    L = _lib.lib()
+    gen = torch.Generator(device=DEV).manual_seed(9)
+    for rows, cols, transposed in ((300, 130, True), (77, 1000, True), (64, 64, True), (45, 33, False)):
+        src_store = torch.randint(0, 256, (cols, rows) if transposed else (rows, cols * 2), generator=gen,
+                                  device=DEV, dtype=torch.int32).to(torch.uint8)
+        view = src_store.t() if transposed else src_store[:, ::2]
+        dst = torch.full((rows, cols + 5), 0xAB, dtype=torch.uint8, device=DEV)
+        rc = L.dopt_fp8_pack_kmajor(view.data_ptr(), rows, cols, view.stride(0), view.stride(1), dst.data_ptr(),
+                                    cols + 5, torch.cuda.current_stream().cuda_stream)
+        _lib.check(rc, "fp8_pack_kmajor")
+        assert torch.equal(dst[:, :cols], view), (rows, cols, transposed)
+        assert bool((dst[:, cols:] == 0xAB).all())
+
+
 def test_fp8_gemm_rejects_bad_shapes():
     a = torch.zeros(100, 120, dtype=torch.float8_e4m3fn, device=DEV)
     b = torch.zeros(256, 120, dtype=torch.float8_e4m3fn, device=DEV)
