@@ -165,6 +165,53 @@ def fp8_probe(mode: str) -> int:
     return 0
 
 
+def counter_probe(name: str) -> int:
+    """One kernel below 70% of HBM peak, 3 + 10 launches, for rocprofv3 --pmc runs (instruction mix,
+    VALU activity, HBM bytes): "philox" / "nearest" = the config-2 quant-pack (bf16 [256,256,56,56]
+    |N(0,1)|, g = 256, 2-bit); "gelu" / "silu" = the fused activation forward on the ViT MLP
+    activation (bf16 [256,197,3072] N(0,1), g = 128, 2-bit); "bn_squash" / "bn_relu" = the
+    BatchNorm normalize + quant-pack forward on the ResNet stage-1 activation (bf16
+    [256,256,56,56], g = 512, 2-bit)."""
+    import torch
+
+    import deep_optimization_amd  # noqa: F401
+
+    dev = torch.device("cuda:0")
+    ops = torch.ops.act_lib
+    gen = torch.Generator(device=dev).manual_seed(0)
+    if name in ("philox", "nearest"):
+        x = torch.randn((256, 256, 56, 56), generator=gen, device=dev).abs_().to(torch.bfloat16).view(256, -1, G_SIZE)
+        rn = PHILOX if name == "philox" else NEAREST
+        fn = lambda: ops.quant_pack(x, BITS, G_SIZE, False, 0.0, False, rn, None, 1, 0, torch.float32)  # noqa: E731
+    elif name in ("gelu", "silu"):
+        v = torch.randn((256, 197, 3072), generator=gen, device=dev).to(torch.bfloat16)
+        if name == "gelu":
+            fn = lambda: ops.gelu_fwd_fused_quan_pack(v, 2, 128)  # noqa: E731
+        else:
+            fn = lambda: ops.silu_fwd_quan_pack(v, 2, 128, False, 0, False)  # noqa: E731
+    elif name in ("bn_squash", "bn_relu"):
+        N, C, HW = 256, 256, 56 * 56
+        g = dict(M=N * HW, HW=HW, stride_n=C * HW, stride_c=HW)
+        x = torch.randn((N, C, HW), generator=gen, device=dev).to(torch.bfloat16)
+        w = torch.rand(C, generator=gen, device=dev) + 0.5
+        b = torch.randn(C, generator=gen, device=dev)
+        s_, q_ = ops.bn_fwd_reduce(x, **g, BLOCK_M=1024, num_warps=8, num_stages=5)
+        if name == "bn_squash":
+            fn = lambda: ops.bn_fwd_norm_quant_pack_fused(x, s_, q_, w, b, None, None, **g, BLOCK_M=1024, bits=2,  # noqa: E731
+                                                          sync=False, avg_alam=False, alam_bits=0, num_warps=8,
+                                                          num_stages=5)
+        else:
+            fn = lambda: ops.bn_relu_fwd_norm_fused_quant_pack(x, s_, q_, w, b, None, None, **g, relu=True,  # noqa: E731
+                                                               relu6=False, BLOCK_SIZE=1024, BITS=2, sync=False)
+    else:
+        raise SystemExit(f"unknown counter probe {name!r}")
+    for _ in range(13):
+        fn()
+    torch.cuda.synchronize()
+    print(f"counter probe {name}: 13 launches")
+    return 0
+
+
 def dw_probe() -> int:
     """Three weight-gradient GEMMs at the ViT-B/16 bs-128 fc1 shape (dy bf16 [25216, 3072], x_hat
     bf16 [25216, 768], no bias gradient), for rocprofv3 --pmc runs."""
@@ -453,6 +500,7 @@ def main() -> int:
     ap.add_argument("--pmc-probe", action="store_true")
     ap.add_argument("--fp8-probe", choices=("random", "constant", "hipblaslt"))
     ap.add_argument("--dw-probe", action="store_true")
+    ap.add_argument("--counter-probe", choices=("philox", "nearest", "gelu", "silu", "bn_squash", "bn_relu"))
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}). "
@@ -463,6 +511,8 @@ def main() -> int:
         return pmc_probe()
     if args.fp8_probe:
         return fp8_probe(args.fp8_probe)
+    if args.counter_probe:
+        return counter_probe(args.counter_probe)
     if args.dw_probe:
         return dw_probe()
 
@@ -761,21 +811,64 @@ def main() -> int:
 
         # the CPU restatement of the reference quantizer on the same workload (all 256 samples,
         # noise-tensor rounding, pack + unpack), every host thread, 2 warm-ups, median of 10
+        def cpu_median(fn, reps=10, warm=2):
+            ts = []
+            for rep in range(reps + warm):
+                t0 = time.perf_counter()
+                fn()
+                if rep >= warm:
+                    ts.append(time.perf_counter() - t0)
+            return statistics.median(ts), statistics.mean(ts)
+
         xs = x.contiguous().view(torch.int16).cpu().numpy().view(np.uint16).reshape(-1, G_SIZE)
         us = noise.cpu().numpy().reshape(-1, G_SIZE)
-        times = []
-        for rep in range(12):
-            t0 = time.perf_counter()
+
+        def c2_round_trip():
             rp, rs, rm = oracle.quant_pack(xs, G_SIZE, BITS, rounding=oracle.STOCH_NOISE, noise=us)
             oracle.dequant_unpack(rp, rs, rm, G_SIZE, BITS, y_dtype=oracle.BF16)
-            if rep >= 2:
-                times.append(time.perf_counter() - t0)
-        ct = statistics.median(times)
-        out["cpu_baseline"] = {"value": round(rt_bytes / ct / 1e9, 3), "unit": "GB/s", "cores": oracle.num_threads(),
-                               "kind": "port",
+        ct, cmean = cpu_median(c2_round_trip)
+        del xs, us
+        cpu_model = "unknown"
+        try:
+            with open("/proc/cpuinfo") as f:
+                cpu_model = next(ln.split(":", 1)[1].strip() for ln in f if ln.startswith("model name"))
+        except (OSError, StopIteration):
+            pass
+        configs = {"C2": {"GB/s": round(rt_bytes / ct / 1e9, 3), "s_per_round_trip": round(ct, 4)}}
+        # config 1 (the reference's CPU case): fp32 [8,64,32,32] ~ N(0,1) seed 0, g = 256 as 16 x 16
+        # spatial tiles, 2-bit nearest, fp32 scale/min, round trip to fp32
+        g1 = torch.Generator().manual_seed(0)
+        x1 = torch.randn(8, 64, 32, 32, generator=g1, dtype=torch.float32).numpy()
+
+        def c1_round_trip():
+            rp, rs, rm = oracle.quant_pack(x1, 256, 2, tile_nchw=(8, 64, 32, 32))
+            oracle.dequant_unpack(rp, rs, rm, 256, 2, tile_nchw=(8, 64, 32, 32), y_dtype=oracle.F32)
+        n1 = x1.size
+        c1t, _ = cpu_median(c1_round_trip, reps=50, warm=5)
+        c1_bytes = 2 * (n1 * 4 + n1 * 2 // 8 + (n1 // 256) * 8)
+        configs["C1"] = {"GB/s": round(c1_bytes / c1t / 1e9, 3), "s_per_round_trip": round(c1t, 6)}
+        # config 3: ViT-B/16 MLP activation GELU(N(0,1)) bf16 [256,197,3072], g = 128, Philox rounding
+        # (the GPU sweep's stream), pack + unpack to bf16, each bit width
+        vg3 = torch.Generator(device=dev).manual_seed(2)
+        v3 = torch.nn.functional.gelu(torch.randn((256, 197, 3072), generator=vg3, device=dev)).to(torch.bfloat16)
+        v3s = v3.view(torch.int16).cpu().numpy().view(np.uint16).reshape(-1, 128)
+        del v3
+        n3 = v3s.size
+        for b in (1, 2, 4, 8):
+            def c3_round_trip(b=b):
+                rp, rs, rm = oracle.quant_pack(v3s, 128, b, rounding=oracle.STOCH_PHILOX, seed=1, offset=0)
+                oracle.dequant_unpack(rp, rs, rm, 128, b, y_dtype=oracle.BF16)
+            c3t, _ = cpu_median(c3_round_trip, reps=5, warm=1)
+            c3_bytes = pack_bytes(n3, n3 // 128, 2, b) + unpack_bytes(n3, n3 // 128, 2, b)
+            configs[f"C3_{b}bit"] = {"GB/s": round(c3_bytes / c3t / 1e9, 3), "s_per_round_trip": round(c3t, 4)}
+        del v3s
+        out["cpu_baseline"] = {"value": configs["C2"]["GB/s"], "unit": "GB/s", "cores": oracle.num_threads(),
+                               "kind": "port", "cpu_model": cpu_model,
                                "sample": f"the full workload ({n_elem} elements, noise-tensor 2-bit, g={G_SIZE}), "
                                          "pack + unpack with the C oracle (OpenMP), median of 10 runs after 2 warm-ups "
-                                         f"({statistics.mean(times):.2f} s each)"}
+                                         f"({cmean:.2f} s each); configs C1 (median of 50) and C3 (the full "
+                                         "[256,197,3072] activation per bit width, median of 5) beside it",
+                               "configs": configs}
         out["cpu_baseline"]["gpu_over_cpu"] = round(value / out["cpu_baseline"]["value"], 1)
 
     print(json.dumps(out))

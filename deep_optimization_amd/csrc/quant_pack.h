@@ -142,6 +142,29 @@ __device__ __forceinline__ uint32_t cvt_u32(float f) {
     return d;
 }
 
+// N codes rint(z[0..N-1]) packed little-endian at BITS bits each (N * BITS <= 32) with
+// v_cvt_pk_u8_f32, which rounds to nearest even, saturates to [0, 255] and maps NaN to 0 (measured
+// on MI355X), and inserts the byte into a dword in one instruction. Codes are gathered byte-wise
+// first: partial word D_s holds code CPB*i + s in byte i (CPB = 8/BITS codes per byte), and the
+// packed word is the OR of D_s << s*BITS. Equal to OR(cvt_u32(rint(z[k])) << k*BITS) when every
+// rint(z[k]) lies in [0, 2^BITS - 1] or z[k] is NaN or in (-0.5, 0]: one instruction per code
+// plus CPB - 1 shift-ORs per word, against rint + convert + shift-OR.
+template <int BITS, int N>
+__device__ __forceinline__ uint32_t pack_rne_codes(const float* z) {
+    constexpr int CPB = 8 / BITS;
+    constexpr int NB = (N + CPB - 1) / CPB;
+    uint32_t acc = 0;
+#pragma unroll
+    for (int s = 0; s < (CPB < N ? CPB : N); ++s) {
+        uint32_t d = 0;
+#pragma unroll
+        for (int i = 0; i < NB; ++i)
+            if (CPB * i + s < N) d = __builtin_amdgcn_cvt_pk_u8_f32(z[CPB * i + s], (uint32_t)i, d);
+        acc = s == 0 ? d : (d << (s * BITS)) | acc;
+    }
+    return acc;
+}
+
 __device__ __forceinline__ bool wave_any(bool p) { return __builtin_amdgcn_ballot_w64(p) != 0; }
 
 template <int DT, int BITS, int G, int RN, int UB, int LPG_, int P, int PRE, bool NT>
@@ -316,31 +339,38 @@ __global__ __launch_bounds__(256) void quant_pack_kernel(QuantPackArgs a) {
                         }
                     }
                 }
-                uint32_t q[UE];
-                #pragma unroll
-                for (int k = 0; k < UE; ++k) {
-                    const float t = v[i][k] - mn;
-                    float qf;
-                    if constexpr (RN == RN_NEAREST) {
-                        qf = __builtin_fmaf(t, inv, half_m);
-                    } else {
-                        qf = __builtin_fmaf(t, inv, u[k]);
-                        qf = qf - 0.5f;
-                        qf = __builtin_rintf(qf);
-                    }
-                    // NaN -> 0, as the reference's clamp; always on for a caller's noise tensor
-                    if constexpr (CL || RN == RN_NOISE) qf = __builtin_amdgcn_fmed3f(qf, 0.0f, qmaxf);
-                    q[k] = cvt_u32(qf);
-                }
                 // UBITS code bits of this unit, little-endian
+                constexpr int PER = UBITS >= 32 ? 32 / BITS : UE;  // codes per packed dword
                 uint32_t d[UBITS >= 32 ? UBITS / 32 : 1];
-                #pragma unroll
-                for (int j = 0; j < (UBITS >= 32 ? UBITS / 32 : 1); ++j) {
-                    uint32_t acc = 0;
-                    constexpr int PER = UBITS >= 32 ? 32 / BITS : UE;
+                if constexpr (RN == RN_NEAREST) {
+                    uint32_t q[UE];
                     #pragma unroll
-                    for (int k = 0; k < PER; ++k) acc |= q[j * PER + k] << (k * BITS);
-                    d[j] = acc;
+                    for (int k = 0; k < UE; ++k) {
+                        float qf = __builtin_fmaf(v[i][k] - mn, inv, half_m);
+                        // NaN -> 0, as the reference's clamp
+                        if constexpr (CL) qf = __builtin_amdgcn_fmed3f(qf, 0.0f, qmaxf);
+                        q[k] = cvt_u32(qf);
+                    }
+                    #pragma unroll
+                    for (int j = 0; j < (UBITS >= 32 ? UBITS / 32 : 1); ++j) {
+                        uint32_t acc = 0;
+                        #pragma unroll
+                        for (int k = 0; k < PER; ++k) acc |= q[j * PER + k] << (k * BITS);
+                        d[j] = acc;
+                    }
+                } else {
+                    // z = fma(t, inv, u) - 0.5; the code rint(z) (clamped to [0, QMAX] where the
+                    // clamp can matter: clamp and rint commute, both bounds being integers) is
+                    // rounded, converted and packed by pack_rne_codes
+                    float z[UE];
+                    #pragma unroll
+                    for (int k = 0; k < UE; ++k) {
+                        z[k] = __builtin_fmaf(v[i][k] - mn, inv, u[k]) - 0.5f;
+                        // NaN -> 0, as the reference's clamp; always on for a caller's noise tensor
+                        if constexpr (CL || RN == RN_NOISE) z[k] = __builtin_amdgcn_fmed3f(z[k], 0.0f, qmaxf);
+                    }
+                    #pragma unroll
+                    for (int j = 0; j < (UBITS >= 32 ? UBITS / 32 : 1); ++j) d[j] = pack_rne_codes<BITS, PER>(&z[j * PER]);
                 }
                 uint32_t* dst = a.packed + (uint64_t)r * W;
                 const bool ok = r < a.n_groups;

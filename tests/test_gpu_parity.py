@@ -243,7 +243,8 @@ def test_bad_bits_raise_value_error_on_device():
 
 
 # ----------------------------------------------------------------------------- edge cases
-def test_special_values_bit_exact():
+@pytest.mark.parametrize("bits", [1, 2, 4, 8])
+def test_special_values_bit_exact(bits):
     g = 256
     x = make_input((1, 9, g), torch.float32, seed=5)
     x[0, 0, 3] = float("inf")
@@ -256,9 +257,12 @@ def test_special_values_bit_exact():
     x[0, 5, :] = 7.0  # constant
     x[0, 6, :] = 3e38  # range overflows to inf
     x[0, 6, 1] = -3e38
-    for rounding in ("nearest", "philox"):
-        gpu = gpu_quant(x, 2, g, rounding, seed=1, offset=2)
-        ref = oracle_quant(x, 2, g, rounding, seed=1, offset=2)
+    noise = torch.rand(x.shape, generator=torch.Generator().manual_seed(3))
+    noise[0, :, :4] = torch.tensor([0.0, 1.0 - 2.0**-24, 0.5, 2.0**-24])
+    for rounding in ("nearest", "philox", "noise"):
+        nz = noise if rounding == "noise" else None
+        gpu = gpu_quant(x, bits, g, rounding, noise=nz, seed=1, offset=2)
+        ref = oracle_quant(x, bits, g, rounding, noise=nz, seed=1, offset=2)
         assert_quant_equal(gpu, ref, rounding)
 
 
