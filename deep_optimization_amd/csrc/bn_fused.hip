@@ -357,10 +357,10 @@ __device__ __forceinline__ void channel_stats(const BnFwdArgs& a, int64_t c, int
 // ------------------------------------------------------------------ forward
 // One 2048-element block of the forward: y (and the mask / codes / scale / min) from the lane's 8
 // loaded values. Whole groups are active or not (M % group == 0), so the group's lanes agree.
-template <int MODE, int V>
+template <int MODE, int V, bool R6>
 __device__ __forceinline__ void fwd_block(const BnFwdArgs& a, int64_t c, RowCursor pos, int64_t e0, int64_t M,
                                           bool active, const float* v, float mean, float inv, float w, float b,
-                                          int lg, int bits, int relu6) {
+                                          int lg, int bits) {
     const BnGeom& g = a.g;
     float xh[EPL], y[EPL];
 #pragma unroll
@@ -378,9 +378,9 @@ __device__ __forceinline__ void fwd_block(const BnFwdArgs& a, int64_t c, RowCurs
         if constexpr (MODE == BN_RELU_QUANT) {
 #pragma unroll
             for (int k = 0; k < EPL; ++k) {
-                const bool on = relu6 ? (y[k] > 0.0f && y[k] < 6.0f) : (y[k] > 0.0f);
+                const bool on = R6 ? (y[k] > 0.0f && y[k] < 6.0f) : (y[k] > 0.0f);
                 m8 |= (uint32_t)on << k;
-                y[k] = relu6 ? __builtin_amdgcn_fmed3f(y[k], 0.0f, 6.0f) : (on ? y[k] : 0.0f);
+                y[k] = R6 ? __builtin_amdgcn_fmed3f(y[k], 0.0f, 6.0f) : (on ? y[k] : 0.0f);
             }
         }
         if (active) store8_bf16<V>(a.y, g, pos, e0, M, y);
@@ -421,20 +421,31 @@ __device__ __forceinline__ void fwd_block(const BnFwdArgs& a, int64_t c, RowCurs
             // 2^-60 <= step < inf and a in [0, rng] the quotient lies in [0, qmax], and whenever it
             // can reach a rounding boundary of the code (q >= ~1e-7) the remainder is normal.
             // (Checked bit-for-bit against fp32 division on 4e8 random and quantizer-shaped pairs.)
+            // (The test is per group; one wave-uniform branch keeps the common case free of
+            // per-element lane masking.)
             const float invs = 1.0f / step;
             const bool fastdiv = step >= 0x1p-60f && step < __builtin_huge_valf();
+            if (__builtin_amdgcn_ballot_w64(!fastdiv) == 0) {
 #pragma unroll
-            for (int k = 0; k < EPL; ++k) {
-                const float num = t[k] - mn;
-                float quo;
-                if (fastdiv) {
+                for (int k = 0; k < EPL; ++k) {
+                    const float num = t[k] - mn;
                     const float q0 = num * invs;
-                    quo = fmaf(fmaf(-q0, step, num), invs, q0);
-                } else {
-                    quo = num / step;
+                    const float quo = fmaf(fmaf(-q0, step, num), invs, q0);
+                    q[k] = (int)__builtin_amdgcn_fmed3f(quo + half_m, 0.0f, qmaxf);
                 }
-                const float qf = __builtin_amdgcn_fmed3f(quo + half_m, 0.0f, qmaxf);
-                q[k] = (int)qf;
+            } else {
+#pragma unroll
+                for (int k = 0; k < EPL; ++k) {
+                    const float num = t[k] - mn;
+                    float quo;
+                    if (fastdiv) {
+                        const float q0 = num * invs;
+                        quo = fmaf(fmaf(-q0, step, num), invs, q0);
+                    } else {
+                        quo = num / step;
+                    }
+                    q[k] = (int)__builtin_amdgcn_fmed3f(quo + half_m, 0.0f, qmaxf);
+                }
             }
         }
         store_codes(a.packed + c * ((M * bits) >> 5), e0, q, bits, active);
@@ -448,23 +459,23 @@ __device__ __forceinline__ void fwd_block(const BnFwdArgs& a, int64_t c, RowCurs
 
 // A workgroup covers ITER consecutive 2048-element blocks of one channel; all loads are issued
 // before the first block is processed.
-template <int DT, int MODE, int V>
-__global__ __launch_bounds__(TPB) void bn_fwd_kernel(BnFwdArgs a, int lg, int bits, int relu6) {
+template <int DT, int MODE, int V, bool R6>
+__global__ __launch_bounds__(TPB) void bn_fwd_kernel(BnFwdArgs a, int lg, int bits) {
     const int64_t c = blockIdx.y;
     const int64_t M = a.g.N * a.g.HW;
     const int64_t base = (int64_t)blockIdx.x * BN_CHUNK + (int64_t)threadIdx.x * EPL;
     RowCursor cur[ITER];
     block_cursors(a.g, c, base, cur);
+    // lanes past M read the channel's first elements instead (their results are not stored and
+    // whole groups lie on one side of M): no branch around the loads, so all ITER are in flight
+    // together (a masked load merged with a default value waits for its data)
     float v[ITER][EPL];
 #pragma unroll
     for (int it = 0; it < ITER; ++it) {
         const int64_t e0 = base + it * WG_ELEMS;
-        if (e0 < M) {
-            load8<DT, V>(a.x, a.g, cur[it], e0, M, v[it]);
-        } else {
-#pragma unroll
-            for (int k = 0; k < EPL; ++k) v[it][k] = 0.0f;
-        }
+        const bool in = e0 < M;
+        const RowCursor p = {in ? cur[it].row : c * a.g.stride_c, in ? cur[it].r : 0u};
+        load8<DT, V>(a.x, a.g, p, in ? e0 : 0, M, v[it]);
     }
     float mean, inv;
     channel_stats(a, c, M, mean, inv);
@@ -472,7 +483,7 @@ __global__ __launch_bounds__(TPB) void bn_fwd_kernel(BnFwdArgs a, int lg, int bi
 #pragma unroll
     for (int it = 0; it < ITER; ++it) {
         const int64_t e0 = base + it * WG_ELEMS;
-        fwd_block<MODE, V>(a, c, cur[it], e0, M, e0 < M, v[it], mean, inv, w, b, lg, bits, relu6);
+        fwd_block<MODE, V, R6>(a, c, cur[it], e0, M, e0 < M, v[it], mean, inv, w, b, lg, bits);
     }
 }
 
@@ -633,14 +644,16 @@ int fwd_dt(const BnFwdArgs& a, int mode, int group, int bits, int vw, hipStream_
     const int64_t M = a.g.N * a.g.HW;
     const int lg = mode == BN_NORM ? 3 : log2i(group);
     const dim3 grid((unsigned)bn_nchunks(M), (unsigned)a.g.C);
-    const int relu6 = mode == BN_RELU6_QUANT;
-#define DOPT_BN_FWD(MODE_, V_) hipLaunchKernelGGL((bn_fwd_kernel<DT, MODE_, V_>), grid, dim3(TPB), 0, s, a, lg, bits, relu6)
+#define DOPT_BN_FWD(MODE_, V_) hipLaunchKernelGGL((bn_fwd_kernel<DT, MODE_, V_, false>), grid, dim3(TPB), 0, s, a, lg, bits)
+#define DOPT_BN_FWD_RELU6(V_) hipLaunchKernelGGL((bn_fwd_kernel<DT, BN_RELU_QUANT, V_, true>), grid, dim3(TPB), 0, s, a, lg, bits)
 #define DOPT_BN_FWD_NORM(V_) DOPT_BN_FWD(BN_NORM, V_)
 #define DOPT_BN_FWD_QUANT(V_) DOPT_BN_FWD(BN_QUANT, V_)
 #define DOPT_BN_FWD_RELU(V_) DOPT_BN_FWD(BN_RELU_QUANT, V_)
     if (mode == BN_NORM) DOPT_BN_BY_WIDTH(vw, DOPT_BN_FWD_NORM);
     else if (mode == BN_QUANT) DOPT_BN_BY_WIDTH(vw, DOPT_BN_FWD_QUANT);
+    else if (mode == BN_RELU6_QUANT) DOPT_BN_BY_WIDTH(vw, DOPT_BN_FWD_RELU6);
     else DOPT_BN_BY_WIDTH(vw, DOPT_BN_FWD_RELU);
+#undef DOPT_BN_FWD_RELU6
 #undef DOPT_BN_FWD_RELU
 #undef DOPT_BN_FWD_QUANT
 #undef DOPT_BN_FWD_NORM

@@ -68,6 +68,9 @@ __device__ __forceinline__ void block_minmax(float& mn, float& mx) {
 // Raw v_min/v_max (and 3-operand forms): no NaN canonicalisation of the operands, which fminf /
 // fmaxf would add in IEEE mode. Equal to fminf / fmaxf for operands that are numbers or quiet NaNs
 // (every arithmetic result and every bit copy of one), the only operands these kernels pass.
+// Inline asm is outside the compiler's hazard tracking: an operand must not be the direct result
+// of a transcendental (v_exp/v_rcp/v_sqrt...), which a following VALU may read only after one
+// wait state; callers with such operands use fminf / fmaxf.
 __device__ __forceinline__ float vmin3(float a, float b, float c) {
     float d;
     asm("v_min3_f32 %0, %1, %2, %3" : "=v"(d) : "v"(a), "v"(b), "v"(c));
@@ -184,14 +187,17 @@ __device__ __forceinline__ float fast_sigmoid(float x) {
 // s = (1 + t)/2 = sigmoid(2u) and 1 - t^2 = 4 s (1 - s), the same function without the
 // cancellation of 1 + t for x below about -4 (where an fp32 tanh is already -1):
 // u = x (a + a b x^2), s = 1 / (1 + 2^(-2 log2(e) u)), dy/dx = s + x s (1 - s) (2a + 6ab x^2).
+// The factor -2 log2(e) is folded into the polynomial's coefficients and x s (1 - s) = y - y s is
+// one fma.
 __device__ __forceinline__ void gelu_and_grad(float x, float& y, float& d) {
     const float a = 0.7978845608028654f, ab = 0.7978845608028654f * 0.044715f;
+    const float k = -2.8853900817779268f;  // -2 log2(e)
     const float x2 = x * x;
-    const float u = x * __builtin_fmaf(ab, x2, a);
-    const float s = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-2.8853900817779268f * u));
+    const float ku = x * __builtin_fmaf(k * ab, x2, k * a);
+    const float s = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(ku));
     y = x * s;
     const float c = __builtin_fmaf(6.0f * ab, x2, 2.0f * a);
-    d = __builtin_fmaf(y * (1.0f - s), c, s);
+    d = __builtin_fmaf(__builtin_fmaf(-y, s, y), c, s);
 }
 // SiLU value and derivative (kernel_implementation.py:225-229): s = sigmoid(x), y = x s,
 // dy/dx = s + x s (1 - s)
@@ -206,9 +212,10 @@ __device__ __forceinline__ float two_tanh_half_fast(float x) {
     const float r = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-1.4426950408889634f * x));
     return __builtin_fmaf(4.0f, r, -2.0f);
 }
-// tanh(2d) / 2 of a clamped activation derivative, as sigmoid(4d) - 1/2 (absolute error ~1e-7)
-__device__ __forceinline__ float half_tanh2_fast(float d) {
-    return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-5.7707801635558535f * d)) - 0.5f;
+// tanh(2d) / 2 of a clamped activation derivative is sigmoid(4d) - 1/2 (absolute error ~1e-7);
+// this returns sigmoid(4d), the caller subtracts 1/2 where it can do so once per group
+__device__ __forceinline__ float sigmoid4_fast(float d) {
+    return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-5.7707801635558535f * d));
 }
 
 // ------------------------------------------------------------------ Philox4x32-10

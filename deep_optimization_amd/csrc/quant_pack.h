@@ -181,27 +181,25 @@ __global__ __launch_bounds__(256) void quant_pack_kernel(QuantPackArgs a) {
     const uint32_t g0 = (blockIdx.x * C::WAVES + (threadIdx.x >> 6)) * (uint32_t)C::GPW;
     const char* xb = (const char*)a.x;
 
-    // ---- every load of the wave first: P*CPL units of LOADS 16-byte vectors per lane
+    // ---- every load of the wave first: P*CPL units of LOADS 16-byte vectors per lane. Lanes past
+    // the last group (n_groups >= 1: the launcher skips empty calls) load the last group again and
+    // store nothing; the loads carry no branch, so all of them are in flight together (a load
+    // under a lane mask, merged with a default value, waits for its data before the next issues)
     uint4 raw[P][CPL][LOADS];
     uint4 nz[P][CPL][RN == RN_NOISE ? UE / 4 : 1];
     #pragma unroll
     for (int p = 0; p < P; ++p) {
-        const uint32_t r = g0 + p * GPP + slot;
-        const bool ok = r < a.n_groups;
+        const uint32_t r0 = g0 + p * GPP + slot;
+        const uint32_t r = r0 < a.n_groups ? r0 : a.n_groups - 1;
         #pragma unroll
         for (int i = 0; i < CPL; ++i) {
             const uint32_t e0 = (uint32_t)(i * LPG + li) * UE;
             #pragma unroll
-            for (int l = 0; l < LOADS; ++l) {
-                raw[p][i][l] = make_uint4(0u, 0u, 0u, 0u);
-                if (ok) raw[p][i][l] = ld16<NT>(xb + group_elem_index<G>(a, r, e0 + l * E16) * C::BYTES);
-            }
+            for (int l = 0; l < LOADS; ++l)
+                raw[p][i][l] = ld16<NT>(xb + group_elem_index<G>(a, r, e0 + l * E16) * C::BYTES);
             if constexpr (RN == RN_NOISE) {
                 #pragma unroll
-                for (int k = 0; k < UE / 4; ++k) {
-                    nz[p][i][k] = make_uint4(0u, 0u, 0u, 0u);
-                    if (ok) nz[p][i][k] = ld16<NT>(a.noise + (uint64_t)r * G + e0 + 4 * k);
-                }
+                for (int k = 0; k < UE / 4; ++k) nz[p][i][k] = ld16<NT>(a.noise + (uint64_t)r * G + e0 + 4 * k);
             }
         }
     }
@@ -242,7 +240,11 @@ __global__ __launch_bounds__(256) void quant_pack_kernel(QuantPackArgs a) {
                     for (int k = 0; k < UE; ++k) v[i][k] = squash_half_tanh2(v[i][k]);
             }
         } else if constexpr (PRE == PRE_GELU || PRE == PRE_SILU) {
-            // activation value (stored bf16) and its squashed derivative (quantized)
+            // activation value (stored bf16) and its squashed derivative tanh(2 clamp(d, -3, 3)) / 2,
+            // quantized as s = sigmoid(4 clamp(d, -3, 3)) = tanh(...) / 2 + 1/2: for finite x the
+            // derivative is at least -0.17 (GELU; SiLU -0.1), so s >= 0.33 and s - 1/2 is exact
+            // (Sterbenz), as is min - 1/2; differences of the shifted values, hence range, step
+            // and codes, are those of s itself, and only the group's min is stored shifted
 #pragma unroll
             for (int i = 0; i < CPL; ++i) {
                 const uint32_t e0 = (uint32_t)(i * LPG + li) * UE;
@@ -254,7 +256,7 @@ __global__ __launch_bounds__(256) void quant_pack_kernel(QuantPackArgs a) {
                         gelu_and_grad(v[i][k], yv[k], d);
                     else
                         silu_and_grad(v[i][k], yv[k], d);
-                    v[i][k] = half_tanh2_fast(__builtin_amdgcn_fmed3f(d, -3.0f, 3.0f));
+                    v[i][k] = sigmoid4_fast(__builtin_amdgcn_fmed3f(d, -3.0f, 3.0f));
                 }
                 if (r < a.n_groups) {
 #pragma unroll
@@ -270,16 +272,32 @@ __global__ __launch_bounds__(256) void quant_pack_kernel(QuantPackArgs a) {
                 }
             }
         }
-        // lane-local min/max with raw 3-operand min/max over the lane's CPL*UE values
+        // lane-local min/max over the lane's CPL*UE values. Loaded (or clamped) values go
+        // through raw v_min3/v_max3 (inline asm: no NaN canonicalisation of the operands). The
+        // activation pre-transforms end in v_rcp_f32, whose result a VALU may read only after one
+        // wait state, which the compiler enforces for its own instructions but not for inline
+        // asm; their values are arithmetic results (canonical), so compiler min/max add nothing.
+        constexpr bool TRANS_IN = PRE == PRE_GELU || PRE == PRE_SILU;
         float mn = v[0][0], mx = v[0][0];
         #pragma unroll
         for (int j = 1; j + 1 < CPL * UE; j += 2) {
             const float f0 = v[j / UE][j % UE], f1 = v[(j + 1) / UE][(j + 1) % UE];
-            mn = vmin3(mn, f0, f1);
-            mx = vmax3(mx, f0, f1);
+            if constexpr (TRANS_IN) {
+                mn = fminf(mn, fminf(f0, f1));
+                mx = fmaxf(mx, fmaxf(f0, f1));
+            } else {
+                mn = vmin3(mn, f0, f1);
+                mx = vmax3(mx, f0, f1);
+            }
         }
-        mn = vmin(mn, v[CPL - 1][UE - 1]);  // CPL*UE is even: one value is left over
-        mx = vmax(mx, v[CPL - 1][UE - 1]);
+        // CPL*UE is even: one value is left over
+        if constexpr (TRANS_IN) {
+            mn = fminf(mn, v[CPL - 1][UE - 1]);
+            mx = fmaxf(mx, v[CPL - 1][UE - 1]);
+        } else {
+            mn = vmin(mn, v[CPL - 1][UE - 1]);
+            mx = vmax(mx, v[CPL - 1][UE - 1]);
+        }
         if (wave_any(mn != mn || mx != mx)) {
             // a NaN partial result (signalling NaN input, or a lane of only NaNs): IEEE
             // fminf/fmaxf ignore NaN operands; a lane of only NaNs keeps NaN, which the
@@ -303,7 +321,10 @@ __global__ __launch_bounds__(256) void quant_pack_kernel(QuantPackArgs a) {
         const float step = rng > 0.0f ? rng / qmaxf : 1.0f;
         const float inv = 1.0f / step;
         step_p[p] = step;
-        mn_p[p] = mn;
+        if constexpr (PRE == PRE_GELU || PRE == PRE_SILU)
+            mn_p[p] = mn - 0.5f;
+        else
+            mn_p[p] = mn;
         const bool clampq = wave_any(inv == __builtin_inff());
 
         // codes + store; the clamped variant runs only for waves holding a group with inv = +inf
