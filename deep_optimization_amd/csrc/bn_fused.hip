@@ -78,6 +78,17 @@ __device__ __forceinline__ void block_cursors(const BnGeom& g, int64_t c, int64_
     }
 }
 
+// A block at or past M (a lane of the last workgroup) reads the channel's first block instead:
+// every load stays in bounds and carries no lane-mask branch, so all of a lane's loads are in
+// flight together (a masked load merged with a default value waits for its data); callers drop
+// the results of such blocks (whole groups lie on one side of M).
+__device__ __forceinline__ void block_or_first(const BnGeom& g, int64_t c, const RowCursor& cur, int64_t e0,
+                                               int64_t M, RowCursor& p, int64_t& e) {
+    const bool in = e0 < M;
+    p = {in ? cur.row : c * g.stride_c, in ? cur.r : 0u};
+    e = in ? e0 : 0;
+}
+
 // V consecutive elements of one row at element offset off (aligned to V elements)
 template <int DT, int V>
 __device__ __forceinline__ void ldv(const void* base, int64_t off, float* v) {
@@ -195,14 +206,8 @@ __device__ __forceinline__ void group_minmax(float& mn, float& mx, int lpg) {
         mn = vmin(mn, dpp_f32<0x140>(mn));
         mx = vmax(mx, dpp_f32<0x140>(mx));
     }
-    if (lpg >= 32) {
-        mn = vmin(mn, __shfl_xor(mn, 16, 64));
-        mx = vmax(mx, __shfl_xor(mx, 16, 64));
-    }
-    if (lpg >= 64) {
-        mn = vmin(mn, __shfl_xor(mn, 32, 64));
-        mx = vmax(mx, __shfl_xor(mx, 32, 64));
-    }
+    if (lpg >= 32) swap_minmax<16>(mn, mx);
+    if (lpg >= 64) swap_minmax<32>(mn, mx);
 }
 
 // Writes the lane's 8 codes (bits each) into the channel bitstream at element e0: 1-bit codes
@@ -242,21 +247,20 @@ __device__ __forceinline__ void store_mask(uint32_t* chan, int64_t e0, uint32_t 
 }
 
 // the lane's 8 codes read back from the channel bitstream
+// (e0 is a multiple of 8, so below 8 bits the lane's 8 * bits code bits lie in one dword and at
+// 8 bits in two; both dwords are loaded at selected addresses, with no branch, then extracted)
 __device__ __forceinline__ void load_codes(const uint32_t* chan, int64_t e0, int bits, int* q) {
-    if (bits == 8) {
-        const uint2 w = *(const uint2*)(chan + e0 / 4);
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            q[k] = (w.x >> (8 * k)) & 0xff;
-            q[k + 4] = (w.y >> (8 * k)) & 0xff;
-        }
-        return;
-    }
+    const bool b8 = bits == 8;
     const int64_t bit0 = e0 * bits;
-    const uint32_t w = chan[bit0 >> 5] >> (bit0 & 31);
-    const uint32_t qm = (1u << bits) - 1u;
+    const uint32_t* p = chan + (bit0 >> 5);
+    const uint32_t w0 = p[0] >> (bit0 & 31);  // bit0 & 31 == 0 at 8 bits
+    const uint32_t w1 = p[b8 ? 1 : 0];
 #pragma unroll
-    for (int k = 0; k < EPL; ++k) q[k] = (w >> (k * bits)) & qm;
+    for (int k = 0; k < EPL; ++k) {
+        const uint32_t src = (b8 && k >= 4) ? w1 : w0;
+        const uint32_t off = b8 ? 8u * (uint32_t)(k & 3) : (uint32_t)(k * bits);
+        q[k] = (int)__builtin_amdgcn_ubfe(src, off, (uint32_t)bits);
+    }
 }
 
 // ------------------------------------------------------------------ statistics
@@ -271,22 +275,21 @@ __global__ __launch_bounds__(TPB) void bn_stats_kernel(const void* __restrict__ 
     float v[ITER][EPL];
 #pragma unroll
     for (int it = 0; it < ITER; ++it) {
-        const int64_t e0 = base + it * WG_ELEMS;
-        if (e0 < M) {
-            load8<DT, V>(x, g, cur[it], e0, M, v[it]);
-        } else {
-#pragma unroll
-            for (int k = 0; k < EPL; ++k) v[it][k] = 0.0f;
-        }
+        RowCursor p;
+        int64_t e;
+        block_or_first(g, c, cur[it], base + it * WG_ELEMS, M, p, e);
+        load8<DT, V>(x, g, p, e, M, v[it]);
     }
     float s = 0.0f, s2 = 0.0f;
 #pragma unroll
-    for (int it = 0; it < ITER; ++it)
+    for (int it = 0; it < ITER; ++it) {
+        if (base + it * WG_ELEMS >= M) continue;  // a stand-in block: no contribution
 #pragma unroll
         for (int k = 0; k < EPL; ++k) {
             s += v[it][k];
             s2 = fmaf(v[it][k], v[it][k], s2);
         }
+    }
     block_sum2(s, s2);
     if (threadIdx.x == 0) {
         partial[c * nchunks + chunk] = s;
@@ -388,7 +391,6 @@ __device__ __forceinline__ void fwd_block(const BnFwdArgs& a, int64_t c, RowCurs
 
         // values quantized: the squashed x_hat (BN_QUANT) or x_hat itself (ReLU modes)
         float t[EPL];
-        float mn = __builtin_huge_valf(), mx = -__builtin_huge_valf();
 #pragma unroll
         for (int k = 0; k < EPL; ++k) {
             if constexpr (MODE == BN_QUANT) {
@@ -396,8 +398,13 @@ __device__ __forceinline__ void fwd_block(const BnFwdArgs& a, int64_t c, RowCurs
             } else {
                 t[k] = xh[k];
             }
-            mn = vmin(mn, t[k]);
-            mx = vmax(mx, t[k]);
+        }
+        // min / max of {+-inf, t[0..7]} (an all-NaN lane keeps the infinities), 3-operand forms
+        float mn = __builtin_huge_valf(), mx = -__builtin_huge_valf();
+#pragma unroll
+        for (int k = 0; k < EPL; k += 2) {
+            mn = vmin3(mn, t[k], t[k + 1]);
+            mx = vmax3(mx, t[k], t[k + 1]);
         }
         const int lpg = 1 << (lg - 3);  // group / EPL
         group_minmax(mn, mx, lpg);
@@ -466,16 +473,13 @@ __global__ __launch_bounds__(TPB) void bn_fwd_kernel(BnFwdArgs a, int lg, int bi
     const int64_t base = (int64_t)blockIdx.x * BN_CHUNK + (int64_t)threadIdx.x * EPL;
     RowCursor cur[ITER];
     block_cursors(a.g, c, base, cur);
-    // lanes past M read the channel's first elements instead (their results are not stored and
-    // whole groups lie on one side of M): no branch around the loads, so all ITER are in flight
-    // together (a masked load merged with a default value waits for its data)
     float v[ITER][EPL];
 #pragma unroll
     for (int it = 0; it < ITER; ++it) {
-        const int64_t e0 = base + it * WG_ELEMS;
-        const bool in = e0 < M;
-        const RowCursor p = {in ? cur[it].row : c * a.g.stride_c, in ? cur[it].r : 0u};
-        load8<DT, V>(a.x, a.g, p, in ? e0 : 0, M, v[it]);
+        RowCursor p;
+        int64_t e;
+        block_or_first(a.g, c, cur[it], base + it * WG_ELEMS, M, p, e);
+        load8<DT, V>(a.x, a.g, p, e, M, v[it]);
     }
     float mean, inv;
     channel_stats(a, c, M, mean, inv);
@@ -540,7 +544,10 @@ __global__ __launch_bounds__(TPB) void bn_bwd_reduce_kernel(BnBwdArgs a, int lg,
 #pragma unroll
         for (int it = 0; it < ITER; ++it) {
             const int64_t e0 = base + it * WG_ELEMS;
-            if (e0 < M) bwd_operands<DYT, MODE, V>(a, c, cur[it], e0, M, lg, bits, xh[it], dy[it]);
+            RowCursor p;
+            int64_t e;
+            block_or_first(a.g, c, cur[it], e0, M, p, e);
+            bwd_operands<DYT, MODE, V>(a, c, p, e, M, lg, bits, xh[it], dy[it]);
         }
 #pragma unroll
         for (int it = 0; it < ITER; ++it) {
@@ -560,7 +567,10 @@ __global__ __launch_bounds__(TPB) void bn_bwd_reduce_kernel(BnBwdArgs a, int lg,
 #pragma unroll
         for (int it = 0; it < ITER; ++it) {
             const int64_t e0 = base + it * WG_ELEMS;
-            if (e0 < M) bwd_codes<DYT, MODE, V>(a, c, cur[it], e0, M, lg, bits, q[it], sc[it], mn[it], dy[it]);
+            RowCursor p;
+            int64_t e;
+            block_or_first(a.g, c, cur[it], e0, M, p, e);
+            bwd_codes<DYT, MODE, V>(a, c, p, e, M, lg, bits, q[it], sc[it], mn[it], dy[it]);
         }
 #pragma unroll
         for (int it = 0; it < ITER; ++it) {
@@ -593,7 +603,10 @@ __global__ __launch_bounds__(TPB) void bn_bwd_dx_kernel(BnBwdArgs a, int lg, int
 #pragma unroll
     for (int it = 0; it < ITER; ++it) {
         const int64_t e0 = base + it * WG_ELEMS;
-        if (e0 < M) bwd_operands<DYT, MODE, V>(a, c, cur[it], e0, M, lg, bits, xh[it], dy[it]);
+        RowCursor p;
+        int64_t e;
+        block_or_first(a.g, c, cur[it], e0, M, p, e);
+        bwd_operands<DYT, MODE, V>(a, c, p, e, M, lg, bits, xh[it], dy[it]);
     }
     const float Mf = (float)M;
     float dws, dbs;

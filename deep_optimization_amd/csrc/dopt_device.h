@@ -92,6 +92,27 @@ __device__ __forceinline__ float vmax(float a, float b) {
     return d;
 }
 
+// min/max with lane l ^ D (D = 16 or 32) on every lane: v_permlane16_swap / v_permlane32_swap
+// of a register with itself leaves the pair {x[l & ~D], x[l | D]}, in that order on both lanes of
+// the pair (measured on MI355X), one VALU op per exchange instead of an LDS permute; both lanes
+// then compute the same min/max of the same ordered operands
+template <int D>
+__device__ __forceinline__ void swap_minmax(float& mn, float& mx) {
+    static_assert(D == 16 || D == 32, "row swaps exchange 16 or 32 lanes");
+    const uint32_t a = __float_as_uint(mn), b = __float_as_uint(mx);
+    if constexpr (D == 16) {
+        const auto sa = __builtin_amdgcn_permlane16_swap(a, a, false, false);
+        const auto sb = __builtin_amdgcn_permlane16_swap(b, b, false, false);
+        mn = vmin(__uint_as_float(sa[0]), __uint_as_float(sa[1]));
+        mx = vmax(__uint_as_float(sb[0]), __uint_as_float(sb[1]));
+    } else {
+        const auto sa = __builtin_amdgcn_permlane32_swap(a, a, false, false);
+        const auto sb = __builtin_amdgcn_permlane32_swap(b, b, false, false);
+        mn = vmin(__uint_as_float(sa[0]), __uint_as_float(sa[1]));
+        mx = vmax(__uint_as_float(sb[0]), __uint_as_float(sb[1]));
+    }
+}
+
 // ------------------------------------------------------------------ 16-byte global access
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 

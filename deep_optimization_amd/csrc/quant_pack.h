@@ -125,14 +125,8 @@ __device__ __forceinline__ void group_minmax(float& mn, float& mx) {
         mn = vmin(mn, dpp_f32<0x140>(mn));
         mx = vmax(mx, dpp_f32<0x140>(mx));
     }
-    if constexpr (LPG >= 32) {
-        mn = vmin(mn, __shfl_xor(mn, 16, 64));
-        mx = vmax(mx, __shfl_xor(mx, 16, 64));
-    }
-    if constexpr (LPG >= 64) {
-        mn = vmin(mn, __shfl_xor(mn, 32, 64));
-        mx = vmax(mx, __shfl_xor(mx, 32, 64));
-    }
+    if constexpr (LPG >= 32) swap_minmax<16>(mn, mx);
+    if constexpr (LPG >= 64) swap_minmax<32>(mn, mx);
 }
 
 // v_cvt_u32_f32: truncating, saturating, NaN -> 0
