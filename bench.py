@@ -212,6 +212,43 @@ def counter_probe(name: str) -> int:
     return 0
 
 
+def valu_probe() -> int:
+    """Issue cost of one VALU instruction kind (dopt_valu_probe): ns per wave-instruction per SIMD
+    for v_fma_f32, v_exp_f32, v_rcp_f32 and v_mad_u64_u32 + v_xor_b32, median of 5 event-timed
+    windows of 10 launches of 2048 workgroups (8192 waves, 4096 steps per lane)."""
+    import torch
+
+    import deep_optimization_amd  # noqa: F401
+    from deep_optimization_amd import _lib
+
+    L = _lib.lib()
+    dev = torch.device("cuda:0")
+    blocks = 2048
+    out = torch.empty(blocks * 256, device=dev)
+    st = torch.cuda.current_stream(dev)
+    simds = torch.cuda.get_device_properties(dev).multi_processor_count * 4
+    per_simd = blocks * 4 * 8 * 512 / simds  # wave-instructions per SIMD per launch
+    res = {}
+    for kind, name in enumerate(("v_fma_f32", "v_exp_f32", "v_rcp_f32", "v_mad_u64_u32+v_xor_b32")):
+        fn = lambda kind=kind: _lib.check(L.dopt_valu_probe(kind, out.data_ptr(), blocks, st.cuda_stream),  # noqa: E731
+                                          "valu_probe")
+        for _ in range(3):
+            fn()
+        ts = []
+        for _ in range(5):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(st)
+            for _ in range(10):
+                fn()
+            e1.record(st)
+            e1.synchronize()
+            ts.append(e0.elapsed_time(e1) / 10 * 1e3)
+        us = statistics.median(ts)
+        res[name] = {"us_per_launch": round(us, 2), "ns_per_wave_instruction": round(us * 1e3 / per_simd, 4)}
+    print(json.dumps({"valu_probe": res, "simds": simds}))
+    return 0
+
+
 def dw_probe() -> int:
     """Three weight-gradient GEMMs at the ViT-B/16 bs-128 fc1 shape (dy bf16 [25216, 3072], x_hat
     bf16 [25216, 768], no bias gradient), for rocprofv3 --pmc runs."""
@@ -500,6 +537,7 @@ def main() -> int:
     ap.add_argument("--pmc-probe", action="store_true")
     ap.add_argument("--fp8-probe", choices=("random", "constant", "hipblaslt"))
     ap.add_argument("--dw-probe", action="store_true")
+    ap.add_argument("--valu-probe", action="store_true")
     ap.add_argument("--counter-probe", choices=("philox", "nearest", "gelu", "silu", "bn_squash", "bn_relu"))
     args = ap.parse_args()
     if args.gpus != 1:
@@ -515,6 +553,8 @@ def main() -> int:
         return counter_probe(args.counter_probe)
     if args.dw_probe:
         return dw_probe()
+    if args.valu_probe:
+        return valu_probe()
 
     import torch
 

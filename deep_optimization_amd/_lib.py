@@ -47,6 +47,7 @@ EXPORTS = (
     "dopt_graph_node_counts",
     "dopt_graph_replace_memsets",
     "dopt_stream_probe",
+    "dopt_valu_probe",
 )
 
 _lib = None
@@ -131,6 +132,8 @@ def lib() -> ctypes.CDLL:
         L.dopt_graph_replace_memsets.restype = i32
         L.dopt_stream_probe.argtypes = [vp, vp, vp, vp, i64, i32, vp]
         L.dopt_stream_probe.restype = i32
+        L.dopt_valu_probe.argtypes = [i32, vp, i64, vp]
+        L.dopt_valu_probe.restype = i32
         _lib = L
     return _lib
 

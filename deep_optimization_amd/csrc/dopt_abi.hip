@@ -24,6 +24,7 @@ int launch_relu_unpack(const uint32_t* packed, const void* dy, int dyt, void* dx
 int launch_act_forward(const void* x, int dt, void* y, void* aux, uint64_t n, int act, hipStream_t s);
 const char* graph_node_counts(hipGraph_t g, int64_t* counts, int n_counts);
 const char* graph_replace_memsets(hipGraph_t g, int64_t* replaced);
+const char* launch_valu_rate(int kind, float* out, uint32_t n_blocks, hipStream_t s);
 const char* launch_stream_mix(const void* x, const void* noise, void* codes, void* meta, uint64_t n_units, int bits,
                               hipStream_t s);
 }  // namespace dopt
@@ -769,6 +770,17 @@ int dopt_graph_replace_memsets(void* graph, int64_t* n_replaced) {
     *n_replaced = 0;
     if (const char* e = dopt::graph_replace_memsets((hipGraph_t)graph, n_replaced))
         return fail(DOPT_EHIP, "graph_replace_memsets: %s failed after %lld replacements", e, (long long)*n_replaced);
+    return ok();
+}
+
+int dopt_valu_probe(int kind, float* out, int64_t n_blocks, void* stream) {
+    if (kind < 0 || kind > 3) return fail(DOPT_EINVAL, "kind must be 0..3 (fma, exp, rcp, mad64+xor), got %d", kind);
+    if (n_blocks < 1 || n_blocks > 65536) return fail(DOPT_EINVAL, "n_blocks must be in [1, 65536], got %lld",
+                                                      (long long)n_blocks);
+    if (!out || ((uintptr_t)out & 3u)) return fail(DOPT_EINVAL, "out must be a 4-byte aligned pointer");
+    (void)hipGetLastError();
+    if (const char* e = dopt::launch_valu_rate(kind, out, (uint32_t)n_blocks, (hipStream_t)stream))
+        return fail(DOPT_EHIP, "valu_probe launch: %s", e);
     return ok();
 }
 

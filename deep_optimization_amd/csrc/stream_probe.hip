@@ -47,7 +47,49 @@ hipError_t launch(const void* x, const void* noise, void* codes, void* meta, uin
     return hipGetLastError();
 }
 
+// Issue-rate probe: every lane runs 8 independent chains of VALU_STEPS steps of one instruction
+// kind and writes one value, so a launch of many waves measures the time per wave-instruction
+// of that kind on a SIMD (the cost model behind the instruction-bound kernels' roofline).
+constexpr int VALU_STEPS = 512;
+
+template <int KIND>
+__global__ __launch_bounds__(PROBE_THREADS) void valu_rate_kernel(float* __restrict__ out, float seed) {
+    float v[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = seed + 0.01f * (float)(threadIdx.x + j);
+    const float b = seed * 0.5f, c = seed * 0.25f;
+    for (int i = 0; i < VALU_STEPS; ++i) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            if constexpr (KIND == 0) v[j] = __builtin_fmaf(v[j], b, c);            // v_fma_f32
+            if constexpr (KIND == 1) v[j] = __builtin_amdgcn_exp2f(-v[j]);          // v_exp_f32
+            if constexpr (KIND == 2) v[j] = __builtin_amdgcn_rcpf(v[j]);            // v_rcp_f32
+            if constexpr (KIND == 3) {                                              // v_mad_u64_u32 + v_xor
+                const uint64_t p = (uint64_t)__float_as_uint(v[j]) * 0xD2511F53u;
+                v[j] = __uint_as_float((uint32_t)(p >> 32) ^ (uint32_t)p);
+            }
+        }
+    }
+    float s = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) s += v[j];
+    out[(uint64_t)blockIdx.x * PROBE_THREADS + threadIdx.x] = s;
+}
+
 }  // namespace
+
+// kind 0..3 (fma, exp, rcp, mad64 + xor); out holds n_blocks * 256 floats
+const char* launch_valu_rate(int kind, float* out, uint32_t n_blocks, hipStream_t s) {
+    switch (kind) {
+        case 0: hipLaunchKernelGGL(valu_rate_kernel<0>, dim3(n_blocks), dim3(PROBE_THREADS), 0, s, out, 0.3f); break;
+        case 1: hipLaunchKernelGGL(valu_rate_kernel<1>, dim3(n_blocks), dim3(PROBE_THREADS), 0, s, out, 0.3f); break;
+        case 2: hipLaunchKernelGGL(valu_rate_kernel<2>, dim3(n_blocks), dim3(PROBE_THREADS), 0, s, out, 0.3f); break;
+        case 3: hipLaunchKernelGGL(valu_rate_kernel<3>, dim3(n_blocks), dim3(PROBE_THREADS), 0, s, out, 0.3f); break;
+        default: return "kind";
+    }
+    const hipError_t e = hipGetLastError();
+    return e == hipSuccess ? nullptr : hipGetErrorString(e);
+}
 
 // bits in {0, 1, 2, 4, 8}; 0 = reads only. Returns nullptr or the name of what failed.
 const char* launch_stream_mix(const void* x, const void* noise, void* codes, void* meta, uint64_t n_units, int bits,

@@ -345,6 +345,16 @@ int dopt_graph_replace_memsets(void* graph, int64_t* n_replaced);
 int dopt_stream_probe(const void* x, const void* noise, void* codes, void* meta, int64_t n_units, int bits,
                       void* stream);
 
+/*
+ * Diagnostic, no counterpart in the reference: the issue cost of one VALU instruction kind on
+ * this GPU, for the cost model of the instruction-bound kernels. Launches n_blocks workgroups of
+ * 256 lanes (4 waves); every lane runs 8 independent chains of 512 steps of kind 0 = v_fma_f32,
+ * 1 = v_exp_f32, 2 = v_rcp_f32, 3 = v_mad_u64_u32 + v_xor_b32 and writes one float to
+ * out[n_blocks * 256] (meaningless values). Time per wave-instruction per SIMD = launch time *
+ * (SIMDs) / (n_blocks * 4 * 8 * 512). n_blocks in [1, 65536].
+ */
+int dopt_valu_probe(int kind, float* out, int64_t n_blocks, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

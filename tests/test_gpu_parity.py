@@ -609,6 +609,21 @@ def test_stream_probe_rejects_bad_arguments():
     assert L.dopt_stream_probe(buf.data_ptr(), None, buf.data_ptr(), buf.data_ptr(), -1, 2, s) == _lib.EINVAL
 
 
+@pytest.mark.parametrize("kind", [0, 1, 2, 3])
+def test_valu_probe_runs(kind):
+    """dopt_valu_probe (the instruction-cost probe the benchmark reports) launches, finishes and
+    writes every output element."""
+    L = _lib.lib()
+    sentinel = 0x7FC0DEAD  # a NaN payload the probe's chains do not produce
+    out = torch.full((8 * 256,), sentinel, dtype=torch.int32, device="cuda")
+    s = torch.cuda.current_stream().cuda_stream
+    assert L.dopt_valu_probe(kind, out.data_ptr(), 8, s) == 0
+    torch.cuda.synchronize()
+    assert not (out == sentinel).any()
+    if kind < 3:  # float chains from positive seeds stay finite; kind 3 hashes bit patterns
+        assert torch.isfinite(out.view(torch.float32)).all()
+
+
 def test_beyond_2pow32_elements():
     """A bf16 activation of 2^32 + 2^24 elements (8.6 GB; g = 1024, 4,210,688 groups): element
     offsets past 2^32 take the kernels' 64-bit address arithmetic, and the Philox counter (the
