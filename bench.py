@@ -215,7 +215,9 @@ def counter_probe(name: str) -> int:
 def valu_probe() -> int:
     """Issue cost of one VALU instruction kind (dopt_valu_probe): ns per wave-instruction per SIMD
     for v_fma_f32, v_exp_f32, v_rcp_f32 and v_mad_u64_u32 + v_xor_b32, median of 5 event-timed
-    windows of 10 launches of 2048 workgroups (8192 waves, 4096 steps per lane)."""
+    windows of 10 launches of 2048 workgroups (8192 waves, 4096 steps per lane); then the
+    sustained bf16 MFMA rate of the weight-gradient GEMM's inner-loop shape with random and with
+    constant operands."""
     import torch
 
     import deep_optimization_amd  # noqa: F401
@@ -229,7 +231,8 @@ def valu_probe() -> int:
     simds = torch.cuda.get_device_properties(dev).multi_processor_count * 4
     per_simd = blocks * 4 * 8 * 512 / simds  # wave-instructions per SIMD per launch
     res = {}
-    for kind, name in enumerate(("v_fma_f32", "v_exp_f32", "v_rcp_f32", "v_mad_u64_u32+v_xor_b32")):
+    for kind, name in enumerate(("v_fma_f32", "v_exp_f32", "v_rcp_f32", "v_mad_u64_u32+v_xor_b32", "mfma_bf16_random",
+                                 "mfma_bf16_constant")):
         fn = lambda kind=kind: _lib.check(L.dopt_valu_probe(kind, out.data_ptr(), blocks, st.cuda_stream),  # noqa: E731
                                           "valu_probe")
         for _ in range(3):
@@ -244,7 +247,11 @@ def valu_probe() -> int:
             e1.synchronize()
             ts.append(e0.elapsed_time(e1) / 10 * 1e3)
         us = statistics.median(ts)
-        res[name] = {"us_per_launch": round(us, 2), "ns_per_wave_instruction": round(us * 1e3 / per_simd, 4)}
+        if kind < 4:
+            res[name] = {"us_per_launch": round(us, 2), "ns_per_wave_instruction": round(us * 1e3 / per_simd, 4)}
+        else:
+            tf = blocks * 4 * 64 * 16 * 32768 / us / 1e6
+            res[name] = {"us_per_launch": round(us, 2), "TFLOP/s": round(tf, 1), "frac_bf16_peak": round(tf / 2500.0, 4)}
     print(json.dumps({"valu_probe": res, "simds": simds}))
     return 0
 

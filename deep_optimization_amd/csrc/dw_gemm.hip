@@ -342,10 +342,20 @@ struct V2Codes {
     static constexpr int LOADS = BITS ? 4 + NC + 2 : 8;        // DMAs per thread per step
 };
 
-template <int BITS, bool DB>
-__global__ __launch_bounds__(THREADS, 1) void dw_gemm_v2_kernel(DwArgs a) {
+// NW waves per workgroup: 4 (2 x 2, 128 x 128 per wave: 256 accumulators, one wave per SIMD) or,
+// for bf16 x_hat, 8 (2 x 4, 128 x 64 per wave: 128 accumulators, two waves per SIMD, so one
+// wave's MFMAs run while the other waits at the slab barrier or on its operand reads). The
+// workgroup tile, the DMA ring and the order of the MFMA steps are the same either way.
+template <int BITS, bool DB, int NW>
+__global__ __launch_bounds__(64 * NW, 1) void dw_gemm_v2_kernel(DwArgs a) {
     static_assert(BITS == 0 || BITS == 1 || BITS == 2 || BITS == 4, "bf16, or 1/2/4-bit codes");
+    static_assert(NW == 4 || (NW == 8 && BITS == 0), "8 waves for bf16 x_hat only");
     using CS = V2Codes<BITS>;
+    constexpr int WN = NW / 2;            // waves along n
+    constexpr int CW = BN / WN;           // columns per wave
+    constexpr int TNW = CW / 32;          // 32 x 32 blocks per wave along n
+    constexpr int JJ = 16 / NW;           // 1 KB DMA blocks per wave per operand tile
+    constexpr int LD = BITS == 0 ? 2 * JJ : CS::LOADS;  // DMAs per wave per slab
     __shared__ __attribute__((aligned(1024))) char sa0[V2_TILE];
     __shared__ __attribute__((aligned(1024))) char sa1[V2_TILE];
     __shared__ __attribute__((aligned(1024))) char sa2[V2_TILE];
@@ -373,9 +383,9 @@ __global__ __launch_bounds__(THREADS, 1) void dw_gemm_v2_kernel(DwArgs a) {
     const int nk = (int)(kt1 - kt0);
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
+    const int wm = wave / WN, wn = wave % WN;
 
-    // global -> LDS: instruction j of wave w fills 1 KB block b = 4j + w of a tile = rows 2b, 2b+1;
+    // global -> LDS: instruction j of wave w fills 1 KB block b = NW j + w of a tile = rows 2b, 2b+1;
     // lane l -> row 2b + l/32, position l % 32 <- global chunk (l % 32) ^ (4 * (row % 4)).
     // The global address is a wave-uniform slab base plus a loop-invariant 32-bit lane offset.
     // The LDS offsets carry `opaque0`, a zero the compiler cannot see through: its wait insertion
@@ -383,10 +393,10 @@ __global__ __launch_bounds__(THREADS, 1) void dw_gemm_v2_kernel(DwArgs a) {
     // disjoint from that load's bytes would otherwise wait for every load in flight.
     int opaque0;
     asm volatile("s_mov_b32 %0, 0" : "=s"(opaque0));
-    uint32_t offa[4], offb[4];
+    uint32_t offa[JJ], offb[JJ];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int r = 2 * (4 * j + wave) + (lane >> 5), c = (lane & 31) ^ ((r & 3) << 2);
+    for (int j = 0; j < JJ; ++j) {
+        const int r = 2 * (NW * j + wave) + (lane >> 5), c = (lane & 31) ^ ((r & 3) << 2);
         offa[j] = (uint32_t)(r * a.ldd + c * 8) * 2u;
         offb[j] = (uint32_t)(r * a.ldx + c * 8) * 2u;
     }
@@ -399,15 +409,15 @@ __global__ __launch_bounds__(THREADS, 1) void dw_gemm_v2_kernel(DwArgs a) {
         const char* ga = (const char*)(a.dy + kt * V2_BK * a.ldd + m0);
         char* da = sa + opaque0;
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-            __builtin_amdgcn_global_load_lds((gbl_void_t*)(ga + offa[j]), (lds_void_t*)(da + (4 * j + wave) * 1024), 16,
-                                             0, 0);
+        for (int j = 0; j < JJ; ++j)
+            __builtin_amdgcn_global_load_lds((gbl_void_t*)(ga + offa[j]), (lds_void_t*)(da + (NW * j + wave) * 1024),
+                                             16, 0, 0);
         if constexpr (BITS == 0) {
             const char* gb = (const char*)(a.xh + kt * V2_BK * a.ldx + n0);
             char* db = sb + opaque0;
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
-                __builtin_amdgcn_global_load_lds((gbl_void_t*)(gb + offb[j]), (lds_void_t*)(db + (4 * j + wave) * 1024),
+            for (int j = 0; j < JJ; ++j)
+                __builtin_amdgcn_global_load_lds((gbl_void_t*)(gb + offb[j]), (lds_void_t*)(db + (NW * j + wave) * 1024),
                                                  16, 0, 0);
         } else {
             const int64_t e0 = kt * V2_BK * a.N + n0;  // a multiple of 256
@@ -472,11 +482,11 @@ __global__ __launch_bounds__(THREADS, 1) void dw_gemm_v2_kernel(DwArgs a) {
         }
     };
 
-    f32x16_t acc[TM][TN];
+    f32x16_t acc[TM][TNW];
 #pragma unroll
     for (int i = 0; i < TM; ++i)
 #pragma unroll
-        for (int j = 0; j < TN; ++j)
+        for (int j = 0; j < TNW; ++j)
 #pragma unroll
             for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
     // bias gradient from the dy fragments already in registers: lane l of fragment ii holds
@@ -485,12 +495,12 @@ __global__ __launch_bounds__(THREADS, 1) void dw_gemm_v2_kernel(DwArgs a) {
     float dbacc[TM] = {};
     const bool db_wave = DB && tn == 0 && wn == 0;
 
-    uint4 fa0[TM], fb0[TN], fa1[TM], fb1[TN];
+    uint4 fa0[TM], fb0[TNW], fa1[TM], fb1[TNW];
     auto read_frags = [&](const char* sa, const char* sb, int kk, uint4* fa, uint4* fb) {
 #pragma unroll
         for (int ii = 0; ii < TM; ++ii) fa[ii] = v2_frag(sa, kk, wm * 128 + ii * 32, lane);
 #pragma unroll
-        for (int jj = 0; jj < TN; ++jj) fb[jj] = v2_frag(sb, kk, wn * 128 + jj * 32, lane);
+        for (int jj = 0; jj < TNW; ++jj) fb[jj] = v2_frag(sb, kk, wn * CW + jj * 32, lane);
     };
     // bias-gradient pairs of fragment row ii
     auto db_row = [&](const uint4* fa, int ii) {
@@ -505,7 +515,7 @@ __global__ __launch_bounds__(THREADS, 1) void dw_gemm_v2_kernel(DwArgs a) {
     // the MFMAs of fragment row ii
     auto mma_row = [&](const uint4* fa, const uint4* fb, int ii) {
 #pragma unroll
-        for (int jj = 0; jj < TN; ++jj) acc[ii][jj] = mfma_bf16(fa[ii], fb[jj], acc[ii][jj]);
+        for (int jj = 0; jj < TNW; ++jj) acc[ii][jj] = mfma_bf16(fa[ii], fb[jj], acc[ii][jj]);
     };
     auto mma = [&](const uint4* fa, const uint4* fb) {
 #pragma unroll
@@ -513,19 +523,23 @@ __global__ __launch_bounds__(THREADS, 1) void dw_gemm_v2_kernel(DwArgs a) {
 #pragma unroll
         for (int ii = 0; ii < TM; ++ii) db_row(fa, ii);
     };
-    constexpr int NM = TM * TN;            // MFMAs per 16 tokens
-    constexpr int NR = 2 * (TM + TN);      // transposing reads per 16 tokens
+    constexpr int NM = TM * TNW;           // MFMAs per 16 tokens
+    constexpr int NR = 2 * (TM + TNW);     // transposing reads per 16 tokens
     // step i: slab i in stage (ca, cb), its code slot cc; slab i+1 in (na, nb), its codes in slot
     // nc (packed x_hat: decoded into nb here, before the barrier that publishes it)
     auto step = [&](char* ca, char* cb, char* cc, char* na, char* nb, const char* nc, int i) {
         if constexpr (BITS == 0) {
+            // the transposing reads of the slab's second half go out two per MFMA over the first
+            // half of the MFMAs, so they have returned by the wait before the barrier (one per
+            // MFMA left the last read's latency exposed there)
             read_frags(ca, cb, 1, fa1, fb1);
             mma(fa0, fb0);
 #pragma unroll
-            for (int q = 0; q < NR; ++q) {
+            for (int q = 0; q < NR / 2; ++q) {
+                __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // two LDS reads
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
-                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
             }
+            __builtin_amdgcn_sched_group_barrier(0x008, NM - NR / 2, 0);  // the other MFMAs
         } else {
             // codes first (their wait then leaves the operand reads in flight), and the decode
             // of slab i+1 in four pieces between the four MFMA rows, fenced so that the VALU work
@@ -542,7 +556,7 @@ __global__ __launch_bounds__(THREADS, 1) void dw_gemm_v2_kernel(DwArgs a) {
             }
         }
         if constexpr (BITS == 0)
-            wait_vm_lds<16>();  // slab i+1 landed (slabs i+2, i+3 may stay in flight)
+            wait_vm_lds<2 * LD>();  // slab i+1 landed (slabs i+2, i+3 may stay in flight)
         else
             wait_vm_lds<CS::LOADS>();  // slab i+2 landed (slab i+3 may stay in flight)
         barrier_only();
@@ -553,7 +567,7 @@ __global__ __launch_bounds__(THREADS, 1) void dw_gemm_v2_kernel(DwArgs a) {
         for (int q = 0; q < NM; ++q) {
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
             __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
-            if (q < CS::LOADS) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // one global load
+            if (q < LD) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // one global load
         }
     };
 
@@ -563,7 +577,7 @@ __global__ __launch_bounds__(THREADS, 1) void dw_gemm_v2_kernel(DwArgs a) {
         issue(sa2, sb2, sc2, kt0 + 2);
         issue(sa3, sb3, sc3, kt0 + 3);
         if constexpr (BITS == 0) {
-            wait_vm_lds<3 * CS::LOADS>();
+            wait_vm_lds<3 * LD>();
         } else {
             // slab 0 is decoded here, slab i+1 in step i (its loads landed by step i-1's wait)
             wait_vm_lds<2 * CS::LOADS>();
@@ -592,8 +606,8 @@ __global__ __launch_bounds__(THREADS, 1) void dw_gemm_v2_kernel(DwArgs a) {
 #pragma unroll
     for (int i = 0; i < TM; ++i)
 #pragma unroll
-        for (int j = 0; j < TN; ++j) {
-            const int64_t col = n0 + wn * 128 + j * 32 + (lane & 31);
+        for (int j = 0; j < TNW; ++j) {
+            const int64_t col = n0 + wn * CW + j * 32 + (lane & 31);
 #pragma unroll
             for (int v = 0; v < 16; ++v) {
                 const int64_t row = m0 + wm * 128 + i * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
@@ -728,15 +742,15 @@ int launch_dw_gemm(DwArgs a, int mode, bool with_db, float* out32, uint16_t* out
         a.db_partial = a.partial + (int64_t)splits * a.M * a.N;
         const int64_t W = (a.M / BM) * (a.N / BN) * used;
         const dim3 grid((unsigned)(DW_XCDS * ((W + DW_XCDS - 1) / DW_XCDS)));
-#define DOPT_DW2(BITS_)                                                                              \
-    do {                                                                                             \
-        if (with_db) hipLaunchKernelGGL((dw_gemm_v2_kernel<BITS_, true>), grid, dim3(THREADS), 0, st, a);  \
-        else hipLaunchKernelGGL((dw_gemm_v2_kernel<BITS_, false>), grid, dim3(THREADS), 0, st, a);         \
+#define DOPT_DW2(BITS_, NW_)                                                                                   \
+    do {                                                                                                       \
+        if (with_db) hipLaunchKernelGGL((dw_gemm_v2_kernel<BITS_, true, NW_>), grid, dim3(64 * NW_), 0, st, a); \
+        else hipLaunchKernelGGL((dw_gemm_v2_kernel<BITS_, false, NW_>), grid, dim3(64 * NW_), 0, st, a);        \
     } while (0)
-        if (mode == DW_B_BF16) DOPT_DW2(0);
-        else if (a.bits == 1) DOPT_DW2(1);
-        else if (a.bits == 2) DOPT_DW2(2);
-        else DOPT_DW2(4);
+        if (mode == DW_B_BF16) DOPT_DW2(0, 4);
+        else if (a.bits == 1) DOPT_DW2(1, 4);
+        else if (a.bits == 2) DOPT_DW2(2, 4);
+        else DOPT_DW2(4, 4);
 #undef DOPT_DW2
         launch_dw_reduce(a.partial, used, a.M * a.N, out32, out16, a.db_partial, a.M, with_db ? db : nullptr, st);
         return 0;

@@ -76,11 +76,57 @@ __global__ __launch_bounds__(PROBE_THREADS) void valu_rate_kernel(float* __restr
     out[(uint64_t)blockIdx.x * PROBE_THREADS + threadIdx.x] = s;
 }
 
+// MFMA-stream probe in the shape of the weight-gradient GEMM's inner loop: each wave keeps a 4 x 4
+// grid of 32 x 32 fp32 accumulators (256 per lane, one wave per SIMD) and per step issues the 16
+// v_mfma_f32_32x32x16_bf16 acc[i][j] += A[i] B[j], with nothing else in the loop. RANDOM: the 4 + 4
+// operand fragments hold pseudo-random bf16 values in (-1, 1) that differ per lane and fragment;
+// otherwise every fragment is one constant. The operand data changes the sustained MFMA rate.
+constexpr int MFMA_STEPS = 64;
+typedef __bf16 probe_bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float probe_f32x16_t __attribute__((ext_vector_type(16)));
+
+template <bool RANDOM>
+__global__ __launch_bounds__(PROBE_THREADS, 1) void mfma_rate_kernel(float* __restrict__ out) {
+    probe_bf16x8_t a[4], b[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            uint32_t h = (threadIdx.x * 8u + (uint32_t)e) * 2654435761u ^ (uint32_t)(i + 1) * 40503u;
+            h ^= h >> 15;
+            const float ra = RANDOM ? (float)(h & 0xffffu) / 32768.0f - 1.0f : 0.5f;
+            const float rb = RANDOM ? (float)(h >> 16) / 32768.0f - 1.0f : 0.5f;
+            a[i][e] = (__bf16)ra;
+            b[i][e] = (__bf16)rb;
+        }
+    probe_f32x16_t acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
+    for (int st = 0; st < MFMA_STEPS; ++st)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
+    float t = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) t += acc[i][j][0] + acc[i][j][15];
+    out[(uint64_t)blockIdx.x * PROBE_THREADS + threadIdx.x] = t;
+}
+
 }  // namespace
 
-// kind 0..3 (fma, exp, rcp, mad64 + xor); out holds n_blocks * 256 floats
+// kind 0..3 (fma, exp, rcp, mad64 + xor), 4 / 5 (bf16 MFMA stream, random / constant operands);
+// out holds n_blocks * 256 floats
 const char* launch_valu_rate(int kind, float* out, uint32_t n_blocks, hipStream_t s) {
     switch (kind) {
+        case 4: hipLaunchKernelGGL(mfma_rate_kernel<true>, dim3(n_blocks), dim3(PROBE_THREADS), 0, s, out); break;
+        case 5: hipLaunchKernelGGL(mfma_rate_kernel<false>, dim3(n_blocks), dim3(PROBE_THREADS), 0, s, out); break;
         case 0: hipLaunchKernelGGL(valu_rate_kernel<0>, dim3(n_blocks), dim3(PROBE_THREADS), 0, s, out, 0.3f); break;
         case 1: hipLaunchKernelGGL(valu_rate_kernel<1>, dim3(n_blocks), dim3(PROBE_THREADS), 0, s, out, 0.3f); break;
         case 2: hipLaunchKernelGGL(valu_rate_kernel<2>, dim3(n_blocks), dim3(PROBE_THREADS), 0, s, out, 0.3f); break;

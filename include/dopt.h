@@ -351,7 +351,10 @@ int dopt_stream_probe(const void* x, const void* noise, void* codes, void* meta,
  * 256 lanes (4 waves); every lane runs 8 independent chains of 512 steps of kind 0 = v_fma_f32,
  * 1 = v_exp_f32, 2 = v_rcp_f32, 3 = v_mad_u64_u32 + v_xor_b32 and writes one float to
  * out[n_blocks * 256] (meaningless values). Time per wave-instruction per SIMD = launch time *
- * (SIMDs) / (n_blocks * 4 * 8 * 512). n_blocks in [1, 65536].
+ * (SIMDs) / (n_blocks * 4 * 8 * 512). Kinds 4 and 5 instead stream v_mfma_f32_32x32x16_bf16 in
+ * the weight-gradient GEMM's inner-loop shape (a 4 x 4 grid of accumulators per wave, one wave per
+ * SIMD, 64 steps of 16 MFMAs, nothing else), with pseudo-random (4) or constant (5) operands:
+ * n_blocks * 4 * 64 * 16 * 32768 flops per launch. n_blocks in [1, 65536].
  */
 int dopt_valu_probe(int kind, float* out, int64_t n_blocks, void* stream);
 
