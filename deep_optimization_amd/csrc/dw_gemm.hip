@@ -280,6 +280,7 @@ __device__ __forceinline__ void wait_vm() {
 
 // 8 bf16 of one MFMA operand: column `col` of the stage tile (lane's column within the 32-wide
 // fragment applied by the transpose), rows kk*16 + 8*(g/2) + {0..7}
+template <int RB>  // LDS row pitch in bytes (512: 256-column tiles, 256: 128-column tiles)
 __device__ __forceinline__ uint4 v2_frag(const char* tile, int kk, int col0, int lane) {
     const int g = lane >> 4, t = lane & 15, u = t >> 2, v = t & 3;
     const int colw = col0 + 16 * (g & 1) + 4 * v;  // first of the 4 columns this lane reads
@@ -287,7 +288,7 @@ __device__ __forceinline__ uint4 v2_frag(const char* tile, int kk, int col0, int
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
         const int r = kk * 16 + 8 * (g >> 1) + 4 * h + u;
-        const char* p = tile + r * V2_ROWB + v2_pos(r, colw >> 3) + ((colw & 4) << 1);
+        const char* p = tile + r * RB + v2_pos(r, colw >> 3) + ((colw & 4) << 1);
         const v4i16_t x = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t*)p);
         const uint32_t lo = (uint32_t)(uint16_t)x[0] | ((uint32_t)(uint16_t)x[1] << 16);
         const uint32_t hi = (uint32_t)(uint16_t)x[2] | ((uint32_t)(uint16_t)x[3] << 16);
@@ -339,14 +340,15 @@ struct V2Codes {
     static constexpr int NC = BITS == 2 ? 2 : 1;             // code DMAs per thread per slab
     static constexpr int CODE_BYTES = BITS ? 1024 * BITS : 0;  // codes of one slab
     static constexpr int SLOT = BITS ? CODE_BYTES + 2048 : 16;  // + scale and min dwords (4 B per thread each)
-    static constexpr int LOADS = BITS ? 4 + NC + 2 : 8;        // DMAs per thread per step
 };
 
 // NW waves per workgroup: 4 (2 x 2, 128 x 128 per wave: 256 accumulators, one wave per SIMD) or,
 // for bf16 x_hat, 8 (2 x 4, 128 x 64 per wave: 128 accumulators, two waves per SIMD, so one
 // wave's MFMAs run while the other waits at the slab barrier or on its operand reads). The
 // workgroup tile, the DMA ring and the order of the MFMA steps are the same either way.
-template <int BITS, bool DB, int NW>
+// BMT: output rows per workgroup tile, 256 or (for small outputs, so fewer K splits fill the GPU
+// and fewer split partials go through HBM) 128; the waves then cover 64 rows each.
+template <int BITS, bool DB, int NW, int BMT>
 __global__ __launch_bounds__(64 * NW, 1) void dw_gemm_v2_kernel(DwArgs a) {
     static_assert(BITS == 0 || BITS == 1 || BITS == 2 || BITS == 4, "bf16, or 1/2/4-bit codes");
     static_assert(NW == 4 || (NW == 8 && BITS == 0), "8 waves for bf16 x_hat only");
@@ -354,12 +356,20 @@ __global__ __launch_bounds__(64 * NW, 1) void dw_gemm_v2_kernel(DwArgs a) {
     constexpr int WN = NW / 2;            // waves along n
     constexpr int CW = BN / WN;           // columns per wave
     constexpr int TNW = CW / 32;          // 32 x 32 blocks per wave along n
-    constexpr int JJ = 16 / NW;           // 1 KB DMA blocks per wave per operand tile
-    constexpr int LD = BITS == 0 ? 2 * JJ : CS::LOADS;  // DMAs per wave per slab
-    __shared__ __attribute__((aligned(1024))) char sa0[V2_TILE];
-    __shared__ __attribute__((aligned(1024))) char sa1[V2_TILE];
-    __shared__ __attribute__((aligned(1024))) char sa2[V2_TILE];
-    __shared__ __attribute__((aligned(1024))) char sa3[V2_TILE];
+    constexpr int JJ = 16 / NW;           // 1 KB DMA blocks per wave per x_hat tile
+    static_assert(BMT == 256 || BMT == 128, "tile rows");
+    constexpr int RA = BMT * 2;           // bytes per LDS row of a dy tile
+    constexpr int TILE_A = V2_BK * RA;    // bytes of one dy tile
+    constexpr int JA = TILE_A / 1024 / NW;  // 1 KB DMA blocks per wave per dy tile
+    constexpr int RPB = 1024 / RA;        // dy rows per 1 KB block
+    constexpr int LPR = RA / 16;          // lanes per dy row
+    constexpr int RW = BMT / 2;           // rows per wave (2 waves along m)
+    constexpr int TMW = RW / 32;          // 32 x 32 blocks per wave along m
+    constexpr int LD = BITS == 0 ? JA + JJ : JA + CS::NC + 2;  // DMAs per wave per slab
+    __shared__ __attribute__((aligned(1024))) char sa0[TILE_A];
+    __shared__ __attribute__((aligned(1024))) char sa1[TILE_A];
+    __shared__ __attribute__((aligned(1024))) char sa2[TILE_A];
+    __shared__ __attribute__((aligned(1024))) char sa3[TILE_A];
     __shared__ __attribute__((aligned(1024))) char sb0[V2_TILE];
     __shared__ __attribute__((aligned(1024))) char sb1[V2_TILE];
     __shared__ __attribute__((aligned(1024))) char sb2[V2_TILE];
@@ -369,7 +379,7 @@ __global__ __launch_bounds__(64 * NW, 1) void dw_gemm_v2_kernel(DwArgs a) {
     __shared__ __attribute__((aligned(1024))) char sc2[CS::SLOT];
     __shared__ __attribute__((aligned(1024))) char sc3[CS::SLOT];
 
-    const int tiles_n = (int)(a.N / BN), tiles = (int)(a.M / BM) * tiles_n;
+    const int tiles_n = (int)(a.N / BN), tiles = (int)(a.M / BMT) * tiles_n;
     const int W = tiles * a.splits, per = (W + DW_XCDS - 1) / DW_XCDS;
     const int xcd = blockIdx.x % DW_XCDS, local = blockIdx.x / DW_XCDS;
     if (local >= per) return;
@@ -377,7 +387,7 @@ __global__ __launch_bounds__(64 * NW, 1) void dw_gemm_v2_kernel(DwArgs a) {
     if (L >= W) return;
     const int split = L / tiles, t = L % tiles;
     const int tm = t / tiles_n, tn = t % tiles_n;
-    const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
+    const int64_t m0 = (int64_t)tm * BMT, n0 = (int64_t)tn * BN;
     const int64_t kt0 = (int64_t)split * a.kt_per_split;
     const int64_t kt1 = min(kt0 + a.kt_per_split, a.K / V2_BK);
     const int nk = (int)(kt1 - kt0);
@@ -393,11 +403,16 @@ __global__ __launch_bounds__(64 * NW, 1) void dw_gemm_v2_kernel(DwArgs a) {
     // disjoint from that load's bytes would otherwise wait for every load in flight.
     int opaque0;
     asm volatile("s_mov_b32 %0, 0" : "=s"(opaque0));
-    uint32_t offa[JJ], offb[JJ];
+    // (a dy tile of 128 columns has 256-byte rows: 4 rows per block, 16 lanes per row)
+    uint32_t offa[JA], offb[JJ];
+#pragma unroll
+    for (int j = 0; j < JA; ++j) {
+        const int r = RPB * (NW * j + wave) + lane / LPR, c = (lane % LPR) ^ ((r & 3) << 2);
+        offa[j] = (uint32_t)(r * a.ldd + c * 8) * 2u;
+    }
 #pragma unroll
     for (int j = 0; j < JJ; ++j) {
         const int r = 2 * (NW * j + wave) + (lane >> 5), c = (lane & 31) ^ ((r & 3) << 2);
-        offa[j] = (uint32_t)(r * a.ldd + c * 8) * 2u;
         offb[j] = (uint32_t)(r * a.ldx + c * 8) * 2u;
     }
     // packed x_hat: this thread's decode row and column run, and its flat element offset in a slab
@@ -409,7 +424,7 @@ __global__ __launch_bounds__(64 * NW, 1) void dw_gemm_v2_kernel(DwArgs a) {
         const char* ga = (const char*)(a.dy + kt * V2_BK * a.ldd + m0);
         char* da = sa + opaque0;
 #pragma unroll
-        for (int j = 0; j < JJ; ++j)
+        for (int j = 0; j < JA; ++j)
             __builtin_amdgcn_global_load_lds((gbl_void_t*)(ga + offa[j]), (lds_void_t*)(da + (NW * j + wave) * 1024),
                                              16, 0, 0);
         if constexpr (BITS == 0) {
@@ -482,9 +497,9 @@ __global__ __launch_bounds__(64 * NW, 1) void dw_gemm_v2_kernel(DwArgs a) {
         }
     };
 
-    f32x16_t acc[TM][TNW];
+    f32x16_t acc[TMW][TNW];
 #pragma unroll
-    for (int i = 0; i < TM; ++i)
+    for (int i = 0; i < TMW; ++i)
 #pragma unroll
         for (int j = 0; j < TNW; ++j)
 #pragma unroll
@@ -492,15 +507,15 @@ __global__ __launch_bounds__(64 * NW, 1) void dw_gemm_v2_kernel(DwArgs a) {
     // bias gradient from the dy fragments already in registers: lane l of fragment ii holds
     // column (l % 32) at 8 consecutive tokens as 4 bf16 pairs, and one v_dot2 with (1, 1) adds a
     // pair. Only the waves with wn == 0 of the workgroups with tn == 0 (one per dy tile) sum.
-    float dbacc[TM] = {};
+    float dbacc[TMW] = {};
     const bool db_wave = DB && tn == 0 && wn == 0;
 
-    uint4 fa0[TM], fb0[TNW], fa1[TM], fb1[TNW];
+    uint4 fa0[TMW], fb0[TNW], fa1[TMW], fb1[TNW];
     auto read_frags = [&](const char* sa, const char* sb, int kk, uint4* fa, uint4* fb) {
 #pragma unroll
-        for (int ii = 0; ii < TM; ++ii) fa[ii] = v2_frag(sa, kk, wm * 128 + ii * 32, lane);
+        for (int ii = 0; ii < TMW; ++ii) fa[ii] = v2_frag<RA>(sa, kk, wm * RW + ii * 32, lane);
 #pragma unroll
-        for (int jj = 0; jj < TNW; ++jj) fb[jj] = v2_frag(sb, kk, wn * CW + jj * 32, lane);
+        for (int jj = 0; jj < TNW; ++jj) fb[jj] = v2_frag<V2_ROWB>(sb, kk, wn * CW + jj * 32, lane);
     };
     // bias-gradient pairs of fragment row ii
     auto db_row = [&](const uint4* fa, int ii) {
@@ -519,12 +534,12 @@ __global__ __launch_bounds__(64 * NW, 1) void dw_gemm_v2_kernel(DwArgs a) {
     };
     auto mma = [&](const uint4* fa, const uint4* fb) {
 #pragma unroll
-        for (int ii = 0; ii < TM; ++ii) mma_row(fa, fb, ii);
+        for (int ii = 0; ii < TMW; ++ii) mma_row(fa, fb, ii);
 #pragma unroll
-        for (int ii = 0; ii < TM; ++ii) db_row(fa, ii);
+        for (int ii = 0; ii < TMW; ++ii) db_row(fa, ii);
     };
-    constexpr int NM = TM * TNW;           // MFMAs per 16 tokens
-    constexpr int NR = 2 * (TM + TNW);     // transposing reads per 16 tokens
+    constexpr int NM = TMW * TNW;          // MFMAs per 16 tokens
+    constexpr int NR = 2 * (TMW + TNW);    // transposing reads per 16 tokens
     // step i: slab i in stage (ca, cb), its code slot cc; slab i+1 in (na, nb), its codes in slot
     // nc (packed x_hat: decoded into nb here, before the barrier that publishes it)
     auto step = [&](char* ca, char* cb, char* cc, char* na, char* nb, const char* nc, int i) {
@@ -542,23 +557,23 @@ __global__ __launch_bounds__(64 * NW, 1) void dw_gemm_v2_kernel(DwArgs a) {
             __builtin_amdgcn_sched_group_barrier(0x008, NM - NR / 2, 0);  // the other MFMAs
         } else {
             // codes first (their wait then leaves the operand reads in flight), and the decode
-            // of slab i+1 in four pieces between the four MFMA rows, fenced so that the VALU work
-            // runs beside the matrix pipe instead of before it
+            // of slab i+1 in four pieces between the MFMA rows, fenced so that the VALU work runs
+            // beside the matrix pipe instead of before it
             const DecodeIn din = decode_load(nc, kt0 + i + 1);
             read_frags(ca, cb, 1, fa1, fb1);
 #pragma unroll
-            for (int ii = 0; ii < TM; ++ii) {
-                mma_row(fa0, fb0, ii);
+            for (int c = 0; c < 4; ++c) {
+                if (c < TMW) mma_row(fa0, fb0, c);
                 __builtin_amdgcn_sched_barrier(0);
-                decode_chunk(din, nb, ii);
-                db_row(fa0, ii);
+                decode_chunk(din, nb, c);
+                if (c < TMW) db_row(fa0, c);
                 __builtin_amdgcn_sched_barrier(0);
             }
         }
         if constexpr (BITS == 0)
             wait_vm_lds<2 * LD>();  // slab i+1 landed (slabs i+2, i+3 may stay in flight)
         else
-            wait_vm_lds<CS::LOADS>();  // slab i+2 landed (slab i+3 may stay in flight)
+            wait_vm_lds<LD>();  // slab i+2 landed (slab i+3 may stay in flight)
         barrier_only();
         issue(ca, cb, cc, kt0 + i + 4);
         read_frags(na, nb, 0, fa0, fb0);
@@ -580,11 +595,11 @@ __global__ __launch_bounds__(64 * NW, 1) void dw_gemm_v2_kernel(DwArgs a) {
             wait_vm_lds<3 * LD>();
         } else {
             // slab 0 is decoded here, slab i+1 in step i (its loads landed by step i-1's wait)
-            wait_vm_lds<2 * CS::LOADS>();
+            wait_vm_lds<2 * LD>();
             const DecodeIn din = decode_load(sc0, kt0);
 #pragma unroll
             for (int c = 0; c < 4; ++c) decode_chunk(din, sb0, c);
-            wait_vm_lds<2 * CS::LOADS>();
+            wait_vm_lds<2 * LD>();
         }
         barrier_only();
         read_frags(sa0, sb0, 0, fa0, fb0);
@@ -604,22 +619,22 @@ __global__ __launch_bounds__(64 * NW, 1) void dw_gemm_v2_kernel(DwArgs a) {
 
     float* P = a.partial + (int64_t)split * a.M * a.N;
 #pragma unroll
-    for (int i = 0; i < TM; ++i)
+    for (int i = 0; i < TMW; ++i)
 #pragma unroll
         for (int j = 0; j < TNW; ++j) {
             const int64_t col = n0 + wn * CW + j * 32 + (lane & 31);
 #pragma unroll
             for (int v = 0; v < 16; ++v) {
-                const int64_t row = m0 + wm * 128 + i * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+                const int64_t row = m0 + wm * RW + i * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
                 P[row * a.N + col] = acc[i][j][v];
             }
         }
     if (db_wave) {
         // lanes l and l + 32 hold the two token halves of column l % 32
 #pragma unroll
-        for (int ii = 0; ii < TM; ++ii) {
+        for (int ii = 0; ii < TMW; ++ii) {
             const float other = __shfl_xor(dbacc[ii], 32);
-            if (lane < 32) a.db_partial[(int64_t)split * a.M + m0 + wm * 128 + ii * 32 + lane] = dbacc[ii] + other;
+            if (lane < 32) a.db_partial[(int64_t)split * a.M + m0 + wm * RW + ii * 32 + lane] = dbacc[ii] + other;
         }
     }
 }
@@ -705,8 +720,13 @@ void launch_dw_reduce(const float* partial, int used, int64_t MN, float* out32, 
 
 }  // namespace
 
+// Output rows per workgroup of the pipelined kernel: 128 when 256 x 256 tiles would number 16 or
+// fewer (the split count, and with it the fp32 split partials written and read back, halves).
+int dw_tile_rows(int64_t M, int64_t N) { return (M / 256) * (N / 256) <= 16 ? 128 : 256; }
+
 int dw_splits(int64_t M, int64_t N, int64_t K) {
-    const int64_t tiles = std::max<int64_t>((M / BM) * (N / BN), 1);
+    // the same for every kernel of a shape, so all of them split K at the same token boundaries
+    const int64_t tiles = std::max<int64_t>((M / dw_tile_rows(M, N)) * (N / BN), 1);
     const int64_t kts = (K + BK - 1) / BK;
     // one round of at most 256 workgroups (one per CU: 128 KB of LDS each)
     int64_t s = std::max<int64_t>(256 / tiles, 1);
@@ -740,18 +760,25 @@ int launch_dw_gemm(DwArgs a, int mode, bool with_db, float* out32, uint16_t* out
         const int used = (int)((kts + a.kt_per_split - 1) / a.kt_per_split);
         a.splits = used;
         a.db_partial = a.partial + (int64_t)splits * a.M * a.N;
-        const int64_t W = (a.M / BM) * (a.N / BN) * used;
+        const int bmt = dw_tile_rows(a.M, a.N);
+        const int64_t W = (a.M / bmt) * (a.N / BN) * used;
         const dim3 grid((unsigned)(DW_XCDS * ((W + DW_XCDS - 1) / DW_XCDS)));
-#define DOPT_DW2(BITS_, NW_)                                                                                   \
-    do {                                                                                                       \
-        if (with_db) hipLaunchKernelGGL((dw_gemm_v2_kernel<BITS_, true, NW_>), grid, dim3(64 * NW_), 0, st, a); \
-        else hipLaunchKernelGGL((dw_gemm_v2_kernel<BITS_, false, NW_>), grid, dim3(64 * NW_), 0, st, a);        \
+#define DOPT_DW2T(BITS_, BMT_)                                                                                     \
+    do {                                                                                                           \
+        if (with_db) hipLaunchKernelGGL((dw_gemm_v2_kernel<BITS_, true, 4, BMT_>), grid, dim3(256), 0, st, a);      \
+        else hipLaunchKernelGGL((dw_gemm_v2_kernel<BITS_, false, 4, BMT_>), grid, dim3(256), 0, st, a);             \
     } while (0)
-        if (mode == DW_B_BF16) DOPT_DW2(0, 4);
-        else if (a.bits == 1) DOPT_DW2(1, 4);
-        else if (a.bits == 2) DOPT_DW2(2, 4);
-        else DOPT_DW2(4, 4);
+#define DOPT_DW2(BITS_)                          \
+    do {                                         \
+        if (bmt == 128) DOPT_DW2T(BITS_, 128);   \
+        else DOPT_DW2T(BITS_, 256);              \
+    } while (0)
+        if (mode == DW_B_BF16) DOPT_DW2(0);
+        else if (a.bits == 1) DOPT_DW2(1);
+        else if (a.bits == 2) DOPT_DW2(2);
+        else DOPT_DW2(4);
 #undef DOPT_DW2
+#undef DOPT_DW2T
         launch_dw_reduce(a.partial, used, a.M * a.N, out32, out16, a.db_partial, a.M, with_db ? db : nullptr, st);
         return 0;
     }

@@ -35,7 +35,7 @@ def check_close(got, dy, x):
     assert bool((err <= 1e-4 * mag + 1e-6).all()), float((err / (mag + 1e-30)).max())
 
 
-@pytest.mark.parametrize("K,M,N", [(25216, 768, 768), (1000, 256, 512), (64, 512, 256), (4100, 1024, 256)])
+@pytest.mark.parametrize("K,M,N", [(25216, 768, 768), (1000, 256, 512), (64, 512, 256), (4100, 1024, 256), (2048, 2304, 768)])
 def test_bf16_operand(K, M, N):
     dy, x = operands(K, M, N, K + M)
     dw, db = ops.dw_gemm(dy, x, None, None, None, N, 0, 0, True, torch.float32)
