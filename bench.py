@@ -232,7 +232,7 @@ def valu_probe() -> int:
     per_simd = blocks * 4 * 8 * 512 / simds  # wave-instructions per SIMD per launch
     res = {}
     for kind, name in enumerate(("v_fma_f32", "v_exp_f32", "v_rcp_f32", "v_mad_u64_u32+v_xor_b32", "mfma_bf16_random",
-                                 "mfma_bf16_constant")):
+                                 "mfma_bf16_constant", "mfma_fp8_random", "mfma_fp8_constant")):
         fn = lambda kind=kind: _lib.check(L.dopt_valu_probe(kind, out.data_ptr(), blocks, st.cuda_stream),  # noqa: E731
                                           "valu_probe")
         for _ in range(3):
@@ -249,9 +249,12 @@ def valu_probe() -> int:
         us = statistics.median(ts)
         if kind < 4:
             res[name] = {"us_per_launch": round(us, 2), "ns_per_wave_instruction": round(us * 1e3 / per_simd, 4)}
-        else:
+        elif kind < 6:
             tf = blocks * 4 * 64 * 16 * 32768 / us / 1e6
             res[name] = {"us_per_launch": round(us, 2), "TFLOP/s": round(tf, 1), "frac_bf16_peak": round(tf / 2500.0, 4)}
+        else:
+            tf = blocks * 4 * 64 * 16 * 131072 / us / 1e6
+            res[name] = {"us_per_launch": round(us, 2), "TFLOP/s": round(tf, 1), "frac_fp8_peak": round(tf / 5000.0, 4)}
     print(json.dumps({"valu_probe": res, "simds": simds}))
     return 0
 

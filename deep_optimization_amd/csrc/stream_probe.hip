@@ -119,12 +119,55 @@ __global__ __launch_bounds__(PROBE_THREADS, 1) void mfma_rate_kernel(float* __re
     out[(uint64_t)blockIdx.x * PROBE_THREADS + threadIdx.x] = t;
 }
 
+// The same for the FP8 GEMM's instruction, v_mfma_scale_f32_32x32x64_f8f6f4 with e4m3 operands
+// and unit scales: 4 x 4 accumulators per wave, 4 + 4 fragments of 32 bytes per lane. RANDOM:
+// pseudo-random e4m3 bytes (finite, |v| <= 448), otherwise one constant byte.
+typedef int probe_v8i_t __attribute__((ext_vector_type(8)));
+
+template <bool RANDOM>
+__global__ __launch_bounds__(PROBE_THREADS, 1) void mfma_fp8_rate_kernel(float* __restrict__ out) {
+    probe_v8i_t a[4], b[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            uint32_t h = (threadIdx.x * 8u + (uint32_t)e) * 2654435761u ^ (uint32_t)(i + 1) * 40503u;
+            h ^= h >> 13;
+            // clear bit 6 of each byte: exponent field <= 7 of 15, so no NaN encodings (0x7f / 0xff)
+            const uint32_t ra = RANDOM ? (h & 0xbfbfbfbfu) : 0x38383838u;
+            const uint32_t rb = RANDOM ? ((h * 0x9E3779B9u) & 0xbfbfbfbfu) : 0x38383838u;
+            a[i][e] = (int)ra;
+            b[i][e] = (int)rb;
+        }
+    probe_f32x16_t acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
+    for (int st = 0; st < MFMA_STEPS; ++st)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a[i], b[j], acc[i][j], 0, 0, 0, 0, 0, 0);
+    float t = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) t += acc[i][j][0] + acc[i][j][15];
+    out[(uint64_t)blockIdx.x * PROBE_THREADS + threadIdx.x] = t;
+}
+
 }  // namespace
 
-// kind 0..3 (fma, exp, rcp, mad64 + xor), 4 / 5 (bf16 MFMA stream, random / constant operands);
-// out holds n_blocks * 256 floats
+// kind 0..3 (fma, exp, rcp, mad64 + xor), 4 / 5 (bf16 MFMA stream, random / constant operands),
+// 6 / 7 (fp8 MFMA stream, random / constant operands); out holds n_blocks * 256 floats
 const char* launch_valu_rate(int kind, float* out, uint32_t n_blocks, hipStream_t s) {
     switch (kind) {
+        case 6: hipLaunchKernelGGL(mfma_fp8_rate_kernel<true>, dim3(n_blocks), dim3(PROBE_THREADS), 0, s, out); break;
+        case 7: hipLaunchKernelGGL(mfma_fp8_rate_kernel<false>, dim3(n_blocks), dim3(PROBE_THREADS), 0, s, out); break;
         case 4: hipLaunchKernelGGL(mfma_rate_kernel<true>, dim3(n_blocks), dim3(PROBE_THREADS), 0, s, out); break;
         case 5: hipLaunchKernelGGL(mfma_rate_kernel<false>, dim3(n_blocks), dim3(PROBE_THREADS), 0, s, out); break;
         case 0: hipLaunchKernelGGL(valu_rate_kernel<0>, dim3(n_blocks), dim3(PROBE_THREADS), 0, s, out, 0.3f); break;

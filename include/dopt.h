@@ -354,7 +354,9 @@ int dopt_stream_probe(const void* x, const void* noise, void* codes, void* meta,
  * (SIMDs) / (n_blocks * 4 * 8 * 512). Kinds 4 and 5 instead stream v_mfma_f32_32x32x16_bf16 in
  * the weight-gradient GEMM's inner-loop shape (a 4 x 4 grid of accumulators per wave, one wave per
  * SIMD, 64 steps of 16 MFMAs, nothing else), with pseudo-random (4) or constant (5) operands:
- * n_blocks * 4 * 64 * 16 * 32768 flops per launch. n_blocks in [1, 65536].
+ * n_blocks * 4 * 64 * 16 * 32768 flops per launch. Kinds 6 and 7 do the same with the FP8 GEMM's
+ * v_mfma_scale_f32_32x32x64_f8f6f4 (e4m3, unit scales; 131072 flops each), random (6) or
+ * constant (7) operands. n_blocks in [1, 65536].
  */
 int dopt_valu_probe(int kind, float* out, int64_t n_blocks, void* stream);
 

@@ -609,7 +609,7 @@ def test_stream_probe_rejects_bad_arguments():
     assert L.dopt_stream_probe(buf.data_ptr(), None, buf.data_ptr(), buf.data_ptr(), -1, 2, s) == _lib.EINVAL
 
 
-@pytest.mark.parametrize("kind", [0, 1, 2, 3, 4, 5])
+@pytest.mark.parametrize("kind", [0, 1, 2, 3, 4, 5, 6, 7])
 def test_valu_probe_runs(kind):
     """dopt_valu_probe (the instruction-cost probe the benchmark reports) launches, finishes and
     writes every output element."""
