@@ -259,6 +259,69 @@ def valu_probe() -> int:
     return 0
 
 
+def host_probe() -> int:
+    """Host cost of one eager operator call, and of its parts, on inputs small enough that the GPU
+    work is negligible (one 256-element bf16 group, 2-bit nearest): per-call wall time of 2000
+    back-to-back calls (one synchronize at the end), medians of 5 windows, for
+      - torch.ops.act_lib.quant_pack / dequant_unpack (dispatcher + Python wrapper + ctypes + launch),
+      - the same Python implementations called directly (no dispatcher),
+      - the raw ctypes calls into libdopt with preallocated outputs (marshalling + launch),
+      - the wrapper's pieces: _aligned (contiguous + alignment test), torch.empty x 3, the stream
+        lookup."""
+    import torch
+
+    import deep_optimization_amd  # noqa: F401
+    from deep_optimization_amd import _lib, act_lib
+
+    dev = torch.device("cuda:0")
+    L = _lib.lib()
+    ops = torch.ops.act_lib
+    x = torch.randn((1, 1, G_SIZE), device=dev).to(torch.bfloat16)
+    packed = torch.empty((1, G_SIZE * BITS // 32), dtype=torch.int32, device=dev)
+    scale = torch.empty(1, dtype=torch.float32, device=dev)
+    xmin = torch.empty(1, dtype=torch.float32, device=dev)
+    y = torch.empty((1, 1, G_SIZE), dtype=torch.bfloat16, device=dev)
+    st = torch.cuda.current_stream(dev).cuda_stream
+    p0, s0, m0 = ops.quant_pack(x, BITS, G_SIZE, False, 0.0, False, NEAREST, None, 1, 0, torch.float32)
+
+    def raw_pack():
+        L.dopt_quant_pack(x.data_ptr(), _lib.BF16, 1, G_SIZE, BITS, None, NEAREST, None, 1, 0, 0, 0.0,
+                          packed.data_ptr(), scale.data_ptr(), xmin.data_ptr(), _lib.F32, st)
+
+    def raw_unpack():
+        L.dopt_dequant_unpack(packed.data_ptr(), scale.data_ptr(), xmin.data_ptr(), _lib.F32, 1, G_SIZE, BITS, None,
+                              y.data_ptr(), _lib.BF16, st)
+
+    cases = {
+        "op_quant_pack": lambda: ops.quant_pack(x, BITS, G_SIZE, False, 0.0, False, NEAREST, None, 1, 0, torch.float32),
+        "op_dequant_unpack": lambda: ops.dequant_unpack(p0, s0, m0, BITS, G_SIZE, torch.bfloat16),
+        "python_impl_quant_pack": lambda: act_lib._quant_pack(x, BITS, G_SIZE, False, 0.0, False, NEAREST, None, 1, 0,
+                                                              torch.float32),
+        "ctypes_quant_pack": raw_pack,
+        "ctypes_dequant_unpack": raw_unpack,
+        "aligned": lambda: act_lib._aligned(x),
+        "torch_empty_x3": lambda: (torch.empty((1, 16), dtype=torch.int32, device=dev),
+                                   torch.empty(1, dtype=torch.float32, device=dev),
+                                   torch.empty(1, dtype=torch.float32, device=dev)),
+        "stream_lookup": lambda: act_lib._stream(x),
+    }
+    res = {}
+    for name, fn in cases.items():
+        for _ in range(200):
+            fn()
+        torch.cuda.synchronize()
+        ts = []
+        for _ in range(5):
+            t0 = time.perf_counter()
+            for _ in range(2000):
+                fn()
+            torch.cuda.synchronize()
+            ts.append((time.perf_counter() - t0) / 2000 * 1e6)
+        res[name] = round(statistics.median(ts), 2)
+    print(json.dumps({"host_probe_us_per_call": res}))
+    return 0
+
+
 def dw_probe() -> int:
     """Three weight-gradient GEMMs at the ViT-B/16 bs-128 fc1 shape (dy bf16 [25216, 3072], x_hat
     bf16 [25216, 768], no bias gradient), for rocprofv3 --pmc runs."""
@@ -548,6 +611,7 @@ def main() -> int:
     ap.add_argument("--fp8-probe", choices=("random", "constant", "hipblaslt"))
     ap.add_argument("--dw-probe", action="store_true")
     ap.add_argument("--valu-probe", action="store_true")
+    ap.add_argument("--host-probe", action="store_true")
     ap.add_argument("--counter-probe", choices=("philox", "nearest", "gelu", "silu", "bn_squash", "bn_relu"))
     args = ap.parse_args()
     if args.gpus != 1:
@@ -565,6 +629,8 @@ def main() -> int:
         return dw_probe()
     if args.valu_probe:
         return valu_probe()
+    if args.host_probe:
+        return host_probe()
 
     import torch
 
