@@ -48,6 +48,8 @@ EXPORTS = (
     "dopt_graph_replace_memsets",
     "dopt_stream_probe",
     "dopt_valu_probe",
+    "dopt_alam_quant_pack",
+    "dopt_alam_dequant_unpack",
 )
 
 _lib = None
@@ -134,6 +136,10 @@ def lib() -> ctypes.CDLL:
         L.dopt_stream_probe.restype = i32
         L.dopt_valu_probe.argtypes = [i32, vp, i64, vp]
         L.dopt_valu_probe.restype = i32
+        L.dopt_alam_quant_pack.argtypes = [vp, i32, i64, i32, i32, i32, i32, ctypes.c_float, vp, vp, vp, vp]
+        L.dopt_alam_quant_pack.restype = i32
+        L.dopt_alam_dequant_unpack.argtypes = [vp, vp, vp, i64, i32, i32, i32, ctypes.c_uint64, vp, vp]
+        L.dopt_alam_dequant_unpack.restype = i32
         _lib = L
     return _lib
 

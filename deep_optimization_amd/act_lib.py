@@ -258,40 +258,90 @@ dequant_unpack_tiles = _op(
 
 
 # --------------------------------------------------------------------------- reference schemas
+ALAM_SEED = 42  # the reference operators' fixed seed (act_triton_kernel.py:339, :374)
+
+
 def _no_alam(avg_alam: bool, where: str) -> None:
+    """The BatchNorm operators' avg_alam mode is not built (the quantizer's is, below)."""
     if avg_alam:
         raise NotImplementedError(
-            f"{where}: avg_alam=True is not implemented (the reference disables it for every "
-            "Linear/Conv layer, controller.py:186-187, and its dequant noise uses Triton's tl.randn)")
+            f"{where}: avg_alam=True is not implemented for the BatchNorm operators (their reference "
+            "layers pass avg_alam=False; the quantizer operators quant_pack_triton / dequant_unpack_triton "
+            "support it)")
+
+
+def _alam_words(bits: int, group_size: int, alam_bits: int) -> int:
+    """Packed words per group with avg_alam: the reference's cdiv(NWORDS, alam_bits), where its
+    reshape of the codes into runs of alam_bits requires alam_bits to divide NWORDS."""
+    _, nwords, _ = _bits_consts(bits, group_size)
+    if alam_bits < 1 or alam_bits & (alam_bits - 1) or nwords % alam_bits:
+        raise RuntimeError(f"avg_alam: alam_bits must be a power of two dividing group_size*bits/32 = {nwords}, "
+                           f"got {alam_bits}")
+    return nwords // alam_bits
 
 
 def _quant_pack_triton(x, bits, group_size, avg_alam, alam_bits, clamp, clamp_alpha):
     """Reference semantics (act_triton_kernel.py:336-368): [clamp], tanh squash, nearest
-    rounding, bf16 scale and min."""
-    _no_alam(avg_alam, "quant_pack_triton")
+    rounding, bf16 scale and min; with avg_alam the mean of every run of alam_bits code
+    arguments is truncated into one code (:116-118)."""
     if x.dim() != 3 or x.shape[-1] != group_size:  # the reference's x.view(N * G, group_size)
         raise RuntimeError(f"quant_pack_triton expects x of shape [N, G, {group_size}], got {tuple(x.shape)}")
     N, G, _ = x.shape
-    packed, scale, xmin = _quant_pack_launch(x, N * G, bits, group_size, None, clamp, clamp_alpha,
-                                             True, ROUND_NEAREST, None, 0, 0, torch.bfloat16)
+    if not avg_alam:
+        packed, scale, xmin = _quant_pack_launch(x, N * G, bits, group_size, None, clamp, clamp_alpha,
+                                                 True, ROUND_NEAREST, None, 0, 0, torch.bfloat16)
+        return packed, scale.view(N, G), xmin.view(N, G)
+    anw = _alam_words(bits, group_size, alam_bits)
+    if x.dtype not in _DTYPE_CODE:
+        raise RuntimeError(f"quant_pack_triton: unsupported input dtype {x.dtype}")
+    _require_cuda(x)
+    x = x.contiguous()
+    packed = torch.empty((N * G, anw), dtype=torch.int32, device=x.device)
+    scale = torch.empty((N * G,), dtype=torch.bfloat16, device=x.device)
+    xmin = torch.empty((N * G,), dtype=torch.bfloat16, device=x.device)
+    rc = _lib.lib().dopt_alam_quant_pack(x.data_ptr(), _DTYPE_CODE[x.dtype], N * G, group_size, bits, alam_bits,
+                                         _flags(clamp, True), float(clamp_alpha), packed.data_ptr(), scale.data_ptr(),
+                                         xmin.data_ptr(), _stream(x))
+    _lib.check(rc, "alam_quant_pack")
     return packed, scale.view(N, G), xmin.view(N, G)
+
+
+def _quant_pack_triton_fake(x, bits, group_size, avg_alam, alam_bits, clamp, clamp_alpha):
+    N, G = x.shape[0], x.shape[1]
+    if not avg_alam:
+        return _meta3(x, N, G, bits, group_size, torch.bfloat16)
+    anw = _alam_words(bits, group_size, alam_bits)
+    return (x.new_empty((N * G, anw), dtype=torch.int32), x.new_empty((N, G), dtype=torch.bfloat16),
+            x.new_empty((N, G), dtype=torch.bfloat16))
 
 
 quant_pack_triton = _op(
     "quant_pack_triton(Tensor x, int bits, int group_size, bool avg_alam, int alam_bits, bool clamp, "
     "float clamp_alpha) -> (Tensor, Tensor, Tensor)",
-    _quant_pack_triton,
-    lambda x, bits, group_size, avg_alam, alam_bits, clamp, clamp_alpha:
-        _meta3(x, x.shape[0], x.shape[1], bits, group_size, torch.bfloat16))
+    _quant_pack_triton, _quant_pack_triton_fake)
 
 
 def _dequant_unpack_triton(packed, scale, xmin, bits, group_size, avg_alam, alam_bits):
     """Reference semantics (act_triton_kernel.py:372-395): bf16 output [N, G, g] whatever the
-    scale dtype (the reference allocates y as bf16, :382), one rounding from fp32."""
-    _no_alam(avg_alam, "dequant_unpack_triton")
+    scale dtype (the reference allocates y as bf16, :382), one rounding from fp32. With avg_alam
+    each code covers alam_bits elements and carries Triton-randn noise (seed 42 + group,
+    element offset) minus 0.5 (:212-219)."""
     N, G = scale.shape
     y = torch.empty((N, G, group_size), dtype=torch.bfloat16, device=packed.device)
-    return _dequant_launch(packed, scale, xmin, N * G, bits, group_size, None, y)
+    if not avg_alam:
+        return _dequant_launch(packed, scale, xmin, N * G, bits, group_size, None, y)
+    anw = _alam_words(bits, group_size, alam_bits)
+    if scale.dtype != torch.bfloat16 or xmin.dtype != torch.bfloat16:
+        raise RuntimeError("dequant_unpack_triton: avg_alam takes the bf16 scale and min its quantizer writes")
+    if packed.numel() != N * G * anw:
+        raise RuntimeError(f"dequant_unpack_triton: packed holds {packed.numel()} words, expected {N * G * anw} "
+                           f"({N * G} groups of {anw})")
+    _require_cuda(packed, scale, xmin)
+    packed, scale, xmin = packed.contiguous(), scale.contiguous(), xmin.contiguous()
+    rc = _lib.lib().dopt_alam_dequant_unpack(packed.data_ptr(), scale.data_ptr(), xmin.data_ptr(), N * G, group_size,
+                                             bits, alam_bits, ALAM_SEED, y.data_ptr(), _stream(packed))
+    _lib.check(rc, "alam_dequant_unpack")
+    return y
 
 
 dequant_unpack_triton = _op(

@@ -30,6 +30,7 @@ SOURCES = [
     "dw_gemm.hip",
     "graph_tools.hip",
     "stream_probe.hip",
+    "alam.hip",
 ]
 
 ARCH = "gfx950"

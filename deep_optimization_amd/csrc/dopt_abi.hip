@@ -25,6 +25,10 @@ int launch_act_forward(const void* x, int dt, void* y, void* aux, uint64_t n, in
 const char* graph_node_counts(hipGraph_t g, int64_t* counts, int n_counts);
 const char* graph_replace_memsets(hipGraph_t g, int64_t* replaced);
 const char* launch_valu_rate(int kind, float* out, uint32_t n_blocks, hipStream_t s);
+int launch_alam_quant_pack(const void* x, int dt, int64_t n_groups, int g, int bits, int alam, int flags,
+                           float clamp_alpha, uint32_t* packed, uint16_t* scale, uint16_t* minv, hipStream_t s);
+int launch_alam_dequant(const uint32_t* packed, const uint16_t* scale, const uint16_t* minv, int64_t n_groups,
+                        int g, int bits, int alam, uint64_t seed, uint16_t* y, hipStream_t s);
 const char* launch_stream_mix(const void* x, const void* noise, void* codes, void* meta, uint64_t n_units, int bits,
                               hipStream_t s);
 }  // namespace dopt
@@ -269,6 +273,53 @@ int dopt_dequant_unpack(const uint32_t* packed, const void* scale, const void* m
         rc = dopt::launch_dequant_unpack_dt<dopt::DT_BF16>(a, bits, group_size, dopt::DY_NONE, s);
     if (rc) return fail(DOPT_EUNSUPPORTED, "no dequant kernel for bits=%d g=%d", bits, group_size);
     return hip_status("dequant_unpack launch");
+}
+
+static int check_alam(int64_t n_groups, int group_size, int bits, int alam_bits) {
+    int rc;
+    if ((rc = check_bits(bits))) return rc;
+    if ((rc = check_group(group_size))) return rc;
+    if (n_groups < 0 || n_groups >= (int64_t)1 << 31)
+        return fail(DOPT_EINVAL, "n_groups must be in [0, 2^31), got %lld", (long long)n_groups);
+    const int nw = group_size * bits / 32;
+    if (alam_bits < 1 || (alam_bits & (alam_bits - 1)) || nw % alam_bits)
+        return fail(DOPT_EINVAL,
+                    "alam_bits must be a power of two dividing group_size*bits/32 = %d (the reference reshapes the "
+                    "codes into runs of alam_bits), got %d", nw, alam_bits);
+    return DOPT_OK;
+}
+
+int dopt_alam_quant_pack(const void* x, int x_dtype, int64_t n_groups, int group_size, int bits, int alam_bits,
+                         int flags, float clamp_alpha, uint32_t* packed, uint16_t* scale, uint16_t* minv,
+                         void* stream) {
+    int rc;
+    if ((rc = check_alam(n_groups, group_size, bits, alam_bits))) return rc;
+    if (x_dtype != DOPT_F32 && x_dtype != DOPT_F16 && x_dtype != DOPT_BF16)
+        return fail(DOPT_EINVAL, "unsupported input dtype code %d", x_dtype);
+    if (flags & ~(DOPT_FLAG_CLAMP | DOPT_FLAG_SQUASH)) return fail(DOPT_EINVAL, "unknown flags 0x%x", flags);
+    if (n_groups == 0) return ok();
+    if (!x || !packed || !scale || !minv) return fail(DOPT_EINVAL, "null pointer argument");
+    if (((uintptr_t)x % (x_dtype == DOPT_F32 ? 4u : 2u)) || ((uintptr_t)packed & 3u) || ((uintptr_t)scale & 1u) ||
+        ((uintptr_t)minv & 1u))
+        return fail(DOPT_EINVAL, "x, packed, scale and min must be aligned to their element size");
+    (void)hipGetLastError();
+    dopt::launch_alam_quant_pack(x, x_dtype, n_groups, group_size, bits, alam_bits, flags, clamp_alpha, packed,
+                                 scale, minv, (hipStream_t)stream);
+    return hip_status("alam_quant_pack launch");
+}
+
+int dopt_alam_dequant_unpack(const uint32_t* packed, const uint16_t* scale, const uint16_t* minv, int64_t n_groups,
+                             int group_size, int bits, int alam_bits, uint64_t seed, uint16_t* y, void* stream) {
+    int rc;
+    if ((rc = check_alam(n_groups, group_size, bits, alam_bits))) return rc;
+    if (n_groups == 0) return ok();
+    if (!packed || !scale || !minv || !y) return fail(DOPT_EINVAL, "null pointer argument");
+    if (((uintptr_t)packed & 3u) || ((uintptr_t)scale & 1u) || ((uintptr_t)minv & 1u) || ((uintptr_t)y & 1u))
+        return fail(DOPT_EINVAL, "packed, scale, min and y must be aligned to their element size");
+    (void)hipGetLastError();
+    dopt::launch_alam_dequant(packed, scale, minv, n_groups, group_size, bits, alam_bits, seed, y,
+                              (hipStream_t)stream);
+    return hip_status("alam_dequant_unpack launch");
 }
 
 int dopt_pack_codes(const int8_t* codes, int64_t n_groups, int group_size, int bits, uint32_t* packed, void* stream) {

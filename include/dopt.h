@@ -102,6 +102,26 @@ int dopt_dequant_unpack(const uint32_t* packed, const void* scale, const void* m
                         void* y, int y_dtype, void* stream);
 
 /*
+ * The reference quantizer's avg_alam mode (act_triton_kernel.py:336-395: quant_pack_triton and
+ * dequant_unpack_triton with avg_alam=True; kernels :116-118 and :212-219).
+ *
+ * dopt_alam_quant_pack: as dopt_quant_pack with nearest rounding and bf16 scale/min, flat layout,
+ * except that each run of alam_bits consecutive nearest-code arguments fma(x - min, 1/step,
+ * 0.5 - 1e-6) is averaged (summed left to right) before truncation: group_size / alam_bits codes
+ * per group in packed [n_groups, group_size*bits/32/alam_bits] uint32. alam_bits is a power of two
+ * dividing group_size*bits/32 (the reference's reshape needs it); x any alignment of its dtype.
+ *
+ * dopt_alam_dequant_unpack: y bf16 [n_groups, group_size]; element e of group r is
+ * bf16(fma(code[e / alam_bits] + randn(seed + r, e) - 0.5, scale[r], min[r])) with Triton's randn
+ * (Philox4x32-10, counter (e, 0, 0, 0), key seed + r; Box-Muller); the reference passes seed 42.
+ */
+int dopt_alam_quant_pack(const void* x, int x_dtype, int64_t n_groups, int group_size, int bits, int alam_bits,
+                         int flags, float clamp_alpha, uint32_t* packed, uint16_t* scale, uint16_t* minv,
+                         void* stream);
+int dopt_alam_dequant_unpack(const uint32_t* packed, const uint16_t* scale, const uint16_t* minv, int64_t n_groups,
+                             int group_size, int bits, int alam_bits, uint64_t seed, uint16_t* y, void* stream);
+
+/*
  * Code-only pack: int8 codes [n_groups, group_size] -> uint32 words [n_groups, group_size*bits/32],
  * word = sum_j int32(code[j]) << (j*bits) with 32-bit wrap-around (identical to OR for codes in
  * [0, 2^bits)). Replaces act_lib::pack_triton (act_triton_kernel.py:398-417, kernel :246-281).

@@ -84,6 +84,12 @@ def lib():
         L.oracle_bn_bwd_dx.argtypes = [i32, vp, vp, vp, vp, vp, vp, i32, i64, i64, i64, i64, i64, i32, i32, vp, vp,
                                        vp, vp, f32, i32, vp]
         L.oracle_bn_bwd_dx.restype = i32
+        L.oracle_alam_quant_pack.argtypes = [vp, i32, i64, i32, i32, i32, i32, f32, vp, vp, vp]
+        L.oracle_alam_quant_pack.restype = i32
+        L.oracle_alam_dequant_unpack.argtypes = [vp, vp, vp, i64, i32, i32, i32, u64, vp]
+        L.oracle_alam_dequant_unpack.restype = i32
+        L.oracle_triton_randn.argtypes = [u64, ctypes.c_uint32]
+        L.oracle_triton_randn.restype = f32
         _lib = L
     return _lib
 
@@ -157,6 +163,41 @@ def dequant_unpack(packed, scale, mn, group_size: int, bits: int, *, tile_nchw=N
                                      bits, _ptr(tile), _ptr(y), y_dtype)
     _check(rc)
     return y
+
+
+ALAM_SEED = 42  # the reference operators' fixed seed (act_triton_kernel.py:339, :374)
+
+
+def alam_quant_pack(x: np.ndarray, group_size: int, bits: int, alam_bits: int, *, flags=0, clamp_alpha=0.0):
+    """The reference quantizer's avg_alam mode -> (packed uint32 [NG, NW / alam_bits], scale and
+    min as uint16 bf16 bits [NG])."""
+    x = np.ascontiguousarray(x)
+    ng = x.size // group_size
+    nw = group_size * bits // 32
+    packed = np.zeros((ng, max(nw // max(alam_bits, 1), 1)), dtype=np.uint32)
+    scale = np.zeros(ng, dtype=np.uint16)
+    mn = np.zeros(ng, dtype=np.uint16)
+    _check(lib().oracle_alam_quant_pack(_ptr(x), _dtype_code(x), ng, group_size, bits, alam_bits, flags,
+                                        clamp_alpha, _ptr(packed), _ptr(scale), _ptr(mn)))
+    return packed, scale, mn
+
+
+def alam_dequant_unpack(packed, scale, mn, group_size: int, bits: int, alam_bits: int, seed: int = ALAM_SEED):
+    """avg_alam dequantize: each code repeated alam_bits times plus Triton-randn noise - 0.5 ->
+    bf16 bits (uint16) [NG, g]."""
+    packed = np.ascontiguousarray(packed, dtype=np.uint32)
+    scale = np.ascontiguousarray(scale, dtype=np.uint16)
+    mn = np.ascontiguousarray(mn, dtype=np.uint16)
+    ng = scale.size
+    y = np.zeros((ng, group_size), dtype=np.uint16)
+    _check(lib().oracle_alam_dequant_unpack(_ptr(packed), _ptr(scale), _ptr(mn), ng, group_size, bits, alam_bits,
+                                            seed, _ptr(y)))
+    return y
+
+
+def triton_randn(seed: int, offset: int) -> float:
+    """One value of Triton's tl.randn(seed, offset) as this oracle restates it."""
+    return float(lib().oracle_triton_randn(seed, offset))
 
 
 def pack_codes(codes: np.ndarray, group_size: int, bits: int) -> np.ndarray:

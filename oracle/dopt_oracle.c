@@ -44,6 +44,12 @@
  *                                  quantized values (squashed mode), bounds |x_hat' - t| <= scale/2
  *   BatchNorm squash (2 tanh(x/2)) parity unpinned at bit level (libdevice tanh in the reference)
  *   BatchNorm backward             pinned: against torch's float64 batch_norm autograd on x_hat
+ *   ALAM averaging (quantize)      pinned: closed form (mean of the runs' nearest-code arguments),
+ *                                  A = 1 equals oracle_quant_pack, A = 2 brute force in float64;
+ *                                  summation order for A >= 4 is a stated choice
+ *   ALAM noise (Triton randn)      Philox part pinned by the known-answer vectors; Box-Muller
+ *                                  pinned against float64 from the same uniforms; moments of
+ *                                  the noise checked; the fp32 log/cos are the C library's
  */
 #include <math.h>
 #include <stdint.h>
@@ -304,6 +310,125 @@ int oracle_dequant_unpack(const uint32_t* packed, const void* scale, const void*
                 ((float*)y)[o] = v;
             else
                 ((uint16_t*)y)[o] = f32_to_bf16(v);
+        }
+    }
+    return O_OK;
+}
+
+/* ---------------------------------------------------------------- ALAM averaging
+ * The reference quantizer's avg_alam mode (AC/act_triton_kernel.py:336-368 host side, :116-118 and
+ * :212-219 in the kernels; seed 42 in both operators, :339 and :374).
+ *
+ * Quantize: the non-ALAM pre-transform, min/max, step (rng/QMAX, 1 for rng = 0) and
+ * qf[e] = fma(t[e], inv, 0.5 - 1e-6) (:55-114), then every run of A = alam_bits consecutive qf is
+ * averaged: qa[c] = (qf[cA] + qf[cA+1] + ... + qf[cA+A-1]) / A (:116-118, a reshape to
+ * (g/A, A) and tl.sum over the runs). The sum is taken left to right: Triton reduces the elements
+ * a thread holds in index order, and a run of A <= 8 consecutive values of a 1-D block sits in
+ * one thread; that order is this restatement's choice where A >= 4 (parity of the summation
+ * order unpinned at bit level). code = clamp(trunc(qa), 0, QMAX) (:156-158; NaN -> 0 as in
+ * oracle_quant_pack), g/A codes packed into NW/A words (:160-171). Scale and min are bf16.
+ * Requires A a power of two dividing NW = g * bits / 32 (the reference's reshape).
+ *
+ * Dequantize (:199-241): code c = e / A repeated A times (:212-214), plus Gaussian noise
+ * n = randn(seed + r, e) - 0.5 (:216-218), y = bf16(fma(code + n, scale, min)) (:223, :241).
+ * randn is Triton's (triton/language/random.py, restated): Philox4x32-10 with counter
+ * (e, 0, 0, 0) and key (lo32(seed + r), hi32(seed + r)); the first two output words w0, w1 map to
+ * uniforms u = f32(w < 0 ? ~w : w) * 0x2fffffff (w as int32; the fp32 constant 4.6566127342e-10);
+ * u1 = max(1e-7, u1), r = sqrt(-2 log u1), n = r cos(6.283185307179586 u2) (Box-Muller, first
+ * output). log, cos and sqrt are the C library's fp32 functions here and libdevice's in the
+ * reference: parity of the noise is to a few fp32 ulps, not bits. */
+static float triton_uniform(uint32_t w) {
+    int32_t i = (int32_t)w;
+    if (i < 0) i = ~i;
+    return (float)i * u2f(0x2fffffffu);
+}
+
+float oracle_triton_randn(uint64_t seed, uint32_t offset) {
+    const uint32_t ctr[4] = {offset, 0u, 0u, 0u};
+    const uint32_t key[2] = {(uint32_t)seed, (uint32_t)(seed >> 32)};
+    uint32_t w[4];
+    oracle_philox4x32_10(ctr, key, w);
+    float u1 = triton_uniform(w[0]), u2 = triton_uniform(w[1]);
+    u1 = fmaxf(1.0e-7f, u1);
+    const float th = 6.283185307179586f * u2;
+    const float r = sqrtf(-2.0f * logf(u1));
+    return r * cosf(th);
+}
+
+static int alam_check(int64_t n_groups, int g, int bits, int alam_bits) {
+    int s = 0;
+    int rc = check_common(n_groups, g, bits, NULL, &s);
+    if (rc) return rc;
+    const int NW = g / (32 / bits);
+    if (alam_bits < 1 || (alam_bits & (alam_bits - 1)) || NW % alam_bits) return O_EINVAL;
+    return O_OK;
+}
+
+int oracle_alam_quant_pack(const void* x, int x_dtype, int64_t n_groups, int g, int bits, int alam_bits,
+                           int flags, float clamp_alpha, uint32_t* packed, uint16_t* scale, uint16_t* minv) {
+    int rc = alam_check(n_groups, g, bits, alam_bits);
+    if (rc) return rc;
+    if (x_dtype != O_F32 && x_dtype != O_F16 && x_dtype != O_BF16) return O_EINVAL;
+    const int A = alam_bits, QMAX = (1 << bits) - 1, VPW = 32 / bits, ANW = g / VPW / A;
+    const float qmaxf = (float)QMAX, half_m = (float)(0.5 - 1e-6);
+#pragma omp parallel
+    {
+        float* xs = (float*)malloc(sizeof(float) * g);
+        int* q = (int*)malloc(sizeof(int) * (g / A));
+#pragma omp for schedule(static)
+        for (int64_t r = 0; r < n_groups; ++r) {
+            for (int e = 0; e < g; ++e) {
+                float v = load_elem(x, x_dtype, r * g + e);
+                if (flags & O_FLAG_CLAMP) v = fminf(fmaxf(v, -clamp_alpha), clamp_alpha);
+                if (flags & O_FLAG_SQUASH) v = tanhf(v / 0.5f) * 0.5f;
+                xs[e] = v;
+            }
+            float mn = xs[0], mx = xs[0];
+            for (int e = 1; e < g; ++e) {
+                mn = fminf(mn, xs[e]);
+                mx = fmaxf(mx, xs[e]);
+            }
+            mn = mn + 0.0f;
+            const float rng = mx - mn;
+            const float step = (rng > 0.0f) ? rng / qmaxf : 1.0f;
+            const float inv = 1.0f / step;
+            for (int c = 0; c < g / A; ++c) {
+                float sum = fmaf(xs[c * A] - mn, inv, half_m);
+                for (int k = 1; k < A; ++k) sum = sum + fmaf(xs[c * A + k] - mn, inv, half_m);
+                float qa = sum / (float)A;
+                if (qa != qa) qa = 0.0f;
+                qa = fminf(fmaxf(qa, 0.0f), qmaxf);
+                q[c] = (int)qa;
+            }
+            for (int w = 0; w < ANW; ++w) {
+                uint32_t word = 0;
+                for (int j = 0; j < VPW; ++j) word |= (uint32_t)q[w * VPW + j] << (j * bits);
+                packed[r * ANW + w] = word;
+            }
+            scale[r] = f32_to_bf16(step);
+            minv[r] = f32_to_bf16(mn);
+        }
+        free(xs);
+        free(q);
+    }
+    return O_OK;
+}
+
+int oracle_alam_dequant_unpack(const uint32_t* packed, const uint16_t* scale, const uint16_t* minv,
+                               int64_t n_groups, int g, int bits, int alam_bits, uint64_t seed, uint16_t* y) {
+    int rc = alam_check(n_groups, g, bits, alam_bits);
+    if (rc) return rc;
+    const int A = alam_bits, VPW = 32 / bits, ANW = g / VPW / A;
+    const uint32_t QMAX = (1u << bits) - 1u;
+#pragma omp parallel for schedule(static)
+    for (int64_t r = 0; r < n_groups; ++r) {
+        const float sc = bf16_to_f32(scale[r]), mn = bf16_to_f32(minv[r]);
+        for (int e = 0; e < g; ++e) {
+            const int c = e / A;
+            const uint32_t qv = (packed[r * ANW + c / VPW] >> ((c % VPW) * bits)) & QMAX;
+            const float n = oracle_triton_randn(seed + (uint64_t)r, (uint32_t)e);
+            const float qf = (float)qv + (n - 0.5f);
+            y[r * g + e] = f32_to_bf16(fmaf(qf, sc, mn));
         }
     }
     return O_OK;

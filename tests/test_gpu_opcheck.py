@@ -23,7 +23,8 @@ TESTS = ("test_schema", "test_faketensor", "test_aot_dispatch_static", "test_aot
 
 
 @pytest.mark.parametrize("case", [
-    "quant_pack", "quant_pack_triton", "dequant_unpack", "dequant_unpack_triton", "quant_pack_tiles",
+    "quant_pack", "quant_pack_triton", "dequant_unpack", "dequant_unpack_triton", "quant_pack_triton_alam",
+    "dequant_unpack_triton_alam", "quant_pack_tiles",
     "pack_triton", "unpack_triton", "fp8_gemm_nt", "fp8_linear", "relu_fwd_fused_pack", "dw_gemm"])
 def test_opcheck(case):
     x = _x((2, 8, 256))
@@ -37,6 +38,11 @@ def test_opcheck(case):
     elif case == "dequant_unpack_triton":
         p, s, m = ops.quant_pack_triton(x, 4, 256, False, 0, True, 3.0)
         args = (p, s, m, 4, 256, False, 0)
+    elif case == "quant_pack_triton_alam":
+        args = (x, 2, 256, True, 4, True, 3.0)
+    elif case == "dequant_unpack_triton_alam":
+        p, s, m = ops.quant_pack_triton(x, 4, 256, True, 2, True, 3.0)
+        args = (p, s, m, 4, 256, True, 2)
     elif case == "quant_pack_tiles":
         args = (_x((2, 4, 32, 48)), 2, 256, False, 0.0, False, 0, None, 0, 0, torch.float32)
     elif case == "pack_triton":
@@ -53,7 +59,8 @@ def test_opcheck(case):
         args = (_x((512, 256), 3), _x((512, 256), 4), None, None, None, 256, 0, 0, True, torch.float32)
     # test_schema mutates-and-compares its inputs with arithmetic torch lacks for fp8 tensors
     tests = TESTS[1:] if case.startswith("fp8") else TESTS
-    torch.library.opcheck(getattr(ops, case).default, args, test_utils=tests)
+    name = case[:-len("_alam")] if case.endswith("_alam") else case  # the avg_alam cases of the same op
+    torch.library.opcheck(getattr(ops, name).default, args, test_utils=tests)
 
 
 def test_compile_round_trip_matches_eager():

@@ -204,10 +204,87 @@ def test_reference_schema_ops(bits):
     np.testing.assert_array_equal(np_view(y).reshape(yo.shape), yo)
 
 
-def test_avg_alam_is_rejected():
-    x = torch.zeros(1, 1, 256, dtype=torch.bfloat16, device=DEV)
-    with pytest.raises(NotImplementedError):
-        torch.ops.act_lib.quant_pack_triton(x, 2, 256, True, 2, False, 0.0)
+# ----------------------------------------------------------------------------- ALAM averaging
+def _codes(packed, bits):
+    """Little-endian b-bit fields of uint32 words -> [rows, words * 32 / b] (any code count)."""
+    w = np.ascontiguousarray(packed).view(np.uint32).reshape(packed.shape[0], -1).astype(np.uint64)
+    sh = np.arange(32 // bits, dtype=np.uint64) * np.uint64(bits)
+    return ((w[:, :, None] >> sh) & np.uint64((1 << bits) - 1)).reshape(w.shape[0], -1).astype(np.int64)
+
+
+def _alam_gpu_raw(x, bits, g, alam, flags=0, alpha=0.0):
+    """dopt_alam_quant_pack through the C ABI on a [NG, g] tensor -> (packed, scale, min) on the CPU."""
+    L = _lib.lib()
+    xd = x.to(DEV).contiguous()
+    ng = xd.numel() // g
+    p = torch.empty((ng, g * bits // 32 // alam), dtype=torch.int32, device=DEV)
+    s = torch.empty(ng, dtype=torch.bfloat16, device=DEV)
+    m = torch.empty(ng, dtype=torch.bfloat16, device=DEV)
+    code = {torch.float32: _lib.F32, torch.float16: _lib.F16, torch.bfloat16: _lib.BF16}[xd.dtype]
+    rc = L.dopt_alam_quant_pack(xd.data_ptr(), code, ng, g, bits, alam, flags, alpha, p.data_ptr(), s.data_ptr(),
+                                m.data_ptr(), torch.cuda.current_stream().cuda_stream)
+    assert rc == 0, L.dopt_last_error()
+    torch.cuda.synchronize()
+    return np_view(p), np_view(s), np_view(m)
+
+
+@pytest.mark.parametrize("bits,alam", [(1, 1), (1, 8), (2, 2), (2, 4), (4, 4), (8, 2), (8, 8)])
+@pytest.mark.parametrize("g", [64, 256, 1024])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=["bf16", "f32"])
+def test_alam_quant_pack_bit_exact_without_squash(dtype, g, bits, alam):
+    """Without the squash (a C-ABI option; the operator always squashes) the codes, scale and min
+    are bit-exact against the oracle: min/max, step, the fma code arguments, the left-to-right
+    run sums and the truncation."""
+    if (g * bits // 32) % alam:
+        pytest.skip("alam_bits must divide the group's words")
+    x = make_input((3, 37, g), dtype, seed=bits * 7 + alam)
+    p, s, m = _alam_gpu_raw(x, bits, g, alam)
+    rp, rs, rm = oracle.alam_quant_pack(np_view(x).reshape(-1, g), g, bits, alam)
+    np.testing.assert_array_equal(p.view(np.uint32).reshape(rp.shape), rp)
+    np.testing.assert_array_equal(s, rs)
+    np.testing.assert_array_equal(m, rm)
+    # the clamp alone (NaN and +-inf included) is exact as well
+    x.view(-1)[:3] = torch.tensor([float("nan"), float("inf"), -float("inf")]).to(dtype)
+    p, s, m = _alam_gpu_raw(x, bits, g, alam, flags=oracle.FLAG_CLAMP, alpha=2.5)
+    rp, rs, rm = oracle.alam_quant_pack(np_view(x).reshape(-1, g), g, bits, alam, flags=oracle.FLAG_CLAMP,
+                                        clamp_alpha=2.5)
+    np.testing.assert_array_equal(p.view(np.uint32).reshape(rp.shape), rp)
+    np.testing.assert_array_equal(s, rs)
+    np.testing.assert_array_equal(m, rm)
+
+
+@pytest.mark.parametrize("bits,alam", [(2, 2), (4, 4), (8, 8), (1, 8)])
+def test_alam_reference_operators(bits, alam):
+    """quant_pack_triton / dequant_unpack_triton with avg_alam=True (the reference's clamp 3 +
+    squash): packed [NG, NW / alam_bits], scale/min within 1 bf16 ulp of the oracle (the squash is
+    tolerance-only) and codes within one; the dequant of the GPU's own codes equals the oracle's
+    within one bf16 ulp (the noise's log / cos differ by fp32 ulps between the libraries), with
+    the element-to-noise mapping of Triton's randn(42 + group, element)."""
+    g = 256
+    x = make_input((4, 50, g), torch.bfloat16, seed=bits + alam)
+    p, s, m = torch.ops.act_lib.quant_pack_triton(x.to(DEV), bits, g, True, alam, True, 3.0)
+    assert p.shape == (200, g * bits // 32 // alam) and s.shape == (4, 50) and s.dtype == torch.bfloat16
+    rp, rs, rm = oracle.alam_quant_pack(np_view(x).reshape(-1, g), g, bits, alam, flags=3, clamp_alpha=3.0)
+    np.testing.assert_allclose(s.float().cpu().numpy().reshape(-1), oracle.bf16_bits_to_f32(rs), rtol=2 ** -7)
+    np.testing.assert_allclose(m.float().cpu().numpy().reshape(-1), oracle.bf16_bits_to_f32(rm), rtol=2 ** -7,
+                               atol=1e-30)
+    cg, cr = _codes(np_view(p), bits), _codes(rp, bits)
+    assert np.max(np.abs(cg - cr)) <= 1 and np.mean(cg != cr) < 2e-3
+    y = torch.ops.act_lib.dequant_unpack_triton(p, s, m, bits, g, True, alam)
+    torch.cuda.synchronize()
+    assert y.shape == (4, 50, g) and y.dtype == torch.bfloat16
+    yo = oracle.alam_dequant_unpack(np_view(p), np_view(s).reshape(-1), np_view(m).reshape(-1), g, bits, alam)
+    yg = np_view(y).reshape(yo.shape).astype(np.int64)
+    diff = np.abs(yg - yo.astype(np.int64))  # bf16 bit patterns: same sign, so ulp distance
+    assert diff.max() <= 1 and np.mean(diff != 0) < 0.01
+
+
+def test_alam_rejects_bad_run_lengths():
+    x = torch.zeros(1, 1, 64, dtype=torch.bfloat16, device=DEV)
+    with pytest.raises(RuntimeError):
+        torch.ops.act_lib.quant_pack_triton(x, 2, 64, True, 8, False, 0.0)  # 4 words per group
+    with pytest.raises(RuntimeError):
+        torch.ops.act_lib.quant_pack_triton(x, 2, 64, True, 3, False, 0.0)
 
 
 def test_mismatched_sizes_are_rejected_before_launch():

@@ -559,3 +559,114 @@ def test_noise_near_one_is_clamped_to_qmax():
         pre = np.rint((fma32(t, inv, u[np.arange(64), imax]) - np.float32(0.5)).astype(np.float32))
         assert (pre == qmax + 1).mean() > 0.3
         np.testing.assert_array_equal(p, numpy_quant(x, bits, NOISE, u)[0])
+
+
+# ----------------------------------------------------------------------------- ALAM averaging
+SQ_CL = oracle.FLAG_SQUASH | oracle.FLAG_CLAMP
+
+
+def _bf16_to_f32(bits_u16):
+    return (np.asarray(bits_u16, dtype=np.uint32) << 16).view(np.float32)
+
+
+@pytest.mark.parametrize("bits", [1, 2, 4, 8])
+def test_alam_one_equals_the_quantizer(bits):
+    """alam_bits = 1 averages runs of one value: the plain quantizer with bf16 meta."""
+    x = np.random.default_rng(bits).standard_normal((6, 256)).astype(np.float32)
+    p, s, m = oracle.alam_quant_pack(x, 256, bits, 1, flags=SQ_CL, clamp_alpha=3.0)
+    rp, rs, rm = oracle.quant_pack(x, 256, bits, flags=SQ_CL, clamp_alpha=3.0, meta_dtype=BF16)
+    np.testing.assert_array_equal(p, rp)
+    np.testing.assert_array_equal(s, rs)
+    np.testing.assert_array_equal(m, rm)
+
+
+@pytest.mark.parametrize("bits", [1, 2, 4, 8])
+def test_alam_two_on_pairs_of_equal_values(bits):
+    """With every run of 2 holding one value twice, the run's mean is that value's code argument
+    exactly (qf + qf and the halving are exact), so the ALAM codes are the plain codes of the
+    even elements."""
+    base = np.random.default_rng(10 + bits).standard_normal((5, 128)).astype(np.float32)
+    x = np.repeat(base, 2, axis=1)  # [5, 256], x[2c] == x[2c + 1]
+    p, s, m = oracle.alam_quant_pack(x, 256, bits, 2, flags=oracle.FLAG_SQUASH)
+    rp, rs, rm = oracle.quant_pack(x, 256, bits, flags=oracle.FLAG_SQUASH, meta_dtype=BF16)
+    codes = oracle.unpack_codes(p, 128, bits).view(np.uint8)
+    plain = oracle.unpack_codes(rp, 256, bits).view(np.uint8)
+    np.testing.assert_array_equal(codes, plain[:, 0::2])
+    np.testing.assert_array_equal(s, rs)
+    np.testing.assert_array_equal(m, rm)
+
+
+@pytest.mark.parametrize("bits,alam", [(2, 2), (2, 4), (4, 4), (8, 8), (1, 8)])
+def test_alam_codes_are_the_truncated_run_means(bits, alam):
+    """Each code is trunc(mean of the run's nearest-code arguments), with the arguments taken from
+    the plain quantizer's own step and min (pinned above) and the mean in float64: equal except
+    where summation order decides a boundary, and never off by more than one."""
+    rng = np.random.default_rng(bits * 31 + alam)
+    x = rng.standard_normal((8, 512)).astype(np.float32)
+    p, s, m = oracle.alam_quant_pack(x, 512, bits, alam, flags=oracle.FLAG_SQUASH)
+    # squashed values and the plain quantizer's fp32 step / min for the same groups
+    xs = np.tanh(x.astype(np.float64) / 0.5) * 0.5
+    _, s32, m32 = oracle.quant_pack(x, 512, bits, flags=oracle.FLAG_SQUASH, meta_dtype=F32)
+    np.testing.assert_array_equal(_bf16_to_f32(s), _bf16_to_f32(oracle.quant_pack(
+        x, 512, bits, flags=oracle.FLAG_SQUASH, meta_dtype=BF16)[1]))
+    qf = (xs - m32[:, None].astype(np.float64)) / s32[:, None].astype(np.float64) + (0.5 - 1e-6)
+    want = np.clip(np.floor(qf.reshape(8, 512 // alam, alam).mean(axis=2)), 0, (1 << bits) - 1)
+    got = oracle.unpack_codes(p, 512 // alam, bits).view(np.uint8).astype(np.float64)
+    assert np.max(np.abs(got - want)) <= 1
+    assert np.mean(got != want) < 0.002
+
+
+def test_alam_rejects_shapes_the_reference_cannot_reshape():
+    x = np.zeros((1, 64), np.float32)
+    with pytest.raises(oracle.OracleError):
+        oracle.alam_quant_pack(x, 64, 2, 8)  # 4 words of codes: 8 does not divide them
+    with pytest.raises(oracle.OracleError):
+        oracle.alam_quant_pack(x, 64, 2, 3)  # not a power of two
+
+
+def test_triton_randn_box_muller_from_the_philox_words():
+    """Triton's randn: the first two Philox words (pinned by the known-answer vectors) -> uniforms
+    (int32 folded to non-negative, times fp32(4.6566127342e-10)) -> Box-Muller's first output.
+    Checked against float64 from the same words, to fp32 rounding of log / cos / sqrt."""
+    for seed, off in [(42, 0), (42, 1), (43, 7), (42 + 100000, 255), (2**33 + 5, 1023)]:
+        ctr = np.array([off, 0, 0, 0], np.uint32)
+        key = np.array([seed & 0xFFFFFFFF, seed >> 32], np.uint32)
+        out = np.zeros(4, np.uint32)
+        oracle.lib().oracle_philox4x32_10(ctr.ctypes.data, key.ctypes.data, out.ctypes.data)
+
+        def uni(w):
+            i = int(np.array(w, np.uint32).view(np.int32))
+            i = ~i if i < 0 else i
+            return float(np.float32(i) * np.float32(4.6566127342e-10))
+        u1, u2 = max(uni(out[0]), float(np.float32(1e-7))), uni(out[1])
+        want = np.sqrt(-2.0 * np.log(u1)) * np.cos(2.0 * np.pi * u2)
+        got = oracle.triton_randn(seed, off)
+        assert abs(got - want) <= 8e-6 * max(1.0, abs(want)), (seed, off, got, want)
+
+
+def test_triton_randn_is_standard_normal():
+    vals = np.array([oracle.triton_randn(42 + r, e) for r in range(64) for e in range(512)])
+    assert abs(vals.mean()) < 0.01
+    assert abs(vals.std() - 1.0) < 0.01
+    # two-sided tail frequencies of a standard normal
+    assert abs(np.mean(np.abs(vals) > 1.0) - 0.3173) < 0.01
+    assert abs(np.mean(np.abs(vals) > 2.0) - 0.0455) < 0.005
+
+
+@pytest.mark.parametrize("bits,alam", [(2, 2), (4, 4), (8, 2)])
+def test_alam_dequant_is_code_plus_centred_noise(bits, alam):
+    """y = bf16(fma(code + n - 0.5, scale, min)) with n the noise above: given the codes, the
+    residual (y - min) / scale - code has the noise's distribution shifted by -0.5, and element e
+    of group r carries randn(42 + r, e)."""
+    x = np.random.default_rng(7).standard_normal((64, 256)).astype(np.float32)
+    p, s, m = oracle.alam_quant_pack(x, 256, bits, alam, flags=oracle.FLAG_SQUASH)
+    y = _bf16_to_f32(oracle.alam_dequant_unpack(p, s, m, 256, bits, alam)).astype(np.float64)
+    sc, mn = _bf16_to_f32(s).astype(np.float64), _bf16_to_f32(m).astype(np.float64)
+    codes = np.repeat(oracle.unpack_codes(p, 256 // alam, bits).view(np.uint8).astype(np.float64), alam, axis=1)
+    resid = (y - mn[:, None]) / sc[:, None] - codes
+    assert abs(resid.mean() + 0.5) < 0.03
+    assert abs(resid.std() - 1.0) < 0.03
+    for r, e in [(0, 0), (3, 17), (63, 255)]:
+        n = oracle.triton_randn(42 + r, e)
+        want = (codes[r, e] + (n - 0.5)) * sc[r] + mn[r]
+        assert abs(y[r, e] - want) <= 2 ** -7 * abs(want) + 1e-30
