@@ -425,7 +425,7 @@ def _kmajor(t: Tensor, rows: int, k: int, stride_r: int, stride_k: int, k_pad: i
     """(tensor, row stride) of an e4m3 operand as the GEMM reads it: rows K-contiguous, row stride a
     multiple of 16, 16-byte aligned. Used in place when it already is; otherwise packed by
     dopt_fp8_pack_kmajor into a fresh [rows, k_pad] buffer whose padding columns are zero."""
-    if stride_k == 1 and k == k_pad and stride_r % 16 == 0 and k <= stride_r <= (1 << 23) and t.data_ptr() % 16 == 0:
+    if stride_k == 1 and k == k_pad and stride_r % 16 == 0 and k <= stride_r < (1 << 23) and t.data_ptr() % 16 == 0:
         return t, stride_r
     out = (torch.zeros if k_pad != k else torch.empty)((rows, k_pad), dtype=torch.uint8, device=t.device)
     rc = _lib.lib().dopt_fp8_pack_kmajor(t.data_ptr(), rows, k, stride_r, stride_k, out.data_ptr(), k_pad, _stream(t))

@@ -364,8 +364,9 @@ int dopt_fp8_gemm_nt(const uint8_t* A, const uint8_t* B, int64_t M, int64_t N, i
                     "fp8 GEMM needs 16-byte aligned A and B, lda and ldb multiples of 16 and >= K, a 2-byte aligned C "
                     "and ldc >= N (got lda=%lld ldb=%lld ldc=%lld K=%lld N=%lld)",
                     (long long)lda, (long long)ldb, (long long)ldc, (long long)K, (long long)N);
-    if (lda > (1 << 23) || ldb > (1 << 23))
-        return fail(DOPT_EINVAL, "fp8 GEMM row strides must be at most 2^23 bytes (32-bit tile offsets), got %lld, %lld",
+    // a 256-row tile's offsets (up to 256 * lda) must stay inside the buffer range 0x7FFFFF00
+    if (lda >= (1 << 23) || ldb >= (1 << 23))
+        return fail(DOPT_EINVAL, "fp8 GEMM row strides must be below 2^23 bytes (32-bit tile offsets), got %lld, %lld",
                     (long long)lda, (long long)ldb);
     if ((M + 255) / 256 * ((N + 255) / 256) >= ((int64_t)1 << 31))
         return fail(DOPT_EINVAL, "fp8 GEMM output too large: %lld x %lld", (long long)M, (long long)N);

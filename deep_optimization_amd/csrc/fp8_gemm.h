@@ -2,6 +2,10 @@
 //   C[m][n] = bf16(out_scale * sum_k A[m][k] * B[n][k]), fp32 accumulation, one rounding.
 // Any M, N >= 0; K a multiple of 16 (one 16-byte load per lane); A, B rows 16-byte aligned.
 //
+// Two kernels share the tiling below: fp8_gemm_nt_kernel computes one tile per workgroup, and
+// fp8_gemm_nt_persistent_kernel (further down, the launcher's choice for an even, non-zero
+// number of K slabs) runs one workgroup per CU over a list of tiles.
+//
 // Tiling: a workgroup of 4 waves (2 x 2) computes a BM x BN tile; each wave a (BM/2) x (BN/2)
 // sub-tile as TM x TN blocks of v_mfma_f32_32x32x64_f8f6f4 (fp8 x fp8 -> fp32, 32 x 32 x 64 per
 // instruction, 16 accumulator registers per block). At 128 x 128 per wave one 128-byte K slab
@@ -49,6 +53,8 @@ namespace dopt {
 
 typedef int v8i_t __attribute__((ext_vector_type(8)));
 typedef float v16f_t __attribute__((ext_vector_type(16)));
+typedef uint32_t v4u_t __attribute__((ext_vector_type(4)));
+typedef uint32_t v2u_t __attribute__((ext_vector_type(2)));
 typedef __attribute__((address_space(3))) void lds_void_t;
 
 __device__ __forceinline__ v16f_t mfma_fp8_32x32x64(const v8i_t& a, const v8i_t& b, const v16f_t& c) {
@@ -309,6 +315,320 @@ inline int fp8_gemm_launch(const uint8_t* A, const uint8_t* B, int64_t M, int64_
         hipLaunchKernelGGL((fp8_gemm_nt_kernel<C, false>), dim3((uint32_t)tiles), dim3(C::THREADS), 0, s, p);
     else
         hipLaunchKernelGGL((fp8_gemm_nt_kernel<C, true>), dim3((uint32_t)tiles), dim3(C::THREADS), 0, s, p);
+    return 0;
+}
+
+// ---------------------------------------------------------------------------------------------
+// Persistent form: one workgroup per CU walks a list of tiles, and its slab pipeline runs across
+// tile boundaries. The loads of a tile's first two slabs are issued during the last two slabs of
+// the previous tile, so a tile starts with its operands in LDS. The epilogue stages through an
+// LDS array of its own (32 rows of a wave's tile at a time), so its C stores drain while the
+// next tile's MFMAs run.
+//
+// Tile list: XCD x (workgroup ids x, x+8, ...) owns the contiguous tile range of the
+// non-persistent kernel; its g_x workgroups take tiles first + local, first + local + g_x, ...,
+// so at any time the XCD's workgroups work on neighbouring tiles of one GROUP_M group.
+//
+// The MFMA takes B's fragment as its first operand and A's as its second, which transposes the
+// accumulator: lane l holds row i*32 + l%32 of A's tile and, in registers 4q..4q+3, the four
+// consecutive columns j*32 + 8q + 4*(l/32) + {0..3}. Each lane writes 8-byte runs of bf16 into
+// the staging rows, and 16-byte row chunks go out with whole-row coalescing.
+template <class C, bool EDGE>
+__global__ __launch_bounds__(256, 1) void fp8_gemm_nt_persistent_kernel(Fp8GemmArgs p) {
+    constexpr int BM = C::BM, BN = C::BN, BK = C::BK, TM = C::TM, TN = C::TN, WM = C::WM, WN = C::WN;
+    constexpr int CPR = WN / 8;             // 16-byte chunks per staged row
+    constexpr int ESTAGE = 32 * WN * 2;     // bytes staged per wave: 32 rows of its tile
+    static_assert(CPR == 8 || CPR == 16, "staging swizzle");
+    const int64_t M = p.M, N = p.N, K = p.K, lda = p.lda, ldb = p.ldb, ldc = p.ldc;
+    __shared__ __attribute__((aligned(1024))) uint8_t sA0[BM * BK];
+    __shared__ __attribute__((aligned(1024))) uint8_t sA1[BM * BK];
+    __shared__ __attribute__((aligned(1024))) uint8_t sB0[BN * BK];
+    __shared__ __attribute__((aligned(1024))) uint8_t sB1[BN * BK];
+    __shared__ __attribute__((aligned(1024))) uint8_t sE[4 * ESTAGE];
+
+    // ---- this workgroup's tiles
+    const uint32_t tiles_m = p.tiles_m, tiles_n = p.tiles_n;
+    const uint32_t n_tiles = tiles_m * tiles_n;
+    const uint32_t G = gridDim.x, bid = blockIdx.x;
+    const uint32_t xcd = bid % GEMM_XCDS, local = bid / GEMM_XCDS;
+    const uint32_t g_x = G / GEMM_XCDS + (xcd < G % GEMM_XCDS ? 1u : 0u);
+    const uint32_t per = n_tiles / GEMM_XCDS, rem = n_tiles % GEMM_XCDS;
+    const uint32_t first = xcd * per + min(xcd, rem), cnt = per + (xcd < rem ? 1u : 0u);
+    const uint32_t my = local < cnt ? (cnt - local + g_x - 1) / g_x : 0u;
+    const uint32_t nk = (uint32_t)((K + BK - 1) / BK);
+    const uint32_t total = my * nk;
+    if (total == 0) return;  // the same for every wave of the workgroup
+    auto coords = [&](uint32_t i, uint32_t& tm, uint32_t& tn) __attribute__((always_inline)) {
+        const uint32_t t = first + local + i * g_x;
+        const uint32_t group = C::GROUP_M * tiles_n;
+        const uint32_t first_m = (t / group) * C::GROUP_M;
+        const uint32_t gsize = min(tiles_m - first_m, (uint32_t)C::GROUP_M);
+        tm = first_m + (t % group) % gsize;
+        tn = (t % group) / gsize;
+    };
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: tile bases stay scalar
+    const int wm = wave >> 1, wn = wave & 1;
+
+    // ---- global -> LDS slab loads (lane mapping and swizzle as in fp8_gemm_nt_kernel), two slabs
+    // ahead of the compute side
+    const int lrow8 = lane >> 3;
+    const int lchunk = (lane & 7) ^ ((4 * (wave & 1) + (lane >> 4)) & 7);
+    const int r0 = 8 * wave + lrow8;
+    const uint32_t offa0 = (uint32_t)(r0 * lda + lchunk * 16), offb0 = (uint32_t)(r0 * ldb + lchunk * 16);
+    const uint32_t stepa = (uint32_t)(32 * lda), stepb = (uint32_t)(32 * ldb);
+    // Tile it's slabs are issued from cur_t's buffer resources and tile it+1's from next_t's: slab
+    // k of the compute side issues slab k+2 of the stream, which for the last two slabs of a tile
+    // is slab k+2-nk of the next tile. The choice is a set of scalar selects, so a slab has no
+    // branches and the next slab's operand reads stay interleaved with its MFMAs.
+    struct IssueTile {
+        __amdgpu_buffer_rsrc_t ra, rb;
+        int rows_a, rows_b;
+        bool live;
+    };
+    auto issue_tile = [&](uint32_t i) __attribute__((always_inline)) {
+        IssueTile t;
+        uint32_t tm, tn;
+        t.live = i < my;
+        coords(t.live ? i : my - 1, tm, tn);
+        const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
+        t.ra = __builtin_amdgcn_make_buffer_rsrc((void*)(p.A + m0 * lda), (short)0, (int)GEMM_RANGE, 0x00020000);
+        t.rb = __builtin_amdgcn_make_buffer_rsrc((void*)(p.B + n0 * ldb), (short)0, (int)GEMM_RANGE, 0x00020000);
+        t.rows_a = EDGE ? (int)min((int64_t)BM, M - m0) - r0 : BM;
+        t.rows_b = EDGE ? (int)min((int64_t)BN, N - n0) - r0 : BN;
+        return t;
+    };
+    IssueTile cur_t = issue_tile(0), next_t = issue_tile(1);
+    // The lane's row/chunk offset goes in voffset, the wave-uniform row-block and K offsets in
+    // soffset. A lane that must load nothing (a slab past this workgroup's last tile; with EDGE a
+    // row past M or N or 16 bytes past K) gets voffset GEMM_OOB, past the resource's range.
+    auto issue = [&](uint8_t* sa, uint8_t* sb, uint32_t ks) __attribute__((always_inline)) {
+        const bool nxt = ks >= nk;
+        const __amdgpu_buffer_rsrc_t ra = nxt ? next_t.ra : cur_t.ra;
+        const __amdgpu_buffer_rsrc_t rb = nxt ? next_t.rb : cur_t.rb;
+        const bool live = nxt ? next_t.live : cur_t.live;
+        const int64_t k0 = (int64_t)(nxt ? ks - nk : ks) * BK;
+        const uint32_t va = live ? offa0 : GEMM_OOB, vb = live ? offb0 : GEMM_OOB;
+        int la = C::BM, lb = C::BN;
+        if constexpr (EDGE) {
+            const bool k_ok = k0 + lchunk * 16 < K;
+            la = k_ok ? (nxt ? next_t.rows_a : cur_t.rows_a) : 0;
+            lb = k_ok ? (nxt ? next_t.rows_b : cur_t.rows_b) : 0;
+        }
+#pragma unroll
+        for (int j = 0; j < C::LA; ++j)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_void_t*)(sa + wave * 1024 + j * 4096), 16,
+                                                     !EDGE || 32 * j < la ? va : GEMM_OOB,
+                                                     (int)(j * stepa + (uint32_t)k0), 0, 0);
+#pragma unroll
+        for (int j = 0; j < C::LB; ++j)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_void_t*)(sb + wave * 1024 + j * 4096), 16,
+                                                     !EDGE || 32 * j < lb ? vb : GEMM_OOB,
+                                                     (int)(j * stepb + (uint32_t)k0), 0, 0);
+    };
+
+    const int orow = lane & 31;
+    const int oc = 2 * (lane >> 5);
+    const int sw = (lane >> 1) & 7;
+    // LDS accesses use native vector types and shallow address arithmetic: a HIP uint4 access is
+    // split into four dword accesses a level deeper, past the depth to which the LDS lowering
+    // attaches the alias scopes that tell the compiler an operand read does not touch the buffer
+    // an in-flight global -> LDS load is writing (without them it waits for those loads)
+    auto read_ops = [&](const uint8_t* sa, const uint8_t* sb, int h, v8i_t* a, v8i_t* b) __attribute__((always_inline)) {
+        const int ra0 = (WM * wm + orow) * BK, rb0 = (WN * wn + orow) * BK;
+        const int p0 = ((4 * h + oc) ^ sw) * 16, p1 = ((4 * h + oc + 1) ^ sw) * 16;
+#pragma unroll
+        for (int i = 0; i < TM; ++i) {
+            const v4u_t x0 = *(const v4u_t*)(sa + (ra0 + i * 32 * BK + p0));
+            const v4u_t x1 = *(const v4u_t*)(sa + (ra0 + i * 32 * BK + p1));
+            a[i] = __builtin_bit_cast(v8i_t, __builtin_shufflevector(x0, x1, 0, 1, 2, 3, 4, 5, 6, 7));
+        }
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+            const v4u_t x0 = *(const v4u_t*)(sb + (rb0 + j * 32 * BK + p0));
+            const v4u_t x1 = *(const v4u_t*)(sb + (rb0 + j * 32 * BK + p1));
+            b[j] = __builtin_bit_cast(v8i_t, __builtin_shufflevector(x0, x1, 0, 1, 2, 3, 4, 5, 6, 7));
+        }
+    };
+
+    v16f_t acc[TM][TN];
+    auto zero_acc = [&]() __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int j = 0; j < TN; ++j)
+#pragma unroll
+                for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
+    };
+    zero_acc();
+    v8i_t a0[TM], b0[TN], a1[TM], b1[TN];
+    auto mma = [&](const v8i_t* a, const v8i_t* b) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int j = 0; j < TN; ++j) acc[i][j] = mfma_fp8_32x32x64(b[j], a[i], acc[i][j]);
+    };
+
+    // ---- epilogue of compute tile i: scale, round once to bf16, stage 32 rows of the wave's
+    // tile at a time (16-byte chunk c of row r at position c ^ (r % CPR)), store row chunks
+    uint8_t* stage = sE + wave * ESTAGE;
+    auto epilogue = [&](uint32_t i_tile) __attribute__((always_inline)) {
+        uint32_t tm, tn;
+        coords(i_tile, tm, tn);
+        const int64_t row0 = (int64_t)tm * BM + WM * wm, col0 = (int64_t)tn * BN + WN * wn;
+        // the lane index passes through an empty asm so that the addresses below are computed
+        // here, once per tile, instead of being hoisted out of the tile loop into registers
+        int ln = lane;
+        asm volatile("" : "+v"(ln));
+        uint32_t ldc2 = (uint32_t)ldc * 2;  // row pitch of C in bytes (< GEMM_RANGE / BM on this path)
+        asm volatile("" : "+s"(ldc2));
+        const int er = ln & 31, h = ln >> 5;
+        const int rr = ln / CPR, rc = ln % CPR;  // read side: row rr + r * (64 / CPR), chunk rc
+        // whole tiles: one buffer resource per tile, the lane's offset in voffset and the row
+        // block's in soffset
+        const __amdgpu_buffer_rsrc_t rcs = __builtin_amdgcn_make_buffer_rsrc(
+            (void*)(p.C + row0 * ldc + col0), (short)0, (int)GEMM_RANGE, 0x00020000);
+        const uint32_t vo = (uint32_t)rr * ldc2 + (uint32_t)rc * 16;
+#pragma unroll
+        for (int i = 0; i < TM; ++i) {
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int j = 0; j < TN; ++j) {
+                // one 32 x 32 block's accumulators move to VGPRs here, not all of them at once
+                v16f_t t = acc[i][j];
+                asm volatile("" : "+v"(t));
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const v2u_t w = {pack_bf16x2(t[4 * q] * p.out_scale, t[4 * q + 1] * p.out_scale),
+                                     pack_bf16x2(t[4 * q + 2] * p.out_scale, t[4 * q + 3] * p.out_scale)};
+                    const int c = (j * 32 + 8 * q) / 8;
+                    *(v2u_t*)(stage + (er * (WN * 2) + ((c ^ (er & (CPR - 1))) * 16) + 8 * h)) = w;
+                }
+            }
+#pragma unroll
+            for (int r = 0; r < 32 * CPR / 64; ++r) {
+                const int row = rr + r * (64 / CPR);
+                const v4u_t v = *(const v4u_t*)(stage + (row * (WN * 2) + ((rc ^ (row & (CPR - 1))) * 16)));
+                const int grow = i * 32 + row;
+                if constexpr (!EDGE) {
+                    __builtin_amdgcn_raw_buffer_store_b128(v, rcs, vo,
+                                                           (int)((uint32_t)(i * 32 + r * (64 / CPR)) * ldc2), 0);
+                } else {
+                    if (row0 + grow >= M) continue;
+                    const int64_t n = col0 + rc * 8;
+                    uint16_t* dst = p.C + (row0 + grow) * ldc + n;
+                    if (p.vec_store && n + 8 <= N) {
+                        *(v4u_t*)dst = v;
+                    } else {
+                        const uint16_t e8[8] = {(uint16_t)v.x, (uint16_t)(v.x >> 16), (uint16_t)v.y,
+                                                (uint16_t)(v.y >> 16), (uint16_t)v.z, (uint16_t)(v.z >> 16),
+                                                (uint16_t)v.w, (uint16_t)(v.w >> 16)};
+                        for (int e = 0; e < 8 && n + e < N; ++e) dst[e] = e8[e];
+                    }
+                }
+            }
+        }
+    };
+
+    // ---- one slab of the stream: buffer PAR holds slab s, the other buffer slab s+1 (loads in
+    // flight), half 0 operands of slab s in a0/b0; schedule as the even interleave of
+    // fp8_gemm_nt_kernel. The LAST slab of a tile leaves the next slab's half-0 operand read to
+    // after the epilogue, which then has the operand registers to itself.
+    // Vector memory operations complete in issue order and vmcnt counts stores too: in the slab
+    // after an epilogue the wait at the barrier is vmcnt(EPI_STORES), which covers the slab loads
+    // issued before the epilogue's stores and leaves those stores in flight. That takes the
+    // epilogue's exact store count: whole-chunk stores only (no EDGE instance, aligned C).
+    constexpr int EPI_STORES = TM * (32 * CPR / 64);
+    static_assert(EPI_STORES < 64, "vmcnt field");
+    constexpr int WAIT_EPI = (EPI_STORES & 15) | ((EPI_STORES >> 4) << 14) | (7 << 4);  // lgkmcnt(0)
+    auto slab = [&](uint8_t* sa, uint8_t* sb, uint8_t* na, uint8_t* nb, uint32_t k, auto last, auto epi)
+                    __attribute__((always_inline)) {
+        constexpr bool LAST = decltype(last)::value;
+        constexpr bool AFTER_EPI = decltype(epi)::value && !EDGE;
+        constexpr int NM = TM * TN;
+        read_ops(sa, sb, 1, a1, b1);
+        mma(a0, b0);
+#pragma unroll
+        for (int q = 0; q < NM; ++q) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        }
+        if constexpr (AFTER_EPI) __builtin_amdgcn_s_waitcnt(WAIT_EPI);
+        else __builtin_amdgcn_s_waitcnt(0);
+        // a bare barrier: __syncthreads' release fence would wait for the epilogue's stores; the
+        // memory clobber keeps the compiler from moving memory operations across it
+        asm volatile("s_barrier" ::: "memory");
+        issue(sa, sb, k + 2);
+        if constexpr (!LAST) read_ops(na, nb, 0, a0, b0);
+        mma(a1, b1);
+        if constexpr (LAST) {
+#pragma unroll
+            for (int q = 0; q < NM; ++q) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+            }
+        } else {
+#pragma unroll
+            for (int q = 0; q < NM; ++q) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            }
+        }
+    };
+    using BF = std::integral_constant<bool, false>;
+    using BT = std::integral_constant<bool, true>;
+
+    issue(sA0, sB0, 0);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    issue(sA1, sB1, 1);
+    read_ops(sA0, sB0, 0, a0, b0);
+    // nk is even, so every tile starts in buffer 0. The first slab of each later tile follows its
+    // predecessor's epilogue in straight-line code, so that the compiler's own wait bookkeeping
+    // sees the stores in flight on one path only and adds no waits of its own to that slab.
+    slab(sA0, sB0, sA1, sB1, 0, BF{}, BF{});
+    for (uint32_t it = 0;;) {
+        for (uint32_t k = 1; k + 2 < nk; k += 2) {
+            slab(sA1, sB1, sA0, sB0, k, BF{}, BF{});
+            slab(sA0, sB0, sA1, sB1, k + 1, BF{}, BF{});
+        }
+        slab(sA1, sB1, sA0, sB0, nk - 1, BT{}, BF{});
+        __builtin_amdgcn_sched_barrier(0);
+        epilogue(it);
+        __builtin_amdgcn_sched_barrier(0);
+        zero_acc();
+        // the next slab's loads were covered by the last slab's wait
+        read_ops(sA0, sB0, 0, a0, b0);
+        if (++it == my) break;
+        cur_t = next_t;
+        next_t = issue_tile(it + 1);
+        slab(sA0, sB0, sA1, sB1, 0, BF{}, BT{});
+    }
+    // the loads issued past the last slab write zeros into LDS: they land before the workgroup ends
+    __builtin_amdgcn_s_waitcnt(0);
+}
+
+// Persistent launch: min(tiles, CUs) workgroups (n_cu from the caller). An odd or zero slab
+// count (K / BK rounded up) takes the non-persistent kernel (which writes C = 0 for K = 0).
+template <class C>
+inline int fp8_gemm_persistent_launch(const uint8_t* A, const uint8_t* B, int64_t M, int64_t N, int64_t K,
+                                      int64_t lda, int64_t ldb, float out_scale, uint16_t* Cm, int64_t ldc,
+                                      int n_cu, hipStream_t s) {
+    Fp8GemmArgs p{A, B, Cm, M, N, K, lda, ldb, ldc, out_scale, (uint32_t)((M + C::BM - 1) / C::BM),
+                  (uint32_t)((N + C::BN - 1) / C::BN), (uint32_t)(ldc % 8 == 0 && ((uintptr_t)Cm & 15) == 0)};
+    const uint64_t tiles = (uint64_t)p.tiles_m * p.tiles_n;
+    if (tiles == 0) return 0;
+    const uint32_t grid = (uint32_t)(tiles < (uint64_t)n_cu ? tiles : (uint64_t)n_cu);
+    const int64_t nk = (K + C::BK - 1) / C::BK;
+    if (nk == 0 || nk % 2) return fp8_gemm_launch<C>(A, B, M, N, K, lda, ldb, out_scale, Cm, ldc, s);
+    // whole tiles with aligned C store through a buffer resource: a tile's offsets must stay in range
+    if (M % C::BM == 0 && N % C::BN == 0 && K % C::BK == 0 && p.vec_store && (int64_t)C::BM * ldc * 2 < GEMM_RANGE)
+        hipLaunchKernelGGL((fp8_gemm_nt_persistent_kernel<C, false>), dim3(grid), dim3(C::THREADS), 0, s, p);
+    else
+        hipLaunchKernelGGL((fp8_gemm_nt_persistent_kernel<C, true>), dim3(grid), dim3(C::THREADS), 0, s, p);
     return 0;
 }
 

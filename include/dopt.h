@@ -147,7 +147,7 @@ int dopt_unpack_codes(const uint32_t* packed, int64_t n_groups, int group_size, 
  * _DOLinear.backward (Activation_Compression/modules/ops.py:508-512).
  * Any M, N >= 0 (edge tiles masked, like linear.py's masked loads and stores :80-81, :93-95);
  * K % 16 == 0 (DOPT_EUNSUPPORTED otherwise; K == 0 gives C = 0); A, B 16-byte aligned; lda, ldb
- * multiples of 16, >= K and <= 2^23; ldc >= N (16-byte stores when C is 16-byte aligned and
+ * multiples of 16, >= K and < 2^23; ldc >= N (16-byte stores when C is 16-byte aligned and
  * ldc % 8 == 0, element stores otherwise).
  */
 int dopt_fp8_gemm_nt(const uint8_t* A, const uint8_t* B, int64_t M, int64_t N, int64_t K,

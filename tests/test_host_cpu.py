@@ -128,6 +128,8 @@ class TestValidationWithoutDevice:
         assert L.dopt_fp8_gemm_nt(8, 16, 256, 256, 128, 128, 128, 1.0, 16, 256, None) == _lib.EINVAL  # A unaligned
         assert L.dopt_fp8_gemm_nt(16, 16, 256, 250, 128, 128, 128, 1.0, 16, 249, None) == _lib.EINVAL  # ldc < N
         assert L.dopt_fp8_gemm_nt(16, 16, 256, 256, 128, 1 << 24, 128, 1.0, 16, 256, None) == _lib.EINVAL  # lda > 2^23
+        # a 256-row tile at lda = 2^23 would reach offset 2^31 - 1, past the buffer range
+        assert L.dopt_fp8_gemm_nt(16, 16, 256, 256, 128, 1 << 23, 128, 1.0, 16, 256, None) == _lib.EINVAL
 
 
 def test_bits_consts_contract():
