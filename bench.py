@@ -19,7 +19,9 @@ and the captured weight-noise step replayed from one HIP graph vs run eagerly.
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-extras] [--no-cpu]
        python bench.py --pmc-probe   (one copy kernel + the dominant kernel, for rocprofv3 --pmc)
        python bench.py --fp8-probe random|constant   (the 8192^3 FP8 GEMM alone, for rocprofv3 --pmc)
-       python bench.py --dw-probe   (three weight-gradient GEMMs at the ViT fc1 shape, for rocprofv3 --pmc)
+       python bench.py --dw-probe [--dw-tokens K1,K2,...]   (three weight-gradient GEMMs at the ViT fc1
+                   shape, for rocprofv3 --pmc; with --dw-tokens, five at each token count, a K sweep
+                   under rocprofv3 --kernel-trace)
 """
 from __future__ import annotations
 
@@ -322,22 +324,27 @@ def host_probe() -> int:
     return 0
 
 
-def dw_probe() -> int:
-    """Three weight-gradient GEMMs at the ViT-B/16 bs-128 fc1 shape (dy bf16 [25216, 3072], x_hat
-    bf16 [25216, 768], no bias gradient), for rocprofv3 --pmc runs."""
+def dw_probe(tokens: str | None = None) -> int:
+    """Weight-gradient GEMMs at the ViT-B/16 bs-128 fc1 shape (dy bf16 [K, 3072], x_hat bf16
+    [K, 768], no bias gradient): three at K = 25216 tokens for rocprofv3 --pmc runs, or with
+    `tokens` (comma-separated K values) five at each K, for a kernel-trace K sweep that separates
+    the cost per token from the fixed cost of a call (pipeline fill, split partials, reduce)."""
     import torch
 
     import deep_optimization_amd  # noqa: F401
 
     dev = torch.device("cuda:0")
-    g = torch.Generator(device=dev).manual_seed(7)
-    K, cin, cout = 128 * 197, 768, 3072
-    dy = torch.randn((K, cout), generator=g, device=dev).to(torch.bfloat16)
-    xh = torch.randn((K, cin), generator=g, device=dev).to(torch.bfloat16)
-    for _ in range(3):
-        torch.ops.act_lib.dw_gemm(dy, xh, None, None, None, cin, 0, 0, False, torch.bfloat16)
-    torch.cuda.synchronize()
-    print(f"dw probe: 3 x dw_gemm M={cout} N={cin} K={K}")
+    cin, cout = 768, 3072
+    ks, reps = ([int(k) for k in tokens.split(",")], 5) if tokens else ([128 * 197], 3)
+    for K in ks:
+        g = torch.Generator(device=dev).manual_seed(7)
+        dy = torch.randn((K, cout), generator=g, device=dev).to(torch.bfloat16)
+        xh = torch.randn((K, cin), generator=g, device=dev).to(torch.bfloat16)
+        for _ in range(reps):
+            torch.ops.act_lib.dw_gemm(dy, xh, None, None, None, cin, 0, 0, False, torch.bfloat16)
+        torch.cuda.synchronize()
+        print(f"dw probe: {reps} x dw_gemm M={cout} N={cin} K={K}", flush=True)
+        del dy, xh
     return 0
 
 
@@ -610,6 +617,7 @@ def main() -> int:
     ap.add_argument("--pmc-probe", action="store_true")
     ap.add_argument("--fp8-probe", choices=("random", "constant", "hipblaslt"))
     ap.add_argument("--dw-probe", action="store_true")
+    ap.add_argument("--dw-tokens", default=None)
     ap.add_argument("--valu-probe", action="store_true")
     ap.add_argument("--host-probe", action="store_true")
     ap.add_argument("--counter-probe", choices=("philox", "nearest", "gelu", "silu", "bn_squash", "bn_relu"))
@@ -626,7 +634,7 @@ def main() -> int:
     if args.counter_probe:
         return counter_probe(args.counter_probe)
     if args.dw_probe:
-        return dw_probe()
+        return dw_probe(args.dw_tokens)
     if args.valu_probe:
         return valu_probe()
     if args.host_probe:
