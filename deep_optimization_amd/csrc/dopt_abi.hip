@@ -826,10 +826,10 @@ int dopt_graph_replace_memsets(void* graph, int64_t* n_replaced) {
 }
 
 int dopt_valu_probe(int kind, float* out, int64_t n_blocks, void* stream) {
-    if (kind < 0 || kind > 7)
+    if (kind < 0 || kind > 8)
         return fail(DOPT_EINVAL,
-                    "kind must be 0..7 (fma, exp, rcp, mad64+xor, bf16 MFMA random / constant, fp8 MFMA random / "
-                    "constant), got %d", kind);
+                    "kind must be 0..8 (fma, exp, rcp, mad64+xor, bf16 MFMA random / constant, fp8 MFMA random / "
+                    "constant, exact-division check), got %d", kind);
     if (n_blocks < 1 || n_blocks > 65536) return fail(DOPT_EINVAL, "n_blocks must be in [1, 65536], got %lld",
                                                       (long long)n_blocks);
     if (!out || ((uintptr_t)out & 3u)) return fail(DOPT_EINVAL, "out must be a 4-byte aligned pointer");

@@ -10,6 +10,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "quant_pack.h"
+
 namespace dopt {
 namespace {
 
@@ -160,12 +162,30 @@ __global__ __launch_bounds__(PROBE_THREADS, 1) void mfma_fp8_rate_kernel(float* 
     out[(uint64_t)blockIdx.x * PROBE_THREADS + threadIdx.x] = t;
 }
 
+// The quantizer's fast exact-division helpers against the IEEE division, over every non-negative
+// fp32 bit pattern (+0 .. +inf, strided over the grid): div_by_qmax<3/15/255>(x) against x / QMAX,
+// and exact_rcp(x) against 1 / x. Each thread writes its count of differing bit patterns.
+__global__ __launch_bounds__(PROBE_THREADS) void division_check_kernel(float* __restrict__ out) {
+    const uint32_t t = blockIdx.x * PROBE_THREADS + threadIdx.x, nt = gridDim.x * PROBE_THREADS;
+    uint32_t bad = 0;
+    for (uint32_t u = t; u <= 0x7F800000u; u += nt) {
+        const float x = __uint_as_float(u);
+        bad += __float_as_uint(div_by_qmax<3>(x)) != __float_as_uint(x / 3.0f);
+        bad += __float_as_uint(div_by_qmax<15>(x)) != __float_as_uint(x / 15.0f);
+        bad += __float_as_uint(div_by_qmax<255>(x)) != __float_as_uint(x / 255.0f);
+        bad += __float_as_uint(exact_rcp(x)) != __float_as_uint(1.0f / x);
+    }
+    out[(uint64_t)blockIdx.x * PROBE_THREADS + threadIdx.x] = (float)bad;
+}
+
 }  // namespace
 
 // kind 0..3 (fma, exp, rcp, mad64 + xor), 4 / 5 (bf16 MFMA stream, random / constant operands),
-// 6 / 7 (fp8 MFMA stream, random / constant operands); out holds n_blocks * 256 floats
+// 6 / 7 (fp8 MFMA stream, random / constant operands), 8 (exact-division check: per-thread counts
+// of mismatches, 0 expected); out holds n_blocks * 256 floats
 const char* launch_valu_rate(int kind, float* out, uint32_t n_blocks, hipStream_t s) {
     switch (kind) {
+        case 8: hipLaunchKernelGGL(division_check_kernel, dim3(n_blocks), dim3(PROBE_THREADS), 0, s, out); break;
         case 6: hipLaunchKernelGGL(mfma_fp8_rate_kernel<true>, dim3(n_blocks), dim3(PROBE_THREADS), 0, s, out); break;
         case 7: hipLaunchKernelGGL(mfma_fp8_rate_kernel<false>, dim3(n_blocks), dim3(PROBE_THREADS), 0, s, out); break;
         case 4: hipLaunchKernelGGL(mfma_rate_kernel<true>, dim3(n_blocks), dim3(PROBE_THREADS), 0, s, out); break;

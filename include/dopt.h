@@ -376,7 +376,10 @@ int dopt_stream_probe(const void* x, const void* noise, void* codes, void* meta,
  * SIMD, 64 steps of 16 MFMAs, nothing else), with pseudo-random (4) or constant (5) operands:
  * n_blocks * 4 * 64 * 16 * 32768 flops per launch. Kinds 6 and 7 do the same with the FP8 GEMM's
  * v_mfma_scale_f32_32x32x64_f8f6f4 (e4m3, unit scales; 131072 flops each), random (6) or
- * constant (7) operands. n_blocks in [1, 65536].
+ * constant (7) operands. Kind 8 checks the quant-pack kernels' fast exact-division helpers (step =
+ * range / QMAX for QMAX = 3, 15, 255 and inv = 1 / step) against the IEEE fp32 division for every
+ * non-negative fp32 bit pattern, strided over the grid: out[t] = thread t's count of differing
+ * results (0 expected). n_blocks in [1, 65536].
  */
 int dopt_valu_probe(int kind, float* out, int64_t n_blocks, void* stream);
 

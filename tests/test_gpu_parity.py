@@ -701,6 +701,19 @@ def test_valu_probe_runs(kind):
         assert torch.isfinite(out.view(torch.float32)).all()
 
 
+def test_fast_exact_division_matches_ieee():
+    """The quantizer's step = range / QMAX (multiply by the rounded reciprocal, one fma correction)
+    and inv = 1 / step (v_rcp_f32 and one fma Newton step, the IEEE division for waves holding a
+    subnormal or huge step) give the correctly rounded fp32 result for every non-negative fp32
+    input: dopt_valu_probe kind 8 compares them with the division on all 2^31 + 1 bit patterns."""
+    L = _lib.lib()
+    out = torch.full((4096 * 256,), -1.0, dtype=torch.float32, device="cuda")
+    assert L.dopt_valu_probe(8, out.data_ptr(), 4096, torch.cuda.current_stream().cuda_stream) == 0
+    torch.cuda.synchronize()
+    assert not (out < 0).any()  # every thread reported
+    assert int(out.sum().item()) == 0
+
+
 def test_beyond_2pow32_elements():
     """A bf16 activation of 2^32 + 2^24 elements (8.6 GB; g = 1024, 4,210,688 groups): element
     offsets past 2^32 take the kernels' 64-bit address arithmetic, and the Philox counter (the

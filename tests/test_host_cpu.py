@@ -113,7 +113,7 @@ class TestValidationWithoutDevice:
 
     def test_valu_probe_argument_checks(self):
         L = _lib.lib()
-        assert L.dopt_valu_probe(8, 16, 8, None) == _lib.EINVAL  # unknown kind
+        assert L.dopt_valu_probe(9, 16, 8, None) == _lib.EINVAL  # unknown kind
         assert L.dopt_valu_probe(-1, 16, 8, None) == _lib.EINVAL
         assert L.dopt_valu_probe(0, 16, 0, None) == _lib.EINVAL  # no blocks
         assert L.dopt_valu_probe(0, 16, 65537, None) == _lib.EINVAL
