@@ -194,17 +194,17 @@ __device__ __forceinline__ void block_sum2(float& a, float& b) {
 // min / max over aligned blocks of lpg lanes (lpg in 4..64, wave-uniform); raw v_min / v_max
 // (the operands are computed values: numbers or quiet NaNs)
 __device__ __forceinline__ void group_minmax(float& mn, float& mx, int lpg) {
-    mn = vmin(mn, dpp_f32<0xB1>(mn));
-    mx = vmax(mx, dpp_f32<0xB1>(mx));
-    mn = vmin(mn, dpp_f32<0x4E>(mn));
-    mx = vmax(mx, dpp_f32<0x4E>(mx));
+    mn = vmin_dpp<0xB1>(mn);
+    mx = vmax_dpp<0xB1>(mx);
+    mn = vmin_dpp<0x4E>(mn);
+    mx = vmax_dpp<0x4E>(mx);
     if (lpg >= 8) {
-        mn = vmin(mn, dpp_f32<0x141>(mn));
-        mx = vmax(mx, dpp_f32<0x141>(mx));
+        mn = vmin_dpp<0x141>(mn);
+        mx = vmax_dpp<0x141>(mx);
     }
     if (lpg >= 16) {
-        mn = vmin(mn, dpp_f32<0x140>(mn));
-        mx = vmax(mx, dpp_f32<0x140>(mx));
+        mn = vmin_dpp<0x140>(mn);
+        mx = vmax_dpp<0x140>(mx);
     }
     if (lpg >= 32) swap_minmax<16>(mn, mx);
     if (lpg >= 64) swap_minmax<32>(mn, mx);
@@ -363,7 +363,7 @@ __device__ __forceinline__ void channel_stats(const BnFwdArgs& a, int64_t c, int
 template <int MODE, int V, bool R6>
 __device__ __forceinline__ void fwd_block(const BnFwdArgs& a, int64_t c, RowCursor pos, int64_t e0, int64_t M,
                                           bool active, const float* v, float mean, float inv, float w, float b,
-                                          int lg, int bits) {
+                                          int lg, int bits, float qmaxf, float rqmax) {
     const BnGeom& g = a.g;
     float xh[EPL], y[EPL];
 #pragma unroll
@@ -408,13 +408,13 @@ __device__ __forceinline__ void fwd_block(const BnFwdArgs& a, int64_t c, RowCurs
         }
         const int lpg = 1 << (lg - 3);  // group / EPL
         group_minmax(mn, mx, lpg);
-        const float qmaxf = (float)((1 << bits) - 1);
+        // step = rng / qmax and 1 / step, both rounded as the IEEE divisions round them
         const float rng = mx - mn;
-        const float step = rng > 0.0f ? rng / qmaxf : 1.0f;
+        const float step = rng > 0.0f ? div_by_qmax_rt(rng, qmaxf, rqmax) : 1.0f;
+        const float invs = exact_rcp(step);
         const float half_m = 0.49999899f;  // fp32(0.5 - 1e-6) = 0x3EFFFFDE
         int q[EPL];
         if constexpr (MODE == BN_QUANT) {
-            const float invs = 1.0f / step;
 #pragma unroll
             for (int k = 0; k < EPL; ++k) {
                 const float qf = __builtin_amdgcn_fmed3f(fmaf(t[k] - mn, invs, half_m), 0.0f, qmaxf);
@@ -430,7 +430,6 @@ __device__ __forceinline__ void fwd_block(const BnFwdArgs& a, int64_t c, RowCurs
             // (Checked bit-for-bit against fp32 division on 4e8 random and quantizer-shaped pairs.)
             // (The test is per group; one wave-uniform branch keeps the common case free of
             // per-element lane masking.)
-            const float invs = 1.0f / step;
             const bool fastdiv = step >= 0x1p-60f && step < __builtin_huge_valf();
             if (__builtin_amdgcn_ballot_w64(!fastdiv) == 0) {
 #pragma unroll
@@ -484,10 +483,11 @@ __global__ __launch_bounds__(TPB) void bn_fwd_kernel(BnFwdArgs a, int lg, int bi
     float mean, inv;
     channel_stats(a, c, M, mean, inv);
     const float w = a.w[c], b = a.b[c];
+    const float qmaxf = (float)((1 << bits) - 1), rqmax = 1.0f / qmaxf;
 #pragma unroll
     for (int it = 0; it < ITER; ++it) {
         const int64_t e0 = base + it * WG_ELEMS;
-        fwd_block<MODE, V, R6>(a, c, cur[it], e0, M, e0 < M, v[it], mean, inv, w, b, lg, bits);
+        fwd_block<MODE, V, R6>(a, c, cur[it], e0, M, e0 < M, v[it], mean, inv, w, b, lg, bits, qmaxf, rqmax);
     }
 }
 

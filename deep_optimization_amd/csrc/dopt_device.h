@@ -92,6 +92,39 @@ __device__ __forceinline__ float vmax(float a, float b) {
     return d;
 }
 
+// min / max of v and its DPP-permuted copy (CTRL one of 0xB1, 0x4E, 0x141, 0x140 above) in one
+// VALU instruction: v_min_f32_dpp / v_max_f32_dpp, the permute applied to src0. The leading
+// s_nop 4 gives the wait states a DPP instruction requires after a VALU write of its VGPR operand
+// (two) or of EXEC (five), which the compiler does not insert before inline asm; the nop idles
+// only this wave, not the SIMD's VALU. Raw v_min / v_max semantics as for vmin / vmax.
+#define DOPT_DPP_ASM(OP, CTRLTXT) \
+    asm("s_nop 4\n\t" OP " %0, %1, %1 " CTRLTXT " row_mask:0xf bank_mask:0xf" : "=v"(d) : "v"(v))
+template <int CTRL>
+__device__ __forceinline__ float vmin_dpp(float v) {
+    float d;
+    if constexpr (CTRL == 0xB1) DOPT_DPP_ASM("v_min_f32_dpp", "quad_perm:[1,0,3,2]");
+    else if constexpr (CTRL == 0x4E) DOPT_DPP_ASM("v_min_f32_dpp", "quad_perm:[2,3,0,1]");
+    else if constexpr (CTRL == 0x141) DOPT_DPP_ASM("v_min_f32_dpp", "row_half_mirror");
+    else {
+        static_assert(CTRL == 0x140, "vmin_dpp: quad_perm 0xB1 / 0x4E, row_half_mirror or row_mirror");
+        DOPT_DPP_ASM("v_min_f32_dpp", "row_mirror");
+    }
+    return d;
+}
+template <int CTRL>
+__device__ __forceinline__ float vmax_dpp(float v) {
+    float d;
+    if constexpr (CTRL == 0xB1) DOPT_DPP_ASM("v_max_f32_dpp", "quad_perm:[1,0,3,2]");
+    else if constexpr (CTRL == 0x4E) DOPT_DPP_ASM("v_max_f32_dpp", "quad_perm:[2,3,0,1]");
+    else if constexpr (CTRL == 0x141) DOPT_DPP_ASM("v_max_f32_dpp", "row_half_mirror");
+    else {
+        static_assert(CTRL == 0x140, "vmax_dpp: quad_perm 0xB1 / 0x4E, row_half_mirror or row_mirror");
+        DOPT_DPP_ASM("v_max_f32_dpp", "row_mirror");
+    }
+    return d;
+}
+#undef DOPT_DPP_ASM
+
 // min/max with lane l ^ D (D = 16 or 32) on every lane: v_permlane16_swap / v_permlane32_swap
 // of a register with itself leaves the pair {x[l & ~D], x[l | D]}, in that order on both lanes of
 // the pair (measured on MI355X), one VALU op per exchange instead of an LDS permute; both lanes
@@ -237,6 +270,38 @@ __device__ __forceinline__ float two_tanh_half_fast(float x) {
 // this returns sigmoid(4d), the caller subtracts 1/2 where it can do so once per group
 __device__ __forceinline__ float sigmoid4_fast(float d) {
     return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-5.7707801635558535f * d));
+}
+
+// ------------------------------------------------------------------ exact division, fewer instructions
+__device__ __forceinline__ bool wave_any(bool p) { return __builtin_amdgcn_ballot_w64(p) != 0; }
+
+// step = rng / qmax for rng > 0 (finite or +inf) and qmax = 2^bits - 1, rounded as the IEEE fp32
+// division rounds it: q0 = rng * c with c = RN(1/qmax), r = fma(-q0, qmax, rng) (exact),
+// q1 = fma(r, c, q0). Checked on gfx950 against the correctly rounded division for every
+// non-negative fp32 rng and qmax = 1, 3, 15, 255 (compile-time and run-time divisors): equal for
+// all but rng = +inf, where r is NaN and q0 = +inf is the quotient. Five VALU instructions against
+// about eleven for the division sequence. qmax = 1 gives c = 1, r = 0 and q1 = rng.
+__device__ __forceinline__ float div_by_qmax_rt(float rng, float qmax, float c) {
+    const float q0 = rng * c;
+    const float q1 = __builtin_fmaf(__builtin_fmaf(-q0, qmax, rng), c, q0);
+    return rng == __builtin_inff() ? q0 : q1;
+}
+template <int QMAX>
+__device__ __forceinline__ float div_by_qmax(float rng) {
+    if constexpr (QMAX == 1) return rng;
+    else return div_by_qmax_rt(rng, (float)QMAX, 1.0f / (float)QMAX);
+}
+
+// 1 / x for x > 0, rounded as the IEEE fp32 division rounds it: v_rcp_f32 and one fma Newton step,
+// y = fma(fma(-x, y0, 1), y0, y0), which on gfx950 equals the correctly rounded reciprocal for
+// every normal x in [2^-126, 2^126) (checked for each of them). A wave holding any x outside that
+// range (subnormal, huge, +inf) takes the division for all its lanes.
+__device__ __forceinline__ float exact_rcp(float x) {
+    if (!wave_any(!(x >= 0x1p-126f && x < 0x1p126f))) {
+        const float y0 = __builtin_amdgcn_rcpf(x);
+        return __builtin_fmaf(__builtin_fmaf(-x, y0, 1.0f), y0, y0);
+    }
+    return 1.0f / x;
 }
 
 // ------------------------------------------------------------------ Philox4x32-10

@@ -159,37 +159,6 @@ __device__ __forceinline__ uint32_t pack_rne_codes(const float* z) {
     return acc;
 }
 
-__device__ __forceinline__ bool wave_any(bool p) { return __builtin_amdgcn_ballot_w64(p) != 0; }
-
-// step = rng / QMAX for rng > 0 (finite or +inf), rounded as the IEEE fp32 division rounds it:
-// q0 = rng * RN(1/QMAX), r = fma(-q0, QMAX, rng) (exact), q1 = fma(r, RN(1/QMAX), q0). Checked on
-// gfx950 against the correctly rounded division for every non-negative fp32 rng and QMAX = 3, 15,
-// 255: equal for all but rng = +inf, where r is NaN and q0 = +inf is the quotient. Five VALU
-// instructions against about eleven for the division sequence.
-template <int QMAX>
-__device__ __forceinline__ float div_by_qmax(float rng) {
-    if constexpr (QMAX == 1) {
-        return rng;
-    } else {
-        constexpr float d = (float)QMAX, c = 1.0f / (float)QMAX;
-        const float q0 = rng * c;
-        const float q1 = __builtin_fmaf(__builtin_fmaf(-q0, d, rng), c, q0);
-        return rng == __builtin_inff() ? q0 : q1;
-    }
-}
-
-// 1 / x for x > 0, rounded as the IEEE fp32 division rounds it: v_rcp_f32 and one fma Newton step,
-// y = fma(fma(-x, y0, 1), y0, y0), which on gfx950 equals the correctly rounded reciprocal for
-// every normal x in [2^-126, 2^126) (checked for each of them). A wave holding any x outside that
-// range (subnormal, huge, +inf) takes the division for all its lanes.
-__device__ __forceinline__ float exact_rcp(float x) {
-    if (!wave_any(!(x >= 0x1p-126f && x < 0x1p126f))) {
-        const float y0 = __builtin_amdgcn_rcpf(x);
-        return __builtin_fmaf(__builtin_fmaf(-x, y0, 1.0f), y0, y0);
-    }
-    return 1.0f / x;
-}
-
 template <int DT, int BITS, int G, int RN, int UB, int LPG_, int P, int PRE, bool NT>
 __global__ __launch_bounds__(256) void quant_pack_kernel(QuantPackArgs a) {
     using C = QuantPackCfg<DT, BITS, G, RN, UB, LPG_, P>;

@@ -164,15 +164,26 @@ __global__ __launch_bounds__(PROBE_THREADS, 1) void mfma_fp8_rate_kernel(float* 
 
 // The quantizer's fast exact-division helpers against the IEEE division, over every non-negative
 // fp32 bit pattern (+0 .. +inf, strided over the grid): div_by_qmax<3/15/255>(x) against x / QMAX,
-// and exact_rcp(x) against 1 / x. Each thread writes its count of differing bit patterns.
+// div_by_qmax_rt with the divisor 2^bits - 1 known only at run time (bits = 1, 2, 4, 8, taken from
+// the launch width, which the compiler cannot fold) against x / qmax, and exact_rcp(x) against
+// 1 / x. Each thread writes its count of differing bit patterns.
 __global__ __launch_bounds__(PROBE_THREADS) void division_check_kernel(float* __restrict__ out) {
     const uint32_t t = blockIdx.x * PROBE_THREADS + threadIdx.x, nt = gridDim.x * PROBE_THREADS;
+    const int one = (int)(blockDim.x / PROBE_THREADS);  // 1
+    float qm[4], rq[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        qm[i] = (float)((1 << (one << i)) - 1);  // 1, 3, 15, 255
+        rq[i] = 1.0f / qm[i];
+    }
     uint32_t bad = 0;
     for (uint32_t u = t; u <= 0x7F800000u; u += nt) {
         const float x = __uint_as_float(u);
         bad += __float_as_uint(div_by_qmax<3>(x)) != __float_as_uint(x / 3.0f);
         bad += __float_as_uint(div_by_qmax<15>(x)) != __float_as_uint(x / 15.0f);
         bad += __float_as_uint(div_by_qmax<255>(x)) != __float_as_uint(x / 255.0f);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) bad += __float_as_uint(div_by_qmax_rt(x, qm[i], rq[i])) != __float_as_uint(x / qm[i]);
         bad += __float_as_uint(exact_rcp(x)) != __float_as_uint(1.0f / x);
     }
     out[(uint64_t)blockIdx.x * PROBE_THREADS + threadIdx.x] = (float)bad;
