@@ -212,7 +212,8 @@ __device__ __forceinline__ void group_minmax(float& mn, float& mx, int lpg) {
 
 // Writes the lane's 8 codes (bits each) into the channel bitstream at element e0: 1-bit codes
 // merge over 4 lanes, 2-bit over 2, 4-bit fill one word, 8-bit two.
-__device__ __forceinline__ void store_codes(uint32_t* chan, int64_t e0, const int* q, int bits, bool active) {
+// (e0 < 2^32: 32-bit index arithmetic from the channel's base)
+__device__ __forceinline__ void store_codes(uint32_t* chan, uint32_t e0, const int* q, int bits, bool active) {
     const int lane = threadIdx.x & 63;
     if (bits == 8) {
         const uint32_t lo = (uint32_t)q[0] | ((uint32_t)q[1] << 8) | ((uint32_t)q[2] << 16) | ((uint32_t)q[3] << 24);
@@ -238,7 +239,7 @@ __device__ __forceinline__ void store_codes(uint32_t* chan, int64_t e0, const in
 }
 
 // 8 mask bits of a lane -> one word over 4 lanes
-__device__ __forceinline__ void store_mask(uint32_t* chan, int64_t e0, uint32_t m8, bool active) {
+__device__ __forceinline__ void store_mask(uint32_t* chan, uint32_t e0, uint32_t m8, bool active) {
     const int lane = threadIdx.x & 63;
     uint32_t v = m8 << (8 * (lane & 3));
     v |= dpp_u32<0xB1>(v);
@@ -387,7 +388,7 @@ __device__ __forceinline__ void fwd_block(const BnFwdArgs& a, int64_t c, RowCurs
             }
         }
         if (active) store8_bf16<V>(a.y, g, pos, e0, M, y);
-        if constexpr (MODE == BN_RELU_QUANT) store_mask(a.relu_packed + c * (M >> 5), e0, m8, active);
+        if constexpr (MODE == BN_RELU_QUANT) store_mask(a.relu_packed + c * (M >> 5), (uint32_t)e0, m8, active);
 
         // values quantized: the squashed x_hat (BN_QUANT) or x_hat itself (ReLU modes)
         float t[EPL];
@@ -454,11 +455,13 @@ __device__ __forceinline__ void fwd_block(const BnFwdArgs& a, int64_t c, RowCurs
                 }
             }
         }
-        store_codes(a.packed + c * ((M * bits) >> 5), e0, q, bits, active);
+        store_codes(a.packed + c * ((M * bits) >> 5), (uint32_t)e0, q, bits, active);
         if (active && ((threadIdx.x & 63) & (lpg - 1)) == 0) {
-            const int64_t gi = c * (M >> lg) + (e0 >> lg);
-            a.scale[gi] = to_bf16(step);
-            a.minv[gi] = to_bf16(mn);
+            // the group's entry at a 32-bit byte offset from the channel's first (< 2^29)
+            const int64_t g0 = c * (M >> lg);
+            const uint32_t off = ((uint32_t)e0 >> lg) * 2u;
+            *(uint16_t*)((char*)(a.scale + g0) + off) = to_bf16(step);
+            *(uint16_t*)((char*)(a.minv + g0) + off) = to_bf16(mn);
         }
     }
 }
@@ -480,8 +483,22 @@ __global__ __launch_bounds__(TPB) void bn_fwd_kernel(BnFwdArgs a, int lg, int bi
         block_or_first(a.g, c, cur[it], base + it * WG_ELEMS, M, p, e);
         load8<DT, V>(a.x, a.g, p, e, M, v[it]);
     }
+    // the channel's mean and inverse std: computed by wave 0 alone and passed through LDS (the
+    // other waves' loads are in flight meanwhile)
     float mean, inv;
-    channel_stats(a, c, M, mean, inv);
+    {
+        __shared__ float stat[2];
+        if (threadIdx.x < 64) {
+            channel_stats(a, c, M, mean, inv);
+            if (threadIdx.x == 0) {
+                stat[0] = mean;
+                stat[1] = inv;
+            }
+        }
+        __syncthreads();
+        mean = stat[0];
+        inv = stat[1];
+    }
     const float w = a.w[c], b = a.b[c];
     const float qmaxf = (float)((1 << bits) - 1), rqmax = 1.0f / qmaxf;
 #pragma unroll
