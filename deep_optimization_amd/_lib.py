@@ -42,6 +42,9 @@ EXPORTS = (
     "dopt_bn_train_backward",
     "dopt_bn_bwd_reduce",
     "dopt_bn_bwd_dx",
+    "dopt_bn_norm_quant_alam",
+    "dopt_bn_bwd_reduce_alam",
+    "dopt_bn_bwd_dx_alam",
     "dopt_dw_gemm_workspace_floats",
     "dopt_dw_gemm",
     "dopt_graph_node_counts",
@@ -124,6 +127,21 @@ def lib() -> ctypes.CDLL:
         L.dopt_bn_bwd_dx.argtypes = [i32, vp, vp, vp, vp, vp, vp, i32, i64, i64, i64, i64, i64, i32, i32, vp, vp, vp, vp,
                                      f32, i32, vp, vp]
         L.dopt_bn_bwd_dx.restype = i32
+        # x, dt, N, C, HW, stride_n, stride_c, sum, sumsq, mean_in, invstd_in, sync, weight, bias, eps, group,
+        # bits, alam_bits, y, packed, scale, min, mean_out, var_out, stream
+        L.dopt_bn_norm_quant_alam.argtypes = [vp, i32, i64, i64, i64, i64, i64, vp, vp, vp, vp, i32, vp, vp, f32, i32,
+                                              i32, i32, vp, vp, vp, vp, vp, vp, vp]
+        L.dopt_bn_norm_quant_alam.restype = i32
+        # packed, scale, min, dy, dy_dt, N, C, HW, stride_n, stride_c, group, bits, alam_bits, workspace, dweight,
+        # dbias, stream
+        L.dopt_bn_bwd_reduce_alam.argtypes = [vp, vp, vp, vp, i32, i64, i64, i64, i64, i64, i32, i32, i32, vp, vp, vp,
+                                              vp]
+        L.dopt_bn_bwd_reduce_alam.restype = i32
+        # packed, scale, min, dy, dy_dt, N, C, HW, stride_n, stride_c, group, bits, alam_bits, dweight, dbias,
+        # weight, var, eps, var_is_invstd, dx, stream
+        L.dopt_bn_bwd_dx_alam.argtypes = [vp, vp, vp, vp, i32, i64, i64, i64, i64, i64, i32, i32, i32, vp, vp, vp, vp,
+                                          f32, i32, vp, vp]
+        L.dopt_bn_bwd_dx_alam.restype = i32
         L.dopt_dw_gemm_workspace_floats.argtypes = [i64, i64, i64]
         L.dopt_dw_gemm_workspace_floats.restype = i64
         L.dopt_dw_gemm.argtypes = [vp, i64, vp, i64, vp, vp, vp, i32, i32, i64, i64, i64, vp, vp, vp, vp, vp]

@@ -262,12 +262,15 @@ ALAM_SEED = 42  # the reference operators' fixed seed (act_triton_kernel.py:339,
 
 
 def _no_alam(avg_alam: bool, where: str) -> None:
-    """The BatchNorm operators' avg_alam mode is not built (the quantizer's is, below)."""
+    """The SiLU operators' avg_alam mode is not built: the reference's forward kernel reshapes the
+    group's G codes to G / alam_bits before packing (activations/kernel_implementation.py:330),
+    which Triton rejects for alam_bits >= 2, and with alam_bits = 1 the mode only adds tl.rand
+    noise to the codes in the backward (:382-390). The quantizer and BatchNorm operators support it."""
     if avg_alam:
         raise NotImplementedError(
-            f"{where}: avg_alam=True is not implemented for the BatchNorm operators (their reference "
-            "layers pass avg_alam=False; the quantizer operators quant_pack_triton / dequant_unpack_triton "
-            "support it)")
+            f"{where}: avg_alam=True is not implemented for the SiLU operators (the reference's forward "
+            "kernel cannot reshape the codes for alam_bits >= 2; the quantizer and BatchNorm operators "
+            "support avg_alam)")
 
 
 def _alam_words(bits: int, group_size: int, alam_bits: int) -> int:

@@ -17,7 +17,12 @@ reference's callers pass ``input.view(N, C, HW)``, which already is).
 
 Differences from the reference: sums are deterministic (ordered two-stage reduction, where the
 reference accumulates fp32 atomics); relu6 clamps y to [0, 6] (the reference's fused kernel
-writes 0 for y >= 6, bn_act_fusion.py:73-75); avg_alam raises NotImplementedError.
+writes 0 for y >= 6, bn_act_fusion.py:73-75).
+
+avg_alam (the squashed operators): one code per run of alam_bits elements, the truncated mean of
+the run's code arguments; packed [C, M * bits / 32 / alam_bits]; the backward reduce adds the
+reference's tl.rand noise to the codes, the input gradient does not
+(kernel_implementation.py:194-237, :374-391, :455-462).
 """
 from __future__ import annotations
 
@@ -27,7 +32,7 @@ import torch
 from torch import Tensor
 
 from . import _lib
-from .act_lib import _DTYPE_CODE, _bits_consts, _no_alam, _op, _require_cuda, _stream
+from .act_lib import _DTYPE_CODE, _alam_words, _bits_consts, _op, _require_cuda, _stream
 
 EPS_FUSED = 1e-5
 EPS_PLAIN = 1e-7
@@ -57,6 +62,16 @@ def _ptr(t: Optional[Tensor]):
 def _workspace(X: Tensor, N: int, C: int, HW: int) -> Tensor:
     n = int(_lib.lib().dopt_bn_workspace_floats(N, C, HW))
     return torch.empty(max(n, 1), dtype=torch.float32, device=X.device)
+
+
+def _alam_run(avg_alam: bool, alam_bits: int, group: int, bits: int) -> int:
+    """avg_alam's elements per code, alam_bits (checked as the reference's reshape needs it), or 0
+    without avg_alam. alam_bits = 1 keeps the plain codes, but the backward reduce still adds the
+    reference's noise."""
+    if not avg_alam:
+        return 0
+    _alam_words(bits, group, alam_bits)
+    return int(alam_bits)
 
 
 def _group(BLOCK: int) -> int:
@@ -90,7 +105,7 @@ bn_fwd_reduce = _op(
     "int num_stages) -> (Tensor, Tensor)", _bn_fwd_reduce, _bn_fwd_reduce_fake)
 
 
-def _norm_launch(X, SUM, SUM_SQUARE, GAMMA, BETA, mean, var, M, HW, sync, mode, group, bits, eps):
+def _norm_launch(X, SUM, SUM_SQUARE, GAMMA, BETA, mean, var, M, HW, sync, mode, group, bits, eps, alam=0):
     _require_cuda(X, GAMMA, BETA)
     X3, N, C = _geom(X, M, HW)
     dev = X.device
@@ -99,7 +114,7 @@ def _norm_launch(X, SUM, SUM_SQUARE, GAMMA, BETA, mean, var, M, HW, sync, mode, 
     x_hat = None if quant else torch.empty(X3.shape, dtype=torch.bfloat16, device=dev)
     packed = relu_packed = scale = xmin = None
     if quant:
-        packed = torch.empty((C, M * bits // 32), dtype=torch.int32, device=dev)
+        packed = torch.empty((C, M * bits // 32 // max(alam, 1)), dtype=torch.int32, device=dev)
         scale = torch.empty((C, M // group), dtype=torch.bfloat16, device=dev)
         xmin = torch.empty_like(scale)
         if mode in (_lib.BN_RELU_QUANT, _lib.BN_RELU6_QUANT):
@@ -120,10 +135,17 @@ def _norm_launch(X, SUM, SUM_SQUARE, GAMMA, BETA, mean, var, M, HW, sync, mode, 
         mean_in = inv_in = None
         mean_out = torch.empty(C, dtype=torch.float32, device=dev)
         var_out = torch.empty_like(mean_out)
-    rc = _lib.lib().dopt_bn_norm_quant(
-        X3.data_ptr(), _DTYPE_CODE[X3.dtype], N, C, HW, C * HW, HW, _ptr(s), _ptr(q), _ptr(mean_in), _ptr(inv_in),
-        int(bool(sync)), w.data_ptr(), b.data_ptr(), float(eps), mode, group, bits, y.data_ptr(), _ptr(x_hat),
-        _ptr(packed), _ptr(relu_packed), _ptr(scale), _ptr(xmin), _ptr(mean_out), _ptr(var_out), _stream(X))
+    if alam:
+        rc = _lib.lib().dopt_bn_norm_quant_alam(
+            X3.data_ptr(), _DTYPE_CODE[X3.dtype], N, C, HW, C * HW, HW, _ptr(s), _ptr(q), _ptr(mean_in),
+            _ptr(inv_in), int(bool(sync)), w.data_ptr(), b.data_ptr(), float(eps), group, bits, alam, y.data_ptr(),
+            _ptr(packed), _ptr(scale), _ptr(xmin), _ptr(mean_out), _ptr(var_out), _stream(X))
+    else:
+        rc = _lib.lib().dopt_bn_norm_quant(
+            X3.data_ptr(), _DTYPE_CODE[X3.dtype], N, C, HW, C * HW, HW, _ptr(s), _ptr(q), _ptr(mean_in),
+            _ptr(inv_in), int(bool(sync)), w.data_ptr(), b.data_ptr(), float(eps), mode, group, bits, y.data_ptr(),
+            _ptr(x_hat), _ptr(packed), _ptr(relu_packed), _ptr(scale), _ptr(xmin), _ptr(mean_out), _ptr(var_out),
+            _stream(X))
     _lib.check(rc, "bn normalize")
     return y, x_hat, packed, relu_packed, scale, xmin, mean_out, var_out
 
@@ -152,20 +174,21 @@ bn_fwd_norm = _op(
 
 def _bn_fwd_norm_quant_pack_fused(X, SUM, SUM_SQUARE, GAMMA, BETA, mean=None, var=None, *, M, HW, stride_n, stride_c,
                                   BLOCK_M, bits, sync, avg_alam, alam_bits, num_warps, num_stages):
-    """-> (y bf16, packed [C, M*bits/32], scale, min bf16 [C, M/(BLOCK_M/2)], mean, var)
-    (kernel_registration.py:83-150); eps 1e-5, codes of 2 tanh(clamp(x_hat, -3, 3)/2)."""
-    _no_alam(avg_alam, "bn_fwd_norm_quant_pack_fused")
+    """-> (y bf16, packed [C, M*bits/32] (/ alam_bits with avg_alam), scale, min bf16
+    [C, M/(BLOCK_M/2)], mean, var) (kernel_registration.py:83-150); eps 1e-5, codes of
+    2 tanh(clamp(x_hat, -3, 3)/2)."""
     g = _group(BLOCK_M)
     _bits_consts(bits, g)
+    alam = _alam_run(avg_alam, alam_bits, g, bits)
     y, _, packed, _, scale, xmin, mo, vo = _norm_launch(X, SUM, SUM_SQUARE, GAMMA, BETA, mean, var, M, HW, sync,
-                                                        _lib.BN_QUANT, g, bits, EPS_FUSED)
+                                                        _lib.BN_QUANT, g, bits, EPS_FUSED, alam)
     return y, packed, scale, xmin, mo, vo
 
 
-def _quant_fakes(X, M, HW, g, bits, sync):
+def _quant_fakes(X, M, HW, g, bits, sync, alam=0):
     N, C = X.shape[0], X.shape[1]
     y = X.new_empty((N, C, HW), dtype=torch.bfloat16)
-    packed = X.new_empty((C, M * bits // 32), dtype=torch.int32)
+    packed = X.new_empty((C, M * bits // 32 // max(alam, 1)), dtype=torch.int32)
     scale = X.new_empty((C, M // g), dtype=torch.bfloat16)
     st = None if sync else X.new_empty((C,), dtype=torch.float32)
     return y, packed, scale, st
@@ -173,7 +196,8 @@ def _quant_fakes(X, M, HW, g, bits, sync):
 
 def _bn_fwd_norm_quant_pack_fused_fake(X, SUM, SUM_SQUARE, GAMMA, BETA, mean=None, var=None, *, M, HW, stride_n,
                                        stride_c, BLOCK_M, bits, sync, avg_alam, alam_bits, num_warps, num_stages):
-    y, packed, scale, st = _quant_fakes(X, M, HW, BLOCK_M // 2, bits, sync)
+    y, packed, scale, st = _quant_fakes(X, M, HW, BLOCK_M // 2, bits, sync,
+                                        _alam_run(avg_alam, alam_bits, BLOCK_M // 2, bits))
     return y, packed, scale, torch.empty_like(scale), st, None if sync else torch.empty_like(st)
 
 
@@ -222,11 +246,12 @@ def _bwd_common(mode, DY, M, HW, x_hat=None, packed=None, relu_packed=None, scal
     return DY3, N, C, xh, c(packed), c(relu_packed), c(scale), c(xmin)
 
 
-def _check_saved(C, M, group, bits, p, rp, sc, mn, *vecs):
+def _check_saved(C, M, group, bits, p, rp, sc, mn, *vecs, alam=0):
     """The kernels read the saved tensors unchecked: their sizes must match the channel layout."""
-    if p is not None and p.numel() * p.element_size() * 8 != C * M * bits:
+    a = max(alam, 1)
+    if p is not None and p.numel() * p.element_size() * 8 * a != C * M * bits:
         raise RuntimeError(f"BatchNorm backward: packed codes hold {p.numel() * p.element_size()} bytes, "
-                           f"expected {C * M * bits // 8}")
+                           f"expected {C * M * bits // 8 // a}")
     if rp is not None and rp.numel() * rp.element_size() * 8 < C * M:
         raise RuntimeError("BatchNorm backward: the ReLU mask is too small for the tensor")
     for t in (sc, mn):
@@ -237,28 +262,39 @@ def _check_saved(C, M, group, bits, p, rp, sc, mn, *vecs):
             raise RuntimeError(f"BatchNorm backward: per-channel vectors must hold {C} values, got {t.numel()}")
 
 
-def _bwd_reduce(mode, DY, M, HW, group, bits, **kw):
+def _bwd_reduce(mode, DY, M, HW, group, bits, alam=0, **kw):
     DY3, N, C, xh, p, rp, sc, mn = _bwd_common(mode, DY, M, HW, **kw)
-    _check_saved(C, M, group, bits, p, rp, sc, mn)
+    _check_saved(C, M, group, bits, p, rp, sc, mn, alam=alam)
     dw = torch.empty(C, dtype=torch.float32, device=DY.device)
     db = torch.empty_like(dw)
     ws = _workspace(DY, N, C, HW)
-    rc = _lib.lib().dopt_bn_bwd_reduce(mode, _ptr(xh), _ptr(p), _ptr(rp), _ptr(sc), _ptr(mn), DY3.data_ptr(),
-                                       _DTYPE_CODE[DY3.dtype], N, C, HW, C * HW, HW, group, bits, ws.data_ptr(),
-                                       dw.data_ptr(), db.data_ptr(), _stream(DY))
+    if alam:
+        rc = _lib.lib().dopt_bn_bwd_reduce_alam(_ptr(p), _ptr(sc), _ptr(mn), DY3.data_ptr(), _DTYPE_CODE[DY3.dtype], N,
+                                                C, HW, C * HW, HW, group, bits, alam, ws.data_ptr(), dw.data_ptr(),
+                                                db.data_ptr(), _stream(DY))
+    else:
+        rc = _lib.lib().dopt_bn_bwd_reduce(mode, _ptr(xh), _ptr(p), _ptr(rp), _ptr(sc), _ptr(mn), DY3.data_ptr(),
+                                           _DTYPE_CODE[DY3.dtype], N, C, HW, C * HW, HW, group, bits, ws.data_ptr(),
+                                           dw.data_ptr(), db.data_ptr(), _stream(DY))
     _lib.check(rc, "bn backward reduce")
     return dw, db
 
 
-def _bwd_dx(mode, DY, M, HW, group, bits, DW, DB, W, VAR, eps, var_is_invstd, **kw):
+def _bwd_dx(mode, DY, M, HW, group, bits, DW, DB, W, VAR, eps, var_is_invstd, alam=0, **kw):
     DY3, N, C, xh, p, rp, sc, mn = _bwd_common(mode, DY, M, HW, **kw)
     dx = torch.empty(DY3.shape, dtype=torch.bfloat16, device=DY.device)
     dw, db, w, v = _f32(DW), _f32(DB), _f32(W), _f32(VAR)
-    _check_saved(C, M, group, bits, p, rp, sc, mn, dw, db, w, v)
-    rc = _lib.lib().dopt_bn_bwd_dx(mode, _ptr(xh), _ptr(p), _ptr(rp), _ptr(sc), _ptr(mn), DY3.data_ptr(),
-                                   _DTYPE_CODE[DY3.dtype], N, C, HW, C * HW, HW, group, bits, dw.data_ptr(),
-                                   db.data_ptr(), w.data_ptr(), v.data_ptr(), float(eps), int(bool(var_is_invstd)),
-                                   dx.data_ptr(), _stream(DY))
+    _check_saved(C, M, group, bits, p, rp, sc, mn, dw, db, w, v, alam=alam)
+    if alam:
+        rc = _lib.lib().dopt_bn_bwd_dx_alam(_ptr(p), _ptr(sc), _ptr(mn), DY3.data_ptr(), _DTYPE_CODE[DY3.dtype], N, C,
+                                            HW, C * HW, HW, group, bits, alam, dw.data_ptr(), db.data_ptr(),
+                                            w.data_ptr(), v.data_ptr(), float(eps), int(bool(var_is_invstd)),
+                                            dx.data_ptr(), _stream(DY))
+    else:
+        rc = _lib.lib().dopt_bn_bwd_dx(mode, _ptr(xh), _ptr(p), _ptr(rp), _ptr(sc), _ptr(mn), DY3.data_ptr(),
+                                       _DTYPE_CODE[DY3.dtype], N, C, HW, C * HW, HW, group, bits, dw.data_ptr(),
+                                       db.data_ptr(), w.data_ptr(), v.data_ptr(), float(eps),
+                                       int(bool(var_is_invstd)), dx.data_ptr(), _stream(DY))
     _lib.check(rc, "bn backward dx")
     return dx
 
@@ -294,10 +330,10 @@ bn_bwd_dx = _op(
 def _bn_bwd_reduce_dequant_unpack_fused(x_hat_packed, dy, scale, min, *, M, HW, stride_n, stride_c, BLOCK_M, bits,
                                         avg_alam, alam_bits):
     """-> (DW, DB) (kernel_registration.py:211-240)."""
-    _no_alam(avg_alam, "bn_bwd_reduce_dequant_unpack_fused")
     g = _group(BLOCK_M)
     _bits_consts(bits, g)
-    return _bwd_reduce(_lib.BN_QUANT, dy, M, HW, g, bits, packed=x_hat_packed, scale=scale, xmin=min)
+    return _bwd_reduce(_lib.BN_QUANT, dy, M, HW, g, bits, _alam_run(avg_alam, alam_bits, g, bits),
+                       packed=x_hat_packed, scale=scale, xmin=min)
 
 
 bn_bwd_reduce_dequant_unpack_fused = _op(
@@ -311,11 +347,10 @@ bn_bwd_reduce_dequant_unpack_fused = _op(
 def _bn_bwd_dx_dequant_unpack_fused(x_hat_packed, dy, scale, min, DW, DB, W, VAR, *, M, HW, stride_n, stride_c,
                                     BLOCK_M, bits, sync, avg_alam, alam_bits):
     """-> bf16 dx [N, C, HW] (kernel_registration.py:243-276); eps 1e-7, VAR = invstd with sync."""
-    _no_alam(avg_alam, "bn_bwd_dx_dequant_unpack_fused")
     g = _group(BLOCK_M)
     _bits_consts(bits, g)
-    return _bwd_dx(_lib.BN_QUANT, dy, M, HW, g, bits, DW, DB, W, VAR, EPS_PLAIN, sync, packed=x_hat_packed,
-                   scale=scale, xmin=min)
+    return _bwd_dx(_lib.BN_QUANT, dy, M, HW, g, bits, DW, DB, W, VAR, EPS_PLAIN, sync,
+                   _alam_run(avg_alam, alam_bits, g, bits), packed=x_hat_packed, scale=scale, xmin=min)
 
 
 bn_bwd_dx_dequant_unpack_fused = _op(

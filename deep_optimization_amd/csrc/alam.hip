@@ -119,12 +119,6 @@ struct AlamDqArgs {
     uint64_t seed;
 };
 
-__device__ __forceinline__ float triton_uniform(uint32_t w) {
-    int32_t i = (int32_t)w;
-    if (i < 0) i = ~i;
-    return (float)i * __uint_as_float(0x2fffffffu);
-}
-
 __global__ __launch_bounds__(256) void alam_dequant_kernel(AlamDqArgs a) {
     const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (i >= a.total) return;

@@ -5,7 +5,8 @@
 // tensor of one call (x, y, x_hat, dy, dx) shares that geometry. Per channel, groups are runs of
 // `group` consecutive elements, and the packed codes, the 1-bit ReLU mask and the bf16 scale/min
 // are flat per-channel arrays:
-//   packed       [C, M * bits / 32]   little-endian bitstream of the codes
+//   packed       [C, M * bits / 32]   little-endian bitstream of the codes ([C, M * bits / 32 / A]
+//                                     with avg_alam: one code per run of A elements)
 //   relu_packed  [C, M / 32]          bit e of channel c = mask of element e
 //   scale, minv  [C, M / group]       bf16
 #pragma once
@@ -49,6 +50,7 @@ struct BnFwdArgs {
     float run_keep, run_mom;
     const float* partial;    // when set (sync == 0): the statistics kernel's [2, C, nchunks] partials,
     int64_t nchunks;         // summed here instead of reading sum / sumsq
+    int alam_lg;             // BN_QUANT with avg_alam: log2 of the run length A (0: off)
 };
 
 struct BnBwdArgs {
@@ -70,6 +72,8 @@ struct BnBwdArgs {
     float eps;
     int var_is_invstd;
     uint16_t* dx;            // bf16
+    int alam;                // BN_QUANT with avg_alam (the reduce adds the reference's noise, also at A = 1)
+    int alam_lg;             // log2 of avg_alam's run length A
 };
 
 // vw: elements per vector access (8, 4, 2 or 1); it divides HW, stride_n and stride_c, and every

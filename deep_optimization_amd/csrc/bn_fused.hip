@@ -264,6 +264,28 @@ __device__ __forceinline__ void load_codes(const uint32_t* chan, int64_t e0, int
     }
 }
 
+// avg_alam: the codes of the lane's 8 elements, element e carrying code e / A of the channel's
+// stream of M / A codes (kernel_implementation.py:374-377, :455-458: each code repeated A times).
+// e0 is a multiple of 8: below A = 8 the lane's 8 / A codes fill an aligned (8 / A) * bits <= 32
+// bit field, from A = 8 on its 8 elements share one code, so one dword holds them.
+__device__ __forceinline__ void load_codes_alam(const uint32_t* chan, uint32_t e0, int bits, int alam_lg, int* q) {
+    const uint32_t c0 = e0 >> alam_lg, bit0 = c0 * (uint32_t)bits;
+    const uint32_t w = chan[bit0 >> 5] >> (bit0 & 31);
+#pragma unroll
+    for (int k = 0; k < EPL; ++k) {
+        const uint32_t off = (((e0 + (uint32_t)k) >> alam_lg) - c0) * (uint32_t)bits;
+        q[k] = (int)__builtin_amdgcn_ubfe(w, off, (uint32_t)bits);
+    }
+}
+
+template <bool ALAM>
+__device__ __forceinline__ void lane_codes(const BnBwdArgs& a, int64_t c, int64_t e0, int64_t M, int bits, int* q) {
+    if (ALAM && a.alam_lg > 0)
+        load_codes_alam(a.packed + c * (((M >> a.alam_lg) * bits) >> 5), (uint32_t)e0, bits, a.alam_lg, q);
+    else
+        load_codes(a.packed + c * ((M * bits) >> 5), e0, bits, q);
+}
+
 // ------------------------------------------------------------------ statistics
 template <int DT, int V>
 __global__ __launch_bounds__(TPB) void bn_stats_kernel(const void* __restrict__ x, BnGeom g,
@@ -359,9 +381,43 @@ __device__ __forceinline__ void channel_stats(const BnFwdArgs& a, int64_t c, int
 }
 
 // ------------------------------------------------------------------ forward
+// avg_alam codes of one wave's 512 consecutive elements (kernel_implementation.py:194-237): every
+// run of A = 2^alam_lg elements becomes one code, the truncated mean of the run's
+// qf = fma(t - min, 1/scale, 0.5 - 1e-6) (summed left to right, then times 1/A: exact, A a power
+// of two), clamped to [0, QMAX] (NaN -> 0). A divides the group, so runs never straddle groups, and
+// the channel's codes form one bitstream of M / A codes. Through LDS: the wave's 512 qf, its
+// 512 / A codes (one byte each), then its (16 bits) / A words, each written when its elements lie
+// below M. A wave's LDS operations complete in order, so its own reads see its writes.
+__device__ __forceinline__ void alam_store(uint32_t* chan, uint32_t e0, uint32_t M, const float* t, float mn, float invs,
+                                        float qmaxf, int bits, int alam_lg) {
+    __shared__ float qs[TPB / 64][64 * EPL];
+    __shared__ uint8_t cs[TPB / 64][64 * EPL];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const float half_m = 0.49999899f;  // fp32(0.5 - 1e-6)
+#pragma unroll
+    for (int k = 0; k < EPL; ++k) qs[wave][lane * EPL + k] = fmaf(t[k] - mn, invs, half_m);
+    __builtin_amdgcn_wave_barrier();
+    const int A = 1 << alam_lg, ncodes = (64 * EPL) >> alam_lg;
+    const float inv_a = 1.0f / (float)A;
+    for (int k = lane; k < ncodes; k += 64) {
+        float sum = qs[wave][k * A];
+        for (int j = 1; j < A; ++j) sum = sum + qs[wave][k * A + j];
+        cs[wave][k] = (uint8_t)(int)__builtin_amdgcn_fmed3f(sum * inv_a, 0.0f, qmaxf);
+    }
+    __builtin_amdgcn_wave_barrier();
+    const int vpw = 32 / bits, nwords = (2 * EPL * bits) >> alam_lg;
+    const uint32_t ew = e0 - (uint32_t)lane * EPL;  // the wave's first element
+    if (lane < nwords && ew + (uint32_t)(lane * vpw * A) < M) {
+        uint32_t word = 0;
+        for (int j = 0; j < vpw; ++j) word |= (uint32_t)cs[wave][lane * vpw + j] << (j * bits);
+        chan[(((ew >> alam_lg) * bits) >> 5) + lane] = word;
+    }
+    __builtin_amdgcn_wave_barrier();
+}
+
 // One 2048-element block of the forward: y (and the mask / codes / scale / min) from the lane's 8
 // loaded values. Whole groups are active or not (M % group == 0), so the group's lanes agree.
-template <int MODE, int V, bool R6>
+template <int MODE, int V, bool R6, bool ALAM>
 __device__ __forceinline__ void fwd_block(const BnFwdArgs& a, int64_t c, RowCursor pos, int64_t e0, int64_t M,
                                           bool active, const float* v, float mean, float inv, float w, float b,
                                           int lg, int bits, float qmaxf, float rqmax) {
@@ -413,49 +469,54 @@ __device__ __forceinline__ void fwd_block(const BnFwdArgs& a, int64_t c, RowCurs
         const float rng = mx - mn;
         const float step = rng > 0.0f ? div_by_qmax_rt(rng, qmaxf, rqmax) : 1.0f;
         const float invs = exact_rcp(step);
-        const float half_m = 0.49999899f;  // fp32(0.5 - 1e-6) = 0x3EFFFFDE
-        int q[EPL];
-        if constexpr (MODE == BN_QUANT) {
-#pragma unroll
-            for (int k = 0; k < EPL; ++k) {
-                const float qf = __builtin_amdgcn_fmed3f(fmaf(t[k] - mn, invs, half_m), 0.0f, qmaxf);
-                q[k] = (int)qf;
-            }
+        if constexpr (ALAM) {
+            alam_store(a.packed + c * (((M >> a.alam_lg) * bits) >> 5), (uint32_t)e0, (uint32_t)M, t, mn, invs,
+                       qmaxf, bits, a.alam_lg);
         } else {
-            // (t - mn) / step, correctly rounded, without a division per element: with y = 1/step
-            // correctly rounded (one division per group), q0 = RN(a y) and the exact remainder
-            // r = fma(-q0, step, a), RN(q0 + r y) is the correctly rounded a / step (Markstein's
-            // theorem, the IA-64 division), given no overflow and a normal remainder. With
-            // 2^-60 <= step < inf and a in [0, rng] the quotient lies in [0, qmax], and whenever it
-            // can reach a rounding boundary of the code (q >= ~1e-7) the remainder is normal.
-            // (Checked bit-for-bit against fp32 division on 4e8 random and quantizer-shaped pairs.)
-            // (The test is per group; one wave-uniform branch keeps the common case free of
-            // per-element lane masking.)
-            const bool fastdiv = step >= 0x1p-60f && step < __builtin_huge_valf();
-            if (__builtin_amdgcn_ballot_w64(!fastdiv) == 0) {
+            const float half_m = 0.49999899f;  // fp32(0.5 - 1e-6) = 0x3EFFFFDE
+            int q[EPL];
+            if constexpr (MODE == BN_QUANT) {
 #pragma unroll
                 for (int k = 0; k < EPL; ++k) {
-                    const float num = t[k] - mn;
-                    const float q0 = num * invs;
-                    const float quo = fmaf(fmaf(-q0, step, num), invs, q0);
-                    q[k] = (int)__builtin_amdgcn_fmed3f(quo + half_m, 0.0f, qmaxf);
+                    const float qf = __builtin_amdgcn_fmed3f(fmaf(t[k] - mn, invs, half_m), 0.0f, qmaxf);
+                    q[k] = (int)qf;
                 }
             } else {
+                // (t - mn) / step, correctly rounded, without a division per element: with y = 1/step
+                // correctly rounded (one division per group), q0 = RN(a y) and the exact remainder
+                // r = fma(-q0, step, a), RN(q0 + r y) is the correctly rounded a / step (Markstein's
+                // theorem, the IA-64 division), given no overflow and a normal remainder. With
+                // 2^-60 <= step < inf and a in [0, rng] the quotient lies in [0, qmax], and whenever it
+                // can reach a rounding boundary of the code (q >= ~1e-7) the remainder is normal.
+                // (Checked bit-for-bit against fp32 division on 4e8 random and quantizer-shaped pairs.)
+                // (The test is per group; one wave-uniform branch keeps the common case free of
+                // per-element lane masking.)
+                const bool fastdiv = step >= 0x1p-60f && step < __builtin_huge_valf();
+                if (__builtin_amdgcn_ballot_w64(!fastdiv) == 0) {
 #pragma unroll
-                for (int k = 0; k < EPL; ++k) {
-                    const float num = t[k] - mn;
-                    float quo;
-                    if (fastdiv) {
+                    for (int k = 0; k < EPL; ++k) {
+                        const float num = t[k] - mn;
                         const float q0 = num * invs;
-                        quo = fmaf(fmaf(-q0, step, num), invs, q0);
-                    } else {
-                        quo = num / step;
+                        const float quo = fmaf(fmaf(-q0, step, num), invs, q0);
+                        q[k] = (int)__builtin_amdgcn_fmed3f(quo + half_m, 0.0f, qmaxf);
                     }
-                    q[k] = (int)__builtin_amdgcn_fmed3f(quo + half_m, 0.0f, qmaxf);
+                } else {
+#pragma unroll
+                    for (int k = 0; k < EPL; ++k) {
+                        const float num = t[k] - mn;
+                        float quo;
+                        if (fastdiv) {
+                            const float q0 = num * invs;
+                            quo = fmaf(fmaf(-q0, step, num), invs, q0);
+                        } else {
+                            quo = num / step;
+                        }
+                        q[k] = (int)__builtin_amdgcn_fmed3f(quo + half_m, 0.0f, qmaxf);
+                    }
                 }
             }
+            store_codes(a.packed + c * ((M * bits) >> 5), (uint32_t)e0, q, bits, active);
         }
-        store_codes(a.packed + c * ((M * bits) >> 5), (uint32_t)e0, q, bits, active);
         if (active && ((threadIdx.x & 63) & (lpg - 1)) == 0) {
             // the group's entry at a 32-bit byte offset from the channel's first (< 2^29)
             const int64_t g0 = c * (M >> lg);
@@ -468,7 +529,7 @@ __device__ __forceinline__ void fwd_block(const BnFwdArgs& a, int64_t c, RowCurs
 
 // A workgroup covers ITER consecutive 2048-element blocks of one channel; all loads are issued
 // before the first block is processed.
-template <int DT, int MODE, int V, bool R6>
+template <int DT, int MODE, int V, bool R6, bool ALAM = false>
 __global__ __launch_bounds__(TPB) void bn_fwd_kernel(BnFwdArgs a, int lg, int bits) {
     const int64_t c = blockIdx.y;
     const int64_t M = a.g.N * a.g.HW;
@@ -504,13 +565,13 @@ __global__ __launch_bounds__(TPB) void bn_fwd_kernel(BnFwdArgs a, int lg, int bi
 #pragma unroll
     for (int it = 0; it < ITER; ++it) {
         const int64_t e0 = base + it * WG_ELEMS;
-        fwd_block<MODE, V, R6>(a, c, cur[it], e0, M, e0 < M, v[it], mean, inv, w, b, lg, bits, qmaxf, rqmax);
+        fwd_block<MODE, V, R6, ALAM>(a, c, cur[it], e0, M, e0 < M, v[it], mean, inv, w, b, lg, bits, qmaxf, rqmax);
     }
 }
 
 // ------------------------------------------------------------------ backward
 // dy (times the ReLU mask) and x_hat' of the lane's 8 elements
-template <int DYT, int MODE, int V>
+template <int DYT, int MODE, int V, bool ALAM>
 __device__ __forceinline__ void bwd_operands(const BnBwdArgs& a, int64_t c, RowCursor pos, int64_t e0, int64_t M,
                                              int lg, int bits, float* xh, float* dy) {
     load8<DYT, V>(a.dy, a.g, pos, e0, M, dy);
@@ -518,7 +579,7 @@ __device__ __forceinline__ void bwd_operands(const BnBwdArgs& a, int64_t c, RowC
         load8<DT_BF16, V>(a.xhat, a.g, pos, e0, M, xh);
     } else {
         int q[EPL];
-        load_codes(a.packed + c * ((M * bits) >> 5), e0, bits, q);
+        lane_codes<ALAM>(a, c, e0, M, bits, q);
         const int64_t gi = c * (M >> lg) + (e0 >> lg);
         const float sc = bf16_bits_to_f32(a.scale[gi]);
         const float mn = bf16_bits_to_f32(a.minv[gi]);
@@ -533,11 +594,11 @@ __device__ __forceinline__ void bwd_operands(const BnBwdArgs& a, int64_t c, RowC
 }
 
 // dy (times the ReLU mask), the codes and the group's scale / min of the lane's 8 elements
-template <int DYT, int MODE, int V>
+template <int DYT, int MODE, int V, bool ALAM>
 __device__ __forceinline__ void bwd_codes(const BnBwdArgs& a, int64_t c, RowCursor pos, int64_t e0, int64_t M, int lg,
                                           int bits, int* q, float& sc, float& mn, float* dy) {
     load8<DYT, V>(a.dy, a.g, pos, e0, M, dy);
-    load_codes(a.packed + c * ((M * bits) >> 5), e0, bits, q);
+    lane_codes<ALAM>(a, c, e0, M, bits, q);
     const int64_t gi = c * (M >> lg) + (e0 >> lg);
     sc = bf16_bits_to_f32(a.scale[gi]);
     mn = bf16_bits_to_f32(a.minv[gi]);
@@ -548,7 +609,10 @@ __device__ __forceinline__ void bwd_codes(const BnBwdArgs& a, int64_t c, RowCurs
     }
 }
 
-template <int DYT, int MODE, int V>
+// With avg_alam (ALAM) the reduce adds the reference's noise to each code before the product
+// (kernel_implementation.py:377-381): q + (tl.rand(42 + b, e mod G) - 0.5), b = e / (2 G) the
+// index of the reference's two-group block; the seed does not depend on the channel.
+template <int DYT, int MODE, int V, bool ALAM = false>
 __global__ __launch_bounds__(TPB) void bn_bwd_reduce_kernel(BnBwdArgs a, int lg, int bits, int64_t nchunks) {
     const int64_t c = blockIdx.y, chunk = blockIdx.x;
     const int64_t M = a.g.N * a.g.HW;
@@ -564,7 +628,7 @@ __global__ __launch_bounds__(TPB) void bn_bwd_reduce_kernel(BnBwdArgs a, int lg,
             RowCursor p;
             int64_t e;
             block_or_first(a.g, c, cur[it], e0, M, p, e);
-            bwd_operands<DYT, MODE, V>(a, c, p, e, M, lg, bits, xh[it], dy[it]);
+            bwd_operands<DYT, MODE, V, false>(a, c, p, e, M, lg, bits, xh[it], dy[it]);
         }
 #pragma unroll
         for (int it = 0; it < ITER; ++it) {
@@ -587,16 +651,27 @@ __global__ __launch_bounds__(TPB) void bn_bwd_reduce_kernel(BnBwdArgs a, int lg,
             RowCursor p;
             int64_t e;
             block_or_first(a.g, c, cur[it], e0, M, p, e);
-            bwd_codes<DYT, MODE, V>(a, c, p, e, M, lg, bits, q[it], sc[it], mn[it], dy[it]);
+            bwd_codes<DYT, MODE, V, ALAM>(a, c, p, e, M, lg, bits, q[it], sc[it], mn[it], dy[it]);
         }
 #pragma unroll
         for (int it = 0; it < ITER; ++it) {
             if (base + it * WG_ELEMS >= M) continue;
             float gdy = 0.0f, gdyq = 0.0f;
+            if constexpr (ALAM) {
+                const uint32_t e0 = (uint32_t)(base + it * WG_ELEMS);
+                const uint64_t seed = 42u + (e0 >> (lg + 1));
 #pragma unroll
-            for (int k = 0; k < EPL; ++k) {
-                gdy += dy[it][k];
-                gdyq = fmaf(dy[it][k], (float)q[it][k], gdyq);
+                for (int k = 0; k < EPL; ++k) {
+                    const float u = triton_rand(seed, (e0 + (uint32_t)k) & ((1u << lg) - 1u));
+                    gdy += dy[it][k];
+                    gdyq = fmaf(dy[it][k], (float)q[it][k] + (u - 0.5f), gdyq);
+                }
+            } else {
+#pragma unroll
+                for (int k = 0; k < EPL; ++k) {
+                    gdy += dy[it][k];
+                    gdyq = fmaf(dy[it][k], (float)q[it][k], gdyq);
+                }
             }
             sdy += gdy;
             sdyx = fmaf(sc[it], gdyq, fmaf(mn[it], gdy, sdyx));
@@ -609,7 +684,7 @@ __global__ __launch_bounds__(TPB) void bn_bwd_reduce_kernel(BnBwdArgs a, int lg,
     }
 }
 
-template <int DYT, int MODE, int V>
+template <int DYT, int MODE, int V, bool ALAM = false>
 __global__ __launch_bounds__(TPB) void bn_bwd_dx_kernel(BnBwdArgs a, int lg, int bits) {
     const int64_t c = blockIdx.y;
     const int64_t M = a.g.N * a.g.HW;
@@ -623,7 +698,7 @@ __global__ __launch_bounds__(TPB) void bn_bwd_dx_kernel(BnBwdArgs a, int lg, int
         RowCursor p;
         int64_t e;
         block_or_first(a.g, c, cur[it], e0, M, p, e);
-        bwd_operands<DYT, MODE, V>(a, c, p, e, M, lg, bits, xh[it], dy[it]);
+        bwd_operands<DYT, MODE, V, ALAM>(a, c, p, e, M, lg, bits, xh[it], dy[it]);
     }
     const float Mf = (float)M;
     float dws, dbs;
@@ -676,14 +751,17 @@ int fwd_dt(const BnFwdArgs& a, int mode, int group, int bits, int vw, hipStream_
     const dim3 grid((unsigned)bn_nchunks(M), (unsigned)a.g.C);
 #define DOPT_BN_FWD(MODE_, V_) hipLaunchKernelGGL((bn_fwd_kernel<DT, MODE_, V_, false>), grid, dim3(TPB), 0, s, a, lg, bits)
 #define DOPT_BN_FWD_RELU6(V_) hipLaunchKernelGGL((bn_fwd_kernel<DT, BN_RELU_QUANT, V_, true>), grid, dim3(TPB), 0, s, a, lg, bits)
+#define DOPT_BN_FWD_ALAM(V_) hipLaunchKernelGGL((bn_fwd_kernel<DT, BN_QUANT, V_, false, true>), grid, dim3(TPB), 0, s, a, lg, bits)
 #define DOPT_BN_FWD_NORM(V_) DOPT_BN_FWD(BN_NORM, V_)
 #define DOPT_BN_FWD_QUANT(V_) DOPT_BN_FWD(BN_QUANT, V_)
 #define DOPT_BN_FWD_RELU(V_) DOPT_BN_FWD(BN_RELU_QUANT, V_)
     if (mode == BN_NORM) DOPT_BN_BY_WIDTH(vw, DOPT_BN_FWD_NORM);
+    else if (mode == BN_QUANT && a.alam_lg > 0) DOPT_BN_BY_WIDTH(vw, DOPT_BN_FWD_ALAM);
     else if (mode == BN_QUANT) DOPT_BN_BY_WIDTH(vw, DOPT_BN_FWD_QUANT);
     else if (mode == BN_RELU6_QUANT) DOPT_BN_BY_WIDTH(vw, DOPT_BN_FWD_RELU6);
     else DOPT_BN_BY_WIDTH(vw, DOPT_BN_FWD_RELU);
 #undef DOPT_BN_FWD_RELU6
+#undef DOPT_BN_FWD_ALAM
 #undef DOPT_BN_FWD_RELU
 #undef DOPT_BN_FWD_QUANT
 #undef DOPT_BN_FWD_NORM
@@ -702,16 +780,20 @@ int bwd_dt(const BnBwdArgs& a, int mode, int group, int bits, int vw, bool reduc
 #define DOPT_BN_RED(MODE_, V_) hipLaunchKernelGGL((bn_bwd_reduce_kernel<DYT, MODE_, V_>), grid, dim3(TPB), 0, s, a, lg, bits, nch)
 #define DOPT_BN_RED_NORM(V_) DOPT_BN_RED(BN_NORM, V_)
 #define DOPT_BN_RED_QUANT(V_) DOPT_BN_RED(BN_QUANT, V_)
+#define DOPT_BN_RED_ALAM(V_) hipLaunchKernelGGL((bn_bwd_reduce_kernel<DYT, BN_QUANT, V_, true>), grid, dim3(TPB), 0, s, a, lg, bits, nch)
 #define DOPT_BN_RED_RELU(V_) DOPT_BN_RED(BN_RELU_QUANT, V_)
         if (nch == 0) {
         } else if (m == BN_NORM) {
             DOPT_BN_BY_WIDTH(vw, DOPT_BN_RED_NORM);
+        } else if (m == BN_QUANT && a.alam) {
+            DOPT_BN_BY_WIDTH(vw, DOPT_BN_RED_ALAM);
         } else if (m == BN_QUANT) {
             DOPT_BN_BY_WIDTH(vw, DOPT_BN_RED_QUANT);
         } else {
             DOPT_BN_BY_WIDTH(vw, DOPT_BN_RED_RELU);
         }
 #undef DOPT_BN_RED_RELU
+#undef DOPT_BN_RED_ALAM
 #undef DOPT_BN_RED_QUANT
 #undef DOPT_BN_RED_NORM
 #undef DOPT_BN_RED
@@ -722,11 +804,14 @@ int bwd_dt(const BnBwdArgs& a, int mode, int group, int bits, int vw, bool reduc
 #define DOPT_BN_DX(MODE_, V_) hipLaunchKernelGGL((bn_bwd_dx_kernel<DYT, MODE_, V_>), grid, dim3(TPB), 0, s, a, lg, bits)
 #define DOPT_BN_DX_NORM(V_) DOPT_BN_DX(BN_NORM, V_)
 #define DOPT_BN_DX_QUANT(V_) DOPT_BN_DX(BN_QUANT, V_)
+#define DOPT_BN_DX_ALAM(V_) hipLaunchKernelGGL((bn_bwd_dx_kernel<DYT, BN_QUANT, V_, true>), grid, dim3(TPB), 0, s, a, lg, bits)
 #define DOPT_BN_DX_RELU(V_) DOPT_BN_DX(BN_RELU_QUANT, V_)
         if (m == BN_NORM) DOPT_BN_BY_WIDTH(vw, DOPT_BN_DX_NORM);
+        else if (m == BN_QUANT && a.alam_lg > 0) DOPT_BN_BY_WIDTH(vw, DOPT_BN_DX_ALAM);
         else if (m == BN_QUANT) DOPT_BN_BY_WIDTH(vw, DOPT_BN_DX_QUANT);
         else DOPT_BN_BY_WIDTH(vw, DOPT_BN_DX_RELU);
 #undef DOPT_BN_DX_RELU
+#undef DOPT_BN_DX_ALAM
 #undef DOPT_BN_DX_QUANT
 #undef DOPT_BN_DX_NORM
 #undef DOPT_BN_DX

@@ -153,6 +153,22 @@ int bn_quant_checks(int mode, int64_t M, int group_size, int bits, const void* p
     return DOPT_OK;
 }
 
+// log2 of avg_alam's run length A: a power of two dividing the group's code words
+// group_size * bits / 32, as the reference's reshape of the codes into runs requires
+// (kernel_registration.py:124-128)
+int bn_alam_lg(int group_size, int bits, int alam_bits, int* lg) {
+    int rc;
+    if ((rc = check_bits(bits))) return rc;
+    const int nwords = group_size * bits / 32;
+    if (alam_bits < 1 || (alam_bits & (alam_bits - 1)) || nwords < 1 || nwords % alam_bits)
+        return fail(DOPT_EINVAL, "alam_bits must be a power of two dividing group_size*bits/32 = %d, got %d", nwords,
+                    alam_bits);
+    int l = 0;
+    while ((1 << l) < alam_bits) ++l;
+    *lg = l;
+    return DOPT_OK;
+}
+
 // Static per-device scratch of dopt_bn_train_forward_noalloc: the statistics kernel's workgroup
 // partials, which the normalize kernel sums. Each partial slot is written before it is read in
 // the same call, so nothing needs clearing between calls. In host code `scratch` is only a
@@ -523,11 +539,12 @@ int dopt_bn_reduce(const void* x, int x_dtype, int64_t N, int64_t C, int64_t HW,
     return hip_status("bn_reduce launch");
 }
 
-int dopt_bn_norm_quant(const void* x, int x_dtype, int64_t N, int64_t C, int64_t HW, int64_t stride_n,
-                       int64_t stride_c, const float* sum, const float* sumsq, const float* mean_in,
-                       const float* invstd_in, int sync, const float* weight, const float* bias, float eps, int mode,
-                       int group_size, int bits, void* y, void* x_hat, uint32_t* packed, uint32_t* relu_packed,
-                       void* scale, void* minv, float* mean_out, float* var_out, void* stream) {
+static int bn_norm_quant_impl(const void* x, int x_dtype, int64_t N, int64_t C, int64_t HW, int64_t stride_n,
+                              int64_t stride_c, const float* sum, const float* sumsq, const float* mean_in,
+                              const float* invstd_in, int sync, const float* weight, const float* bias, float eps,
+                              int mode, int group_size, int bits, int alam_lg, void* y, void* x_hat, uint32_t* packed,
+                              uint32_t* relu_packed, void* scale, void* minv, float* mean_out, float* var_out,
+                              void* stream) {
     int rc;
     dopt::BnGeom g;
     if ((rc = bn_geom(N, C, HW, stride_n, stride_c, &g))) return rc;
@@ -558,10 +575,33 @@ int dopt_bn_norm_quant(const void* x, int x_dtype, int64_t N, int64_t C, int64_t
     a.minv = (uint16_t*)minv;
     a.mean_out = mean_out;
     a.var_out = var_out;
+    a.alam_lg = alam_lg;
     (void)hipGetLastError();
     dopt::launch_bn_fwd(a, x_dtype, mode, group_size, bits,
                         bn_width(g, {{x, bn_bytes(x_dtype)}, {y, 2}, {x_hat, 2}}), (hipStream_t)stream);
     return hip_status("bn_norm_quant launch");
+}
+
+int dopt_bn_norm_quant(const void* x, int x_dtype, int64_t N, int64_t C, int64_t HW, int64_t stride_n,
+                       int64_t stride_c, const float* sum, const float* sumsq, const float* mean_in,
+                       const float* invstd_in, int sync, const float* weight, const float* bias, float eps, int mode,
+                       int group_size, int bits, void* y, void* x_hat, uint32_t* packed, uint32_t* relu_packed,
+                       void* scale, void* minv, float* mean_out, float* var_out, void* stream) {
+    return bn_norm_quant_impl(x, x_dtype, N, C, HW, stride_n, stride_c, sum, sumsq, mean_in, invstd_in, sync, weight,
+                              bias, eps, mode, group_size, bits, 0, y, x_hat, packed, relu_packed, scale, minv,
+                              mean_out, var_out, stream);
+}
+
+int dopt_bn_norm_quant_alam(const void* x, int x_dtype, int64_t N, int64_t C, int64_t HW, int64_t stride_n,
+                            int64_t stride_c, const float* sum, const float* sumsq, const float* mean_in,
+                            const float* invstd_in, int sync, const float* weight, const float* bias, float eps,
+                            int group_size, int bits, int alam_bits, void* y, uint32_t* packed, void* scale,
+                            void* minv, float* mean_out, float* var_out, void* stream) {
+    int rc, lg = 0;
+    if ((rc = bn_alam_lg(group_size, bits, alam_bits, &lg))) return rc;
+    return bn_norm_quant_impl(x, x_dtype, N, C, HW, stride_n, stride_c, sum, sumsq, mean_in, invstd_in, sync, weight,
+                              bias, eps, DOPT_BN_QUANT, group_size, bits, lg, y, nullptr, packed, nullptr, scale, minv,
+                              mean_out, var_out, stream);
 }
 
 }  // extern "C"
@@ -689,10 +729,10 @@ int dopt_bn_train_backward(int mode, const uint32_t* packed, const uint32_t* rel
     return hip_status("bn_train_backward launch");
 }
 
-int dopt_bn_bwd_reduce(int mode, const void* x_hat, const uint32_t* packed, const uint32_t* relu_packed,
-                       const void* scale, const void* minv, const void* dy, int dy_dtype, int64_t N, int64_t C,
-                       int64_t HW, int64_t stride_n, int64_t stride_c, int group_size, int bits, float* workspace,
-                       float* dweight, float* dbias, void* stream) {
+static int bn_bwd_reduce_impl(int mode, const void* x_hat, const uint32_t* packed, const uint32_t* relu_packed,
+                              const void* scale, const void* minv, const void* dy, int dy_dtype, int64_t N, int64_t C,
+                              int64_t HW, int64_t stride_n, int64_t stride_c, int group_size, int bits, int alam,
+                              int alam_lg, float* workspace, float* dweight, float* dbias, void* stream) {
     int rc;
     dopt::BnGeom g;
     if ((rc = bn_geom(N, C, HW, stride_n, stride_c, &g))) return rc;
@@ -714,6 +754,8 @@ int dopt_bn_bwd_reduce(int mode, const void* x_hat, const uint32_t* packed, cons
     a.partial = workspace;
     a.dw = dweight;
     a.db = dbias;
+    a.alam = alam;
+    a.alam_lg = alam_lg;
     (void)hipGetLastError();
     dopt::launch_bn_bwd_reduce(a, dy_dtype, mode, group_size, bits,
                                bn_width(g, {{dy, bn_bytes(dy_dtype)}, {mode == DOPT_BN_NORM ? x_hat : nullptr, 2}}),
@@ -721,11 +763,28 @@ int dopt_bn_bwd_reduce(int mode, const void* x_hat, const uint32_t* packed, cons
     return hip_status("bn_bwd_reduce launch");
 }
 
-int dopt_bn_bwd_dx(int mode, const void* x_hat, const uint32_t* packed, const uint32_t* relu_packed,
-                   const void* scale, const void* minv, const void* dy, int dy_dtype, int64_t N, int64_t C, int64_t HW,
-                   int64_t stride_n, int64_t stride_c, int group_size, int bits, const float* dweight,
-                   const float* dbias, const float* weight, const float* var, float eps, int var_is_invstd, void* dx,
-                   void* stream) {
+int dopt_bn_bwd_reduce(int mode, const void* x_hat, const uint32_t* packed, const uint32_t* relu_packed,
+                       const void* scale, const void* minv, const void* dy, int dy_dtype, int64_t N, int64_t C,
+                       int64_t HW, int64_t stride_n, int64_t stride_c, int group_size, int bits, float* workspace,
+                       float* dweight, float* dbias, void* stream) {
+    return bn_bwd_reduce_impl(mode, x_hat, packed, relu_packed, scale, minv, dy, dy_dtype, N, C, HW, stride_n,
+                              stride_c, group_size, bits, 0, 0, workspace, dweight, dbias, stream);
+}
+
+int dopt_bn_bwd_reduce_alam(const uint32_t* packed, const void* scale, const void* minv, const void* dy, int dy_dtype,
+                            int64_t N, int64_t C, int64_t HW, int64_t stride_n, int64_t stride_c, int group_size,
+                            int bits, int alam_bits, float* workspace, float* dweight, float* dbias, void* stream) {
+    int rc, lg = 0;
+    if ((rc = bn_alam_lg(group_size, bits, alam_bits, &lg))) return rc;
+    return bn_bwd_reduce_impl(DOPT_BN_QUANT, nullptr, packed, nullptr, scale, minv, dy, dy_dtype, N, C, HW, stride_n,
+                              stride_c, group_size, bits, 1, lg, workspace, dweight, dbias, stream);
+}
+
+static int bn_bwd_dx_impl(int mode, const void* x_hat, const uint32_t* packed, const uint32_t* relu_packed,
+                          const void* scale, const void* minv, const void* dy, int dy_dtype, int64_t N, int64_t C,
+                          int64_t HW, int64_t stride_n, int64_t stride_c, int group_size, int bits, int alam_lg,
+                          const float* dweight, const float* dbias, const float* weight, const float* var, float eps,
+                          int var_is_invstd, void* dx, void* stream) {
     int rc;
     dopt::BnGeom g;
     if ((rc = bn_geom(N, C, HW, stride_n, stride_c, &g))) return rc;
@@ -750,11 +809,32 @@ int dopt_bn_bwd_dx(int mode, const void* x_hat, const uint32_t* packed, const ui
     a.eps = eps;
     a.var_is_invstd = var_is_invstd != 0;
     a.dx = (uint16_t*)dx;
+    a.alam = alam_lg > 0;
+    a.alam_lg = alam_lg;
     (void)hipGetLastError();
     dopt::launch_bn_bwd_dx(a, dy_dtype, mode, group_size, bits,
                            bn_width(g, {{dy, bn_bytes(dy_dtype)}, {dx, 2}, {mode == DOPT_BN_NORM ? x_hat : nullptr, 2}}),
                            (hipStream_t)stream);
     return hip_status("bn_bwd_dx launch");
+}
+
+int dopt_bn_bwd_dx(int mode, const void* x_hat, const uint32_t* packed, const uint32_t* relu_packed,
+                   const void* scale, const void* minv, const void* dy, int dy_dtype, int64_t N, int64_t C, int64_t HW,
+                   int64_t stride_n, int64_t stride_c, int group_size, int bits, const float* dweight,
+                   const float* dbias, const float* weight, const float* var, float eps, int var_is_invstd, void* dx,
+                   void* stream) {
+    return bn_bwd_dx_impl(mode, x_hat, packed, relu_packed, scale, minv, dy, dy_dtype, N, C, HW, stride_n, stride_c,
+                          group_size, bits, 0, dweight, dbias, weight, var, eps, var_is_invstd, dx, stream);
+}
+
+int dopt_bn_bwd_dx_alam(const uint32_t* packed, const void* scale, const void* minv, const void* dy, int dy_dtype,
+                        int64_t N, int64_t C, int64_t HW, int64_t stride_n, int64_t stride_c, int group_size,
+                        int bits, int alam_bits, const float* dweight, const float* dbias, const float* weight,
+                        const float* var, float eps, int var_is_invstd, void* dx, void* stream) {
+    int rc, lg = 0;
+    if ((rc = bn_alam_lg(group_size, bits, alam_bits, &lg))) return rc;
+    return bn_bwd_dx_impl(DOPT_BN_QUANT, nullptr, packed, nullptr, scale, minv, dy, dy_dtype, N, C, HW, stride_n,
+                          stride_c, group_size, bits, lg, dweight, dbias, weight, var, eps, var_is_invstd, dx, stream);
 }
 
 int64_t dopt_dw_gemm_workspace_floats(int64_t M, int64_t N, int64_t K) {

@@ -339,4 +339,18 @@ __device__ __forceinline__ float philox_byte_to_u(uint32_t w, int k) {
     return __builtin_fmaf(b, 1.0f / 256.0f, 1.0f / 512.0f);
 }
 
+// Triton's uint_to_uniform_float (triton/language/random.py) of a Philox output word: the word as
+// int32, folded to non-negative (~i for i < 0), times fp32(4.6566127342e-10) = 0x2fffffff.
+__device__ __forceinline__ float triton_uniform(uint32_t w) {
+    int32_t i = (int32_t)w;
+    if (i < 0) i = ~i;
+    return (float)i * __uint_as_float(0x2fffffffu);
+}
+
+// Triton's tl.rand(seed, offset) for a 32-bit offset: the first word of Philox4x32-10 with counter
+// (offset, 0, 0, 0) and key (lo32, hi32 of seed), as a uniform in [0, 1).
+__device__ __forceinline__ float triton_rand(uint64_t seed, uint32_t offset) {
+    return triton_uniform(philox4x32_10(offset, 0u, 0u, 0u, (uint32_t)seed, (uint32_t)(seed >> 32)).x);
+}
+
 }  // namespace dopt

@@ -30,7 +30,6 @@ from torch.amp import custom_bwd, custom_fwd
 from torch.autograd import Function
 
 from .. import _lib, bn_lib  # noqa: F401  (bn_lib registers the BatchNorm act_lib operators)
-from ..act_lib import _no_alam
 from .module_utils import unified_dequantize, unified_quantize
 
 _NW, _NS = 8, 5  # launch-tuning arguments of the reference's operators (ignored by the kernels)
@@ -79,14 +78,24 @@ class _DOBatchNorm(Function):
             ctx.meta = (BLOCK_M, meta, target_name, None, None, True)
             return y3.view(N, C, H, W)
         avg_alam, alam_bits = m["AVG_ALAM"], m["ALAM_BITS"]
-        _no_alam(avg_alam, "DOBatchNorm2d")
+        if avg_alam:
+            # the reference's path (normalization_ops.py:72-98): statistics, then normalize +
+            # quant-pack with one code per run of alam_bits elements, then the running statistics
+            sum_, sumsq_ = torch.ops.act_lib.bn_fwd_reduce(x3, **geo, BLOCK_M=BLOCK_M, num_warps=_NW, num_stages=_NS)
+            y, packed, scale, xmin, mean, var = torch.ops.act_lib.bn_fwd_norm_quant_pack_fused(
+                x3, sum_, sumsq_, weight, bias, None, None, **geo, BLOCK_M=BLOCK_M, bits=m["bits"], sync=False,
+                avg_alam=True, alam_bits=alam_bits, num_warps=_NW, num_stages=_NS)
+            _update_running(running_mean, running_var, mean, var, momentum)
+            ctx.save_for_backward(weight, packed, scale, xmin, var)
+            ctx.meta = (BLOCK_M, meta, target_name, True, alam_bits, False)
+            return y.view(N, C, H, W)
         # statistics, normalize + quant-pack and the running-statistics update in one operator
         # call (the reference's bn_fwd_reduce + bn_fwd_norm_quant_pack_fused + update)
         y, packed, _, scale, xmin, mean, var = torch.ops.act_lib.bn_train_fwd(
             x3, weight, bias, _stat(running_mean, x3), _stat(running_var, x3), momentum, BLOCK_M, m["bits"],
             _lib.BN_QUANT)
         ctx.save_for_backward(weight, packed, scale, xmin, var)
-        ctx.meta = (BLOCK_M, meta, target_name, avg_alam, alam_bits, False)
+        ctx.meta = (BLOCK_M, meta, target_name, False, 0, False)
         return y.view(N, C, H, W)
 
     @staticmethod
@@ -105,6 +114,16 @@ class _DOBatchNorm(Function):
                                                             num_stages=_NS)
             dx = torch.ops.act_lib.bn_bwd_dx(x_hat, dy3, var, weight, dbeta, dgamma, **geo, BLOCK_M=BLOCK_M,
                                              sync=False, num_warps=_NW, num_stages=_NS)
+        elif avg_alam:
+            # normalization_ops.py:141-157: the reduce restores the codes with the reference's noise,
+            # the input gradient without
+            weight, packed, scale, xmin, var = ctx.saved_tensors
+            bits = meta[f"{target_name}"]["bits"]
+            dgamma, dbeta = torch.ops.act_lib.bn_bwd_reduce_dequant_unpack_fused(
+                packed, dy3, scale, xmin, **geo, BLOCK_M=BLOCK_M, bits=bits, avg_alam=True, alam_bits=alam_bits)
+            dx = torch.ops.act_lib.bn_bwd_dx_dequant_unpack_fused(
+                packed, dy3, scale, xmin, dgamma, dbeta, weight, var, **geo, BLOCK_M=BLOCK_M, bits=bits, sync=False,
+                avg_alam=True, alam_bits=alam_bits)
         else:
             weight, packed, scale, xmin, var = ctx.saved_tensors
             bits = meta[f"{target_name}"]["bits"]

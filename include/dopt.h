@@ -260,6 +260,19 @@ int dopt_bn_norm_quant(const void* x, int x_dtype, int64_t N, int64_t C, int64_t
                        int group_size, int bits, void* y, void* x_hat, uint32_t* packed, uint32_t* relu_packed,
                        void* scale, void* minv, float* mean_out, float* var_out, void* stream);
 
+/* dopt_bn_norm_quant in DOPT_BN_QUANT mode with avg_alam: every run of A = alam_bits consecutive
+ * elements of a channel becomes one code, trunc((qf[0] + ... + qf[A-1]) / A) clamped to
+ * [0, QMAX] (NaN -> 0), qf = fma(t - min, 1/scale, 0.5-1e-6) as above, summed left to right.
+ * alam_bits is a power of two dividing group_size*bits/32; packed is [C, M*bits/32/A], the
+ * channel's M/A codes as one bitstream; scale / min per group as without avg_alam. Replaces
+ * act_lib::bn_fwd_norm_quant_pack_fused with avg_alam=True (kernel_registration.py:83-150,
+ * kernel_implementation.py:194-237). */
+int dopt_bn_norm_quant_alam(const void* x, int x_dtype, int64_t N, int64_t C, int64_t HW, int64_t stride_n,
+                            int64_t stride_c, const float* sum, const float* sumsq, const float* mean_in,
+                            const float* invstd_in, int sync, const float* weight, const float* bias, float eps,
+                            int group_size, int bits, int alam_bits, void* y, uint32_t* packed, void* scale,
+                            void* minv, float* mean_out, float* var_out, void* stream);
+
 /* The training forward of the compressed BatchNorm layer in one call: the statistics kernel's
  * workgroup partials (into workspace, dopt_bn_workspace_floats() floats), then the normalize (+ ReLU)
  * + quant-pack kernel of dopt_bn_norm_quant (sync = 0), which sums the partials itself in the
@@ -309,6 +322,17 @@ int dopt_bn_bwd_reduce(int mode, const void* x_hat, const uint32_t* packed, cons
                        int64_t HW, int64_t stride_n, int64_t stride_c, int group_size, int bits, float* workspace,
                        float* dweight, float* dbias, void* stream);
 
+/* dopt_bn_bwd_reduce of dopt_bn_norm_quant_alam's codes: element e of a channel carries code e/A
+ * plus the reference's noise, x_hat' = fma(q + (u - 0.5), scale, min) with u = Triton's
+ * tl.rand(42 + e / (2 group_size), e mod group_size) (Philox4x32-10 first word, counter
+ * (offset, 0, 0, 0), key the seed's low and high words, as a uniform in [0, 1)); the noise is
+ * added at alam_bits = 1 too, whose codes are dopt_bn_norm_quant's. Replaces
+ * act_lib::bn_bwd_reduce_dequant_unpack_fused with avg_alam=True (kernel_registration.py:211-240,
+ * kernel_implementation.py:374-391). */
+int dopt_bn_bwd_reduce_alam(const uint32_t* packed, const void* scale, const void* minv, const void* dy, int dy_dtype,
+                            int64_t N, int64_t C, int64_t HW, int64_t stride_n, int64_t stride_c, int group_size,
+                            int bits, int alam_bits, float* workspace, float* dweight, float* dbias, void* stream);
+
 /* dx = (fma(-x_hat', dweight/M, dy*m - dbias/M) * weight) * invstd -> bf16, invstd = var_is_invstd ? var :
  * 1/sqrt(var + eps). Replaces act_lib::bn_bwd_dx (kernel_registration.py:181-208),
  * act_lib::bn_bwd_dx_dequant_unpack_fused (:243-276) and act_lib::bn_relu_bwd_dx_fused_dequant_unpack
@@ -318,6 +342,14 @@ int dopt_bn_bwd_dx(int mode, const void* x_hat, const uint32_t* packed, const ui
                    int64_t stride_n, int64_t stride_c, int group_size, int bits, const float* dweight,
                    const float* dbias, const float* weight, const float* var, float eps, int var_is_invstd, void* dx,
                    void* stream);
+
+/* dopt_bn_bwd_dx of dopt_bn_norm_quant_alam's codes: x_hat' = fma(q, scale, min) with q = code e/A
+ * (no noise). Replaces act_lib::bn_bwd_dx_dequant_unpack_fused with avg_alam=True
+ * (kernel_registration.py:243-276, kernel_implementation.py:455-462). */
+int dopt_bn_bwd_dx_alam(const uint32_t* packed, const void* scale, const void* minv, const void* dy, int dy_dtype,
+                        int64_t N, int64_t C, int64_t HW, int64_t stride_n, int64_t stride_c, int group_size,
+                        int bits, int alam_bits, const float* dweight, const float* dbias, const float* weight,
+                        const float* var, float eps, int var_is_invstd, void* dx, void* stream);
 
 /* ---------------------------------------------------------------- Linear weight gradient
  * dW[m][n] = sum_k dy[k][m] * x_hat[k][n] (bf16 MFMA, fp32 accumulation) and, when db is not NULL,

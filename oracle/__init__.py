@@ -77,12 +77,13 @@ def lib():
         L.oracle_bn_reduce.argtypes = [vp, i32, i64, i64, i64, i64, i64, vp, vp]
         L.oracle_bn_reduce.restype = i32
         L.oracle_bn_norm_quant.argtypes = [vp, i32, i64, i64, i64, i64, i64, vp, vp, vp, vp, i32, vp, vp, f32, i32,
-                                           i32, i32, vp, vp, vp, vp, vp, vp, vp, vp, vp]
+                                           i32, i32, vp, vp, vp, vp, vp, vp, vp, vp, vp, i32]
         L.oracle_bn_norm_quant.restype = i32
-        L.oracle_bn_bwd_reduce.argtypes = [i32, vp, vp, vp, vp, vp, vp, i32, i64, i64, i64, i64, i64, i32, i32, vp, vp]
+        L.oracle_bn_bwd_reduce.argtypes = [i32, vp, vp, vp, vp, vp, vp, i32, i64, i64, i64, i64, i64, i32, i32, vp, vp,
+                                           i32]
         L.oracle_bn_bwd_reduce.restype = i32
         L.oracle_bn_bwd_dx.argtypes = [i32, vp, vp, vp, vp, vp, vp, i32, i64, i64, i64, i64, i64, i32, i32, vp, vp,
-                                       vp, vp, f32, i32, vp]
+                                       vp, vp, f32, i32, vp, i32]
         L.oracle_bn_bwd_dx.restype = i32
         L.oracle_alam_quant_pack.argtypes = [vp, i32, i64, i32, i32, i32, i32, f32, vp, vp, vp]
         L.oracle_alam_quant_pack.restype = i32
@@ -90,6 +91,8 @@ def lib():
         L.oracle_alam_dequant_unpack.restype = i32
         L.oracle_triton_randn.argtypes = [u64, ctypes.c_uint32]
         L.oracle_triton_randn.restype = f32
+        L.oracle_triton_rand.argtypes = [u64, ctypes.c_uint32]
+        L.oracle_triton_rand.restype = f32
         _lib = L
     return _lib
 
@@ -200,6 +203,11 @@ def triton_randn(seed: int, offset: int) -> float:
     return float(lib().oracle_triton_randn(seed, offset))
 
 
+def triton_rand(seed: int, offset: int) -> float:
+    """One value of Triton's tl.rand(seed, offset) as this oracle restates it."""
+    return float(lib().oracle_triton_rand(seed, offset))
+
+
 def pack_codes(codes: np.ndarray, group_size: int, bits: int) -> np.ndarray:
     codes = np.ascontiguousarray(codes, dtype=np.int8)
     ng = codes.size // group_size
@@ -307,11 +315,12 @@ def bn_reduce(x: np.ndarray):
 
 
 def bn_norm_quant(x: np.ndarray, weight, bias, *, mode, group_size=0, bits=2, eps=1e-5, sum=None, sumsq=None,
-                  mean=None, invstd=None):
+                  mean=None, invstd=None, alam_bits=0):
     """Normalize (+ ReLU) (+ quant-pack) of a contiguous [N, C, ...] array. Statistics: fp32 sum /
     sumsq (non-sync) or fp32 mean / invstd (sync). Returns a dict with y (bf16 bits, x's shape),
-    x_hat (BN_NORM), packed [C, M*bits/32], relu_packed [C, M/32], scale / min (bf16 bits
-    [C, M/g]), mean / var (non-sync) and t (fp32 [C, M], the quantized values)."""
+    x_hat (BN_NORM), packed [C, M*bits/32] ([C, M*bits/32/alam_bits] with avg_alam, alam_bits > 0),
+    relu_packed [C, M/32], scale / min (bf16 bits [C, M/g]), mean / var (non-sync) and t (fp32
+    [C, M], the quantized values)."""
     x = np.ascontiguousarray(x)
     N, C, HW, sn, sc = _bn_geom(x)
     M = N * HW
@@ -322,7 +331,7 @@ def bn_norm_quant(x: np.ndarray, weight, bias, *, mode, group_size=0, bits=2, ep
     out = {"y": np.zeros(x.shape, dtype=np.uint16)}
     quant = mode != BN_NORM
     out["x_hat"] = np.zeros(x.shape, dtype=np.uint16) if not quant else None
-    out["packed"] = np.zeros((C, M * bits // 32), dtype=np.uint32) if quant else None
+    out["packed"] = np.zeros((C, M * bits // 32 // max(alam_bits, 1)), dtype=np.uint32) if quant else None
     out["relu_packed"] = np.zeros((C, M // 32), dtype=np.uint32) if mode in (BN_RELU_QUANT, BN_RELU6_QUANT) else None
     ng = M // group_size if quant else 0
     out["scale"] = np.zeros((C, ng), dtype=np.uint16) if quant else None
@@ -334,7 +343,7 @@ def bn_norm_quant(x: np.ndarray, weight, bias, *, mode, group_size=0, bits=2, ep
                                       _ptr(invstd), int(sync), _ptr(w), _ptr(b), float(eps), mode, group_size, bits,
                                       _ptr(out["y"]), _ptr(out["x_hat"]), _ptr(out["packed"]),
                                       _ptr(out["relu_packed"]), _ptr(out["scale"]), _ptr(out["min"]),
-                                      _ptr(out["mean"]), _ptr(out["var"]), _ptr(out["t"])))
+                                      _ptr(out["mean"]), _ptr(out["var"]), _ptr(out["t"]), int(alam_bits)))
     return out
 
 
@@ -345,18 +354,19 @@ def _bn_bwd_args(mode, x_hat, packed, relu_packed, scale, mn, dy):
 
 
 def bn_bwd_reduce(dy: np.ndarray, *, mode, x_hat=None, packed=None, relu_packed=None, scale=None, min=None,
-                  group_size=0, bits=2):
-    """-> (dweight, dbias) float64 [C]: sum(dy*m * x_hat'), sum(dy*m)."""
+                  group_size=0, bits=2, alam_bits=0):
+    """-> (dweight, dbias) float64 [C]: sum(dy*m * x_hat'), sum(dy*m); with avg_alam (alam_bits > 0)
+    x_hat' carries the reference's tl.rand noise."""
     xh, p, rp, s, mn, dy = _bn_bwd_args(mode, x_hat, packed, relu_packed, scale, min, dy)
     N, C, HW, sn, sc = _bn_geom(dy)
     dw, db = np.zeros(C), np.zeros(C)
     _check(lib().oracle_bn_bwd_reduce(mode, _ptr(xh), _ptr(p), _ptr(rp), _ptr(s), _ptr(mn), _ptr(dy), _dtype_code(dy),
-                                      N, C, HW, sn, sc, group_size, bits, _ptr(dw), _ptr(db)))
+                                      N, C, HW, sn, sc, group_size, bits, _ptr(dw), _ptr(db), int(alam_bits)))
     return dw, db
 
 
 def bn_bwd_dx(dy: np.ndarray, dweight, dbias, weight, var, *, mode, eps=1e-7, var_is_invstd=False, x_hat=None,
-              packed=None, relu_packed=None, scale=None, min=None, group_size=0, bits=2):
+              packed=None, relu_packed=None, scale=None, min=None, group_size=0, bits=2, alam_bits=0):
     """-> dx as bf16 bits (uint16), dy's shape; dweight / dbias / weight / var fp32 [C]."""
     xh, p, rp, s, mn, dy = _bn_bwd_args(mode, x_hat, packed, relu_packed, scale, min, dy)
     N, C, HW, sn, sc = _bn_geom(dy)
@@ -365,7 +375,7 @@ def bn_bwd_dx(dy: np.ndarray, dweight, dbias, weight, var, *, mode, eps=1e-7, va
     dx = np.zeros(dy.shape, dtype=np.uint16)
     _check(lib().oracle_bn_bwd_dx(mode, _ptr(xh), _ptr(p), _ptr(rp), _ptr(s), _ptr(mn), _ptr(dy), _dtype_code(dy), N,
                                   C, HW, sn, sc, group_size, bits, _ptr(dw), _ptr(db), _ptr(w), _ptr(v), float(eps),
-                                  int(var_is_invstd), _ptr(dx)))
+                                  int(var_is_invstd), _ptr(dx), int(alam_bits)))
     return dx
 
 

@@ -355,6 +355,17 @@ float oracle_triton_randn(uint64_t seed, uint32_t offset) {
     return r * cosf(th);
 }
 
+/* Triton's tl.rand(seed, offset) for a 32-bit offset (triton/language/random.py, restated): the
+ * first word of Philox4x32-10 with counter (offset, 0, 0, 0) and key (lo32, hi32 of seed), mapped
+ * to [0, 1) as above. */
+float oracle_triton_rand(uint64_t seed, uint32_t offset) {
+    const uint32_t ctr[4] = {offset, 0u, 0u, 0u};
+    const uint32_t key[2] = {(uint32_t)seed, (uint32_t)(seed >> 32)};
+    uint32_t w[4];
+    oracle_philox4x32_10(ctr, key, w);
+    return triton_uniform(w[0]);
+}
+
 static int alam_check(int64_t n_groups, int g, int bits, int alam_bits) {
     int s = 0;
     int rc = check_common(n_groups, g, bits, NULL, &s);
@@ -666,6 +677,13 @@ int oracle_act_dequant_mul(const uint32_t* packed, const void* scale, const void
 #define O_BN_RELU_QUANT 2
 #define O_BN_RELU6_QUANT 3
 
+/* avg_alam's run length: a power of two dividing the group's g * bits / 32 code words
+ * (kernel_registration.py:124-128) */
+static int bn_alam_check(int g, int bits, int alam_bits) {
+    const int nw = g * bits / 32;
+    return alam_bits < 1 || (alam_bits & (alam_bits - 1)) || nw < 1 || nw % alam_bits;
+}
+
 static int64_t bn_off(int64_t HW, int64_t sn, int64_t sc, int64_t c, int64_t e) {
     int64_t n = e / HW;
     return n * sn + c * sc + (e - n * HW);
@@ -700,22 +718,27 @@ int oracle_bn_reduce(const void* x, int x_dtype, int64_t N, int64_t C, int64_t H
  *     clamped to [0, QMAX] (:157-177)
  *   BN_RELU*: m = y > 0 (relu6: 0 < y < 6); y = m ? y : 0 (relu6: min(max(y, 0), 6)); codes of
  *     t = x_hat with q = trunc((t - min)/scale + (0.5-1e-6)) (bn_act_fusion.py:63-101)
- *   t_out (optional, fp32 [C, M]): the values the codes quantize */
+ *   t_out (optional, fp32 [C, M]): the values the codes quantize
+ *   alam_bits > 0 (BN_QUANT only, the avg_alam mode, :194-237): one code per run of A = alam_bits
+ *     elements, trunc of the run's qf summed left to right and divided by A (the summation order is
+ *     this restatement's choice, as in oracle_alam_quant_pack); packed [C, M*bits/32/A] */
 int oracle_bn_norm_quant(const void* x, int x_dtype, int64_t N, int64_t C, int64_t HW, int64_t sn, int64_t sc,
                          const float* sum, const float* sumsq, const float* mean_in, const float* invstd_in,
                          int sync, const float* w, const float* b, float eps, int mode, int g, int bits,
                          uint16_t* y, uint16_t* x_hat, uint32_t* packed, uint32_t* relu_packed, uint16_t* scale,
-                         uint16_t* minv, float* mean_out, float* var_out, float* t_out) {
+                         uint16_t* minv, float* mean_out, float* var_out, float* t_out, int alam_bits) {
     if (N < 0 || C < 0 || HW < 0 || mode < 0 || mode > 3) return O_EINVAL;
     const int64_t M = N * HW;
     if (mode != O_BN_NORM) {
         if (bits != 1 && bits != 2 && bits != 4 && bits != 8) return O_EBITS;
         if (g < 32 || g > 512 || (g & (g - 1)) || M % g) return O_EINVAL;
     }
+    if (alam_bits && (mode != O_BN_QUANT || bn_alam_check(g, bits, alam_bits))) return O_EINVAL;
+    const int A = alam_bits > 0 ? alam_bits : 1;
     const int QMAX = (1 << bits) - 1;
     const float qmaxf = (float)QMAX;
     const float half_m = (float)(0.5 - 1e-6);
-    const int64_t TW = M * bits / 32, NG = mode == O_BN_NORM ? 0 : M / g;
+    const int64_t TW = M * bits / 32 / A, NG = mode == O_BN_NORM ? 0 : M / g;
 #pragma omp parallel
     {
         float* t = (float*)malloc(sizeof(float) * (g > 0 ? g : 1));
@@ -770,14 +793,23 @@ int oracle_bn_norm_quant(const void* x, int x_dtype, int64_t N, int64_t C, int64
                 float rng = mx - mn;
                 float step = rng > 0.0f ? rng / qmaxf : 1.0f;
                 float invs = 1.0f / step;
-                uint32_t* words = packed + c * TW + r * (g * bits / 32);
-                for (int k = 0; k < g * bits / 32; ++k) words[k] = 0;
-                for (int e = 0; e < g; ++e) {
-                    float qf = mode == O_BN_QUANT ? fmaf(t[e] - mn, invs, half_m) : (t[e] - mn) / step + half_m;
+                uint32_t* words = packed + c * TW + r * (g * bits / 32 / A);
+                for (int k = 0; k < g * bits / 32 / A; ++k) words[k] = 0;
+                /* one code per run of A elements (A = 1 without avg_alam): the run's qf summed left
+                 * to right, divided by A (kernel_implementation.py:194-199) */
+                for (int k = 0; k < g / A; ++k) {
+                    float qf = 0.0f;
+                    for (int j = 0; j < A; ++j) {
+                        const int e = k * A + j;
+                        const float v = mode == O_BN_QUANT ? fmaf(t[e] - mn, invs, half_m)
+                                                           : (t[e] - mn) / step + half_m;
+                        qf = j ? qf + v : v;
+                    }
+                    if (A > 1) qf = qf / (float)A;
                     if (qf != qf) qf = 0.0f;
                     qf = fminf(fmaxf(qf, 0.0f), qmaxf);
                     int q = (int)qf;
-                    words[(e * bits) / 32] |= (uint32_t)q << ((e * bits) % 32);
+                    words[(k * bits) / 32] |= (uint32_t)q << ((k * bits) % 32);
                 }
                 scale[c * NG + r] = f32_to_bf16(step);
                 minv[c * NG + r] = f32_to_bf16(mn);
@@ -792,17 +824,22 @@ int oracle_bn_norm_quant(const void* x, int x_dtype, int64_t N, int64_t C, int64
  * :463-470; bn_act_fusion.py:160-172, :247-255): x_hat' = fma(q, scale, min) or the bf16 x_hat */
 static void bn_bwd_elem(int mode, const uint16_t* x_hat, const uint32_t* packed, const uint32_t* relu_packed,
                         const uint16_t* scale, const uint16_t* minv, const void* dy, int dy_dtype, int64_t M,
-                        int64_t HW, int64_t sn, int64_t sc, int g, int bits, int64_t c, int64_t e, float* xh,
-                        float* dyv) {
+                        int64_t HW, int64_t sn, int64_t sc, int g, int bits, int A, int noise, int64_t c, int64_t e,
+                        float* xh, float* dyv) {
     const int64_t o = bn_off(HW, sn, sc, c, e);
     float d = load_elem(dy, dy_dtype, o);
     if (mode == O_BN_NORM) {
         *xh = bf16_to_f32(x_hat[o]);
     } else {
-        const int64_t bit = e * bits;
-        uint32_t q = (packed[c * (M * bits / 32) + bit / 32] >> (bit % 32)) & ((1u << bits) - 1u);
+        /* code e / A (each code repeated A times with avg_alam, :374-377, :455-458), plus
+         * tl.rand(42 + b, e mod g) - 0.5 in the avg_alam reduce, b = e / (2 g) the reference's
+         * two-group block index (:379-381) */
+        const int64_t bit = (e / A) * bits;
+        uint32_t q = (packed[c * (M * bits / 32 / A) + bit / 32] >> (bit % 32)) & ((1u << bits) - 1u);
         const int64_t gi = c * (M / g) + e / g;
-        *xh = fmaf((float)q, bf16_to_f32(scale[gi]), bf16_to_f32(minv[gi]));
+        float qf = (float)q;
+        if (noise) qf = qf + (oracle_triton_rand(42u + (uint64_t)(e / (2 * g)), (uint32_t)(e % g)) - 0.5f);
+        *xh = fmaf(qf, bf16_to_f32(scale[gi]), bf16_to_f32(minv[gi]));
         if (mode != O_BN_QUANT) {
             uint32_t m = (relu_packed[c * (M / 32) + e / 32] >> (e % 32)) & 1u;
             d = d * (float)m;
@@ -814,16 +851,19 @@ static void bn_bwd_elem(int mode, const uint16_t* x_hat, const uint32_t* packed,
 /* dweight = sum(dy*m * x_hat'), dbias = sum(dy*m) per channel, in double */
 int oracle_bn_bwd_reduce(int mode, const uint16_t* x_hat, const uint32_t* packed, const uint32_t* relu_packed,
                          const uint16_t* scale, const uint16_t* minv, const void* dy, int dy_dtype, int64_t N,
-                         int64_t C, int64_t HW, int64_t sn, int64_t sc, int g, int bits, double* dw, double* db) {
+                         int64_t C, int64_t HW, int64_t sn, int64_t sc, int g, int bits, double* dw, double* db,
+                         int alam_bits) {
     if (N < 0 || C < 0 || HW < 0 || mode < 0 || mode > 3) return O_EINVAL;
+    if (alam_bits && (mode != O_BN_QUANT || bn_alam_check(g, bits, alam_bits))) return O_EINVAL;
+    const int A = alam_bits > 0 ? alam_bits : 1;
     const int64_t M = N * HW;
 #pragma omp parallel for schedule(static)
     for (int64_t c = 0; c < C; ++c) {
         double a = 0.0, s = 0.0;
         for (int64_t e = 0; e < M; ++e) {
             float xh, d;
-            bn_bwd_elem(mode, x_hat, packed, relu_packed, scale, minv, dy, dy_dtype, M, HW, sn, sc, g, bits, c, e,
-                        &xh, &d);
+            bn_bwd_elem(mode, x_hat, packed, relu_packed, scale, minv, dy, dy_dtype, M, HW, sn, sc, g, bits, A,
+                        alam_bits > 0, c, e, &xh, &d);
             a += (double)d * (double)xh;
             s += d;
         }
@@ -838,8 +878,10 @@ int oracle_bn_bwd_reduce(int mode, const uint16_t* x_hat, const uint32_t* packed
 int oracle_bn_bwd_dx(int mode, const uint16_t* x_hat, const uint32_t* packed, const uint32_t* relu_packed,
                      const uint16_t* scale, const uint16_t* minv, const void* dy, int dy_dtype, int64_t N, int64_t C,
                      int64_t HW, int64_t sn, int64_t sc, int g, int bits, const float* dw, const float* db,
-                     const float* w, const float* var, float eps, int var_is_invstd, uint16_t* dx) {
+                     const float* w, const float* var, float eps, int var_is_invstd, uint16_t* dx, int alam_bits) {
     if (N < 0 || C < 0 || HW < 0 || mode < 0 || mode > 3) return O_EINVAL;
+    if (alam_bits && (mode != O_BN_QUANT || bn_alam_check(g, bits, alam_bits))) return O_EINVAL;
+    const int A = alam_bits > 0 ? alam_bits : 1;
     const int64_t M = N * HW;
     const float Mf = (float)M;
 #pragma omp parallel for schedule(static)
@@ -848,8 +890,8 @@ int oracle_bn_bwd_dx(int mode, const uint16_t* x_hat, const uint32_t* packed, co
         const float inv = var_is_invstd ? var[c] : 1.0f / sqrtf(var[c] + eps);
         for (int64_t e = 0; e < M; ++e) {
             float xh, d;
-            bn_bwd_elem(mode, x_hat, packed, relu_packed, scale, minv, dy, dy_dtype, M, HW, sn, sc, g, bits, c, e,
-                        &xh, &d);
+            bn_bwd_elem(mode, x_hat, packed, relu_packed, scale, minv, dy, dy_dtype, M, HW, sn, sc, g, bits, A, 0,
+                        c, e, &xh, &d);
             dx[bn_off(HW, sn, sc, c, e)] = f32_to_bf16((fmaf(-xh, dwm, d - dbm) * wc) * inv);
         }
     }

@@ -11,7 +11,8 @@ Bar:
     1% of the elements, scale and min within one bf16 ulp.
 Shapes cover every access width of the kernels (8 elements per access at HW = 256, 784; 4 at
 HW = 196; 2 at HW = 50; 1 at HW = 49 and for a misaligned input view), group sizes 32..512
-(BLOCK_M 64..1024), bits 1/2/4/8, bf16 / fp32 / fp16 inputs, and the sync path.
+(BLOCK_M 64..1024), bits 1/2/4/8, bf16 / fp32 / fp16 inputs, the sync path, and the squashed
+operators' avg_alam mode (runs of 1..64 elements per code, the reduce's tl.rand noise).
 """
 import numpy as np
 import pytest
@@ -224,9 +225,68 @@ def test_errors():
     with pytest.raises(ValueError):
         ops.bn_relu_fwd_norm_fused_quant_pack(x3, s, q, w, w, None, None, **g, relu=True, relu6=False, BLOCK_SIZE=64,
                                               BITS=3, sync=False)
-    with pytest.raises(NotImplementedError):
+    with pytest.raises(RuntimeError, match="alam_bits"):  # 2-bit groups of 32 have 2 code words: 4 runs cannot fill them
         ops.bn_fwd_norm_quant_pack_fused(x3, s, q, w, w, None, None, **g, BLOCK_M=64, bits=2, sync=False,
-                                         avg_alam=True, alam_bits=2, num_warps=8, num_stages=5)
+                                         avg_alam=True, alam_bits=4, num_warps=8, num_stages=5)
+
+
+# ----------------------------------------------------------------------------- avg_alam
+# (shape, BLOCK_M, bits, alam_bits, dtype): run lengths dividing the group's code words (1: the
+# plain codes, noise in the reduce only; 16 and 64: runs spanning 2 and 8 lanes), every access width
+# (8 at 16x16 / 28x28, 4 at 14x14, 2 at 5x10, 1 at 7x7), groups of 32..256, and channels whose last
+# wave of 512 elements lies partly past M (7x7: M = 1568)
+ACASES = [((4, 16, 16, 16), 64, 2, 2, torch.bfloat16), ((4, 16, 16, 16), 64, 8, 8, torch.float32),
+          ((16, 8, 14, 14), 128, 1, 2, torch.bfloat16), ((16, 32, 14, 14), 128, 4, 4, torch.float16),
+          ((32, 16, 28, 28), 512, 2, 16, torch.bfloat16), ((32, 16, 28, 28), 512, 8, 64, torch.bfloat16),
+          ((32, 8, 7, 7), 64, 4, 4, torch.bfloat16), ((32, 8, 5, 10), 64, 2, 1, torch.bfloat16),
+          ((16, 16, 28, 28), 256, 1, 4, torch.bfloat16)]
+
+
+@pytest.mark.parametrize("case", ACASES, ids=lambda c: "x".join(map(str, c[0])) + f"-B{c[1]}-b{c[2]}-A{c[3]}")
+def test_alam_forward_and_backward(case):
+    """avg_alam=True through the reference's three squashed operators against the oracle: y, mean
+    and var bit for bit; codes (runs' truncated means of tanh-squashed arguments) within one step on
+    under 1% of the runs, scale / min within one bf16 ulp; the reduce (codes plus tl.rand noise)
+    within the fp32 summation bound; dx on the GPU's codes bit for bit."""
+    shape, BLOCK, bits, alam, dtype = case
+    x, w, b = make(shape, dtype, 300 + bits + alam)
+    N, C = shape[0], shape[1]
+    g = geo(x)
+    x3 = x.to(DEV).view(N, C, -1)
+    wd, bd = w.to(DEV), b.to(DEV)
+    s, q = ops.bn_fwd_reduce(x3, **g, BLOCK_M=BLOCK, num_warps=8, num_stages=5)
+    y, packed, scale, xmin, mean, var = ops.bn_fwd_norm_quant_pack_fused(
+        x3, s, q, wd, bd, None, None, **g, BLOCK_M=BLOCK, bits=bits, sync=False, avg_alam=True, alam_bits=alam,
+        num_warps=8, num_stages=5)
+    torch.cuda.synchronize()
+    grp = BLOCK // 2
+    M = g["M"]
+    assert tuple(packed.shape) == (C, M * bits // 32 // alam)
+    ref = oracle.bn_norm_quant(npv(x), w.numpy(), b.numpy(), mode=oracle.BN_QUANT, group_size=grp, bits=bits,
+                               eps=1e-5, sum=npv(s), sumsq=npv(q), alam_bits=alam)
+    np.testing.assert_array_equal(npv(mean), ref["mean"])
+    np.testing.assert_array_equal(npv(var), ref["var"])
+    np.testing.assert_array_equal(npv(y).reshape(-1), ref["y"].reshape(-1))
+    d = np.abs(codes_of(npv(packed), bits) - codes_of(ref["packed"], bits))
+    assert d.max() <= 1 and (d > 0).mean() < 0.01
+    for a, r in ((npv(scale), ref["scale"]), (npv(xmin), ref["min"])):
+        assert np.abs(a.astype(np.int64) - r.astype(np.int64)).max() <= 1
+
+    dy = torch.randn(shape, generator=torch.Generator().manual_seed(8)).to(torch.bfloat16)
+    dy3 = dy.to(DEV).view(N, C, -1)
+    dw, db = ops.bn_bwd_reduce_dequant_unpack_fused(packed, dy3, scale, xmin, **g, BLOCK_M=BLOCK, bits=bits,
+                                                    avg_alam=True, alam_bits=alam)
+    dx = ops.bn_bwd_dx_dequant_unpack_fused(packed, dy3, scale, xmin, dw, db, wd, var, **g, BLOCK_M=BLOCK,
+                                            bits=bits, sync=False, avg_alam=True, alam_bits=alam)
+    torch.cuda.synchronize()
+    kw = dict(mode=oracle.BN_QUANT, packed=npv(packed), scale=npv(scale), min=npv(xmin), group_size=grp, bits=bits,
+              alam_bits=alam)
+    rdw, rdb = oracle.bn_bwd_reduce(npv(dy), **kw)
+    dyf = np.abs(oracle.bf16_bits_to_f32(npv(dy))).astype(np.float64)
+    assert sums_close(npv(db), rdb, dyf.sum(axis=(0, 2, 3)))
+    assert sums_close(npv(dw), rdw, 8.0 * dyf.sum(axis=(0, 2, 3)))  # |x_hat'| < 8 for this data
+    rdx = oracle.bn_bwd_dx(npv(dy), npv(dw), npv(db), w.numpy(), npv(var), eps=1e-7, **kw)
+    np.testing.assert_array_equal(npv(dx).reshape(-1), rdx.reshape(-1))
 
 
 # ----------------------------------------------------------------------------- layers
@@ -264,6 +324,28 @@ def test_do_batchnorm2d_layer(act_padding):
     y.backward(dy)
     assert layer.weight.grad.dtype == torch.float32 and torch.isfinite(x.grad).all()
     # the gradient follows the saved, squashed and quantized x_hat: close to exact BN's in direction
+    xr = x.detach().float().requires_grad_(True)
+    ref.zero_grad()
+    ref(xr).backward(dy.float())
+    cos = torch.nn.functional.cosine_similarity(x.grad.float().flatten(), xr.grad.flatten(), dim=0)
+    assert cos > 0.9, float(cos)
+    torch.testing.assert_close(layer.bias.grad, ref.bias.grad, rtol=1e-3, atol=1e-3)
+
+
+def test_do_batchnorm2d_layer_avg_alam():
+    """The layer with the per-layer meta AVG_ALAM (the Controller sets it from its config for
+    BatchNorm layers, controller.py:179-187): the reference's operator path with runs of 2."""
+    shape = (8, 16, 28, 28)
+    layer, ref, x, meta = _layer_case(DOBatchNorm2d, shape, 256)
+    meta["bn"].update({"AVG_ALAM": True, "ALAM_BITS": 2})
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        y = layer(x)
+    yr = ref(x.detach().float().requires_grad_(True))
+    torch.testing.assert_close(y.float(), yr, rtol=2 ** -7, atol=2e-2)
+    torch.testing.assert_close(layer.running_mean, ref.running_mean, rtol=1e-5, atol=1e-6)
+    dy = torch.randn_like(y)
+    y.backward(dy)
+    assert torch.isfinite(x.grad).all() and torch.isfinite(layer.weight.grad).all()
     xr = x.detach().float().requires_grad_(True)
     ref.zero_grad()
     ref(xr).backward(dy.float())
@@ -414,3 +496,25 @@ def test_layer_operator_opcheck():
     dy = torch.randn(xd.shape, device=DEV).to(torch.bfloat16)
     torch.library.opcheck(ops.bn_train_bwd.default, (packed, rp, dy, scale, mn, w.to(DEV), var, BLOCK, 2,
                                                      _lib.BN_RELU_QUANT), test_utils=tests)
+
+
+def test_alam_operator_opcheck():
+    """The squashed operators with avg_alam: fake kernels give the [C, M*bits/32/alam_bits] codes."""
+    shape, BLOCK = (4, 16, 16, 16), 256
+    x, w, b = make(shape, torch.bfloat16, 3)
+    xd = x.to(DEV).view(4, 16, -1)
+    g = geo(x)
+    tests = ("test_schema", "test_faketensor", "test_aot_dispatch_static", "test_aot_dispatch_dynamic")
+    s, q = ops.bn_fwd_reduce(xd, **g, BLOCK_M=BLOCK, num_warps=8, num_stages=5)
+    kw = dict(**g, BLOCK_M=BLOCK, bits=2, sync=False, avg_alam=True, alam_bits=4, num_warps=8, num_stages=5)
+    torch.library.opcheck(ops.bn_fwd_norm_quant_pack_fused.default, (xd, s, q, w.to(DEV), b.to(DEV), None, None),
+                          kw, test_utils=tests)
+    y, packed, scale, mn, mean, var = ops.bn_fwd_norm_quant_pack_fused(xd, s, q, w.to(DEV), b.to(DEV), None, None,
+                                                                       **kw)
+    dy = torch.randn(xd.shape, device=DEV).to(torch.bfloat16)
+    bk = dict(**g, BLOCK_M=BLOCK, bits=2, avg_alam=True, alam_bits=4)
+    torch.library.opcheck(ops.bn_bwd_reduce_dequant_unpack_fused.default, (packed, dy, scale, mn), bk,
+                          test_utils=tests)
+    dw, db = ops.bn_bwd_reduce_dequant_unpack_fused(packed, dy, scale, mn, **bk)
+    torch.library.opcheck(ops.bn_bwd_dx_dequant_unpack_fused.default, (packed, dy, scale, mn, dw, db, w.to(DEV), var),
+                          dict(bk, sync=False), test_utils=tests)

@@ -111,6 +111,20 @@ class TestValidationWithoutDevice:
         msg = L.dopt_last_error().decode()
         assert "scratch" in msg and "1048576" in msg, msg
 
+    def test_bn_alam_rejects_run_lengths_the_reference_cannot_reshape(self):
+        L = _lib.lib()
+        N, C, HW = 4, 2, 64  # groups of 64 at 2 bits: 4 code words per group
+        for alam in (0, 3, 8):  # not a power of two dividing 4
+            rc = L.dopt_bn_norm_quant_alam(16, _lib.BF16, N, C, HW, C * HW, HW, 16, 16, None, None, 0, 16, 16, 1e-5,
+                                           64, 2, alam, 16, 16, 16, 16, 16, 16, None)
+            assert rc == _lib.EINVAL and "alam_bits" in L.dopt_last_error().decode()
+            assert L.dopt_bn_bwd_reduce_alam(16, 16, 16, 16, _lib.BF16, N, C, HW, C * HW, HW, 64, 2, alam, 16, 16,
+                                             16, None) == _lib.EINVAL
+            assert L.dopt_bn_bwd_dx_alam(16, 16, 16, 16, _lib.BF16, N, C, HW, C * HW, HW, 64, 2, alam, 16, 16, 16,
+                                         16, 1e-7, 0, 16, None) == _lib.EINVAL
+        assert L.dopt_bn_norm_quant_alam(16, _lib.BF16, N, C, HW, C * HW, HW, 16, 16, None, None, 0, 16, 16, 1e-5,
+                                         64, 3, 2, 16, 16, 16, 16, 16, 16, None) == _lib.EBITS
+
     def test_valu_probe_argument_checks(self):
         L = _lib.lib()
         assert L.dopt_valu_probe(9, 16, 8, None) == _lib.EINVAL  # unknown kind

@@ -9,7 +9,11 @@ of the HIP kernels.
     value lying near a rounding boundary; the packed words from numpy.packbits;
   * the squashed mode equals the already pinned quantizer (oracle_quant_pack, nearest, bf16
     scale/min) applied per channel to the values it quantizes;
-  * the ReLU modes' division form keeps |x_hat' - x_hat| <= scale/2 and is monotone.
+  * the ReLU modes' division form keeps |x_hat' - x_hat| <= scale/2 and is monotone;
+  * avg_alam: alam_bits = 1 keeps the plain codes, runs of equal values give the plain codes,
+    codes are the floor of the runs' mean code argument (float64 from the pinned t), the input
+    gradient is the plain one on repeated codes and the reduce adds the Philox-derived tl.rand
+    noise.
 """
 import numpy as np
 import pytest
@@ -184,3 +188,146 @@ def test_relu_backward_masks_dy():
                           mode=oracle.BN_RELU_QUANT, eps=1e-5, packed=out["packed"], relu_packed=out["relu_packed"],
                           scale=out["scale"], min=out["min"], group_size=32, bits=2)
     assert not np.any(bf16(dx))
+
+
+# ----------------------------------------------------------------------------- avg_alam
+def _codes(packed, bits):
+    """codes of a little-endian code bitstream (numpy.unpackbits)"""
+    b = np.unpackbits(np.ascontiguousarray(packed).reshape(-1).view(np.uint8), bitorder="little")
+    return (b.reshape(-1, bits).astype(np.int64) << np.arange(bits)).sum(axis=1)
+
+
+def _philox_uniform(seed, off):
+    """tl.rand(seed, off) from the Philox words (pinned by the known-answer vectors): word 0 as
+    int32, folded to non-negative, times fp32(4.6566127342e-10)"""
+    ctr = np.array([off, 0, 0, 0], np.uint32)
+    key = np.array([seed & 0xFFFFFFFF, seed >> 32], np.uint32)
+    out = np.zeros(4, np.uint32)
+    oracle.lib().oracle_philox4x32_10(ctr.ctypes.data, key.ctypes.data, out.ctypes.data)
+    i = int(out[:1].view(np.int32)[0])
+    i = ~i if i < 0 else i
+    return float(np.float32(i) * np.float32(4.6566127342e-10))
+
+
+def test_triton_rand_is_the_first_philox_word_as_a_uniform():
+    for seed, off in [(42, 0), (42, 5), (43, 255), (42 + 7, 511), (2**33 + 1, 17)]:
+        assert oracle.triton_rand(seed, off) == _philox_uniform(seed, off)
+    u = np.array([oracle.triton_rand(42 + b, e) for b in range(16) for e in range(512)])
+    assert u.min() >= 0.0 and u.max() < 1.0
+    assert abs(u.mean() - 0.5) < 0.01 and abs(u.var() - 1.0 / 12.0) < 0.005
+
+
+@pytest.mark.parametrize("bits", [1, 2, 4, 8])
+def test_alam_one_keeps_the_plain_codes(bits):
+    x = rnd((4, 3, 8, 8), 60 + bits, scale=1.5)
+    C = 3
+    w, b = rnd((C,), 61), rnd((C,), 62)
+    s, q = stats32(x)
+    kw = dict(mode=oracle.BN_QUANT, group_size=64, bits=bits, eps=1e-5, sum=s, sumsq=q)
+    plain = oracle.bn_norm_quant(x, w, b, **kw)
+    one = oracle.bn_norm_quant(x, w, b, alam_bits=1, **kw)
+    for k in ("y", "packed", "scale", "min"):
+        np.testing.assert_array_equal(one[k], plain[k])
+
+
+@pytest.mark.parametrize("bits", [1, 2, 4, 8])
+def test_alam_two_on_pairs_of_equal_values(bits):
+    """Runs of two equal x_hat (sync path: x_hat = x): the mean of a pair of equal qf is that qf
+    exactly, so the codes are the plain mode's codes of every other element."""
+    x = np.repeat(rnd((1, 2, 128), 70 + bits, scale=1.2), 2, axis=2)  # [1, 2, 256], pairs of equal values
+    plain = _sync(x, bits, oracle.BN_QUANT, 256)
+    got = oracle.bn_norm_quant(x, np.ones(2, np.float32), np.zeros(2, np.float32), mode=oracle.BN_QUANT,
+                               group_size=256, bits=bits, mean=np.zeros(2, np.float32), invstd=np.ones(2, np.float32),
+                               alam_bits=2)
+    want = _codes(plain["packed"], bits).reshape(2, -1)[:, ::2]
+    np.testing.assert_array_equal(_codes(got["packed"], bits).reshape(2, -1), want)
+    np.testing.assert_array_equal(got["scale"], plain["scale"])
+    np.testing.assert_array_equal(got["min"], plain["min"])
+
+
+def _alam_case(bits, alam, seed, g=256):
+    x = rnd((4, 2, 16, 16), seed, scale=1.4, shift=0.2)
+    C = 2
+    w, b = rnd((C,), seed + 1) + 1.0, rnd((C,), seed + 2)
+    s, q = stats32(x)
+    kw = dict(mode=oracle.BN_QUANT, group_size=g, bits=bits, eps=1e-5, sum=s, sumsq=q)
+    return x, w, b, oracle.bn_norm_quant(x, w, b, **kw), oracle.bn_norm_quant(x, w, b, alam_bits=alam, **kw)
+
+
+@pytest.mark.parametrize("bits,alam", [(1, 2), (2, 2), (2, 4), (4, 8), (8, 16), (8, 64)])
+def test_alam_codes_are_the_truncated_run_means(bits, alam):
+    """Each code is floor of the mean of its run's code arguments qf = (t - min) / scale + 0.5 - 1e-6,
+    worked out in float64 from the pinned t, min and scale; runs whose mean lies within 1e-4 of an
+    integer are left out (fp32 summation order)."""
+    g = 256
+    _, _, _, plain, got = _alam_case(bits, alam, 80 + bits + alam, g)
+    t = plain["t"].astype(np.float64).reshape(-1, g)
+    mn = t.min(axis=1, keepdims=True)
+    qmax = (1 << bits) - 1
+    step = (t.max(axis=1, keepdims=True) - mn) / qmax
+    qf = (t - mn) / step + (0.5 - 1e-6)
+    mean = qf.reshape(-1, g // alam, alam).mean(axis=2)
+    want = np.clip(np.floor(mean), 0, qmax)
+    codes = _codes(got["packed"], bits).reshape(want.shape)
+    far = np.abs(mean - np.round(mean)) > 1e-4
+    assert far.mean() > 0.95
+    np.testing.assert_array_equal(codes[far], want[far])
+    np.testing.assert_array_equal(got["scale"], plain["scale"])
+    np.testing.assert_array_equal(got["min"], plain["min"])
+    assert got["packed"].shape == (2, 4 * 256 * bits // 32 // alam)
+
+
+def _repeat_codes(packed, bits, alam):
+    """the plain layout of avg_alam codes: every code written alam times"""
+    return _packbits(np.repeat(_codes(packed, bits), alam).astype(np.uint32), bits).reshape(packed.shape[0], -1)
+
+
+@pytest.mark.parametrize("bits,alam", [(2, 2), (4, 4), (8, 16)])
+def test_alam_backward_is_the_plain_backward_of_repeated_codes(bits, alam):
+    """dx with avg_alam is the plain mode's dx on the codes repeated alam times (no noise, bit for
+    bit); the reduce adds q + (tl.rand(42 + e / (2 g), e mod g) - 0.5) per element: its dbias is the
+    plain one and its dweight the float64 sum of dy * fma(q + noise, scale, min) with the noise
+    from the Philox words."""
+    g = 256
+    x, w, b, _, fw = _alam_case(bits, alam, 90 + bits, g)
+    dy = rnd(x.shape, 91 + bits)
+    rep = _repeat_codes(fw["packed"], bits, alam)
+    kw = dict(mode=oracle.BN_QUANT, scale=fw["scale"], min=fw["min"], group_size=g, bits=bits)
+    dw_p, db_p = oracle.bn_bwd_reduce(dy, packed=rep, **kw)
+    dw_a, db_a = oracle.bn_bwd_reduce(dy, packed=fw["packed"], alam_bits=alam, **kw)
+    np.testing.assert_array_equal(db_a, db_p)
+    C, M = 2, 4 * 256
+    q = _codes(rep, bits).reshape(C, M).astype(np.float32)
+    e = np.arange(M)
+    u = np.array([_philox_uniform(42 + int(k) // (2 * g), int(k) % g) for k in e], dtype=np.float32)
+    qn = q + (u - np.float32(0.5))[None, :]
+    sc = np.repeat(bf16(fw["scale"]), g, axis=1)
+    mn = np.repeat(bf16(fw["min"]), g, axis=1)
+    xq = qn.astype(np.float64) * sc + mn
+    dyc = dy.transpose(1, 0, 2, 3).reshape(C, M).astype(np.float64)
+    want = (dyc * xq).sum(axis=1)
+    assert np.all(np.abs(dw_a - want) <= 1e-6 * (np.abs(dyc) * np.abs(xq)).sum(axis=1))
+    assert np.all(np.abs(dw_a - dw_p) > 0)  # the noise changes dweight
+    args = (dw_a.astype(np.float32), db_a.astype(np.float32), w, fw["var"])
+    dx_p = oracle.bn_bwd_dx(dy, *args, packed=rep, eps=1e-7, **kw)
+    dx_a = oracle.bn_bwd_dx(dy, *args, packed=fw["packed"], alam_bits=alam, eps=1e-7, **kw)
+    np.testing.assert_array_equal(dx_a, dx_p)
+
+
+def test_alam_rejects_run_lengths_the_reference_cannot_reshape():
+    x = rnd((2, 1, 8, 8), 99)
+    w, b = np.ones(1, np.float32), np.zeros(1, np.float32)
+    s, q = stats32(x)
+    for alam in (3, 4):  # g = 64, 2 bits: 4 code words; 3 is no power of two, 4 divides them
+        kw = dict(mode=oracle.BN_QUANT, group_size=64, bits=2, eps=1e-5, sum=s, sumsq=q, alam_bits=alam)
+        if alam == 3:
+            with pytest.raises(RuntimeError):
+                oracle.bn_norm_quant(x, w, b, **kw)
+        else:
+            oracle.bn_norm_quant(x, w, b, **kw)
+    with pytest.raises(RuntimeError):  # 8 does not divide 4 words
+        oracle.bn_norm_quant(x, w, b, mode=oracle.BN_QUANT, group_size=64, bits=2, eps=1e-5, sum=s, sumsq=q,
+                             alam_bits=8)
+    with pytest.raises(RuntimeError):  # avg_alam is a squashed-mode option
+        oracle.bn_norm_quant(x, w, b, mode=oracle.BN_RELU_QUANT, group_size=64, bits=2, eps=1e-5, sum=s, sumsq=q,
+                             alam_bits=2)
