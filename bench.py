@@ -40,6 +40,7 @@ if ROOT not in sys.path:
 HBM_PEAK_GBS = 8000.0
 FP8_PEAK_TFLOPS = 5000.0
 BF16_PEAK_TFLOPS = 2500.0
+SETTLE_S = 0.025  # sustained-load warm-up before every timed extra (seconds of wall time)
 METRIC = "quant-pack+unpack GB/s (% HBM peak) at 2-bit; FP8 GEMM TFLOPS (% peak)"
 PMC_SUMMARY = os.path.join(ROOT, "profiles", "quant_pack_resnet_noise_pmc.md")
 N, C, H, W = 256, 256, 56, 56
@@ -170,7 +171,10 @@ def fp8_probe(mode: str) -> int:
 def counter_probe(name: str) -> int:
     """One kernel below 70% of HBM peak, 3 + 10 launches, for rocprofv3 --pmc runs (instruction mix,
     VALU activity, HBM bytes): "philox" / "nearest" = the config-2 quant-pack (bf16 [256,256,56,56]
-    |N(0,1)|, g = 256, 2-bit); "gelu" / "silu" = the fused activation forward on the ViT MLP
+    |N(0,1)|, g = 256, 2-bit); "vit_philox" / "vit_unpack" = the config-3 2-bit Philox quant-pack
+    and its unpack-dequant (GELU(N(0,1)) bf16 [256,197,3072], g = 128), "vit_step" both in turn
+    (the config-3 step); "gelu" / "silu" = the
+    fused activation forward on the ViT MLP
     activation (bf16 [256,197,3072] N(0,1), g = 128, 2-bit); "bn_squash" / "bn_relu" = the
     BatchNorm normalize + quant-pack forward on the ResNet stage-1 activation (bf16
     [256,256,56,56], g = 512, 2-bit)."""
@@ -185,6 +189,17 @@ def counter_probe(name: str) -> int:
         x = torch.randn((256, 256, 56, 56), generator=gen, device=dev).abs_().to(torch.bfloat16).view(256, -1, G_SIZE)
         rn = PHILOX if name == "philox" else NEAREST
         fn = lambda: ops.quant_pack(x, BITS, G_SIZE, False, 0.0, False, rn, None, 1, 0, torch.float32)  # noqa: E731
+    elif name in ("vit_philox", "vit_unpack", "vit_step"):
+        v = torch.nn.functional.gelu(torch.randn((256, 197, 3072), generator=gen, device=dev)).to(torch.bfloat16)
+        vgrp = v.view(256, -1, 128)
+        pk = lambda: ops.quant_pack(vgrp, 2, 128, False, 0.0, False, PHILOX, None, 1, 0, torch.float32)  # noqa: E731
+        if name == "vit_philox":
+            fn = pk
+        elif name == "vit_step":
+            fn = lambda: ops.dequant_unpack(*pk(), 2, 128, torch.bfloat16)  # noqa: E731
+        else:
+            p_, s_, m_ = pk()
+            fn = lambda: ops.dequant_unpack(p_, s_, m_, 2, 128, torch.bfloat16)  # noqa: E731
     elif name in ("gelu", "silu"):
         v = torch.randn((256, 197, 3072), generator=gen, device=dev).to(torch.bfloat16)
         if name == "gelu":
@@ -620,7 +635,8 @@ def main() -> int:
     ap.add_argument("--dw-tokens", default=None)
     ap.add_argument("--valu-probe", action="store_true")
     ap.add_argument("--host-probe", action="store_true")
-    ap.add_argument("--counter-probe", choices=("philox", "nearest", "gelu", "silu", "bn_squash", "bn_relu"))
+    ap.add_argument("--counter-probe", choices=("philox", "nearest", "vit_philox", "vit_unpack", "vit_step", "gelu",
+                                                "silu", "bn_squash", "bn_relu"))
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}). "
@@ -659,9 +675,21 @@ def main() -> int:
                                  1, 0, torch.float32)
         return ops.dequant_unpack(p, s, m, BITS, G_SIZE, torch.bfloat16)
 
-    def time_steps(fn, steps, warmup):
+    def settle(fn, seconds):
+        """Run fn until `seconds` of wall time have passed, so that the part's clocks have left the
+        state an idle gap leaves them in (the way Triton's do_bench warms up for 25 ms): a 2-5 ms
+        timing window right after one measured a VALU-heavy pack up to 25% slower than the same
+        kernel under sustained load."""
+        t0 = time.perf_counter()
+        while seconds > 0 and time.perf_counter() - t0 < seconds:
+            for _ in range(4):
+                fn()
+            torch.cuda.synchronize()
+
+    def time_steps(fn, steps, warmup, warm_s=SETTLE_S):
         for _ in range(warmup):
             fn()
+        settle(fn, warm_s)
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         for _ in range(steps):
@@ -669,7 +697,7 @@ def main() -> int:
         torch.cuda.synchronize()
         return (time.perf_counter() - t0) / steps
 
-    sec = time_steps(lambda: step(NOISE), args.steps, args.warmup)
+    sec = time_steps(lambda: step(NOISE), args.steps, args.warmup, warm_s=0.0)  # the contract: W warm-up steps
     pb_noise = pack_bytes(n_elem, n_groups, 2, BITS, noise=True)
     ub = unpack_bytes(n_elem, n_groups, 2, BITS)
     rt_bytes = pb_noise + ub
@@ -697,6 +725,7 @@ def main() -> int:
     def event_avg(fn, reps=max(args.steps, 10)):
         for _ in range(3):
             fn()
+        settle(fn, SETTLE_S)
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record(stream)
         for _ in range(reps):
