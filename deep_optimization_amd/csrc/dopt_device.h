@@ -2,8 +2,8 @@
 //
 // Wave model: CDNA4 wavefronts are 64 lanes. A group of `group_size` values is spread over LPG
 // consecutive lanes (LPG a power of two, aligned), so every cross-lane reduction stays inside an
-// aligned LPG-lane block and is done with DPP lane permutes (no LDS round trip) up to 16 lanes,
-// and with ds_bpermute-based shuffles beyond that.
+// aligned LPG-lane block and is done with DPP lane permutes folded into the min/max (no LDS
+// round trip) up to 16 lanes, and with v_permlane16/32_swap beyond that.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -32,37 +32,6 @@ __device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
 template <int CTRL>
 __device__ __forceinline__ float dpp_f32(float v) {
     return __uint_as_float(dpp_u32<CTRL>(__float_as_uint(v)));
-}
-
-// All-reduce min and max over aligned blocks of LPG lanes. After the first two steps every lane
-// of a quad holds the quad's result, so the mirror permutes (which pair lane i with 7-i / 15-i)
-// combine exactly the two halves of the 8- and 16-lane blocks.
-template <int LPG>
-__device__ __forceinline__ void block_minmax(float& mn, float& mx) {
-    if constexpr (LPG >= 2) {
-        mn = fminf(mn, dpp_f32<0xB1>(mn));
-        mx = fmaxf(mx, dpp_f32<0xB1>(mx));
-    }
-    if constexpr (LPG >= 4) {
-        mn = fminf(mn, dpp_f32<0x4E>(mn));
-        mx = fmaxf(mx, dpp_f32<0x4E>(mx));
-    }
-    if constexpr (LPG >= 8) {
-        mn = fminf(mn, dpp_f32<0x141>(mn));
-        mx = fmaxf(mx, dpp_f32<0x141>(mx));
-    }
-    if constexpr (LPG >= 16) {
-        mn = fminf(mn, dpp_f32<0x140>(mn));
-        mx = fmaxf(mx, dpp_f32<0x140>(mx));
-    }
-    if constexpr (LPG >= 32) {
-        mn = fminf(mn, __shfl_xor(mn, 16, 64));
-        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-    }
-    if constexpr (LPG >= 64) {
-        mn = fminf(mn, __shfl_xor(mn, 32, 64));
-        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    }
 }
 
 // Raw v_min/v_max (and 3-operand forms): no NaN canonicalisation of the operands, which fminf /

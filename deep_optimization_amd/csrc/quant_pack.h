@@ -110,20 +110,20 @@ __device__ __forceinline__ uint64_t group_elem_index(const QuantPackArgs& a, uin
 template <int LPG>
 __device__ __forceinline__ void group_minmax(float& mn, float& mx) {
     if constexpr (LPG >= 2) {
-        mn = vmin(mn, dpp_f32<0xB1>(mn));
-        mx = vmax(mx, dpp_f32<0xB1>(mx));
+        mn = vmin_dpp<0xB1>(mn);
+        mx = vmax_dpp<0xB1>(mx);
     }
     if constexpr (LPG >= 4) {
-        mn = vmin(mn, dpp_f32<0x4E>(mn));
-        mx = vmax(mx, dpp_f32<0x4E>(mx));
+        mn = vmin_dpp<0x4E>(mn);
+        mx = vmax_dpp<0x4E>(mx);
     }
     if constexpr (LPG >= 8) {
-        mn = vmin(mn, dpp_f32<0x141>(mn));
-        mx = vmax(mx, dpp_f32<0x141>(mx));
+        mn = vmin_dpp<0x141>(mn);
+        mx = vmax_dpp<0x141>(mx);
     }
     if constexpr (LPG >= 16) {
-        mn = vmin(mn, dpp_f32<0x140>(mn));
-        mx = vmax(mx, dpp_f32<0x140>(mx));
+        mn = vmin_dpp<0x140>(mn);
+        mx = vmax_dpp<0x140>(mx);
     }
     if constexpr (LPG >= 32) swap_minmax<16>(mn, mx);
     if constexpr (LPG >= 64) swap_minmax<32>(mn, mx);
