@@ -34,6 +34,7 @@ EXPORTS = (
     "dopt_act_forward",
     "dopt_act_quant_pack",
     "dopt_act_dequant_mul",
+    "dopt_act_dequant_mul_alam",
     "dopt_bn_workspace_floats",
     "dopt_bn_reduce",
     "dopt_bn_norm_quant",
@@ -101,6 +102,8 @@ def lib() -> ctypes.CDLL:
         L.dopt_act_quant_pack.restype = i32
         L.dopt_act_dequant_mul.argtypes = [vp, vp, vp, i32, i64, i32, i32, vp, vp, i32, vp, vp]
         L.dopt_act_dequant_mul.restype = i32
+        L.dopt_act_dequant_mul_alam.argtypes = [vp, vp, vp, i32, i64, i32, i32, vp, vp, i32, u64, vp, vp]
+        L.dopt_act_dequant_mul_alam.restype = i32
         L.dopt_bn_workspace_floats.argtypes = [i64, i64, i64]
         L.dopt_bn_workspace_floats.restype = i64
         L.dopt_bn_reduce.argtypes = [vp, i32, i64, i64, i64, i64, i64, vp, vp, vp, vp]

@@ -261,16 +261,17 @@ dequant_unpack_tiles = _op(
 ALAM_SEED = 42  # the reference operators' fixed seed (act_triton_kernel.py:339, :374)
 
 
-def _no_alam(avg_alam: bool, where: str) -> None:
-    """The SiLU operators' avg_alam mode is not built: the reference's forward kernel reshapes the
-    group's G codes to G / alam_bits before packing (activations/kernel_implementation.py:330),
-    which Triton rejects for alam_bits >= 2, and with alam_bits = 1 the mode only adds tl.rand
-    noise to the codes in the backward (:382-390). The quantizer and BatchNorm operators support it."""
-    if avg_alam:
+def _silu_alam(avg_alam: bool, alam_bits: int, where: str) -> bool:
+    """The SiLU operators' avg_alam mode exists at alam_bits = 1 only: the reference's forward
+    kernel reshapes the group's G codes to G / alam_bits before packing
+    (activations/kernel_implementation.py:330), which Triton rejects for alam_bits >= 2. At
+    alam_bits = 1 the codes are the plain ones and the backward adds tl.rand noise (:382-390).
+    Returns whether the backward adds that noise."""
+    if avg_alam and alam_bits != 1:
         raise NotImplementedError(
-            f"{where}: avg_alam=True is not implemented for the SiLU operators (the reference's forward "
-            "kernel cannot reshape the codes for alam_bits >= 2; the quantizer and BatchNorm operators "
-            "support avg_alam)")
+            f"{where}: avg_alam=True with alam_bits={alam_bits}: the reference's SiLU forward kernel cannot "
+            "reshape the codes for alam_bits >= 2 (alam_bits = 1 is supported)")
+    return bool(avg_alam)
 
 
 def _alam_words(bits: int, group_size: int, alam_bits: int) -> int:
@@ -603,7 +604,7 @@ def _act_quant_pack_launch(x, act, n_groups, bits, group_size, tile):
     return y, packed, scale, xmin
 
 
-def _act_dequant_mul_launch(packed, dy, scale, xmin, n_groups, bits, group_size, tile):
+def _act_dequant_mul_launch(packed, dy, scale, xmin, n_groups, bits, group_size, tile, alam_seed=None):
     _bits_consts(bits, group_size)
     if dy.dtype not in (torch.bfloat16, torch.float32):
         raise RuntimeError(f"fused activation backward: dy must be bfloat16 or float32, got {dy.dtype}")
@@ -623,9 +624,16 @@ def _act_dequant_mul_launch(packed, dy, scale, xmin, n_groups, bits, group_size,
     if tile is not None:
         import ctypes
         tile_arr = (ctypes.c_int64 * 4)(*tile)
-    rc = _lib.lib().dopt_act_dequant_mul(packed.data_ptr(), scale.contiguous().data_ptr(), xmin.contiguous().data_ptr(),
-                                         _META_CODE[scale.dtype], n_groups, group_size, bits, tile_arr, dy.data_ptr(),
-                                         _DTYPE_CODE[dy.dtype], dx.data_ptr(), _stream(dy))
+    if alam_seed is None:
+        rc = _lib.lib().dopt_act_dequant_mul(packed.data_ptr(), scale.contiguous().data_ptr(),
+                                             xmin.contiguous().data_ptr(), _META_CODE[scale.dtype], n_groups,
+                                             group_size, bits, tile_arr, dy.data_ptr(), _DTYPE_CODE[dy.dtype],
+                                             dx.data_ptr(), _stream(dy))
+    else:
+        rc = _lib.lib().dopt_act_dequant_mul_alam(packed.data_ptr(), scale.contiguous().data_ptr(),
+                                                  xmin.contiguous().data_ptr(), _META_CODE[scale.dtype], n_groups,
+                                                  group_size, bits, tile_arr, dy.data_ptr(), _DTYPE_CODE[dy.dtype],
+                                                  alam_seed, dx.data_ptr(), _stream(dy))
     _lib.check(rc, "act_dequant_mul")
     return dx
 
@@ -679,7 +687,7 @@ def _silu_fwd_quan_pack(x, bits, group_size, avg_alam, alam_bits, pack_only):
     """-> (bf16 y shaped like x, packed, bf16 scale [N*G], bf16 min [N*G], N, G, new_H, new_W,
     padding eligibility, reshape eligibility) (kernel_registration.py:148-198); the spatial-tile
     grouping is read and written in place."""
-    _no_alam(avg_alam, "silu_fwd_quan_pack")
+    _silu_alam(avg_alam, alam_bits, "silu_fwd_quan_pack")  # alam_bits = 1: the plain codes
     N, G, nh, nw, pad_e, rs_e, tile = _silu_layout(x, group_size)
     y, packed, scale, xmin = _act_quant_pack_launch(x, ACT_SILU, N * G, bits, group_size, tile)
     return y, packed, scale, xmin, N, G, nh, nw, pad_e, rs_e
@@ -701,10 +709,12 @@ silu_fwd_quan_pack = _op(
 
 def _silu_bwd_fused_dequan_unpack(packed, dy, scale, min, bits, N, G, group_size, pack_only, new_H, new_W,
                                   spatical_padding_eligibility, spatical_reshape_eligibility, avg_alam, alam_bits):
-    """-> bf16 dx = dy * dequant(packed), shaped like dy (kernel_registration.py:202-237)."""
-    _no_alam(avg_alam, "silu_bwd_fused_dequan_unpack")
+    """-> bf16 dx = dy * dequant(packed), shaped like dy (kernel_registration.py:202-237); with
+    avg_alam (alam_bits = 1) the codes carry tl.rand(42 + group, element) - 0.5 (seed 42, :208)."""
+    noise = _silu_alam(avg_alam, alam_bits, "silu_bwd_fused_dequan_unpack")
     tile = tuple(int(v) for v in dy.shape) if spatical_reshape_eligibility else None
-    return _act_dequant_mul_launch(packed, dy, scale, min, N * G, bits, group_size, tile)
+    return _act_dequant_mul_launch(packed, dy, scale, min, N * G, bits, group_size, tile,
+                                   ALAM_SEED if noise else None)
 
 
 silu_bwd_fused_dequan_unpack = _op(

@@ -15,6 +15,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "dequant_unpack.h"
 #include "dopt_device.h"
 
 namespace dopt {
@@ -135,7 +136,55 @@ __global__ __launch_bounds__(256) void alam_dequant_kernel(AlamDqArgs a) {
     a.y[i] = to_bf16(__builtin_fmaf(qf, bf16_bits_to_f32(a.scale[r]), bf16_bits_to_f32(a.minv[r])));
 }
 
+// The SiLU backward with avg_alam at alam_bits = 1 (activations/kernel_implementation.py:376-400,
+// kernel_registration.py:201-237): the plain codes plus Triton's tl.rand(seed + group, e) - 0.5,
+// dx = bf16(dy * fma(code + noise, scale, min)); one lane per element, the group's element e at
+// the flat or spatial-tile position of the plain operators. The mode has no other user, so the
+// kernel is plain: Philox per element costs ~60 instructions.
+struct AlamDyArgs {
+    DequantArgs d;
+    int g, bits, dy_f32;
+    uint64_t seed;
+    int64_t total;
+};
+
+__device__ __forceinline__ uint64_t alam_elem_index(const DequantArgs& a, uint32_t r, uint32_t e, int g) {
+    if (!a.tiled) return (uint64_t)r * (uint32_t)g + e;
+    const uint32_t band = r / a.tiles_w;
+    const uint32_t tw = r - band * a.tiles_w;
+    const uint32_t smask = (1u << a.log2s) - 1u;
+    return (((uint64_t)band * a.row) << a.log2s) + ((uint64_t)tw << a.log2s) + (uint64_t)(e >> a.log2s) * a.row +
+           (e & smask);
+}
+
+__global__ __launch_bounds__(256) void alam_act_dequant_mul_kernel(AlamDyArgs a) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= a.total) return;
+    const uint32_t r = (uint32_t)(i / a.g), e = (uint32_t)(i - (int64_t)r * a.g);
+    const int vpw = 32 / a.bits, nw = a.g / vpw;
+    const uint32_t q =
+        (a.d.packed[(int64_t)r * nw + e / vpw] >> ((e % vpw) * a.bits)) & ((1u << a.bits) - 1u);
+    float sc, mn;
+    if (a.d.meta_bf16) {
+        sc = bf16_bits_to_f32(((const uint16_t*)a.d.scale)[r]);
+        mn = bf16_bits_to_f32(((const uint16_t*)a.d.minv)[r]);
+    } else {
+        sc = ((const float*)a.d.scale)[r];
+        mn = ((const float*)a.d.minv)[r];
+    }
+    const float act = __builtin_fmaf((float)q + (triton_rand(a.seed + r, e) - 0.5f), sc, mn);
+    const uint64_t o = alam_elem_index(a.d, r, e, a.g);
+    const float dy = a.dy_f32 ? ((const float*)a.d.dy)[o] : bf16_bits_to_f32(((const uint16_t*)a.d.dy)[o]);
+    ((uint16_t*)a.d.y)[o] = to_bf16(dy * act);
+}
+
 }  // namespace
+
+int launch_alam_act_dequant_mul(const DequantArgs& d, int g, int bits, int dy_f32, uint64_t seed, hipStream_t s) {
+    const AlamDyArgs a{d, g, bits, dy_f32, seed, (int64_t)d.n_groups * g};
+    hipLaunchKernelGGL(alam_act_dequant_mul_kernel, dim3((unsigned)((a.total + 255) / 256)), dim3(256), 0, s, a);
+    return 0;
+}
 
 int launch_alam_quant_pack(const void* x, int dt, int64_t n_groups, int g, int bits, int alam, int flags,
                            float clamp_alpha, uint32_t* packed, uint16_t* scale, uint16_t* minv, hipStream_t s) {

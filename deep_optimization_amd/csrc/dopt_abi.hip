@@ -29,6 +29,7 @@ int launch_alam_quant_pack(const void* x, int dt, int64_t n_groups, int g, int b
                            float clamp_alpha, uint32_t* packed, uint16_t* scale, uint16_t* minv, hipStream_t s);
 int launch_alam_dequant(const uint32_t* packed, const uint16_t* scale, const uint16_t* minv, int64_t n_groups,
                         int g, int bits, int alam, uint64_t seed, uint16_t* y, hipStream_t s);
+int launch_alam_act_dequant_mul(const DequantArgs& d, int g, int bits, int dy_f32, uint64_t seed, hipStream_t s);
 const char* launch_stream_mix(const void* x, const void* noise, void* codes, void* meta, uint64_t n_units, int bits,
                               hipStream_t s);
 }  // namespace dopt
@@ -518,6 +519,34 @@ int dopt_act_dequant_mul(const uint32_t* packed, const void* scale, const void* 
                                                        (hipStream_t)stream);
     if (rc) return fail(DOPT_EUNSUPPORTED, "no act_dequant_mul kernel for bits=%d g=%d", bits, group_size);
     return hip_status("act_dequant_mul launch");
+}
+
+int dopt_act_dequant_mul_alam(const uint32_t* packed, const void* scale, const void* minv, int meta_dtype,
+                              int64_t n_groups, int group_size, int bits, const int64_t* tile_nchw, const void* dy,
+                              int dy_dtype, uint64_t seed, void* dx, void* stream) {
+    int rc;
+    if ((rc = check_bits(bits))) return rc;
+    if ((rc = check_group(group_size))) return rc;
+    if (n_groups < 0 || n_groups >= (int64_t)1 << 31)
+        return fail(DOPT_EINVAL, "n_groups must be in [0, 2^31), got %lld", (long long)n_groups);
+    if (meta_dtype != DOPT_F32 && meta_dtype != DOPT_BF16)
+        return fail(DOPT_EINVAL, "scale/min dtype must be F32 or BF16, got code %d", meta_dtype);
+    if (dy_dtype != DOPT_F32 && dy_dtype != DOPT_BF16)
+        return fail(DOPT_EINVAL, "act_dequant_mul_alam: dy dtype must be F32 or BF16, got code %d", dy_dtype);
+    dopt::DequantArgs a{};
+    if ((rc = setup_tiles(tile_nchw, n_groups, group_size, &a.tiled, &a.tiles_w, &a.log2s, &a.row))) return rc;
+    if (n_groups == 0) return ok();
+    if (!packed || !scale || !minv || !dy || !dx) return fail(DOPT_EINVAL, "null pointer argument");
+    a.dy = dy;
+    a.packed = packed;
+    a.scale = scale;
+    a.minv = minv;
+    a.y = dx;
+    a.n_groups = (uint32_t)n_groups;
+    a.meta_bf16 = meta_dtype == DOPT_BF16;
+    (void)hipGetLastError();
+    dopt::launch_alam_act_dequant_mul(a, group_size, bits, dy_dtype == DOPT_F32, seed, (hipStream_t)stream);
+    return hip_status("act_dequant_mul_alam launch");
 }
 
 int64_t dopt_bn_workspace_floats(int64_t N, int64_t C, int64_t HW) {

@@ -221,6 +221,17 @@ int dopt_act_dequant_mul(const uint32_t* packed, const void* scale, const void* 
                          int group_size, int bits, const int64_t* tile_nchw, const void* dy, int dy_dtype, void* dx,
                          void* stream);
 
+/*
+ * dopt_act_dequant_mul with the SiLU backward's avg_alam noise at alam_bits = 1: dx = bf16(dy *
+ * fma(float(q) + (u - 0.5), scale, min)), u = Triton's tl.rand(seed + r, e) for element e of group
+ * r (Philox4x32-10 first word, counter (e, 0, 0, 0), key the low and high words of seed + r, as a
+ * uniform in [0, 1)); the reference passes seed 42. Replaces act_lib::silu_bwd_fused_dequan_unpack
+ * with avg_alam=True, alam_bits=1 (kernel_registration.py:201-237, kernel_implementation.py:376-400).
+ */
+int dopt_act_dequant_mul_alam(const uint32_t* packed, const void* scale, const void* minv, int meta_dtype,
+                              int64_t n_groups, int group_size, int bits, const int64_t* tile_nchw, const void* dy,
+                              int dy_dtype, uint64_t seed, void* dx, void* stream);
+
 /* ---------------------------------------------------------------- BatchNorm
  * An activation [N, C, HW] with element strides (stride_n, stride_c, 1): channel c is the flat
  * sequence e = n*HW + s of M = N*HW elements. Every element tensor of a call (x, y, x_hat, dy,

@@ -73,6 +73,8 @@ def lib():
         L.oracle_act_quant_pack.restype = i32
         L.oracle_act_dequant_mul.argtypes = [vp, vp, vp, i32, i64, i32, i32, vp, vp, i32, vp]
         L.oracle_act_dequant_mul.restype = i32
+        L.oracle_act_dequant_mul_alam.argtypes = [vp, vp, vp, i32, i64, i32, i32, vp, vp, i32, u64, vp]
+        L.oracle_act_dequant_mul_alam.restype = i32
         f32 = ctypes.c_float
         L.oracle_bn_reduce.argtypes = [vp, i32, i64, i64, i64, i64, i64, vp, vp]
         L.oracle_bn_reduce.restype = i32
@@ -281,17 +283,24 @@ def act_quant_pack(x: np.ndarray, act: int, group_size: int, bits: int, *, tile_
     return y, packed, scale, mn
 
 
-def act_dequant_mul(packed, scale, mn, group_size: int, bits: int, dy: np.ndarray, *, tile_nchw=None):
-    """Fused GELU/SiLU backward -> dx = bf16(dy * dequant) as uint16, shaped like dy."""
+def act_dequant_mul(packed, scale, mn, group_size: int, bits: int, dy: np.ndarray, *, tile_nchw=None,
+                    alam_seed=None):
+    """Fused GELU/SiLU backward -> dx = bf16(dy * dequant) as uint16, shaped like dy; with
+    alam_seed (the SiLU backward's avg_alam at alam_bits = 1) each code carries
+    tl.rand(alam_seed + group, element) - 0.5."""
     packed = np.ascontiguousarray(packed, dtype=np.uint32)
     dy = np.ascontiguousarray(dy)
     ng = packed.size * 32 // bits // group_size
     meta_dtype = F32 if scale.dtype == np.float32 else BF16
     tile = None if tile_nchw is None else np.array([int(v) for v in tile_nchw], dtype=np.int64)
     dx = np.zeros(dy.shape, dtype=np.uint16)
-    _check(lib().oracle_act_dequant_mul(_ptr(packed), _ptr(np.ascontiguousarray(scale)), _ptr(np.ascontiguousarray(mn)),
-                                        meta_dtype, ng, group_size, bits, _ptr(tile), _ptr(dy), _dtype_code(dy),
-                                        _ptr(dx)))
+    sc, m = np.ascontiguousarray(scale), np.ascontiguousarray(mn)
+    if alam_seed is None:
+        _check(lib().oracle_act_dequant_mul(_ptr(packed), _ptr(sc), _ptr(m), meta_dtype, ng, group_size, bits,
+                                            _ptr(tile), _ptr(dy), _dtype_code(dy), _ptr(dx)))
+    else:
+        _check(lib().oracle_act_dequant_mul_alam(_ptr(packed), _ptr(sc), _ptr(m), meta_dtype, ng, group_size, bits,
+                                                 _ptr(tile), _ptr(dy), _dtype_code(dy), int(alam_seed), _ptr(dx)))
     return dx
 
 

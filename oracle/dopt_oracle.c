@@ -635,10 +635,12 @@ int oracle_act_quant_pack(const void* x, int x_dtype, int act, int64_t n_groups,
     return O_OK;
 }
 
-/* gelu_bwd / silu_bwd_fused_dequan_unpack (:360-395): dx = bf16(dy * fma(float(q), scale, min)) */
-int oracle_act_dequant_mul(const uint32_t* packed, const void* scale, const void* minv, int meta_dtype,
-                           int64_t n_groups, int g, int bits, const int64_t* tile_nchw, const void* dy,
-                           int dy_dtype, uint16_t* dx) {
+/* gelu_bwd / silu_bwd_fused_dequan_unpack (:360-395): dx = bf16(dy * fma(float(q), scale, min));
+ * with noise (the SiLU backward's avg_alam at alam_bits = 1, :376-400) the code carries
+ * tl.rand(seed + r, e) - 0.5: fma(float(q) + (u - 0.5), scale, min) */
+static int act_dequant_mul_impl(const uint32_t* packed, const void* scale, const void* minv, int meta_dtype,
+                                int64_t n_groups, int g, int bits, const int64_t* tile_nchw, const void* dy,
+                                int dy_dtype, int noise, uint64_t seed, uint16_t* dx) {
     int s = 0;
     int rc = check_common(n_groups, g, bits, tile_nchw, &s);
     if (rc) return rc;
@@ -657,11 +659,27 @@ int oracle_act_dequant_mul(const uint32_t* packed, const void* scale, const void
         for (int e = 0; e < g; ++e) {
             uint32_t qv = (packed[r * NW + e / VPW] >> ((e % VPW) * bits)) & QMAX;
             int64_t o = elem_index(r, e, g, tile_nchw, s);
-            float act = fmaf((float)qv, sc, mn);
+            float qf = (float)qv;
+            if (noise) qf = qf + (oracle_triton_rand(seed + (uint64_t)r, (uint32_t)e) - 0.5f);
+            float act = fmaf(qf, sc, mn);
             dx[o] = f32_to_bf16(load_elem(dy, dy_dtype, o) * act);
         }
     }
     return O_OK;
+}
+
+int oracle_act_dequant_mul(const uint32_t* packed, const void* scale, const void* minv, int meta_dtype,
+                           int64_t n_groups, int g, int bits, const int64_t* tile_nchw, const void* dy,
+                           int dy_dtype, uint16_t* dx) {
+    return act_dequant_mul_impl(packed, scale, minv, meta_dtype, n_groups, g, bits, tile_nchw, dy, dy_dtype, 0, 0,
+                                dx);
+}
+
+int oracle_act_dequant_mul_alam(const uint32_t* packed, const void* scale, const void* minv, int meta_dtype,
+                                int64_t n_groups, int g, int bits, const int64_t* tile_nchw, const void* dy,
+                                int dy_dtype, uint64_t seed, uint16_t* dx) {
+    return act_dequant_mul_impl(packed, scale, minv, meta_dtype, n_groups, g, bits, tile_nchw, dy, dy_dtype, 1,
+                                seed, dx);
 }
 
 /* ---------------------------------------------------------------- BatchNorm

@@ -153,6 +153,34 @@ def test_silu_fused_quan_pack_tiles_and_backward(bits, shape, g):
     np.testing.assert_array_equal(np_view(dx).reshape(-1), want.reshape(-1))
 
 
+@pytest.mark.parametrize("shape,g", [((2, 16, 32, 48), 256), ((2, 32, 14, 14), 128)])
+@pytest.mark.parametrize("dydtype", [torch.bfloat16, torch.float32])
+def test_silu_avg_alam_one_adds_the_reference_noise(shape, g, dydtype):
+    """avg_alam=True at alam_bits = 1 (the only run length the reference's SiLU forward can compile):
+    the forward's outputs are the plain mode's; the backward's dx equals the oracle with each code
+    plus tl.rand(42 + group, element) - 0.5, bit for bit, in the tile layout (256 = 16 x 16 tiles of
+    32 x 48) and the flat one; alam_bits = 2 raises."""
+    x = randn(shape, seed=g, scale=2.5)
+    plain = torch.ops.act_lib.silu_fwd_quan_pack(x.to(DEV), 2, g, False, 0, False)
+    out = torch.ops.act_lib.silu_fwd_quan_pack(x.to(DEV), 2, g, True, 1, False)
+    for a, b in zip(plain, out):
+        assert torch.equal(a, b) if isinstance(a, torch.Tensor) else a == b
+    y, packed, scale, xmin, N, G, nh, nw, pad_e, rs_e = out
+    dy = randn(shape, seed=9, scale=1.0, dtype=dydtype)
+    dx = torch.ops.act_lib.silu_bwd_fused_dequan_unpack(packed, dy.to(DEV), scale, xmin, 2, N, G, g, False, nh, nw,
+                                                        pad_e, rs_e, True, 1)
+    torch.cuda.synchronize()
+    tile = shape if rs_e else None
+    dyn = np_view(dy) if rs_e else np_view(dy).reshape(-1, g)
+    want = oracle.act_dequant_mul(np_view(packed), np_view(scale), np_view(xmin), g, 2, dyn, tile_nchw=tile,
+                                  alam_seed=42)
+    np.testing.assert_array_equal(np_view(dx).reshape(-1), want.reshape(-1))
+    plain_dx = oracle.act_dequant_mul(np_view(packed), np_view(scale), np_view(xmin), g, 2, dyn, tile_nchw=tile)
+    assert np.mean(want.reshape(-1) != plain_dx.reshape(-1)) > 0.5  # the noise moves most elements
+    with pytest.raises(NotImplementedError, match="alam_bits"):
+        torch.ops.act_lib.silu_fwd_quan_pack(x.to(DEV), 2, g, True, 2, False)
+
+
 # ----------------------------------------------------------------------------- layers (autograd)
 def _meta(name, bits, g, act_padding=False, pack_only=False):
     return {name: {"bits": bits, "group_size": g, "act_padding": act_padding, "pack_only": pack_only,

@@ -125,6 +125,19 @@ class TestValidationWithoutDevice:
         assert L.dopt_bn_norm_quant_alam(16, _lib.BF16, N, C, HW, C * HW, HW, 16, 16, None, None, 0, 16, 16, 1e-5,
                                          64, 3, 2, 16, 16, 16, 16, 16, 16, None) == _lib.EBITS
 
+    def test_act_dequant_mul_alam_argument_checks(self):
+        L = _lib.lib()
+        assert L.dopt_act_dequant_mul_alam(16, 16, 16, _lib.BF16, 4, 256, 3, None, 16, _lib.BF16, 42, 16,
+                                           None) == _lib.EBITS
+        assert L.dopt_act_dequant_mul_alam(16, 16, 16, _lib.BF16, 4, 256, 2, None, 16, _lib.F16, 42, 16,
+                                           None) == _lib.EINVAL  # dy must be F32 or BF16
+        assert L.dopt_act_dequant_mul_alam(16, 16, 16, _lib.F16, 4, 256, 2, None, 16, _lib.BF16, 42, 16,
+                                           None) == _lib.EINVAL  # scale / min F32 or BF16
+        assert L.dopt_act_dequant_mul_alam(None, 16, 16, _lib.BF16, 4, 256, 2, None, 16, _lib.BF16, 42, 16,
+                                           None) == _lib.EINVAL  # null codes
+        assert L.dopt_act_dequant_mul_alam(16, 16, 16, _lib.BF16, 0, 256, 2, None, 16, _lib.BF16, 42, 16,
+                                           None) == _lib.OK  # nothing to do
+
     def test_valu_probe_argument_checks(self):
         L = _lib.lib()
         assert L.dopt_valu_probe(9, 16, 8, None) == _lib.EINVAL  # unknown kind

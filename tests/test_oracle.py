@@ -670,3 +670,34 @@ def test_alam_dequant_is_code_plus_centred_noise(bits, alam):
         n = oracle.triton_randn(42 + r, e)
         want = (codes[r, e] + (n - 0.5)) * sc[r] + mn[r]
         assert abs(y[r, e] - want) <= 2 ** -7 * abs(want) + 1e-30
+
+
+def _tl_rand(seed, off):
+    """tl.rand(seed, off) from the Philox words (pinned by the known-answer vectors above)"""
+    ctr = np.array([off, 0, 0, 0], np.uint32)
+    key = np.array([seed & 0xFFFFFFFF, seed >> 32], np.uint32)
+    out = np.zeros(4, np.uint32)
+    oracle.lib().oracle_philox4x32_10(ctr.ctypes.data, key.ctypes.data, out.ctypes.data)
+    i = int(out[:1].view(np.int32)[0])
+    i = ~i if i < 0 else i
+    return np.float32(i) * np.float32(4.6566127342e-10)
+
+
+def test_silu_alam_backward_adds_the_rand_noise():
+    """The SiLU backward with avg_alam at alam_bits = 1: dx = bf16(dy * fma(q + (u - 1/2), scale,
+    min)) with u = tl.rand(42 + group, element), against float64 from the Philox words (one bf16
+    ulp: the float64 form rounds twice); without the seed it is the plain dx."""
+    g, bits, ng = 64, 2, 8
+    x = np.random.default_rng(3).standard_normal((ng, g)).astype(np.float32)
+    p, s, m = oracle.quant_pack(x, g, bits, meta_dtype=oracle.BF16)
+    dy = np.random.default_rng(4).standard_normal((ng, g)).astype(np.float32)
+    got = _bf16_to_f32(oracle.act_dequant_mul(p, s, m, g, bits, dy, alam_seed=42)).astype(np.float64)
+    codes = oracle.unpack_codes(p, g, bits).view(np.uint8).astype(np.float32).reshape(ng, g)
+    sc, mn = _bf16_to_f32(s).astype(np.float64), _bf16_to_f32(m).astype(np.float64)
+    u = np.array([[_tl_rand(42 + r, e) for e in range(g)] for r in range(ng)], dtype=np.float32)
+    qn = (codes + (u - np.float32(0.5))).astype(np.float64)
+    want = dy.astype(np.float64) * (qn * sc[:, None] + mn[:, None])
+    assert np.all(np.abs(got - want) <= 2.0 ** -7 * np.abs(want) + 1e-30)
+    plain = _bf16_to_f32(oracle.act_dequant_mul(p, s, m, g, bits, dy)).astype(np.float64)
+    np.testing.assert_allclose(plain, dy * (codes * sc[:, None] + mn[:, None]), rtol=2.0 ** -7, atol=1e-30)
+    assert np.mean(got != plain) > 0.5
