@@ -452,7 +452,7 @@ def vit_train_step(torch, dev, batch=128, steps=6, warmup=3):
         model = vit_base_patch16_224().to(dev).train()
         if name != "plain":
             ctl = Controller(model, {"batch_size": batch, "default_bits": 2}, input_shape=(3, 224, 224))
-            model = ctl.warp_model()
+            model = ctl.warp_model(quantizer=True)
         opt = torch.optim.AdamW(model.parameters(), lr=3e-3, fused=True)
 
         def one():
@@ -505,7 +505,7 @@ def vit_qdrop_graph_step(torch, dev, batch=128, steps=6, warmup=2):
     yb = torch.randint(0, 1000, (batch,), generator=g, device=dev)
     torch.manual_seed(0)
     model = vit_base_patch16_224().to(dev).train()
-    model = Controller(model, {"batch_size": batch, "default_bits": 2}, input_shape=(3, 224, 224)).warp_model()
+    model = Controller(model, {"batch_size": batch, "default_bits": 2}, input_shape=(3, 224, 224)).warp_model(quantizer=True)
     opt = torch.optim.AdamW(model.parameters(), lr=3e-3, fused=True, capturable=True)
     gr = Graph(model, nn.CrossEntropyLoss(), opt, [(xb, yb)], None, "qdrop", 1)
     graphs, _, _, _, _, loss = gr.capture_cuda_graph_qdrop()
@@ -559,7 +559,7 @@ def resnet_train_step(torch, dev, batch=64, steps=6, warmup=3):
         n_layers = None
         if name != "plain":
             ctl = Controller(model, {"batch_size": batch, "default_bits": 2}, input_shape=(3, 224, 224))
-            model = ctl.warp_model()
+            model = ctl.warp_model(quantizer=True)
             n_layers = sum(1 for v in ctl.meta.values() if isinstance(v, dict))
         opt = torch.optim.SGD(model.parameters(), lr=0.01, momentum=0.9)
 

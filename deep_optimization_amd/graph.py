@@ -26,6 +26,11 @@ the Philox offsets drawn at capture; nearest rounding (the default) has no state
 Behaviour kept from the reference: ``prepare_theta`` gives every trainable parameter a noise
 buffer. Its BatchNorm2d test looks at the module of the outer loop, not at the parameter's
 owner, so it excludes nothing whenever the model has any module that is not a BatchNorm2d.
+
+``graph_module_in_place`` is the module-level counterpart: it turns one module's training
+forward and backward into two replayed graphs (what the reference's Controller gets from
+``torch.compile(mode='reduce-overhead')``, controller.py:316-331) and is what
+``Controller.enable_graph_mode`` applies to the rewritten model.
 """
 from __future__ import annotations
 
@@ -183,5 +188,127 @@ def denoise(model: nn.Module) -> None:
             del p._noise
 
 
+# -- module-level capture: the forward and the backward of one module as two replayed graphs ------
+
+
+def _as_tuple(out):
+    return out if isinstance(out, tuple) else (out,)
+
+
+class _Capture:
+    """The forward graph, the backward graph and their static buffers for one input signature."""
+
+    def __init__(self, module: nn.Module, args, autocast, warmup_iters: int):
+        forward = type(module).forward
+        self.params = tuple(p for p in module.parameters() if p.requires_grad)
+        self.static_in = tuple(a.detach().clone().requires_grad_(a.requires_grad) for a in args)
+        diff_in = tuple(a for a in self.static_in if a.requires_grad) + self.params
+        enabled, dtype = autocast
+
+        def run():
+            # the autocast weight cache is off: a cached cast made outside a graph would be replayed stale
+            with torch.autocast("cuda", dtype=dtype, enabled=enabled, cache_enabled=False):
+                out = forward(module, *self.static_in)
+            self.tuple_out = isinstance(out, tuple)
+            return _as_tuple(out)
+
+        side = cuda.Stream()
+        side.wait_stream(cuda.current_stream())
+        with cuda.stream(side):
+            for _ in range(warmup_iters):
+                outs = [o for o in run() if o.requires_grad]
+                torch.autograd.grad(outs, diff_in, grad_outputs=[torch.zeros_like(o) for o in outs],
+                                    allow_unused=True)
+                del outs
+        cuda.current_stream().wait_stream(side)
+        cuda.synchronize()
+
+        self.fwd = cuda.CUDAGraph(keep_graph=True)
+        self.bwd = cuda.CUDAGraph(keep_graph=True)
+        with cuda.graph(self.fwd):
+            outs = run()
+        self.static_out = tuple(o.detach() for o in outs)
+        self.out_requires_grad = tuple(o.requires_grad for o in outs)
+        graded = [o for o in outs if o.requires_grad]
+        self.static_grad_out = tuple(torch.empty_like(o) for o in graded)
+        with cuda.graph(self.bwd, pool=self.fwd.pool()):
+            grads = torch.autograd.grad(graded, diff_in, grad_outputs=self.static_grad_out, allow_unused=True)
+        del outs, graded
+        grads = iter(grads)
+        self.static_grad_in = tuple(next(grads) if a.requires_grad else None for a in self.static_in) + \
+            tuple(next(grads) for _ in self.params)
+        self.memsets_replaced = finalize(self.fwd) + finalize(self.bwd)
+        cuda.synchronize()
+
+
+class _ReplayFunction(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, cap: _Capture, *inputs):
+        for s, x in zip(cap.static_in, inputs):
+            if s.data_ptr() != x.data_ptr():
+                s.copy_(x)
+        cap.fwd.replay()
+        ctx.cap = cap
+        outs = tuple(o.detach() for o in cap.static_out)
+        ctx.mark_non_differentiable(*(o for o, rg in zip(outs, cap.out_requires_grad) if not rg))
+        return outs
+
+    @staticmethod
+    @torch.autograd.function.once_differentiable
+    def backward(ctx, *grads):
+        cap = ctx.cap
+        graded = (g for g, rg in zip(grads, cap.out_requires_grad) if rg)
+        for static, g in zip(cap.static_grad_out, graded):
+            if g is None:
+                static.zero_()
+            elif static.data_ptr() != g.data_ptr():
+                static.copy_(g)
+        cap.bwd.replay()
+        return (None,) + tuple(None if g is None else g.detach() for g in cap.static_grad_in)
+
+
+def graph_module_in_place(module: nn.Module, warmup_iters: int = 2) -> nn.Module:
+    """Makes ``module``'s training forward and backward replay HIP graphs, in place.
+
+    This is what the reference gets from ``module.compile(mode='reduce-overhead')``
+    (Activation_Compression/controller.py:316-331): the module object, its parameters and its
+    state dict stay the same; its ``forward`` becomes a replay. On the first training call with a
+    given input signature (shapes, dtypes, autocast state) the module is run ``warmup_iters``
+    times eagerly on a side stream, then its forward is captured into one graph and the gradient
+    of its outputs with respect to its floating inputs and trainable parameters into a second,
+    both in one memory pool, memset nodes rewritten into kernels (``finalize``). Later calls copy
+    the inputs into the static input buffers and replay; the backward replays the second graph
+    and hands the parameter gradients to autograd, which accumulates them into ``.grad`` as for
+    any other function.
+
+    Contract (the same as torch.cuda.make_graphed_callables'): a call's outputs live in static
+    buffers that the next call overwrites, so run the backward of one call before the next
+    forward; state a forward mutates outside its outputs (BatchNorm running statistics) is
+    updated by each replay as in eager mode, and by the warm-up runs and the capture once each;
+    hooks inside the module run at capture only. Calls without grad mode, in eval mode or with
+    inputs not on the GPU run the eager forward.
+    """
+    if "forward" in vars(module):
+        return module  # already graphed
+    eager = type(module).forward
+    captures = {}
+
+    def forward(*args):
+        tensors = all(isinstance(a, torch.Tensor) and a.is_cuda for a in args)
+        if not (torch.is_grad_enabled() and module.training and tensors and args):
+            return eager(module, *args)
+        autocast = (torch.is_autocast_enabled("cuda"), torch.get_autocast_dtype("cuda"))
+        key = (tuple((tuple(a.shape), a.dtype, a.requires_grad) for a in args), autocast)
+        cap = captures.get(key)
+        if cap is None:
+            cap = captures[key] = _Capture(module, args, autocast, warmup_iters)
+        outs = _ReplayFunction.apply(cap, *args, *cap.params)
+        return outs if cap.tuple_out else outs[0]
+
+    module.forward = forward
+    module._dopt_graph_captures = captures
+    return module
+
+
 __all__ = ["Graph", "prepare_theta", "inject_noise", "denoise", "graph_node_counts", "replace_memset_nodes",
-           "finalize", "NODE_TYPES"]
+           "finalize", "graph_module_in_place", "NODE_TYPES"]

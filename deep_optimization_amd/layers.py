@@ -110,4 +110,19 @@ class DOConv3d(_DOConvMixin, nn.Conv3d):
         self._init_do(clamp_alpha, target_name, meta)
 
 
-__all__ = ["DOLinear", "DOConv1d", "DOConv2d", "DOConv3d"]
+class RMSNorm(nn.Module):
+    """RMS normalisation over the last axis with a learned gain (Activation_Compression/layers.py:
+    206-216): ``x / sqrt(mean(x^2) + eps) * weight``. Not compressed; the reference's notebooks
+    swap it in for LayerNorm before handing the model to the Controller."""
+
+    def __init__(self, dims, eps=1e-8):
+        super().__init__()
+        self.eps = eps
+        self.weight = nn.Parameter(torch.ones(dims))
+
+    def forward(self, x):
+        rms = x.pow(2).mean(dim=-1, keepdim=True).add(self.eps).sqrt()
+        return x / rms * self.weight
+
+
+__all__ = ["DOLinear", "DOConv1d", "DOConv2d", "DOConv3d", "RMSNorm"]

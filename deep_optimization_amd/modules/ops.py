@@ -8,7 +8,10 @@ arguments and ``meta`` keys (bits, group_size, act_padding, pack_only, AVG_ALAM,
 DIVISION and the optional rounding keys of module_utils). As in the reference, the saved input is
 quantized with ``clamp=True`` and the layer's ``clamp_alpha`` (the tanh squash of the quantizer
 applies), an optional DIVISION low-pass (average pool) is stored beside it and added back when
-the input is restored, and under autocast the computation runs in the autocast dtype.
+the input is restored, and under autocast the computation runs in the autocast dtype. The input
+is quantized whole, not minus its low-pass, so a DIVISION layer's restored input is
+x_hat + upsample(avgpool(x)), about x plus its low-pass (ops.py:245-264, :457-474 with
+module_utils.py:86-102); this is kept as the reference computes it, for parity.
 
 The Linear weight gradient ``dy^T . x_hat`` (and the bias gradient) runs on the gfx950 kernel
 behind ``act_lib::dw_gemm`` when dy is bf16 and both feature counts are multiples of 256; the

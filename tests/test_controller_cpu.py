@@ -25,7 +25,7 @@ def vit_controller():
     model = vit_base_patch16_224()
     ref_state = {k: v.clone() for k, v in model.state_dict().items()}
     c = Controller(model, {"batch_size": 128, "default_bits": 2}, input_shape=(3, 224, 224), device="cpu")
-    c.warp_model()
+    c.warp_model(quantizer=True)
     return c, ref_state
 
 
@@ -98,12 +98,12 @@ def test_cnn_relu_mask_only_and_bits_override():
     model = _Cnn()
     c = Controller(model, {"batch_size": 32, "default_bits": 2, "bits": {"conv2": 4}}, input_shape=(3, 64, 64),
                    device="cpu")
-    c.warp_model()
+    c.warp_model(quantizer=True)
     # outputs: conv1 / bn1 / relu / conv2 / silu [32, 32, 64, 64] bf16 = 8 MiB -> none selected
     assert _targets(c) == []
     c = Controller(_Cnn(), {"batch_size": 64, "default_bits": 2, "bits": {"conv2": 4}}, input_shape=(3, 64, 64),
                    device="cpu")
-    c.warp_model()
+    c.warp_model(quantizer=True)
     assert _targets(c) == ["act1", "act2", "bn1", "conv1", "conv2"]
     assert c.meta["act1"]["pack_only"] and c.meta["act1"]["bits"] == 1
     # BatchNorm groups per channel: S = N*H*W = 64*64*64 = 256 * 1024, N = C = 32
@@ -125,7 +125,7 @@ def test_eval_forward_equals_original():
     with torch.no_grad():
         want = model(x)
     c = Controller(model, {"batch_size": 64, "default_bits": 2}, input_shape=(3, 64, 64), device="cpu")
-    tm = c.warp_model().eval()
+    tm = c.warp_model(quantizer=True).eval()
     with torch.no_grad():
         got = tm(x)
     torch.testing.assert_close(got, want, rtol=0, atol=0)
@@ -177,7 +177,7 @@ def test_batchnorm_swap_keeps_state_and_fuse_bn_act():
     with torch.no_grad():
         want = model(x)
     c = Controller(model, {"batch_size": 64, "default_bits": 2}, input_shape=(3, 64, 64), device="cpu")
-    tm = c.warp_model()
+    tm = c.warp_model(quantizer=True)
     for k, v in ref.items():
         assert torch.equal(tm.bn1.state_dict()[k], v), k
     fused = fuse_bn_act(tm)
@@ -201,7 +201,7 @@ def test_resnet50_selection_and_swap():
 
     torch.manual_seed(0)
     c = Controller(resnet50(), {"batch_size": 64, "default_bits": 2}, input_shape=(3, 224, 224), device="cpu")
-    model = c.warp_model()
+    model = c.warp_model(quantizer=True)
     kinds = {}
     for name, mod in model.named_modules():
         if name in c.meta:

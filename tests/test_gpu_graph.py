@@ -115,7 +115,7 @@ def test_graph_qdrop_step_matches_eager():
     torch.manual_seed(3)
     B, alpha = 32, 0.0375
     base = VisionTransformer(depth=2, num_classes=100).to(DEV)
-    model = Controller(base, {"batch_size": B, "default_bits": 2}, input_shape=(3, 224, 224)).warp_model()
+    model = Controller(base, {"batch_size": B, "default_bits": 2}, input_shape=(3, 224, 224)).warp_model(quantizer=True)
     x = torch.randn(B, 3, 224, 224, device=DEV)
     y = torch.randint(0, 100, (B,), device=DEV)
     crit = nn.CrossEntropyLoss()
@@ -188,7 +188,7 @@ def test_compressed_resnet_step_replays_like_eager(deterministic_miopen):
     torch.manual_seed(4)
     B = 16
     model = Controller(ResNet((1, 1, 1, 1), num_classes=100).to(DEV), {"batch_size": B, "default_bits": 2},
-                       input_shape=(3, 224, 224)).warp_model()
+                       input_shape=(3, 224, 224)).warp_model(quantizer=True)
     assert sum(isinstance(m, DOBatchNorm2d) for m in model.modules()) >= 3
     x = torch.randn(B, 3, 224, 224, device=DEV)
     y = torch.randint(0, 100, (B,), device=DEV)

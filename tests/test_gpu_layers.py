@@ -181,7 +181,7 @@ def test_controller_vit_trains_and_saves_less():
     y = torch.randint(0, 100, (B,), device=DEV)
     plain_bytes = _saved_bytes(base.train(), x)
     c = Controller(base, {"batch_size": B, "default_bits": 2}, input_shape=(3, 224, 224))
-    model = c.warp_model()
+    model = c.warp_model(quantizer=True)
     assert "blocks.1.mlp.fc1" in c.meta and "blocks.1.mlp.act" in c.meta
     comp_bytes = _saved_bytes(model, x)
     # Per block and per token, in units of 768 bf16 values, the plain model saves about 17 (two

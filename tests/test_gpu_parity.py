@@ -84,7 +84,7 @@ def test_quant_pack_flat_parity(dtype, bits, g, rounding):
 
 
 @pytest.mark.parametrize("bits", [1, 2, 4, 8])
-@pytest.mark.parametrize("g", [64, 256, 1024])
+@pytest.mark.parametrize("g", [64, 128, 256, 512, 1024])
 @pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float32], ids=["bf16", "f32"])
 @pytest.mark.parametrize("meta", [torch.float32, torch.bfloat16], ids=["meta32", "meta16"])
 def test_dequant_flat_parity(bits, g, out_dtype, meta):
@@ -519,6 +519,38 @@ def test_resnet_full_size_stochastic(resnet_act):
     y2 = torch.ops.act_lib.dequant_unpack(p2, s2, m2, 2, g, torch.float32)
     rel = float((y2.double() - x.double()).mean() / s2.double().mean())
     assert abs(rel) < 1e-3
+
+
+@pytest.mark.parametrize("bits", [1, 2, 4, 8])
+def test_vit_mlp_full_size_philox(bits):
+    """BASELINE config 3 at its size: GELU(N(0,1)) bf16 [256, 197, 3072] (1,210,368 groups of
+    g = 128), Philox stochastic rounding (seed 1, offset 0), quant-pack then unpack to bf16, as
+    the benchmark runs it. Three windows of 64 groups (the first, the middle, the last) match the
+    oracle bit for bit (codes, scale, min, dequantized bf16), the Philox stream taken from the
+    oracle's generator at those element indices; over the whole tensor every value comes back
+    within one step of the input, plus half a bf16 ulp for the output rounding."""
+    g = 128
+    x = torch.nn.functional.gelu(torch.randn((256, 197, 3072), generator=torch.Generator(device=DEV).manual_seed(2),
+                                             device=DEV)).to(torch.bfloat16)
+    xg = x.view(256, -1, g)
+    ng = x.numel() // g
+    print(f"[config 3] {bits}-bit, {ng} groups", flush=True)
+    p, s, m = torch.ops.act_lib.quant_pack(xg, bits, g, False, 0.0, False, ROUNDINGS["philox"], None, 1, 0,
+                                           torch.float32)
+    y = torch.ops.act_lib.dequant_unpack(p, s, m, bits, g, torch.bfloat16)
+    torch.cuda.synchronize()
+    assert p.shape == (ng, g * bits // 32) and s.shape == (256, ng // 256) and y.shape == xg.shape
+    xf = x.view(-1, g)
+    for w in (slice(0, 64), slice(ng // 2 - 32, ng // 2 + 32), slice(ng - 64, ng)):
+        u = oracle.philox_noise(w.start * g, (w.stop - w.start) * g, 1, 0).reshape(-1, g)
+        ref = oracle.quant_pack(np_view(xf[w]), g, bits, rounding=oracle.STOCH_NOISE, noise=u)
+        assert_quant_equal((p[w], s.view(-1)[w], m.view(-1)[w]), ref, f"{bits}-bit groups {w}")
+        yo = oracle.dequant_unpack(*ref, g, bits, y_dtype=oracle.BF16)
+        np.testing.assert_array_equal(np_view(y.view(-1, g)[w]), yo, err_msg=f"{bits}-bit dequant {w}")
+    yf = y.view(-1, g).float()
+    err = (yf - xf.float()).abs()
+    step = s.view(-1, 1)
+    assert bool((err <= step * (1 + 1e-6) + yf.abs() * 2.0 ** -8).all())
 
 
 # ----------------------------------------------------------------------------- FP8 GEMM

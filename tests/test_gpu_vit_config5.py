@@ -81,7 +81,7 @@ def test_vit_b16_batch128_two_compressed_steps():
     torch.manual_seed(0)
     plain = vit_base_patch16_224().to(DEV).train()
     ctl = Controller(copy.deepcopy(plain), {"batch_size": BATCH, "default_bits": 2}, input_shape=(3, 224, 224))
-    model = ctl.warp_model()
+    model = ctl.warp_model(quantizer=True)
     layers = [k for k, v in ctl.meta.items() if isinstance(v, dict)]
     assert len(layers) == 61, layers
     for blk in range(12):
