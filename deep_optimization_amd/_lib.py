@@ -50,8 +50,6 @@ EXPORTS = (
     "dopt_dw_gemm",
     "dopt_graph_node_counts",
     "dopt_graph_replace_memsets",
-    "dopt_stream_probe",
-    "dopt_valu_probe",
     "dopt_alam_quant_pack",
     "dopt_alam_dequant_unpack",
 )
@@ -153,10 +151,6 @@ def lib() -> ctypes.CDLL:
         L.dopt_graph_node_counts.restype = i32
         L.dopt_graph_replace_memsets.argtypes = [vp, vp]
         L.dopt_graph_replace_memsets.restype = i32
-        L.dopt_stream_probe.argtypes = [vp, vp, vp, vp, i64, i32, vp]
-        L.dopt_stream_probe.restype = i32
-        L.dopt_valu_probe.argtypes = [i32, vp, i64, vp]
-        L.dopt_valu_probe.restype = i32
         L.dopt_alam_quant_pack.argtypes = [vp, i32, i64, i32, i32, i32, i32, ctypes.c_float, vp, vp, vp, vp]
         L.dopt_alam_quant_pack.restype = i32
         L.dopt_alam_dequant_unpack.argtypes = [vp, vp, vp, i64, i32, i32, i32, ctypes.c_uint64, vp, vp]

@@ -29,7 +29,6 @@ SOURCES = [
     "bn_fused.hip",
     "dw_gemm.hip",
     "graph_tools.hip",
-    "stream_probe.hip",
     "alam.hip",
 ]
 

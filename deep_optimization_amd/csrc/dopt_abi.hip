@@ -24,14 +24,11 @@ int launch_relu_unpack(const uint32_t* packed, const void* dy, int dyt, void* dx
 int launch_act_forward(const void* x, int dt, void* y, void* aux, uint64_t n, int act, hipStream_t s);
 const char* graph_node_counts(hipGraph_t g, int64_t* counts, int n_counts);
 const char* graph_replace_memsets(hipGraph_t g, int64_t* replaced);
-const char* launch_valu_rate(int kind, float* out, uint32_t n_blocks, hipStream_t s);
 int launch_alam_quant_pack(const void* x, int dt, int64_t n_groups, int g, int bits, int alam, int flags,
                            float clamp_alpha, uint32_t* packed, uint16_t* scale, uint16_t* minv, hipStream_t s);
 int launch_alam_dequant(const uint32_t* packed, const uint16_t* scale, const uint16_t* minv, int64_t n_groups,
                         int g, int bits, int alam, uint64_t seed, uint16_t* y, hipStream_t s);
 int launch_alam_act_dequant_mul(const DequantArgs& d, int g, int bits, int dy_f32, uint64_t seed, hipStream_t s);
-const char* launch_stream_mix(const void* x, const void* noise, void* codes, void* meta, uint64_t n_units, int bits,
-                              hipStream_t s);
 }  // namespace dopt
 
 namespace {
@@ -931,36 +928,5 @@ int dopt_graph_replace_memsets(void* graph, int64_t* n_replaced) {
     *n_replaced = 0;
     if (const char* e = dopt::graph_replace_memsets((hipGraph_t)graph, n_replaced))
         return fail(DOPT_EHIP, "graph_replace_memsets: %s failed after %lld replacements", e, (long long)*n_replaced);
-    return ok();
-}
-
-int dopt_valu_probe(int kind, float* out, int64_t n_blocks, void* stream) {
-    if (kind < 0 || kind > 8)
-        return fail(DOPT_EINVAL,
-                    "kind must be 0..8 (fma, exp, rcp, mad64+xor, bf16 MFMA random / constant, fp8 MFMA random / "
-                    "constant, exact-division check), got %d", kind);
-    if (n_blocks < 1 || n_blocks > 65536) return fail(DOPT_EINVAL, "n_blocks must be in [1, 65536], got %lld",
-                                                      (long long)n_blocks);
-    if (!out || ((uintptr_t)out & 3u)) return fail(DOPT_EINVAL, "out must be a 4-byte aligned pointer");
-    (void)hipGetLastError();
-    if (const char* e = dopt::launch_valu_rate(kind, out, (uint32_t)n_blocks, (hipStream_t)stream))
-        return fail(DOPT_EHIP, "valu_probe launch: %s", e);
-    return ok();
-}
-
-int dopt_stream_probe(const void* x, const void* noise, void* codes, void* meta, int64_t n_units, int bits,
-                      void* stream) {
-    if (n_units < 0 || n_units > ((int64_t)1 << 31))  // one lane per unit; the grid stays below 2^32 lanes
-        return fail(DOPT_EINVAL, "n_units must be in [0, 2^31], got %lld", (long long)n_units);
-    if (bits != 0 && bits != 1 && bits != 2 && bits != 4 && bits != 8)
-        return fail(DOPT_EINVAL, "bits must be 0, 1, 2, 4 or 8, got %d", bits);
-    if (n_units == 0) return ok();
-    if (!x || !aligned16(x) || (noise && !aligned16(noise))) return fail(DOPT_EINVAL, "x / noise must be 16-byte aligned");
-    if (bits && (!codes || !meta || ((uintptr_t)codes % (uintptr_t)bits) || ((uintptr_t)meta & 7u)))
-        return fail(DOPT_EINVAL, "codes must be bits-byte and meta 8-byte aligned");
-    if (!bits && !codes) return fail(DOPT_EINVAL, "codes must point to at least one byte");
-    (void)hipGetLastError();
-    if (const char* e = dopt::launch_stream_mix(x, noise, codes, meta, (uint64_t)n_units, bits, (hipStream_t)stream))
-        return fail(DOPT_EHIP, "stream_probe launch: %s", e);
     return ok();
 }

@@ -8,9 +8,12 @@
 // quant-pack kernel's lanes take consecutive 16-byte pieces of a group. The bytes written are a
 // hash of the bytes read: they only keep the loads alive.
 #include <hip/hip_runtime.h>
+#include <stdarg.h>
 #include <stdint.h>
+#include <stdio.h>
 
-#include "quant_pack.h"
+#include "dopt_probe.h"
+#include "quant_pack.h"  // the quantizer's division helpers, checked by valu kind 8
 
 namespace dopt {
 namespace {
@@ -194,7 +197,7 @@ __global__ __launch_bounds__(PROBE_THREADS) void division_check_kernel(float* __
 // kind 0..3 (fma, exp, rcp, mad64 + xor), 4 / 5 (bf16 MFMA stream, random / constant operands),
 // 6 / 7 (fp8 MFMA stream, random / constant operands), 8 (exact-division check: per-thread counts
 // of mismatches, 0 expected); out holds n_blocks * 256 floats
-const char* launch_valu_rate(int kind, float* out, uint32_t n_blocks, hipStream_t s) {
+static const char* launch_valu_rate(int kind, float* out, uint32_t n_blocks, hipStream_t s) {
     switch (kind) {
         case 8: hipLaunchKernelGGL(division_check_kernel, dim3(n_blocks), dim3(PROBE_THREADS), 0, s, out); break;
         case 6: hipLaunchKernelGGL(mfma_fp8_rate_kernel<true>, dim3(n_blocks), dim3(PROBE_THREADS), 0, s, out); break;
@@ -212,7 +215,7 @@ const char* launch_valu_rate(int kind, float* out, uint32_t n_blocks, hipStream_
 }
 
 // bits in {0, 1, 2, 4, 8}; 0 = reads only. Returns nullptr or the name of what failed.
-const char* launch_stream_mix(const void* x, const void* noise, void* codes, void* meta, uint64_t n_units, int bits,
+static const char* launch_stream_mix(const void* x, const void* noise, void* codes, void* meta, uint64_t n_units, int bits,
                               hipStream_t s) {
     hipError_t e = hipSuccess;
 #define DOPT_SM(B)                                                                               \
@@ -234,3 +237,61 @@ const char* launch_stream_mix(const void* x, const void* noise, void* codes, voi
 }
 
 }  // namespace dopt
+
+namespace {
+
+thread_local char g_probe_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_probe_err, sizeof(g_probe_err), fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+int ok() {
+    g_probe_err[0] = '\0';
+    return 0;
+}
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+}  // namespace
+
+extern "C" {
+
+const char* dopt_probe_last_error(void) { return g_probe_err; }
+
+int dopt_valu_probe(int kind, float* out, int64_t n_blocks, void* stream) {
+    if (kind < 0 || kind > 8)
+        return fail(-2,
+                    "kind must be 0..8 (fma, exp, rcp, mad64+xor, bf16 MFMA random / constant, fp8 MFMA random / "
+                    "constant, exact-division check), got %d", kind);
+    if (n_blocks < 1 || n_blocks > 65536) return fail(-2, "n_blocks must be in [1, 65536], got %lld",
+                                                      (long long)n_blocks);
+    if (!out || ((uintptr_t)out & 3u)) return fail(-2, "out must be a 4-byte aligned pointer");
+    (void)hipGetLastError();
+    if (const char* e = dopt::launch_valu_rate(kind, out, (uint32_t)n_blocks, (hipStream_t)stream))
+        return fail(-4, "valu_probe launch: %s", e);
+    return ok();
+}
+
+int dopt_stream_probe(const void* x, const void* noise, void* codes, void* meta, int64_t n_units, int bits,
+                      void* stream) {
+    if (n_units < 0 || n_units > ((int64_t)1 << 31))  // one lane per unit; the grid stays below 2^32 lanes
+        return fail(-2, "n_units must be in [0, 2^31], got %lld", (long long)n_units);
+    if (bits != 0 && bits != 1 && bits != 2 && bits != 4 && bits != 8)
+        return fail(-2, "bits must be 0, 1, 2, 4 or 8, got %d", bits);
+    if (n_units == 0) return ok();
+    if (!x || !aligned16(x) || (noise && !aligned16(noise))) return fail(-2, "x / noise must be 16-byte aligned");
+    if (bits && (!codes || !meta || ((uintptr_t)codes % (uintptr_t)bits) || ((uintptr_t)meta & 7u)))
+        return fail(-2, "codes must be bits-byte and meta 8-byte aligned");
+    if (!bits && !codes) return fail(-2, "codes must point to at least one byte");
+    (void)hipGetLastError();
+    if (const char* e = dopt::launch_stream_mix(x, noise, codes, meta, (uint64_t)n_units, bits, (hipStream_t)stream))
+        return fail(-4, "stream_probe launch: %s", e);
+    return ok();
+}
+
+}  // extern "C"

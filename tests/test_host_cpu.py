@@ -138,15 +138,6 @@ class TestValidationWithoutDevice:
         assert L.dopt_act_dequant_mul_alam(16, 16, 16, _lib.BF16, 0, 256, 2, None, 16, _lib.BF16, 42, 16,
                                            None) == _lib.OK  # nothing to do
 
-    def test_valu_probe_argument_checks(self):
-        L = _lib.lib()
-        assert L.dopt_valu_probe(9, 16, 8, None) == _lib.EINVAL  # unknown kind
-        assert L.dopt_valu_probe(-1, 16, 8, None) == _lib.EINVAL
-        assert L.dopt_valu_probe(0, 16, 0, None) == _lib.EINVAL  # no blocks
-        assert L.dopt_valu_probe(0, 16, 65537, None) == _lib.EINVAL
-        assert L.dopt_valu_probe(0, None, 8, None) == _lib.EINVAL
-        assert L.dopt_valu_probe(0, 18, 8, None) == _lib.EINVAL  # unaligned
-
     def test_gemm_shape_checks(self):
         L = _lib.lib()
         assert L.dopt_fp8_gemm_nt(16, 16, 100, 256, 120, 128, 128, 1.0, 16, 256, None) == _lib.EUNSUPPORTED  # K % 16
