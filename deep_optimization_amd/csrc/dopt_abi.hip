@@ -171,7 +171,11 @@ int bn_alam_lg(int group_size, int bits, int alam_bits, int* lg) {
 // partials, which the normalize kernel sums. Each partial slot is written before it is read in
 // the same call, so nothing needs clearing between calls. In host code `scratch` is only a
 // host-side handle: kernels get the device address that hipGetSymbolAddress returns for the
-// current device, looked up on the entry point's first call on that device and kept.
+// current device, looked up on the entry point's first call on that device and kept for the
+// life of the process (a hipDeviceReset, which frees the module and its scratch, invalidates it;
+// this library is not to be used across one). That first call may come while the caller's stream
+// is being captured into a graph: the lookup then runs in the relaxed capture mode, in which a
+// call that is not a stream operation is allowed, and the previous mode is restored after it.
 static __device__ __align__(256) float scratch[DOPT_BN_SCRATCH_FLOATS];
 
 constexpr int kMaxDevices = 64;
@@ -186,7 +190,10 @@ int scratch_of_current_device(float** out) {
     std::lock_guard<std::mutex> lock(g_scratch_mu);
     if (!g_scratch_ptr[dev]) {
         void* p = nullptr;
+        hipStreamCaptureMode mode = hipStreamCaptureModeRelaxed;
+        const hipError_t em = hipThreadExchangeStreamCaptureMode(&mode);
         e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (em == hipSuccess) (void)hipThreadExchangeStreamCaptureMode(&mode);
         if (e != hipSuccess || !p)
             return fail(DOPT_EHIP, "hipGetSymbolAddress(scratch) on device %d: %s", dev, hipGetErrorString(e));
         g_scratch_ptr[dev] = (float*)p;

@@ -612,7 +612,9 @@ __global__ __launch_bounds__(256, 1) void fp8_gemm_nt_persistent_kernel(Fp8GemmA
 }
 
 // Persistent launch: min(tiles, CUs) workgroups (n_cu from the caller). An odd or zero slab
-// count (K / BK rounded up) takes the non-persistent kernel (which writes C = 0 for K = 0).
+// count (K / BK rounded up) takes the non-persistent kernel (which writes C = 0 for K = 0), and
+// so does a device with fewer CUs than XCDs: the tile list gives every XCD with tiles at least one
+// workgroup only when the grid has min(tiles, GEMM_XCDS) or more.
 template <class C>
 inline int fp8_gemm_persistent_launch(const uint8_t* A, const uint8_t* B, int64_t M, int64_t N, int64_t K,
                                       int64_t lda, int64_t ldb, float out_scale, uint16_t* Cm, int64_t ldc,
@@ -623,7 +625,8 @@ inline int fp8_gemm_persistent_launch(const uint8_t* A, const uint8_t* B, int64_
     if (tiles == 0) return 0;
     const uint32_t grid = (uint32_t)(tiles < (uint64_t)n_cu ? tiles : (uint64_t)n_cu);
     const int64_t nk = (K + C::BK - 1) / C::BK;
-    if (nk == 0 || nk % 2) return fp8_gemm_launch<C>(A, B, M, N, K, lda, ldb, out_scale, Cm, ldc, s);
+    if (nk == 0 || nk % 2 || n_cu < GEMM_XCDS)
+        return fp8_gemm_launch<C>(A, B, M, N, K, lda, ldb, out_scale, Cm, ldc, s);
     // whole tiles with aligned C store through a buffer resource: a tile's offsets must stay in range
     if (M % C::BM == 0 && N % C::BN == 0 && K % C::BK == 0 && p.vec_store && (int64_t)C::BM * ldc * 2 < GEMM_RANGE)
         hipLaunchKernelGGL((fp8_gemm_nt_persistent_kernel<C, false>), dim3(grid), dim3(C::THREADS), 0, s, p);
