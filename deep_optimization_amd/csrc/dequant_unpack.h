@@ -55,9 +55,10 @@ struct DequantCfg {
     static_assert(UBITS <= 128, "a unit reads at most one 16-byte code vector");
 };
 
-template <int G>
+// the layout is a template parameter, as in quant_pack.h's group_elem_index
+template <int G, bool TILED>
 __device__ __forceinline__ uint64_t dq_elem_index(const DequantArgs& a, uint32_t r, uint32_t e0) {
-    if (!a.tiled) return (uint64_t)r * G + e0;
+    if constexpr (!TILED) return (uint64_t)r * G + e0;
     const uint32_t band = r / a.tiles_w;
     const uint32_t tw = r - band * a.tiles_w;
     const uint32_t smask = (1u << a.log2s) - 1u;
@@ -65,7 +66,7 @@ __device__ __forceinline__ uint64_t dq_elem_index(const DequantArgs& a, uint32_t
            (uint64_t)(e0 >> a.log2s) * a.row + (e0 & smask);
 }
 
-template <int YT, int BITS, int G, int UB, int LPG_, int P, bool NT, int DYT>
+template <int YT, int BITS, int G, int UB, int LPG_, int P, bool NT, int DYT, bool TILED>
 __global__ __launch_bounds__(256) void dequant_unpack_kernel(DequantArgs a) {
     using C = DequantCfg<YT, BITS, G, UB, LPG_, P, NT>;
     constexpr int UE = C::UE, STORES = C::STORES, CPL = C::CPL, LPG = C::LPG, GPP = C::GPP, W = C::W;
@@ -149,7 +150,7 @@ __global__ __launch_bounds__(256) void dequant_unpack_kernel(DequantArgs a) {
                 if (ok) {
 #pragma unroll
                     for (int l = 0; l < UE / DE; ++l)
-                        widen16<DYT>(ld16<false>((const char*)a.dy + dq_elem_index<G>(a, r, c * UE + l * DE) * DB),
+                        widen16<DYT>(ld16<false>((const char*)a.dy + dq_elem_index<G, TILED>(a, r, c * UE + l * DE) * DB),
                                      &g[l * DE]);
                 } else {
 #pragma unroll
@@ -169,7 +170,7 @@ __global__ __launch_bounds__(256) void dequant_unpack_kernel(DequantArgs a) {
                     v = make_uint4(pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3]), pack_bf16x2(o[4], o[5]),
                                    pack_bf16x2(o[6], o[7]));
                 }
-                if (ok) st16<NT>(yb + dq_elem_index<G>(a, r, c * UE + l * E16) * C::BYTES, v);
+                if (ok) st16<NT>(yb + dq_elem_index<G, TILED>(a, r, c * UE + l * E16) * C::BYTES, v);
             }
         }
     }

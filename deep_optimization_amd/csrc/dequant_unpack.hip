@@ -24,9 +24,17 @@ static int dq_launch(const DequantArgs& a, hipStream_t s) {
     const uint64_t waves = ((uint64_t)a.n_groups + C::GPW - 1) / C::GPW;
     const uint64_t blocks = (waves + C::WAVES - 1) / C::WAVES;
     if (blocks == 0) return 0;
-    hipLaunchKernelGGL((dequant_unpack_kernel<YT, BITS, G, S::UB, S::LPG, S::P, true, DYT>), dim3((uint32_t)blocks),
-                       dim3(64 * C::WAVES), 0, s, a);
-    return 0;
+    if (!a.tiled) {
+        hipLaunchKernelGGL((dequant_unpack_kernel<YT, BITS, G, S::UB, S::LPG, S::P, true, DYT, false>),
+                           dim3((uint32_t)blocks), dim3(64 * C::WAVES), 0, s, a);
+        return 0;
+    }
+    if constexpr (G == 64 || G == 256 || G == 1024) {  // the square group sizes
+        hipLaunchKernelGGL((dequant_unpack_kernel<YT, BITS, G, S::UB, S::LPG, S::P, true, DYT, true>),
+                           dim3((uint32_t)blocks), dim3(64 * C::WAVES), 0, s, a);
+        return 0;
+    }
+    return -1;
 }
 
 template <int YT, int BITS, int G>

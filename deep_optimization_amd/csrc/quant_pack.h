@@ -46,6 +46,14 @@ namespace dopt {
 //             tanh(clamp(gelu'(x), -3, 3)/0.5)*0.5 with the range floored at 1e-4
 //             (AC/modules/activations/kernel_implementation.py:496-535)
 //   PRE_SILU  the same for SiLU (kernel_implementation.py:225-243)
+// At 1 and 2 bits the fused activations find their codes by comparing the clamped derivative d
+// with the group's QMAX thresholds instead of evaluating the squash per element ("threshold
+// codes"): the squash s(d) = sigmoid(4d) is increasing, so the group's min / max of s are s of
+// the min / max of d, and code >= k exactly when s(d) >= s_k = fma(k - (0.5 - 1e-6), step, min),
+// i.e. when d >= t_k = logit(s_k) / 4. Each lane computes the QMAX thresholds of its group once
+// (v_rcp_f32 and v_log_f32 each), and an element costs QMAX compares instead of an exp, a
+// reciprocal and the code arithmetic. The codes differ from the per-element form only for d within
+// the thresholds' fp32 error (about 1e-7) of a boundary; scale and min are computed as before.
 enum { PRE_NONE = 0, PRE_REF = 1, PRE_GELU = 2, PRE_SILU = 3 };
 
 struct QuantPackArgs {
@@ -94,9 +102,12 @@ struct QuantPackCfg {
     static_assert(GPW <= 64, "scale/min gather uses one lane per group");
 };
 
-template <int G>
+// Element index of element e0 of group r. The layout is a template parameter: evaluated at run
+// time, the tile branch was if-converted into every load and store (an integer division by the
+// tile count per access), about a fifth of the fused activation kernels' instructions.
+template <int G, bool TILED>
 __device__ __forceinline__ uint64_t group_elem_index(const QuantPackArgs& a, uint32_t r, uint32_t e0) {
-    if (!a.tiled) return (uint64_t)r * G + e0;
+    if constexpr (!TILED) return (uint64_t)r * G + e0;
     // spatial tile gather of tensor_act_reshape_utils.py:115-125: group r = band*(W/s) + tw
     // holds x[.., band's tile row * s + e/s, tw*s + e%s]
     const uint32_t band = r / a.tiles_w;
@@ -159,13 +170,15 @@ __device__ __forceinline__ uint32_t pack_rne_codes(const float* z) {
     return acc;
 }
 
-template <int DT, int BITS, int G, int RN, int UB, int LPG_, int P, int PRE, bool NT>
+template <int DT, int BITS, int G, int RN, int UB, int LPG_, int P, int PRE, bool NT, bool TILED>
 __global__ __launch_bounds__(256) void quant_pack_kernel(QuantPackArgs a) {
     using C = QuantPackCfg<DT, BITS, G, RN, UB, LPG_, P>;
     constexpr int UE = C::UE, LOADS = C::LOADS, CPL = C::CPL, LPG = C::LPG, GPP = C::GPP, W = C::W;
     constexpr int UBITS = C::UBITS;
     constexpr int QMAX = (1 << BITS) - 1;
     constexpr int E16 = DType<DT>::per16;  // elements per 16-byte load
+    // threshold codes of the fused activations at 1 and 2 bits (see the PRE enum above)
+    constexpr bool THR = (PRE == PRE_GELU || PRE == PRE_SILU) && RN == RN_NEAREST && BITS <= 2;
 
     const int lane = threadIdx.x & 63;
     const int slot = lane / LPG;
@@ -188,7 +201,7 @@ __global__ __launch_bounds__(256) void quant_pack_kernel(QuantPackArgs a) {
             const uint32_t e0 = (uint32_t)(i * LPG + li) * UE;
             #pragma unroll
             for (int l = 0; l < LOADS; ++l)
-                raw[p][i][l] = ld16<NT>(xb + group_elem_index<G>(a, r, e0 + l * E16) * C::BYTES);
+                raw[p][i][l] = ld16<NT>(xb + group_elem_index<G, TILED>(a, r, e0 + l * E16) * C::BYTES);
             if constexpr (RN == RN_NOISE) {
                 #pragma unroll
                 for (int k = 0; k < UE / 4; ++k) nz[p][i][k] = ld16<NT>(a.noise + (uint64_t)r * G + e0 + 4 * k);
@@ -248,13 +261,17 @@ __global__ __launch_bounds__(256) void quant_pack_kernel(QuantPackArgs a) {
                         gelu_and_grad(v[i][k], yv[k], d);
                     else
                         silu_and_grad(v[i][k], yv[k], d);
-                    v[i][k] = sigmoid4_fast(__builtin_amdgcn_fmed3f(d, -3.0f, 3.0f));
+                    const float dc = __builtin_amdgcn_fmed3f(d, -3.0f, 3.0f);
+                    if constexpr (THR)
+                        v[i][k] = dc;
+                    else
+                        v[i][k] = sigmoid4_fast(dc);
                 }
                 if (r < a.n_groups) {
 #pragma unroll
                     for (int l = 0; l < LOADS; ++l) {
                         const float* o = &yv[l * E16];
-                        char* yb = (char*)a.y + group_elem_index<G>(a, r, e0 + l * E16) * 2;
+                        char* yb = (char*)a.y + group_elem_index<G, TILED>(a, r, e0 + l * E16) * 2;
                         if constexpr (E16 == 8)
                             *(uint4*)yb = make_uint4(pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3]),
                                                      pack_bf16x2(o[4], o[5]), pack_bf16x2(o[6], o[7]));
@@ -269,7 +286,8 @@ __global__ __launch_bounds__(256) void quant_pack_kernel(QuantPackArgs a) {
         // activation pre-transforms end in v_rcp_f32, whose result a VALU may read only after one
         // wait state, which the compiler enforces for its own instructions but not for inline
         // asm; their values are arithmetic results (canonical), so compiler min/max add nothing.
-        constexpr bool TRANS_IN = PRE == PRE_GELU || PRE == PRE_SILU;
+        // (threshold codes keep the clamped derivative, a v_med3 result: the raw forms apply)
+        constexpr bool TRANS_IN = (PRE == PRE_GELU || PRE == PRE_SILU) && !THR;
         float mn = v[0][0], mx = v[0][0];
         #pragma unroll
         for (int j = 1; j + 1 < CPL * UE; j += 2) {
@@ -307,6 +325,10 @@ __global__ __launch_bounds__(256) void quant_pack_kernel(QuantPackArgs a) {
             mx = __builtin_isnan(mx) ? __uint_as_float(0x7fc00000u) : mx;
         }
         group_minmax<LPG>(mn, mx);
+        if constexpr (THR) {  // min / max of the squash are the squash of the derivative's
+            mn = sigmoid4_fast(mn);
+            mx = sigmoid4_fast(mx);
+        }
         mn = mn + 0.0f;  // store -0.0 as +0.0
         float rng = mx - mn;
         if constexpr (PRE == PRE_GELU || PRE == PRE_SILU) rng = fmaxf(rng, 1e-4f);  // kernel_implementation.py:236, :529
@@ -317,7 +339,17 @@ __global__ __launch_bounds__(256) void quant_pack_kernel(QuantPackArgs a) {
             mn_p[p] = mn - 0.5f;
         else
             mn_p[p] = mn;
-        const bool clampq = wave_any(inv == __builtin_inff());
+        // thresholds t_k = logit(s_k) / 4 = (ln 2 / 4) log2(s_k / (1 - s_k)); an s_k >= 1 (beyond
+        // the group's max) gives +inf or NaN, which no derivative reaches
+        float thr[THR ? QMAX : 1];
+        if constexpr (THR) {
+#pragma unroll
+            for (int k = 0; k < QMAX; ++k) {
+                const float sk = __builtin_fmaf((float)(k + 1) - half_m, step, mn);
+                thr[k] = 0.17328679513998632f * __builtin_amdgcn_logf(sk * __builtin_amdgcn_rcpf(1.0f - sk));
+            }
+        }
+        const bool clampq = !THR && wave_any(inv == __builtin_inff());  // threshold codes need no clamp
 
         // codes + store; the clamped variant runs only for waves holding a group with inv = +inf
         auto emit = [&](auto clamp_tag) {
@@ -359,10 +391,17 @@ __global__ __launch_bounds__(256) void quant_pack_kernel(QuantPackArgs a) {
                     uint32_t q[UE];
                     #pragma unroll
                     for (int k = 0; k < UE; ++k) {
-                        float qf = __builtin_fmaf(v[i][k] - mn, inv, half_m);
-                        // NaN -> 0, as the reference's clamp
-                        if constexpr (CL) qf = __builtin_amdgcn_fmed3f(qf, 0.0f, qmaxf);
-                        q[k] = cvt_u32(qf);
+                        if constexpr (THR) {
+                            uint32_t c = 0;
+#pragma unroll
+                            for (int j = 0; j < QMAX; ++j) c += v[i][k] >= thr[j] ? 1u : 0u;
+                            q[k] = c;
+                        } else {
+                            float qf = __builtin_fmaf(v[i][k] - mn, inv, half_m);
+                            // NaN -> 0, as the reference's clamp
+                            if constexpr (CL) qf = __builtin_amdgcn_fmed3f(qf, 0.0f, qmaxf);
+                            q[k] = cvt_u32(qf);
+                        }
                     }
                     #pragma unroll
                     for (int j = 0; j < (UBITS >= 32 ? UBITS / 32 : 1); ++j) {

@@ -23,13 +23,15 @@ struct QuantPackShape {
     static constexpr int UBITS = UE * BITS;
     static constexpr int LPD = UBITS >= 32 ? 1 : 32 / UBITS;  // lanes merged per code dword
     // noise tensor and Philox: one unit per lane (Philox: 16 elements, one generator call; measured
-    // 3% faster than two units per lane at config 2); the VALU-heavy activation pre-transforms:
-    // four (more independent work per lane); otherwise two
-    static constexpr int L0 = RN == RN_NOISE || RN == RN_PHILOX ? CPG : (PRE == PRE_GELU || PRE == PRE_SILU) ? CPG / 4 : CPG / 2;
+    // 3% faster than two units per lane at config 2); otherwise two. The fused activations run
+    // GELU with two passes per wave, SiLU with one: measured on the ViT MLP activation (bf16
+    // [256,197,3072], g = 128) over 1-16 units per lane and 1-4 passes, two units per lane gave
+    // the fastest kernels at 1-8 bits (four units, 108 VGPRs for GELU, ran 4-10% slower)
+    static constexpr int L0 = RN == RN_NOISE || RN == RN_PHILOX ? CPG : CPG / 2;
     static constexpr int L1 = L0 < LPD ? LPD : L0;
     static constexpr int L2 = L1 < 2 ? 2 : L1;
     static constexpr int LPG = L2 > 64 ? 64 : L2;
-    static constexpr int P = 1;
+    static constexpr int P = PRE == PRE_GELU ? 2 : 1;
 };
 
 template <int DT, int BITS, int G, int RN, int PRE>
@@ -39,9 +41,17 @@ static int qp_launch(const QuantPackArgs& a, hipStream_t s) {
     const uint64_t waves = ((uint64_t)a.n_groups + C::GPW - 1) / C::GPW;
     const uint64_t blocks = (waves + C::WAVES - 1) / C::WAVES;
     if (blocks == 0) return 0;
-    hipLaunchKernelGGL((quant_pack_kernel<DT, BITS, G, RN, S::UB, S::LPG, S::P, PRE, false>), dim3((uint32_t)blocks),
-                       dim3(64 * C::WAVES), 0, s, a);
-    return 0;
+    if (!a.tiled) {
+        hipLaunchKernelGGL((quant_pack_kernel<DT, BITS, G, RN, S::UB, S::LPG, S::P, PRE, false, false>),
+                           dim3((uint32_t)blocks), dim3(64 * C::WAVES), 0, s, a);
+        return 0;
+    }
+    if constexpr (G == 64 || G == 256 || G == 1024) {  // the square group sizes
+        hipLaunchKernelGGL((quant_pack_kernel<DT, BITS, G, RN, S::UB, S::LPG, S::P, PRE, false, true>),
+                           dim3((uint32_t)blocks), dim3(64 * C::WAVES), 0, s, a);
+        return 0;
+    }
+    return -1;
 }
 
 template <int DT, int BITS, int G>
