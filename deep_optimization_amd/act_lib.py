@@ -19,7 +19,10 @@ tensor_act_reshape_utils.py:128 and :152.
 
 Every operator is registered straight with the dispatcher (``torch.library.Library``: one Python
 call per op, no wrapper layers) for CUDA (HIP) tensors only, and has a fake (meta)
-implementation with the correct output shapes; there is no CPU implementation.
+implementation with the correct output shapes; there is no CPU implementation. The operators the
+compressed layers call most often take their CUDA kernel from the native library instead
+(``_native``, csrc/torch_ops.cpp), with the same checks and outputs as the Python implementations
+here, which stay callable as functions.
 """
 from __future__ import annotations
 
@@ -28,7 +31,7 @@ from typing import Optional
 import torch
 from torch import Tensor
 
-from . import _lib
+from . import _lib, _native
 
 _DTYPE_CODE = {torch.float32: _lib.F32, torch.float16: _lib.F16, torch.bfloat16: _lib.BF16}
 _META_CODE = {torch.float32: _lib.F32, torch.bfloat16: _lib.BF16}
@@ -156,10 +159,13 @@ _LIB = torch.library.Library("act_lib", "DEF")
 
 
 def _op(schema: str, impl, fake):
-    """Define act_lib::<schema>, bind the HIP implementation and the fake (meta) kernel."""
+    """Define act_lib::<schema>, bind the HIP implementation and the fake (meta) kernel. The
+    operators of the native library (``_native.OPS``) get their CUDA kernel from it instead; their
+    Python implementation stays callable as a function."""
     name = schema.split("(", 1)[0]
     _LIB.define(schema)
-    _LIB.impl(name, impl, "CUDA")
+    if not _native.native(name):
+        _LIB.impl(name, impl, "CUDA")
     torch.library.register_fake(f"act_lib::{name}", fake, lib=_LIB)
     return getattr(torch.ops.act_lib, name)
 

@@ -67,8 +67,37 @@ def _compile(src: str) -> str:
     return obj
 
 
+TORCH_LIB = os.path.join(PKG, "libdopt_torch.so")
+INCLUDE = os.path.join(os.path.dirname(PKG), "include")
+
+
+def build_torch_ops(verbose: bool = False) -> str:
+    """The native act_lib operator kernels (csrc/torch_ops.cpp, host C++ against torch's headers and
+    libdopt.so) -> libdopt_torch.so next to libdopt.so."""
+    import torch
+    import torch.utils.cpp_extension as ce
+
+    cxx = shutil.which("g++") or "c++"
+    abi = int(torch._C._GLIBCXX_USE_CXX11_ABI)
+    incs = [f"-I{p}" for p in ce.include_paths(device_type="cuda")] + [f"-I{INCLUDE}"]
+    torch_lib = os.path.join(os.path.dirname(torch.__file__), "lib")
+    tmp = TORCH_LIB + ".tmp"
+    cmd = [cxx, "-O2", "-std=c++17", "-fPIC", "-shared", f"-D_GLIBCXX_USE_CXX11_ABI={abi}", "-DUSE_ROCM=1",
+           "-D__HIP_PLATFORM_AMD__=1", *incs, os.path.join(CSRC, "torch_ops.cpp"), f"-L{PKG}", "-ldopt",
+           f"-L{torch_lib}", "-lc10", "-lc10_hip", "-ltorch", "-ltorch_cpu", "-ltorch_hip",
+           "-Wl,-rpath,$ORIGIN", f"-Wl,-rpath,{torch_lib}", "-o", tmp]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"torch_ops.cpp failed to build:\n{proc.stderr[-4000:]}")
+    os.replace(tmp, TORCH_LIB)
+    if verbose:
+        print(f"built {TORCH_LIB}")
+    return TORCH_LIB
+
+
 def build(jobs: int | None = None, verbose: bool = False) -> str:
-    """Compile every source for gfx950 and link libdopt.so next to this file; returns its path."""
+    """Compile every source for gfx950, link libdopt.so next to this file and build the native
+    operator library on it; returns libdopt.so's path."""
     os.makedirs(OBJ_DIR, exist_ok=True)
     jobs = jobs or min(len(SOURCES), os.cpu_count() or 4, 8)
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
@@ -81,6 +110,7 @@ def build(jobs: int | None = None, verbose: bool = False) -> str:
     os.replace(tmp, LIB)
     if verbose:
         print(f"built {LIB}")
+    build_torch_ops(verbose)
     return LIB
 
 

@@ -10,8 +10,8 @@
   (module_utils.py:86-102 with ops.py:457-474), the operators themselves being bit-exact against
   the CPU oracle elsewhere.
 * ``Controller.warmup`` / ``enable_graph_mode`` (controller.py:316-351): the rewritten model's
-  forward and backward replay HIP graphs; three SGD steps give the losses and gradients of an
-  eager copy of the same rewrite.
+  forward and backward replay HIP graphs and give the losses and gradients of an eager copy of the
+  same rewrite on three batches, before and after an in-place change of every parameter.
 """
 import copy
 
@@ -139,22 +139,31 @@ def test_warmup_graph_mode_matches_eager(restore_matmul_flags):
         crit(eager(batches[0][0]), batches[0][1]).backward()
     for (n_, pe), pg in zip(eager.named_parameters(), graphed.parameters()):
         assert rel_err(pg.grad, pe.grad) <= 1e-3, n_
-    opts = [torch.optim.SGD(m.parameters(), lr=0.05) for m in (eager, graphed)]
-    for step, (x, y) in enumerate(batches):
-        losses = []
-        for m, opt in zip((eager, graphed), opts):
-            opt.zero_grad(set_to_none=True)
-            with torch.autocast("cuda", dtype=torch.bfloat16):
-                loss = crit(m(x), y)
-            loss.backward()
-            losses.append(loss.item())
-        worst = max(rel_err(pg.grad, pe.grad) for pe, pg in zip(eager.parameters(), graphed.parameters()))
-        print(f"[graph mode] step {step}: loss eager {losses[0]:.6f} graph {losses[1]:.6f}, "
-              f"worst grad rel err {worst:.2e}", flush=True)
-        assert abs(losses[1] - losses[0]) <= 1e-4 * abs(losses[0])
-        assert worst <= 1e-3
-        for opt in opts:
-            opt.step()
+    # three batches, then the same in-place change of every parameter in both models (the graphs
+    # read the parameters where they live), then the three batches again; each compared with the
+    # eager copy. (Comparing over optimizer steps instead would amplify the ~1e-5 differences of
+    # the patch convolution's weight gradient, whose solver is MIOpen's choice, through the
+    # training dynamics.)
+    for rnd in range(2):
+        if rnd == 1:
+            with torch.no_grad():
+                for pe, pg in zip(eager.parameters(), graphed.parameters()):
+                    delta = torch.randn_like(pe) * 0.01 * pe.abs().mean().clamp_min(1e-3)
+                    pe.mul_(0.9).add_(delta)
+                    pg.mul_(0.9).add_(delta)
+        for step, (x, y) in enumerate(batches):
+            losses = []
+            for m in (eager, graphed):
+                m.zero_grad(set_to_none=True)
+                with torch.autocast("cuda", dtype=torch.bfloat16):
+                    loss = crit(m(x), y)
+                loss.backward()
+                losses.append(loss.item())
+            worst = max(rel_err(pg.grad, pe.grad) for pe, pg in zip(eager.parameters(), graphed.parameters()))
+            print(f"[graph mode] round {rnd} batch {step}: loss eager {losses[0]:.6f} graph {losses[1]:.6f}, "
+                  f"worst grad rel err {worst:.2e}", flush=True)
+            assert abs(losses[1] - losses[0]) <= 1e-4 * abs(losses[0])
+            assert worst <= 1e-3
     assert len(graphed._dopt_graph_captures) == 1  # every step replayed the one capture
     # eval and no-grad calls run the eager forward
     graphed.eval()

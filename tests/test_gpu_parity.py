@@ -305,12 +305,13 @@ def test_mismatched_sizes_are_rejected_before_launch():
 
 
 def test_tensors_off_the_current_device_are_rejected(monkeypatch):
-    """The C ABI launches on the current device; a tensor elsewhere raises (simulated by making
-    the current-device query answer another index)."""
-    x = torch.randn((2, 4, 256), device=DEV).to(torch.bfloat16)
+    """The C ABI launches on the current device; an operator implemented in Python raises for a
+    tensor elsewhere (simulated by making the current-device query answer another index). The
+    native operators (csrc/torch_ops.cpp) make the tensor's device current instead."""
+    x = torch.randint(0, 4, (2, 4, 256), dtype=torch.int8, device=DEV)
     monkeypatch.setattr(torch.cuda, "current_device", lambda: x.get_device() + 1)
     with pytest.raises(RuntimeError, match="current device"):
-        torch.ops.act_lib.quant_pack(x, 2, 256, False, 0.0, False, 0, None, 0, 0, torch.float32)
+        torch.ops.act_lib.pack_triton(x, 2, 256)
 
 
 def test_bad_bits_raise_value_error_on_device():
