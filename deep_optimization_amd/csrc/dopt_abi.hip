@@ -99,8 +99,10 @@ int bn_geom(int64_t N, int64_t C, int64_t HW, int64_t stride_n, int64_t stride_c
     if (N < 0 || C < 0 || HW < 0 || C > 65535)
         return fail(DOPT_EINVAL, "BatchNorm shape must have N, HW >= 0 and 0 <= C <= 65535, got N=%lld C=%lld HW=%lld",
                     (long long)N, (long long)C, (long long)HW);
-    if (N * HW >= ((int64_t)1 << 31))
-        return fail(DOPT_EINVAL, "BatchNorm channel too large: N*HW=%lld (limit 2^31 - 1)", (long long)(N * HW));
+    // the kernels' grids run the channels along x and the channel's BN_CHUNK-element chunks along y
+    if (N * HW > (int64_t)65535 * dopt::BN_CHUNK)
+        return fail(DOPT_EINVAL, "BatchNorm channel too large: N*HW=%lld (limit 65535 * %lld = %lld)", (long long)(N * HW),
+                    (long long)dopt::BN_CHUNK, (long long)(65535 * dopt::BN_CHUNK));
     if (stride_n < 0 || stride_c < 0) return fail(DOPT_EINVAL, "BatchNorm strides must be non-negative");
     *g = dopt::BnGeom{N, C, HW, stride_n, stride_c};
     return DOPT_OK;
