@@ -331,8 +331,12 @@ inline int fp8_gemm_launch(const uint8_t* A, const uint8_t* B, int64_t M, int64_
 //
 // The MFMA takes B's fragment as its first operand and A's as its second, which transposes the
 // accumulator: lane l holds row i*32 + l%32 of A's tile and, in registers 4q..4q+3, the four
-// consecutive columns j*32 + 8q + 4*(l/32) + {0..3}. Each lane writes 8-byte runs of bf16 into
-// the staging rows, and 16-byte row chunks go out with whole-row coalescing.
+// consecutive columns j*32 + 8q + 4*(l/32) + {0..3}: lanes l and l + 32 hold the two 8-byte halves
+// of the 16-byte chunk of columns j*32 + 8q + {0..7}. For a pair q, q + 1 one v_permlane32_swap
+// per dword gives lane l the whole chunk q and lane l + 32 the whole chunk q + 1, so the staging
+// rows are written with 16-byte stores (8-byte stores of the halves measured 2^20 LDS bank-conflict
+// cycles per 8192^3 call; whole chunks, 16 lanes to a 256-byte bank row, none), and 16-byte row
+// chunks go out with whole-row coalescing.
 template <class C, bool EDGE>
 __global__ __launch_bounds__(256, 1) void fp8_gemm_nt_persistent_kernel(Fp8GemmArgs p) {
     constexpr int BM = C::BM, BN = C::BN, BK = C::BK, TM = C::TM, TN = C::TN, WM = C::WM, WN = C::WN;
@@ -500,11 +504,18 @@ __global__ __launch_bounds__(256, 1) void fp8_gemm_nt_persistent_kernel(Fp8GemmA
                 v16f_t t = acc[i][j];
                 asm volatile("" : "+v"(t));
 #pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    const v2u_t w = {pack_bf16x2(t[4 * q] * p.out_scale, t[4 * q + 1] * p.out_scale),
-                                     pack_bf16x2(t[4 * q + 2] * p.out_scale, t[4 * q + 3] * p.out_scale)};
-                    const int c = (j * 32 + 8 * q) / 8;
-                    *(v2u_t*)(stage + (er * (WN * 2) + ((c ^ (er & (CPR - 1))) * 16) + 8 * h)) = w;
+                for (int q = 0; q < 4; q += 2) {
+                    // own halves of chunks q and q + 1; after the swaps lane l holds chunk q and
+                    // lane l + 32 chunk q + 1, both as {x[0], y[0], x[1], y[1]}
+                    const uint32_t w0x = pack_bf16x2(t[4 * q] * p.out_scale, t[4 * q + 1] * p.out_scale);
+                    const uint32_t w0y = pack_bf16x2(t[4 * q + 2] * p.out_scale, t[4 * q + 3] * p.out_scale);
+                    const uint32_t w1x = pack_bf16x2(t[4 * q + 4] * p.out_scale, t[4 * q + 5] * p.out_scale);
+                    const uint32_t w1y = pack_bf16x2(t[4 * q + 6] * p.out_scale, t[4 * q + 7] * p.out_scale);
+                    const auto x = __builtin_amdgcn_permlane32_swap(w0x, w1x, false, false);
+                    const auto y = __builtin_amdgcn_permlane32_swap(w0y, w1y, false, false);
+                    const v4u_t chunk = {x[0], y[0], x[1], y[1]};
+                    const int c = 4 * j + q + h;
+                    *(v4u_t*)(stage + (er * (WN * 2) + ((c ^ (er & (CPR - 1))) * 16))) = chunk;
                 }
             }
 #pragma unroll
