@@ -2,9 +2,10 @@
 //   C[m][n] = bf16(out_scale * sum_k A[m][k] * B[n][k]), fp32 accumulation, one rounding.
 // Any M, N >= 0; K a multiple of 16 (one 16-byte load per lane); A, B rows 16-byte aligned.
 //
-// Two kernels share the tiling below: fp8_gemm_nt_kernel computes one tile per workgroup, and
-// fp8_gemm_nt_persistent_kernel (further down, the launcher's choice for an even, non-zero
-// number of K slabs) runs one workgroup per CU over a list of tiles.
+// Three kernels share the tiling below: fp8_gemm_nt_kernel computes one tile per workgroup, and
+// fp8_gemm_nt_persistent_kernel and fp8_gemm16_persistent_kernel (further down, the launcher's
+// choice for an even, non-zero number of K slabs; the second on 16x16x128 MFMAs for large K) run
+// one workgroup per CU over a list of tiles.
 //
 // Tiling: a workgroup of 4 waves (2 x 2) computes a BM x BN tile; each wave a (BM/2) x (BN/2)
 // sub-tile as TM x TN blocks of v_mfma_f32_32x32x64_f8f6f4 (fp8 x fp8 -> fp32, 32 x 32 x 64 per
@@ -622,10 +623,354 @@ __global__ __launch_bounds__(256, 1) void fp8_gemm_nt_persistent_kernel(Fp8GemmA
     __builtin_amdgcn_s_waitcnt(0);
 }
 
-// Persistent launch: min(tiles, CUs) workgroups (n_cu from the caller). An odd or zero slab
-// count (K / BK rounded up) takes the non-persistent kernel (which writes C = 0 for K = 0), and
-// so does a device with fewer CUs than XCDs: the tile list gives every XCD with tiles at least one
-// workgroup only when the grid has min(tiles, GEMM_XCDS) or more.
+// ---------------------------------------------------------------------------------------------
+// The same persistent kernel on v_mfma_f32_16x16x128_f8f6f4 (fp8 x fp8 -> fp32, 16 x 16 x 128 per
+// instruction, half the work of the 32x32x64 form in half its cycles). On training-like operands
+// the part's clock follows its power draw, and an MFMA stream of this shape draws less per flop:
+// an instruction-stream probe sustains 3.96 PF/s against 3.47 for 32x32x64 on random e4m3 data
+// (4.8 PF/s for both on constant data). At 8192^3 the kernel takes ~2% more cycles than
+// fp8_gemm_nt_persistent_kernel and runs ~5% faster on random operands; at K = 4096 the two are
+// within noise of each other, so the launcher picks this form for K >= FP8_MFMA16_MIN_K.
+//
+// Same tiles, tile list, LDS buffers and buffer-resource loads as fp8_gemm_nt_persistent_kernel.
+// A wave's 128 x 128 tile is 8 x 8 blocks of 16 x 16; fragment i of A (and of B) is 16 rows x
+// 128 K bytes, lane l supplying row l % 16 and the 32 K bytes from 32 (l / 16): two 16-byte LDS
+// reads. The MFMA takes B's fragment first, so lane l holds row 16 i + l % 16 and columns
+// 16 j + 4 (l / 16) + {0..3} of block (i, j). The epilogue pairs fragment rows 2i and 2i + 1:
+// one v_permlane16_swap per dword gives lanes with even l / 16 the whole 16-byte chunk of row
+// l % 16 and lanes with odd l / 16 that of row 16 + l % 16, so the staging rows are written with
+// 16-byte stores.
+typedef float v4f_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ v4f_t mfma_fp8_16x16x128(const v8i_t& a, const v8i_t& b, const v4f_t& c) {
+    // cbsz = blgp = 0: both operands OCP fp8 e4m3; scale operands 0 select the unscaled MFMA.
+    return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
+}
+
+constexpr int64_t FP8_MFMA16_MIN_K = 8192;
+
+template <class C, bool EDGE>
+__global__ __launch_bounds__(256, 1) void fp8_gemm16_persistent_kernel(Fp8GemmArgs p) {
+    constexpr int BM = C::BM, BN = C::BN, BK = C::BK, TM = C::TM, TN = C::TN, WM = C::WM, WN = C::WN;
+    constexpr int CPR = WN / 8;             // 16-byte chunks per staged row
+    constexpr int ESTAGE = 32 * WN * 2;     // bytes staged per wave: 32 rows of its tile
+    static_assert(CPR == 8 || CPR == 16, "staging swizzle");
+    const int64_t M = p.M, N = p.N, K = p.K, lda = p.lda, ldb = p.ldb, ldc = p.ldc;
+    __shared__ __attribute__((aligned(1024))) uint8_t sA0[BM * BK];
+    __shared__ __attribute__((aligned(1024))) uint8_t sA1[BM * BK];
+    __shared__ __attribute__((aligned(1024))) uint8_t sB0[BN * BK];
+    __shared__ __attribute__((aligned(1024))) uint8_t sB1[BN * BK];
+    __shared__ __attribute__((aligned(1024))) uint8_t sE[4 * ESTAGE];
+
+    // ---- this workgroup's tiles
+    const uint32_t tiles_m = p.tiles_m, tiles_n = p.tiles_n;
+    const uint32_t n_tiles = tiles_m * tiles_n;
+    const uint32_t G = gridDim.x, bid = blockIdx.x;
+    const uint32_t xcd = bid % GEMM_XCDS, local = bid / GEMM_XCDS;
+    const uint32_t g_x = G / GEMM_XCDS + (xcd < G % GEMM_XCDS ? 1u : 0u);
+    const uint32_t per = n_tiles / GEMM_XCDS, rem = n_tiles % GEMM_XCDS;
+    const uint32_t first = xcd * per + min(xcd, rem), cnt = per + (xcd < rem ? 1u : 0u);
+    const uint32_t my = local < cnt ? (cnt - local + g_x - 1) / g_x : 0u;
+    const uint32_t nk = (uint32_t)((K + BK - 1) / BK);
+    const uint32_t total = my * nk;
+    if (total == 0) return;  // the same for every wave of the workgroup
+    auto coords = [&](uint32_t i, uint32_t& tm, uint32_t& tn) __attribute__((always_inline)) {
+        const uint32_t t = first + local + i * g_x;
+        const uint32_t group = C::GROUP_M * tiles_n;
+        const uint32_t first_m = (t / group) * C::GROUP_M;
+        const uint32_t gsize = min(tiles_m - first_m, (uint32_t)C::GROUP_M);
+        tm = first_m + (t % group) % gsize;
+        tn = (t % group) / gsize;
+    };
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: tile bases stay scalar
+    const int wm = wave >> 1, wn = wave & 1;
+
+    // ---- global -> LDS slab loads (lane mapping as in fp8_gemm_nt_kernel), two slabs ahead of the
+    // compute side. LDS chunk swizzle for this fragment shape: logical chunk c of row r at c ^ f(r),
+    // f(r) = r3 | r1 << 1 | r2 << 2 (rn = bit n of r); for row r = 8 (4 j + wave) + lane / 8
+    const int lrow8 = lane >> 3;
+    const int lchunk = (lane & 7) ^ ((wave & 1) | (((lane >> 4) & 1) << 1) | (((lane >> 5) & 1) << 2));
+    const int r0 = 8 * wave + lrow8;
+    const uint32_t offa0 = (uint32_t)(r0 * lda + lchunk * 16), offb0 = (uint32_t)(r0 * ldb + lchunk * 16);
+    const uint32_t stepa = (uint32_t)(32 * lda), stepb = (uint32_t)(32 * ldb);
+    // Slab k of the compute side issues slab k+2 of the stream (for the last two slabs of a tile,
+    // slab k+2-nk of the next tile), as in fp8_gemm_nt_persistent_kernel; `parts` selects the A
+    // loads (1), the B loads (2) or both.
+    struct IssueTile {
+        __amdgpu_buffer_rsrc_t ra, rb;
+        int rows_a, rows_b;
+        bool live;
+    };
+    auto issue_tile = [&](uint32_t i) __attribute__((always_inline)) {
+        IssueTile t;
+        uint32_t tm, tn;
+        t.live = i < my;
+        coords(t.live ? i : my - 1, tm, tn);
+        const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
+        t.ra = __builtin_amdgcn_make_buffer_rsrc((void*)(p.A + m0 * lda), (short)0, (int)GEMM_RANGE, 0x00020000);
+        t.rb = __builtin_amdgcn_make_buffer_rsrc((void*)(p.B + n0 * ldb), (short)0, (int)GEMM_RANGE, 0x00020000);
+        t.rows_a = EDGE ? (int)min((int64_t)BM, M - m0) - r0 : BM;
+        t.rows_b = EDGE ? (int)min((int64_t)BN, N - n0) - r0 : BN;
+        return t;
+    };
+    IssueTile cur_t = issue_tile(0), next_t = issue_tile(1);
+    auto issue = [&](uint8_t* sa, uint8_t* sb, uint32_t ks, int parts = 3) __attribute__((always_inline)) {
+        const bool nxt = ks >= nk;
+        const __amdgpu_buffer_rsrc_t ra = nxt ? next_t.ra : cur_t.ra;
+        const __amdgpu_buffer_rsrc_t rb = nxt ? next_t.rb : cur_t.rb;
+        const bool live = nxt ? next_t.live : cur_t.live;
+        const int64_t k0 = (int64_t)(nxt ? ks - nk : ks) * BK;
+        const uint32_t va = live ? offa0 : GEMM_OOB, vb = live ? offb0 : GEMM_OOB;
+        int la = C::BM, lb = C::BN;
+        if constexpr (EDGE) {
+            const bool k_ok = k0 + lchunk * 16 < K;
+            la = k_ok ? (nxt ? next_t.rows_a : cur_t.rows_a) : 0;
+            lb = k_ok ? (nxt ? next_t.rows_b : cur_t.rows_b) : 0;
+        }
+        if (parts & 1)
+#pragma unroll
+        for (int j = 0; j < C::LA; ++j)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_void_t*)(sa + wave * 1024 + j * 4096), 16,
+                                                     !EDGE || 32 * j < la ? va : GEMM_OOB,
+                                                     (int)(j * stepa + (uint32_t)k0), 0, 0);
+        if (parts & 2)
+#pragma unroll
+        for (int j = 0; j < C::LB; ++j)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_void_t*)(sb + wave * 1024 + j * 4096), 16,
+                                                     !EDGE || 32 * j < lb ? vb : GEMM_OOB,
+                                                     (int)(j * stepb + (uint32_t)k0), 0, 0);
+    };
+
+    // ---- operands: fragment i of A is rows WM*wm + 16 i + lane % 16, K bytes 32 (lane / 16) .. + 32
+    // (logical chunks oc, oc + 1 at positions chunk ^ f(row) = chunk ^ sw; the fragment's base row
+    // is a multiple of 16, so f depends on lane % 16 only)
+    const int orow = lane & 15;
+    const int oc = 2 * (lane >> 4);
+    const int sw = ((lane >> 3) & 1) | (((lane >> 1) & 1) << 1) | (((lane >> 2) & 1) << 2);  // f(lane % 16)
+    const int pa0 = (oc ^ sw) * 16, pa1 = ((oc + 1) ^ sw) * 16;
+    auto read_frag = [&](const uint8_t* s, int base_row) __attribute__((always_inline)) -> v8i_t {
+        const int o = (base_row + orow) * BK;
+        const v4u_t x0 = *(const v4u_t*)(s + (o + pa0));
+        const v4u_t x1 = *(const v4u_t*)(s + (o + pa1));
+        return __builtin_bit_cast(v8i_t, __builtin_shufflevector(x0, x1, 0, 1, 2, 3, 4, 5, 6, 7));
+    };
+    auto read_a = [&](const uint8_t* s, int i) __attribute__((always_inline)) { return read_frag(s, WM * wm + 16 * i); };
+    auto read_b = [&](const uint8_t* s, int j) __attribute__((always_inline)) { return read_frag(s, WN * wn + 16 * j); };
+
+    constexpr int FM = WM / 16, FN = WN / 16, HM = FM / 2;
+    v4f_t acc[FM][FN];
+    auto zero_acc = [&]() __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int j = 0; j < FN; ++j) acc[i][j] = v4f_t{0.0f, 0.0f, 0.0f, 0.0f};
+    };
+    zero_acc();
+    v8i_t a[FM], b[FN];
+
+    // ---- epilogue of compute tile i: scale, round once to bf16, stage 32 rows of the wave's tile
+    // at a time (16-byte chunk c of row r at position c ^ (r % CPR)), store row chunks (as in
+    // fp8_gemm_nt_persistent_kernel)
+    uint8_t* stage = sE + wave * ESTAGE;
+    auto epilogue = [&](uint32_t i_tile) __attribute__((always_inline)) {
+        uint32_t tm, tn;
+        coords(i_tile, tm, tn);
+        const int64_t row0 = (int64_t)tm * BM + WM * wm, col0 = (int64_t)tn * BN + WN * wn;
+        // the lane index passes through an empty asm so that the addresses below are computed
+        // here, once per tile, instead of being hoisted out of the tile loop into registers
+        int ln = lane;
+        asm volatile("" : "+v"(ln));
+        uint32_t ldc2 = (uint32_t)ldc * 2;  // row pitch of C in bytes (< GEMM_RANGE / BM on this path)
+        asm volatile("" : "+s"(ldc2));
+        const int rr = ln / CPR, rc = ln % CPR;  // read side: row rr + r * (64 / CPR), chunk rc
+        // whole tiles: one buffer resource per tile, the lane's offset in voffset and the row
+        // block's in soffset
+        const __amdgpu_buffer_rsrc_t rcs = __builtin_amdgcn_make_buffer_rsrc(
+            (void*)(p.C + row0 * ldc + col0), (short)0, (int)GEMM_RANGE, 0x00020000);
+        const uint32_t vo = (uint32_t)rr * ldc2 + (uint32_t)rc * 16;
+#pragma unroll
+        for (int i = 0; i < TM; ++i) {  // 32-row blocks: fragment rows 2i, 2i + 1
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int j = 0; j < FN; ++j) {
+                // lane l holds rows 16 f + l % 16 (f = 0, 1), columns 16 j + 4 (l / 16) + {0..3}; one
+                // permlane16 swap per dword gives lanes with even l / 16 the whole 16-byte chunk of
+                // row l % 16 and lanes with odd l / 16 the chunk of row 16 + l % 16
+                v4f_t t0 = acc[2 * i][j], t1 = acc[2 * i + 1][j];
+                asm volatile("" : "+v"(t0), "+v"(t1));
+                const uint32_t w0x = pack_bf16x2(t0[0] * p.out_scale, t0[1] * p.out_scale);
+                const uint32_t w0y = pack_bf16x2(t0[2] * p.out_scale, t0[3] * p.out_scale);
+                const uint32_t w1x = pack_bf16x2(t1[0] * p.out_scale, t1[1] * p.out_scale);
+                const uint32_t w1y = pack_bf16x2(t1[2] * p.out_scale, t1[3] * p.out_scale);
+                const auto x = __builtin_amdgcn_permlane16_swap(w0x, w1x, false, false);
+                const auto y = __builtin_amdgcn_permlane16_swap(w0y, w1y, false, false);
+                const v4u_t chunk = {x[0], y[0], x[1], y[1]};
+                const int q4 = ln >> 4, srow = 16 * (q4 & 1) + (ln & 15);
+                const int c = 2 * j + (q4 >> 1);
+                *(v4u_t*)(stage + (srow * (WN * 2) + ((c ^ (srow & (CPR - 1))) * 16))) = chunk;
+            }
+#pragma unroll
+            for (int r = 0; r < 32 * CPR / 64; ++r) {
+                const int row = rr + r * (64 / CPR);
+                const v4u_t v = *(const v4u_t*)(stage + (row * (WN * 2) + ((rc ^ (row & (CPR - 1))) * 16)));
+                const int grow = i * 32 + row;
+                if constexpr (!EDGE) {
+                    __builtin_amdgcn_raw_buffer_store_b128(v, rcs, vo,
+                                                           (int)((uint32_t)(i * 32 + r * (64 / CPR)) * ldc2), 0);
+                } else {
+                    if (row0 + grow >= M) continue;
+                    const int64_t n = col0 + rc * 8;
+                    uint16_t* dst = p.C + (row0 + grow) * ldc + n;
+                    if (p.vec_store && n + 8 <= N) {
+                        *(v4u_t*)dst = v;
+                    } else {
+                        const uint16_t e8[8] = {(uint16_t)v.x, (uint16_t)(v.x >> 16), (uint16_t)v.y,
+                                                (uint16_t)(v.y >> 16), (uint16_t)v.z, (uint16_t)(v.z >> 16),
+                                                (uint16_t)v.w, (uint16_t)(v.w >> 16)};
+                        for (int e = 0; e < 8 && n + e < N; ++e) dst[e] = e8[e];
+                    }
+                }
+            }
+        }
+    };
+
+    // ---- one slab of the stream (sa/sb hold slab k, na/nb slab k+1), two barriers. a[0..HM) and b[]
+    // hold slab k's fragments, read during slab k-1. Fragment rows 0..HM-1 run column by column:
+    // after column 0 (CB columns), barrier 1, once every wave's reads of slab k's B fragments
+    // are complete, gives sb to slab k+2's B loads, spread over columns 1..FN-1 together with
+    // the reads of a[HM..FM) from sa. After barrier 2 (mid-slab) sa takes slab k+2's A loads,
+    // spread over rows HM..FM-1, and slab k+1's fragments are read into registers whose last use
+    // has passed: a[0..HM) first, b[j] after column j. (With both halves' loads issued after
+    // one barrier, sixteen loads fell into a quarter of the slab's 32-cycle MFMA gaps and
+    // stalled the wave: 11% more cycles than without loads, against 2% this way.) The LAST slab
+    // of a tile leaves slab k+1's fragment reads to after the epilogue.
+    // Vector memory operations complete in issue order and vmcnt counts stores too: at barrier 2
+    // the LB B loads just issued (and after an epilogue its EPI_STORES stores, an exact count:
+    // whole-chunk stores, no EDGE instance) may stay in flight; everything before them (slab
+    // k+1's loads) has landed.
+    constexpr int EPI_STORES = TM * (32 * CPR / 64);
+    constexpr int WAIT_LGKM0 = 15 | (3 << 14) | (7 << 4);  // lgkmcnt(0), vmcnt and expcnt not waited for    constexpr int WAIT_LGKM0 = 63 /*vmcnt lo*/ | (3 << 14) /*vmcnt hi*/ | (7 << 4) /*expcnt*/;  // lgkmcnt(0) only
+    constexpr int W2 = C::LB, W2E = C::LB + EPI_STORES;
+    static_assert(W2E < 64, "vmcnt field");
+    constexpr int WAIT2 = (W2 & 15) | ((W2 >> 4) << 14) | (7 << 4);
+    constexpr int WAIT2E = (W2E & 15) | ((W2E >> 4) << 14) | (7 << 4);
+    auto slab = [&](uint8_t* sa, uint8_t* sb, uint8_t* na, uint8_t* nb, uint32_t k, auto last, auto epi)
+                    __attribute__((always_inline)) {
+        constexpr bool LAST = decltype(last)::value;
+        constexpr bool EPI = decltype(epi)::value;
+        constexpr bool AFTER_EPI = EPI && !EDGE;
+        constexpr int CB = 1;  // columns before barrier 1
+#pragma unroll
+        for (int j = 0; j < CB; ++j)
+#pragma unroll
+            for (int i = 0; i < HM; ++i) acc[i][j] = mfma_fp8_16x16x128(b[j], a[i], acc[i][j]);
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_waitcnt(WAIT_LGKM0);
+        asm volatile("s_barrier" ::: "memory");
+        issue(sa, sb, k + 2, 2);
+#pragma unroll
+        for (int i = HM; i < FM; ++i) a[i] = read_a(sa, i);
+#pragma unroll
+        for (int j = CB; j < FN; ++j)
+#pragma unroll
+            for (int i = 0; i < HM; ++i) acc[i][j] = mfma_fp8_16x16x128(b[j], a[i], acc[i][j]);
+        constexpr int NA = HM * (FN - CB), PER = NA / C::LB;
+        // columns 1..FN-1: HM * (FN - 1) MFMAs beside LB loads and 2 (FM - HM) operand reads
+        static_assert(PER >= 2, "two MFMAs per load after barrier 1");
+#pragma unroll
+        for (int q = 0; q < C::LB; ++q) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            if (PER > 2) __builtin_amdgcn_sched_group_barrier(0x008, PER - 2, 0);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x008, NA - PER * C::LB, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (AFTER_EPI) __builtin_amdgcn_s_waitcnt(WAIT2E);
+        else if constexpr (EPI) __builtin_amdgcn_s_waitcnt(0);
+        else __builtin_amdgcn_s_waitcnt(WAIT2);
+        asm volatile("s_barrier" ::: "memory");
+        issue(sa, sb, k + 2, 1);
+        if constexpr (!LAST) {
+#pragma unroll
+            for (int i = 0; i < HM; ++i) a[i] = read_a(na, i);
+        }
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+#pragma unroll
+            for (int i = HM; i < FM; ++i) acc[i][j] = mfma_fp8_16x16x128(b[j], a[i], acc[i][j]);
+            if constexpr (!LAST) b[j] = read_b(nb, j);
+        }
+        // second half: (FM - HM) * FN MFMAs beside LA loads and (not LAST) 2 (HM + FN) reads
+        if constexpr (!LAST) {
+#pragma unroll
+            for (int q = 0; q < C::LA; ++q) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            }
+        } else {
+#pragma unroll
+            for (int q = 0; q < C::LA; ++q) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+                __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+            }
+        }
+    };
+    using BF = std::integral_constant<bool, false>;
+    using BT = std::integral_constant<bool, true>;
+
+    issue(sA0, sB0, 0);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    issue(sA1, sB1, 1);
+#pragma unroll
+    for (int i = 0; i < HM; ++i) a[i] = read_a(sA0, i);
+#pragma unroll
+    for (int j = 0; j < FN; ++j) b[j] = read_b(sB0, j);
+    // nk is even, so every tile starts in buffer 0. The first slab of each later tile follows its
+    // predecessor's epilogue in straight-line code, so that the compiler's own wait bookkeeping
+    // sees the stores in flight on one path only and adds no waits of its own to that slab.
+    slab(sA0, sB0, sA1, sB1, 0, BF{}, BF{});
+    for (uint32_t it = 0;;) {
+        for (uint32_t k = 1; k + 2 < nk; k += 2) {
+            slab(sA1, sB1, sA0, sB0, k, BF{}, BF{});
+            slab(sA0, sB0, sA1, sB1, k + 1, BF{}, BF{});
+        }
+        slab(sA1, sB1, sA0, sB0, nk - 1, BT{}, BF{});
+        __builtin_amdgcn_sched_barrier(0);
+        epilogue(it);
+        __builtin_amdgcn_sched_barrier(0);
+        zero_acc();
+        // the next slab's loads were covered by the last slab's wait
+#pragma unroll
+        for (int i = 0; i < HM; ++i) a[i] = read_a(sA0, i);
+#pragma unroll
+        for (int j = 0; j < FN; ++j) b[j] = read_b(sB0, j);
+        if (++it == my) break;
+        cur_t = next_t;
+        next_t = issue_tile(it + 1);
+        slab(sA0, sB0, sA1, sB1, 0, BF{}, BT{});
+    }
+    // the loads issued past the last slab write zeros into LDS: they land before the workgroup ends
+    __builtin_amdgcn_s_waitcnt(0);
+}
+
+// Persistent launch: min(tiles, CUs) workgroups (n_cu from the caller), the 16x16x128 form for
+// K >= FP8_MFMA16_MIN_K. An odd or zero slab count (K / BK rounded up) takes the non-persistent
+// kernel (which writes C = 0 for K = 0), and so does a device with fewer CUs than XCDs: the tile
+// list gives every XCD with tiles at least one workgroup only when the grid has
+// min(tiles, GEMM_XCDS) or more.
 template <class C>
 inline int fp8_gemm_persistent_launch(const uint8_t* A, const uint8_t* B, int64_t M, int64_t N, int64_t K,
                                       int64_t lda, int64_t ldb, float out_scale, uint16_t* Cm, int64_t ldc,
@@ -639,10 +984,18 @@ inline int fp8_gemm_persistent_launch(const uint8_t* A, const uint8_t* B, int64_
     if (nk == 0 || nk % 2 || n_cu < GEMM_XCDS)
         return fp8_gemm_launch<C>(A, B, M, N, K, lda, ldb, out_scale, Cm, ldc, s);
     // whole tiles with aligned C store through a buffer resource: a tile's offsets must stay in range
-    if (M % C::BM == 0 && N % C::BN == 0 && K % C::BK == 0 && p.vec_store && (int64_t)C::BM * ldc * 2 < GEMM_RANGE)
+    const bool whole =
+        M % C::BM == 0 && N % C::BN == 0 && K % C::BK == 0 && p.vec_store && (int64_t)C::BM * ldc * 2 < GEMM_RANGE;
+    if (K >= FP8_MFMA16_MIN_K) {
+        if (whole)
+            hipLaunchKernelGGL((fp8_gemm16_persistent_kernel<C, false>), dim3(grid), dim3(C::THREADS), 0, s, p);
+        else
+            hipLaunchKernelGGL((fp8_gemm16_persistent_kernel<C, true>), dim3(grid), dim3(C::THREADS), 0, s, p);
+    } else if (whole) {
         hipLaunchKernelGGL((fp8_gemm_nt_persistent_kernel<C, false>), dim3(grid), dim3(C::THREADS), 0, s, p);
-    else
+    } else {
         hipLaunchKernelGGL((fp8_gemm_nt_persistent_kernel<C, true>), dim3(grid), dim3(C::THREADS), 0, s, p);
+    }
     return 0;
 }
 

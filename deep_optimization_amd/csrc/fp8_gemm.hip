@@ -1,9 +1,9 @@
 // FP8 e4m3 scaled GEMM launcher (kernels and tiling in fp8_gemm.h).
 //
 // Configuration: 256 x 256 workgroup tiles (128 x 128 per wave), GROUP_M = 4 tile rows per
-// L2 group, even MFMA / memory interleave; the persistent kernel with one workgroup per CU (the
-// non-persistent one for an odd number of K slabs); measured on MI355X at 8192^3 and
-// 4096x11008x4096.
+// L2 group, even MFMA / memory interleave; the persistent kernels with one workgroup per CU
+// (16x16x128 MFMAs from K = 8192, 32x32x64 below; the non-persistent kernel for an odd number of
+// K slabs); measured on MI355X at 8192^3 and 4096x11008x4096.
 #include <atomic>
 
 #include "fp8_gemm.h"

@@ -578,11 +578,12 @@ def test_fp8_gemm_parity(M, N, K):
 
 
 @pytest.mark.parametrize("M,N,K", [(1, 1, 16), (100, 300, 48), (257, 255, 144), (1000, 777, 1040), (33, 4099, 2064),
-                                   (4095, 4097, 4112), (300, 200, 0)])
+                                   (4095, 4097, 4112), (300, 200, 0), (257, 255, 8336), (600, 520, 8448)])
 def test_fp8_gemm_ragged_shapes(M, N, K):
     """Edge tiles (M, N not multiples of 256, K a multiple of 16 but not of 64; K = 0 gives zeros),
     through the C ABI with padded row strides: lda, ldb > K, ldc > N (odd, so element stores), and a
-    sentinel around the M x N block of C that must stay untouched."""
+    sentinel around the M x N block of C that must stay untouched. K = 8336 and 8448 (an even slab
+    count from K = 8192) take the 16x16x128 persistent kernel's edge instance."""
     gen = torch.Generator(device=DEV).manual_seed(M * 7 + N + K)
     lda, ldb, ldc = K + 32, K + 48, N + 3
     a_buf = torch.randn(M, lda, generator=gen, device=DEV)
