@@ -8,7 +8,8 @@ the C ABI: every output bit for bit.
 * Two calls in a row, the second with a smaller input (it reuses the scratch the first call left
   behind), for every mode: normalize with x_hat, quant-pack, ReLU and ReLU6 + quant-pack; bf16,
   fp16 and fp32 inputs.
-* A shape with 65,536 partial slots (4096 channels of 8 chunks).
+* A shape with 65,536 partial slots (4096 channels of 8 chunks), and one that fills the scratch
+  exactly: 1024 channels of 512 chunks, 2 * 1024 * 512 = 2^20 partial slots (2^32 elements).
 The host-side rejection of shapes beyond the scratch is tested without a GPU
 (tests/test_host_cpu.py)."""
 import pytest
@@ -127,9 +128,7 @@ def test_noalloc_equals_workspace_entry_point_twice(mode, dtype):
 
 
 def test_noalloc_many_partial_slots():
-    """C = 4096 channels of 8 chunks each: 65,536 partial slots (1/16 of the scratch). The scratch
-    limit itself (2 * C * chunks = DOPT_BN_SCRATCH_FLOATS) takes about 2^32 elements with the
-    layer's C <= 65535 (C * M ~ C * chunks * 8192 = 2^32), so this is the largest shape tested."""
+    """C = 4096 channels of 8 chunks each: 65,536 partial slots (1/16 of the scratch)."""
     N, C, H, W, g, bits = 16, 4096, 64, 64, 256, 2
     assert _lib.lib().dopt_bn_workspace_floats(N, C, H * W) == 2 * C * 8
     print(f"[noalloc] partial slots: N={N} C={C} HW={H * W}", flush=True)
@@ -141,3 +140,25 @@ def test_noalloc_many_partial_slots():
         assert torch.equal(got[k], want[k]), k
     assert torch.equal(rm_a, rm_b) and torch.equal(rv_a, rv_b)
     torch.testing.assert_close(got["mean"], x.float().mean(dim=(0, 2, 3)), rtol=1e-5, atol=1e-5)
+
+
+def test_noalloc_at_the_scratch_limit():
+    """C = 1024 channels of N * HW = 1024 * 4096 elements, 512 chunks of 8192 each: the statistics
+    partials take 2 * 1024 * 512 = DOPT_BN_SCRATCH_FLOATS slots, the whole scratch (the last
+    channel's sums of squares in its last slots). 2^32 bf16 elements: 8 GiB of input and 9 GiB of
+    outputs per call. Every output bit for bit against the workspace entry point."""
+    N, C, H, W, g, bits = 1024, 1024, 64, 64, 256, 2
+    L = _lib.lib()
+    assert L.dopt_bn_workspace_floats(N, C, H * W) == 2 * C * 512 == 1 << 20  # DOPT_BN_SCRATCH_FLOATS
+    print(f"[noalloc] scratch limit: N={N} C={C} HW={H * W} ({N * C * H * W} elements)", flush=True)
+    gen = torch.Generator(device=DEV).manual_seed(11)
+    x = torch.randn((N, C, H, W), generator=gen, device=DEV, dtype=torch.bfloat16)
+    x.mul_(2).add_(0.5)
+    w = torch.rand((C,), generator=gen, device=DEV) + 0.5
+    b = torch.randn((C,), generator=gen, device=DEV)
+    want = _call(False, x, N, C, H * W, g, bits, _lib.BN_QUANT, w, b, None, None)
+    got = _call(True, x, N, C, H * W, g, bits, _lib.BN_QUANT, w, b, None, None)
+    for k in _written(_lib.BN_QUANT):
+        assert torch.equal(got[k], want[k]), k
+    del want, got
+    torch.cuda.empty_cache()
