@@ -391,11 +391,15 @@ __global__ __launch_bounds__(256) void quant_pack_kernel(QuantPackArgs a) {
                     uint32_t q[UE];
                     #pragma unroll
                     for (int k = 0; k < UE; ++k) {
-                        if constexpr (THR) {
-                            uint32_t c = 0;
-#pragma unroll
-                            for (int j = 0; j < QMAX; ++j) c += v[i][k] >= thr[j] ? 1u : 0u;
-                            q[k] = c;
+                        if constexpr (THR && BITS == 2) {
+                            // the count of thresholds at or below the value, as a binary search
+                            // over the three sorted thresholds (5 instructions, against 6 for
+                            // three compares and their sum)
+                            const bool hi = v[i][k] >= thr[1];
+                            const float t = hi ? thr[2] : thr[0];
+                            q[k] = (hi ? 2u : 0u) + (v[i][k] >= t ? 1u : 0u);
+                        } else if constexpr (THR) {
+                            q[k] = v[i][k] >= thr[0] ? 1u : 0u;
                         } else {
                             float qf = __builtin_fmaf(v[i][k] - mn, inv, half_m);
                             // NaN -> 0, as the reference's clamp
