@@ -424,10 +424,19 @@ __device__ __forceinline__ void alam_store(uint32_t* chan, uint32_t e0, uint32_t
 
 // One 2048-element block of the forward: y (and the mask / codes / scale / min) from the lane's 8
 // loaded values. Whole groups are active or not (M % group == 0), so the group's lanes agree.
-template <int MODE, int V, bool R6, bool ALAM>
+//
+// THR (the squashed mode at 1 and 2 bits, no ALAM): the squash t = 2 tanh(xc / 2) of the clamped
+// x_hat xc is monotone, so the group's min and max of t are the squash of xc's min and max, and
+// code q >= k exactly when t >= s_k = mn + (k - (0.5 - 1e-6)) step, i.e. when xc is at or above
+// the threshold logit((s_k + 2) / 4) (t = 4 sigmoid(xc) - 2). The lane computes the group's
+// thresholds once (v_log, v_rcp) and compares each element against them: no transcendental per
+// element. The codes equal the per-element form's except where xc lies within the rounding of the
+// transcendentals of a boundary.
+template <int MODE, int V, bool R6, bool ALAM, bool THR = false>
 __device__ __forceinline__ void fwd_block(const BnFwdArgs& a, int64_t c, RowCursor pos, int64_t e0, int64_t M,
                                           bool active, const float* v, float mean, float inv, float w, float b,
                                           int lg, int bits, float qmaxf, float rqmax) {
+    static_assert(!THR || (MODE == BN_QUANT && !ALAM), "threshold codes: the squashed mode without ALAM");
     const BnGeom& g = a.g;
     float xh[EPL], y[EPL];
 #pragma unroll
@@ -457,7 +466,9 @@ __device__ __forceinline__ void fwd_block(const BnFwdArgs& a, int64_t c, RowCurs
         float t[EPL];
 #pragma unroll
         for (int k = 0; k < EPL; ++k) {
-            if constexpr (MODE == BN_QUANT) {
+            if constexpr (THR) {
+                t[k] = __builtin_amdgcn_fmed3f(xh[k], -3.0f, 3.0f);  // xc; squashed only at min / max
+            } else if constexpr (MODE == BN_QUANT) {
                 t[k] = two_tanh_half_fast(__builtin_amdgcn_fmed3f(xh[k], -3.0f, 3.0f));
             } else {
                 t[k] = xh[k];
@@ -472,6 +483,10 @@ __device__ __forceinline__ void fwd_block(const BnFwdArgs& a, int64_t c, RowCurs
         }
         const int lpg = 1 << (lg - 3);  // group / EPL
         group_minmax(mn, mx, lpg);
+        if constexpr (THR) {  // the infinities of an all-NaN group stay as they are
+            mn = mn < 4.0f ? two_tanh_half_fast(mn) : mn;
+            mx = mx > -4.0f ? two_tanh_half_fast(mx) : mx;
+        }
         // step = rng / qmax and 1 / step, both rounded as the IEEE divisions round them
         const float rng = mx - mn;
         const float step = rng > 0.0f ? div_by_qmax_rt(rng, qmaxf, rqmax) : 1.0f;
@@ -482,7 +497,27 @@ __device__ __forceinline__ void fwd_block(const BnFwdArgs& a, int64_t c, RowCurs
         } else {
             const float half_m = 0.49999899f;  // fp32(0.5 - 1e-6) = 0x3EFFFFDE
             int q[EPL];
-            if constexpr (MODE == BN_QUANT) {
+            if constexpr (THR) {
+                // thresholds ln(p / (1 - p)), p = (s_k + 2) / 4; an s_k past the group's max
+                // (p >= 1, or any s_k of a constant group's step 1 beyond it) gives NaN or +inf,
+                // which no xc reaches
+                float th[3];
+#pragma unroll
+                for (int j = 0; j < 3; ++j) {
+                    const float pk = fmaf(fmaf((float)(j + 1) - half_m, step, mn), 0.25f, 0.5f);
+                    th[j] = 0.6931471805599453f * __builtin_amdgcn_logf(pk * __builtin_amdgcn_rcpf(1.0f - pk));
+                }
+                if (bits == 1) {
+#pragma unroll
+                    for (int k = 0; k < EPL; ++k) q[k] = t[k] >= th[0] ? 1 : 0;
+                } else {  // 2 bits: a binary search over the three sorted thresholds
+#pragma unroll
+                    for (int k = 0; k < EPL; ++k) {
+                        const bool hi = t[k] >= th[1];
+                        q[k] = (hi ? 2 : 0) + (t[k] >= (hi ? th[2] : th[0]) ? 1 : 0);
+                    }
+                }
+            } else if constexpr (MODE == BN_QUANT) {
 #pragma unroll
                 for (int k = 0; k < EPL; ++k) {
                     const float qf = __builtin_amdgcn_fmed3f(fmaf(t[k] - mn, invs, half_m), 0.0f, qmaxf);
@@ -536,7 +571,7 @@ __device__ __forceinline__ void fwd_block(const BnFwdArgs& a, int64_t c, RowCurs
 
 // A workgroup covers ITER consecutive 2048-element blocks of one channel; all loads are issued
 // before the first block is processed.
-template <int DT, int MODE, int V, bool R6, bool ALAM = false>
+template <int DT, int MODE, int V, bool R6, bool ALAM = false, bool THR = false>
 __global__ __launch_bounds__(TPB) void bn_fwd_kernel(BnFwdArgs a, int lg, int bits) {
     const int64_t c = blockIdx.x;
     const int64_t M = a.g.N * a.g.HW;
@@ -572,7 +607,8 @@ __global__ __launch_bounds__(TPB) void bn_fwd_kernel(BnFwdArgs a, int lg, int bi
 #pragma unroll
     for (int it = 0; it < ITER; ++it) {
         const int64_t e0 = base + it * WG_ELEMS;
-        fwd_block<MODE, V, R6, ALAM>(a, c, cur[it], e0, M, e0 < M, v[it], mean, inv, w, b, lg, bits, qmaxf, rqmax);
+        fwd_block<MODE, V, R6, ALAM, THR>(a, c, cur[it], e0, M, e0 < M, v[it], mean, inv, w, b, lg, bits, qmaxf,
+                                          rqmax);
     }
 }
 
@@ -759,14 +795,17 @@ int fwd_dt(const BnFwdArgs& a, int mode, int group, int bits, int vw, hipStream_
 #define DOPT_BN_FWD(MODE_, V_) hipLaunchKernelGGL((bn_fwd_kernel<DT, MODE_, V_, false>), grid, dim3(TPB), 0, s, a, lg, bits)
 #define DOPT_BN_FWD_RELU6(V_) hipLaunchKernelGGL((bn_fwd_kernel<DT, BN_RELU_QUANT, V_, true>), grid, dim3(TPB), 0, s, a, lg, bits)
 #define DOPT_BN_FWD_ALAM(V_) hipLaunchKernelGGL((bn_fwd_kernel<DT, BN_QUANT, V_, false, true>), grid, dim3(TPB), 0, s, a, lg, bits)
+#define DOPT_BN_FWD_THR(V_) hipLaunchKernelGGL((bn_fwd_kernel<DT, BN_QUANT, V_, false, false, true>), grid, dim3(TPB), 0, s, a, lg, bits)
 #define DOPT_BN_FWD_NORM(V_) DOPT_BN_FWD(BN_NORM, V_)
 #define DOPT_BN_FWD_QUANT(V_) DOPT_BN_FWD(BN_QUANT, V_)
 #define DOPT_BN_FWD_RELU(V_) DOPT_BN_FWD(BN_RELU_QUANT, V_)
     if (mode == BN_NORM) DOPT_BN_BY_WIDTH(vw, DOPT_BN_FWD_NORM);
     else if (mode == BN_QUANT && a.alam_lg > 0) DOPT_BN_BY_WIDTH(vw, DOPT_BN_FWD_ALAM);
+    else if (mode == BN_QUANT && bits <= 2) DOPT_BN_BY_WIDTH(vw, DOPT_BN_FWD_THR);
     else if (mode == BN_QUANT) DOPT_BN_BY_WIDTH(vw, DOPT_BN_FWD_QUANT);
     else if (mode == BN_RELU6_QUANT) DOPT_BN_BY_WIDTH(vw, DOPT_BN_FWD_RELU6);
     else DOPT_BN_BY_WIDTH(vw, DOPT_BN_FWD_RELU);
+#undef DOPT_BN_FWD_THR
 #undef DOPT_BN_FWD_RELU6
 #undef DOPT_BN_FWD_ALAM
 #undef DOPT_BN_FWD_RELU
