@@ -501,12 +501,13 @@ __device__ __forceinline__ void fwd_block(const BnFwdArgs& a, int64_t c, RowCurs
                 // thresholds ln(p / (1 - p)), p = (s_k + 2) / 4; an s_k past the group's max
                 // (p >= 1, or any s_k of a constant group's step 1 beyond it) gives NaN or +inf,
                 // which no xc reaches
-                float th[3];
-#pragma unroll
-                for (int j = 0; j < 3; ++j) {
-                    const float pk = fmaf(fmaf((float)(j + 1) - half_m, step, mn), 0.25f, 0.5f);
-                    th[j] = 0.6931471805599453f * __builtin_amdgcn_logf(pk * __builtin_amdgcn_rcpf(1.0f - pk));
-                }
+                // lane j of each aligned quad (j < 3; lane 3 repeats j = 2) evaluates threshold j and
+                // quad_perm broadcasts hand every lane all three (a group's G / 8 >= 4 lanes span
+                // whole quads and agree on mn and step)
+                const int jq = (threadIdx.x & 3) < 2 ? (threadIdx.x & 3) + 1 : 3;
+                const float pk = fmaf(fmaf((float)jq - half_m, step, mn), 0.25f, 0.5f);
+                const float tj = 0.6931471805599453f * __builtin_amdgcn_logf(pk * __builtin_amdgcn_rcpf(1.0f - pk));
+                const float th[3] = {dpp_f32<0x00>(tj), dpp_f32<0x55>(tj), dpp_f32<0xAA>(tj)};
                 if (bits == 1) {
 #pragma unroll
                     for (int k = 0; k < EPL; ++k) q[k] = t[k] >= th[0] ? 1 : 0;

@@ -211,6 +211,9 @@ __global__ __launch_bounds__(256) void quant_pack_kernel(QuantPackArgs a) {
 
     const float qmaxf = (float)QMAX;
     const float half_m = 0.49999899f;  // fp32(0.5 - 1e-6) = 0x3EFFFFDE
+    // threshold codes: the boundary this lane evaluates, k + 1 - (0.5 - 1e-6), k = min(lane % 4, 2)
+    const float kq = (float)((lane & 3) < 2 ? (lane & 3) + 1 : 3) - half_m;
+    (void)kq;
     float step_p[P], mn_p[P];
 
     #pragma unroll
@@ -342,7 +345,16 @@ __global__ __launch_bounds__(256) void quant_pack_kernel(QuantPackArgs a) {
         // thresholds t_k = logit(s_k) / 4 = (ln 2 / 4) log2(s_k / (1 - s_k)); an s_k >= 1 (beyond
         // the group's max) gives +inf or NaN, which no derivative reaches
         float thr[THR ? QMAX : 1];
-        if constexpr (THR) {
+        if constexpr (THR && QMAX == 3 && LPG >= 4) {
+            // lane k of each aligned quad (k < 3; lane 3 repeats k = 2) computes threshold k, and
+            // quad_perm broadcasts hand every lane all three: one evaluation instead of three (a
+            // group spans whole quads, so a quad's lanes agree on mn and step)
+            const float sk = __builtin_fmaf(kq, step, mn);
+            const float tk = 0.17328679513998632f * __builtin_amdgcn_logf(sk * __builtin_amdgcn_rcpf(1.0f - sk));
+            thr[0] = dpp_f32<0x00>(tk);
+            thr[1] = dpp_f32<0x55>(tk);
+            thr[2] = dpp_f32<0xAA>(tk);
+        } else if constexpr (THR) {
 #pragma unroll
             for (int k = 0; k < QMAX; ++k) {
                 const float sk = __builtin_fmaf((float)(k + 1) - half_m, step, mn);
