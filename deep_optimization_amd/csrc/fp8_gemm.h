@@ -852,7 +852,7 @@ __global__ __launch_bounds__(256, 1) void fp8_gemm16_persistent_kernel(Fp8GemmAr
     // whole-chunk stores, no EDGE instance) may stay in flight; everything before them (slab
     // k+1's loads) has landed.
     constexpr int EPI_STORES = TM * (32 * CPR / 64);
-    constexpr int WAIT_LGKM0 = 15 | (3 << 14) | (7 << 4);  // lgkmcnt(0), vmcnt and expcnt not waited for    constexpr int WAIT_LGKM0 = 63 /*vmcnt lo*/ | (3 << 14) /*vmcnt hi*/ | (7 << 4) /*expcnt*/;  // lgkmcnt(0) only
+    constexpr int WAIT_LGKM0 = 15 | (3 << 14) | (7 << 4);  // lgkmcnt(0); vmcnt and expcnt not waited for
     constexpr int W2 = C::LB, W2E = C::LB + EPI_STORES;
     static_assert(W2E < 64, "vmcnt field");
     constexpr int WAIT2 = (W2 & 15) | ((W2 >> 4) << 14) | (7 << 4);
