@@ -49,11 +49,13 @@ def test_bf16_operand(K, M, N):
     assert torch.equal(dw, dw2) and torch.equal(db, db2)
 
 
-@pytest.mark.parametrize("bits,g", [(1, 64), (2, 256), (4, 128), (8, 512), (2, 512)])
-@pytest.mark.parametrize("K,M,N", [(2048, 512, 768), (777, 256, 256), (25216, 768, 3072)])
+# the flat activation must split into whole groups (777 x 256 does not at g = 512)
+PACKED_CASES = [(bits, g, K, M, N) for K, M, N in [(2048, 512, 768), (777, 256, 256), (25216, 768, 3072)]
+                for bits, g in [(1, 64), (2, 256), (4, 128), (8, 512), (2, 512)] if (K * N) % g == 0]
+
+
+@pytest.mark.parametrize("bits,g,K,M,N", PACKED_CASES)
 def test_packed_operand_equals_dequantized(bits, g, K, M, N):
-    if (K * N) % g:
-        pytest.skip("activation does not split into whole groups")
     dy, x = operands(K, M, N, 3 * bits + K)
     # the reference quantizer on the flat activation (one sample: groups of g consecutive elements)
     packed, scale, xmin = ops.quant_pack_triton(x.reshape(1, -1, g), bits, g, False, 0, True, 3.0)

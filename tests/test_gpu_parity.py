@@ -228,15 +228,18 @@ def _alam_gpu_raw(x, bits, g, alam, flags=0, alpha=0.0):
     return np_view(p), np_view(s), np_view(m)
 
 
-@pytest.mark.parametrize("bits,alam", [(1, 1), (1, 8), (2, 2), (2, 4), (4, 4), (8, 2), (8, 8)])
-@pytest.mark.parametrize("g", [64, 256, 1024])
+# alam_bits must divide the group's words (1 bit at g = 64 has 2 words, so no runs of 8: rejected,
+# test_alam_rejects_bad_run_lengths)
+ALAM_CASES = [(g, bits, alam) for g in (64, 256, 1024)
+              for bits, alam in [(1, 1), (1, 8), (2, 2), (2, 4), (4, 4), (8, 2), (8, 8)] if (g * bits // 32) % alam == 0]
+
+
+@pytest.mark.parametrize("g,bits,alam", ALAM_CASES)
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=["bf16", "f32"])
 def test_alam_quant_pack_bit_exact_without_squash(dtype, g, bits, alam):
     """Without the squash (a C-ABI option; the operator always squashes) the codes, scale and min
     are bit-exact against the oracle: min/max, step, the fma code arguments, the left-to-right
     run sums and the truncation."""
-    if (g * bits // 32) % alam:
-        pytest.skip("alam_bits must divide the group's words")
     x = make_input((3, 37, g), dtype, seed=bits * 7 + alam)
     p, s, m = _alam_gpu_raw(x, bits, g, alam)
     rp, rs, rm = oracle.alam_quant_pack(np_view(x).reshape(-1, g), g, bits, alam)
