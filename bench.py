@@ -1,6 +1,6 @@
 """Benchmark of the activation-compression hot path on one MI355X.
 
-A step is one forward save + backward restore of BASELINE config 2, the ResNet-50 conv2
+A step is one forward save + backward restore of the benchmark's config 2, the ResNet-50 conv2
 activation: bf16 [256, 256, 56, 56] post-ReLU |N(0,1)| (synthetic, seed 0), group size 256,
 2-bit stochastic rounding with a seeded uniform [0, 1) noise tensor (seed 1) resident in HBM:
 act_lib::quant_pack (pack) then act_lib::dequant_unpack back to bf16 (unpack), both through the
@@ -154,7 +154,7 @@ def batchnorm_layer(torch, dev, event_avg, shape=(256, 256, 56, 56), block=1024,
 
 
 def vit_train_step(torch, dev, batch=128, steps=6, warmup=3):
-    """one ViT-B/16 train step (forward, cross-entropy, backward, fused AdamW step)
+    """Config 5: one ViT-B/16 train step (forward, cross-entropy, backward, fused AdamW step)
     on a fixed synthetic batch (N(0,1) images 224x224x3, random labels over 1000 classes, bf16
     autocast, random-init weights), plain and rewritten by the Controller with every selected saved
     activation 2-bit. Reports ms per step and the peak HBM allocated during the timed steps."""

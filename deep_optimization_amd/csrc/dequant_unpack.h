@@ -9,7 +9,8 @@
 // scale and minimum itself (the LPG lanes of a group share one request) and a unit's UE*BITS
 // code bits as the one dword (or 2/4-dword vector) that holds them; nothing is staged in LDS and
 // no wave waits for another. (Staging them in LDS behind a workgroup barrier cost 12 us of the
-// 81 us the kernel took on config 2 when its inputs came cold from HBM right after quant-pack.)
+// 81 us the kernel took on the 2-bit, g = 256 bf16 [256,256,56,56] case when its inputs came
+// cold from HBM right after quant-pack.)
 #pragma once
 
 #include "dopt_device.h"

@@ -110,10 +110,10 @@ def fp8_probe(mode: str) -> int:
 
 def counter_probe(name: str) -> int:
     """One kernel below 70% of HBM peak, 3 + 10 launches, for rocprofv3 --pmc runs (instruction mix,
-    VALU activity, HBM bytes): "philox" / "nearest" = the config-2 quant-pack (bf16 [256,256,56,56]
-    |N(0,1)|, g = 256, 2-bit); "vit_philox" / "vit_unpack" = the config-3 2-bit Philox quant-pack
+    VALU activity, HBM bytes): "philox" / "nearest" = the ResNet-activation quant-pack (bf16 [256,256,56,56]
+    |N(0,1)|, g = 256, 2-bit); "vit_philox" / "vit_unpack" = the ViT-MLP-activation 2-bit Philox quant-pack
     and its unpack-dequant (GELU(N(0,1)) bf16 [256,197,3072], g = 128), "vit_step" both in turn
-    (the config-3 step); "gelu" / "silu" = the
+    (that step); "gelu" / "silu" = the
     fused activation forward on the ViT MLP
     activation (bf16 [256,197,3072] N(0,1), g = 128, 2-bit); "bn_squash" / "bn_relu" = the
     BatchNorm normalize + quant-pack forward on the ResNet stage-1 activation (bf16

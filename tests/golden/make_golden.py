@@ -2,7 +2,7 @@
 
 The reference has no fixtures for this path, so these are the build's own: seeded inputs and the
 oracle's packed words, scale, min and dequantized output for a handful of small configurations,
-including BASELINE config 1 (fp32 [8, 64, 32, 32] ~ N(0,1), seed 0, g = 256, 2-bit, nearest,
+including the reference's CPU case (fp32 [8, 64, 32, 32] ~ N(0,1), seed 0, g = 256, 2-bit, nearest,
 16 x 16 spatial tiles, fp32 min + scale; the input is regenerated from the seed, not stored).
 GPU tests compare the HIP kernels to these arrays; tests/test_oracle.py checks that the oracle
 still reproduces them.

@@ -6,8 +6,8 @@ same generator). The tanh squash of the reference's pre-transform is the one tol
 kernel evaluates tanh(2x)/2 with its own polynomial / exp form and the oracle with the C
 library's tanhf, so both are compared with float64 (min within 2 fp32 ulps, scale within what
 that gives, codes equal away from rounding boundaries). Small ragged sizes sweep every (dtype,
-bits, group size, rounding) kernel; BASELINE's full ResNet size is checked bit-exact against the
-oracle and through size-independent bounds.
+bits, group size, rounding) kernel; the full ResNet activation (bf16 [256,256,56,56]) is checked
+bit-exact against the oracle and through size-independent bounds.
 """
 import numpy as np
 import pytest
@@ -480,10 +480,10 @@ def test_stream_ordering_on_side_stream():
     np.testing.assert_array_equal(y.cpu().numpy().reshape(yo.shape), yo)
 
 
-# ----------------------------------------------------------------------------- BASELINE full sizes
+# ----------------------------------------------------------------------------- full workload sizes
 @pytest.fixture(scope="module")
 def resnet_act():
-    """bf16 [256, 256, 56, 56] post-ReLU |N(0,1)|, g = 256, 2-bit."""
+    """The ResNet-50 conv2 activation: bf16 [256, 256, 56, 56] post-ReLU |N(0,1)|, g = 256, 2-bit."""
     gen = torch.Generator(device=DEV).manual_seed(0)
     x = torch.randn((256, 256, 56, 56), generator=gen, device=DEV, dtype=torch.float32).abs_().to(torch.bfloat16)
     return x
@@ -527,7 +527,7 @@ def test_resnet_full_size_stochastic(resnet_act):
 
 @pytest.mark.parametrize("bits", [1, 2, 4, 8])
 def test_vit_mlp_full_size_philox(bits):
-    """BASELINE config 3 at its size: GELU(N(0,1)) bf16 [256, 197, 3072] (1,210,368 groups of
+    """The ViT-B/16 MLP activation at its size: GELU(N(0,1)) bf16 [256, 197, 3072] (1,210,368 groups of
     g = 128), Philox stochastic rounding (seed 1, offset 0), quant-pack then unpack to bf16, as
     the benchmark runs it. Three windows of 64 groups (the first, the middle, the last) match the
     oracle bit for bit (codes, scale, min, dequantized bf16), the Philox stream taken from the

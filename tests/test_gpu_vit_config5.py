@@ -1,4 +1,4 @@
-"""BASELINE config 5 at its workload: ViT-B/16 (12 blocks, 1000 classes) on a batch of 128
+"""The end-to-end workload: ViT-B/16 (12 blocks, 1000 classes) on a batch of 128
 synthetic 224x224x3 N(0, 1) images, bf16 autocast, rewritten by the Controller with every selected
 saved activation 2-bit (reference: Activation_Compression/controller.py:63-351 applied to timm's
 vit_base_patch16_224 in test8.ipynb cells 2 and 9).

@@ -301,7 +301,7 @@ class TestLayerGroupMeta:
         assert m == {"group_size": 1024, "act_padding": False, "N": 64, "NG": 64 * 784}
         m = layer_group_meta((32, 100), 1)
         assert m == {"group_size": 256, "act_padding": True, "N": 32, "NG": 32}
-        m = layer_group_meta((8, 64, 32, 32), 2)  # BASELINE config 1 shape
+        m = layer_group_meta((8, 64, 32, 32), 2)  # the reference's CPU case's shape
         assert m["group_size"] == 512 and m["NG"] == 8 * 128
 
     def test_activation_size(self):
