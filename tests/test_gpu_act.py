@@ -130,7 +130,7 @@ def test_gelu_fused_quan_pack_and_backward(bits, g):
     np.testing.assert_array_equal(np_view(dx).reshape(want.shape), want)
 
 
-@pytest.mark.parametrize("bits", [2, 4])
+@pytest.mark.parametrize("bits", [1, 2, 4, 8])  # 1 and 2: threshold codes; 4 and 8: per-element squash
 @pytest.mark.parametrize("shape,g", [((2, 16, 32, 48), 256), ((3, 8, 16, 16), 64), ((2, 32, 14, 14), 128)])
 def test_silu_fused_quan_pack_tiles_and_backward(bits, shape, g):
     x = randn(shape, seed=bits + g, scale=2.5)
