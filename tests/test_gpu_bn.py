@@ -60,6 +60,11 @@ def codes_of(packed, bits):
     return (b.reshape(-1, bits).astype(np.int64) << np.arange(bits)).sum(axis=1)
 
 
+def as_f32(a):
+    """a numpy view from npv as float32 (bf16 bit patterns widened)"""
+    return oracle.bf16_bits_to_f32(a) if a.dtype == np.uint16 else a.astype(np.float32)
+
+
 def sums_close(got, want_f64, mag):
     return np.all(np.abs(got.astype(np.float64) - want_f64) <= 1e-5 * mag + 1e-30)
 
@@ -94,6 +99,20 @@ def test_reduce_and_plain_normalize(shape, dtype):
     np.testing.assert_array_equal(npv(var), ref["var"])
     np.testing.assert_array_equal(npv(y).reshape(-1), ref["y"].reshape(-1))
     np.testing.assert_array_equal(npv(xh).reshape(-1), ref["x_hat"].reshape(-1))
+    # the plain mode's backward on the saved x_hat, dy in the input's dtype
+    dy = torch.randn(shape, generator=torch.Generator().manual_seed(5)).to(dtype)
+    dy3 = dy.to(DEV).view(shape[0], shape[1], -1)
+    dg, dbt = ops.bn_bwd_reduce(xh, dy3, **g, BLOCK_M=256, num_warps=8, num_stages=5)
+    dx = ops.bn_bwd_dx(xh, dy3, var, w.to(DEV), dbt, dg, **g, BLOCK_M=256, sync=False, num_warps=8, num_stages=5)
+    torch.cuda.synchronize()
+    rdg, rdb = oracle.bn_bwd_reduce(npv(dy), mode=oracle.BN_NORM, x_hat=npv(xh))
+    dyf = np.abs(as_f32(npv(dy))).astype(np.float64)
+    assert sums_close(npv(dbt), rdb, dyf.sum(axis=(0, 2, 3)))
+    xhf = np.abs(as_f32(npv(xh))).astype(np.float64).reshape(dyf.shape)
+    assert sums_close(npv(dg), rdg, (dyf * xhf).sum(axis=(0, 2, 3)))
+    rdx = oracle.bn_bwd_dx(npv(dy), npv(dg), npv(dbt), w.numpy(), npv(var), mode=oracle.BN_NORM, eps=1e-7,
+                           x_hat=npv(xh))
+    np.testing.assert_array_equal(npv(dx).reshape(-1), rdx.reshape(-1))
 
 
 # (shape, BLOCK_M): M = N*HW is a multiple of the group BLOCK_M // 2
@@ -104,9 +123,10 @@ QCASES = [((4, 16, 16, 16), 64), ((4, 16, 16, 16), 1024), ((8, 32, 14, 14), 64),
 @pytest.mark.parametrize("case", QCASES, ids=lambda c: "x".join(map(str, c[0])) + f"-B{c[1]}")
 @pytest.mark.parametrize("bits", [1, 2, 4, 8])
 @pytest.mark.parametrize("mode", ["relu", "relu6", "squash"])
-def test_fused_forward_and_backward(case, bits, mode):
+@pytest.mark.parametrize("dtype", DTYPES, ids=["bf16", "f32", "f16"])
+def test_fused_forward_and_backward(case, bits, mode, dtype):
+    """x and dy in one dtype: every (dtype, mode, bits, access width) instance of the four kernels."""
     shape, BLOCK = case
-    dtype = torch.bfloat16 if bits != 4 else torch.float32
     x, w, b = make(shape, dtype, 100 + bits)
     N, C = shape[0], shape[1]
     g = geo(x)
@@ -146,7 +166,7 @@ def test_fused_forward_and_backward(case, bits, mode):
 
     # backward on the GPU's own saved tensors
     gdy = torch.Generator().manual_seed(7)
-    dy = torch.randn(shape, generator=gdy).to(torch.bfloat16)
+    dy = torch.randn(shape, generator=gdy).to(dtype)
     dy3 = dy.to(DEV).view(N, C, -1)
     if mode == "squash":
         dw, db = ops.bn_bwd_reduce_dequant_unpack_fused(packed, dy3, scale, xmin, **g, BLOCK_M=BLOCK, bits=bits,
@@ -164,7 +184,7 @@ def test_fused_forward_and_backward(case, bits, mode):
     kw = dict(mode=omode, packed=npv(packed), relu_packed=None if rp is None else npv(rp), scale=npv(scale),
               min=npv(xmin), group_size=grp, bits=bits)
     rdw, rdb = oracle.bn_bwd_reduce(npv(dy), **kw)
-    dyf = np.abs(oracle.bf16_bits_to_f32(npv(dy))).astype(np.float64)
+    dyf = np.abs(as_f32(npv(dy))).astype(np.float64)
     assert sums_close(npv(db), rdb, dyf.sum(axis=(0, 2, 3)))
     assert sums_close(npv(dw), rdw, 8.0 * dyf.sum(axis=(0, 2, 3)))  # |x_hat'| < 8 for this data
     rdx = oracle.bn_bwd_dx(npv(dy), npv(dw), npv(db), w.numpy(), npv(var), eps=eps, **kw)
@@ -231,24 +251,23 @@ def test_errors():
 
 
 # ----------------------------------------------------------------------------- avg_alam
-# (shape, BLOCK_M, bits, alam_bits, dtype): run lengths dividing the group's code words (1: the
-# plain codes, noise in the reduce only; 16 and 64: runs spanning 2 and 8 lanes), every access width
+# (shape, BLOCK_M, bits, alam_bits): run lengths dividing the group's code words (1: the plain
+# codes, noise in the reduce only; 16 and 64: runs spanning 2 and 8 lanes), every access width
 # (8 at 16x16 / 28x28, 4 at 14x14, 2 at 5x10, 1 at 7x7), groups of 32..256, and channels whose last
-# wave of 512 elements lies partly past M (7x7: M = 1568)
-ACASES = [((4, 16, 16, 16), 64, 2, 2, torch.bfloat16), ((4, 16, 16, 16), 64, 8, 8, torch.float32),
-          ((16, 8, 14, 14), 128, 1, 2, torch.bfloat16), ((16, 32, 14, 14), 128, 4, 4, torch.float16),
-          ((32, 16, 28, 28), 512, 2, 16, torch.bfloat16), ((32, 16, 28, 28), 512, 8, 64, torch.bfloat16),
-          ((32, 8, 7, 7), 64, 4, 4, torch.bfloat16), ((32, 8, 5, 10), 64, 2, 1, torch.bfloat16),
-          ((16, 16, 28, 28), 256, 1, 4, torch.bfloat16)]
+# wave of 512 elements lies partly past M (7x7: M = 1568); each in bf16, fp32 and fp16
+ACASES = [((4, 16, 16, 16), 64, 2, 2), ((4, 16, 16, 16), 64, 8, 8), ((16, 8, 14, 14), 128, 1, 2),
+          ((16, 32, 14, 14), 128, 4, 4), ((32, 16, 28, 28), 512, 2, 16), ((32, 16, 28, 28), 512, 8, 64),
+          ((32, 8, 7, 7), 64, 4, 4), ((32, 8, 5, 10), 64, 2, 1), ((16, 16, 28, 28), 256, 1, 4)]
 
 
 @pytest.mark.parametrize("case", ACASES, ids=lambda c: "x".join(map(str, c[0])) + f"-B{c[1]}-b{c[2]}-A{c[3]}")
-def test_alam_forward_and_backward(case):
-    """avg_alam=True through the reference's three squashed operators against the oracle: y, mean
-    and var bit for bit; codes (runs' truncated means of tanh-squashed arguments) within one step on
-    under 1% of the runs, scale / min within one bf16 ulp; the reduce (codes plus tl.rand noise)
-    within the fp32 summation bound; dx on the GPU's codes bit for bit."""
-    shape, BLOCK, bits, alam, dtype = case
+@pytest.mark.parametrize("dtype", DTYPES, ids=["bf16", "f32", "f16"])
+def test_alam_forward_and_backward(case, dtype):
+    """avg_alam=True through the reference's three squashed operators against the oracle, x and dy
+    in one dtype: y, mean and var bit for bit; codes (runs' truncated means of tanh-squashed
+    arguments) within one step on under 1% of the runs, scale / min within one bf16 ulp; the reduce
+    (codes plus tl.rand noise) within the fp32 summation bound; dx on the GPU's codes bit for bit."""
+    shape, BLOCK, bits, alam = case
     x, w, b = make(shape, dtype, 300 + bits + alam)
     N, C = shape[0], shape[1]
     g = geo(x)
@@ -272,7 +291,7 @@ def test_alam_forward_and_backward(case):
     for a, r in ((npv(scale), ref["scale"]), (npv(xmin), ref["min"])):
         assert np.abs(a.astype(np.int64) - r.astype(np.int64)).max() <= 1
 
-    dy = torch.randn(shape, generator=torch.Generator().manual_seed(8)).to(torch.bfloat16)
+    dy = torch.randn(shape, generator=torch.Generator().manual_seed(8)).to(dtype)
     dy3 = dy.to(DEV).view(N, C, -1)
     dw, db = ops.bn_bwd_reduce_dequant_unpack_fused(packed, dy3, scale, xmin, **g, BLOCK_M=BLOCK, bits=bits,
                                                     avg_alam=True, alam_bits=alam)
@@ -282,7 +301,7 @@ def test_alam_forward_and_backward(case):
     kw = dict(mode=oracle.BN_QUANT, packed=npv(packed), scale=npv(scale), min=npv(xmin), group_size=grp, bits=bits,
               alam_bits=alam)
     rdw, rdb = oracle.bn_bwd_reduce(npv(dy), **kw)
-    dyf = np.abs(oracle.bf16_bits_to_f32(npv(dy))).astype(np.float64)
+    dyf = np.abs(as_f32(npv(dy))).astype(np.float64)
     assert sums_close(npv(db), rdb, dyf.sum(axis=(0, 2, 3)))
     assert sums_close(npv(dw), rdw, 8.0 * dyf.sum(axis=(0, 2, 3)))  # |x_hat'| < 8 for this data
     rdx = oracle.bn_bwd_dx(npv(dy), npv(dw), npv(db), w.numpy(), npv(var), eps=1e-7, **kw)
