@@ -257,7 +257,8 @@ def test_errors():
 # wave of 512 elements lies partly past M (7x7: M = 1568); each in bf16, fp32 and fp16
 ACASES = [((4, 16, 16, 16), 64, 2, 2), ((4, 16, 16, 16), 64, 8, 8), ((16, 8, 14, 14), 128, 1, 2),
           ((16, 32, 14, 14), 128, 4, 4), ((32, 16, 28, 28), 512, 2, 16), ((32, 16, 28, 28), 512, 8, 64),
-          ((32, 8, 7, 7), 64, 4, 4), ((32, 8, 5, 10), 64, 2, 1), ((16, 16, 28, 28), 256, 1, 4)]
+          ((32, 8, 7, 7), 64, 4, 4), ((32, 8, 5, 10), 64, 2, 1), ((32, 8, 5, 10), 64, 4, 2),
+          ((16, 16, 28, 28), 256, 1, 4)]
 
 
 @pytest.mark.parametrize("case", ACASES, ids=lambda c: "x".join(map(str, c[0])) + f"-B{c[1]}-b{c[2]}-A{c[3]}")

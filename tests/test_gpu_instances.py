@@ -188,10 +188,11 @@ def test_unfused_activation_every_dtype(dtype, act):
 # ----------------------------------------------------------------------------- weight gradient
 @pytest.mark.parametrize("bits,g", [(1, 64), (2, 256), (4, 128), (8, 512)])
 @pytest.mark.parametrize("M,N", [(768, 768), (2304, 768)], ids=["128-row tiles", "256-row tiles"])
-def test_packed_dw_without_bias_gradient(bits, g, M, N):
+@pytest.mark.parametrize("K", [2048, 2000])
+def test_packed_dw_without_bias_gradient(bits, g, M, N, K):
     """dw_gemm on packed codes without the bias gradient equals the same call with it, bit for
-    bit (the two are separate kernel instances; 8-bit codes take the register-decoding kernel)."""
-    K = 2048
+    bit (the two are separate kernel instances; 8-bit codes, and K not a multiple of 32, take the
+    register-decoding kernel)."""
     gen = torch.Generator().manual_seed(bits + M)
     dy = (torch.randn((K, M), generator=gen) * 0.1).to(torch.bfloat16).to(DEV)
     x = torch.randn((K, N), generator=gen).to(torch.bfloat16).to(DEV)

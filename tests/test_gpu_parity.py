@@ -235,7 +235,7 @@ ALAM_CASES = [(g, bits, alam) for g in (64, 256, 1024)
 
 
 @pytest.mark.parametrize("g,bits,alam", ALAM_CASES)
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=["bf16", "f32"])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32, torch.float16], ids=["bf16", "f32", "f16"])
 def test_alam_quant_pack_bit_exact_without_squash(dtype, g, bits, alam):
     """Without the squash (a C-ABI option; the operator always squashes) the codes, scale and min
     are bit-exact against the oracle: min/max, step, the fma code arguments, the left-to-right
