@@ -651,7 +651,7 @@ constexpr int64_t FP8_MFMA16_MIN_K = 8192;
 
 template <class C, bool EDGE>
 __global__ __launch_bounds__(256, 1) void fp8_gemm16_persistent_kernel(Fp8GemmArgs p) {
-    constexpr int BM = C::BM, BN = C::BN, BK = C::BK, TM = C::TM, TN = C::TN, WM = C::WM, WN = C::WN;
+    constexpr int BM = C::BM, BN = C::BN, BK = C::BK, TM = C::TM, WM = C::WM, WN = C::WN;
     constexpr int CPR = WN / 8;             // 16-byte chunks per staged row
     constexpr int ESTAGE = 32 * WN * 2;     // bytes staged per wave: 32 rows of its tile
     static_assert(CPR == 8 || CPR == 16, "staging swizzle");

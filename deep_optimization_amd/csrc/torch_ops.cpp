@@ -350,7 +350,7 @@ std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor> bn_train_fwd(
                                  X.scalar_type() == ScalarType::BFloat16),
                 "bn_train_fwd: X must be an [N, C, ...] float tensor, got ", X.sizes(), " ", X.scalar_type());
     const int64_t N = X.size(0), C = X.size(1);
-    const int64_t HW = N * C ? X.numel() / (N * C) : 0;
+    const int64_t HW = N * C != 0 ? X.numel() / (N * C) : 0;
     const int64_t M = N * HW;
     TORCH_CHECK(weight.numel() == C, "bn_train_fwd: weight must hold ", C, " values (one per channel), got ",
                 weight.numel());
@@ -399,7 +399,7 @@ std::tuple<Tensor, Tensor, Tensor> bn_train_bwd(const Tensor& packed_in, const s
     TORCH_CHECK(dy.dim() >= 2, "bn_train_bwd: dy must be [N, C, ...], got ", dy.sizes());
     require_cuda(dy);
     const int64_t N = dy.size(0), C = dy.size(1);
-    const int64_t HW = N * C ? dy.numel() / (N * C) : 0;
+    const int64_t HW = N * C != 0 ? dy.numel() / (N * C) : 0;
     const int64_t M = N * HW;
     const c10::DeviceGuard guard(dy.device());
     const Tensor DY3 = dy.contiguous().view({N, C, HW});
