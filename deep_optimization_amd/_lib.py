@@ -32,6 +32,8 @@ EXPORTS = (
     "dopt_relu_pack",
     "dopt_relu_unpack",
     "dopt_act_forward",
+    "dopt_pact_clamp_forward",
+    "dopt_pact_clamp_backward",
     "dopt_act_quant_pack",
     "dopt_act_dequant_mul",
     "dopt_act_dequant_mul_alam",
@@ -96,6 +98,10 @@ def lib() -> ctypes.CDLL:
         L.dopt_relu_unpack.restype = i32
         L.dopt_act_forward.argtypes = [vp, i32, i64, i32, vp, vp, vp]
         L.dopt_act_forward.restype = i32
+        L.dopt_pact_clamp_forward.argtypes = [vp, i32, i64, f32, vp, vp, vp]
+        L.dopt_pact_clamp_forward.restype = i32
+        L.dopt_pact_clamp_backward.argtypes = [vp, vp, i32, i64, vp, vp]
+        L.dopt_pact_clamp_backward.restype = i32
         L.dopt_act_quant_pack.argtypes = [vp, i32, i32, i64, i32, i32, vp, vp, vp, vp, vp, i32, vp]
         L.dopt_act_quant_pack.restype = i32
         L.dopt_act_dequant_mul.argtypes = [vp, vp, vp, i32, i64, i32, i32, vp, vp, i32, vp, vp]

@@ -589,6 +589,47 @@ silu_triton = _op("silu_triton(Tensor x) -> (Tensor, Tensor)", lambda x: _act_fo
 gelu_triton = _op("gelu_triton(Tensor x) -> (Tensor, Tensor)", lambda x: _act_forward(x, ACT_GELU), _bf16_pair)
 
 
+def _group_pact_clamp_fwd(x, alpha):
+    """-> (bf16 clamp(x, -alpha, alpha), int8 mask |x| <= alpha), both shaped like x
+    (AC/modules/ops.py:587-603)."""
+    if x.dtype not in _DTYPE_CODE:
+        raise RuntimeError(f"group_pact_clamp_fwd: unsupported dtype {x.dtype}")
+    _require_cuda(x)
+    x = _aligned(x)
+    y = torch.empty(x.shape, dtype=torch.bfloat16, device=x.device)
+    mask = torch.empty(x.shape, dtype=torch.int8, device=x.device)
+    rc = _lib.lib().dopt_pact_clamp_forward(x.data_ptr(), _DTYPE_CODE[x.dtype], x.numel(), float(alpha), y.data_ptr(),
+                                            mask.data_ptr(), _stream(x))
+    _lib.check(rc, "group_pact_clamp_fwd")
+    return y, mask
+
+
+def _group_pact_clamp_bwd(mask, alpha, dy):
+    """-> bf16 dx = dy where mask != 0, else 0, shaped like dy; alpha is not used (as in the
+    reference, AC/modules/ops.py:606-622)."""
+    if dy.dtype not in _DTYPE_CODE:
+        raise RuntimeError(f"group_pact_clamp_bwd: unsupported dy dtype {dy.dtype}")
+    if mask.dtype != torch.int8 or mask.numel() != dy.numel():
+        raise RuntimeError(f"group_pact_clamp_bwd: mask must be int8 with dy's {dy.numel()} elements, "
+                           f"got {mask.dtype} with {mask.numel()}")
+    _require_cuda(mask, dy)
+    mask = _aligned(mask.view(dy.shape))
+    dy = _aligned(dy)
+    dx = torch.empty(dy.shape, dtype=torch.bfloat16, device=dy.device)
+    rc = _lib.lib().dopt_pact_clamp_backward(mask.data_ptr(), dy.data_ptr(), _DTYPE_CODE[dy.dtype], dy.numel(),
+                                             dx.data_ptr(), _stream(dy))
+    _lib.check(rc, "group_pact_clamp_bwd")
+    return dx
+
+
+group_pact_clamp_fwd = _op(
+    "group_pact_clamp_fwd(Tensor x, float alpha) -> (Tensor, Tensor)", _group_pact_clamp_fwd,
+    lambda x, alpha: (torch.empty_like(x, dtype=torch.bfloat16), torch.empty_like(x, dtype=torch.int8)))
+group_pact_clamp_bwd = _op(
+    "group_pact_clamp_bwd(Tensor mask, float alpha, Tensor dy) -> Tensor", _group_pact_clamp_bwd,
+    lambda mask, alpha, dy: torch.empty_like(dy, dtype=torch.bfloat16))
+
+
 def _act_quant_pack_launch(x, act, n_groups, bits, group_size, tile):
     _, nwords, _ = _bits_consts(bits, group_size)
     if x.dtype not in (torch.bfloat16, torch.float32):

@@ -6,8 +6,9 @@
 //   relu_unpack_kernel    dx = bf16(dy * mask) from that bitstream (kernel_implementation.py:93-143)
 //   act_forward_kernel    the unfused helpers: relu/relu6 -> (y, int8 mask); gelu/silu -> (bf16 y,
 //                         bf16 derivative) (kernel_implementation.py:9-31, :154-175, :437-466)
+//   pact_clamp_*_kernel   the PACT clamp of AC/modules/ops.py:545-585 and its masked gradient
 //
-// All three are flat elementwise passes over n elements: lane l of a wave owns 8 consecutive
+// All are flat elementwise passes over n elements: lane l of a wave owns 8 consecutive
 // elements (one 16-byte vector of bf16, two of fp32) per pass, the wave's lanes consecutive
 // chunks, so the mask bits of consecutive lanes are consecutive in the bitstream; pieces narrower
 // than a dword are merged across lanes with DPP and written by the first lane of each dword.
@@ -226,6 +227,54 @@ __global__ __launch_bounds__(256) void act_forward_kernel(const void* __restrict
     }
 }
 
+// PACT clamp (AC/modules/ops.py:545-585): y = bf16(clamp(x, -alpha, alpha)) and the int8 mask
+// |x| <= alpha; backward dx = bf16(mask != 0 ? dy : 0). The clamp is fmaxf then fminf, so a NaN x
+// gives -alpha (and mask 0).
+template <int DT>
+__global__ __launch_bounds__(256) void pact_clamp_fwd_kernel(const void* __restrict__ x, float alpha,
+                                                             void* __restrict__ y, int8_t* __restrict__ mask,
+                                                             uint64_t n) {
+    const uint64_t c = ((uint64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * 64 + (threadIdx.x & 63);
+    const uint64_t e0 = c * CE;
+    if (e0 >= n) return;
+    if (e0 + CE > n) {  // ragged tail: one element at a time
+        for (uint64_t e = e0; e < n; ++e) {
+            const float v = load1<DT>(x, e);
+            ((uint16_t*)y)[e] = to_bf16(fminf(fmaxf(v, -alpha), alpha));
+            mask[e] = (int8_t)(fabsf(v) <= alpha);
+        }
+        return;
+    }
+    float v[CE], o[CE];
+    load8<DT>(x, e0, v);
+    uint64_t bytes = 0;
+#pragma unroll
+    for (int k = 0; k < CE; ++k) {
+        o[k] = fminf(fmaxf(v[k], -alpha), alpha);
+        bytes |= (uint64_t)(fabsf(v[k]) <= alpha) << (8 * k);
+    }
+    store8<DT_BF16>(y, e0, o);
+    *(uint64_t*)(mask + e0) = bytes;
+}
+
+template <int DYT>
+__global__ __launch_bounds__(256) void pact_clamp_bwd_kernel(const int8_t* __restrict__ mask, const void* __restrict__ dy,
+                                                             void* __restrict__ dx, uint64_t n) {
+    const uint64_t c = ((uint64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * 64 + (threadIdx.x & 63);
+    const uint64_t e0 = c * CE;
+    if (e0 >= n) return;
+    if (e0 + CE > n) {
+        for (uint64_t e = e0; e < n; ++e) ((uint16_t*)dx)[e] = to_bf16(mask[e] != 0 ? load1<DYT>(dy, e) : 0.0f);
+        return;
+    }
+    float g[CE], o[CE];
+    load8<DYT>(dy, e0, g);
+    const uint64_t mb = *(const uint64_t*)(mask + e0);
+#pragma unroll
+    for (int k = 0; k < CE; ++k) o[k] = ((mb >> (8 * k)) & 0xffu) != 0 ? g[k] : 0.0f;
+    store8<DT_BF16>(dx, e0, o);
+}
+
 template <class K, class... Args>
 int launch_flat(K kernel, uint64_t n, hipStream_t s, Args... args) {
     const uint64_t chunks = (n + CE - 1) / CE;
@@ -298,6 +347,24 @@ int launch_act_forward(const void* x, int dt, void* y, void* aux, uint64_t n, in
         case DT_F32: return act_forward_dt<DT_F32>(x, y, aux, n, act, s);
         case DT_F16: return act_forward_dt<DT_F16>(x, y, aux, n, act, s);
         case DT_BF16: return act_forward_dt<DT_BF16>(x, y, aux, n, act, s);
+    }
+    return -1;
+}
+
+int launch_pact_clamp_fwd(const void* x, int dt, float alpha, void* y, int8_t* mask, uint64_t n, hipStream_t s) {
+    switch (dt) {
+        case DT_F32: return launch_flat(pact_clamp_fwd_kernel<DT_F32>, n, s, x, alpha, y, mask);
+        case DT_F16: return launch_flat(pact_clamp_fwd_kernel<DT_F16>, n, s, x, alpha, y, mask);
+        case DT_BF16: return launch_flat(pact_clamp_fwd_kernel<DT_BF16>, n, s, x, alpha, y, mask);
+    }
+    return -1;
+}
+
+int launch_pact_clamp_bwd(const int8_t* mask, const void* dy, int dyt, void* dx, uint64_t n, hipStream_t s) {
+    switch (dyt) {
+        case DT_F32: return launch_flat(pact_clamp_bwd_kernel<DT_F32>, n, s, mask, dy, dx);
+        case DT_F16: return launch_flat(pact_clamp_bwd_kernel<DT_F16>, n, s, mask, dy, dx);
+        case DT_BF16: return launch_flat(pact_clamp_bwd_kernel<DT_BF16>, n, s, mask, dy, dx);
     }
     return -1;
 }

@@ -22,6 +22,8 @@ int launch_fp8_pack(const uint8_t* src, int64_t rows, int64_t cols, int64_t stri
 int launch_relu_pack(const void* x, int dt, void* y, uint32_t* packed, uint64_t n, int bits, bool relu6, hipStream_t s);
 int launch_relu_unpack(const uint32_t* packed, const void* dy, int dyt, void* dx, uint64_t n, int bits, hipStream_t s);
 int launch_act_forward(const void* x, int dt, void* y, void* aux, uint64_t n, int act, hipStream_t s);
+int launch_pact_clamp_fwd(const void* x, int dt, float alpha, void* y, int8_t* mask, uint64_t n, hipStream_t s);
+int launch_pact_clamp_bwd(const int8_t* mask, const void* dy, int dyt, void* dx, uint64_t n, hipStream_t s);
 const char* graph_node_counts(hipGraph_t g, int64_t* counts, int n_counts);
 const char* graph_replace_memsets(hipGraph_t g, int64_t* replaced);
 int launch_alam_quant_pack(const void* x, int dt, int64_t n_groups, int g, int bits, int alam, int flags,
@@ -455,6 +457,36 @@ int dopt_act_forward(const void* x, int x_dtype, int64_t n, int act, void* y, vo
     if (dopt::launch_act_forward(x, x_dtype, y, aux, (uint64_t)n, act, (hipStream_t)stream))
         return fail(DOPT_EUNSUPPORTED, "no act_forward kernel for dtype %d act %d", x_dtype, act);
     return hip_status("act_forward launch");
+}
+
+int dopt_pact_clamp_forward(const void* x, int x_dtype, int64_t n, float alpha, void* y, int8_t* mask,
+                            void* stream) {
+    if (x_dtype != DOPT_F32 && x_dtype != DOPT_F16 && x_dtype != DOPT_BF16)
+        return fail(DOPT_EINVAL, "pact_clamp_forward: unsupported input dtype code %d", x_dtype);
+    if (!(alpha > 0.0f)) return fail(DOPT_EINVAL, "pact_clamp_forward: alpha must be > 0 (not NaN), got %g", alpha);
+    if (n < 0) return fail(DOPT_EINVAL, "pact_clamp_forward: negative n");
+    if (n == 0) return ok();
+    if (!x || !y || !mask) return fail(DOPT_EINVAL, "null pointer argument");
+    if (!aligned16(x) || !aligned16(y) || ((uintptr_t)mask & 7u))
+        return fail(DOPT_EINVAL, "x and y must be 16-byte and mask 8-byte aligned");
+    (void)hipGetLastError();
+    if (dopt::launch_pact_clamp_fwd(x, x_dtype, alpha, y, mask, (uint64_t)n, (hipStream_t)stream))
+        return fail(DOPT_EUNSUPPORTED, "no pact_clamp_forward kernel for dtype %d", x_dtype);
+    return hip_status("pact_clamp_forward launch");
+}
+
+int dopt_pact_clamp_backward(const int8_t* mask, const void* dy, int dy_dtype, int64_t n, void* dx, void* stream) {
+    if (dy_dtype != DOPT_F32 && dy_dtype != DOPT_F16 && dy_dtype != DOPT_BF16)
+        return fail(DOPT_EINVAL, "pact_clamp_backward: unsupported dy dtype code %d", dy_dtype);
+    if (n < 0) return fail(DOPT_EINVAL, "pact_clamp_backward: negative n");
+    if (n == 0) return ok();
+    if (!mask || !dy || !dx) return fail(DOPT_EINVAL, "null pointer argument");
+    if (!aligned16(dy) || !aligned16(dx) || ((uintptr_t)mask & 7u))
+        return fail(DOPT_EINVAL, "dy and dx must be 16-byte and mask 8-byte aligned");
+    (void)hipGetLastError();
+    if (dopt::launch_pact_clamp_bwd(mask, dy, dy_dtype, dx, (uint64_t)n, (hipStream_t)stream))
+        return fail(DOPT_EUNSUPPORTED, "no pact_clamp_backward kernel for dtype %d", dy_dtype);
+    return hip_status("pact_clamp_backward launch");
 }
 
 int dopt_act_quant_pack(const void* x, int x_dtype, int act, int64_t n_groups, int group_size, int bits,

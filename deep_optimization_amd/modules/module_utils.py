@@ -64,9 +64,11 @@ def quantize(input, bits, pack_only, group_size, act_padding, N, avg_alam, alam_
     groups, N, G, new_H, new_W, ori_shape, pad_elig, reshape_elig, channel_mean = spatical_aware_act_tensor_reshape(
         input, Group_Size=group_size, act_padding=act_padding, pack_only=pack_only)
     if pack_only:
+        # the meta keeps the tile flags: the reference's pack-only meta (module_utils.py:40,55) drops them,
+        # so a mask grouped into spatial tiles came back in flat order wherever H x W holds several tiles
         out = torch.ops.act_lib.pack_triton(groups, bits, group_size)
-        return (out, None, None), (bits, pack_only, group_size, act_padding, N, G, 0, 0, False, False, channel_mean,
-                                   None, None, ori_shape)
+        return (out, None, None), (bits, pack_only, group_size, act_padding, N, G, new_H, new_W, pad_elig,
+                                   reshape_elig, channel_mean, None, None, ori_shape)
     if avg_alam:
         out, scaler, xmin = torch.ops.act_lib.quant_pack_triton(groups, bits, group_size, avg_alam, alam_bits, clamp,
                                                                 clamp_alpha)

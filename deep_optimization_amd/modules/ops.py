@@ -185,4 +185,35 @@ class _DOLinear(Function):
         return dx.view(*input_shape), dw, None, None, None, None, db
 
 
-__all__ = ["_DOConvnd", "_DOConv1d", "_DOConv2d", "_DOConv3d", "_DOLinear"]
+class GroupPACTClampFn(Function):
+    """The reference's PACT clamp Function (AC/modules/ops.py:625-668): forward returns
+    bf16 clamp(x, -alpha, alpha) (act_lib::group_pact_clamp_fwd, in the autocast dtype under
+    autocast) and saves the mask |x| <= alpha bit-packed (1-bit pack-only quantize under
+    meta["<target_name>_clamp"], with the target's act_padding and N); the backward restores the
+    mask and returns dy * mask. ``alpha`` may be a float or a one-element tensor."""
+
+    @staticmethod
+    @custom_fwd(device_type="cuda")
+    def forward(ctx, x, alpha, group_size, meta, target_name):
+        if torch.is_autocast_enabled("cuda"):
+            x = x.to(torch.get_autocast_dtype("cuda"))
+        a = float(alpha.item() if isinstance(alpha, torch.Tensor) else alpha)
+        y, mask = torch.ops.act_lib.group_pact_clamp_fwd(x, a)
+        clamp_name = f"{target_name}_clamp"
+        clamp_meta = {clamp_name: {"bits": 1, "pack_only": True, "group_size": group_size,
+                                   "act_padding": meta[f"{target_name}"]["act_padding"],
+                                   "N": meta[f"{target_name}"]["N"], "AVG_ALAM": False, "ALAM_BITS": 0}}
+        q_tensor, q_meta, _ = unified_quantize(mask, None, clamp_name, clamp_meta, clamp=False, clamp_alpha=a)
+        ctx.save_for_backward(q_tensor[0])
+        ctx.q_meta = q_meta
+        return y
+
+    @staticmethod
+    @custom_bwd(device_type="cuda")
+    def backward(ctx, dy):
+        (packed,) = ctx.saved_tensors
+        mask = unified_dequantize((packed, None, None), ctx.q_meta, None)
+        return dy * mask, None, None, None, None
+
+
+__all__ = ["_DOConvnd", "_DOConv1d", "_DOConv2d", "_DOConv3d", "_DOLinear", "GroupPACTClampFn"]

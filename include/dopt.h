@@ -200,6 +200,22 @@ int dopt_relu_unpack(const uint32_t* packed, const void* dy, int dy_dtype, int64
 int dopt_act_forward(const void* x, int x_dtype, int64_t n, int act, void* y, void* aux, void* stream);
 
 /*
+ * PACT clamp over n elements (any n): y = bf16(clamp(x, -alpha, alpha)) (fmaxf then fminf: a NaN
+ * x gives -alpha) and the int8 mask |x| <= alpha. x F32, F16 or BF16, 16-byte aligned like y;
+ * mask 8-byte aligned; alpha > 0 (else DOPT_EINVAL: at 0 the output's zero signs would depend
+ * on how min and max order -0 and +0).
+ * Replaces act_lib::group_pact_clamp_fwd (AC/modules/ops.py:587-603, kernel :545-561).
+ */
+int dopt_pact_clamp_forward(const void* x, int x_dtype, int64_t n, float alpha, void* y, int8_t* mask,
+                            void* stream);
+
+/*
+ * Its gradient: dx = bf16(mask[e] != 0 ? dy[e] : 0) over n elements; dy F32, F16 or BF16.
+ * Replaces act_lib::group_pact_clamp_bwd (AC/modules/ops.py:606-622, kernel :563-584).
+ */
+int dopt_pact_clamp_backward(const int8_t* mask, const void* dy, int dy_dtype, int64_t n, void* dx, void* stream);
+
+/*
  * Fused GELU / SiLU forward: y = act(x) written as bf16, and per group the derivative
  * d = tanh(clamp(act'(x), -3, 3) / 0.5) * 0.5 quantized like dopt_quant_pack with nearest rounding,
  * the range floored at 1e-4 (kernel_implementation.py:225-243, :496-535). Layout arguments as in

@@ -69,6 +69,10 @@ def lib():
         L.oracle_relu_unpack.restype = i32
         L.oracle_act_forward.argtypes = [vp, i32, i64, i32, vp, vp]
         L.oracle_act_forward.restype = i32
+        L.oracle_pact_clamp_fwd.argtypes = [vp, i32, i64, ctypes.c_float, vp, vp]
+        L.oracle_pact_clamp_fwd.restype = i32
+        L.oracle_pact_clamp_bwd.argtypes = [vp, vp, i32, i64, vp]
+        L.oracle_pact_clamp_bwd.restype = i32
         L.oracle_act_quant_pack.argtypes = [vp, i32, i32, i64, i32, i32, vp, vp, vp, vp, vp, i32]
         L.oracle_act_quant_pack.restype = i32
         L.oracle_act_dequant_mul.argtypes = [vp, vp, vp, i32, i64, i32, i32, vp, vp, i32, vp]
@@ -267,6 +271,24 @@ def act_forward(x: np.ndarray, act: int):
         y, aux = np.zeros(x.shape, dtype=np.uint16), np.zeros(x.shape, dtype=np.uint16)
     _check(lib().oracle_act_forward(_ptr(x), _dtype_code(x), x.size, act, _ptr(y), _ptr(aux)))
     return y, aux
+
+
+def pact_clamp_fwd(x: np.ndarray, alpha: float):
+    """PACT clamp -> (bf16 clamp(x, -alpha, alpha) as uint16 bits, int8 mask |x| <= alpha), x's shape."""
+    x = np.ascontiguousarray(x)
+    y = np.zeros(x.shape, dtype=np.uint16)
+    mask = np.zeros(x.shape, dtype=np.int8)
+    _check(lib().oracle_pact_clamp_fwd(_ptr(x), _dtype_code(x), x.size, float(alpha), _ptr(y), _ptr(mask)))
+    return y, mask
+
+
+def pact_clamp_bwd(mask: np.ndarray, dy: np.ndarray) -> np.ndarray:
+    """Its gradient -> bf16 (uint16 bits) dy where mask != 0, else +0, dy's shape."""
+    mask = np.ascontiguousarray(mask, dtype=np.int8)
+    dy = np.ascontiguousarray(dy)
+    dx = np.zeros(dy.shape, dtype=np.uint16)
+    _check(lib().oracle_pact_clamp_bwd(_ptr(mask), _ptr(dy), _dtype_code(dy), dy.size, _ptr(dx)))
+    return dx
 
 
 def act_quant_pack(x: np.ndarray, act: int, group_size: int, bits: int, *, tile_nchw=None, meta_dtype=BF16):

@@ -570,6 +570,25 @@ int oracle_act_forward(const void* x, int x_dtype, int64_t n, int act, void* y, 
     return O_OK;
 }
 
+/* The PACT clamp of AC/modules/ops.py: clamp_fused_fwd_triton (:545-561) stores
+ * bf16(clamp(x, -alpha, alpha)) and the int8 mask |x| <= alpha; clamp_fused_bwd_triton (:563-584)
+ * stores bf16(mask != 0 ? dy : 0). The clamp is fmaxf then fminf (a NaN x gives -alpha). */
+int oracle_pact_clamp_fwd(const void* x, int x_dtype, int64_t n, float alpha, uint16_t* y, int8_t* mask) {
+    if (n < 0 || !(alpha > 0.0f)) return O_EINVAL;
+    for (int64_t i = 0; i < n; ++i) {
+        const float v = load_elem(x, x_dtype, i);
+        y[i] = f32_to_bf16(fminf(fmaxf(v, -alpha), alpha));
+        mask[i] = (int8_t)(fabsf(v) <= alpha);
+    }
+    return O_OK;
+}
+
+int oracle_pact_clamp_bwd(const int8_t* mask, const void* dy, int dy_dtype, int64_t n, uint16_t* dx) {
+    if (n < 0) return O_EINVAL;
+    for (int64_t i = 0; i < n; ++i) dx[i] = f32_to_bf16(mask[i] != 0 ? load_elem(dy, dy_dtype, i) : 0.0f);
+    return O_OK;
+}
+
 /* gelu_fwd_fused_quan_pack_triton (:468-535) / silu_fwd_fused_quan_pack_triton (:180-243):
  * y = act(x) as bf16; d = tanh(clamp(act'(x), -3, 3) / 0.5) * 0.5; per group mn, mx,
  * rng = max(mx - mn, 1e-4), step = rng / QMAX, inv = 1 / step,

@@ -15,6 +15,7 @@ import torch
 import deep_optimization_amd  # noqa: F401
 import oracle
 from deep_optimization_amd.modules.activations import DOGELU, DOReLU_Variance, DOSiLU
+from deep_optimization_amd.modules.ops import GroupPACTClampFn
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -229,3 +230,48 @@ def test_relu_layer_padding_path_uses_pack_only():
     y.backward(torch.ones_like(y))
     assert torch.equal(y, torch.relu(x.detach()))
     assert torch.equal(x.grad, (x.detach() > 0).to(x.dtype))
+
+
+# ----------------------------------------------------------------------------- PACT clamp
+@pytest.mark.parametrize("alpha", [3.0, 0.75])
+@pytest.mark.parametrize("numel", [7, 4099, 65544])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32, torch.float16], ids=["bf16", "f32", "f16"])
+def test_group_pact_clamp_ops_bit_exact(dtype, numel, alpha):
+    """act_lib::group_pact_clamp_fwd / _bwd against the oracle, bit for bit: bf16 y, int8 mask, and
+    the gradient for bf16 / fp32 / fp16 dy; inputs at exactly +-alpha and a NaN included."""
+    x = randn((numel,), seed=numel, scale=2.0, dtype=dtype)
+    x[:3] = torch.tensor([alpha, -alpha, float("nan")]).to(dtype)
+    y, mask = torch.ops.act_lib.group_pact_clamp_fwd(x.to(DEV), alpha)
+    ry, rmask = oracle.pact_clamp_fwd(np_view(x), alpha)
+    np.testing.assert_array_equal(np_view(y), ry)
+    np.testing.assert_array_equal(mask.cpu().numpy(), rmask)
+    for dyt in (torch.bfloat16, torch.float32, torch.float16):
+        dy = randn((numel,), seed=3, scale=1.0, dtype=dyt)
+        dx = torch.ops.act_lib.group_pact_clamp_bwd(mask, alpha, dy.to(DEV))
+        np.testing.assert_array_equal(np_view(dx), oracle.pact_clamp_bwd(rmask, np_view(dy)))
+
+
+@pytest.mark.parametrize("shape,g,pad,alpha", [((4, 8, 32, 32), 256, False, 1.5), ((4, 8, 32, 32), 64, False, "tensor"),
+                                               ((6, 3, 10, 10), 256, True, 1.5), ((64, 512), 128, False, 1.5)])
+def test_group_pact_clamp_function(shape, g, pad, alpha):
+    """GroupPACTClampFn: the forward's bf16 clamp bit for bit against the oracle, the mask saved
+    as 1-bit packed codes, and the backward dy * mask in element order; spatial-tile grouping with
+    several tiles per channel map (32x32 maps in 16x16 and 8x8 tiles), flat groups zero-padded per
+    sample (10x10 maps, act_padding), a 2-D input; alpha a float or a one-element tensor (the reference layers pass an nn.Parameter)."""
+    a = torch.tensor([1.5], dtype=torch.bfloat16, device=DEV) if alpha == "tensor" else alpha
+    x = randn(shape, seed=1, scale=2.0).to(DEV).requires_grad_(True)
+    meta = {"conv": {"act_padding": pad, "N": shape[0]}}
+    y = GroupPACTClampFn.apply(x, a, g, meta, "conv")
+    ry, rmask = oracle.pact_clamp_fwd(np_view(x.detach()), 1.5)
+    np.testing.assert_array_equal(np_view(y).reshape(-1), ry.reshape(-1))
+    dy = randn(x.shape, seed=2, scale=1.0).to(DEV)
+    y.backward(dy)
+    want = dy * torch.from_numpy(rmask).to(DEV).view(x.shape)
+    assert x.grad.dtype == want.dtype and torch.equal(x.grad, want)
+
+
+def test_group_pact_clamp_rejects_non_positive_alpha():
+    x = torch.randn(64, device=DEV).to(torch.bfloat16)
+    for bad in (0.0, -1.0, float("nan")):
+        with pytest.raises(RuntimeError, match="alpha must be > 0"):
+            torch.ops.act_lib.group_pact_clamp_fwd(x, bad)

@@ -231,6 +231,26 @@ def test_quantize_pack_only_meta():
         assert y.shape == x.shape and y.dtype == torch.int8
 
 
+def test_quantize_pack_only_tile_meta_inverts_the_grouping():
+    """A 1-bit mask grouped into spatial tiles (32x32 maps, 8x8 tiles) keeps its tile flags in the meta,
+    so the restore puts every bit back at its element. The reference's pack-only meta
+    (module_utils.py:40,55) records (0, 0, False, False) here, and its restore returns the tile-ordered
+    codes in flat order: a deliberate deviation, pinned by the brute-force inverse below."""
+    shape, g = (2, 3, 32, 32), 64
+    with FakeTensorMode():
+        x = torch.empty(shape, dtype=torch.int8, device="cuda")
+        (p, s, m), qm, _ = mu.unified_quantize(x, None, "layer", _meta(1, g, False, 2, pack_only=True), False, 1.0)
+        assert s is None and m is None and p.shape == (2 * 3 * 16, g // 32)
+    assert qm[:11] == (1, True, g, False, 2, 3 * 16, 4, 4, False, True, False)
+    x = (torch.rand(shape, generator=torch.Generator().manual_seed(0)) < 0.5).to(torch.int8)
+    groups = tr.spatical_aware_act_tensor_reshape(x, g, False, True)[0]
+    # group j of sample n holds the 8x8 tile (c, th, tw) = divmod over (C, 4, 4), row-major inside
+    c, th, tw = 1, 2, 3
+    assert torch.equal(groups[1, (c * 4 + th) * 4 + tw].view(8, 8), x[1, c, 8 * th:8 * th + 8, 8 * tw:8 * tw + 8])
+    back = tr.spatical_aware_act_tensor_reshape_back(groups, shape, g, qm[6], qm[7], qm[3], qm[8], qm[9], qm[10])
+    assert torch.equal(back, x)
+
+
 def test_non_square_group_with_divisible_map_raises():
     x = torch.zeros(1, 2, 22, 22)
     with pytest.raises(RuntimeError, match="square group size"):

@@ -701,3 +701,62 @@ def test_silu_alam_backward_adds_the_rand_noise():
     plain = _bf16_to_f32(oracle.act_dequant_mul(p, s, m, g, bits, dy)).astype(np.float64)
     np.testing.assert_allclose(plain, dy * (codes * sc[:, None] + mn[:, None]), rtol=2.0 ** -7, atol=1e-30)
     assert np.mean(got != plain) > 0.5
+
+
+# ----------------------------------------------------------------------------- PACT clamp
+def _torch_bf16_bits(a):
+    """torch's own fp32 -> bf16 rounding (RNE), as uint16 bit patterns"""
+    return torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32)).to(torch.bfloat16).view(torch.int16).numpy() \
+        .view(np.uint16)
+
+
+@pytest.mark.parametrize("dtype", ["f32", "f16", "bf16"])
+@pytest.mark.parametrize("alpha", [3.0, 0.5, 1e-3, float("inf")])
+def test_pact_clamp_forward_closed_form(dtype, alpha):
+    """y = torch's bf16 of numpy clip(x, -alpha, alpha) and mask = |x| <= alpha, element for element;
+    inputs at exactly +-alpha, +-0, past alpha and large; a NaN x gives -alpha and mask 0 (fmax then
+    fmin)."""
+    rng = np.random.default_rng(int(alpha * 1000) if np.isfinite(alpha) else 99)
+    vals = np.concatenate([rng.standard_normal(4096) * 4, [alpha, -alpha, 0.0, -0.0, 1e30, -1e30]])
+    vals = vals[np.isfinite(vals)].astype(np.float32)
+    if dtype == "bf16":
+        x = _torch_bf16_bits(vals)
+        xf = oracle.bf16_bits_to_f32(x)
+    elif dtype == "f16":
+        x = vals.astype(np.float16)
+        xf = x.astype(np.float32)
+    else:
+        x = vals
+        xf = x
+    y, mask = oracle.pact_clamp_fwd(x, alpha)
+    np.testing.assert_array_equal(y, _torch_bf16_bits(np.clip(xf, np.float32(-alpha), np.float32(alpha))))
+    np.testing.assert_array_equal(mask, (np.abs(xf) <= np.float32(alpha)).astype(np.int8))
+    if np.isfinite(alpha):
+        assert mask[np.abs(xf) == np.float32(alpha)].all()  # the boundary is inside (<=, not <)
+    yn, mn = oracle.pact_clamp_fwd(np.array([np.nan], dtype=np.float32), alpha)
+    assert yn[0] == _torch_bf16_bits(np.array([-alpha]))[0] and mn[0] == 0  # bf16(-alpha)
+
+
+@pytest.mark.parametrize("dtype", ["f32", "f16", "bf16"])
+def test_pact_clamp_backward_closed_form(dtype):
+    """dx = torch's bf16 of where(mask != 0, dy, +0): any non-zero mask byte passes dy."""
+    rng = np.random.default_rng(5)
+    dyf = (rng.standard_normal(1031) * 3).astype(np.float32)
+    mask = rng.integers(-3, 3, size=1031).astype(np.int8)
+    if dtype == "bf16":
+        dy = _torch_bf16_bits(dyf)
+        dyv = oracle.bf16_bits_to_f32(dy)
+    elif dtype == "f16":
+        dy = dyf.astype(np.float16)
+        dyv = dy.astype(np.float32)
+    else:
+        dy, dyv = dyf, dyf
+    got = oracle.pact_clamp_bwd(mask, dy)
+    np.testing.assert_array_equal(got, _torch_bf16_bits(np.where(mask != 0, dyv, np.float32(0.0))))
+    assert not (got[mask == 0] & 0x8000).any()  # +0, never -0, where the mask is clear
+
+
+def test_pact_clamp_rejects_non_positive_or_nan_alpha():
+    for bad in (-1.0, 0.0, float("nan")):
+        with pytest.raises(oracle.OracleError):
+            oracle.pact_clamp_fwd(np.zeros(4, dtype=np.float32), bad)
