@@ -613,7 +613,7 @@ def _group_pact_clamp_bwd(mask, alpha, dy):
         raise RuntimeError(f"group_pact_clamp_bwd: mask must be int8 with dy's {dy.numel()} elements, "
                            f"got {mask.dtype} with {mask.numel()}")
     _require_cuda(mask, dy)
-    mask = _aligned(mask.view(dy.shape))
+    mask = _aligned(mask).view(dy.shape)
     dy = _aligned(dy)
     dx = torch.empty(dy.shape, dtype=torch.bfloat16, device=dy.device)
     rc = _lib.lib().dopt_pact_clamp_backward(mask.data_ptr(), dy.data_ptr(), _DTYPE_CODE[dy.dtype], dy.numel(),

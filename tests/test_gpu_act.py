@@ -270,6 +270,37 @@ def test_group_pact_clamp_function(shape, g, pad, alpha):
     assert x.grad.dtype == want.dtype and torch.equal(x.grad, want)
 
 
+def test_group_pact_clamp_function_under_autocast():
+    """Under autocast the Function clamps the input cast to the autocast dtype (as the reference's
+    forward does): fp32 x under fp16 autocast equals the clamp of x.half(); the gradient reaches the
+    fp32 leaf as fp32."""
+    x = randn((2, 4, 16, 16), seed=11, scale=2.0, dtype=torch.float32).to(DEV).requires_grad_(True)
+    meta = {"conv": {"act_padding": False, "N": 2}}
+    with torch.autocast("cuda", dtype=torch.float16):
+        y = GroupPACTClampFn.apply(x, 0.8, 64, meta, "conv")
+    ry, rmask = oracle.pact_clamp_fwd(np_view(x.detach().half()), 0.8)
+    np.testing.assert_array_equal(np_view(y).reshape(-1), ry.reshape(-1))
+    dy = randn(x.shape, seed=12, scale=1.0).to(DEV)
+    y.backward(dy)
+    assert x.grad.dtype == torch.float32
+    assert torch.equal(x.grad, (dy * torch.from_numpy(rmask).to(DEV).view(x.shape)).float())
+
+
+def test_group_pact_clamp_empty_and_strided_inputs():
+    """Empty tensors give empty outputs without a launch; a transposed input and a strided mask are
+    read in their logical order."""
+    y, mask = torch.ops.act_lib.group_pact_clamp_fwd(torch.empty(0, 5, device=DEV), 1.0)
+    assert y.shape == (0, 5) and y.dtype == torch.bfloat16 and mask.shape == (0, 5) and mask.dtype == torch.int8
+    x = randn((96, 40), seed=8, scale=2.0, dtype=torch.float32).to(DEV).t()
+    y, mask = torch.ops.act_lib.group_pact_clamp_fwd(x, 1.25)
+    ry, rmask = oracle.pact_clamp_fwd(np_view(x.contiguous()), 1.25)
+    np.testing.assert_array_equal(np_view(y), ry)
+    np.testing.assert_array_equal(mask.cpu().numpy(), rmask)
+    dy = randn((40, 96), seed=9, scale=1.0).to(DEV)
+    dx = torch.ops.act_lib.group_pact_clamp_bwd(mask.t().contiguous().t(), 1.25, dy)
+    np.testing.assert_array_equal(np_view(dx), oracle.pact_clamp_bwd(rmask, np_view(dy)))
+
+
 def test_group_pact_clamp_rejects_non_positive_alpha():
     x = torch.randn(64, device=DEV).to(torch.bfloat16)
     for bad in (0.0, -1.0, float("nan")):
