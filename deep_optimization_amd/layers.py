@@ -16,7 +16,13 @@ Differences from the reference:
     without ``.apply`` (:126), so their training forward raises in the reference. Their eval
     forward keeps the reference's input clamp to [-clamp_alpha, clamp_alpha] (:62, :138);
   * with a non-zeros ``padding_mode`` the input is padded once, as nn.Conv does; the reference
-    pads it with F.pad and then again through the Function's ``padding`` (layers.py:86-90).
+    pads it with F.pad and then again through the Function's ``padding`` (layers.py:86-90);
+  * the PACT clamp the reference's DOConv1d / DOConv3d put in front of the Function (layers.py:69,
+    :74, :152, :157, with the never-defined ``self.pact_alpha``) is opt-in on every Conv layer: a
+    ``pact_alpha`` (float or one-element tensor) runs ``GroupPACTClampFn`` on the training input
+    first; without autocast its bf16 output is cast back to the input's dtype (exactly: the values
+    are bf16) so that the convolution's operands agree. The default, None, is the reference's
+    behaviour on every path that runs there.
 """
 from __future__ import annotations
 
@@ -24,7 +30,7 @@ import torch
 import torch.nn.functional as F
 from torch import nn
 
-from .modules.ops import _DOConv1d, _DOConv2d, _DOConv3d, _DOLinear
+from .modules.ops import GroupPACTClampFn, _DOConv1d, _DOConv2d, _DOConv3d, _DOLinear
 
 
 class DOLinear(nn.Linear):
@@ -47,8 +53,9 @@ class _DOConvMixin:
     _fn = None
     _eval_clamp = False
 
-    def _init_do(self, clamp_alpha, target_name, meta):
+    def _init_do(self, clamp_alpha, target_name, meta, pact_alpha):
         self.clamp_alpha = clamp_alpha
+        self.pact_alpha = pact_alpha
         self.target_name = target_name
         self.meta = {} if meta is None else meta
         self.ema_grad_meta = None
@@ -56,6 +63,10 @@ class _DOConvMixin:
 
     def forward(self, x):
         if self.training:
+            if self.pact_alpha is not None:
+                y = GroupPACTClampFn.apply(x, self.pact_alpha, self.meta[f"{self.target_name}"]["group_size"],
+                                           self.meta, self.target_name)
+                x = y if torch.is_autocast_enabled("cuda") else y.to(x.dtype)
             if self.padding_mode != "zeros":
                 x = F.pad(x, self._reversed_padding_repeated_twice, mode=self.padding_mode)
                 padding = 0
@@ -81,10 +92,10 @@ class DOConv1d(_DOConvMixin, nn.Conv1d):
 
     def __init__(self, in_channels, out_channels, kernel_size, stride=1, padding=0, dilation=1, groups=1,
                  padding_mode="zeros", clamp_alpha=3.0, target_name=None, meta=None, bias=False, device=None,
-                 dtype=None):
+                 dtype=None, pact_alpha=None):
         nn.Conv1d.__init__(self, in_channels, out_channels, kernel_size, stride, padding, dilation, groups, bias=bias,
                            padding_mode=padding_mode, device=device, dtype=dtype)
-        self._init_do(clamp_alpha, target_name, meta)
+        self._init_do(clamp_alpha, target_name, meta, pact_alpha)
 
 
 class DOConv2d(_DOConvMixin, nn.Conv2d):
@@ -92,10 +103,10 @@ class DOConv2d(_DOConvMixin, nn.Conv2d):
 
     def __init__(self, in_channels, out_channels, kernel_size, stride=1, padding=0, dilation=1, groups=1,
                  padding_mode="zeros", clamp_alpha=3.0, target_name=None, meta=None, bias=False, device=None,
-                 dtype=None):
+                 dtype=None, pact_alpha=None):
         nn.Conv2d.__init__(self, in_channels, out_channels, kernel_size, stride, padding, dilation, groups, bias=bias,
                            padding_mode=padding_mode, device=device, dtype=dtype)
-        self._init_do(clamp_alpha, target_name, meta)
+        self._init_do(clamp_alpha, target_name, meta, pact_alpha)
 
 
 class DOConv3d(_DOConvMixin, nn.Conv3d):
@@ -104,10 +115,10 @@ class DOConv3d(_DOConvMixin, nn.Conv3d):
 
     def __init__(self, in_channels, out_channels, kernel_size, stride=1, padding=0, dilation=1, groups=1,
                  padding_mode="zeros", clamp_alpha=3.0, target_name=None, meta=None, bias=False, device=None,
-                 dtype=None):
+                 dtype=None, pact_alpha=None):
         nn.Conv3d.__init__(self, in_channels, out_channels, kernel_size, stride, padding, dilation, groups, bias=bias,
                            padding_mode=padding_mode, device=device, dtype=dtype)
-        self._init_do(clamp_alpha, target_name, meta)
+        self._init_do(clamp_alpha, target_name, meta, pact_alpha)
 
 
 class RMSNorm(nn.Module):

@@ -144,6 +144,39 @@ def test_do_conv2d(bits, case):
     assert rel_err(x.grad, want_dx) <= 1e-2
 
 
+@pytest.mark.parametrize("autocast", [True, False])
+def test_do_conv2d_pact_clamp(autocast):
+    """pact_alpha set: the training input goes through GroupPACTClampFn first. The forward is the
+    convolution of clamp(bf16(x), -1, 1); the weight gradient uses the clamped input's quantized
+    copy (16 x 16 tiles); the input gradient is the convolution's, zero where |x| > alpha."""
+    torch.manual_seed(5)
+    shape, bits, g = (4, 64, 32, 32), 2, 256
+    meta = meta_for("conv", shape, bits, group_size=g, NG=4 * 64 * 4)
+    layer = DOConv2d(shape[1], 96, 3, padding=1, target_name="conv", meta=meta, pact_alpha=1.0).to(DEV).train()
+    x = torch.randn(shape, device=DEV).requires_grad_(True)
+    xc = x.detach().bfloat16().clamp(-1.0, 1.0)
+    with torch.autocast("cuda", dtype=torch.bfloat16, enabled=autocast):
+        y = layer(x)
+    if autocast:
+        want_y = F.conv2d(xc, layer.weight.detach().bfloat16(), None, 1, 1)
+        assert torch.equal(y, want_y)
+    else:
+        assert y.dtype == torch.float32
+        assert rel_err(y, F.conv2d(xc.float(), layer.weight.detach(), None, 1, 1)) <= 1e-6
+    dy = torch.randn_like(y)
+    y.backward(dy)
+    packed, scale, xmin = torch.ops.act_lib.quant_pack_tiles(xc, bits, g, True, 3.0, True, 0, None, 0, 0,
+                                                              torch.bfloat16)
+    x_hat = torch.ops.act_lib.dequant_unpack_tiles(packed, scale, xmin, bits, g, *shape, torch.bfloat16)
+    dyf = dy.float()
+    assert rel_err(layer.weight.grad, conv2d_weight(x_hat.float(), layer.weight.shape, dyf, padding=1)) <= 1e-2
+    w = layer.weight.detach().bfloat16().float() if autocast else layer.weight.detach()
+    # the mask is |x| <= alpha on the tensor the clamp reads: bf16 under autocast, the fp32 x without
+    inside = (x.detach().bfloat16() if autocast else x.detach()).abs() <= 1.0
+    assert x.grad.dtype == torch.float32 and not x.grad[~inside].any()
+    assert rel_err(x.grad, conv2d_input(shape, w, dyf, padding=1) * inside) <= 1e-2
+
+
 def test_tile_layout_reference_chain_matches_flat_permutation():
     """The in-place tile operators equal the reference's permuted copy
     (tensor_act_reshape_utils.py:115-125) followed by the flat operators."""
