@@ -87,7 +87,7 @@ __global__ __launch_bounds__(256) void relu_pack_kernel(const void* __restrict__
                                                         uint32_t* __restrict__ packed, uint64_t n) {
     constexpr int UBITS = CE * BITS;  // code bits per chunk
     const int lane = threadIdx.x & 63;
-    const uint64_t c = ((uint64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * 64 + lane;  // chunk index
+    const uint64_t c = (linear_block() * 4 + (threadIdx.x >> 6)) * 64 + lane;  // chunk index
     const uint64_t e0 = c * CE;
     const bool ok = e0 < n;
     uint32_t mbits = 0;  // one bit per element
@@ -141,7 +141,7 @@ template <int DYT, int BITS>
 __global__ __launch_bounds__(256) void relu_unpack_kernel(const uint32_t* __restrict__ packed, const void* __restrict__ dy,
                                                           void* __restrict__ dx, uint64_t n) {
     constexpr int UBITS = CE * BITS;
-    const uint64_t c = ((uint64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * 64 + (threadIdx.x & 63);
+    const uint64_t c = (linear_block() * 4 + (threadIdx.x >> 6)) * 64 + (threadIdx.x & 63);
     const uint64_t e0 = c * CE;
     if (e0 >= n) return;
     uint32_t cw[UBITS > 32 ? 2 : 1];
@@ -174,7 +174,7 @@ __device__ __forceinline__ float load1(const void* base, uint64_t e) {
 template <int DT, int ACT>
 __global__ __launch_bounds__(256) void act_forward_kernel(const void* __restrict__ x, void* __restrict__ y,
                                                           void* __restrict__ aux, uint64_t n) {
-    const uint64_t c = ((uint64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * 64 + (threadIdx.x & 63);
+    const uint64_t c = (linear_block() * 4 + (threadIdx.x >> 6)) * 64 + (threadIdx.x & 63);
     const uint64_t e0 = c * CE;
     if (e0 >= n) return;
     if (e0 + CE > n) {
@@ -234,7 +234,7 @@ template <int DT>
 __global__ __launch_bounds__(256) void pact_clamp_fwd_kernel(const void* __restrict__ x, float alpha,
                                                              void* __restrict__ y, int8_t* __restrict__ mask,
                                                              uint64_t n) {
-    const uint64_t c = ((uint64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * 64 + (threadIdx.x & 63);
+    const uint64_t c = (linear_block() * 4 + (threadIdx.x >> 6)) * 64 + (threadIdx.x & 63);
     const uint64_t e0 = c * CE;
     if (e0 >= n) return;
     if (e0 + CE > n) {  // ragged tail: one element at a time
@@ -260,7 +260,7 @@ __global__ __launch_bounds__(256) void pact_clamp_fwd_kernel(const void* __restr
 template <int DYT>
 __global__ __launch_bounds__(256) void pact_clamp_bwd_kernel(const int8_t* __restrict__ mask, const void* __restrict__ dy,
                                                              void* __restrict__ dx, uint64_t n) {
-    const uint64_t c = ((uint64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * 64 + (threadIdx.x & 63);
+    const uint64_t c = (linear_block() * 4 + (threadIdx.x >> 6)) * 64 + (threadIdx.x & 63);
     const uint64_t e0 = c * CE;
     if (e0 >= n) return;
     if (e0 + CE > n) {
@@ -280,7 +280,7 @@ int launch_flat(K kernel, uint64_t n, hipStream_t s, Args... args) {
     const uint64_t chunks = (n + CE - 1) / CE;
     const uint64_t blocks = (chunks + 255) / 256;
     if (blocks == 0) return 0;
-    hipLaunchKernelGGL(kernel, dim3((uint32_t)blocks), dim3(256), 0, s, args..., n);
+    hipLaunchKernelGGL(kernel, linear_grid(blocks, 256), dim3(256), 0, s, args..., n);
     return 0;
 }
 

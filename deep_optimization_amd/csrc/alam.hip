@@ -58,7 +58,7 @@ __global__ __launch_bounds__(64 * ALAM_WAVES) void alam_quant_pack_kernel(AlamAr
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     // a wave past the last group redoes the last one and stores nothing, so every wave reaches
     // the barrier (n_groups >= 1: the launcher skips empty calls)
-    const int64_t r0 = (int64_t)blockIdx.x * ALAM_WAVES + wave;
+    const int64_t r0 = (int64_t)linear_block() * ALAM_WAVES + wave;
     const bool active = r0 < a.n_groups;
     const int64_t r = active ? r0 : a.n_groups - 1;
     const int g = a.g, per = g / 64;
@@ -121,7 +121,7 @@ struct AlamDqArgs {
 };
 
 __global__ __launch_bounds__(256) void alam_dequant_kernel(AlamDqArgs a) {
-    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int64_t i = (int64_t)linear_block() * 256 + threadIdx.x;
     if (i >= a.total) return;
     const int64_t r = i / a.g;
     const int e = (int)(i - r * a.g);
@@ -158,7 +158,7 @@ __device__ __forceinline__ uint64_t alam_elem_index(const DequantArgs& a, uint32
 }
 
 __global__ __launch_bounds__(256) void alam_act_dequant_mul_kernel(AlamDyArgs a) {
-    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int64_t i = (int64_t)linear_block() * 256 + threadIdx.x;
     if (i >= a.total) return;
     const uint32_t r = (uint32_t)(i / a.g), e = (uint32_t)(i - (int64_t)r * a.g);
     const int vpw = 32 / a.bits, nw = a.g / vpw;
@@ -182,14 +182,14 @@ __global__ __launch_bounds__(256) void alam_act_dequant_mul_kernel(AlamDyArgs a)
 
 int launch_alam_act_dequant_mul(const DequantArgs& d, int g, int bits, int dy_f32, uint64_t seed, hipStream_t s) {
     const AlamDyArgs a{d, g, bits, dy_f32, seed, (int64_t)d.n_groups * g};
-    hipLaunchKernelGGL(alam_act_dequant_mul_kernel, dim3((unsigned)((a.total + 255) / 256)), dim3(256), 0, s, a);
+    hipLaunchKernelGGL(alam_act_dequant_mul_kernel, linear_grid((uint64_t)(a.total + 255) / 256, 256), dim3(256), 0, s, a);
     return 0;
 }
 
 int launch_alam_quant_pack(const void* x, int dt, int64_t n_groups, int g, int bits, int alam, int flags,
                            float clamp_alpha, uint32_t* packed, uint16_t* scale, uint16_t* minv, hipStream_t s) {
     const AlamArgs a{x, packed, scale, minv, n_groups, g, bits, alam, flags, clamp_alpha};
-    const dim3 grid((unsigned)((n_groups + ALAM_WAVES - 1) / ALAM_WAVES));
+    const dim3 grid = linear_grid((uint64_t)(n_groups + ALAM_WAVES - 1) / ALAM_WAVES, 64 * ALAM_WAVES);
     if (dt == DT_F32) hipLaunchKernelGGL(alam_quant_pack_kernel<DT_F32>, grid, dim3(64 * ALAM_WAVES), 0, s, a);
     else if (dt == DT_F16) hipLaunchKernelGGL(alam_quant_pack_kernel<DT_F16>, grid, dim3(64 * ALAM_WAVES), 0, s, a);
     else hipLaunchKernelGGL(alam_quant_pack_kernel<DT_BF16>, grid, dim3(64 * ALAM_WAVES), 0, s, a);
@@ -199,7 +199,7 @@ int launch_alam_quant_pack(const void* x, int dt, int64_t n_groups, int g, int b
 int launch_alam_dequant(const uint32_t* packed, const uint16_t* scale, const uint16_t* minv, int64_t n_groups,
                         int g, int bits, int alam, uint64_t seed, uint16_t* y, hipStream_t s) {
     const AlamDqArgs a{packed, scale, minv, y, n_groups * g, g, bits, alam, seed};
-    const dim3 grid((unsigned)((a.total + 255) / 256));
+    const dim3 grid = linear_grid((uint64_t)(a.total + 255) / 256, 256);
     hipLaunchKernelGGL(alam_dequant_kernel, grid, dim3(256), 0, s, a);
     return 0;
 }

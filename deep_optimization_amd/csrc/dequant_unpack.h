@@ -79,7 +79,7 @@ __global__ __launch_bounds__(256) void dequant_unpack_kernel(DequantArgs a) {
     const int wv = threadIdx.x >> 6;
     const int slot = lane / LPG;
     const int li = lane % LPG;
-    const uint32_t g0 = (blockIdx.x * C::WAVES + wv) * (uint32_t)C::GPW;
+    const uint32_t g0 = (uint32_t)((linear_block() * C::WAVES + wv) * C::GPW);  // < 2^32 as in quant_pack
 
     // ---- each lane loads its groups' scale and min itself (the LPG lanes of a group read the
     // same address, one request); no staging, so the waves of a workgroup never wait for each other

@@ -26,12 +26,12 @@ static int dq_launch(const DequantArgs& a, hipStream_t s) {
     if (blocks == 0) return 0;
     if (!a.tiled) {
         hipLaunchKernelGGL((dequant_unpack_kernel<YT, BITS, G, S::UB, S::LPG, S::P, true, DYT, false>),
-                           dim3((uint32_t)blocks), dim3(64 * C::WAVES), 0, s, a);
+                           linear_grid(blocks, 64 * C::WAVES), dim3(64 * C::WAVES), 0, s, a);
         return 0;
     }
     if constexpr (G == 64 || G == 256 || G == 1024) {  // the square group sizes
         hipLaunchKernelGGL((dequant_unpack_kernel<YT, BITS, G, S::UB, S::LPG, S::P, true, DYT, true>),
-                           dim3((uint32_t)blocks), dim3(64 * C::WAVES), 0, s, a);
+                           linear_grid(blocks, 64 * C::WAVES), dim3(64 * C::WAVES), 0, s, a);
         return 0;
     }
     return -1;

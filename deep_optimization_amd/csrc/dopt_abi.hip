@@ -52,19 +52,6 @@ int ok() {
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
-// The flat elementwise kernels (ReLU pack / unpack, activation forward, PACT clamp) run one
-// 256-lane workgroup per 2048 elements, and one dispatch holds at most 2^32 - 1 work-items, i.e.
-// 2^24 - 1 workgroups.
-constexpr int64_t kFlatMaxElems = (int64_t)((1 << 24) - 1) * 2048;
-static_assert(kFlatMaxElems == DOPT_FLAT_MAX_ELEMS, "the header's bound");
-
-int check_flat_n(int64_t n, const char* what) {
-    if (n > kFlatMaxElems)
-        return fail(DOPT_EINVAL, "%s: n = %lld exceeds the %lld elements of one launch", what, (long long)n,
-                    (long long)kFlatMaxElems);
-    return DOPT_OK;
-}
-
 int check_bits(int bits) {
     if (bits != 1 && bits != 2 && bits != 4 && bits != 8)
         return fail(DOPT_EBITS, "bits must be one of (1,2,4,8). got %d", bits);
@@ -433,7 +420,6 @@ int dopt_relu_pack(const void* x, int x_dtype, int64_t n, int relu6, int bits, v
     if (x_dtype != DOPT_F32 && x_dtype != DOPT_BF16)
         return fail(DOPT_EINVAL, "relu_pack: input dtype must be F32 or BF16, got code %d", x_dtype);
     if (n < 0 || n % 64) return fail(DOPT_EINVAL, "relu_pack: n must be a non-negative multiple of 64, got %lld", (long long)n);
-    if ((rc = check_flat_n(n, "relu_pack"))) return rc;
     if (n == 0) return ok();
     if (!x || !y || !packed) return fail(DOPT_EINVAL, "null pointer argument");
     if (!aligned16(x) || !aligned16(y) || !aligned16(packed)) return fail(DOPT_EINVAL, "x, y and packed must be 16-byte aligned");
@@ -449,7 +435,6 @@ int dopt_relu_unpack(const uint32_t* packed, const void* dy, int dy_dtype, int64
     if (dy_dtype != DOPT_F32 && dy_dtype != DOPT_F16 && dy_dtype != DOPT_BF16)
         return fail(DOPT_EINVAL, "relu_unpack: unsupported dy dtype code %d", dy_dtype);
     if (n < 0 || n % 64) return fail(DOPT_EINVAL, "relu_unpack: n must be a non-negative multiple of 64, got %lld", (long long)n);
-    if ((rc = check_flat_n(n, "relu_unpack"))) return rc;
     if (n == 0) return ok();
     if (!packed || !dy || !dx) return fail(DOPT_EINVAL, "null pointer argument");
     if (!aligned16(dy) || !aligned16(dx) || ((uintptr_t)packed & 7u))
@@ -465,7 +450,6 @@ int dopt_act_forward(const void* x, int x_dtype, int64_t n, int act, void* y, vo
         return fail(DOPT_EINVAL, "act_forward: unsupported input dtype code %d", x_dtype);
     if (act < DOPT_ACT_RELU || act > DOPT_ACT_SILU) return fail(DOPT_EINVAL, "act_forward: unknown activation %d", act);
     if (n < 0) return fail(DOPT_EINVAL, "act_forward: negative n");
-    if (int rc = check_flat_n(n, "act_forward")) return rc;
     if (n == 0) return ok();
     if (!x || !y || !aux) return fail(DOPT_EINVAL, "null pointer argument");
     if (!aligned16(x) || !aligned16(y) || !aligned16(aux)) return fail(DOPT_EINVAL, "x, y and aux must be 16-byte aligned");
@@ -481,7 +465,6 @@ int dopt_pact_clamp_forward(const void* x, int x_dtype, int64_t n, float alpha, 
         return fail(DOPT_EINVAL, "pact_clamp_forward: unsupported input dtype code %d", x_dtype);
     if (!(alpha > 0.0f)) return fail(DOPT_EINVAL, "pact_clamp_forward: alpha must be > 0 (not NaN), got %g", alpha);
     if (n < 0) return fail(DOPT_EINVAL, "pact_clamp_forward: negative n");
-    if (int rc = check_flat_n(n, "pact_clamp_forward")) return rc;
     if (n == 0) return ok();
     if (!x || !y || !mask) return fail(DOPT_EINVAL, "null pointer argument");
     if (!aligned16(x) || !aligned16(y) || ((uintptr_t)mask & 7u))
@@ -496,7 +479,6 @@ int dopt_pact_clamp_backward(const int8_t* mask, const void* dy, int dy_dtype, i
     if (dy_dtype != DOPT_F32 && dy_dtype != DOPT_F16 && dy_dtype != DOPT_BF16)
         return fail(DOPT_EINVAL, "pact_clamp_backward: unsupported dy dtype code %d", dy_dtype);
     if (n < 0) return fail(DOPT_EINVAL, "pact_clamp_backward: negative n");
-    if (int rc = check_flat_n(n, "pact_clamp_backward")) return rc;
     if (n == 0) return ok();
     if (!mask || !dy || !dx) return fail(DOPT_EINVAL, "null pointer argument");
     if (!aligned16(dy) || !aligned16(dx) || ((uintptr_t)mask & 7u))

@@ -21,6 +21,22 @@ struct DType {
     static constexpr int per16 = 16 / bytes;  // elements in one 16-byte chunk
 };
 
+// ------------------------------------------------------------------ grids past 2^32 work-items
+// A dispatch's grid size is a 32-bit count of work-items per dimension, so a 1-D grid holds at
+// most 2^32 - 1 work-items. Launchers whose block count grows with the input take linear_grid():
+// a 1-D grid while it fits, else rows of GRID_ROW blocks, block b at x = b % GRID_ROW and
+// y = b / GRID_ROW. Kernels recover b with linear_block() (every row of a multi-row grid is
+// GRID_ROW wide); the blocks past the last one, in the final row, take the kernels' own
+// past-the-end path (loads clamped or skipped, no stores).
+constexpr uint32_t GRID_ROW = 1u << 16;
+
+inline dim3 linear_grid(uint64_t blocks, uint32_t threads) {
+    if (blocks * threads <= 0xFFFFFFFFull) return dim3((uint32_t)blocks);
+    return dim3(GRID_ROW, (uint32_t)((blocks + GRID_ROW - 1) / GRID_ROW));
+}
+
+__device__ __forceinline__ uint64_t linear_block() { return (uint64_t)blockIdx.y * GRID_ROW + blockIdx.x; }
+
 // ------------------------------------------------------------------ lane permutes (DPP)
 // DPP controls: quad_perm [1,0,3,2] = 0xB1 (lane ^ 1), quad_perm [2,3,0,1] = 0x4E (lane ^ 2),
 // row_half_mirror = 0x141 (lane i <-> 7-i within 8), row_mirror = 0x140 (i <-> 15-i within 16),

@@ -11,7 +11,7 @@ template <int BITS>
 __global__ __launch_bounds__(256) void pack_codes_kernel(const int8_t* __restrict__ codes, uint32_t* __restrict__ out,
                                                          uint64_t n_words) {
     constexpr int VPW = 32 / BITS;
-    const uint64_t w = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+    const uint64_t w = linear_block() * 256 + threadIdx.x;
     if (w >= n_words) return;
     uint32_t b[8];
     const int8_t* src = codes + w * VPW;
@@ -42,7 +42,7 @@ __global__ __launch_bounds__(256) void unpack_codes_kernel(const uint32_t* __res
                                                            uint64_t n_words) {
     constexpr int VPW = 32 / BITS;
     constexpr uint32_t QMAX = (1u << BITS) - 1u;
-    const uint64_t w = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+    const uint64_t w = linear_block() * 256 + threadIdx.x;
     if (w >= n_words) return;
     const uint32_t word = packed[w];
     uint32_t b[8] = {0, 0, 0, 0, 0, 0, 0, 0};
@@ -65,10 +65,10 @@ int launch_pack_codes(const int8_t* codes, uint32_t* out, uint64_t n_words, int 
     const uint64_t blocks = (n_words + 255) / 256;
     if (blocks == 0) return 0;
     switch (bits) {
-        case 1: hipLaunchKernelGGL(pack_codes_kernel<1>, dim3(blocks), dim3(256), 0, s, codes, out, n_words); return 0;
-        case 2: hipLaunchKernelGGL(pack_codes_kernel<2>, dim3(blocks), dim3(256), 0, s, codes, out, n_words); return 0;
-        case 4: hipLaunchKernelGGL(pack_codes_kernel<4>, dim3(blocks), dim3(256), 0, s, codes, out, n_words); return 0;
-        case 8: hipLaunchKernelGGL(pack_codes_kernel<8>, dim3(blocks), dim3(256), 0, s, codes, out, n_words); return 0;
+        case 1: hipLaunchKernelGGL(pack_codes_kernel<1>, linear_grid(blocks, 256), dim3(256), 0, s, codes, out, n_words); return 0;
+        case 2: hipLaunchKernelGGL(pack_codes_kernel<2>, linear_grid(blocks, 256), dim3(256), 0, s, codes, out, n_words); return 0;
+        case 4: hipLaunchKernelGGL(pack_codes_kernel<4>, linear_grid(blocks, 256), dim3(256), 0, s, codes, out, n_words); return 0;
+        case 8: hipLaunchKernelGGL(pack_codes_kernel<8>, linear_grid(blocks, 256), dim3(256), 0, s, codes, out, n_words); return 0;
     }
     return -1;
 }
@@ -77,10 +77,10 @@ int launch_unpack_codes(const uint32_t* packed, int8_t* codes, uint64_t n_words,
     const uint64_t blocks = (n_words + 255) / 256;
     if (blocks == 0) return 0;
     switch (bits) {
-        case 1: hipLaunchKernelGGL(unpack_codes_kernel<1>, dim3(blocks), dim3(256), 0, s, packed, codes, n_words); return 0;
-        case 2: hipLaunchKernelGGL(unpack_codes_kernel<2>, dim3(blocks), dim3(256), 0, s, packed, codes, n_words); return 0;
-        case 4: hipLaunchKernelGGL(unpack_codes_kernel<4>, dim3(blocks), dim3(256), 0, s, packed, codes, n_words); return 0;
-        case 8: hipLaunchKernelGGL(unpack_codes_kernel<8>, dim3(blocks), dim3(256), 0, s, packed, codes, n_words); return 0;
+        case 1: hipLaunchKernelGGL(unpack_codes_kernel<1>, linear_grid(blocks, 256), dim3(256), 0, s, packed, codes, n_words); return 0;
+        case 2: hipLaunchKernelGGL(unpack_codes_kernel<2>, linear_grid(blocks, 256), dim3(256), 0, s, packed, codes, n_words); return 0;
+        case 4: hipLaunchKernelGGL(unpack_codes_kernel<4>, linear_grid(blocks, 256), dim3(256), 0, s, packed, codes, n_words); return 0;
+        case 8: hipLaunchKernelGGL(unpack_codes_kernel<8>, linear_grid(blocks, 256), dim3(256), 0, s, packed, codes, n_words); return 0;
     }
     return -1;
 }

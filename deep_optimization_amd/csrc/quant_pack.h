@@ -183,7 +183,8 @@ __global__ __launch_bounds__(256) void quant_pack_kernel(QuantPackArgs a) {
     const int lane = threadIdx.x & 63;
     const int slot = lane / LPG;
     const int li = lane % LPG;
-    const uint32_t g0 = (blockIdx.x * C::WAVES + (threadIdx.x >> 6)) * (uint32_t)C::GPW;
+    // below 2^32: n_groups < 2^31, and a grid's blocks past the end add fewer than GRID_ROW * WAVES * GPW
+    const uint32_t g0 = (uint32_t)((linear_block() * C::WAVES + (threadIdx.x >> 6)) * C::GPW);
     const char* xb = (const char*)a.x;
 
     // ---- every load of the wave first: P*CPL units of LOADS 16-byte vectors per lane. Lanes past

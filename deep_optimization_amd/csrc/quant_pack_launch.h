@@ -43,12 +43,12 @@ static int qp_launch(const QuantPackArgs& a, hipStream_t s) {
     if (blocks == 0) return 0;
     if (!a.tiled) {
         hipLaunchKernelGGL((quant_pack_kernel<DT, BITS, G, RN, S::UB, S::LPG, S::P, PRE, false, false>),
-                           dim3((uint32_t)blocks), dim3(64 * C::WAVES), 0, s, a);
+                           linear_grid(blocks, 64 * C::WAVES), dim3(64 * C::WAVES), 0, s, a);
         return 0;
     }
     if constexpr (G == 64 || G == 256 || G == 1024) {  // the square group sizes
         hipLaunchKernelGGL((quant_pack_kernel<DT, BITS, G, RN, S::UB, S::LPG, S::P, PRE, false, true>),
-                           dim3((uint32_t)blocks), dim3(64 * C::WAVES), 0, s, a);
+                           linear_grid(blocks, 64 * C::WAVES), dim3(64 * C::WAVES), 0, s, a);
         return 0;
     }
     return -1;

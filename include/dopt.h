@@ -173,16 +173,10 @@ int dopt_fp8_pack_kmajor(const uint8_t* src, int64_t rows, int64_t cols, int64_t
 #define DOPT_ACT_GELU 2  /* tanh form: x (1 + tanh(a (x + b x^3))) / 2, a = sqrt(2/pi), b = 0.044715 */
 #define DOPT_ACT_SILU 3  /* x sigmoid(x) */
 
-/* Most elements one call of the flat elementwise entry points below takes (dopt_relu_pack,
- * dopt_relu_unpack, dopt_act_forward, dopt_pact_clamp_*): one launch of 2^24 - 1 workgroups of
- * 2048 elements. Larger n -> DOPT_EINVAL. */
-#define DOPT_FLAT_MAX_ELEMS 34359736320LL
-
 /*
  * y = relu(x) (x where the mask holds, else 0; fp32 inputs come out rounded to bf16 as in the
  * reference) and the mask packed as `bits`-bit codes (0 or 1) in the quantizer's bitstream.
- * x, y: n elements of x_dtype (F32 or BF16); packed: n*bits/32 uint32; n % 64 == 0,
- * n <= DOPT_FLAT_MAX_ELEMS.
+ * x, y: n elements of x_dtype (F32 or BF16); packed: n*bits/32 uint32; n % 64 == 0.
  * Replaces act_lib::relu_fwd_fused_pack (modules/activations/kernel_registration.py:42-72,
  * kernel modules/activations/kernel_implementation.py:34-90).
  */
@@ -191,14 +185,14 @@ int dopt_relu_pack(const void* x, int x_dtype, int64_t n, int relu6, int bits, v
 
 /*
  * dx = bf16(dy * mask), mask = lowest bit of each `bits`-bit code. dy: n elements of dy_dtype
- * (F32, F16 or BF16); dx: n bf16; n % 64 == 0, n <= DOPT_FLAT_MAX_ELEMS.
+ * (F32, F16 or BF16); dx: n bf16; n % 64 == 0.
  * Replaces act_lib::relu_bwd_fused_unpack (kernel_registration.py:74-94, kernel_implementation.py:93-143).
  */
 int dopt_relu_unpack(const uint32_t* packed, const void* dy, int dy_dtype, int64_t n, int bits, void* dx,
                      void* stream);
 
 /*
- * Unfused activation forward over n <= DOPT_FLAT_MAX_ELEMS elements: RELU/RELU6 -> y in x's type and an int8
+ * Unfused activation forward over n elements (any n): RELU/RELU6 -> y in x's type and an int8
  * mask in aux; GELU/SILU -> bf16 y and the bf16 derivative in aux.
  * Replaces act_lib::relu_triton, silu_triton, gelu_triton (kernel_registration.py:22-39,
  * :132-146, :245-259).
@@ -206,7 +200,7 @@ int dopt_relu_unpack(const uint32_t* packed, const void* dy, int dy_dtype, int64
 int dopt_act_forward(const void* x, int x_dtype, int64_t n, int act, void* y, void* aux, void* stream);
 
 /*
- * PACT clamp over n <= DOPT_FLAT_MAX_ELEMS elements: y = bf16(clamp(x, -alpha, alpha)) (fmaxf then fminf: a NaN
+ * PACT clamp over n elements (any n): y = bf16(clamp(x, -alpha, alpha)) (fmaxf then fminf: a NaN
  * x gives -alpha) and the int8 mask |x| <= alpha. x F32, F16 or BF16, 16-byte aligned like y;
  * mask 8-byte aligned; alpha > 0 (else DOPT_EINVAL: at 0 the output's zero signs would depend
  * on how min and max order -0 and +0).

@@ -100,23 +100,6 @@ class TestValidationWithoutDevice:
         assert L.dopt_pack_codes(16, 4, 64, 5, 16, None) == _lib.EBITS
         assert L.dopt_unpack_codes(16, 4, 48, 2, 16, None) == _lib.EINVAL
 
-    def test_flat_entry_points_reject_more_than_one_launch(self):
-        """n past DOPT_FLAT_MAX_ELEMS ((2^24 - 1) workgroups of 2048 elements) is an argument error
-        before anything is launched; the bound itself passes the size check."""
-        L = _lib.lib()
-        big = ((1 << 24) - 1) * 2048 + 64
-        calls = {
-            "relu_pack": lambda n: L.dopt_relu_pack(16, _lib.BF16, n, 0, 1, 16, 16, None),
-            "relu_unpack": lambda n: L.dopt_relu_unpack(16, 16, _lib.BF16, n, 1, 16, None),
-            "act_forward": lambda n: L.dopt_act_forward(16, _lib.BF16, n, 0, 16, 16, None),
-            "pact_clamp_forward": lambda n: L.dopt_pact_clamp_forward(16, _lib.BF16, n, 1.0, 16, 16, None),
-            "pact_clamp_backward": lambda n: L.dopt_pact_clamp_backward(16, 16, _lib.BF16, n, 16, None),
-        }
-        for name, call in calls.items():
-            assert call(big) == _lib.EINVAL, name
-            msg = L.dopt_last_error().decode()
-            assert name in msg and "34359736320" in msg, msg
-
     def test_bn_noalloc_rejects_shapes_beyond_the_scratch(self):
         L = _lib.lib()
         N, C, HW = 1024, 2048, 56 * 56  # 2 * 2048 * 392 partials: more than the 2^20 floats of scratch
