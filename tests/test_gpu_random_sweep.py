@@ -4,7 +4,11 @@ Philox with 40-bit seeds and offsets), clamp, scale/min dtype, output dtype, fla
 layouts, ragged shapes, and inputs with NaN, +-inf and signed zeros; also the host plumbing
 (unified_quantize -> unified_dequantize without the squash, against the CPU grouping + the
 oracle, 2-D / 3-D / 4-D, with and without act_padding), the ReLU mask pack / unpack, the PACT clamp
-and code pack / unpack. Fixed seeds; each case that differs is reported by its parameters.
+and code pack / unpack; and the BatchNorm normalize + quant-pack and its backward (ReLU, ReLU6
+and squashed modes, random N, C, H, W with N*HW a multiple of the group) to the bar of
+tests/test_gpu_bn.py: sums within an fp32 summation bound, everything downstream of them bit for
+bit, the squashed mode's codes within one step on under 1% of the elements. Fixed seeds; each
+case that differs is reported by its parameters.
 """
 import random
 
@@ -16,6 +20,7 @@ import deep_optimization_amd  # noqa: F401
 import oracle
 from deep_optimization_amd.modules import module_utils as mu
 from deep_optimization_amd.modules import tensor_act_reshape_utils as tr
+from tests.test_gpu_bn import as_f32, check_stats, codes_of, geo, npv, sums_close
 from tests.test_gpu_parity import ROUNDINGS, assert_quant_equal, np_view
 
 pytestmark = pytest.mark.gpu
@@ -198,7 +203,81 @@ def case_codes():
     return name
 
 
-CASES = [case_flat] * 4 + [case_tile] * 3 + [case_module] * 3 + [case_relu, case_pact, case_codes]
+def case_bn():
+    dt = rng.choice(DTYPES)
+    bits = rng.choice([1, 2, 4, 8])
+    BLOCK = rng.choice([64, 128, 256, 512, 1024])
+    grp = BLOCK // 2
+    M = grp * rng.randint(1, 6)
+    HW = rng.choice([d for d in range(1, min(M, 1024) + 1) if M % d == 0])
+    H = rng.choice([d for d in range(1, HW + 1) if HW % d == 0])
+    shape = (M // HW, rng.randint(1, 8 * big()), H, HW // H)
+    N, C = shape[0], shape[1]
+    mode = rng.choice(["relu", "relu6", "squash"])
+    gen = torch.Generator().manual_seed(rng.randrange(1 << 30))
+    x = (torch.randn(shape, generator=gen) * rng.choice([0.01, 1.7, 50.0]) + rng.choice([0.0, 0.5, -3.0])).to(dt)
+    w = torch.rand(C, generator=gen) + 0.5
+    b = torch.randn(C, generator=gen) * 0.3
+    name = f"bn {dt} {shape} BLOCK{BLOCK} b{bits} {mode}"
+    g = geo(x)
+    ops = torch.ops.act_lib
+    x3 = x.to(DEV).view(N, C, -1)
+    wd, bd = w.to(DEV), b.to(DEV)
+    s, q = ops.bn_fwd_reduce(x3, **g, BLOCK_M=BLOCK, num_warps=8, num_stages=5)
+    if mode == "squash":
+        y, packed, scale, xmin, mean, var = ops.bn_fwd_norm_quant_pack_fused(
+            x3, s, q, wd, bd, None, None, **g, BLOCK_M=BLOCK, bits=bits, sync=False, avg_alam=False, alam_bits=0,
+            num_warps=8, num_stages=5)
+        rp, omode = None, oracle.BN_QUANT
+    else:
+        y, packed, rp, scale, xmin, mean, var = ops.bn_relu_fwd_norm_fused_quant_pack(
+            x3, s, q, wd, bd, None, None, **g, relu=mode == "relu", relu6=mode == "relu6", BLOCK_SIZE=BLOCK,
+            BITS=bits, sync=False)
+        omode = oracle.BN_RELU_QUANT if mode == "relu" else oracle.BN_RELU6_QUANT
+    torch.cuda.synchronize()
+    check_stats(x, s, q)
+    ref = oracle.bn_norm_quant(npv(x), w.numpy(), b.numpy(), mode=omode, group_size=grp, bits=bits, eps=1e-5,
+                               sum=npv(s), sumsq=npv(q))
+    for what, got, want in (("mean", mean, ref["mean"]), ("var", var, ref["var"]), ("y", y, ref["y"])):
+        np.testing.assert_array_equal(npv(got).reshape(-1), want.reshape(-1), err_msg=f"{what} {name}")
+    if rp is not None:
+        np.testing.assert_array_equal(npv(rp), ref["relu_packed"], err_msg=name)
+    if mode == "squash":
+        d = np.abs(codes_of(npv(packed), bits) - codes_of(ref["packed"], bits))
+        assert d.max() <= 1 and (d > 0).mean() < 0.01, name
+        for a, r in ((npv(scale), ref["scale"]), (npv(xmin), ref["min"])):
+            assert np.abs(a.astype(np.int64) - r.astype(np.int64)).max() <= 1, name
+    else:
+        for what, got, want in (("packed", packed, ref["packed"]), ("scale", scale, ref["scale"]),
+                                ("min", xmin, ref["min"])):
+            np.testing.assert_array_equal(npv(got), want, err_msg=f"{what} {name}")
+    dy = torch.randn(shape, generator=gen).to(dt)
+    dy3 = dy.to(DEV).view(N, C, -1)
+    if mode == "squash":
+        dw, db = ops.bn_bwd_reduce_dequant_unpack_fused(packed, dy3, scale, xmin, **g, BLOCK_M=BLOCK, bits=bits,
+                                                        avg_alam=False, alam_bits=0)
+        dx = ops.bn_bwd_dx_dequant_unpack_fused(packed, dy3, scale, xmin, dw, db, wd, var, **g, BLOCK_M=BLOCK,
+                                                bits=bits, sync=False, avg_alam=False, alam_bits=0)
+        eps = 1e-7
+    else:
+        dw, db = ops.bn_relu_bwd_reduce_fused_dequant_unpack(packed, rp, dy3, scale, xmin, **g, BLOCK_SIZE=BLOCK,
+                                                             BITS=bits)
+        dx = ops.bn_relu_bwd_dx_fused_dequant_unpack(packed, rp, dy3, dw, db, wd, var, scale, xmin, **g,
+                                                     BLOCK_SIZE=BLOCK, BITS=bits)
+        eps = 1e-5
+    torch.cuda.synchronize()
+    kw = dict(mode=omode, packed=npv(packed), relu_packed=None if rp is None else npv(rp), scale=npv(scale),
+              min=npv(xmin), group_size=grp, bits=bits)
+    rdw, rdb = oracle.bn_bwd_reduce(npv(dy), **kw)
+    dyf = np.abs(as_f32(npv(dy))).astype(np.float64)
+    assert sums_close(npv(db), rdb, dyf.sum(axis=(0, 2, 3))), f"db {name}"
+    assert sums_close(npv(dw), rdw, 8.0 * dyf.sum(axis=(0, 2, 3))), f"dw {name}"
+    rdx = oracle.bn_bwd_dx(npv(dy), npv(dw), npv(db), w.numpy(), npv(var), eps=eps, **kw)
+    np.testing.assert_array_equal(npv(dx).reshape(-1), rdx.reshape(-1), err_msg=f"dx {name}")
+    return name
+
+
+CASES = [case_flat] * 4 + [case_tile] * 3 + [case_module] * 3 + [case_relu, case_pact, case_codes] + [case_bn] * 2
 
 
 @pytest.mark.parametrize("seed,n,scale", [(101, 3000, 1), (102, 3000, 1), (103, 600, 8)])
