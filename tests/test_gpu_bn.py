@@ -7,8 +7,9 @@ Bar:
     oracle sums;
   * everything downstream of the sums, given the GPU's sums: bit-exact (mean, var, y, x_hat,
     ReLU mask, codes, scale, min, dx), except the squashed mode's codes, which go through tanh
-    (libdevice in the reference, ocml here, the C library in the oracle): within one code on under
-    1% of the elements, scale and min within one bf16 ulp.
+    (libdevice in the reference, ocml here, the C library in the oracle): within one code, and
+    different only at elements whose float64 code argument lies within the two tanh evaluations'
+    error of a rounding boundary (squash_codes_close); scale and min within one bf16 ulp.
 Shapes cover every access width of the kernels (8 elements per access at HW = 256, 784; 4 at
 HW = 196; 2 at HW = 50; 1 at HW = 49 and for a misaligned input view), group sizes 32..512
 (BLOCK_M 64..1024), bits 1/2/4/8, bf16 / fp32 / fp16 inputs, the sync path, and the squashed
@@ -63,6 +64,44 @@ def codes_of(packed, bits):
 def as_f32(a):
     """a numpy view from npv as float32 (bf16 bit patterns widened)"""
     return oracle.bf16_bits_to_f32(a) if a.dtype == np.uint16 else a.astype(np.float32)
+
+
+def squash_codes_close(x, mean, var, gpu_packed, ref_packed, bits, grp, eps=1e-5):
+    """Squashed-mode codes against the oracle's: within one step everywhere, and different only
+    where the element's code argument, worked out in float64 from the kernels' fp32
+    x_hat = (x - mean) * (1 / sqrt(var + eps)), lies within the two squash evaluations' error of a
+    rounding boundary. Each evaluation of 2 tanh(x/2) is within 2e-7 of the exact value (ocml here,
+    the C library's tanhf in the oracle; libdevice in the reference), so elements closer than that
+    to a boundary may round either way; data with few distinct values can stack many elements on
+    one exact tie (the argument at k + 1/2 steps). Returns (ok, message)."""
+    cg, cr = codes_of(gpu_packed, bits), codes_of(ref_packed, bits)
+    d = np.abs(cg - cr)
+    if d.max(initial=0) > 1:
+        return False, f"codes {d.max()} apart"
+    idx = np.flatnonzero(d)
+    if idx.size == 0:
+        return True, ""
+    xs = np.asarray(as_f32(npv(x)), dtype=np.float32)
+    N, C = xs.shape[0], xs.shape[1]
+    x3 = xs.reshape(N, C, -1)
+    HW = x3.shape[2]
+    M = N * HW
+    mean32, var32 = as_f32(npv(mean)), as_f32(npv(var))
+    inv32 = np.float32(1.0) / np.sqrt(var32 + np.float32(eps))
+    qmax = (1 << bits) - 1
+    for k in idx:
+        c, e = divmod(int(k), M)
+        r = e // grp
+        es = np.arange(r * grp, (r + 1) * grp)
+        xh = ((x3[es // HW, c, es % HW] - mean32[c]) * inv32[c]).astype(np.float64)
+        t = 2.0 * np.tanh(np.clip(xh, -3.0, 3.0) / 2.0)
+        mn, mx = t.min(), t.max()
+        step = (mx - mn) / qmax if mx > mn else 1.0
+        arg = (t[e - r * grp] - mn) / step + 0.5
+        tol = 6e-7 / step + 1e-4
+        if abs(arg - round(arg)) > tol:
+            return False, f"code {k} (channel {c}, element {e}) differs {abs(arg - round(arg)):.3g} from a boundary"
+    return True, ""
 
 
 def sums_close(got, want_f64, mag):
@@ -155,8 +194,8 @@ def test_fused_forward_and_backward(case, bits, mode, dtype):
     if rp is not None:
         np.testing.assert_array_equal(npv(rp), ref["relu_packed"])
     if mode == "squash":
-        d = np.abs(codes_of(npv(packed), bits) - codes_of(ref["packed"], bits))
-        assert d.max() <= 1 and (d > 0).mean() < 0.01
+        ok, msg = squash_codes_close(x, mean, var, npv(packed), ref["packed"], bits, grp)
+        assert ok, msg
         for a, r in ((npv(scale), ref["scale"]), (npv(xmin), ref["min"])):
             assert np.abs(a.astype(np.int64) - r.astype(np.int64)).max() <= 1
     else:

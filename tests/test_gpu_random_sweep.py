@@ -7,8 +7,8 @@ oracle, 2-D / 3-D / 4-D, with and without act_padding), the ReLU mask pack / unp
 and code pack / unpack; and the BatchNorm normalize + quant-pack and its backward (ReLU, ReLU6
 and squashed modes, random N, C, H, W with N*HW a multiple of the group) to the bar of
 tests/test_gpu_bn.py: sums within an fp32 summation bound, everything downstream of them bit for
-bit, the squashed mode's codes within one step on under 1% of the elements. Fixed seeds; each
-case that differs is reported by its parameters.
+bit, the squashed mode's codes within one step and different only at near-ties of the float64
+code argument. Fixed seeds; each case that differs is reported by its parameters.
 """
 import random
 
@@ -20,7 +20,7 @@ import deep_optimization_amd  # noqa: F401
 import oracle
 from deep_optimization_amd.modules import module_utils as mu
 from deep_optimization_amd.modules import tensor_act_reshape_utils as tr
-from tests.test_gpu_bn import as_f32, check_stats, codes_of, geo, npv, sums_close
+from tests.test_gpu_bn import as_f32, check_stats, geo, npv, squash_codes_close, sums_close
 from tests.test_gpu_parity import ROUNDINGS, assert_quant_equal, np_view
 
 pytestmark = pytest.mark.gpu
@@ -243,8 +243,8 @@ def case_bn():
     if rp is not None:
         np.testing.assert_array_equal(npv(rp), ref["relu_packed"], err_msg=name)
     if mode == "squash":
-        d = np.abs(codes_of(npv(packed), bits) - codes_of(ref["packed"], bits))
-        assert d.max() <= 1 and (d > 0).mean() < 0.01, name
+        ok, msg = squash_codes_close(x, mean, var, npv(packed), ref["packed"], bits, grp)
+        assert ok, f"{name}: {msg}"
         for a, r in ((npv(scale), ref["scale"]), (npv(xmin), ref["min"])):
             assert np.abs(a.astype(np.int64) - r.astype(np.int64)).max() <= 1, name
     else:

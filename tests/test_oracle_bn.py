@@ -331,3 +331,47 @@ def test_alam_rejects_run_lengths_the_reference_cannot_reshape():
     with pytest.raises(RuntimeError):  # avg_alam is a squashed-mode option
         oracle.bn_norm_quant(x, w, b, mode=oracle.BN_RELU_QUANT, group_size=64, bits=2, eps=1e-5, sum=s, sumsq=q,
                              alam_bits=2)
+
+
+def test_squash_code_bar_accepts_exact_ties_and_rejects_planted_mistakes():
+    """The GPU tests' bar for the squashed mode's codes (tests/test_gpu_bn.py::squash_codes_close),
+    checked on oracle codes: bf16 data with five distinct values, symmetric about a channel mean of
+    exactly -3.0, puts every x = -3.0 element at x_hat = 0 and its code argument exactly at a half
+    step, where the last ulp of the squash decides the rounding. A one-step flip of those elements
+    passes; a one-step flip elsewhere, a two-step difference, and codes from a planted wrong eps
+    (1e-2 in place of 1e-5) fail."""
+    from tests.test_gpu_bn import codes_of, squash_codes_close
+
+    vals = torch.tensor([-3.03125, -3.015625, -3.0, -2.984375, -2.96875])
+    pattern = torch.tensor([0, 1, 2, 3, 4, 2, 2, 2])
+    col = vals[pattern[torch.arange(256) % 8]]
+    x = torch.stack([col, col.flip(0)], dim=1).view(256, 2, 1, 1).to(torch.bfloat16)
+    xn = x.view(torch.int16).numpy().view(np.uint16)
+    w, b = np.ones(2, np.float32), np.zeros(2, np.float32)
+    s, q = oracle.bn_reduce(xn)
+
+    def quant(eps):
+        return oracle.bn_norm_quant(xn, w, b, mode=oracle.BN_QUANT, group_size=128, bits=8, eps=eps, sum=s, sumsq=q)
+
+    ref = quant(1e-5)
+    mean, var = torch.from_numpy(ref["mean"]), torch.from_numpy(ref["var"])
+    assert float(mean[0]) == -3.0 and float(mean[1]) == -3.0
+    codes = codes_of(ref["packed"], 8).reshape(2, 256)
+    xc = x.float().view(256, 2).t().numpy()  # channel-major, like the codes
+    tie = xc == -3.0
+
+    def packed(c):
+        return np.ascontiguousarray(c.astype(np.uint8)).view(np.uint32)
+
+    flipped = codes.copy()
+    flipped[tie] = np.where(codes[tie] >= 128, codes[tie] - 1, codes[tie] + 1)
+    assert squash_codes_close(x, mean, var, packed(flipped), ref["packed"], 8, 128)[0]
+    for e in np.flatnonzero(~tie[0])[:3]:  # one step off at an element far from a boundary
+        c = codes.copy()
+        c[0, e] += 1 if c[0, e] < 255 else -1
+        assert not squash_codes_close(x, mean, var, packed(c), ref["packed"], 8, 128)[0]
+    c = codes.copy()
+    e = np.flatnonzero(tie[0])[0]
+    c[0, e] += 2 if c[0, e] < 128 else -2
+    assert not squash_codes_close(x, mean, var, packed(c), ref["packed"], 8, 128)[0]
+    assert not squash_codes_close(x, mean, var, quant(1e-2)["packed"], ref["packed"], 8, 128)[0]
