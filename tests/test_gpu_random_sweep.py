@@ -9,7 +9,8 @@ and squashed modes, random N, C, H, W with N*HW a multiple of the group) to the 
 tests/test_gpu_bn.py: sums within an fp32 summation bound, everything downstream of them bit for
 bit, the squashed mode's codes within one step and different only at near-ties of the float64
 code argument; and the fused GELU / SiLU forward and backward on continuous data to the bar of
-tests/test_gpu_act.py. Fixed seeds; each case that differs is reported by its parameters.
+tests/test_gpu_act.py; and the weight-gradient GEMM (bf16 and packed operands, ragged K) to the bar of
+tests/test_gpu_dw.py. Fixed seeds; each case that differs is reported by its parameters.
 """
 import random
 
@@ -21,8 +22,10 @@ import deep_optimization_amd  # noqa: F401
 import oracle
 from deep_optimization_amd.modules import module_utils as mu
 from deep_optimization_amd.modules import tensor_act_reshape_utils as tr
-from tests.test_gpu_bn import as_f32, check_stats, geo, npv, squash_codes_close, sums_close
 from tests.test_gpu_act import _check_act_quant
+from tests.test_gpu_bn import as_f32, check_stats, geo, npv, squash_codes_close, sums_close
+from tests.test_gpu_dw import check_close as dw_check_close
+from tests.test_gpu_dw import operands as dw_operands
 from tests.test_gpu_parity import ROUNDINGS, assert_quant_equal, np_view
 
 pytestmark = pytest.mark.gpu
@@ -324,7 +327,34 @@ def case_act():
     return name
 
 
-CASES = [case_flat] * 4 + [case_tile] * 3 + [case_module] * 3 + [case_relu, case_pact, case_codes] + [case_bn] * 2 + [case_act] * 2
+def case_dw():
+    """The weight-gradient GEMM on random M, N (multiples of 256) and ragged K, to the bar of
+    tests/test_gpu_dw.py: dW and db within 1e-4 of the sum of the terms' magnitudes of float64
+    products, the bf16 output the rounding of the fp32 one, and the packed-code path bit for bit
+    equal to the bf16 path fed with the dequantized activation."""
+    M, N = 256 * rng.randint(1, 8), 256 * rng.randint(1, 8)
+    K = rng.randint(1, 20000)
+    bits = rng.choice([1, 2, 4, 8])
+    g = rng.choice([g_ for g_ in (64, 128, 256, 512, 1024) if (K * N) % g_ == 0])
+    name = f"dw M{M} N{N} K{K} b{bits} g{g}"
+    dy, x = dw_operands(K, M, N, rng.randrange(1 << 30))
+    ops = torch.ops.act_lib
+    packed, scale, xmin = ops.quant_pack_triton(x.reshape(1, -1, g), bits, g, False, 0, True, 3.0)
+    x_hat = ops.dequant_unpack_triton(packed, scale, xmin, bits, g, False, 0).reshape(K, N)
+    want, wdb = ops.dw_gemm(dy, x_hat, None, None, None, N, 0, 0, True, torch.float32)
+    got, gdb = ops.dw_gemm(dy, None, packed, scale, xmin, N, bits, g, True, torch.float32)
+    w16, _ = ops.dw_gemm(dy, x_hat, None, None, None, N, 0, 0, False, torch.bfloat16)
+    torch.cuda.synchronize()
+    assert torch.equal(got, want), name
+    assert torch.equal(w16, want.to(torch.bfloat16)), name
+    dw_check_close(want, dy, x_hat)
+    mag = dy.double().abs().sum(0)
+    for d in (wdb, gdb):
+        assert bool(((d.double() - dy.double().sum(0)).abs() <= 1e-4 * mag + 1e-6).all()), f"db {name}"
+    return name
+
+
+CASES = [case_flat] * 4 + [case_tile] * 3 + [case_module] * 3 + [case_relu, case_pact, case_codes] + [case_bn] * 2 + [case_act] * 2 + [case_dw]
 
 
 @pytest.mark.parametrize("seed,n,scale", [(101, 3000, 1), (102, 3000, 1), (103, 600, 8)])
