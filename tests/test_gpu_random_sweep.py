@@ -10,7 +10,8 @@ tests/test_gpu_bn.py: sums within an fp32 summation bound, everything downstream
 bit, the squashed mode's codes within one step and different only at near-ties of the float64
 code argument; and the fused GELU / SiLU forward and backward on continuous data to the bar of
 tests/test_gpu_act.py; and the weight-gradient GEMM (bf16 and packed operands, ragged K) to the bar of
-tests/test_gpu_dw.py. Fixed seeds; each case that differs is reported by its parameters.
+tests/test_gpu_dw.py; and the FP8 GEMM (random shapes, padded strides, a sentinel around C) to the bar
+of tests/test_gpu_parity.py. Fixed seeds; each case that differs is reported by its parameters.
 """
 import random
 
@@ -20,6 +21,7 @@ import torch
 
 import deep_optimization_amd  # noqa: F401
 import oracle
+from deep_optimization_amd import _lib
 from deep_optimization_amd.modules import module_utils as mu
 from deep_optimization_amd.modules import tensor_act_reshape_utils as tr
 from tests.test_gpu_act import _check_act_quant
@@ -354,7 +356,35 @@ def case_dw():
     return name
 
 
-CASES = [case_flat] * 4 + [case_tile] * 3 + [case_module] * 3 + [case_relu, case_pact, case_codes] + [case_bn] * 2 + [case_act] * 2 + [case_dw]
+def case_fp8():
+    """The FP8 e4m3 GEMM through the C ABI on random M, N, K (K a multiple of 16, a quarter of the
+    cases from 8192 up, the 16x16x128 kernel) with padded row strides holding NaN encodings and a
+    sentinel around C, to the bar of tests/test_gpu_parity.py: within bf16 rounding (plus 1e-3 of
+    the largest magnitude) of the fp32 product of the same e4m3 operands, nothing written outside
+    M x N."""
+    big_k = rng.random() < 0.25
+    M, N = (rng.randint(1, 600), rng.randint(1, 600)) if big_k else (rng.randint(1, 3000), rng.randint(1, 3000))
+    K = 16 * (rng.randint(512, 560) if big_k else rng.randint(1, 300))
+    lda, ldb, ldc = K + 16 * rng.randint(0, 3), K + 16 * rng.randint(0, 3), N + rng.randint(0, 9)
+    gen = torch.Generator(device=DEV).manual_seed(rng.randrange(1 << 30))
+    a8 = (torch.randn(M, lda, generator=gen, device=DEV) * 40).clamp(-448, 448).to(torch.float8_e4m3fn)
+    b8 = (torch.randn(N, ldb, generator=gen, device=DEV) * 40).clamp(-448, 448).to(torch.float8_e4m3fn)
+    a8.view(torch.uint8)[:, K:] = 0x7F
+    b8.view(torch.uint8)[:, K:] = 0xFF
+    c = torch.full((M + 1, ldc), 77.0, dtype=torch.bfloat16, device=DEV)
+    name = f"fp8 M{M} N{N} K{K} lda{lda} ldb{ldb} ldc{ldc}"
+    rc = _lib.lib().dopt_fp8_gemm_nt(a8.data_ptr(), b8.data_ptr(), M, N, K, lda, ldb, 1.0 / 1600.0, c.data_ptr(),
+                                     ldc, torch.cuda.current_stream().cuda_stream)
+    _lib.check(rc, "fp8_gemm_nt")
+    ref = (a8[:, :K].float() @ b8[:, :K].float().t()) / 1600.0
+    got = c[:M, :N].float()
+    assert bool(torch.isfinite(got).all()), name
+    assert bool(((got - ref).abs() <= ref.abs() * 2 ** -7 + 1e-3 * ref.abs().max()).all()), name
+    assert bool((c[:M, N:] == 77.0).all()) and bool((c[M:] == 77.0).all()), f"{name}: written outside C"
+    return name
+
+
+CASES = [case_flat] * 4 + [case_tile] * 3 + [case_module] * 3 + [case_relu, case_pact, case_codes] + [case_bn] * 2 + [case_act] * 2 + [case_dw, case_fp8]
 
 
 @pytest.mark.parametrize("seed,n,scale", [(101, 3000, 1), (102, 3000, 1), (103, 600, 8)])
