@@ -33,24 +33,27 @@ __device__ __forceinline__ void load8(const void* base, uint64_t e0, float* v) {
     }
 }
 
-// stores 8 floats in the element type DT (bf16 rounding RNE; f32 verbatim)
+// stores 8 floats in the element type DT (bf16 rounding RNE; f32 verbatim). The outputs of these
+// kernels are written once and read by another kernel later, so they are streamed (non-temporal):
+// measured on bf16 [256,256,56,56] at 1 bit, the ReLU forward 138 -> 133 us, its backward 139 -> 132.5 us
 template <int DT>
 __device__ __forceinline__ void store8(void* base, uint64_t e0, const float* v) {
     char* p = (char*)base + e0 * DType<DT>::bytes;
     if constexpr (DT == DT_F32) {
-        *(uint4*)p = make_uint4(__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]), __float_as_uint(v[3]));
-        *(uint4*)(p + 16) = make_uint4(__float_as_uint(v[4]), __float_as_uint(v[5]), __float_as_uint(v[6]),
-                                       __float_as_uint(v[7]));
+        st16<true>(p, make_uint4(__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]),
+                                 __float_as_uint(v[3])));
+        st16<true>(p + 16, make_uint4(__float_as_uint(v[4]), __float_as_uint(v[5]), __float_as_uint(v[6]),
+                                      __float_as_uint(v[7])));
     } else if constexpr (DT == DT_BF16) {
-        *(uint4*)p = make_uint4(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]), pack_bf16x2(v[4], v[5]),
-                                pack_bf16x2(v[6], v[7]));
+        st16<true>(p, make_uint4(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]), pack_bf16x2(v[4], v[5]),
+                                 pack_bf16x2(v[6], v[7])));
     } else {
         uint32_t w[4];
 #pragma unroll
         for (int k = 0; k < 4; ++k)
             w[k] = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)v[2 * k]) |
                    ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)v[2 * k + 1]) << 16);
-        *(uint4*)p = make_uint4(w[0], w[1], w[2], w[3]);
+        st16<true>(p, make_uint4(w[0], w[1], w[2], w[3]));
     }
 }
 
@@ -68,7 +71,7 @@ __device__ __forceinline__ void store8_masked(void* base, uint64_t e0, const voi
             r.y = (m & 2u) ? r.y : 0u;
             r.z = (m & 4u) ? r.z : 0u;
             r.w = (m & 8u) ? r.w : 0u;
-            *(uint4*)(dst + 16 * h) = r;
+            st16<true>(dst + 16 * h, r);
         }
     } else {
         uint4 r = ld16<false>(src);
@@ -78,7 +81,7 @@ __device__ __forceinline__ void store8_masked(void* base, uint64_t e0, const voi
             const uint32_t lo = (mbits >> (2 * k)) & 1u, hi = (mbits >> (2 * k + 1)) & 1u;
             w[k] &= (lo ? 0x0000ffffu : 0u) | (hi ? 0xffff0000u : 0u);
         }
-        *(uint4*)dst = make_uint4(w[0], w[1], w[2], w[3]);
+        st16<true>(dst, make_uint4(w[0], w[1], w[2], w[3]));
     }
 }
 
