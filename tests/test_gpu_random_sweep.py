@@ -11,7 +11,8 @@ bit, the squashed mode's codes within one step and different only at near-ties o
 code argument; and the fused GELU / SiLU forward and backward on continuous data to the bar of
 tests/test_gpu_act.py; and the weight-gradient GEMM (bf16 and packed operands, ragged K) to the bar of
 tests/test_gpu_dw.py; and the FP8 GEMM (random shapes, padded strides, a sentinel around C) to the bar
-of tests/test_gpu_parity.py. Fixed seeds; each case that differs is reported by its parameters.
+of tests/test_gpu_parity.py; and the ALAM quantizer and its dequantization. Fixed seeds; each case
+that differs is reported by its parameters.
 """
 import random
 
@@ -384,7 +385,52 @@ def case_fp8():
     return name
 
 
-CASES = [case_flat] * 4 + [case_tile] * 3 + [case_module] * 3 + [case_relu, case_pact, case_codes] + [case_bn] * 2 + [case_act] * 2 + [case_dw, case_fp8]
+def case_alam():
+    """The ALAM (avg_alam) quantizer through the C ABI without the squash: codes, scale and min bit
+    for bit (runs of alam_bits code arguments summed left to right); its dequantization within one
+    bf16 ulp plus 1e-5 of the group's step per element (the Box-Muller noise's log / cos are the C
+    library's in the oracle, a few fp32 ulps from the GPU's, which matters where the result cancels
+    to near zero)."""
+    dt = rng.choice(DTYPES)
+    g = rng.choice([64, 128, 256, 512, 1024])
+    bits, alam = rng.choice([(b_, a_) for b_ in (1, 2, 4, 8) for a_ in (1, 2, 4, 8) if (g * b_ // 32) % a_ == 0])
+    ng = rng.randint(1, 60 * big())
+    clamp = rng.random() < 0.3
+    x = rand_x((ng, g), dt)
+    name = f"alam {dt} g{g} b{bits} A{alam} ng{ng} clamp{clamp}"
+    L, st = _lib.lib(), torch.cuda.current_stream().cuda_stream
+    xd = x.to(DEV)
+    p = torch.empty((ng, g * bits // 32 // alam), dtype=torch.int32, device=DEV)
+    s_ = torch.empty(ng, dtype=torch.bfloat16, device=DEV)
+    m = torch.empty(ng, dtype=torch.bfloat16, device=DEV)
+    code = {torch.float32: _lib.F32, torch.float16: _lib.F16, torch.bfloat16: _lib.BF16}[dt]
+    flags = oracle.FLAG_CLAMP if clamp else 0
+    rc = L.dopt_alam_quant_pack(xd.data_ptr(), code, ng, g, bits, alam, flags, 2.5, p.data_ptr(), s_.data_ptr(),
+                                m.data_ptr(), st)
+    assert rc == 0, L.dopt_last_error()
+    y = torch.empty((ng, g), dtype=torch.bfloat16, device=DEV)
+    rc = L.dopt_alam_dequant_unpack(p.data_ptr(), s_.data_ptr(), m.data_ptr(), ng, g, bits, alam, oracle.ALAM_SEED,
+                                    y.data_ptr(), st)
+    assert rc == 0, L.dopt_last_error()
+    torch.cuda.synchronize()
+    rp, rs, rm = oracle.alam_quant_pack(np_view(x), g, bits, alam, flags=flags, clamp_alpha=2.5)
+    np.testing.assert_array_equal(np_view(p).view(np.uint32).reshape(rp.shape), rp, err_msg=name)
+    np.testing.assert_array_equal(np_view(s_), rs, err_msg=name)
+    np.testing.assert_array_equal(np_view(m), rm, err_msg=name)
+    yo = oracle.alam_dequant_unpack(rp, rs, rm, g, bits, alam)
+    yg = oracle.bf16_bits_to_f32(np_view(y).reshape(-1)).astype(np.float64)
+    yr = oracle.bf16_bits_to_f32(yo.reshape(-1)).astype(np.float64)
+    step = np.repeat(oracle.bf16_bits_to_f32(rs).astype(np.float64), g)
+    # one bf16 ulp, plus the noise's fp32 error (a few ulps of |n| <= ~5, times the step) where
+    # q + n - 1/2 and min nearly cancel
+    tol = 2.0 ** -7 * np.maximum(np.abs(yg), np.abs(yr)) + 1e-5 * step
+    with np.errstate(invalid="ignore"):  # inf - inf where a group's range is infinite
+        ok = (yg == yr) | (np.abs(yg - yr) <= tol) | (np.isnan(yg) & np.isnan(yr))
+    assert ok.all(), f"{name}: dequant {int((~ok).sum())} values beyond one bf16 ulp + 1e-5 step"
+    return name
+
+
+CASES = [case_flat] * 4 + [case_tile] * 3 + [case_module] * 3 + [case_relu, case_pact, case_codes] + [case_bn] * 2 + [case_act] * 2 + [case_dw, case_fp8, case_alam]
 
 
 @pytest.mark.parametrize("seed,n,scale", [(101, 3000, 1), (102, 3000, 1), (103, 600, 8)])
