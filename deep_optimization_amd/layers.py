@@ -20,8 +20,8 @@ Differences from the reference:
   * the PACT clamp the reference's DOConv1d / DOConv3d put in front of the Function (layers.py:69,
     :74, :152, :157, with the never-defined ``self.pact_alpha``) is opt-in on every Conv layer: a
     ``pact_alpha`` (float or one-element tensor) runs ``GroupPACTClampFn`` on the training input
-    first; without autocast its bf16 output is cast back to the input's dtype (exactly: the values
-    are bf16) so that the convolution's operands agree. The default, None, is the reference's
+    first (read as a float at construction); without autocast its bf16 output is cast back to the
+    input's dtype (exactly: the values are bf16) so that the convolution's operands agree. The default, None, is the reference's
     behaviour on every path that runs there.
 """
 from __future__ import annotations
@@ -55,7 +55,9 @@ class _DOConvMixin:
 
     def _init_do(self, clamp_alpha, target_name, meta, pact_alpha):
         self.clamp_alpha = clamp_alpha
-        self.pact_alpha = pact_alpha
+        # a constant (GroupPACTClampFn gives alpha no gradient, as the reference's does): read once
+        # here, so the training forward makes no host synchronisation and stays graph-capturable
+        self.pact_alpha = None if pact_alpha is None else float(pact_alpha)
         self.target_name = target_name
         self.meta = {} if meta is None else meta
         self.ema_grad_meta = None
