@@ -14,7 +14,9 @@ What is pinned and how:
     weights come back to their values (one fp32 add and subtract);
   * a Controller-rewritten ResNet (compressed Conv / BatchNorm / ReLU beside torch's layers)
     captured as forward + loss + backward: three replays give an eager step's loss and gradients
-    within 1e-5 relative, with MIOpen's deterministic solvers.
+    within 1e-5 relative, with MIOpen's deterministic solvers;
+  * a DOConv2d with the PACT clamp in front, captured as forward + backward: no memset node, and
+    three replays equal eager steps to 1e-5.
 """
 import ctypes
 
@@ -233,3 +235,56 @@ def test_compressed_resnet_step_replays_like_eager(deterministic_miopen):
         for i, (p, gg) in enumerate(zip(params, g_graph)):
             if gg.any():
                 assert rel_err(gg, p.grad) <= 1e-5, (r, i, rel_err(gg, p.grad))
+
+
+def test_pact_conv_layer_replays_like_eager(deterministic_miopen):
+    """A DOConv2d with the PACT clamp in front (pact_alpha) captured as forward + backward under
+    bf16 autocast: the clamp's operators and its 1-bit mask pack make no host synchronisation and
+    no memset node; each of three replays gives the eager step's output and the input and weight
+    gradients (relative error <= 1e-5)."""
+    from deep_optimization_amd.controller import layer_group_meta
+    from deep_optimization_amd.layers import DOConv2d
+
+    torch.manual_seed(5)
+    shape = (8, 32, 32, 32)
+    meta = {"conv": {"pack_only": False, "bits": 2, "AVG_ALAM": False, "ALAM_BITS": 0, "DIVISION": None,
+                     **layer_group_meta(shape, 2)}}
+    layer = DOConv2d(32, 64, 3, padding=1, target_name="conv", meta=meta, pact_alpha=1.0).to(DEV).train()
+    x = torch.randn(shape, device=DEV).requires_grad_(True)
+    dy = torch.randn(8, 64, 32, 32, device=DEV).to(torch.bfloat16)
+    leaves = [x, layer.weight]
+
+    def step():
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            y = layer(x)
+        y.backward(dy)
+        return y
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for t in leaves:
+            t.grad = torch.zeros_like(t)
+        step()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph(keep_graph=True)
+    for t in leaves:
+        t.grad.zero_()
+    with torch.cuda.graph(g, stream=side):
+        y_static = step().detach()
+    finalize(g)
+    assert graph_node_counts(g).get("memset", 0) == 0
+    for r in range(3):
+        for t in leaves:
+            t.grad.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        y_graph, g_graph = y_static.clone(), [t.grad.clone() for t in leaves]
+        for t in leaves:
+            t.grad.zero_()
+        y_e = step().detach()
+        torch.cuda.synchronize()
+        assert rel_err(y_graph, y_e) <= 1e-5, r
+        for gg, t in zip(g_graph, leaves):
+            assert rel_err(gg, t.grad) <= 1e-5, (r, rel_err(gg, t.grad))
