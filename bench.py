@@ -555,6 +555,19 @@ def main() -> int:
                                 "packed_bytes": ve * b // 8 + vng * 8, "compression_vs_bf16": round(ve * 2 / (ve * b / 8 + vng * 8), 2),
                                 "ms_per_step": round(st * 1e3, 4)}
         extras["vit_mlp_sweep_philox_g128"] = sweep
+        # the reference's one measured figure (AC/test2.ipynb cell 0): its Triton dequant-unpack alone,
+        # 2-bit, bf16 [8192, 768], g = 256, 0.024 ms per call on unstated hardware; the same operator
+        # (act_lib::dequant_unpack_triton) on the same shape, 14,254,080 algorithmic bytes per call
+        ng_r = 8192 * 768 // 256
+        xr = torch.randn((1, ng_r, 256), generator=torch.Generator(device=dev).manual_seed(5), device=dev)
+        pr, sr, mr = ops.quant_pack_triton(xr.to(torch.bfloat16), 2, 256, False, 0, True, 3.0)
+        t_r = event_avg(lambda: ops.dequant_unpack_triton(pr, sr, mr, 2, 256, False, 0))
+        rb = unpack_bytes(8192 * 768, ng_r, 2, 2) - ng_r * 4  # bf16 scale / min: 4 bytes per group, not 8
+        extras["reference_notebook_dequant_8192x768_2bit"] = {
+            "us": round(t_r * 1e6, 2), "GB/s": round(rb / t_r / 1e9, 1), "bytes": rb,
+            "reference_us": 24.0, "vs_reference": round(24.0e-6 / t_r, 2),
+            "note": "AC/test2.ipynb cell 0's figure, hardware unstated: a small, launch-bound call"}
+        del xr, pr, sr, mr
         progress("fused activation layers")
         # fused activation layers: GELU / SiLU (y + 2-bit quantized derivative, g = 128, bf16
         # scale/min) on the ViT MLP activation, ReLU (y + 1-bit mask) on the ResNet activation;
